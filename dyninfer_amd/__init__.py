@@ -1,0 +1,266 @@
+"""dyninfer_amd — MI355X (gfx950) quantized weight-matmul path for dyninfer.
+
+Python host mirror of the C ABI in ``include/dyninfer_mi355x.h`` (the drop-in
+boundary).  Every compute call goes through ``libdyninfer_mi355x.so``; there
+is no fallback of any kind: if the library is missing or the device is not
+gfx950, calls raise.  torch is used only to own device memory and streams.
+
+Reference correspondences:
+  * ``QWeight`` — a quantized parameter binding: GGUF ``BlockQuantized`` data
+    (crates/dyninfer-checkpoint-gguf/src/convention.rs:200-279) or MLX
+    ``GroupQuantized`` packed/scales/biases (crates/dyninfer-checkpoint-safetensors/src/mlx.rs:152-261),
+    in their exact on-disk bytes;
+  * ``Context.qlinear`` — the helper the selected lowering calls for a
+    Linear / OutputProjection (gguf_codegen.rs:268-314, mlx_affine.rs:557-626);
+  * ``Context.dequant`` — ``emit_dequant`` (gguf_codegen.rs:350-526);
+  * ``candidates`` / ``registry_select`` / ``registry_require`` — kernel
+    candidates and ``KernelRegistry::{select,require}``
+    (crates/dyninfer-kernel-registry/src/lib.rs:302-399).
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+__all__ = [
+    "LIB_PATH", "DyninferError", "QWeight", "Context", "library", "candidates", "registry_select",
+    "registry_require", "supports", "ENC_Q4_0", "ENC_Q4_1", "ENC_Q8_0", "ENC_Q6_K", "ENC_MLX_U4",
+    "DTYPE_F32", "DTYPE_F16", "DTYPE_BF16", "block_geometry", "weight_bytes",
+]
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdyninfer_mi355x.so")
+
+OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_HIP, ERR_DEVICE, ERR_BUFFER_TOO_SMALL = 0, 1, 2, 3, 4, 5
+ENC_Q4_0, ENC_Q4_1, ENC_Q8_0, ENC_Q6_K, ENC_MLX_U4 = 2, 3, 8, 14, 0x1004
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+ENCODING_IDS = {ENC_Q4_0: "gguf.q4_0", ENC_Q4_1: "gguf.q4_1", ENC_Q8_0: "gguf.q8_0", ENC_Q6_K: "gguf.q6_k",
+                ENC_MLX_U4: "mlx.affine.u4"}
+# (weights per block, bytes per block): gguf_codegen.rs:23-38
+_GGUF_BLOCK = {ENC_Q4_0: (32, 18), ENC_Q4_1: (32, 20), ENC_Q8_0: (32, 34), ENC_Q6_K: (256, 210)}
+
+EXPORTED_SYMBOLS = (
+    "dyninfer_mi355x_open", "dyninfer_mi355x_close", "dyninfer_mi355x_last_error", "dyninfer_mi355x_qlinear",
+    "dyninfer_mi355x_qlinear_multi", "dyninfer_mi355x_dequant", "dyninfer_mi355x_supports",
+    "dyninfer_mi355x_candidates_json", "dyninfer_mi355x_registry_select", "dyninfer_mi355x_registry_require",
+    "dyninfer_mi355x_version",
+)
+
+
+class DyninferError(RuntimeError):
+    """Non-zero status from the C ABI; ``code`` is the status, the message is last_error."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+        self.message = message
+
+
+class _QWeightC(ctypes.Structure):
+    _fields_ = [
+        ("encoding", ctypes.c_uint32), ("group_size", ctypes.c_uint32), ("rows", ctypes.c_uint64),
+        ("cols", ctypes.c_uint64), ("data", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+        ("biases", ctypes.c_void_p), ("scale_dtype", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+    ]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def library() -> ctypes.CDLL:
+    """Load the built library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: build it with `python -m dyninfer_amd.build` "
+                          "(the MI355X path has no fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    P, U32, I, SZ = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int, ctypes.c_size_t
+    W = ctypes.POINTER(_QWeightC)
+    sig = {
+        "dyninfer_mi355x_open": (I, [I, ctypes.POINTER(P)]),
+        "dyninfer_mi355x_close": (I, [P]),
+        "dyninfer_mi355x_last_error": (ctypes.c_char_p, []),
+        "dyninfer_mi355x_qlinear": (I, [P, W, P, U32, U32, P, U32, P]),
+        "dyninfer_mi355x_qlinear_multi": (I, [P, W, U32, P, U32, U32, ctypes.POINTER(P), U32, P]),
+        "dyninfer_mi355x_dequant": (I, [P, W, P, P]),
+        "dyninfer_mi355x_supports": (I, [W, U32, U32, U32]),
+        "dyninfer_mi355x_candidates_json": (ctypes.c_char_p, []),
+        "dyninfer_mi355x_registry_select": (I, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, P, SZ,
+                                                ctypes.POINTER(SZ)]),
+        "dyninfer_mi355x_registry_require": (I, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, P, SZ,
+                                                 ctypes.POINTER(SZ)]),
+        "dyninfer_mi355x_version": (ctypes.c_char_p, []),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _check(rc: int) -> None:
+    if rc != OK:
+        raise DyninferError(rc, library().dyninfer_mi355x_last_error().decode())
+
+
+def block_geometry(encoding: int):
+    """(weights per block, bytes per block) of a GGUF encoding."""
+    return _GGUF_BLOCK[encoding]
+
+
+def weight_bytes(encoding: int, rows: int, cols: int, group_size: int = 64, scale_bytes: int = 2) -> int:
+    """On-disk weight bytes: the algorithmic HBM traffic of one GEMV pass."""
+    if encoding in _GGUF_BLOCK:
+        bw, bb = _GGUF_BLOCK[encoding]
+        return rows * (cols // bw) * bb
+    return rows * cols // 2 + 2 * rows * (cols // group_size) * scale_bytes
+
+
+def _ptr(t) -> Optional[int]:
+    if t is None:
+        return None
+    return t.data_ptr() if hasattr(t, "data_ptr") else int(t)
+
+
+@dataclass
+class QWeight:
+    """A quantized weight [rows = N out, cols = K in] in its on-disk bytes.
+
+    GGUF: ``data`` holds the interleaved blocks.  MLX U4: ``data`` = packed u32
+    words, ``scales``/``biases`` = [N, K/group] of ``scale_dtype``.  Tensors (or
+    raw device addresses) must stay alive while kernels use them.
+    """
+    encoding: int
+    rows: int
+    cols: int
+    data: object
+    scales: object = None
+    biases: object = None
+    group_size: int = 0
+    scale_dtype: int = DTYPE_BF16
+
+    def c(self) -> _QWeightC:
+        return _QWeightC(self.encoding, self.group_size, self.rows, self.cols, _ptr(self.data), _ptr(self.scales),
+                         _ptr(self.biases), self.scale_dtype, 0)
+
+    @property
+    def nbytes(self) -> int:
+        sb = 4 if self.scale_dtype == DTYPE_F32 else 2
+        return weight_bytes(self.encoding, self.rows, self.cols, self.group_size or 64, sb)
+
+
+def _dtype_code(t) -> int:
+    import torch
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    if t.dtype == torch.bfloat16:
+        return DTYPE_BF16
+    if t.dtype == torch.float16:
+        return DTYPE_F16
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def supports(w: QWeight, rows: int, x_dtype: int = DTYPE_F32, y_dtype: int = DTYPE_F32) -> bool:
+    wc = w.c()
+    return bool(library().dyninfer_mi355x_supports(ctypes.byref(wc), rows, x_dtype, y_dtype))
+
+
+class Context:
+    """An open library context on one gfx950 device (dyninfer_mi355x_open/close)."""
+
+    def __init__(self, device: int = 0):
+        self._lib = library()
+        self.device = device
+        h = ctypes.c_void_p()
+        _check(self._lib.dyninfer_mi355x_open(device, ctypes.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.dyninfer_mi355x_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def _stream(stream) -> Optional[int]:
+        if stream is None:
+            import torch
+            return torch.cuda.current_stream().cuda_stream
+        return stream if isinstance(stream, int) else stream.cuda_stream
+
+    def qlinear(self, w: QWeight, x, y=None, y_dtype=None, stream=None):
+        """y = x · Wᵀ (f32 accumulation).  x: [rows, K] f32 or bf16 device tensor."""
+        import torch
+        rows = x.shape[0] if x.dim() == 2 else 1
+        if y is None:
+            y = torch.empty((rows, w.rows), dtype=y_dtype or torch.float32, device=x.device)
+        wc = w.c()
+        _check(self._lib.dyninfer_mi355x_qlinear(self._h, ctypes.byref(wc), x.data_ptr(), _dtype_code(x), rows,
+                                                 y.data_ptr(), _dtype_code(y), self._stream(stream)))
+        return y
+
+    def qlinear_multi(self, ws: Sequence[QWeight], x, ys=None, y_dtype=None, stream=None):
+        """One launch for several weights sharing activation x (same encoding and K)."""
+        import torch
+        rows = x.shape[0] if x.dim() == 2 else 1
+        if ys is None:
+            ys = [torch.empty((rows, w.rows), dtype=y_dtype or torch.float32, device=x.device) for w in ws]
+        arr = (_QWeightC * len(ws))(*[w.c() for w in ws])
+        yp = (ctypes.c_void_p * len(ws))(*[y.data_ptr() for y in ys])
+        _check(self._lib.dyninfer_mi355x_qlinear_multi(self._h, arr, len(ws), x.data_ptr(), _dtype_code(x), rows,
+                                                       yp, _dtype_code(ys[0]), self._stream(stream)))
+        return ys
+
+    def dequant(self, w: QWeight, out=None, stream=None):
+        """Bit-exact f32 dequantisation of W on the device -> [rows, cols]."""
+        import torch
+        dev = torch.device("cuda", self.device)
+        if out is None:
+            out = torch.empty((w.rows, w.cols), dtype=torch.float32, device=dev)
+        wc = w.c()
+        _check(self._lib.dyninfer_mi355x_dequant(self._h, ctypes.byref(wc), out.data_ptr(), self._stream(stream)))
+        return out
+
+
+def candidates() -> list:
+    """This library's gfx950 KernelCandidateDescriptors (serde JSON)."""
+    return json.loads(library().dyninfer_mi355x_candidates_json().decode())
+
+
+def _registry(fn, request: dict, target: dict, cands) -> dict:
+    lib = library()
+    cj = None if cands is None else json.dumps(cands).encode()
+    rq, tg = json.dumps(request).encode(), json.dumps(target).encode()
+    n = ctypes.c_size_t(0)
+    rc = getattr(lib, fn)(cj, rq, tg, None, 0, ctypes.byref(n))
+    if rc not in (OK, ERR_BUFFER_TOO_SMALL):
+        _check(rc)
+    buf = ctypes.create_string_buffer(n.value + 1)
+    _check(getattr(lib, fn)(cj, rq, tg, ctypes.cast(buf, ctypes.c_void_p), n.value + 1, ctypes.byref(n)))
+    return json.loads(buf.value.decode())
+
+
+def registry_select(request: dict, target: dict, cands=None) -> dict:
+    """KernelRegistry::select over ``cands`` (default: this library's candidates) -> SelectionReport."""
+    return _registry("dyninfer_mi355x_registry_select", request, target, cands)
+
+
+def registry_require(request: dict, target: dict, cands=None) -> dict:
+    """KernelRegistry::require -> SelectedKernelCandidate, or DyninferError(ERR_UNSUPPORTED, E_KERNEL_COVERAGE…)."""
+    return _registry("dyninfer_mi355x_registry_require", request, target, cands)

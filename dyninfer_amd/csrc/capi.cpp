@@ -1,0 +1,280 @@
+// C ABI of the MI355X quantized weight-matmul library (include/dyninfer_mi355x.h).
+//
+// Host-side validation mirrors the reference's encoding checks
+// (q4_0.rs:40-113, gguf_block.rs:66-156, mlx_affine.rs:55-155): unsupported
+// encodings and shapes are rejected with DYNINFER_MI355X_ERR_UNSUPPORTED, never
+// routed to a fallback (README.md:83-84 "never falls back to CPU").
+#include "../../include/dyninfer_mi355x.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "kernels.hpp"
+#include "registry.hpp"
+
+struct dyninfer_mi355x_ctx {
+    int device;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(DYNINFER_MI355X_ERR_HIP, std::string(what) + ": " + hipGetErrorName(e) + ": " + hipGetErrorString(e));
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// Makes ctx->device current for the duration of a call, restoring the caller's.
+struct DeviceGuard {
+    int prev = -1;
+    hipError_t err = hipSuccess;
+    explicit DeviceGuard(int dev) {
+        err = hipGetDevice(&prev);
+        if (err == hipSuccess && prev != dev) err = hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+uint32_t block_weights(uint32_t enc) {
+    switch (enc) {
+    case DYNINFER_ENC_GGUF_Q4_0:
+    case DYNINFER_ENC_GGUF_Q4_1:
+    case DYNINFER_ENC_GGUF_Q8_0: return 32;
+    case DYNINFER_ENC_GGUF_Q6_K: return 256;
+    default: return 0;
+    }
+}
+
+const char* enc_name(uint32_t enc) {
+    switch (enc) {
+    case DYNINFER_ENC_GGUF_Q4_0: return "gguf.q4_0";
+    case DYNINFER_ENC_GGUF_Q4_1: return "gguf.q4_1";
+    case DYNINFER_ENC_GGUF_Q8_0: return "gguf.q8_0";
+    case DYNINFER_ENC_GGUF_Q6_K: return "gguf.q6_k";
+    case DYNINFER_ENC_MLX_AFFINE_U4: return "mlx.affine.u4";
+    default: return "unknown";
+    }
+}
+
+// Validates a weight descriptor.  Returns 0 or an error code (message set).
+int check_weight(const dyninfer_qweight_t* w) {
+    if (!w) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "weight descriptor is NULL");
+    if (w->rows == 0 || w->cols == 0)
+        return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "weight has an empty dimension");
+    if (w->rows > 0xFFFFFFFFull || w->cols > 0x7FFFFFFFull)
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "weight dimensions exceed the 32-bit kernel indexing");
+    if (!w->data) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "weight data pointer is NULL");
+    const uint32_t bw = block_weights(w->encoding);
+    if (bw) {
+        if (w->cols % bw)
+            return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
+                        std::string(enc_name(w->encoding)) + ": logical axis 1 (" + std::to_string(w->cols) +
+                            ") is not a multiple of the block size " + std::to_string(bw));
+        const uintptr_t need = w->encoding == DYNINFER_ENC_GGUF_Q4_1 ? 4 : 2;
+        if (!aligned(w->data, need))
+            return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string(enc_name(w->encoding)) +
+                                                                  ": block data must be " + std::to_string(need) +
+                                                                  "-byte aligned");
+        return 0;
+    }
+    if (w->encoding != DYNINFER_ENC_MLX_AFFINE_U4)
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "unsupported encoding " + std::to_string(w->encoding));
+    if (w->group_size == 0 || w->group_size % 32 || w->cols % w->group_size)
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
+                    "mlx.affine.u4: group size must be a positive multiple of 32 dividing the logical axis");
+    if (!w->scales || !w->biases)
+        return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "mlx.affine.u4: scales and biases are required");
+    uintptr_t es;
+    switch (w->scale_dtype) {
+    case DYNINFER_DTYPE_F32: es = 4; break;
+    case DYNINFER_DTYPE_F16:
+    case DYNINFER_DTYPE_BF16: es = 2; break;
+    default: return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "mlx.affine.u4: scale dtype must be f32, f16 or bf16");
+    }
+    if (!aligned(w->data, 4) || !aligned(w->scales, es) || !aligned(w->biases, es))
+        return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "mlx.affine.u4: component pointers are misaligned");
+    return 0;
+}
+
+// Activation/output dtype rules.  GGUF weights take f32 activations (the
+// reference's all-f32 contract for quantized linears,
+// crates/dyninfer-compiler/src/lib.rs:289-306); Q4_0 additionally takes bf16
+// activations on its MFMA path.  MLX U4 takes f32 or bf16.
+int check_io(uint32_t enc, uint32_t count, uint32_t x_dtype, uint32_t y_dtype, uint32_t rows) {
+    if (rows == 0) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "rows must be >= 1");
+    if (x_dtype != DYNINFER_DTYPE_F32 && x_dtype != DYNINFER_DTYPE_BF16)
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "activations must be f32 or bf16");
+    if (y_dtype != DYNINFER_DTYPE_F32 && y_dtype != DYNINFER_DTYPE_BF16)
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "outputs must be f32 or bf16");
+    if (x_dtype == DYNINFER_DTYPE_BF16 && enc != DYNINFER_ENC_MLX_AFFINE_U4 &&
+        !(enc == DYNINFER_ENC_GGUF_Q4_0 && count == 1))
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
+                    std::string(enc_name(enc)) + ": bf16 activations are supported for single gguf.q4_0 weights "
+                                                 "(MFMA path) and mlx.affine.u4 only; pass f32 activations");
+    return 0;
+}
+
+int check_ctx(dyninfer_mi355x_ctx_t* ctx) {
+    if (!ctx) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "context is NULL");
+    return 0;
+}
+
+dmx::GemvProblem problem_of(const dyninfer_qweight_t* w, void* y) {
+    dmx::GemvProblem p;
+    p.w = static_cast<const uint8_t*>(w->data);
+    p.sc = static_cast<const uint8_t*>(w->scales);
+    p.bi = static_cast<const uint8_t*>(w->biases);
+    p.y = y;
+    p.n = (uint32_t)w->rows;
+    return p;
+}
+
+size_t esize(uint32_t dt) { return dt == DYNINFER_DTYPE_F32 ? 4 : 2; }
+
+// Runs rows > 16 through the GEMV kernels 16 activation rows at a time.
+hipError_t gemv_rows(const dyninfer_qweight_t* ws, uint32_t count, const void* x, uint32_t x_dtype, uint32_t rows,
+                     void* const* ys, uint32_t y_dtype, hipStream_t st) {
+    const uint32_t K = (uint32_t)ws[0].cols;
+    for (uint32_t r0 = 0; r0 < rows; r0 += dmx::kMaxGemvBatch) {
+        const uint32_t nb = rows - r0 < (uint32_t)dmx::kMaxGemvBatch ? rows - r0 : (uint32_t)dmx::kMaxGemvBatch;
+        dmx::GemvProblem probs[dmx::kMaxProblems];
+        for (uint32_t i = 0; i < count; i++)
+            probs[i] = problem_of(&ws[i], static_cast<uint8_t*>(ys[i]) + (size_t)r0 * ws[i].rows * esize(y_dtype));
+        const void* xr = static_cast<const uint8_t*>(x) + (size_t)r0 * K * esize(x_dtype);
+        hipError_t e = dmx::gemv_launch(ws[0].encoding, probs, (int)count, K, xr, x_dtype == DYNINFER_DTYPE_BF16, nb,
+                                        y_dtype == DYNINFER_DTYPE_BF16, ws[0].group_size, ws[0].scale_dtype, st);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dyninfer_mi355x_last_error(void) { return g_last_error.c_str(); }
+
+const char* dyninfer_mi355x_version(void) { return "dyninfer-mi355x 0.1.0 (gfx950); kernel-registry 6"; }
+
+int dyninfer_mi355x_open(int device, dyninfer_mi355x_ctx_t** out_ctx) {
+    if (!out_ctx) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "out_ctx is NULL");
+    *out_ctx = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (device < 0 || device >= count)
+        return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT,
+                    "device " + std::to_string(device) + " out of range (" + std::to_string(count) + " devices)");
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(DYNINFER_MI355X_ERR_DEVICE,
+                    std::string("device is ") + prop.gcnArchName + "; this library's kernels are built for gfx950 only");
+    *out_ctx = new dyninfer_mi355x_ctx{device};
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_close(dyninfer_mi355x_ctx_t* ctx) {
+    delete ctx;
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_supports(const dyninfer_qweight_t* w, uint32_t rows, uint32_t x_dtype, uint32_t y_dtype) {
+    if (check_weight(w) || check_io(w->encoding, 1, x_dtype, y_dtype, rows)) return 0;
+    return 1;
+}
+
+int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws, uint32_t count,
+                                  const void* x, uint32_t x_dtype, uint32_t rows, void* const* ys, uint32_t y_dtype,
+                                  void* stream) {
+    if (int rc = check_ctx(ctx)) return rc;
+    if (!ws || count == 0 || count > (uint32_t)dmx::kMaxProblems)
+        return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "count must be 1..4 with a weight array");
+    if (!x || !ys) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "x / y pointers are NULL");
+    for (uint32_t i = 0; i < count; i++) {
+        if (int rc = check_weight(&ws[i])) return rc;
+        if (!ys[i]) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "output pointer is NULL");
+        if (!aligned(ys[i], esize(y_dtype))) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "output is misaligned");
+        if (ws[i].encoding != ws[0].encoding || ws[i].cols != ws[0].cols ||
+            (ws[0].encoding == DYNINFER_ENC_MLX_AFFINE_U4 &&
+             (ws[i].group_size != ws[0].group_size || ws[i].scale_dtype != ws[0].scale_dtype)))
+            return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT,
+                        "grouped weights must share encoding, K, group size and scale dtype");
+    }
+    if (int rc = check_io(ws[0].encoding, count, x_dtype, y_dtype, rows)) return rc;
+    if (!aligned(x, 16)) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "activations must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    if (ws[0].encoding == DYNINFER_ENC_GGUF_Q4_0 && x_dtype == DYNINFER_DTYPE_BF16) {
+        // Q4_0 with bf16 activations: dequant-to-LDS + f16 MFMA for any row count.
+        e = dmx::gemm_q4_0_launch(static_cast<const uint8_t*>(ws[0].data), (uint32_t)ws[0].rows,
+                                  (uint32_t)ws[0].cols, x, rows, ys[0], y_dtype == DYNINFER_DTYPE_BF16, st);
+    } else {
+        e = gemv_rows(ws, count, x, x_dtype, rows, ys, y_dtype, st);
+    }
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_qlinear(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* w, const void* x, uint32_t x_dtype,
+                            uint32_t rows, void* y, uint32_t y_dtype, void* stream) {
+    void* ys[1] = {y};
+    return dyninfer_mi355x_qlinear_multi(ctx, w, 1, x, x_dtype, rows, ys, y_dtype, stream);
+}
+
+int dyninfer_mi355x_dequant(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* w, float* out, void* stream) {
+    if (int rc = check_ctx(ctx)) return rc;
+    if (int rc = check_weight(w)) return rc;
+    if (!out || !aligned(out, 4)) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "output is NULL or misaligned");
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipError_t e = dmx::dequant_launch(w->encoding, static_cast<const uint8_t*>(w->data),
+                                       static_cast<const uint8_t*>(w->scales), static_cast<const uint8_t*>(w->biases),
+                                       (uint32_t)w->rows, (uint32_t)w->cols, w->group_size, w->scale_dtype, out,
+                                       static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "dequant launch");
+    return DYNINFER_MI355X_OK;
+}
+
+const char* dyninfer_mi355x_candidates_json(void) { return dmx::candidates_json().c_str(); }
+
+static int registry_call(const char* c, const char* r, const char* t, char* out, size_t cap, size_t* len, bool req) {
+    if (!r || !t) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "request / target JSON is NULL");
+    std::string res, err;
+    const int rc = dmx::registry_select(c, r, t, req, res, err);
+    if (rc == 1) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, err);
+    if (rc == 2) return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, err);
+    if (len) *len = res.size();
+    if (!out || cap < res.size() + 1)
+        return fail(DYNINFER_MI355X_ERR_BUFFER_TOO_SMALL, "output buffer needs " + std::to_string(res.size() + 1) + " bytes");
+    std::memcpy(out, res.c_str(), res.size() + 1);
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_registry_select(const char* candidates_json, const char* request_json, const char* target_json,
+                                    char* out, size_t out_cap, size_t* out_len) {
+    return registry_call(candidates_json, request_json, target_json, out, out_cap, out_len, false);
+}
+
+int dyninfer_mi355x_registry_require(const char* candidates_json, const char* request_json, const char* target_json,
+                                     char* out, size_t out_cap, size_t* out_len) {
+    return registry_call(candidates_json, request_json, target_json, out, out_cap, out_len, true);
+}
+
+}  // extern "C"

@@ -1,0 +1,82 @@
+// Shared gfx950 device helpers for the quantized weight-matmul kernels.
+//
+// Encodings are consumed in their on-disk byte layout (no repack):
+//   GGUF blocks (gguf_codegen.rs:15-48): Q4_0 18 B / 32 w, Q4_1 20 B / 32 w,
+//   Q8_0 34 B / 32 w, Q6_K 210 B / 256 w; row o, block b at (o*K/B + b)*bytes.
+//   MLX affine U4: packed u32 [N, K/8] + scales/biases [N, K/g].
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dmx {
+
+// Multi-dword vector types that only promise 4-byte alignment: GGUF blocks are
+// 2-byte aligned, so every weight load is issued from the 4-byte-aligned dword
+// that contains the block start and realigned in registers.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+
+// A generic pointer re-typed as a global-memory (address space 1) pointer, so
+// loads compile to global_load_* instead of flat_load_*.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(const void* p) {
+    return (const __attribute__((address_space(1))) T*)(p);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
+    return (float)h;  // v_cvt_f32_f16: exact widening (arith.extf)
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
+    return __uint_as_float(bits << 16);
+}
+
+// f32 -> bf16 round-to-nearest-even (NaN quieted).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// Byte lane i of a dword as float (v_cvt_f32_ubyte{0..3}).
+template <int I>
+__device__ __forceinline__ float ubyte_f32(uint32_t v) {
+    return (float)((v >> (8 * I)) & 0xFFu);
+}
+
+// Load NDW consecutive dwords starting at a 4-byte-aligned address.  Every
+// dword read overlaps the block being read, so no read leaves the page of a
+// valid byte.
+template <int NDW>
+__device__ __forceinline__ void load_dwords(const uint32_t* __restrict__ p, uint32_t (&d)[NDW]) {
+#pragma unroll
+    for (int i = 0; i + 4 <= NDW; i += 4) {
+        u32x4_a4 v = *gptr<u32x4_a4>(p + i);
+        d[i] = v.x; d[i + 1] = v.y; d[i + 2] = v.z; d[i + 3] = v.w;
+    }
+    constexpr int R = NDW & 3;
+    constexpr int B0 = NDW - R;
+    if constexpr (R == 3) {
+        u32x2_a4 v = *gptr<u32x2_a4>(p + B0);
+        d[B0] = v.x; d[B0 + 1] = v.y; d[B0 + 2] = *gptr<uint32_t>(p + B0 + 2);
+    } else if constexpr (R == 2) {
+        u32x2_a4 v = *gptr<u32x2_a4>(p + B0);
+        d[B0] = v.x; d[B0 + 1] = v.y;
+    } else if constexpr (R == 1) {
+        d[B0] = *gptr<uint32_t>(p + B0);
+    }
+}
+
+// Realign NDW raw dwords (loaded from the aligned dword containing the block
+// start) by `sh` bytes (0 or 2) so that e[0] holds block bytes 0..3.  The last
+// dword only needs its low half (blocks with bytes % 4 == 2).
+template <int NDW>
+__device__ __forceinline__ void realign(const uint32_t (&raw)[NDW], uint32_t sh, uint32_t (&e)[NDW]) {
+#pragma unroll
+    for (int i = 0; i + 1 < NDW; i++) e[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
+    e[NDW - 1] = __builtin_amdgcn_alignbyte(raw[NDW - 1], raw[NDW - 1], sh);
+}
+
+}  // namespace dmx

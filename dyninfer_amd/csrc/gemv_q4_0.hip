@@ -1,0 +1,8 @@
+// Decode GEMV instantiations for GGUF Q4_0 (kernel templates in gemv_kernels.hpp).
+#include "gemv_kernels.hpp"
+
+namespace dmx {
+hipError_t gemv_launch_q4_0(const GemvParams& p, uint32_t B, bool xbf16, hipStream_t st) {
+    return launch_gguf_gemv<EncQ40, 16>(p, B, xbf16, st);
+}
+}  // namespace dmx

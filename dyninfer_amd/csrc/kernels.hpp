@@ -1,0 +1,60 @@
+// Internal host-side interface between the C ABI (capi.cpp) and the kernel
+// translation units.  Not part of the public boundary.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dmx {
+
+constexpr int kMaxProblems = 4;  // weights sharing one activation per GEMV launch
+constexpr int kMaxGemvBatch = 16;
+
+enum Enc : uint32_t { ENC_Q4_0 = 2, ENC_Q4_1 = 3, ENC_Q8_0 = 8, ENC_Q6_K = 14, ENC_MLX_U4 = 0x1004 };
+enum DType : uint32_t { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+
+// Kernel parameters of one GEMV launch (passed by value as the kernel argument).
+struct GemvParams {
+    const uint8_t* w[kMaxProblems];   // GGUF blocks, or MLX packed words
+    const uint8_t* sc[kMaxProblems];  // MLX scales
+    const uint8_t* bi[kMaxProblems];  // MLX biases
+    void* y[kMaxProblems];
+    uint32_t n[kMaxProblems];
+    uint32_t rb_begin[kMaxProblems];  // first row block of each problem
+    uint32_t total_rb;                // row blocks over all problems
+    uint32_t nprob;
+    const void* x;
+    uint32_t K;
+    uint32_t ldx;         // activation row stride, elements
+    uint32_t ldy;         // output row stride, elements (per problem: its N)
+    uint32_t batch;       // activation rows actually present (<= kernel's B)
+    uint32_t lanes_log2;  // lanes cooperating on one weight row (L = 2^lanes_log2 divides K/chunk)
+    uint32_t y_bf16;      // store bf16 instead of f32
+    uint32_t group;       // MLX group size
+    uint32_t sdtype;      // MLX scale/bias dtype
+};
+
+struct GemvProblem {
+    const uint8_t* w;
+    const uint8_t* sc;
+    const uint8_t* bi;
+    void* y;
+    uint32_t n;
+};
+
+// Decode GEMV: y_i[r, :] = x[r, :] · W_iᵀ for r < batch (<= 16).
+hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x,
+                       bool x_bf16, uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype,
+                       hipStream_t stream);
+
+// Bit-exact dequantisation to f32 [N, K].
+hipError_t dequant_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, const uint8_t* bi, uint32_t N,
+                          uint32_t K, uint32_t group, uint32_t sdtype, float* out, hipStream_t stream);
+
+// Q4_0 prefill GEMM on MFMA: Y[M, N] = X[M, K] · Wᵀ, X bf16, Y f32 or bf16.
+hipError_t gemm_q4_0_launch(const uint8_t* w, uint32_t N, uint32_t K, const void* x, uint32_t M,
+                            void* y, bool y_bf16, hipStream_t stream);
+
+// Shape limits of the GEMM kernel (checked by the C ABI before launching).
+bool gemm_q4_0_supported(uint32_t N, uint32_t K, uint32_t M);
+
+}  // namespace dmx

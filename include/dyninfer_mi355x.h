@@ -1,0 +1,177 @@
+/*
+ * dyninfer_mi355x.h — C ABI of the MI355X (gfx950) quantized weight-matmul library.
+ *
+ * Drop-in boundary for dyninfer's `rocm` target.  Today the reference lowers a
+ * quantized linear to IREE-generated code: the selected kernel's lowering id is
+ * dispatched by ParameterLowerings::emit_linear_call
+ * (crates/dyninfer-compiler/src/lowering/parameter.rs:141-183) to the encoding's
+ * MLIR emitter (crates/dyninfer-quantization/src/quantizations/gguf_codegen.rs:268-314,
+ * mlx_affine.rs:557-626) and run through the IREE runtime C wrapper
+ * (third_party/iree_runtime_c_api/wrapper.h:74-105).  This library replaces that
+ * generated code for lowering ids ending in `.mi355x_hip`: the runtime calls the
+ * entry points below with device pointers to the weight's exact on-disk bytes.
+ *
+ * Conventions (mirroring third_party/iree_runtime_c_api/wrapper.h:38-63):
+ *   - every entry point returns an int status, 0 = success;
+ *   - on failure dyninfer_mi355x_last_error() returns a message for the calling
+ *     thread (thread-local, unlike the wrapper's process-global g_last_error,
+ *     wrapper.c:238);
+ *   - opaque context handle with open/close pair (wrapper.h:39-60);
+ *   - all buffers are caller-owned device memory; the library never repacks or
+ *     copies weights and keeps no allocation between calls (README.md:5-9,
+ *     crates/dyninfer-compiler/src/lib.rs:630);
+ *   - work is enqueued asynchronously on the caller's HIP stream (`stream` is a
+ *     hipStream_t passed as void*; NULL = the null stream); concurrent calls on
+ *     distinct streams are allowed; there is no CPU fallback (README.md:83-84).
+ */
+#ifndef DYNINFER_MI355X_H
+#define DYNINFER_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+enum {
+    DYNINFER_MI355X_OK = 0,
+    DYNINFER_MI355X_ERR_INVALID_ARGUMENT = 1, /* null pointer, zero size, bad dtype, misaligned base */
+    DYNINFER_MI355X_ERR_UNSUPPORTED = 2,      /* encoding / shape outside the qualified envelope
+                                                  (E_UNSUPPORTED_ENCODING, crates/dyninfer-error/src/lib.rs:54-72) */
+    DYNINFER_MI355X_ERR_HIP = 3,              /* HIP runtime error; message carries hipGetErrorString */
+    DYNINFER_MI355X_ERR_DEVICE = 4,           /* device is not gfx950 */
+    DYNINFER_MI355X_ERR_BUFFER_TOO_SMALL = 5  /* output string buffer too small (registry calls) */
+};
+
+/* Encodings.  GGUF values are the GGML type codes
+ * (crates/dyninfer-checkpoint-gguf/src/types.rs:10-43). */
+enum {
+    DYNINFER_ENC_GGUF_Q4_0 = 2,
+    DYNINFER_ENC_GGUF_Q4_1 = 3,
+    DYNINFER_ENC_GGUF_Q8_0 = 8,
+    DYNINFER_ENC_GGUF_Q6_K = 14,
+    DYNINFER_ENC_MLX_AFFINE_U4 = 0x1004
+};
+
+/* Element types of activations, outputs and MLX scales/biases. */
+enum { DYNINFER_DTYPE_F32 = 0, DYNINFER_DTYPE_F16 = 1, DYNINFER_DTYPE_BF16 = 2 };
+
+/*
+ * A quantized weight, logically [rows = out features N, cols = in features K],
+ * row-major, "native" orientation (crates/dyninfer-kernel-registry/src/lib.rs:84-89).
+ *
+ * GGUF (PhysicalEncoding::BlockQuantized, crates/dyninfer-checkpoint-gguf/src/convention.rs:200-279):
+ *   `data` = the tensor's interleaved blocks, N*(K/B)*bytes_per_block bytes; row o, block b
+ *   starts at byte (o*K/B + b)*bytes_per_block (gguf_codegen.rs:350-367).  `data` must be
+ *   2-byte aligned (4-byte for Q4_1).  scales/biases/group_size/scale_dtype are ignored.
+ * MLX affine U4 (PhysicalEncoding::GroupQuantized, crates/dyninfer-checkpoint-safetensors/src/mlx.rs:152-261):
+ *   `data` = packed u32 [N, K/8] (lane i = bits 4i..4i+3), `scales`, `biases` = [N, K/group_size]
+ *   of `scale_dtype` (f32/f16/bf16), each aligned to its element size.
+ */
+typedef struct dyninfer_qweight {
+    uint32_t encoding;
+    uint32_t group_size;  /* MLX only */
+    uint64_t rows;        /* N */
+    uint64_t cols;        /* K */
+    const void* data;
+    const void* scales;   /* MLX only */
+    const void* biases;   /* MLX only */
+    uint32_t scale_dtype; /* MLX only */
+    uint32_t reserved;
+} dyninfer_qweight_t;
+
+typedef struct dyninfer_mi355x_ctx dyninfer_mi355x_ctx_t;
+
+/* Open a context on HIP device `device` (must be gfx950).  Mirrors
+ * dyninfer_iree_session_create (wrapper.h:39-58) minus module loading: the
+ * kernels are linked into this library. */
+int dyninfer_mi355x_open(int device, dyninfer_mi355x_ctx_t** out_ctx);
+int dyninfer_mi355x_close(dyninfer_mi355x_ctx_t* ctx);
+
+/* Thread-local message for the last failing call on this thread ("" if none).
+ * Mirrors dyninfer_iree_last_error (wrapper.h:62-63). */
+const char* dyninfer_mi355x_last_error(void);
+
+/*
+ * y = x · Wᵀ with f32 accumulation: y[r, o] = Σ_k x[r, k] · w[o, k] where w is the
+ * reference's dequantised value (gguf_codegen.rs:268-314 `emit_linear`;
+ * mlx_affine.rs:557-626 `emit_linear_u4`; output projection = the same helper,
+ * gguf_codegen.rs:157-159).  `rows` = activation rows (1..16 for decode; any for prefill).
+ * x: [rows, K] row-major, dtype x_dtype (f32 or bf16); y: [rows, N], dtype y_dtype
+ * (f32 or bf16).  rows <= 16 runs the decode GEMV kernels (VALU, HBM-bound);
+ * rows >= 17 runs the prefill path (Q4_0: dequant-to-LDS + MFMA; other encodings: the
+ * GEMV kernels over row chunks).
+ */
+int dyninfer_mi355x_qlinear(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* w,
+                            const void* x, uint32_t x_dtype, uint32_t rows,
+                            void* y, uint32_t y_dtype, void* stream);
+
+/*
+ * Several weights that share one activation (q/k/v, gate/up) in a single launch:
+ * y_i = x · W_iᵀ for i < count.  All weights must have the same encoding (and group
+ * size / scale dtype) and the same K; N may differ.  count <= 4, rows <= 16.
+ * No reference counterpart as one call: the reference emits one helper call per
+ * linear (parameter.rs:141-183); this is the same arithmetic batched into one launch.
+ */
+int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws,
+                                  uint32_t count, const void* x, uint32_t x_dtype, uint32_t rows,
+                                  void* const* ys, uint32_t y_dtype, void* stream);
+
+/*
+ * Dequantise W to f32 [N, K] on the device, bit-exactly as the reference's
+ * lowering does (gguf_codegen.rs:350-526 `emit_dequant`; mlx_affine.rs:593-598).
+ * The qualification hook for bit-exact tests; not on the hot path.
+ */
+int dyninfer_mi355x_dequant(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* w,
+                            float* out, void* stream);
+
+/*
+ * 1 if (w, rows, x_dtype, y_dtype) is inside the qualified envelope, else 0 (and
+ * last_error says why).  Host-only; same rules as the validation in
+ * q4_0.rs:40-113 / gguf_block.rs:66-156 / mlx_affine.rs:55-155 plus this
+ * library's shape limits.  Pointers are checked for alignment only.
+ */
+int dyninfer_mi355x_supports(const dyninfer_qweight_t* w, uint32_t rows, uint32_t x_dtype,
+                             uint32_t y_dtype);
+
+/*
+ * Kernel-registry candidates qualified for gfx950, as a JSON array of serde
+ * KernelCandidateDescriptor objects (crates/dyninfer-kernel-registry/src/lib.rs:132-149),
+ * the counterpart of QuantizationDefinition::kernel_candidates
+ * (gguf_codegen.rs:50-113, mlx_affine.rs:157-238).  Static storage; never free it.
+ */
+const char* dyninfer_mi355x_candidates_json(void);
+
+/*
+ * C++ restatement of KernelRegistry::select (crates/dyninfer-kernel-registry/src/lib.rs:302-348),
+ * rejection_reasons (:499-584) and DeterministicCostModel (:249-268) over serde JSON:
+ *   candidates_json: JSON array of KernelCandidateDescriptor (NULL = this library's own set)
+ *   request_json:    KernelRequest object (:152-167)
+ *   target_json:     TargetProfile object (crates/dyninfer-core/src/types.rs:244-272; driver,
+ *                    architecture, features are read)
+ * Writes a SelectionReport object (:218-223) to out (NUL-terminated) and its length
+ * to *out_len.  Duplicate candidate ids fail like KernelRegistry::register (:283-296).
+ */
+int dyninfer_mi355x_registry_select(const char* candidates_json, const char* request_json,
+                                    const char* target_json, char* out, size_t out_cap,
+                                    size_t* out_len);
+
+/*
+ * KernelRegistry::require (lib.rs:350-399): like registry_select but writes the
+ * SelectedKernelCandidate object, and when nothing is selected returns
+ * DYNINFER_MI355X_ERR_UNSUPPORTED with last_error starting "E_KERNEL_COVERAGE".
+ */
+int dyninfer_mi355x_registry_require(const char* candidates_json, const char* request_json,
+                                     const char* target_json, char* out, size_t out_cap,
+                                     size_t* out_len);
+
+/* Library version string and the KernelRegistry::VERSION this registry expects ("6"). */
+const char* dyninfer_mi355x_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DYNINFER_MI355X_H */

@@ -1,0 +1,238 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars (written here as the tests use them):
+  * dequantisation: bit-exact (every f32 bit pattern) with the oracle's
+    restatement of the reference's MLIR dequant bodies;
+  * GEMV / GEMM outputs: max over outputs of |y - y_ref| / Σ_k |w||x| <= 2e-3,
+    y_ref the f64 contraction of the exactly dequantised weights (the
+    north-star tolerance).  The f32 GEMV paths are also held to 1e-4, far
+    tighter than the contract, so a dropped or mis-scaled block cannot hide.
+"""
+import numpy as np
+import pytest
+import torch
+
+import dyninfer_amd as d
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+TIGHT = 1e-4
+ENC = {oracle.Q4_0: d.ENC_Q4_0, oracle.Q4_1: d.ENC_Q4_1, oracle.Q8_0: d.ENC_Q8_0, oracle.Q6_K: d.ENC_Q6_K}
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def offset_bytes(data: np.ndarray, off: int):
+    """Device copy of `data` starting `off` bytes into a larger buffer (keeps the buffer alive)."""
+    buf = torch.zeros(data.size + 16, dtype=torch.uint8, device="cuda")
+    buf[off:off + data.size] = dev(data)
+    return buf, buf.data_ptr() + off
+
+
+def gguf(gtype, n, k, seed, off=0):
+    data = oracle.synth_gguf(gtype, n, k, seed)
+    if off:
+        buf, ptr = offset_bytes(data, off)
+        w = d.QWeight(ENC[gtype], n, k, ptr)
+        w._keep = buf
+    else:
+        w = d.QWeight(ENC[gtype], n, k, dev(data))
+    return w, data
+
+
+def assert_bits_equal(got: np.ndarray, ref: np.ndarray):
+    g = got.view(np.uint32)
+    r = ref.view(np.uint32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    bad = (g != r) & ~nan
+    assert not bad.any(), f"{bad.sum()} differing elements, first at {np.argwhere(bad)[0]}: " \
+                          f"got {got[tuple(np.argwhere(bad)[0])]} ref {ref[tuple(np.argwhere(bad)[0])]}"
+
+
+def gemv_err(y: np.ndarray, x: np.ndarray, w: np.ndarray) -> float:
+    y64, absdot = oracle.linear_f64(x, w)
+    return oracle.normalized_error(y, y64, absdot)
+
+
+# ----------------------------------------------------------------- dequant
+@pytest.mark.parametrize("gtype", oracle.GGUF_TYPES, ids=oracle.NAMES.get)
+@pytest.mark.parametrize("n,k,off", [(1, 256, 0), (3, 256, 0), (64, 512, 0), (5, 256, 2), (33, 768, 2), (7, 1024, 0)])
+def test_dequant_gguf_bit_exact(ctx, gtype, n, k, off):
+    if gtype == oracle.Q4_1 and off % 4:
+        pytest.skip("Q4_1 blocks are 4-byte aligned by contract")
+    w, data = gguf(gtype, n, k, seed=n * 7 + k, off=off)
+    got = ctx.dequant(w).cpu().numpy()
+    assert_bits_equal(got, oracle.dequant_gguf(gtype, data, n, k))
+
+
+def _special_scale_blocks(gtype, scales):
+    bw, bb = oracle.BLOCK[gtype]
+    rows = len(scales)
+    data = oracle.synth_gguf(gtype, rows, bw, 99).reshape(rows, bb)
+    pos = 208 if gtype == oracle.Q6_K else 0
+    for i, s in enumerate(scales):
+        data[i, pos] = s & 0xFF
+        data[i, pos + 1] = s >> 8
+    if gtype == oracle.Q4_0:  # include code 8 (weight exactly zero) in every block
+        data[:, 2] = (data[:, 2] & 0xF0) | 0x08
+    return data.ravel(), rows, bw
+
+
+@pytest.mark.parametrize("gtype", oracle.GGUF_TYPES, ids=oracle.NAMES.get)
+def test_dequant_special_scales(ctx, gtype):
+    # -0, +0, smallest subnormal, largest subnormal, 1.0, -2.5, max, +inf, -inf, NaN
+    scales = [0x8000, 0x0000, 0x0001, 0x03FF, 0x3C00, 0xC100, 0x7BFF, 0x7C00, 0xFC00, 0x7E00]
+    data, rows, k = _special_scale_blocks(gtype, scales)
+    w = d.QWeight(ENC[gtype], rows, k, dev(data))
+    assert_bits_equal(ctx.dequant(w).cpu().numpy(), oracle.dequant_gguf(gtype, data, rows, k))
+
+
+@pytest.mark.parametrize("sdtype", [oracle.D_BF16, oracle.D_F16, oracle.D_F32])
+@pytest.mark.parametrize("n,k,g", [(3, 64, 32), (17, 256, 64), (8, 512, 128)])
+def test_dequant_mlx_bit_exact(ctx, sdtype, n, k, g):
+    packed, sc, bi = oracle.synth_mlx_u4(n, k, g, sdtype, seed=n + k + g)
+    w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), g, sdtype)
+    assert_bits_equal(ctx.dequant(w).cpu().numpy(), oracle.dequant_mlx_u4(packed, sc, bi, sdtype, n, k, g))
+
+
+# ----------------------------------------------------------------- GEMV
+GEMV_SHAPES = [(1, 256), (67, 512), (1024, 1024), (3072, 1024), (1024, 3072), (513, 4096)]
+
+
+@pytest.mark.parametrize("gtype", oracle.GGUF_TYPES, ids=oracle.NAMES.get)
+@pytest.mark.parametrize("n,k", GEMV_SHAPES)
+@pytest.mark.parametrize("batch", [1, 4, 16])
+def test_gemv_gguf(ctx, gtype, n, k, batch):
+    w, data = gguf(gtype, n, k, seed=1000 + n + k + batch)
+    x = oracle.randn(batch * k, seed=n * 31 + batch).reshape(batch, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    err = gemv_err(y, x, oracle.dequant_gguf(gtype, data, n, k))
+    assert err <= TOL and err <= TIGHT, err
+
+
+@pytest.mark.parametrize("gtype", oracle.GGUF_TYPES, ids=oracle.NAMES.get)
+@pytest.mark.parametrize("batch", [2, 3, 5, 7, 9, 12, 15])
+def test_gemv_gguf_odd_batches(ctx, gtype, batch):
+    n, k = 300, 1024
+    w, data = gguf(gtype, n, k, seed=77 + batch, off=2 if gtype != oracle.Q4_1 else 0)
+    x = oracle.randn(batch * k, seed=batch).reshape(batch, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    err = gemv_err(y, x, oracle.dequant_gguf(gtype, data, n, k))
+    assert err <= TIGHT, err
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_gemv_multi_qkv(ctx, batch):
+    # q/k/v of Qwen3-0.6B share one activation: one launch, three outputs
+    k = 1024
+    shapes = [2048, 1024, 1024]
+    ws, datas = zip(*[gguf(oracle.Q4_0, n, k, seed=5 + i) for i, n in enumerate(shapes)])
+    x = oracle.randn(batch * k, seed=11).reshape(batch, k)
+    ys = ctx.qlinear_multi(list(ws), dev(x))
+    for y, data, n in zip(ys, datas, shapes):
+        err = gemv_err(y.cpu().numpy(), x, oracle.dequant_gguf(oracle.Q4_0, data, n, k))
+        assert err <= TIGHT, err
+
+
+@pytest.mark.parametrize("sdtype", [oracle.D_BF16, oracle.D_F16, oracle.D_F32])
+@pytest.mark.parametrize("n,k,g", [(1, 64, 64), (1024, 1024, 64), (3072, 1024, 64), (1024, 3072, 64), (96, 512, 32),
+                                   (40, 512, 128)])
+@pytest.mark.parametrize("batch", [1, 8, 16])
+def test_gemv_mlx_bf16_io(ctx, sdtype, n, k, g, batch):
+    packed, sc, bi = oracle.synth_mlx_u4(n, k, g, sdtype, seed=n + k + batch)
+    w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), g, sdtype)
+    xb = oracle.f32_to_bf16_bits(oracle.randn(batch * k, seed=batch + 3)).reshape(batch, k)
+    x = oracle.bf16_bits_to_f32(xb)
+    y = ctx.qlinear(w, dev(xb).view(torch.bfloat16), y_dtype=torch.bfloat16)
+    y = y.view(torch.int16).cpu().numpy().view(np.uint16)
+    # bf16 output: one RNE rounding of the f32 accumulation (relative 2^-9 of |y|)
+    wf = oracle.dequant_mlx_u4(packed, sc, bi, sdtype, n, k, g)
+    y64, absdot = oracle.linear_f64(x, wf)
+    yf = oracle.bf16_bits_to_f32(y).reshape(batch, n)
+    err = np.abs(yf - y64) / np.where(absdot > 0, absdot, 1)
+    rounding = np.abs(y64) * 2.0 ** -8 / np.where(absdot > 0, absdot, 1)
+    assert np.all(err <= TOL + rounding), err.max()
+
+
+def test_gemv_mlx_f32_io(ctx):
+    n, k, g = 257, 2048, 64
+    packed, sc, bi = oracle.synth_mlx_u4(n, k, g, oracle.D_BF16, seed=4)
+    w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), g, oracle.D_BF16)
+    x = oracle.randn(4 * k, seed=9).reshape(4, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    assert gemv_err(y, x, oracle.dequant_mlx_u4(packed, sc, bi, oracle.D_BF16, n, k, g)) <= TIGHT
+
+
+# ----------------------------------------------------------------- GEMM (Q4_0 MFMA)
+@pytest.mark.parametrize("m,n,k", [(1, 128, 64), (17, 130, 96), (128, 256, 512), (200, 384, 1024), (512, 3072, 1024),
+                                   (512, 1024, 3072), (128, 2048, 1024), (2048, 1024, 1024)])
+@pytest.mark.parametrize("ybf16", [False, True])
+def test_gemm_q4_0(ctx, m, n, k, ybf16):
+    w, data = gguf(oracle.Q4_0, n, k, seed=m + n + k)
+    xb = oracle.f32_to_bf16_bits(oracle.randn(m * k, seed=m)).reshape(m, k)
+    x = oracle.bf16_bits_to_f32(xb)
+    y = ctx.qlinear(w, dev(xb).view(torch.bfloat16), y_dtype=torch.bfloat16 if ybf16 else torch.float32)
+    if ybf16:
+        y = oracle.bf16_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16))
+    else:
+        y = y.cpu().numpy()
+    wf = oracle.dequant_gguf(oracle.Q4_0, data, n, k)
+    y64, absdot = oracle.linear_f64(x, wf)
+    den = np.where(absdot > 0, absdot, 1)
+    extra = np.abs(y64) * 2.0 ** -8 / den if ybf16 else 0.0
+    err = np.abs(y.astype(np.float64) - y64) / den
+    assert np.all(err <= TOL + extra), err.max()
+
+
+# ----------------------------------------------------------------- BASELINE full sizes
+def _rows_subset(gtype, data, n, k, rows):
+    bw, bb = oracle.BLOCK[gtype]
+    rb = (k // bw) * bb
+    return np.concatenate([data[r * rb:(r + 1) * rb] for r in rows])
+
+
+@pytest.mark.parametrize("gtype,n,k,batch", [
+    (oracle.Q6_K, 151936, 1024, 1),   # Qwen3-0.6B tied lm_head
+    (oracle.Q6_K, 4096, 12288, 4),    # Qwen3-8B down_proj
+    (oracle.Q4_0, 12288, 4096, 16),   # Qwen3-8B gate/up
+    (oracle.Q8_0, 1024, 3072, 4),     # Qwen3-0.6B down_proj
+])
+def test_gemv_full_size_rows_subset(ctx, gtype, n, k, batch):
+    """Full BASELINE shapes: 512 random output rows checked against the oracle,
+    plus linearity in x over the whole output (size-independent property)."""
+    w, data = gguf(gtype, n, k, seed=n + k)
+    x1 = oracle.randn(batch * k, seed=1).reshape(batch, k)
+    x2 = oracle.randn(batch * k, seed=2).reshape(batch, k)
+    y1 = ctx.qlinear(w, dev(x1)).cpu().numpy()
+    rows = np.sort(np.random.default_rng(0).choice(n, size=min(512, n), replace=False))
+    sub = _rows_subset(gtype, data, n, k, rows)
+    wsub = oracle.dequant_gguf(gtype, sub, len(rows), k)
+    assert gemv_err(np.ascontiguousarray(y1[:, rows]), x1, wsub) <= TIGHT
+    # linearity: y(2 x1 - x2) == 2 y(x1) - y(x2) up to f32 rounding
+    y2 = ctx.qlinear(w, dev(x2)).cpu().numpy()
+    y3 = ctx.qlinear(w, dev((2 * x1 - x2).astype(np.float32))).cpu().numpy()
+    scale = np.abs(2 * y1).max() + np.abs(y2).max()
+    assert np.abs(y3 - (2 * y1 - y2)).max() <= 1e-4 * scale
+    # zero activation gives exactly zero
+    z = ctx.qlinear(w, torch.zeros((batch, k), dtype=torch.float32, device="cuda"))
+    assert torch.count_nonzero(z).item() == 0
+
+
+# ----------------------------------------------------------------- error paths (host-side checks, no kernel runs)
+def test_errors_are_reported_not_faulted(ctx):
+    data = torch.zeros(18 * 4, dtype=torch.uint8, device="cuda")
+    x = torch.zeros((1, 100), dtype=torch.float32, device="cuda")
+    with pytest.raises(d.DyninferError) as e:
+        ctx.qlinear(d.QWeight(d.ENC_Q4_0, 1, 100, data), x)  # K not a multiple of 32
+    assert e.value.code == d.ERR_UNSUPPORTED
+    with pytest.raises(d.DyninferError) as e:
+        ctx.qlinear(d.QWeight(99, 1, 128, data), x)
+    assert e.value.code == d.ERR_UNSUPPORTED
+    with pytest.raises(d.DyninferError) as e:
+        ctx.qlinear(d.QWeight(d.ENC_Q4_0, 1, 128, data.data_ptr() + 1), torch.zeros((1, 128), device="cuda"))
+    assert e.value.code == d.ERR_INVALID_ARGUMENT
