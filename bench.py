@@ -1,0 +1,427 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized weight-matmul path (one JSON line on stdout).
+
+Metric: "quant GEMV weight HBM GB/s (% of 8 TB/s); Q4_0 prefill
+GEMM TFLOP/s".  `value` is measured on BASELINE config 1 — the Qwen3-0.6B
+mixed-encoding GGUF decode step at batch 1: 28 layers of q/k/v/o/gate/up
+(Q4_0 on even layers, Q4_1 on odd) and down (Q8_0), plus the tied lm_head
+(Q6_K), 430,402,560 weight bytes per step.  One step = every one of those
+GEMVs once, in layer order, launched as a decode step would be: q/k/v as one
+launch (shared activation), o, gate/up as one launch, down, then lm_head;
+the step is captured once in a HIP graph and replayed.  Weights are seeded
+synthetic bytes in the BASELINE distributions, resident in HBM before timing.
+
+value = weight bytes per step x steps / timed seconds (GB/s).  The other
+configurations (0: rotating-pool single GEMV, 2: MLX U4 step, 3: Q4_0 prefill
+GEMM, 4: Qwen3-8B step) are reported under "extra".
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA, TFLOP/s
+METRIC = "quant GEMV weight HBM GB/s (% of 8 TB/s); Q4_0 prefill GEMM TFLOP/s"
+
+# Qwen3-0.6B (hidden 1024, 28 layers, 16 q heads / 8 kv heads x 128, ffn 3072, vocab 151936)
+QWEN06 = dict(layers=28, hidden=1024, q=2048, kv=1024, ffn=3072, vocab=151936)
+# Qwen3-8B (hidden 4096, 36 layers, GQA 32/8 x 128, ffn 12288, vocab 151936)
+QWEN8 = dict(layers=36, hidden=4096, q=4096, kv=1024, ffn=12288, vocab=151936)
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ synthetic weights (on the GPU)
+def gguf_tensor(torch, d, enc: int, n: int, k: int, gen):
+    """Seeded GGUF blocks in the BASELINE distributions, built on the device."""
+    bw, bb = d.block_geometry(enc)
+    nblk = n * (k // bw)
+    dev = "cuda"
+    blocks = torch.randint(0, 256, (nblk, bb), dtype=torch.uint8, device=dev, generator=gen)
+    scale = (torch.randn(nblk, device=dev, generator=gen).abs() * 0.01).half().view(torch.uint8).view(nblk, 2)
+    if enc == d.ENC_Q6_K:
+        sc = torch.randint(-32, 32, (nblk, 16), dtype=torch.int8, device=dev, generator=gen).view(torch.uint8)
+        blocks[:, 192:208] = sc
+        blocks[:, 208:210] = scale
+    else:
+        blocks[:, 0:2] = scale
+        if enc == d.ENC_Q4_1:
+            m = (torch.randn(nblk, device=dev, generator=gen) * 0.01).half().view(torch.uint8).view(nblk, 2)
+            blocks[:, 2:4] = m
+        elif enc == d.ENC_Q8_0:
+            q = torch.randint(-127, 128, (nblk, 32), dtype=torch.int16, device=dev, generator=gen)
+            blocks[:, 2:34] = q.to(torch.int8).view(torch.uint8)
+    return d.QWeight(enc, n, k, blocks.view(-1))
+
+
+def mlx_tensor(torch, d, n: int, k: int, group: int, gen):
+    dev = "cuda"
+    packed = torch.randint(0, 2**31 - 1, (n * k // 8,), dtype=torch.int32, device=dev, generator=gen)
+    packed ^= torch.randint(0, 2, (n * k // 8,), dtype=torch.int32, device=dev, generator=gen) << 31
+    g = n * (k // group)
+    scales = (torch.randn(g, device=dev, generator=gen).abs() * 0.02).bfloat16()
+    biases = (torch.randn(g, device=dev, generator=gen) * 0.01).bfloat16()
+    return d.QWeight(d.ENC_MLX_U4, n, k, packed, scales, biases, group, d.DTYPE_BF16)
+
+
+# ------------------------------------------------------------------ decode step sets
+class StepSet:
+    """The matmuls of one decode step, grouped into launches as a decode step issues them."""
+
+    def __init__(self, name: str):
+        self.name = name
+        self.launches = []  # (label, [QWeight], input key, [output keys])
+        self.weight_bytes = 0
+
+    def add(self, label, ws, xin, outs):
+        self.launches.append((label, ws, xin, outs))
+        self.weight_bytes += sum(w.nbytes for w in ws)
+
+
+def gguf_step_06b(torch, d, gen) -> StepSet:
+    c = QWEN06
+    s = StepSet("qwen3-0.6b mixed gguf")
+    for layer in range(c["layers"]):
+        enc = d.ENC_Q4_0 if layer % 2 == 0 else d.ENC_Q4_1
+        h, q, kv, f = c["hidden"], c["q"], c["kv"], c["ffn"]
+        s.add(f"qkv.{d.ENCODING_IDS[enc]}", [gguf_tensor(torch, d, enc, q, h, gen), gguf_tensor(torch, d, enc, kv, h, gen),
+                                             gguf_tensor(torch, d, enc, kv, h, gen)], "h", ["q", "k", "v"])
+        s.add(f"o.{d.ENCODING_IDS[enc]}", [gguf_tensor(torch, d, enc, h, q, gen)], "attn", ["o"])
+        s.add(f"gate_up.{d.ENCODING_IDS[enc]}", [gguf_tensor(torch, d, enc, f, h, gen), gguf_tensor(torch, d, enc, f, h, gen)],
+              "h", ["gate", "up"])
+        s.add("down.gguf.q8_0", [gguf_tensor(torch, d, d.ENC_Q8_0, h, f, gen)], "act", ["down"])
+    s.add("lm_head.gguf.q6_k", [gguf_tensor(torch, d, d.ENC_Q6_K, c["vocab"], c["hidden"], gen)], "h", ["logits"])
+    return s
+
+
+def gguf_step_8b(torch, d, gen) -> StepSet:
+    c = QWEN8
+    s = StepSet("qwen3-8b gguf")
+    h, q, kv, f = c["hidden"], c["q"], c["kv"], c["ffn"]
+    for _ in range(c["layers"]):
+        s.add("qkv.gguf.q4_0", [gguf_tensor(torch, d, d.ENC_Q4_0, q, h, gen), gguf_tensor(torch, d, d.ENC_Q4_0, kv, h, gen),
+                                gguf_tensor(torch, d, d.ENC_Q4_0, kv, h, gen)], "h", ["q", "k", "v"])
+        s.add("o.gguf.q4_0", [gguf_tensor(torch, d, d.ENC_Q4_0, h, q, gen)], "attn", ["o"])
+        s.add("gate_up.gguf.q4_0", [gguf_tensor(torch, d, d.ENC_Q4_0, f, h, gen), gguf_tensor(torch, d, d.ENC_Q4_0, f, h, gen)],
+              "h", ["gate", "up"])
+        s.add("down.gguf.q6_k", [gguf_tensor(torch, d, d.ENC_Q6_K, h, f, gen)], "act", ["down"])
+    s.add("lm_head.gguf.q6_k", [gguf_tensor(torch, d, d.ENC_Q6_K, c["vocab"], h, gen)], "h", ["logits"])
+    return s
+
+
+def mlx_step_06b(torch, d, gen) -> StepSet:
+    c = QWEN06
+    s = StepSet("qwen3-0.6b mlx affine u4 g64")
+    h, q, kv, f = c["hidden"], c["q"], c["kv"], c["ffn"]
+    for _ in range(c["layers"]):
+        s.add("qkv.mlx.u4", [mlx_tensor(torch, d, q, h, 64, gen), mlx_tensor(torch, d, kv, h, 64, gen),
+                             mlx_tensor(torch, d, kv, h, 64, gen)], "h", ["q", "k", "v"])
+        s.add("o.mlx.u4", [mlx_tensor(torch, d, h, q, 64, gen)], "attn", ["o"])
+        s.add("gate_up.mlx.u4", [mlx_tensor(torch, d, f, h, 64, gen), mlx_tensor(torch, d, f, h, 64, gen)], "h",
+              ["gate", "up"])
+        s.add("down.mlx.u4", [mlx_tensor(torch, d, h, f, 64, gen)], "act", ["down"])
+    s.add("lm_head.mlx.u4", [mlx_tensor(torch, d, c["vocab"], h, 64, gen)], "h", ["logits"])
+    return s
+
+
+class StepRunner:
+    """Activations/outputs for one StepSet at a batch size, and the step itself."""
+
+    def __init__(self, torch, d, ctx, steps: StepSet, batch: int, xdtype, ydtype):
+        self.torch, self.d, self.ctx, self.set, self.batch = torch, d, ctx, steps, batch
+        dims = {}
+        for _, ws, xin, outs in steps.launches:
+            dims[xin] = ws[0].cols
+            for o, w in zip(outs, ws):
+                dims[o] = w.rows
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(1234)
+        self.bufs = {}
+        for key, n in dims.items():
+            dt = xdtype if key in ("h", "attn", "act") else ydtype
+            self.bufs[key] = (torch.randn(batch, n, device="cuda", generator=gen)).to(dt)
+        self.stream = torch.cuda.Stream()
+
+    def launch(self, i: int, stream) -> None:
+        _, ws, xin, outs = self.set.launches[i]
+        x = self.bufs[xin]
+        ys = [self.bufs[o] for o in outs]
+        if len(ws) == 1:
+            self.ctx.qlinear(ws[0], x, ys[0], stream=stream)
+        else:
+            self.ctx.qlinear_multi(ws, x, ys, stream=stream)
+
+    def step(self, stream) -> None:
+        for i in range(len(self.set.launches)):
+            self.launch(i, stream)
+
+    def capture(self):
+        torch = self.torch
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(self.stream):
+            self.step(self.stream)  # load code objects / occupancy queries outside the capture
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=self.stream):
+                self.step(self.stream)
+        torch.cuda.synchronize()
+        return g
+
+    def time_graph(self, g, steps: int, warmup: int) -> float:
+        """ms per replay; replays and events both on the runner's stream."""
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            for _ in range(warmup):
+                g.replay()
+            torch.cuda.synchronize()
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record(self.stream)
+            for _ in range(steps):
+                g.replay()
+            t1.record(self.stream)
+            torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / steps
+
+    def per_launch_times(self, reps: int = 5):
+        """Eager pass with HIP events around every launch on the launch stream:
+        {label: (launches, total ms, weight bytes)} averaged over reps."""
+        torch = self.torch
+        stats = {}
+        st = self.stream
+        with torch.cuda.stream(st):
+            for _ in range(2):
+                self.step(st)
+            torch.cuda.synchronize()
+            evs = []
+            for _ in range(reps):
+                for i in range(len(self.set.launches)):
+                    a = torch.cuda.Event(enable_timing=True)
+                    b = torch.cuda.Event(enable_timing=True)
+                    a.record(st)
+                    self.launch(i, st)
+                    b.record(st)
+                    evs.append((i, a, b))
+            torch.cuda.synchronize()
+        for i, a, b in evs:
+            label, ws, _, _ = self.set.launches[i]
+            n, ms, nb = stats.get(label, (0, 0.0, 0))
+            stats[label] = (n + 1, ms + a.elapsed_time(b), nb + sum(w.nbytes for w in ws))
+        return stats
+
+
+# ------------------------------------------------------------------ other configurations
+def bench_rotating_gemv(torch, d, ctx, enc, n, k, batch, pool_bytes=1.2e9, iters=200):
+    """Config 0: one GEMV timed over a rotating pool of distinct weight copies (> MALL)."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+    w0 = gguf_tensor(torch, d, enc, n, k, gen)
+    copies = max(2, int(pool_bytes // w0.nbytes))
+    ws = [w0] + [gguf_tensor(torch, d, enc, n, k, gen) for _ in range(copies - 1)]
+    x = torch.randn(batch, k, device="cuda", generator=gen)
+    y = torch.empty(batch, n, device="cuda")
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        for w in ws[:4]:
+            ctx.qlinear(w, x, y, stream=st)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            for i in range(copies):
+                ctx.qlinear(ws[i], x, y, stream=st)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = max(1, iters // copies)
+        a.record(st)
+        for _ in range(reps):
+            g.replay()
+        b.record(st)
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / (reps * copies)
+    del ws
+    return {"us_per_gemv": ms * 1e3, "weight_GBps": w0.nbytes / ms / 1e6, "copies": copies,
+            "hbm_frac": w0.nbytes / ms / 1e6 / HBM_PEAK_GBS}
+
+
+def bench_gemm(torch, d, ctx, m, n, k, iters=50):
+    """Config 3: Q4_0 prefill GEMM (bf16 X, f16 MFMA, f32 accumulate, bf16 Y)."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    w = gguf_tensor(torch, d, d.ENC_Q4_0, n, k, gen)
+    x = torch.randn(m, k, device="cuda", generator=gen).bfloat16()
+    y = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        for _ in range(3):
+            ctx.qlinear(w, x, y, stream=st)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(iters):
+            ctx.qlinear(w, x, y, stream=st)
+        b.record(st)
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / iters
+    tflops = 2.0 * m * n * k / ms / 1e9
+    return {"us": ms * 1e3, "TFLOPs": tflops, "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS}
+
+
+# ------------------------------------------------------------------ CPU baseline
+def cpu_baseline(seconds: float = 12.0):
+    """The oracle's CPU contraction (dequantisation adjacent to an f32 dot, the
+    reference's CPU semantics) timed on this host over config 1's matmuls, for a
+    bounded sample: whole decode steps repeated until `seconds` have elapsed."""
+    import numpy as np
+    import oracle
+    threads = min(os.cpu_count() or 1, 16)
+    c = QWEN06
+    h, q, kv, f = c["hidden"], c["q"], c["kv"], c["ffn"]
+    mats = []
+    for layer in range(c["layers"]):
+        t = oracle.Q4_0 if layer % 2 == 0 else oracle.Q4_1
+        for (n, k) in [(q, h), (kv, h), (kv, h), (h, q), (f, h), (f, h)]:
+            mats.append((t, n, k))
+        mats.append((oracle.Q8_0, h, f))
+    mats.append((oracle.Q6_K, c["vocab"], h))
+    data = [(t, n, k, oracle.synth_gguf(t, n, k, seed=i)) for i, (t, n, k) in enumerate(mats)]
+    nbytes = sum(x[3].size for x in data)
+    xs = {k: oracle.randn(k, seed=k).reshape(1, k) for k in {h, q, f}}
+    for t, n, k, w in data[:8]:  # warm-up
+        oracle.qlinear_gguf_f32(t, w, xs[k], n, k, threads)
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        for t, n, k, w in data:
+            oracle.qlinear_gguf_f32(t, w, xs[k], n, k, threads)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or steps >= 200:
+            break
+    return {"value": nbytes * steps / el / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} full config-1 decode steps at batch 1 ({nbytes} weight bytes each, "
+                      f"{el:.1f} s), oracle/oracle.c qlinear_gguf_f32 with {threads} OpenMP threads"}
+
+
+# ------------------------------------------------------------------ main
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--no-extra", action="store_true", help="skip configs 0/2/3/4")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path; run with --gpus 1)", file=sys.stderr)
+        return 2
+
+    import torch
+    import dyninfer_amd as d
+
+    ctx = d.Context(0)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+
+    log("building config 1 weights (Qwen3-0.6B mixed GGUF) ...")
+    s1 = gguf_step_06b(torch, d, gen)
+    r1 = StepRunner(torch, d, ctx, s1, args.batch, torch.float32, torch.float32)
+    g1 = r1.capture()
+    ms = r1.time_graph(g1, args.steps, args.warmup)
+    value = s1.weight_bytes / ms / 1e6
+    log(f"config 1 batch {args.batch}: {ms * 1e3:.1f} us/step, {value:.1f} GB/s")
+
+    # dominant kernel of the step: largest total time in an event-instrumented eager pass
+    stats = r1.per_launch_times()
+    dom_label, (dn, dms, dbytes) = max(stats.items(), key=lambda kv: kv[1][1])
+    dom_us = dms / dn * 1e3
+    dom_bytes = dbytes / dn
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": dom_label, "bytes_per_launch": int(dom_bytes), "avg_launch_us": round(dom_us, 2)}
+    tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    if os.path.exists(tfile):
+        with open(tfile) as fh:
+            roofline["traffic"] = json.load(fh).get(dom_label)
+    breakdown = {k: {"launches_per_step": v[0] // 5, "us_per_launch": round(v[1] / v[0] * 1e3, 2),
+                     "GBps": round(v[2] / v[0] / (v[1] / v[0]) / 1e6, 1)} for k, v in sorted(stats.items())}
+
+    extra = {"config1_breakdown_eager": breakdown}
+    if not args.no_extra:
+        r4b = StepRunner(torch, d, ctx, s1, 4, torch.float32, torch.float32)
+        ms4 = r4b.time_graph(r4b.capture(), max(5, args.steps // 2), 3)
+        extra["config1_batch4"] = {"us_per_step": round(ms4 * 1e3, 1), "weight_GBps": round(s1.weight_bytes / ms4 / 1e6, 1),
+                                   "tokens_per_s": round(4 / (ms4 * 1e-3), 1)}
+        del r4b
+        log("config 0 (rotating pool) ...")
+        extra["config0_q4_0_3072x1024_b1"] = {k: round(v, 4) for k, v in
+                                              bench_rotating_gemv(torch, d, ctx, d.ENC_Q4_0, 3072, 1024, 1).items()}
+        log("config 2 (MLX U4 step) ...")
+        s2 = mlx_step_06b(torch, d, gen)
+        c2 = {}
+        for b in (1, 8, 16):
+            r2 = StepRunner(torch, d, ctx, s2, b, torch.bfloat16, torch.bfloat16)
+            ms2 = r2.time_graph(r2.capture(), max(5, args.steps // 2), 3)
+            c2[f"batch{b}"] = {"us_per_step": round(ms2 * 1e3, 1), "weight_GBps": round(s2.weight_bytes / ms2 / 1e6, 1)}
+        c2["weight_bytes_per_step"] = s2.weight_bytes
+        extra["config2_mlx_u4_step"] = c2
+        del s2, r2
+        log("config 3 (Q4_0 GEMM) ...")
+        c3 = {}
+        for m in (128, 512, 2048):
+            for (n, k) in [(3072, 1024), (1024, 3072), (2048, 1024)]:
+                c3[f"M{m}_N{n}_K{k}"] = {kk: round(v, 4) for kk, v in bench_gemm(torch, d, ctx, m, n, k).items()}
+        extra["config3_q4_0_gemm"] = c3
+        log("config 4 (Qwen3-8B step) ...")
+        s4 = gguf_step_8b(torch, d, gen)
+        c4 = {"weight_bytes_per_step": s4.weight_bytes}
+        for b in (1, 4, 16):
+            r = StepRunner(torch, d, ctx, s4, b, torch.float32, torch.float32)
+            ms8 = r.time_graph(r.capture(), max(3, args.steps // 5), 2)
+            c4[f"batch{b}"] = {"us_per_step": round(ms8 * 1e3, 1), "weight_GBps": round(s4.weight_bytes / ms8 / 1e6, 1),
+                               "hbm_frac": round(s4.weight_bytes / ms8 / 1e6 / HBM_PEAK_GBS, 4),
+                               "tokens_per_s": round(b / (ms8 * 1e-3), 1)}
+        extra["config4_qwen3_8b_step"] = c4
+        del s4
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline ...")
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded GGUF blocks in the BASELINE distributions, resident in HBM)",
+        "config": {"workload": "BASELINE config 1: Qwen3-0.6B mixed GGUF decode-step GEMV set "
+                               "(Q4_0/Q4_1 projections by layer, Q8_0 down, Q6_K lm_head), graph-replayed",
+                   "batch": args.batch, "weight_bytes_per_step": s1.weight_bytes,
+                   "launches_per_step": len(s1.launches), "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -28,7 +28,8 @@ from typing import Optional, Sequence
 __all__ = [
     "LIB_PATH", "DyninferError", "QWeight", "Context", "library", "candidates", "registry_select",
     "registry_require", "supports", "ENC_Q4_0", "ENC_Q4_1", "ENC_Q8_0", "ENC_Q6_K", "ENC_MLX_U4",
-    "DTYPE_F32", "DTYPE_F16", "DTYPE_BF16", "block_geometry", "weight_bytes",
+    "DTYPE_F32", "DTYPE_F16", "DTYPE_BF16", "block_geometry", "weight_bytes", "ERR_INVALID_ARGUMENT",
+    "ERR_UNSUPPORTED", "ERR_HIP", "ERR_DEVICE", "ERR_BUFFER_TOO_SMALL",
 ]
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdyninfer_mi355x.so")

@@ -1,6 +1,9 @@
 // Decode GEMV dispatch: lays out the wave grid over up to four weights that
 // share one activation, picks the lanes-per-row split, and calls the
 // per-encoding instantiations (gemv_<enc>.hip; kernels in gemv_kernels.hpp).
+#include <mutex>
+#include <vector>
+
 #include "kernels.hpp"
 
 namespace dmx {
@@ -11,13 +14,38 @@ hipError_t gemv_launch_q8_0(const GemvParams& p, uint32_t B, bool xbf16, hipStre
 hipError_t gemv_launch_q6_k(const GemvParams& p, uint32_t B, bool xbf16, hipStream_t st);
 hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, bool xbf16, hipStream_t st);
 
-namespace {
-
-uint32_t pow2_floor(uint32_t v) {
-    uint32_t r = 1;
-    while (r * 2 <= v) r *= 2;
-    return r;
+hipError_t cached_occupancy(const void* kernel, size_t lds, int* per_cu, int* cus) {
+    struct Entry {
+        const void* kernel;
+        size_t lds;
+        int dev, per_cu, cus;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        for (const Entry& c : cache)
+            if (c.kernel == kernel && c.lds == lds && c.dev == dev) {
+                *per_cu = c.per_cu;
+                *cus = c.cus;
+                return hipSuccess;
+            }
+    }
+    int n = 0, blocks = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 256, lds);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    cache.push_back({kernel, lds, dev, blocks, n});
+    *per_cu = blocks;
+    *cus = n;
+    return hipSuccess;
 }
+
+namespace {
 
 struct EncInfo {
     uint32_t chunk_weights;  // weights one lane handles per step

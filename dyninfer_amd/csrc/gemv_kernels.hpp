@@ -303,18 +303,19 @@ constexpr int rows_per_group() {
 // Largest activation bytes staged in LDS per workgroup.
 constexpr size_t kMaxLdsX = 64u * 1024u;
 
+// Resident workgroups per CU for (kernel, dynamic LDS) on the current device
+// and its CU count, cached after the first query (host side, thread-safe).
+hipError_t cached_occupancy(const void* kernel, size_t lds, int* per_cu, int* cus);
+
 // Launch of one kernel instantiation with a persistent grid: as many
 // workgroups as fit on the device at once (capped by the row-block count).
 template <class KERNEL>
 hipError_t launch_persistent(KERNEL kernel, const GemvParams& p, size_t lds, hipStream_t st) {
-    int dev = 0, cus = 0, per_cu = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds);
+    int cus = 0, per_cu = 0;
+    hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, &per_cu, &cus);
     if (e != hipSuccess) return e;
-    if (per_cu < 1) per_cu = 1;
     const uint64_t want = ((uint64_t)p.total_rb + 3) / 4;  // 4 waves per workgroup
-    const uint64_t cap = (uint64_t)per_cu * (uint64_t)cus;
+    const uint64_t cap = (uint64_t)(per_cu < 1 ? 1 : per_cu) * (uint64_t)cus;
     const uint32_t blocks = (uint32_t)(want < cap ? want : cap);
     hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), lds, st, p);
     return hipGetLastError();

@@ -1,0 +1,122 @@
+"""C-ABI boundary checks that need no GPU: the library loads, exports every
+entry point include/*.h declares, and validates arguments host-side exactly
+as documented (no compute call is made here)."""
+import ctypes
+import glob
+import os
+import re
+import threading
+
+import pytest
+
+import dyninfer_amd as d
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(dyninfer_mi355x_\w+)\s*\(", text))
+    return names
+
+
+def test_every_declared_symbol_is_exported():
+    names = declared_symbols()
+    assert len(names) >= 11
+    lib = d.library()
+    for n in names:
+        assert hasattr(lib, n), n
+    assert names == set(d.EXPORTED_SYMBOLS)
+
+
+def test_nm_exports_are_c_linkage():
+    out = os.popen(f"nm -D --defined-only {d.LIB_PATH}").read()
+    for n in declared_symbols():
+        assert re.search(rf"\bT {n}$", out, re.M), n
+
+
+def test_version_and_candidates_json():
+    assert b"gfx950" in d.library().dyninfer_mi355x_version()
+    assert len(d.candidates()) == 10
+
+
+def w(enc, rows=64, cols=256, data=0x1000, **kw):
+    return d.QWeight(enc, rows, cols, data, **kw)
+
+
+@pytest.mark.parametrize("enc,cols,ok", [
+    (d.ENC_Q4_0, 256, True), (d.ENC_Q4_0, 100, False), (d.ENC_Q4_1, 64, True), (d.ENC_Q8_0, 96, True),
+    (d.ENC_Q6_K, 256, True), (d.ENC_Q6_K, 384, False), (99, 256, False)])
+def test_supports_block_multiples(enc, cols, ok):
+    assert d.supports(w(enc, cols=cols), 1) == ok
+
+
+def test_supports_alignment_rules():
+    assert d.supports(w(d.ENC_Q4_0, data=0x1002), 1)          # GGUF: 2-byte aligned is enough
+    assert not d.supports(w(d.ENC_Q4_0, data=0x1001), 1)
+    assert not d.supports(w(d.ENC_Q4_1, data=0x1002), 1)      # Q4_1 blocks are 20 bytes: 4-byte base
+    assert not d.supports(w(d.ENC_Q4_0, data=0), 1)           # NULL
+
+
+def test_supports_mlx_rules():
+    good = w(d.ENC_MLX_U4, data=0x1000, scales=0x2000, biases=0x3000, group_size=64, scale_dtype=d.DTYPE_BF16)
+    assert d.supports(good, 8, d.DTYPE_BF16, d.DTYPE_BF16)
+    assert not d.supports(w(d.ENC_MLX_U4, scales=0x2000, biases=0x3000, group_size=48), 1)  # not a multiple of 32
+    assert not d.supports(w(d.ENC_MLX_U4, cols=96, scales=0x2000, biases=0x3000, group_size=64), 1)
+    assert not d.supports(w(d.ENC_MLX_U4, scales=0, biases=0x3000, group_size=64), 1)
+    assert not d.supports(w(d.ENC_MLX_U4, scales=0x2001, biases=0x3000, group_size=64), 1)
+    assert not d.supports(w(d.ENC_MLX_U4, scales=0x2000, biases=0x3000, group_size=64, scale_dtype=7), 1)
+
+
+def test_supports_dtype_rules():
+    assert d.supports(w(d.ENC_Q4_0), 512, d.DTYPE_BF16, d.DTYPE_BF16)   # MFMA path
+    assert not d.supports(w(d.ENC_Q6_K), 1, d.DTYPE_BF16)              # GGUF decode takes f32 activations
+    assert not d.supports(w(d.ENC_Q4_0), 1, d.DTYPE_F16)
+    assert not d.supports(w(d.ENC_Q6_K), 1, d.DTYPE_BF16)
+    assert "bf16 activations" in d.library().dyninfer_mi355x_last_error().decode()
+    assert not d.supports(w(d.ENC_Q4_0), 0)
+
+
+def test_calls_without_context_fail_cleanly():
+    lib = d.library()
+    wc = w(d.ENC_Q4_0).c()
+    rc = lib.dyninfer_mi355x_qlinear(None, ctypes.byref(wc), 0x1000, d.DTYPE_F32, 1, 0x2000, d.DTYPE_F32, None)
+    assert rc == d.ERR_INVALID_ARGUMENT
+    assert "context" in lib.dyninfer_mi355x_last_error().decode()
+    rc = lib.dyninfer_mi355x_dequant(None, ctypes.byref(wc), 0x1000, None)
+    assert rc == d.ERR_INVALID_ARGUMENT
+
+
+def test_open_without_gpu_reports_hip_error():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(d.DyninferError) as e:
+        d.Context(0)
+    assert e.value.code in (d.ERR_HIP, d.ERR_INVALID_ARGUMENT)
+
+
+def test_last_error_is_thread_local():
+    lib = d.library()
+    assert not d.supports(w(d.ENC_Q4_0, cols=100), 1)
+    main_msg = lib.dyninfer_mi355x_last_error().decode()
+    assert "multiple of the block size" in main_msg
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(lib.dyninfer_mi355x_last_error().decode()))
+    t.start()
+    t.join()
+    assert seen == [""]
+    assert lib.dyninfer_mi355x_last_error().decode() == main_msg
+
+
+def test_registry_output_buffer_too_small():
+    lib = d.library()
+    n = ctypes.c_size_t(0)
+    buf = ctypes.create_string_buffer(8)
+    req = b'{"operation_id":"o","operation":"linear","orientation":"native","mode":"decode"}'
+    rc = lib.dyninfer_mi355x_registry_select(None, req, b'{"driver":"hip","architecture":"gfx950","features":[]}',
+                                             ctypes.cast(buf, ctypes.c_void_p), 8, ctypes.byref(n))
+    assert rc == d.ERR_BUFFER_TOO_SMALL and n.value > 8
