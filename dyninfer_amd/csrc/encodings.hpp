@@ -22,6 +22,7 @@
 // mlx quad_perm), so the kernel converts them with v_cvt_f32_ubyte{0..3}.
 #pragma once
 #include "device_common.hpp"
+#include "kernels.hpp"
 
 namespace dmx {
 
@@ -43,14 +44,17 @@ __device__ __forceinline__ uint32_t and_or_opaque(uint32_t a, uint32_t b) {
     return r;
 }
 
-// Realigned dwords of a GGUF block of BB bytes (BB % 4 == 2 or 0), loaded from
-// the 4-byte-aligned dword containing its first byte.
-template <int NDW>
-__device__ __forceinline__ void load_block(const uint8_t* p, uint32_t (&e)[NDW]) {
+// Raw dwords of a GGUF block, loaded from the 4-byte-aligned dword containing
+// its first byte, with the byte shift (0 or 2) that realign() applies later.
+// Realigning after the load keeps the loads free of consumers, so a lane can
+// have every row's block in flight at once.
+template <int NDW, class RAW>
+__device__ __forceinline__ RAW load_raw_block(const uint8_t* p) {
     const uintptr_t a = (uintptr_t)p;
-    uint32_t raw[NDW];
-    load_dwords<NDW>(reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3), raw);
-    realign<NDW>(raw, (uint32_t)(a & 3u), e);
+    RAW r;
+    load_dwords<NDW>(reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3), r.d);
+    r.sh = (uint32_t)(a & 3u);
+    return r;
 }
 
 // ------------------------------------------------------------------ GGUF Q4_0
@@ -59,9 +63,13 @@ __device__ __forceinline__ void load_block(const uint8_t* p, uint32_t (&e)[NDW])
 struct EncQ40 {
     static constexpr int CW = 32, NG = 1, GW = 32, NDW = 5, BB = 18;
     struct Chunk { uint32_t q[4]; float d; };
-    __device__ __forceinline__ static Chunk load(const uint8_t* row, uint32_t u) {
+    struct Raw { uint32_t d[NDW]; uint32_t sh; };
+    __device__ __forceinline__ static Raw load_raw(const uint8_t* row, uint32_t u) {
+        return load_raw_block<NDW, Raw>(row + (size_t)u * 18u);
+    }
+    __device__ __forceinline__ static Chunk unpack(const Raw& r) {
         uint32_t e[NDW];
-        load_block<NDW>(row + (size_t)u * 18u, e);
+        realign<NDW>(r.d, r.sh, e);
         Chunk c;
         c.d = f16_bits_to_f32(e[0]);
 #pragma unroll
@@ -85,14 +93,18 @@ struct EncQ40 {
 struct EncQ41 {
     static constexpr int CW = 32, NG = 1, GW = 32, NDW = 5, BB = 20;
     struct Chunk { uint32_t q[4]; float d, m; };
-    __device__ __forceinline__ static Chunk load(const uint8_t* row, uint32_t u) {
-        uint32_t e[NDW];
-        load_dwords<NDW>(reinterpret_cast<const uint32_t*>(row + (size_t)u * 20u), e);
+    struct Raw { uint32_t d[NDW]; };
+    __device__ __forceinline__ static Raw load_raw(const uint8_t* row, uint32_t u) {
+        Raw r;
+        load_dwords<NDW>(reinterpret_cast<const uint32_t*>(row + (size_t)u * 20u), r.d);
+        return r;
+    }
+    __device__ __forceinline__ static Chunk unpack(const Raw& r) {
         Chunk c;
-        c.d = f16_bits_to_f32(e[0]);
-        c.m = f16_bits_to_f32(e[0] >> 16);
+        c.d = f16_bits_to_f32(r.d[0]);
+        c.m = f16_bits_to_f32(r.d[0] >> 16);
 #pragma unroll
-        for (int t = 0; t < 4; t++) c.q[t] = e[t + 1];
+        for (int t = 0; t < 4; t++) c.q[t] = r.d[t + 1];
         return c;
     }
     __device__ __forceinline__ static float scale(const Chunk& c, int) { return c.d; }
@@ -110,9 +122,13 @@ struct EncQ41 {
 struct EncQ80 {
     static constexpr int CW = 32, NG = 1, GW = 32, NDW = 9, BB = 34;
     struct Chunk { uint32_t q[8]; float d; };
-    __device__ __forceinline__ static Chunk load(const uint8_t* row, uint32_t u) {
+    struct Raw { uint32_t d[NDW]; uint32_t sh; };
+    __device__ __forceinline__ static Raw load_raw(const uint8_t* row, uint32_t u) {
+        return load_raw_block<NDW, Raw>(row + (size_t)u * 34u);
+    }
+    __device__ __forceinline__ static Chunk unpack(const Raw& r) {
         uint32_t e[NDW];
-        load_block<NDW>(row + (size_t)u * 34u, e);
+        realign<NDW>(r.d, r.sh, e);
         Chunk c;
         c.d = f16_bits_to_f32(e[0]);
 #pragma unroll
@@ -139,9 +155,13 @@ struct EncQ80 {
 struct EncQ6K {
     static constexpr int CW = 256, NG = 16, GW = 16, NDW = 53, BB = 210;
     struct Chunk { uint32_t e[NDW]; };
-    __device__ __forceinline__ static Chunk load(const uint8_t* row, uint32_t u) {
+    struct Raw { uint32_t d[NDW]; uint32_t sh; };
+    __device__ __forceinline__ static Raw load_raw(const uint8_t* row, uint32_t u) {
+        return load_raw_block<NDW, Raw>(row + (size_t)u * 210u);
+    }
+    __device__ __forceinline__ static Chunk unpack(const Raw& r) {
         Chunk c;
-        load_block<NDW>(row + (size_t)u * 210u, c.e);
+        realign<NDW>(r.d, r.sh, c.e);
         return c;
     }
     __device__ __forceinline__ static float dsuper(const Chunk& c) { return f16_bits_to_f32(c.e[52]); }
@@ -177,6 +197,25 @@ struct EncMlxU4 {
     static constexpr int CW = 32, NG = 1, GW = 32;
     static constexpr int QUADS = 8;
     struct Chunk { uint32_t w[4]; float s, b; };
+    // raw: packed words plus the scale/bias bit patterns (f32, or f16/bf16 in the
+    // low half) and their dtype
+    struct Raw { uint32_t w[4]; uint32_t s, b, kind; };
+    __device__ __forceinline__ static Chunk unpack(const Raw& r) {
+        Chunk c;
+#pragma unroll
+        for (int i = 0; i < 4; i++) c.w[i] = r.w[i];
+        if (r.kind == DT_F32) {
+            c.s = __uint_as_float(r.s);
+            c.b = __uint_as_float(r.b);
+        } else if (r.kind == DT_F16) {
+            c.s = f16_bits_to_f32(r.s);
+            c.b = f16_bits_to_f32(r.b);
+        } else {
+            c.s = bf16_bits_to_f32(r.s);
+            c.b = bf16_bits_to_f32(r.b);
+        }
+        return c;
+    }
     __device__ __forceinline__ static int kofs(int, int j) { return 4 * j; }
     __device__ __forceinline__ static float scale(const Chunk& c, int) { return c.s; }
     __device__ __forceinline__ static float offset(const Chunk& c, int) { return c.b; }

@@ -33,10 +33,16 @@
 
 namespace dmx {
 
+// a[i] for a wave-uniform i.  The four values are pinned in scalar registers
+// first: otherwise the optimiser folds the select chain back into a dynamic
+// index of the kernel-argument array, which it can only serve from a private
+// (scratch) copy of the array.
 template <class T>
 __device__ __forceinline__ T pick(uint32_t i, const T (&a)[kMaxProblems]) {
     static_assert(kMaxProblems == 4, "pick() assumes 4 problems");
-    return i == 0 ? a[0] : i == 1 ? a[1] : i == 2 ? a[2] : a[3];
+    T v0 = a[0], v1 = a[1], v2 = a[2], v3 = a[3];
+    asm("" : "+s"(v0), "+s"(v1), "+s"(v2), "+s"(v3));
+    return i == 0 ? v0 : i == 1 ? v1 : i == 2 ? v2 : v3;
 }
 
 // Four consecutive activations of row r at element k, as f32.
@@ -151,26 +157,27 @@ __device__ __forceinline__ void chunk_dot(const typename E::Chunk (&c)[R], const
     }
 }
 
-// Row block -> (problem, rows) for lane group g.
+// Row block -> problem, its row count and first row (all wave-uniform: kept
+// in scalar registers so selecting the problem's pointers never indexes the
+// kernel-argument arrays dynamically).
 struct RowBlock {
-    uint32_t pi, n, row0;
+    uint32_t pi, n, base;
 };
 
-template <int R>
-__device__ __forceinline__ RowBlock row_block(const GemvParams& p, uint32_t rb, uint32_t g) {
+__device__ __forceinline__ RowBlock row_block(const GemvParams& p, uint32_t rb, uint32_t rows_per_rb) {
     uint32_t pi = 0;
 #pragma unroll
     for (int i = 1; i < kMaxProblems; i++) pi += (i < (int)p.nprob && rb >= p.rb_begin[i]) ? 1u : 0u;
     RowBlock r;
     r.pi = pi;
     r.n = pick(pi, p.n);
-    r.row0 = ((rb - pick(pi, p.rb_begin)) * (64u >> p.lanes_log2) + g) * (uint32_t)R;
+    r.base = (rb - pick(pi, p.rb_begin)) * rows_per_rb;
     return r;
 }
 
 template <int R, int B>
-__device__ __forceinline__ void reduce_store(float (&acc)[R][B], const RowBlock& rb, uint32_t j, uint32_t L,
-                                             const GemvParams& p) {
+__device__ __forceinline__ void reduce_store(float (&acc)[R][B], const RowBlock& rb, uint32_t row0, uint32_t j,
+                                             uint32_t L, const GemvParams& p) {
     for (uint32_t off = L >> 1; off > 0; off >>= 1) {
 #pragma unroll
         for (int i = 0; i < R; i++)
@@ -181,7 +188,7 @@ __device__ __forceinline__ void reduce_store(float (&acc)[R][B], const RowBlock&
         void* y = pick(rb.pi, p.y);
 #pragma unroll
         for (int i = 0; i < R; i++) {
-            const uint32_t row = rb.row0 + (uint32_t)i;
+            const uint32_t row = row0 + (uint32_t)i;
             if (row >= rb.n) continue;
 #pragma unroll
             for (int b = 0; b < B; b++) {
@@ -195,16 +202,20 @@ __device__ __forceinline__ void reduce_store(float (&acc)[R][B], const RowBlock&
     }
 }
 
-// The persistent task pipeline shared by all encodings.  load(rb, i, u) returns
-// chunk u of row i of row block rb (rows past the end alias the last row, in
-// bounds; their sums are never stored).
+// The persistent task pipeline shared by all encodings.  load(rb, row, u)
+// returns the raw bytes of chunk u of a row (rows past the end are clamped to
+// the last row by the caller: in bounds, their sums are never stored).  Every
+// load is unconditional — at the end of the sequence the current task is
+// loaded again — so the compiler's wait counters can keep all of a lane's
+// loads in flight across one task of compute.
 template <class E, int R, int B, class XS, class LOAD>
 __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const XS& xsrc, LOAD&& load) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
     const uint32_t W = gridDim.x * (blockDim.x >> 6);
     const uint32_t L = 1u << p.lanes_log2;
     const uint32_t j = lane & (L - 1u), g = lane >> p.lanes_log2;
+    const uint32_t rows_per_rb = (64u >> p.lanes_log2) * (uint32_t)R;
     const uint32_t cpl = (p.K / (uint32_t)E::CW) >> p.lanes_log2;  // chunks per lane per row block
     if (wid >= p.total_rb) return;
     const uint32_t T = (p.total_rb - wid + W - 1) / W * cpl;  // tasks of this wave
@@ -215,34 +226,59 @@ __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const XS& xsr
 #pragma unroll
         for (int b = 0; b < B; b++) acc[i][b] = 0.0f;
 
-    typename E::Chunk cur[R], nxt[R];
+    auto load_task = [&](typename E::Raw (&dst)[R], const RowBlock& rb, uint32_t c) {
+        const uint32_t row0 = rb.base + g * (uint32_t)R;
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const uint32_t row = row0 + (uint32_t)i < rb.n ? row0 + (uint32_t)i : rb.n - 1u;
+            dst[i] = load(rb, row, j + c * L);
+        }
+    };
+
+    // Two register buffers in ping-pong (no copies between them, so waiting
+    // for one buffer never waits for the loads in flight into the other).
+    typename E::Raw ba[R], bb[R];
     uint32_t nrb = wid, nc = 0;  // the task loaded next
-    RowBlock nblk = row_block<R>(p, nrb, g);
-#pragma unroll
-    for (int i = 0; i < R; i++) nxt[i] = load(nblk, i, j + nc * L);
-    for (uint32_t t = 0; t < T; t++) {
-        const RowBlock cblk = nblk;
-        const uint32_t cc = nc;
-#pragma unroll
-        for (int i = 0; i < R; i++) cur[i] = nxt[i];
-        if (++nc == cpl) {
-            nc = 0;
-            nrb += W;
-            nblk = row_block<R>(p, nrb, g);
+    RowBlock nblk = row_block(p, nrb, rows_per_rb);
+    auto advance = [&](uint32_t t) {
+        if (t + 1 < T) {  // wave-uniform; past the end the last task is loaded again
+            if (++nc == cpl) {
+                nc = 0;
+                nrb += W;
+                nblk = row_block(p, nrb, rows_per_rb);
+            }
         }
-        if (t + 1 < T) {
+    };
+    auto compute = [&](const typename E::Raw (&buf)[R], const RowBlock& blk, uint32_t c) {
+        typename E::Chunk ch[R];
 #pragma unroll
-            for (int i = 0; i < R; i++) nxt[i] = load(nblk, i, j + nc * L);
-        }
-        chunk_dot<E, R, B>(cur, xsrc, (j + cc * L) * (uint32_t)E::CW, acc);
-        if (cc + 1 == cpl) {
-            reduce_store<R, B>(acc, cblk, j, L, p);
+        for (int i = 0; i < R; i++) ch[i] = E::unpack(buf[i]);
+        chunk_dot<E, R, B>(ch, xsrc, (j + c * L) * (uint32_t)E::CW, acc);
+        if (c + 1 == cpl) {
+            reduce_store<R, B>(acc, blk, blk.base + g * (uint32_t)R, j, L, p);
 #pragma unroll
             for (int i = 0; i < R; i++)
 #pragma unroll
                 for (int b = 0; b < B; b++) acc[i][b] = 0.0f;
         }
+    };
+    load_task(ba, nblk, nc);
+    uint32_t t = 0;
+    for (; t + 2 <= T; t += 2) {
+        // task t is in ba: load task t+1 into bb, compute ba
+        RowBlock blk = nblk;
+        uint32_t c = nc;
+        advance(t);
+        load_task(bb, nblk, nc);
+        compute(ba, blk, c);
+        // task t+1 is in bb: load task t+2 into ba, compute bb
+        blk = nblk;
+        c = nc;
+        advance(t + 1);
+        load_task(ba, nblk, nc);
+        compute(bb, blk, c);
     }
+    if (t < T) compute(ba, nblk, nc);  // odd task count: the last task is in ba
 }
 
 // ---------------------------------------------------------------- GGUF
@@ -252,9 +288,8 @@ __global__ __launch_bounds__(256) void gguf_gemv_kernel(const GemvParams p) {
     extern __shared__ float xs_dyn[];
     if constexpr (XL) stage_x<E::CW, B, XBF16>(xs_dyn, p.x, p.K, p.ldx, p.batch);
     const size_t rowbytes = (size_t)(p.K / (uint32_t)E::CW) * E::BB;
-    auto load = [&](const RowBlock& rb, int i, uint32_t u) {
-        const uint32_t row = rb.row0 + (uint32_t)i < rb.n ? rb.row0 + (uint32_t)i : rb.n - 1u;
-        return E::load(pick(rb.pi, p.w) + (size_t)row * rowbytes, u);
+    auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) {
+        return E::load_raw(pick(rb.pi, p.w) + (size_t)row * rowbytes, u);
     };
     if constexpr (XL) gemv_pipeline<E, R, B>(p, XLds<E::CW>{xs_dyn, p.K + 4u * (p.K / (uint32_t)E::CW)}, load);
     else gemv_pipeline<E, R, B>(p, XGlobal<XBF16>{p.x, p.ldx, p.batch}, load);
@@ -268,25 +303,23 @@ __global__ __launch_bounds__(256) void mlx_u4_gemv_kernel(const GemvParams p) {
     if constexpr (XL) stage_x<E::CW, B, XBF16>(xs_dyn, p.x, p.K, p.ldx, p.batch);
     const uint32_t ngroups = p.K / p.group;
     const uint32_t chunks_per_group = p.group / 32u;
-    auto load = [&](const RowBlock& rb, int i, uint32_t u) {
-        const uint32_t row = rb.row0 + (uint32_t)i < rb.n ? rb.row0 + (uint32_t)i : rb.n - 1u;
-        E::Chunk c;
+    const bool f32s = p.sdtype == DT_F32;
+    auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) {
+        E::Raw r;
         const uint32_t* wbase = reinterpret_cast<const uint32_t*>(pick(rb.pi, p.w));
-        load_dwords<4>(wbase + (size_t)row * (p.K / 8u) + (size_t)u * 4u, c.w);
+        load_dwords<4>(wbase + (size_t)row * (p.K / 8u) + (size_t)u * 4u, r.w);
         const size_t gi = (size_t)row * ngroups + u / chunks_per_group;
         const uint8_t* scb = pick(rb.pi, p.sc);
         const uint8_t* bib = pick(rb.pi, p.bi);
-        if (p.sdtype == DT_F32) {
-            c.s = gptr<float>(scb)[gi];
-            c.b = gptr<float>(bib)[gi];
-        } else if (p.sdtype == DT_F16) {
-            c.s = f16_bits_to_f32(gptr<uint16_t>(scb)[gi]);
-            c.b = f16_bits_to_f32(gptr<uint16_t>(bib)[gi]);
+        if (f32s) {
+            r.s = gptr<uint32_t>(scb)[gi];
+            r.b = gptr<uint32_t>(bib)[gi];
         } else {
-            c.s = bf16_bits_to_f32(gptr<uint16_t>(scb)[gi]);
-            c.b = bf16_bits_to_f32(gptr<uint16_t>(bib)[gi]);
+            r.s = gptr<uint16_t>(scb)[gi];
+            r.b = gptr<uint16_t>(bib)[gi];
         }
-        return c;
+        r.kind = p.sdtype;
+        return r;
     };
     if constexpr (XL) gemv_pipeline<E, R, B>(p, XLds<E::CW>{xs_dyn, p.K + 4u * (p.K / (uint32_t)E::CW)}, load);
     else gemv_pipeline<E, R, B>(p, XGlobal<XBF16>{p.x, p.ldx, p.batch}, load);
