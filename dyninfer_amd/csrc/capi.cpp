@@ -58,6 +58,16 @@ uint32_t block_weights(uint32_t enc) {
     }
 }
 
+uint64_t block_bytes(uint32_t enc) {
+    switch (enc) {
+    case DYNINFER_ENC_GGUF_Q4_0: return 18;
+    case DYNINFER_ENC_GGUF_Q4_1: return 20;
+    case DYNINFER_ENC_GGUF_Q8_0: return 34;
+    case DYNINFER_ENC_GGUF_Q6_K: return 210;
+    default: return 0;
+    }
+}
+
 const char* enc_name(uint32_t enc) {
     switch (enc) {
     case DYNINFER_ENC_GGUF_Q4_0: return "gguf.q4_0";
@@ -88,6 +98,13 @@ int check_weight(const dyninfer_qweight_t* w) {
             return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string(enc_name(w->encoding)) +
                                                                   ": block data must be " + std::to_string(need) +
                                                                   "-byte aligned");
+        if (w->rows * (w->cols / bw) * block_bytes(w->encoding) > 0xFFFFFFF0ull)
+            return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, std::string(enc_name(w->encoding)) +
+                                                             ": one weight tensor is limited to 4 GiB (32-bit offsets)");
+        if (!dmx::gemv_k_supported(w->encoding, (uint32_t)w->cols))
+            return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
+                        std::string(enc_name(w->encoding)) + ": logical axis 1 (" + std::to_string(w->cols) +
+                            ") is too long for one workgroup's activation tile in LDS");
         return 0;
     }
     if (w->encoding != DYNINFER_ENC_MLX_AFFINE_U4)
@@ -106,6 +123,11 @@ int check_weight(const dyninfer_qweight_t* w) {
     }
     if (!aligned(w->data, 4) || !aligned(w->scales, es) || !aligned(w->biases, es))
         return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "mlx.affine.u4: component pointers are misaligned");
+    if (w->rows * w->cols / 2 > 0xFFFFFFF0ull || w->rows * (w->cols / w->group_size) * es > 0xFFFFFFF0ull)
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "mlx.affine.u4: one weight tensor is limited to 4 GiB (32-bit offsets)");
+    if (!dmx::gemv_k_supported(w->encoding, (uint32_t)w->cols))
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "mlx.affine.u4: logical axis 1 (" + std::to_string(w->cols) +
+                                                        ") is too long for one workgroup's activation tile in LDS");
     return 0;
 }
 

@@ -23,6 +23,11 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(const
     return (const __attribute__((address_space(1))) T*)(p);
 }
 
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gptr_mut(void* p) {
+    return (__attribute__((address_space(1))) T*)(p);
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
     _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
     return (float)h;  // v_cvt_f32_f16: exact widening (arith.extf)

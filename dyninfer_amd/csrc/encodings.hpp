@@ -1,206 +1,325 @@
 // Per-encoding chunk decoders for the gfx950 GEMV kernels.
 //
-// A "chunk" is the unit one lane processes per step: CW consecutive weights of
-// one row, split into NG scale groups of GW = CW/NG weights.  Within a group
-// every weight is w = d·c + m with an unsigned integer code c (0..255) and two
-// f32 constants (d, m) of the group, so the kernel computes
-//     Σ_k w_k x_k = d · Σ_k c_k x_k + m · Σ_k x_k
-// with one byte->float convert and one fma per weight and activation row,
-// and two fmas per group.  The (c, d, m) of each encoding, against the
+// A chunk is what one lane handles per step: CW weights of one row (one GGUF
+// block, a quarter of a Q6_K super-block, 32 MLX weights).  Its integer codes
+// become packed f16 pairs by the exponent trick: with a code c < 1024 in the
+// mantissa bits, the f16 bit pattern 0x6400 | c is exactly 1024 + c, so one
+// v_and_or_b32 decodes two weights.  A code at mantissa bits 4.. decodes to
+// 1024 + 16c; those pairs meet activations stored divided by 16 (exact).
+// v_dot2_f32_f16 multiplies two decoded codes by two f16 activations (each
+// product exact in f32) and adds them to an f32 accumulator, which starts at
+// -C for the chunk's scale group:
+//     Σ_k (c_k - off)·v_k = Σ_k P_k·v_k - C,   C = Σ_k coef_k·v_k,
+// coef = 1024 + off for pairs at bit 0 and 1024 + 16·off for pairs at bit 4,
+// where P is the decoded pair value and v the stored activation.  v is the
+// activation scaled by a power of two per scale group (largest magnitude in
+// [2^13, 2^14), so f16 neither overflows nor flushes small values) and
+// rounded to f16: the only rounding besides f32 accumulation, relative 2^-11
+// per product, well inside the 2e-3 normalised tolerance.  The group result is
+// then s·acc (s the power of two) times the weight scale, plus the weight
+// offset times Σx for affine encodings.  Per encoding, against the
 // reference's dequantisation (gguf_codegen.rs:382-526, mlx_affine.rs:593-598):
-//   Q4_0  c = nibble q,            d = f16 d,        m = -8·d        (w = (q-8)·d)
-//   Q4_1  c = nibble q,            d = f16 d,        m = f16 m       (w = q·d + m)
-//   Q8_0  c = int8 q + 128,        d = f16 d,        m = -128·d      (w = q·d)
-//   Q6_K  c = 6-bit q (0..63),     d = sc·d,         m = -32·sc·d    (w = (q-32)·sc·d)
-//   MLX   c = nibble q,            d = scale,        m = bias        (w = q·s + b)
-// (-8·d, -128·d, -32·sc·d and sc·d are exact in f32.)  The contraction is
-// therefore the reference's up to f32 reassociation; the bit-exact
-// dequantisation hook is dequant.hip.
+//   Q4_0  w = (q-8)·d            code q (nibble), off 8
+//   Q4_1  w = q·d + m            code q,          off 0, + m·Σx
+//   Q8_0  w = q·d                code q+128 (xor 0x80), off 128
+//   Q6_K  w = (q-32)·sc·d        6-bit code q,    off 32, per 16-weight group
+//   MLX   w = q·s + b            code q,          off 0, + b·Σx
 //
-// Codes are delivered four at a time, as the four bytes of a dword whose
-// weights are four consecutive k (or, for MLX, in the order given by
-// mlx quad_perm), so the kernel converts them with v_cvt_f32_ubyte{0..3}.
+// Layout contract with the activation staging (gemv_kernels.hpp): for code
+// dword t of a chunk the lane reads PPT f16 pairs, pair h holding activations
+// xoff(t, h, 0) and xoff(t, h, 1) (offsets within the chunk's activation runs),
+// divided by 16 when dv(t, h), accumulated into group grp(t, h).
 #pragma once
 #include "device_common.hpp"
 #include "kernels.hpp"
 
 namespace dmx {
 
-// v & mask, hidden from the optimiser: with the mask's known zero bits the
-// compiler would rewrite later byte extractions into v_bfe + v_cvt_f32_ubyte0
-// instead of a single v_cvt_f32_ubyte{1,2,3}.
-template <uint32_t MASK>
-__device__ __forceinline__ uint32_t and_opaque(uint32_t v) {
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// c + a.lo·b.lo + a.hi·b.hi (v_dot2_f32_f16)
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b), c, false);
+}
+
+constexpr uint32_t kMagic = 0x64006400u;  // f16 1024.0 in both halves
+
+// (a & m) | b as one v_and_or_b32.  Written as asm because the compiler
+// otherwise emits v_and_b32 + v_or_b32 with literal operands (a VOP3 op takes
+// no literal on gfx9).  The mask lives in a scalar register and b in a vector
+// register (gfx9 allows one scalar operand per VALU instruction), both loaded
+// once outside the loops.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t b) {
     uint32_t r;
-    asm("v_and_b32 %0, %2, %1" : "=v"(r) : "v"(v), "i"(MASK));
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(b));
     return r;
 }
 
-// (a & MASK) | b, opaque (v_and_or_b32).
-template <uint32_t MASK>
-__device__ __forceinline__ uint32_t and_or_opaque(uint32_t a, uint32_t b) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %3, %2" : "=v"(r) : "v"(a), "v"(b), "s"(MASK));  // VOP3: no literal on gfx9
-    return r;
+// Selector for v_perm_b32 that extracts the dword starting `sh` bytes into a
+// 4-byte-aligned pair {hi, lo}, plus a fixed byte offset `add` (0 or 2).
+__device__ __forceinline__ uint32_t realign_sel(uint32_t sh, uint32_t add) {
+    return 0x03020100u + 0x01010101u * (sh + add);
 }
 
-// Raw dwords of a GGUF block, loaded from the 4-byte-aligned dword containing
-// its first byte, with the byte shift (0 or 2) that realign() applies later.
-// Realigning after the load keeps the loads free of consumers, so a lane can
-// have every row's block in flight at once.
-template <int NDW, class RAW>
-__device__ __forceinline__ RAW load_raw_block(const uint8_t* p) {
-    const uintptr_t a = (uintptr_t)p;
-    RAW r;
-    load_dwords<NDW>(reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3), r.d);
-    r.sh = (uint32_t)(a & 3u);
+// The four decoded pairs of a dword of nibble codes whose weights are
+// (i, i+2) [bits 0-3 and 16-19], (j, j+2) x16 [bits 4-7 and 20-23],
+// and the same one byte up [bits 8-11/24-27, 12-15/28-31].
+__device__ __forceinline__ void nibble_pairs(uint32_t d, uint32_t (&p)[4]) {
+    const uint32_t d8 = d >> 8;
+    p[0] = and_or(d, 0x000F000Fu, kMagic);
+    p[1] = and_or(d, 0x00F000F0u, kMagic);
+    p[2] = and_or(d8, 0x000F000Fu, kMagic);
+    p[3] = and_or(d8, 0x00F000F0u, kMagic);
+}
+
+// Raw dwords of a 2-byte-aligned GGUF block: NDW dwords from the 4-byte-
+// aligned dword holding its first byte (each dword overlaps the block, so no
+// load leaves a page the block touches), and the byte shift 0 or 2.
+template <int NDW>
+struct RawBlock {
+    uint32_t d[NDW];
+    uint32_t sh;
+};
+
+// A 2-byte-aligned block at byte offset `off` from a uniform base, addressed
+// as the 4-byte-aligned uniform base abase = base & ~3 plus the per-lane
+// 32-bit offset o = off + (base & 3) (32-bit offsets keep the address
+// arithmetic per lane to one add; o never wraps, since the C ABI limits a
+// weight to 4 GiB minus 16 bytes).  The loads start at abase + (o & ~3).
+struct AlignedOffset {
+    const uint8_t* abase;
+    uint32_t o;
+};
+
+__device__ __forceinline__ AlignedOffset aligned_offset(const uint8_t* base, uint32_t off) {
+    const uint32_t bsh = (uint32_t)((uintptr_t)base & 3u);
+    return {base - bsh, off + bsh};
+}
+
+template <int NDW>
+__device__ __forceinline__ RawBlock<NDW> load_raw_block(const uint8_t* base, uint32_t off) {
+    const AlignedOffset a = aligned_offset(base, off);
+    RawBlock<NDW> r;
+    r.sh = a.o & 3u;
+    load_dwords<NDW>(reinterpret_cast<const uint32_t*>(a.abase + (a.o & ~3u)), r.d);
     return r;
 }
 
 // ------------------------------------------------------------------ GGUF Q4_0
-// 18-byte block: f16 d, 16 bytes; low nibble of byte l = weight l, high = 16+l
-// (gguf_codegen.rs:412-472, lane map :452).
+// 18-byte block: f16 d, 16 bytes qs; low nibble of qs[l] = weight l, high =
+// weight 16+l (gguf_codegen.rs:412-472, lane map :452).  Code dword t = qs
+// bytes 4t..4t+3.
 struct EncQ40 {
-    static constexpr int CW = 32, NG = 1, GW = 32, NDW = 5, BB = 18;
-    struct Chunk { uint32_t q[4]; float d; };
-    struct Raw { uint32_t d[NDW]; uint32_t sh; };
-    __device__ __forceinline__ static Raw load_raw(const uint8_t* row, uint32_t u) {
-        return load_raw_block<NDW, Raw>(row + (size_t)u * 18u);
+    static constexpr uint32_t ENC = ENC_Q4_0;
+    static constexpr int CW = 32, QK = 32, NT = 4, PPT = 4, NG = 1, NDW = 5, BB = 18;
+    static constexpr bool AFFINE = false;
+    static constexpr int NRUN = 1, RUNLEN = 32, RUNSTRIDE = 0;  // activation runs of a chunk
+    __device__ __forceinline__ static uint32_t xbase(uint32_t u) { return 32u * u; }
+    static constexpr float coef(bool dv) { return dv ? 1152.0f : 1032.0f; }
+    static constexpr int xoff(int t, int h, int e) { return 4 * t + (h >> 1) + 2 * e + 16 * (h & 1); }
+    static constexpr bool dv(int, int h) { return (h & 1) != 0; }
+    static constexpr int grp(int, int) { return 0; }
+    using Raw = RawBlock<NDW>;
+    struct Chunk { uint32_t q[NT]; float d; };
+    __device__ __forceinline__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u) {
+        return load_raw_block<NDW>(w, rowoff + u * (uint32_t)BB);
     }
-    __device__ __forceinline__ static Chunk unpack(const Raw& r) {
-        uint32_t e[NDW];
-        realign<NDW>(r.d, r.sh, e);
+    __device__ __forceinline__ static Chunk unpack(const Raw& r, uint32_t) {
         Chunk c;
-        c.d = f16_bits_to_f32(e[0]);
+        const uint32_t sel = realign_sel(r.sh, 2);
 #pragma unroll
-        for (int t = 0; t < 4; t++) c.q[t] = __builtin_amdgcn_alignbyte(e[t + 1], e[t], 2);
+        for (int t = 0; t < NT; t++) c.q[t] = __builtin_amdgcn_perm(r.d[t + 1], r.d[t], sel);
+        c.d = f16_bits_to_f32(r.d[0] >> (8u * r.sh));
         return c;
     }
-    __device__ __forceinline__ static float scale(const Chunk& c, int) { return c.d; }
-    __device__ __forceinline__ static float offset(const Chunk& c, int) { return -8.0f * c.d; }
-    // quad j of group 0: j < 4 -> low nibbles of quant dword j (k = 4j);
-    // j >= 4 -> high nibbles of dword j-4 (k = 16 + 4(j-4)).
-    static constexpr int QUADS = 8;
-    __device__ __forceinline__ static int kofs(int, int j) { return j < 4 ? 4 * j : 16 + 4 * (j - 4); }
-    __device__ __forceinline__ static uint32_t codes(const Chunk& c, int, int j) {
-        return j < 4 ? and_opaque<0x0F0F0F0Fu>(c.q[j]) : and_opaque<0x0F0F0F0Fu>(c.q[j - 4] >> 4);
-    }
+    __device__ __forceinline__ static void pairs(const Chunk& c, int t, uint32_t (&p)[PPT]) { nibble_pairs(c.q[t], p); }
+    __device__ __forceinline__ static float gscale(const Chunk& c, int) { return c.d; }
+    __device__ __forceinline__ static float goffset(const Chunk&, int) { return 0.0f; }
+    __device__ __forceinline__ static void zero_if(Chunk& c, bool z) { c.d = z ? 0.0f : c.d; }
 };
 
 // ------------------------------------------------------------------ GGUF Q4_1
-// 20-byte block: f16 d, f16 m, 16 bytes of nibbles (same lane map); blocks are
+// 20-byte block: f16 d, f16 m, 16 bytes qs (same nibble map).  Blocks are
 // 4-byte aligned (the C ABI requires a 4-byte-aligned base).
 struct EncQ41 {
-    static constexpr int CW = 32, NG = 1, GW = 32, NDW = 5, BB = 20;
-    struct Chunk { uint32_t q[4]; float d, m; };
+    static constexpr uint32_t ENC = ENC_Q4_1;
+    static constexpr int CW = 32, QK = 32, NT = 4, PPT = 4, NG = 1, NDW = 5, BB = 20;
+    static constexpr bool AFFINE = true;
+    static constexpr int NRUN = 1, RUNLEN = 32, RUNSTRIDE = 0;
+    __device__ __forceinline__ static uint32_t xbase(uint32_t u) { return 32u * u; }
+    static constexpr float coef(bool) { return 1024.0f; }
+    static constexpr int xoff(int t, int h, int e) { return EncQ40::xoff(t, h, e); }
+    static constexpr bool dv(int t, int h) { return EncQ40::dv(t, h); }
+    static constexpr int grp(int, int) { return 0; }
     struct Raw { uint32_t d[NDW]; };
-    __device__ __forceinline__ static Raw load_raw(const uint8_t* row, uint32_t u) {
+    struct Chunk { uint32_t q[NT]; float d, m; };
+    __device__ __forceinline__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u) {
         Raw r;
-        load_dwords<NDW>(reinterpret_cast<const uint32_t*>(row + (size_t)u * 20u), r.d);
+        load_dwords<NDW>(reinterpret_cast<const uint32_t*>(w + (rowoff + u * (uint32_t)BB)), r.d);
         return r;
     }
-    __device__ __forceinline__ static Chunk unpack(const Raw& r) {
+    __device__ __forceinline__ static Chunk unpack(const Raw& r, uint32_t) {
         Chunk c;
+#pragma unroll
+        for (int t = 0; t < NT; t++) c.q[t] = r.d[t + 1];
         c.d = f16_bits_to_f32(r.d[0]);
         c.m = f16_bits_to_f32(r.d[0] >> 16);
-#pragma unroll
-        for (int t = 0; t < 4; t++) c.q[t] = r.d[t + 1];
         return c;
     }
-    __device__ __forceinline__ static float scale(const Chunk& c, int) { return c.d; }
-    __device__ __forceinline__ static float offset(const Chunk& c, int) { return c.m; }
-    static constexpr int QUADS = 8;
-    __device__ __forceinline__ static int kofs(int, int j) { return j < 4 ? 4 * j : 16 + 4 * (j - 4); }
-    __device__ __forceinline__ static uint32_t codes(const Chunk& c, int, int j) {
-        return j < 4 ? and_opaque<0x0F0F0F0Fu>(c.q[j]) : and_opaque<0x0F0F0F0Fu>(c.q[j - 4] >> 4);
+    __device__ __forceinline__ static void pairs(const Chunk& c, int t, uint32_t (&p)[PPT]) { nibble_pairs(c.q[t], p); }
+    __device__ __forceinline__ static float gscale(const Chunk& c, int) { return c.d; }
+    __device__ __forceinline__ static float goffset(const Chunk& c, int) { return c.m; }
+    __device__ __forceinline__ static void zero_if(Chunk& c, bool z) {
+        c.d = z ? 0.0f : c.d;
+        c.m = z ? 0.0f : c.m;
     }
 };
 
 // ------------------------------------------------------------------ GGUF Q8_0
 // 34-byte block: f16 d, 32 int8 codes (gguf_codegen.rs:382-410).  Codes are
-// flipped to q + 128 (xor 0x80) so they convert as unsigned bytes.
+// flipped to q + 128 (xor 0x80) so they decode as unsigned bytes.
 struct EncQ80 {
-    static constexpr int CW = 32, NG = 1, GW = 32, NDW = 9, BB = 34;
-    struct Chunk { uint32_t q[8]; float d; };
-    struct Raw { uint32_t d[NDW]; uint32_t sh; };
-    __device__ __forceinline__ static Raw load_raw(const uint8_t* row, uint32_t u) {
-        return load_raw_block<NDW, Raw>(row + (size_t)u * 34u);
+    static constexpr uint32_t ENC = ENC_Q8_0;
+    static constexpr int CW = 32, QK = 32, NT = 8, PPT = 2, NG = 1, NDW = 9, BB = 34;
+    static constexpr bool AFFINE = false;
+    static constexpr int NRUN = 1, RUNLEN = 32, RUNSTRIDE = 0;
+    __device__ __forceinline__ static uint32_t xbase(uint32_t u) { return 32u * u; }
+    static constexpr float coef(bool) { return 1152.0f; }
+    static constexpr int xoff(int t, int h, int e) { return 4 * t + h + 2 * e; }
+    static constexpr bool dv(int, int) { return false; }
+    static constexpr int grp(int, int) { return 0; }
+    using Raw = RawBlock<NDW>;
+    struct Chunk { uint32_t q[NT]; float d; };
+    __device__ __forceinline__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u) {
+        return load_raw_block<NDW>(w, rowoff + u * (uint32_t)BB);
     }
-    __device__ __forceinline__ static Chunk unpack(const Raw& r) {
-        uint32_t e[NDW];
-        realign<NDW>(r.d, r.sh, e);
+    __device__ __forceinline__ static Chunk unpack(const Raw& r, uint32_t) {
         Chunk c;
-        c.d = f16_bits_to_f32(e[0]);
+        const uint32_t sel = realign_sel(r.sh, 2);
 #pragma unroll
-        for (int t = 0; t < 8; t++) c.q[t] = __builtin_amdgcn_alignbyte(e[t + 1], e[t], 2);
+        for (int t = 0; t < NT; t++) c.q[t] = __builtin_amdgcn_perm(r.d[t + 1], r.d[t], sel) ^ 0x80808080u;
+        c.d = f16_bits_to_f32(r.d[0] >> (8u * r.sh));
         return c;
     }
-    __device__ __forceinline__ static float scale(const Chunk& c, int) { return c.d; }
-    __device__ __forceinline__ static float offset(const Chunk& c, int) { return -128.0f * c.d; }
-    static constexpr int QUADS = 8;
-    __device__ __forceinline__ static int kofs(int, int j) { return 4 * j; }
-    __device__ __forceinline__ static uint32_t codes(const Chunk& c, int, int j) {
-        uint32_t r;
-        asm("v_xor_b32 %0, %2, %1" : "=v"(r) : "v"(c.q[j]), "i"(0x80808080u));
-        return r;
+    __device__ __forceinline__ static void pairs(const Chunk& c, int t, uint32_t (&p)[PPT]) {
+        const uint32_t d = c.q[t], d8 = d >> 8;
+        p[0] = and_or(d, 0x00FF00FFu, kMagic);   // weights 4t, 4t+2
+        p[1] = and_or(d8, 0x00FF00FFu, kMagic);  // weights 4t+1, 4t+3
     }
+    __device__ __forceinline__ static float gscale(const Chunk& c, int) { return c.d; }
+    __device__ __forceinline__ static float goffset(const Chunk&, int) { return 0.0f; }
+    __device__ __forceinline__ static void zero_if(Chunk& c, bool z) { c.d = z ? 0.0f : c.d; }
 };
 
 // ------------------------------------------------------------------ GGUF Q6_K
 // 210-byte super-block of 256 (gguf_codegen.rs:474-526): ql = bytes 0..128,
 // qh = 128..192, sc = int8 192..208, d = f16 208..210.  Weight
-// n*128 + h*64 + p*32 + s*16 + l: low4 = nibble h of ql[n*64 + p*32 + s*16 + l],
-// high2 = (qh[n*32 + s*16 + l] >> 2(2h+p)) & 3, sub-scale sc[n*8 + h*4 + p*2 + s].
-// Group g = (n, h, p, s) = 16 weights; quads j = 0..3 are l = 4j..4j+3.
+// n*128 + 32j + 16s + i (n, s in {0,1}, j in 0..3, i in 0..15) has
+//   low 4 bits  = nibble (j >> 1) of ql[64n + 32(j & 1) + 16s + i],
+//   high 2 bits = bits 2j..2j+1 of qh[32n + 16s + i],
+//   scale       = sc[8n + 2j + s].
+// Chunk u is the quarter (n, s) = ((u >> 1) & 1, u & 1) of super-block u >> 2:
+// 64 weights in four 16-weight groups j, read as three 16-byte runs
+// A = ql[64n+16s..], B = ql[64n+32+16s..], H = qh[32n+16s..] plus the scales.
+// Code dword t holds positions i = 4t..4t+3 of the three runs; its eight pairs
+// are (j = 0..3) x (positions (4t, 4t+2), then (4t+1, 4t+3)); groups 2 and 3
+// decode the nibble at bits 4..7 (x16).
 struct EncQ6K {
-    static constexpr int CW = 256, NG = 16, GW = 16, NDW = 53, BB = 210;
-    struct Chunk { uint32_t e[NDW]; };
-    struct Raw { uint32_t d[NDW]; uint32_t sh; };
-    __device__ __forceinline__ static Raw load_raw(const uint8_t* row, uint32_t u) {
-        return load_raw_block<NDW, Raw>(row + (size_t)u * 210u);
+    static constexpr uint32_t ENC = ENC_Q6_K;
+    static constexpr int CW = 64, QK = 256, NT = 4, PPT = 8, NG = 4, BB = 210;
+    static constexpr bool AFFINE = false;
+    static constexpr int NRUN = 4, RUNLEN = 16, RUNSTRIDE = 32;  // activation runs of group j at 32j
+    __device__ __forceinline__ static uint32_t xbase(uint32_t u) {
+        return 256u * (u >> 2) + 128u * ((u >> 1) & 1u) + 16u * (u & 1u);
     }
-    __device__ __forceinline__ static Chunk unpack(const Raw& r) {
+    static constexpr float coef(bool dv) { return dv ? 1536.0f : 1056.0f; }
+    static constexpr int xoff(int t, int h, int e) { return 32 * (h & 3) + 4 * t + (h >> 2) + 2 * e; }
+    static constexpr bool dv(int, int h) { return (h & 3) >= 2; }
+    static constexpr int grp(int, int h) { return h & 3; }
+    struct Raw { uint32_t a[5], b[5], h[5], s[5]; uint32_t sh; };
+    struct Chunk { uint32_t a[NT], b[NT], h[NT]; float dsc[NG]; };
+    __device__ __forceinline__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u) {
+        const AlignedOffset a = aligned_offset(w, rowoff + (u >> 2) * (uint32_t)BB);
+        const uint32_t n = (u >> 1) & 1u, s = u & 1u;
+        const uint32_t sh = a.o & 3u;
+        const uint32_t* al = reinterpret_cast<const uint32_t*>(a.abase + (a.o & ~3u));
+        const uint32_t oa = (64u * n + 16u * s) >> 2;
+        Raw r;
+        load_dwords<5>(al + oa, r.a);
+        load_dwords<5>(al + oa + 8u, r.b);
+        load_dwords<5>(al + ((128u + 32u * n + 16u * s) >> 2), r.h);
+        load_dwords<5>(al + (192u >> 2), r.s);  // sc[0..16) and d
+        r.sh = sh;
+        return r;
+    }
+    __device__ __forceinline__ static Chunk unpack(const Raw& r, uint32_t u) {
         Chunk c;
-        realign<NDW>(r.d, r.sh, c.e);
+        const uint32_t sel = realign_sel(r.sh, 0);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            c.a[t] = __builtin_amdgcn_perm(r.a[t + 1], r.a[t], sel);
+            c.b[t] = __builtin_amdgcn_perm(r.b[t + 1], r.b[t], sel);
+            c.h[t] = __builtin_amdgcn_perm(r.h[t + 1], r.h[t], sel);
+        }
+        const bool n = ((u >> 1) & 1u) != 0;
+        const uint32_t bs = 8u * (u & 1u);
+        // sc bytes 8n + s + {0, 2} (groups 0, 1) and 8n + 4 + s + {0, 2} (groups 2, 3)
+        const uint32_t s01 = __builtin_amdgcn_perm(n ? r.s[3] : r.s[1], n ? r.s[2] : r.s[0], sel);
+        const uint32_t s23 = __builtin_amdgcn_perm(n ? r.s[4] : r.s[2], n ? r.s[3] : r.s[1], sel);
+        // d = bytes 16..17 of the run
+        const float d = f16_bits_to_f32(r.sh ? (r.s[4] >> 16) : r.s[4]);
+        c.dsc[0] = (float)(int32_t)__builtin_amdgcn_sbfe(s01, bs, 8u) * d;
+        c.dsc[1] = (float)(int32_t)__builtin_amdgcn_sbfe(s01, bs + 16u, 8u) * d;
+        c.dsc[2] = (float)(int32_t)__builtin_amdgcn_sbfe(s23, bs, 8u) * d;
+        c.dsc[3] = (float)(int32_t)__builtin_amdgcn_sbfe(s23, bs + 16u, 8u) * d;
         return c;
     }
-    __device__ __forceinline__ static float dsuper(const Chunk& c) { return f16_bits_to_f32(c.e[52]); }
-    __device__ __forceinline__ static float scale(const Chunk& c, int g) {
-        const int8_t sc = (int8_t)((c.e[48 + g / 4] >> (8 * (g % 4))) & 0xFFu);
-        return (float)sc * dsuper(c);
+    __device__ __forceinline__ static void pairs(const Chunk& c, int t, uint32_t (&p)[PPT]) {
+        const uint32_t A = c.a[t], B = c.b[t], H = c.h[t];
+        // positions (4t, 4t+2): bytes 0 and 2
+        {
+            const uint32_t h4 = H << 4, h2 = H << 2;
+            p[0] = and_or(A, 0x000F000Fu, and_or(h4, 0x00300030u, kMagic));  // j=0: ql lo, qh bits 0-1
+            p[1] = and_or(B, 0x000F000Fu, and_or(h2, 0x00300030u, kMagic));  // j=1: ql lo, qh bits 2-3
+            p[2] = and_or(A, 0x00F000F0u, and_or(h4, 0x03000300u, kMagic));  // j=2: ql hi, qh bits 4-5 (x16)
+            p[3] = and_or(B, 0x00F000F0u, and_or(h2, 0x03000300u, kMagic));  // j=3: ql hi, qh bits 6-7 (x16)
+        }
+        // positions (4t+1, 4t+3): bytes 1 and 3
+        {
+            const uint32_t A8 = A >> 8, B8 = B >> 8, h4 = H >> 4, h2 = H >> 6;
+            p[4] = and_or(A8, 0x000F000Fu, and_or(h4, 0x00300030u, kMagic));
+            p[5] = and_or(B8, 0x000F000Fu, and_or(h2, 0x00300030u, kMagic));
+            p[6] = and_or(A8, 0x00F000F0u, and_or(h4, 0x03000300u, kMagic));
+            p[7] = and_or(B8, 0x00F000F0u, and_or(h2, 0x03000300u, kMagic));
+        }
     }
-    __device__ __forceinline__ static float offset(const Chunk& c, int g) { return -32.0f * scale(c, g); }
-    static constexpr int QUADS = 4;
-    __device__ __forceinline__ static int kofs(int g, int j) {
-        const int n = g >> 3, h = (g >> 2) & 1, p = (g >> 1) & 1, s = g & 1;
-        return n * 128 + h * 64 + p * 32 + s * 16 + 4 * j;
-    }
-    __device__ __forceinline__ static uint32_t codes(const Chunk& c, int g, int j) {
-        const int n = g >> 3, h = (g >> 2) & 1, p = (g >> 1) & 1, s = g & 1;
-        const uint32_t ql = c.e[n * 16 + p * 8 + s * 4 + j];
-        const uint32_t qh = c.e[32 + n * 8 + s * 4 + j];
-        const uint32_t low = (ql >> (4 * h)) & 0x0F0F0F0Fu;
-        const int hs = 2 * (2 * h + p);
-        const uint32_t hi = hs <= 4 ? (qh << (4 - hs)) : (qh >> (hs - 4));
-        return and_or_opaque<0x30303030u>(hi, low);
+    __device__ __forceinline__ static float gscale(const Chunk& c, int g) { return c.dsc[g]; }
+    __device__ __forceinline__ static float goffset(const Chunk&, int) { return 0.0f; }
+    __device__ __forceinline__ static void zero_if(Chunk& c, bool z) {
+#pragma unroll
+        for (int g = 0; g < NG; g++) c.dsc[g] = z ? 0.0f : c.dsc[g];
     }
 };
 
 // ------------------------------------------------------------------ MLX affine U4
 // One chunk = 32 weights = 4 packed u32 words (weight i of a word = bits
 // 4i..4i+3, fixture.rs:307-311) sharing one scale and bias (group size is a
-// multiple of 32).  Quad j covers k = 4j..4j+3: word j/2, nibbles 4(j&1)..+3,
-// i.e. bytes b0/b1 (j even) or b2/b3 (j odd) of lo = w & 0x0F0F0F0F (even
-// nibbles) and hi = (w >> 4) & 0x0F0F0F0F (odd nibbles).  codes() interleaves
-// them back into k order with one v_perm.
+// multiple of 32).  Word t's pairs: nibbles (0,4), (1,5) x16, (2,6), (3,7) x16.
 struct EncMlxU4 {
-    static constexpr int CW = 32, NG = 1, GW = 32;
-    static constexpr int QUADS = 8;
-    struct Chunk { uint32_t w[4]; float s, b; };
-    // raw: packed words plus the scale/bias bit patterns (f32, or f16/bf16 in the
+    static constexpr uint32_t ENC = ENC_MLX_U4;
+    static constexpr int CW = 32, NT = 4, PPT = 4, NG = 1;
+    static constexpr bool AFFINE = true;
+    static constexpr int NRUN = 1, RUNLEN = 32, RUNSTRIDE = 0;
+    __device__ __forceinline__ static uint32_t xbase(uint32_t u) { return 32u * u; }
+    static constexpr float coef(bool) { return 1024.0f; }
+    static constexpr int xoff(int t, int h, int e) { return 8 * t + 2 * (h >> 1) + (h & 1) + 4 * e; }
+    static constexpr bool dv(int, int h) { return (h & 1) != 0; }
+    static constexpr int grp(int, int) { return 0; }
+    // packed words plus the scale/bias bit patterns (f32, or f16/bf16 in the
     // low half) and their dtype
     struct Raw { uint32_t w[4]; uint32_t s, b, kind; };
-    __device__ __forceinline__ static Chunk unpack(const Raw& r) {
+    struct Chunk { uint32_t w[4]; float s, b; };
+    __device__ __forceinline__ static Chunk unpack(const Raw& r, uint32_t) {
         Chunk c;
 #pragma unroll
         for (int i = 0; i < 4; i++) c.w[i] = r.w[i];
@@ -216,15 +335,18 @@ struct EncMlxU4 {
         }
         return c;
     }
-    __device__ __forceinline__ static int kofs(int, int j) { return 4 * j; }
-    __device__ __forceinline__ static float scale(const Chunk& c, int) { return c.s; }
-    __device__ __forceinline__ static float offset(const Chunk& c, int) { return c.b; }
-    __device__ __forceinline__ static uint32_t codes(const Chunk& c, int, int j) {
-        const uint32_t w = c.w[j >> 1];
-        const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-        // bytes (lo.b0, hi.b0, lo.b1, hi.b1) or (lo.b2, hi.b2, lo.b3, hi.b3)
-        const uint32_t sel = (j & 1) ? 0x03070206u : 0x01050004u;
-        return __builtin_amdgcn_perm(lo, hi, sel);
+    __device__ __forceinline__ static void pairs(const Chunk& c, int t, uint32_t (&p)[PPT]) {
+        const uint32_t w = c.w[t], w8 = w >> 8;
+        p[0] = and_or(w, 0x000F000Fu, kMagic);   // nibbles 0, 4
+        p[1] = and_or(w, 0x00F000F0u, kMagic);   // nibbles 1, 5 (x16)
+        p[2] = and_or(w8, 0x000F000Fu, kMagic);  // nibbles 2, 6
+        p[3] = and_or(w8, 0x00F000F0u, kMagic);  // nibbles 3, 7 (x16)
+    }
+    __device__ __forceinline__ static float gscale(const Chunk& c, int) { return c.s; }
+    __device__ __forceinline__ static float goffset(const Chunk& c, int) { return c.b; }
+    __device__ __forceinline__ static void zero_if(Chunk& c, bool z) {
+        c.s = z ? 0.0f : c.s;
+        c.b = z ? 0.0f : c.b;
     }
 };
 

@@ -8,13 +8,13 @@
 
 namespace dmx {
 
-hipError_t gemv_launch_q4_0(const GemvParams& p, uint32_t B, bool xbf16, hipStream_t st);
-hipError_t gemv_launch_q4_1(const GemvParams& p, uint32_t B, bool xbf16, hipStream_t st);
-hipError_t gemv_launch_q8_0(const GemvParams& p, uint32_t B, bool xbf16, hipStream_t st);
-hipError_t gemv_launch_q6_k(const GemvParams& p, uint32_t B, bool xbf16, hipStream_t st);
-hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q4_0(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q4_1(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q8_0(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q6_k(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st);
 
-hipError_t cached_occupancy(const void* kernel, size_t lds, int* per_cu, int* cus) {
+hipError_t cached_occupancy(const void* kernel, size_t lds, int threads, int* per_cu, int* cus) {
     struct Entry {
         const void* kernel;
         size_t lds;
@@ -36,7 +36,9 @@ hipError_t cached_occupancy(const void* kernel, size_t lds, int* per_cu, int* cu
     }
     int n = 0, blocks = 0;
     e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 256, lds);
+    if (e == hipSuccess && lds > 64u * 1024u)
+        e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, threads, lds);
     if (e != hipSuccess) return e;
     std::lock_guard<std::mutex> lock(mu);
     cache.push_back({kernel, lds, dev, blocks, n});
@@ -45,38 +47,63 @@ hipError_t cached_occupancy(const void* kernel, size_t lds, int* per_cu, int* cu
     return hipSuccess;
 }
 
+// LDS one workgroup may use on the current device (cached per device).
+static hipError_t lds_limit(uint32_t* out) {
+    static std::mutex mu;
+    static std::vector<std::pair<int, uint32_t>> cache;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& c : cache)
+        if (c.first == dev) {
+            *out = c.second;
+            return hipSuccess;
+        }
+    int v = 0;
+    e = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (e != hipSuccess) return e;
+    const uint32_t lim = (uint32_t)v < kLdsBytes ? (uint32_t)v : kLdsBytes;
+    cache.push_back({dev, lim});
+    *out = lim;
+    return hipSuccess;
+}
+
+bool gemv_k_supported(uint32_t enc, uint32_t K) { return xtile_bytes(enc, 1, K) <= kLdsBytes; }
+
 namespace {
 
 struct EncInfo {
     uint32_t chunk_weights;  // weights one lane handles per step
-    uint32_t max_b;          // largest register batch instantiated
-    bool super_block;        // Q6_K: 256-weight chunks hold fewer rows per lane
+    bool q6k;                // 64-weight Q6_K chunks hold fewer rows per lane
 };
 
 bool enc_info(uint32_t enc, EncInfo& e) {
     switch (enc) {
-    case ENC_Q4_0: e = {32, 16, false}; return true;
-    case ENC_Q4_1: e = {32, 16, false}; return true;
-    case ENC_Q8_0: e = {32, 16, false}; return true;
-    case ENC_Q6_K: e = {256, 8, true}; return true;
-    case ENC_MLX_U4: e = {32, 16, false}; return true;
+    case ENC_Q4_0:
+    case ENC_Q4_1:
+    case ENC_Q8_0:
+    case ENC_MLX_U4: e = {32, false}; return true;
+    case ENC_Q6_K: e = {64, true}; return true;
     default: return false;
     }
 }
 
-// Rows per lane group; must match rows_per_group<E, B>() in gemv_kernels.hpp.
+// Rows per lane group for register batch B; must match rows_per_group<E, B>()
+// in gemv_kernels.hpp.  With one activation row, a single row per group is
+// also instantiated.
 uint32_t rows_per_group(const EncInfo& e, uint32_t B) {
-    if (e.super_block) return 1;
-    return B <= 2 ? 4 : (B <= 8 ? 2 : 1);
+    if (e.q6k) return B <= 2 ? 2 : 1;
+    return B <= 4 ? 4 : 2;
 }
 
-hipError_t launch(uint32_t enc, const GemvParams& p, uint32_t B, bool xbf16, hipStream_t st) {
+hipError_t launch(uint32_t enc, const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st) {
     switch (enc) {
-    case ENC_Q4_0: return gemv_launch_q4_0(p, B, xbf16, st);
-    case ENC_Q4_1: return gemv_launch_q4_1(p, B, xbf16, st);
-    case ENC_Q8_0: return gemv_launch_q8_0(p, B, xbf16, st);
-    case ENC_Q6_K: return gemv_launch_q6_k(p, B, xbf16, st);
-    case ENC_MLX_U4: return gemv_launch_mlx_u4(p, B, xbf16, st);
+    case ENC_Q4_0: return gemv_launch_q4_0(p, B, R, xbf16, st);
+    case ENC_Q4_1: return gemv_launch_q4_1(p, B, R, xbf16, st);
+    case ENC_Q8_0: return gemv_launch_q8_0(p, B, R, xbf16, st);
+    case ENC_Q6_K: return gemv_launch_q6_k(p, B, R, xbf16, st);
+    case ENC_MLX_U4: return gemv_launch_mlx_u4(p, B, R, xbf16, st);
     default: return hipErrorInvalidValue;
     }
 }
@@ -88,11 +115,19 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     EncInfo info;
     if (!enc_info(enc, info) || nprob < 1 || nprob > kMaxProblems || batch < 1 || batch > (uint32_t)kMaxGemvBatch)
         return hipErrorInvalidValue;
-    // Batches larger than the widest instantiation run as consecutive passes.
-    if (batch > info.max_b) {
+    // Register batch: the next power of two, halved while its activation tile
+    // does not fit one workgroup's LDS; larger batches run as several passes.
+    uint32_t lim = 0;
+    hipError_t le = lds_limit(&lim);
+    if (le != hipSuccess) return le;
+    uint32_t B = 1;
+    while (B < batch && B < max_register_batch(enc)) B *= 2;
+    while (B > 1 && xtile_bytes(enc, B, K) > lim) B /= 2;
+    if (xtile_bytes(enc, B, K) > lim) return hipErrorInvalidValue;
+    if (batch > B) {
         const size_t xes = x_bf16 ? 2 : 4, yes = y_bf16 ? 2 : 4;
-        for (uint32_t r0 = 0; r0 < batch; r0 += info.max_b) {
-            const uint32_t nb = batch - r0 < info.max_b ? batch - r0 : info.max_b;
+        for (uint32_t r0 = 0; r0 < batch; r0 += B) {
+            const uint32_t nb = batch - r0 < B ? batch - r0 : B;
             GemvProblem sub[kMaxProblems];
             for (int i = 0; i < nprob; i++) {
                 sub[i] = probs[i];
@@ -104,24 +139,25 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
         }
         return hipSuccess;
     }
-    uint32_t B = 1;
-    while (B < batch) B *= 2;
-    const uint32_t R = rows_per_group(info, B);
     const uint32_t nch = K / info.chunk_weights;
-    uint64_t nsum = 0;
-    for (int i = 0; i < nprob; i++) nsum += probs[i].n;
-    // Lanes per row group: a power of two dividing the chunk count (every lane
-    // gets the same number of chunks per row block), the smallest that still
-    // yields >= 4096 row blocks (4 waves per SIMD), at most 64.  Fewer lanes
-    // per row mean longer per-lane chunk runs and fewer cross-lane reductions;
-    // more lanes mean more waves for matrices with few rows.
-    uint32_t lmax = 1;
-    while (lmax < 64 && nch % (2 * lmax) == 0) lmax *= 2;
+    // Lanes per row group: the largest power of two <= min(64, chunks), so the
+    // lanes of a wave read one contiguous run of rows (each load instruction
+    // covers consecutive blocks; splitting a wave over distant rows costs DRAM
+    // locality) and a row block's chunks need few rounds.  When L does not
+    // divide the chunk count, the lanes past the last chunk add zero.
     uint32_t L = 1;
-    auto rbs_for = [&](uint32_t l) { return nsum * l / (64ull * R); };
-    while (L < lmax && rbs_for(L) < 4096) L *= 2;
+    while (L < 64 && 2 * L <= nch) L *= 2;
     uint32_t lanes_log2 = 0;
     while ((1u << lanes_log2) < L) lanes_log2++;
+    // Rows per lane group: with one activation row, a single row when the
+    // matrices are too small to give every resident wave (~4096) two row
+    // blocks — more waves and a shorter per-task chain — else the wider tile.
+    uint32_t R = rows_per_group(info, B);
+    if (B == 1) {
+        uint64_t rbs = 0;
+        for (int i = 0; i < nprob; i++) rbs += (probs[i].n + (64u >> lanes_log2) * R - 1) / ((64u >> lanes_log2) * R);
+        if (rbs < 8192) R = 1;
+    }
     const uint32_t rows_per_rb = (64u >> lanes_log2) * R;
 
     GemvParams p = {};
@@ -147,7 +183,7 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     p.y_bf16 = y_bf16 ? 1u : 0u;
     p.group = group;
     p.sdtype = sdtype;
-    return launch(enc, p, B, x_bf16, stream);
+    return launch(enc, p, B, R, x_bf16, stream);
 }
 
 }  // namespace dmx

@@ -4,164 +4,324 @@
 // Semantics: y[b, o] = Σ_k x[b, k] · w[o, k] with f32 accumulation, w the
 // reference's dequantised weight (gguf_codegen.rs:268-314 `emit_linear`,
 // mlx_affine.rs:557-626 `emit_linear_u4`).  IREE's reduction order is itself
-// unspecified, so results agree within f32 reassociation, not bitwise.
+// unspecified, so results agree within f32 reassociation and the f16 rounding
+// of activations (encodings.hpp), not bitwise.
 //
-// Mapping (wave64; the packed weights are streamed once from HBM):
+// Mapping (wave64, 512-thread workgroups; packed weights stream once from HBM):
+//   * the activations are staged once per workgroup in LDS as f16 pairs in
+//     each encoding's decode order, with per-(row, chunk, group) constants
+//     (-C, power-of-two scale, Σx) — encodings.hpp gives the contract;
 //   * the weight rows are cut into row blocks of G·R rows (G = 64/L lane
-//     groups per wave, R rows per group); L lanes of a group split the K range:
-//     lane j takes chunks j, j+L, ... (cpl = chunks/L of them per row block);
-//   * the grid is persistent (occupancy x CUs waves): wave w walks row blocks
-//     w, w+W, ... and the lane's sequence of (row block, chunk) tasks runs as
-//     one software pipeline — the next task's weight bytes are loaded before
-//     the current task is computed, across row-block boundaries, so HBM
-//     latency hides behind arithmetic instead of being paid per wave;
-//   * GGUF blocks are only 2-byte aligned: each is loaded from the 4-byte-
-//     aligned dword containing its start and realigned in registers;
-//   * activations are staged once per workgroup in LDS as f32 (padded by 16
-//     bytes per chunk so the L lanes of a group hit distinct banks), or read
-//     through L1/L2 when B·K does not fit;
-//   * per weight: one v_cvt_f32_ubyte and one fma per activation row; each
-//     group's scale d and offset m are applied once as d·Σc·x + m·Σx
-//     (encodings.hpp), and Σx is shared by the R rows;
+//     groups per wave, R rows per group); the L lanes of a group split K:
+//     lane j takes chunks j, j+L, ... (cpl = ceil(chunks/L) of them per row
+//     block; a lane past the last chunk re-reads the last one and adds zero),
+//     so neighbouring lanes read neighbouring blocks (coalesced) and
+//     neighbouring activation chunks (distinct LDS banks, 16-byte padding);
+//   * the grid is persistent (occupancy x CUs workgroups): wave w walks row
+//     blocks w, w+W, ... and the lane's (row block, chunk) tasks run as one
+//     software pipeline — the next task's weight bytes are loaded before the
+//     current task is computed, and the first task's before the activation
+//     staging, so HBM latency overlaps staging and arithmetic;
+//   * per weight: half a v_and_or_b32 and half a v_dot2_f32_f16 per
+//     activation row; per group and row: two or three f32 ops;
 //   * at the end of a row block the L lanes combine their R·B partial sums
 //     with cross-lane shuffles and lane 0 of the group stores.
 // Several weights that share one activation (q/k/v, gate/up) are served by one
 // launch: row blocks are numbered across the problems.
 #pragma once
+#include <type_traits>
+
 #include "encodings.hpp"
 #include "kernels.hpp"
 
 namespace dmx {
 
-// a[i] for a wave-uniform i.  The four values are pinned in scalar registers
-// first: otherwise the optimiser folds the select chain back into a dynamic
-// index of the kernel-argument array, which it can only serve from a private
-// (scratch) copy of the array.
+constexpr int kGemvThreads = 512;
+
+// a[i] for a wave-uniform i, branch-free.  The four values are pinned in
+// scalar registers first (otherwise the optimiser folds the selection back
+// into a dynamic index of the kernel-argument array, which it can only serve
+// from a private scratch copy), then combined with masks (a select chain is
+// turned into branches, and branches between a load and its use cost the
+// wait counters their precision).
 template <class T>
 __device__ __forceinline__ T pick(uint32_t i, const T (&a)[kMaxProblems]) {
     static_assert(kMaxProblems == 4, "pick() assumes 4 problems");
-    T v0 = a[0], v1 = a[1], v2 = a[2], v3 = a[3];
-    asm("" : "+s"(v0), "+s"(v1), "+s"(v2), "+s"(v3));
-    return i == 0 ? v0 : i == 1 ? v1 : i == 2 ? v2 : v3;
+    static_assert(sizeof(T) == 8 || sizeof(T) == 4, "pick() takes pointers and 32-bit values");
+    typedef typename std::conditional<sizeof(T) == 8, uint64_t, uint32_t>::type U;
+    U v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] = __builtin_bit_cast(U, a[k]);
+    asm("" : "+s"(v[0]), "+s"(v[1]), "+s"(v[2]), "+s"(v[3]));
+    U r = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) r |= v[k] & ((U)0 - (U)(i == (uint32_t)k));
+    return __builtin_bit_cast(T, r);
 }
 
-// Four consecutive activations of row r at element k, as f32.
-template <bool XBF16>
-__device__ __forceinline__ float4 load_x4(const void* __restrict__ x, uint32_t ldx, uint32_t r, uint32_t k) {
-    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// ---------------------------------------------------------------- activation tile
+// LDS layout: pairs u32 [B][nch][XPW] (XPW = NT·PPT + 4: the chunk's decode-
+// ordered f16 pairs and 16 bytes of bank padding), then constants
+// f32 [B][nch][NG][NCF] = (-C, s, s·Σx, 0) (NCF = 2 without the Σx term).
+template <class E>
+struct XTile {
+    static constexpr int XPW = E::NT * E::PPT + 4;
+    static constexpr int NCF = E::AFFINE ? 4 : 2;
+    static constexpr uint32_t chunk_bytes = XPW * 4 + E::NG * NCF * 4;
+    static_assert(chunk_bytes == xtile_chunk_bytes(E::ENC), "host/device activation tile layouts differ");
+};
+
+// f32 [n] of activation row b at element k (f32 or bf16 source), 16-byte loads.
+template <bool XBF16, int N>
+__device__ __forceinline__ void load_xrun(const void* __restrict__ x, size_t off, float (&v)[N]) {
     typedef float f32x4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     if constexpr (XBF16) {
-        const uint16_t* xp = static_cast<const uint16_t*>(x) + (size_t)r * ldx + k;
-        const u32x2 v = *gptr<u32x2>(xp);
-        return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
-                           __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
+        static_assert(N % 8 == 0, "bf16 runs are read 8 at a time");
+        const uint16_t* xp = static_cast<const uint16_t*>(x) + off;
+#pragma unroll
+        for (int i = 0; i < N; i += 8) {
+            const u32x4 q = *gptr<u32x4>(xp + i);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v[i + 2 * j] = __uint_as_float(q[j] << 16);
+                v[i + 2 * j + 1] = __uint_as_float(q[j] & 0xFFFF0000u);
+            }
+        }
     } else {
-        const float* xp = static_cast<const float*>(x) + (size_t)r * ldx + k;
-        const f32x4 v = *gptr<f32x4>(xp);
-        return make_float4(v.x, v.y, v.z, v.w);
+        static_assert(N % 4 == 0, "f32 runs are read 4 at a time");
+        const float* xp = static_cast<const float*>(x) + off;
+#pragma unroll
+        for (int i = 0; i < N; i += 4) {
+            const f32x4 q = *gptr<f32x4>(xp + i);
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[i + j] = q[j];
+        }
     }
 }
 
-// LDS activation layout: f32 [B][KP] with 4 padding floats after every chunk
-// of CW, KP = K + 4·K/CW.
-template <int CW>
-__device__ __forceinline__ uint32_t lds_index(uint32_t k) { return k + 4u * (k / (uint32_t)CW); }
-
-template <int CW>
-__host__ __device__ constexpr size_t lds_bytes(uint32_t B, uint32_t K) {
-    return (size_t)B * (K + 4u * (K / (uint32_t)CW)) * 4u;
-}
-
-template <int CW>
-struct XLds {
-    const float* xs;
-    uint32_t KP;
-    __device__ __forceinline__ float4 load(uint32_t b, uint32_t k) const {
-        return *reinterpret_cast<const float4*>(xs + (size_t)b * KP + lds_index<CW>(k));
-    }
-};
-
-// Activations read through L1/L2, for B·K too large for LDS.
-template <bool XBF16>
-struct XGlobal {
-    const void* x;
-    uint32_t ldx, batch;
-    __device__ __forceinline__ float4 load(uint32_t b, uint32_t k) const {
-        // rows beyond `batch` re-read row 0 (in bounds); their sums are never stored
-        return load_x4<XBF16>(x, ldx, b < batch ? b : 0u, k);
-    }
-};
-
-// Copies x[0..batch) (f32 or bf16, row stride ldx) into LDS as f32 in the
-// padded layout, rows >= batch zero-filled.  All threads of the workgroup take
-// part; ends with a barrier.
-template <int CW, int B, bool XBF16>
-__device__ __forceinline__ void stage_x(float* xs, const void* __restrict__ x, uint32_t K, uint32_t ldx,
+// Stages activation rows [0, batch) (rows up to B zero-filled) into the tile.
+// One thread per (row, chunk): it reads the chunk's activations, picks each
+// scale group's power of two s = 2^(e-14) from the group's largest magnitude
+// (frexp exponent e, so |x|/s < 2^14), writes the f16 pairs in decode order
+// (pairs meeting x16 codes divided by 16), and the group constants
+// -C = -Σ coef·v and s·Σx over the stored values v.  All threads of the
+// workgroup take part; ends with a barrier.
+template <class E, int B, bool XBF16>
+__device__ __forceinline__ void stage_x(uint8_t* lds, const void* __restrict__ x, uint32_t K, uint32_t ldx,
                                         uint32_t batch) {
-    const uint32_t kq = K / 4u, KP = K + 4u * (K / (uint32_t)CW);
-    for (uint32_t i = threadIdx.x; i < (uint32_t)B * kq; i += blockDim.x) {
-        const uint32_t b = i / kq, k = (i - b * kq) * 4u;
-        const float4 v = b < batch ? load_x4<XBF16>(x, ldx, b, k) : make_float4(0.f, 0.f, 0.f, 0.f);
-        *reinterpret_cast<float4*>(xs + (size_t)b * KP + lds_index<CW>(k)) = v;
+    using XT = XTile<E>;
+    const uint32_t nch = K / (uint32_t)E::CW;
+    uint32_t* xp = reinterpret_cast<uint32_t*>(lds);
+    float* xc = reinterpret_cast<float*>(lds + (size_t)B * nch * XT::XPW * 4u);
+    for (uint32_t item = threadIdx.x; item < (uint32_t)B * nch; item += blockDim.x) {
+        const uint32_t b = item / nch, u = item - b * nch;
+        float v[E::NRUN][E::RUNLEN];
+        if (b < batch) {
+#pragma unroll
+            for (int r = 0; r < E::NRUN; r++)
+                load_xrun<XBF16>(x, (size_t)b * ldx + E::xbase(u) + (uint32_t)(r * E::RUNSTRIDE), v[r]);
+        } else {
+#pragma unroll
+            for (int r = 0; r < E::NRUN; r++)
+#pragma unroll
+                for (int i = 0; i < E::RUNLEN; i++) v[r][i] = 0.0f;
+        }
+        auto val = [&](int t, int h, int e) -> float {
+            const int o = E::xoff(t, h, e);
+            const int r = E::NRUN > 1 ? o / (E::NRUN > 1 ? E::RUNSTRIDE : 1) : 0;
+            return v[r][o - r * E::RUNSTRIDE];
+        };
+        int ex[E::NG];
+#pragma unroll
+        for (int g = 0; g < E::NG; g++) {
+            float m = 0.0f;
+#pragma unroll
+            for (int t = 0; t < E::NT; t++)
+#pragma unroll
+                for (int h = 0; h < E::PPT; h++)
+                    if (E::grp(t, h) == g) m = fmaxf(m, fmaxf(fabsf(val(t, h, 0)), fabsf(val(t, h, 1))));
+            int e = 0;
+            (void)frexpf(m, &e);
+            ex[g] = e < -110 ? -110 : e;  // keeps s = 2^(e-14) a normal f32
+        }
+        float C[E::NG], S[E::NG];
+#pragma unroll
+        for (int g = 0; g < E::NG; g++) C[g] = S[g] = 0.0f;
+        uint32_t pr[E::NT * E::PPT];
+#pragma unroll
+        for (int t = 0; t < E::NT; t++)
+#pragma unroll
+            for (int h = 0; h < E::PPT; h++) {
+                const int g = E::grp(t, h);
+                const bool dv = E::dv(t, h);
+                _Float16 lo = (_Float16)ldexpf(val(t, h, 0), 14 - ex[g]);
+                _Float16 hi = (_Float16)ldexpf(val(t, h, 1), 14 - ex[g]);
+                if (dv) {
+                    lo = lo * (_Float16)0.0625f;
+                    hi = hi * (_Float16)0.0625f;
+                }
+                pr[t * E::PPT + h] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+                                     ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+                const float fl = (float)lo, fh = (float)hi;
+                C[g] = fmaf(E::coef(dv), fh, fmaf(E::coef(dv), fl, C[g]));
+                S[g] = fmaf(dv ? 16.0f : 1.0f, fh, fmaf(dv ? 16.0f : 1.0f, fl, S[g]));
+            }
+        uint4* dst = reinterpret_cast<uint4*>(xp + (size_t)item * XT::XPW);
+#pragma unroll
+        for (int i = 0; i < E::NT * E::PPT; i += 4) dst[i / 4] = make_uint4(pr[i], pr[i + 1], pr[i + 2], pr[i + 3]);
+#pragma unroll
+        for (int g = 0; g < E::NG; g++) {
+            const float s = ldexpf(1.0f, ex[g] - 14);
+            float* c = xc + ((size_t)item * E::NG + g) * XT::NCF;
+            if constexpr (XT::NCF == 4) {
+                *reinterpret_cast<float4*>(c) = make_float4(-C[g], s, s * S[g], 0.0f);
+            } else {
+                *reinterpret_cast<float2*>(c) = make_float2(-C[g], s);
+            }
+        }
     }
     __syncthreads();
 }
 
-// Dot of one chunk position for R rows: acc[i][b] += Σ_groups d·Σc·x + m·Σx.
-template <class E, int R, int B, class XS>
-__device__ __forceinline__ void chunk_dot(const typename E::Chunk (&c)[R], const XS& xsrc, uint32_t k0,
-                                          float (&acc)[R][B]) {
+// ---------------------------------------------------------------- chunk dot product
+// Reads the (-C, s, s·Σx) constants of group g of chunk u for activation row b.
+template <class E>
+__device__ __forceinline__ void load_consts(const float* xc, uint32_t idx, float& negc, float& s, float& sm) {
+    using XT = XTile<E>;
+    const float* cp = xc + (size_t)idx * XT::NCF;
+    if constexpr (XT::NCF == 4) {
+        const float4 q = *reinterpret_cast<const float4*>(cp);
+        negc = q.x;
+        s = q.y;
+        sm = q.z;
+    } else {
+        const float2 q = *reinterpret_cast<const float2*>(cp);
+        negc = q.x;
+        s = q.y;
+        sm = 0.0f;
+    }
+}
+
+// The PPT activation pairs of code dword t of chunk u, activation row b.
+template <class E>
+__device__ __forceinline__ void load_xpairs(const uint32_t* xp, uint32_t idx, int t, uint32_t (&xv)[E::PPT]) {
+    const uint32_t* xq = xp + (size_t)idx * XTile<E>::XPW + t * E::PPT;
+    if constexpr (E::PPT % 4 == 0) {
 #pragma unroll
-    for (int g = 0; g < E::NG; g++) {
-        float part[R][B];
-        float sx[B];
-#pragma unroll
-        for (int b = 0; b < B; b++) {
-            sx[b] = 0.0f;
-#pragma unroll
-            for (int i = 0; i < R; i++) part[i][b] = 0.0f;
+        for (int h = 0; h < E::PPT; h += 4) {
+            const uint4 q = *reinterpret_cast<const uint4*>(xq + h);
+            xv[h] = q.x; xv[h + 1] = q.y; xv[h + 2] = q.z; xv[h + 3] = q.w;
         }
+    } else {
+        static_assert(E::PPT == 2, "pairs per code dword: 2, 4 or 8");
+        const uint2 q = *reinterpret_cast<const uint2*>(xq);
+        xv[0] = q.x; xv[1] = q.y;
+    }
+}
+
+// y[i][b] += Σ over chunk u of row i: w·x, for R rows and B activation rows.
+// Up to 4 activation rows: code dword outer (each dword's pairs are decoded
+// and used at once, R·B·NG accumulators).  More rows: activation row outer
+// (the chunk's pairs are decoded once and kept, R·NG accumulators), which
+// keeps the registers of the wide batches in check.
+template <class E, int R, int B>
+__device__ __forceinline__ void chunk_dot(const typename E::Chunk (&c)[R], const uint8_t* lds, uint32_t nch,
+                                          uint32_t u, float (&y)[R][B]) {
+    using XT = XTile<E>;
+    const uint32_t* xp = reinterpret_cast<const uint32_t*>(lds);
+    const float* xc = reinterpret_cast<const float*>(lds + (size_t)B * nch * XT::XPW * 4u);
+    if constexpr (B <= 4) {
+        float acc[R][B][E::NG];
+        float sc[B][E::NG], sm[B][E::NG];
 #pragma unroll
-        for (int q = 0; q < E::QUADS; q++) {
-            const uint32_t k = k0 + (uint32_t)E::kofs(g, q);
-            float cf[R][4];
+        for (int b = 0; b < B; b++)
 #pragma unroll
-            for (int i = 0; i < R; i++) {
-                const uint32_t v = E::codes(c[i], g, q);
-                cf[i][0] = ubyte_f32<0>(v);
-                cf[i][1] = ubyte_f32<1>(v);
-                cf[i][2] = ubyte_f32<2>(v);
-                cf[i][3] = ubyte_f32<3>(v);
+            for (int g = 0; g < E::NG; g++) {
+                float negc;
+                load_consts<E>(xc, ((uint32_t)b * nch + u) * E::NG + g, negc, sc[b][g], sm[b][g]);
+#pragma unroll
+                for (int i = 0; i < R; i++) acc[i][b][g] = negc;
             }
+#pragma unroll
+        for (int t = 0; t < E::NT; t++) {
+            uint32_t pr[R][E::PPT];
+#pragma unroll
+            for (int i = 0; i < R; i++) E::pairs(c[i], t, pr[i]);
 #pragma unroll
             for (int b = 0; b < B; b++) {
-                const float4 xv = xsrc.load((uint32_t)b, k);
-                sx[b] += (xv.x + xv.y) + (xv.z + xv.w);
+                uint32_t xv[E::PPT];
+                load_xpairs<E>(xp, (uint32_t)b * nch + u, t, xv);
 #pragma unroll
-                for (int i = 0; i < R; i++) {
-                    float a = part[i][b];
-                    a = fmaf(cf[i][0], xv.x, a);
-                    a = fmaf(cf[i][1], xv.y, a);
-                    a = fmaf(cf[i][2], xv.z, a);
-                    a = fmaf(cf[i][3], xv.w, a);
-                    part[i][b] = a;
-                }
+                for (int i = 0; i < R; i++)
+#pragma unroll
+                    for (int h = 0; h < E::PPT; h++) {
+                        float& a = acc[i][b][E::grp(t, h)];
+                        a = dot2(pr[i][h], xv[h], a);
+                    }
             }
         }
 #pragma unroll
-        for (int i = 0; i < R; i++) {
-            const float d = E::scale(c[i], g), m = E::offset(c[i], g);
+        for (int i = 0; i < R; i++)
 #pragma unroll
-            for (int b = 0; b < B; b++) acc[i][b] = fmaf(m, sx[b], fmaf(d, part[i][b], acc[i][b]));
+            for (int b = 0; b < B; b++)
+#pragma unroll
+                for (int g = 0; g < E::NG; g++) {
+                    // weight scale first: d·acc·s is the group's true contribution,
+                    // while acc·s alone (Σ q·x) can overflow f32 for huge activations
+                    y[i][b] = fmaf(E::gscale(c[i], g) * acc[i][b][g], sc[b][g], y[i][b]);
+                    if constexpr (E::AFFINE) y[i][b] = fmaf(E::goffset(c[i], g), sm[b][g], y[i][b]);
+                }
+    } else {
+        uint32_t pr[R][E::NT][E::PPT];
+#pragma unroll
+        for (int i = 0; i < R; i++)
+#pragma unroll
+            for (int t = 0; t < E::NT; t++) E::pairs(c[i], t, pr[i][t]);
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            float acc[R][E::NG], sc[E::NG], sm[E::NG];
+#pragma unroll
+            for (int g = 0; g < E::NG; g++) {
+                float negc;
+                load_consts<E>(xc, ((uint32_t)b * nch + u) * E::NG + g, negc, sc[g], sm[g]);
+#pragma unroll
+                for (int i = 0; i < R; i++) acc[i][g] = negc;
+            }
+#pragma unroll
+            for (int t = 0; t < E::NT; t++) {
+                uint32_t xv[E::PPT];
+                load_xpairs<E>(xp, (uint32_t)b * nch + u, t, xv);
+#pragma unroll
+                for (int i = 0; i < R; i++)
+#pragma unroll
+                    for (int h = 0; h < E::PPT; h++) {
+                        float& a = acc[i][E::grp(t, h)];
+                        a = dot2(pr[i][t][h], xv[h], a);
+                    }
+            }
+#pragma unroll
+            for (int i = 0; i < R; i++)
+#pragma unroll
+                for (int g = 0; g < E::NG; g++) {
+                    y[i][b] = fmaf(E::gscale(c[i], g) * acc[i][g], sc[g], y[i][b]);
+                    if constexpr (E::AFFINE) y[i][b] = fmaf(E::goffset(c[i], g), sm[g], y[i][b]);
+                }
+            // one activation row's LDS reads in flight at a time: hoisting all of
+            // them (which the optimiser does before scheduling) would spill
+            asm volatile("" ::: "memory");
         }
     }
 }
 
-// Row block -> problem, its row count and first row (all wave-uniform: kept
-// in scalar registers so selecting the problem's pointers never indexes the
-// kernel-argument arrays dynamically).
+// Row block -> its problem's pointers, row count and first row (all wave-
+// uniform, computed once per task in scalar registers).
 struct RowBlock {
-    uint32_t pi, n, base;
+    const uint8_t* w;
+    const uint8_t* sc;
+    const uint8_t* bi;
+    void* y;
+    uint32_t n, base;
 };
 
 __device__ __forceinline__ RowBlock row_block(const GemvParams& p, uint32_t rb, uint32_t rows_per_rb) {
@@ -169,23 +329,47 @@ __device__ __forceinline__ RowBlock row_block(const GemvParams& p, uint32_t rb, 
 #pragma unroll
     for (int i = 1; i < kMaxProblems; i++) pi += (i < (int)p.nprob && rb >= p.rb_begin[i]) ? 1u : 0u;
     RowBlock r;
-    r.pi = pi;
+    r.w = pick(pi, p.w);
+    r.sc = pick(pi, p.sc);
+    r.bi = pick(pi, p.bi);
+    r.y = pick(pi, p.y);
     r.n = pick(pi, p.n);
     r.base = (rb - pick(pi, p.rb_begin)) * rows_per_rb;
     return r;
 }
 
+// Sum over each aligned group of L lanes (L a power of two <= 64, wave-
+// uniform), left in every lane of the group: DPP butterflies within rows of
+// 16 lanes (quad permutes, then the half-row and row mirrors, which pair every
+// lane with one of the other half once the halves are uniform), then the
+// gfx950 row-pair and half-wave swaps.  All VALU, no LDS round trips.
+__device__ __forceinline__ float group_sum(float v, uint32_t L) {
+#define DMX_DPP(x, ctrl) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xF, 0xF, false))
+    if (L >= 2) v += DMX_DPP(v, 0xB1);   // quad_perm [1,0,3,2]
+    if (L >= 4) v += DMX_DPP(v, 0x4E);   // quad_perm [2,3,0,1]
+    if (L >= 8) v += DMX_DPP(v, 0x141);  // row_half_mirror
+    if (L >= 16) v += DMX_DPP(v, 0x140); // row_mirror
+#undef DMX_DPP
+    if (L >= 32) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    if (L >= 64) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    return v;
+}
+
 template <int R, int B>
 __device__ __forceinline__ void reduce_store(float (&acc)[R][B], const RowBlock& rb, uint32_t row0, uint32_t j,
                                              uint32_t L, const GemvParams& p) {
-    for (uint32_t off = L >> 1; off > 0; off >>= 1) {
 #pragma unroll
-        for (int i = 0; i < R; i++)
+    for (int i = 0; i < R; i++)
 #pragma unroll
-            for (int b = 0; b < B; b++) acc[i][b] += __shfl_xor(acc[i][b], (int)off, 64);
-    }
+        for (int b = 0; b < B; b++) acc[i][b] = group_sum(acc[i][b], L);
     if (j == 0) {
-        void* y = pick(rb.pi, p.y);
+        void* y = rb.y;
 #pragma unroll
         for (int i = 0; i < R; i++) {
             const uint32_t row = row0 + (uint32_t)i;
@@ -194,8 +378,10 @@ __device__ __forceinline__ void reduce_store(float (&acc)[R][B], const RowBlock&
             for (int b = 0; b < B; b++) {
                 if ((uint32_t)b < p.batch) {
                     const size_t idx = (size_t)b * rb.n + row;
-                    if (p.y_bf16) static_cast<uint16_t*>(y)[idx] = f32_to_bf16_bits(acc[i][b]);
-                    else static_cast<float*>(y)[idx] = acc[i][b];
+                    // global (not flat) stores: a flat store makes the wait counters
+                    // drain every load in flight
+                    if (p.y_bf16) gptr_mut<uint16_t>(y)[idx] = f32_to_bf16_bits(acc[i][b]);
+                    else gptr_mut<float>(y)[idx] = acc[i][b];
                 }
             }
         }
@@ -204,21 +390,23 @@ __device__ __forceinline__ void reduce_store(float (&acc)[R][B], const RowBlock&
 
 // The persistent task pipeline shared by all encodings.  load(rb, row, u)
 // returns the raw bytes of chunk u of a row (rows past the end are clamped to
-// the last row by the caller: in bounds, their sums are never stored).  Every
-// load is unconditional — at the end of the sequence the current task is
-// loaded again — so the compiler's wait counters can keep all of a lane's
-// loads in flight across one task of compute.
-template <class E, int R, int B, class XS, class LOAD>
-__device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const XS& xsrc, LOAD&& load) {
+// the last row: in bounds, their sums are never stored).  Every load is
+// unconditional — a wave without row blocks loads the last row block's first
+// task, and at the end of the sequence the current task is loaded again — so
+// the compiler's wait counters can keep a lane's loads in flight across one
+// task of compute.  stage() stages the activations (with a barrier); it runs
+// after the first task's loads are issued, in every wave.
+template <class E, int R, int B, class LOAD, class STAGE>
+__device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const uint8_t* lds, LOAD&& load, STAGE&& stage) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
     const uint32_t W = gridDim.x * (blockDim.x >> 6);
     const uint32_t L = 1u << p.lanes_log2;
     const uint32_t j = lane & (L - 1u), g = lane >> p.lanes_log2;
     const uint32_t rows_per_rb = (64u >> p.lanes_log2) * (uint32_t)R;
-    const uint32_t cpl = (p.K / (uint32_t)E::CW) >> p.lanes_log2;  // chunks per lane per row block
-    if (wid >= p.total_rb) return;
-    const uint32_t T = (p.total_rb - wid + W - 1) / W * cpl;  // tasks of this wave
+    const uint32_t nch = p.K / (uint32_t)E::CW;
+    const uint32_t cpl = (nch + L - 1u) >> p.lanes_log2;  // chunks per lane per row block
+    const uint32_t T = wid < p.total_rb ? (p.total_rb - wid + W - 1) / W * cpl : 0u;  // tasks of this wave
 
     float acc[R][B];
 #pragma unroll
@@ -231,29 +419,35 @@ __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const XS& xsr
 #pragma unroll
         for (int i = 0; i < R; i++) {
             const uint32_t row = row0 + (uint32_t)i < rb.n ? row0 + (uint32_t)i : rb.n - 1u;
-            dst[i] = load(rb, row, j + c * L);
+            const uint32_t u = j + c * L;
+            dst[i] = load(rb, row, u < nch ? u : nch - 1u);
         }
     };
 
     // Two register buffers in ping-pong (no copies between them, so waiting
     // for one buffer never waits for the loads in flight into the other).
     typename E::Raw ba[R], bb[R];
-    uint32_t nrb = wid, nc = 0;  // the task loaded next
+    uint32_t nrb = wid < p.total_rb ? wid : p.total_rb - 1u, nc = 0;  // the task loaded next
     RowBlock nblk = row_block(p, nrb, rows_per_rb);
+    // wave-uniform and branch-free; past the end the last task is loaded again
     auto advance = [&](uint32_t t) {
-        if (t + 1 < T) {  // wave-uniform; past the end the last task is loaded again
-            if (++nc == cpl) {
-                nc = 0;
-                nrb += W;
-                nblk = row_block(p, nrb, rows_per_rb);
-            }
-        }
+        const bool more = t + 1 < T;
+        const bool wrap = more && nc + 1 == cpl;
+        nc = wrap ? 0u : (more ? nc + 1 : nc);
+        nrb = wrap ? nrb + W : nrb;
+        nblk = row_block(p, nrb, rows_per_rb);
     };
     auto compute = [&](const typename E::Raw (&buf)[R], const RowBlock& blk, uint32_t c) {
+        const uint32_t u0 = j + c * L;
+        const bool past = u0 >= nch;  // a lane past the last chunk: adds zero
+        const uint32_t u = past ? nch - 1u : u0;
         typename E::Chunk ch[R];
 #pragma unroll
-        for (int i = 0; i < R; i++) ch[i] = E::unpack(buf[i]);
-        chunk_dot<E, R, B>(ch, xsrc, (j + c * L) * (uint32_t)E::CW, acc);
+        for (int i = 0; i < R; i++) {
+            ch[i] = E::unpack(buf[i], u);
+            E::zero_if(ch[i], past);
+        }
+        chunk_dot<E, R, B>(ch, lds, nch, u, acc);
         if (c + 1 == cpl) {
             reduce_store<R, B>(acc, blk, blk.base + g * (uint32_t)R, j, L, p);
 #pragma unroll
@@ -263,6 +457,8 @@ __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const XS& xsr
         }
     };
     load_task(ba, nblk, nc);
+    stage();
+    if (T == 0) return;
     uint32_t t = 0;
     for (; t + 2 <= T; t += 2) {
         // task t is in ba: load task t+1 into bb, compute ba
@@ -270,138 +466,114 @@ __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const XS& xsr
         uint32_t c = nc;
         advance(t);
         load_task(bb, nblk, nc);
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch above the compute
         compute(ba, blk, c);
         // task t+1 is in bb: load task t+2 into ba, compute bb
         blk = nblk;
         c = nc;
         advance(t + 1);
         load_task(ba, nblk, nc);
+        __builtin_amdgcn_sched_barrier(0);
         compute(bb, blk, c);
     }
     if (t < T) compute(ba, nblk, nc);  // odd task count: the last task is in ba
 }
 
 // ---------------------------------------------------------------- GGUF
-// XL: activations staged in LDS (dynamic shared memory, lds_bytes<CW>(B, K)).
-template <class E, int B, int R, bool XBF16, bool XL>
-__global__ __launch_bounds__(256) void gguf_gemv_kernel(const GemvParams p) {
-    extern __shared__ float xs_dyn[];
-    if constexpr (XL) stage_x<E::CW, B, XBF16>(xs_dyn, p.x, p.K, p.ldx, p.batch);
-    const size_t rowbytes = (size_t)(p.K / (uint32_t)E::CW) * E::BB;
-    auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) {
-        return E::load_raw(pick(rb.pi, p.w) + (size_t)row * rowbytes, u);
-    };
-    if constexpr (XL) gemv_pipeline<E, R, B>(p, XLds<E::CW>{xs_dyn, p.K + 4u * (p.K / (uint32_t)E::CW)}, load);
-    else gemv_pipeline<E, R, B>(p, XGlobal<XBF16>{p.x, p.ldx, p.batch}, load);
+// Weight offsets are 32-bit (the C ABI limits one weight to 4 GiB), so loads
+// use a uniform 64-bit base plus a per-lane 32-bit offset.
+template <class E, int B, int R, bool XBF16>
+__global__ __launch_bounds__(kGemvThreads) void gguf_gemv_kernel(const GemvParams p) {
+    extern __shared__ __align__(16) uint8_t xlds[];
+    const uint32_t rowbytes = (p.K / (uint32_t)E::QK) * (uint32_t)E::BB;
+    auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) { return E::load(rb.w, row * rowbytes, u); };
+    gemv_pipeline<E, R, B>(p, xlds, load, [&] { stage_x<E, B, XBF16>(xlds, p.x, p.K, p.ldx, p.batch); });
 }
 
 // ---------------------------------------------------------------- MLX affine U4
-template <int B, int R, bool XBF16, bool XL>
-__global__ __launch_bounds__(256) void mlx_u4_gemv_kernel(const GemvParams p) {
+template <int B, int R, bool XBF16>
+__global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_kernel(const GemvParams p) {
     using E = EncMlxU4;
-    extern __shared__ float xs_dyn[];
-    if constexpr (XL) stage_x<E::CW, B, XBF16>(xs_dyn, p.x, p.K, p.ldx, p.batch);
+    extern __shared__ __align__(16) uint8_t xlds[];
     const uint32_t ngroups = p.K / p.group;
     const uint32_t chunks_per_group = p.group / 32u;
     const bool f32s = p.sdtype == DT_F32;
     auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) {
         E::Raw r;
-        const uint32_t* wbase = reinterpret_cast<const uint32_t*>(pick(rb.pi, p.w));
-        load_dwords<4>(wbase + (size_t)row * (p.K / 8u) + (size_t)u * 4u, r.w);
-        const size_t gi = (size_t)row * ngroups + u / chunks_per_group;
-        const uint8_t* scb = pick(rb.pi, p.sc);
-        const uint8_t* bib = pick(rb.pi, p.bi);
+        const uint8_t* wb = rb.w;
+        load_dwords<4>(reinterpret_cast<const uint32_t*>(wb + (row * (p.K / 2u) + u * 16u)), r.w);
+        const uint32_t gi = row * ngroups + u / chunks_per_group;
+        const uint8_t* scb = rb.sc;
+        const uint8_t* bib = rb.bi;
         if (f32s) {
-            r.s = gptr<uint32_t>(scb)[gi];
-            r.b = gptr<uint32_t>(bib)[gi];
+            r.s = *gptr<uint32_t>(scb + gi * 4u);
+            r.b = *gptr<uint32_t>(bib + gi * 4u);
         } else {
-            r.s = gptr<uint16_t>(scb)[gi];
-            r.b = gptr<uint16_t>(bib)[gi];
+            r.s = *gptr<uint16_t>(scb + gi * 2u);
+            r.b = *gptr<uint16_t>(bib + gi * 2u);
         }
         r.kind = p.sdtype;
         return r;
     };
-    if constexpr (XL) gemv_pipeline<E, R, B>(p, XLds<E::CW>{xs_dyn, p.K + 4u * (p.K / (uint32_t)E::CW)}, load);
-    else gemv_pipeline<E, R, B>(p, XGlobal<XBF16>{p.x, p.ldx, p.batch}, load);
+    gemv_pipeline<E, R, B>(p, xlds, load, [&] { stage_x<E, B, XBF16>(xlds, p.x, p.K, p.ldx, p.batch); });
 }
 
 // Rows per lane group for a register batch B: more rows amortise each
-// activation load and Σx, fewer keep the accumulators in registers.
+// activation read from LDS and the per-task overhead, fewer keep the
+// accumulators in registers.  (With one activation row the host may pick a
+// single row per group instead, for matrices too small to fill the GPU.)
 template <class E, int B>
 constexpr int rows_per_group() {
-    if constexpr (E::CW == 256) return 1;  // 53-dword super-blocks: keep occupancy >= 3 waves/SIMD
-    else return B <= 2 ? 4 : (B <= 8 ? 2 : 1);
+    if constexpr (E::ENC == ENC_Q6_K) return B <= 2 ? 2 : 1;
+    else return B <= 4 ? 4 : 2;
 }
-
-// Largest activation bytes staged in LDS per workgroup.
-constexpr size_t kMaxLdsX = 64u * 1024u;
 
 // Resident workgroups per CU for (kernel, dynamic LDS) on the current device
 // and its CU count, cached after the first query (host side, thread-safe).
-hipError_t cached_occupancy(const void* kernel, size_t lds, int* per_cu, int* cus);
+// Also raises the kernel's dynamic-LDS limit when lds needs it.
+hipError_t cached_occupancy(const void* kernel, size_t lds, int threads, int* per_cu, int* cus);
 
-// Launch of one kernel instantiation with a persistent grid: as many
-// workgroups as fit on the device at once (capped by the row-block count).
+// Launch of one kernel instantiation with a persistent grid: as many waves as
+// fit on the device at once (capped by the row-block count).  Fewer waves
+// would even out the row blocks per wave, but cost more in memory-level
+// parallelism than the tail they save.
 template <class KERNEL>
 hipError_t launch_persistent(KERNEL kernel, const GemvParams& p, size_t lds, hipStream_t st) {
     int cus = 0, per_cu = 0;
-    hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, &per_cu, &cus);
+    hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, kGemvThreads, &per_cu, &cus);
     if (e != hipSuccess) return e;
-    const uint64_t want = ((uint64_t)p.total_rb + 3) / 4;  // 4 waves per workgroup
-    const uint64_t cap = (uint64_t)(per_cu < 1 ? 1 : per_cu) * (uint64_t)cus;
+    if (per_cu < 1) return hipErrorInvalidConfiguration;
+    constexpr uint64_t waves = kGemvThreads / 64;
+    const uint64_t want = ((uint64_t)p.total_rb + waves - 1) / waves;
+    const uint64_t cap = (uint64_t)per_cu * (uint64_t)cus;
     const uint32_t blocks = (uint32_t)(want < cap ? want : cap);
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), lds, st, p);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), lds, st, p);
     return hipGetLastError();
 }
 
 // Instantiates and launches the GEMV kernel of encoding E for a power-of-two
-// register batch B <= BMAX.  GGUF decode takes f32 activations, the
-// reference's precision contract for quantized linears
-// (crates/dyninfer-compiler/src/lib.rs:289-306); bf16 activations reach GGUF
-// weights only through the Q4_0 MFMA path.
-template <class E, int BMAX>
-hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, bool xbf16, hipStream_t st) {
+// register batch B (the host has checked that its activation tile fits LDS).
+// GGUF decode takes f32 activations, the reference's precision contract for
+// quantized linears (crates/dyninfer-compiler/src/lib.rs:289-306); bf16
+// activations reach GGUF weights only through the Q4_0 MFMA path.
+template <class E>
+hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st) {
     if (xbf16) return hipErrorInvalidValue;
-    const size_t lds = lds_bytes<E::CW>(B, p.K);
-    const bool xl = lds <= kMaxLdsX;
-#define DMX_CASE(b)                                                                                    \
-    case b:                                                                                            \
-        if constexpr (b <= BMAX) {                                                                     \
-            constexpr int r = rows_per_group<E, b>();                                                  \
-            return xl ? launch_persistent(gguf_gemv_kernel<E, b, r, false, true>, p, lds, st)          \
-                      : launch_persistent(gguf_gemv_kernel<E, b, r, false, false>, p, 0, st);          \
-        } else {                                                                                       \
-            return hipErrorInvalidValue;                                                               \
-        }
+    const size_t lds = (size_t)xtile_bytes(E::ENC, B, p.K);
+    if (B == 1 && R == 1) return launch_persistent(gguf_gemv_kernel<E, 1, 1, false>, p, lds, st);
+#define DMX_CASE(b)                                                                                  \
+    case b:                                                                                          \
+        if constexpr (b <= max_register_batch(E::ENC))                                               \
+            return R == (uint32_t)rows_per_group<E, b>()                                             \
+                       ? launch_persistent(gguf_gemv_kernel<E, b, rows_per_group<E, b>(), false>, p, lds, st) \
+                       : hipErrorInvalidValue;                                                       \
+        else                                                                                         \
+            return hipErrorInvalidValue;
     switch (B) {
         DMX_CASE(1)
         DMX_CASE(2)
         DMX_CASE(4)
         DMX_CASE(8)
-        DMX_CASE(16)
-    default: return hipErrorInvalidValue;
-    }
-#undef DMX_CASE
-}
-
-inline hipError_t launch_mlx_gemv(const GemvParams& p, uint32_t B, bool xbf16, hipStream_t st) {
-    const size_t lds = lds_bytes<EncMlxU4::CW>(B, p.K);
-    const bool xl = lds <= kMaxLdsX;
-#define DMX_CASE(b)                                                                                     \
-    case b: {                                                                                           \
-        constexpr int r = rows_per_group<EncMlxU4, b>();                                                \
-        if (xbf16)                                                                                      \
-            return xl ? launch_persistent(mlx_u4_gemv_kernel<b, r, true, true>, p, lds, st)             \
-                      : launch_persistent(mlx_u4_gemv_kernel<b, r, true, false>, p, 0, st);             \
-        return xl ? launch_persistent(mlx_u4_gemv_kernel<b, r, false, true>, p, lds, st)                \
-                  : launch_persistent(mlx_u4_gemv_kernel<b, r, false, false>, p, 0, st);                \
-    }
-    switch (B) {
-        DMX_CASE(1)
-        DMX_CASE(2)
-        DMX_CASE(4)
-        DMX_CASE(8)
-        DMX_CASE(16)
     default: return hipErrorInvalidValue;
     }
 #undef DMX_CASE

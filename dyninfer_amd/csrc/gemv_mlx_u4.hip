@@ -2,7 +2,24 @@
 #include "gemv_kernels.hpp"
 
 namespace dmx {
-hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, bool xbf16, hipStream_t st) {
-    return launch_mlx_gemv(p, B, xbf16, st);
+hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st) {
+    using E = EncMlxU4;
+    const size_t lds = (size_t)xtile_bytes(E::ENC, B, p.K);
+    if (B == 1 && R == 1)
+        return xbf16 ? launch_persistent(mlx_u4_gemv_kernel<1, 1, true>, p, lds, st)
+                     : launch_persistent(mlx_u4_gemv_kernel<1, 1, false>, p, lds, st);
+    if (R != (uint32_t)(B <= 4 ? 4 : 2)) return hipErrorInvalidValue;
+#define DMX_CASE(b)                                                                                        \
+    case b:                                                                                                \
+        return xbf16 ? launch_persistent(mlx_u4_gemv_kernel<b, rows_per_group<E, b>(), true>, p, lds, st)  \
+                     : launch_persistent(mlx_u4_gemv_kernel<b, rows_per_group<E, b>(), false>, p, lds, st);
+    switch (B) {
+        DMX_CASE(1)
+        DMX_CASE(2)
+        DMX_CASE(4)
+        DMX_CASE(8)
+    default: return hipErrorInvalidValue;
+    }
+#undef DMX_CASE
 }
 }  // namespace dmx

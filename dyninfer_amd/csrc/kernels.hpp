@@ -33,6 +33,24 @@ struct GemvParams {
     uint32_t sdtype;      // MLX scale/bias dtype
 };
 
+// Bytes of the GEMV activation tile in LDS per (activation row, chunk): the
+// chunk's f16 pairs plus 16 bytes of bank padding, then its constants
+// (gemv_kernels.hpp XTile).  Chunks: 32 weights, 64 for Q6_K.
+__host__ __device__ constexpr uint32_t xtile_chunk_weights(uint32_t enc) { return enc == ENC_Q6_K ? 64u : 32u; }
+__host__ __device__ constexpr uint32_t xtile_chunk_bytes(uint32_t enc) {
+    return enc == ENC_Q6_K ? 36u * 4u + 4u * 2u * 4u                      // 32 pair dwords + pad, 4 groups x (-C, s)
+         : (enc == ENC_Q8_0 || enc == ENC_Q4_0) ? 20u * 4u + 2u * 4u      // 16 + pad, (-C, s)
+         : 20u * 4u + 4u * 4u;                                            // Q4_1, MLX: (-C, s, s.Σx, 0)
+}
+__host__ __device__ constexpr uint64_t xtile_bytes(uint32_t enc, uint32_t B, uint32_t K) {
+    return (uint64_t)B * (K / xtile_chunk_weights(enc)) * xtile_chunk_bytes(enc);
+}
+// Widest activation batch one GEMV launch holds in registers (wider batches
+// run as several launches): 8 rows, 4 for Q6_K's larger chunks.
+__host__ __device__ constexpr uint32_t max_register_batch(uint32_t enc) { return enc == ENC_Q6_K ? 4u : 8u; }
+// LDS of one gfx950 workgroup.
+constexpr uint32_t kLdsBytes = 160u * 1024u;
+
 struct GemvProblem {
     const uint8_t* w;
     const uint8_t* sc;
@@ -45,6 +63,9 @@ struct GemvProblem {
 hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x,
                        bool x_bf16, uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype,
                        hipStream_t stream);
+
+// Whether one activation row of K elements fits the GEMV's LDS tile.
+bool gemv_k_supported(uint32_t enc, uint32_t K);
 
 // Bit-exact dequantisation to f32 [N, K].
 hipError_t dequant_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, const uint8_t* bi, uint32_t N,
