@@ -188,31 +188,30 @@ class StepRunner:
             torch.cuda.synchronize()
         return t0.elapsed_time(t1) / steps
 
-    def per_launch_times(self, reps: int = 5):
-        """Eager pass with HIP events around every launch on the launch stream:
-        {label: (launches, total ms, weight bytes)} averaged over reps."""
+    def label_times(self, reps: int = 20):
+        """Per launch label: one graph holding all of the step's launches of that
+        label in step order (distinct weights, so every launch streams from
+        HBM), replayed between HIP events on the launch stream.
+        {label: (launches per step, us per launch, weight bytes per launch)}.
+        The time per launch includes the GPU's own gap between two dependent
+        dispatches (about 1.5 us on MI355X), not host launch overhead."""
         torch = self.torch
-        stats = {}
-        st = self.stream
-        with torch.cuda.stream(st):
-            for _ in range(2):
-                self.step(st)
+        groups = {}
+        for i, (label, _, _, _) in enumerate(self.set.launches):
+            groups.setdefault(label, []).append(i)
+        out = {}
+        for label, idx in groups.items():
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(self.stream):
+                with torch.cuda.graph(g, stream=self.stream):
+                    for i in idx:
+                        self.launch(i, self.stream)
             torch.cuda.synchronize()
-            evs = []
-            for _ in range(reps):
-                for i in range(len(self.set.launches)):
-                    a = torch.cuda.Event(enable_timing=True)
-                    b = torch.cuda.Event(enable_timing=True)
-                    a.record(st)
-                    self.launch(i, st)
-                    b.record(st)
-                    evs.append((i, a, b))
-            torch.cuda.synchronize()
-        for i, a, b in evs:
-            label, ws, _, _ = self.set.launches[i]
-            n, ms, nb = stats.get(label, (0, 0.0, 0))
-            stats[label] = (n + 1, ms + a.elapsed_time(b), nb + sum(w.nbytes for w in ws))
-        return stats
+            ms = self.time_graph(g, reps, 3)
+            nbytes = sum(w.nbytes for i in idx for w in self.set.launches[i][1]) / len(idx)
+            out[label] = (len(idx), ms * 1e3 / len(idx), nbytes)
+            del g
+        return out
 
 
 # ------------------------------------------------------------------ other configurations
@@ -318,6 +317,9 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="skip configs 0/2/3/4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for rocprofv3 --pmc: one 64 MiB device copy (the counters' calibration), then one "
+                         "eager config-1 step; prints the step's launch labels in dispatch order")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -334,28 +336,39 @@ def main() -> int:
     log("building config 1 weights (Qwen3-0.6B mixed GGUF) ...")
     s1 = gguf_step_06b(torch, d, gen)
     r1 = StepRunner(torch, d, ctx, s1, args.batch, torch.float32, torch.float32)
+    if args.pmc_probe:
+        src = torch.ones(16 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)  # reads and writes 64 MiB: the counters' bytes-per-unit calibration
+        torch.cuda.synchronize()
+        with torch.cuda.stream(r1.stream):
+            r1.step(r1.stream)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration_bytes": src.numel() * 4,
+                          "launches": [[lab, sum(w.nbytes for w in ws)] for lab, ws, _, _ in s1.launches]}))
+        return 0
     g1 = r1.capture()
     ms = r1.time_graph(g1, args.steps, args.warmup)
     value = s1.weight_bytes / ms / 1e6
     log(f"config 1 batch {args.batch}: {ms * 1e3:.1f} us/step, {value:.1f} GB/s")
 
-    # dominant kernel of the step: largest total time in an event-instrumented eager pass
-    stats = r1.per_launch_times()
-    dom_label, (dn, dms, dbytes) = max(stats.items(), key=lambda kv: kv[1][1])
-    dom_us = dms / dn * 1e3
-    dom_bytes = dbytes / dn
+    # dominant kernel of the step: the launch label with the largest total time
+    stats = r1.label_times()
+    dom_label, (dn, dom_us, dom_bytes) = max(stats.items(), key=lambda kv: kv[1][0] * kv[1][1])
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": dom_label, "bytes_per_launch": int(dom_bytes), "avg_launch_us": round(dom_us, 2)}
+                "kernel": dom_label, "bytes_per_launch": int(dom_bytes), "avg_launch_us": round(dom_us, 3),
+                "timing": "HIP events around a graph of the label's launches; includes the dispatch gap"}
     tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     if os.path.exists(tfile):
         with open(tfile) as fh:
             roofline["traffic"] = json.load(fh).get(dom_label)
-    breakdown = {k: {"launches_per_step": v[0] // 5, "us_per_launch": round(v[1] / v[0] * 1e3, 2),
-                     "GBps": round(v[2] / v[0] / (v[1] / v[0]) / 1e6, 1)} for k, v in sorted(stats.items())}
+    breakdown = {k: {"launches_per_step": n, "us_per_launch": round(us, 3),
+                     "GBps": round(nb / (us * 1e-6) / 1e9, 1)} for k, (n, us, nb) in sorted(stats.items())}
 
-    extra = {"config1_breakdown_eager": breakdown}
+    extra = {"config1_breakdown": breakdown}
     if not args.no_extra:
         r4b = StepRunner(torch, d, ctx, s1, 4, torch.float32, torch.float32)
         ms4 = r4b.time_graph(r4b.capture(), max(5, args.steps // 2), 3)
