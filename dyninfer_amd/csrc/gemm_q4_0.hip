@@ -5,22 +5,28 @@
 // paged, parameter.rs:107-121, dense_decoder.rs:53-56).
 //
 // Data path (no repack: W is read as GGUF blocks straight from HBM):
-//   * a workgroup (4 waves) computes a BM x BN tile of Y (64x128 or 128x64,
-//     picked per shape so the grid covers the 256 CUs); each wave a 2x4 or
-//     4x2 set of v_mfma_f32_16x16x32_f16 blocks;
-//   * K advances 64 per stage (two Q4_0 blocks = two MFMA depths); the
-//     global loads of stage s+3 are issued when stage s is staged, so three
-//     stages (192 K) of loads are in flight behind the MFMA work;
-//   * W: each thread loads Q4_0 blocks (realigned from 2-byte alignment) and
-//     dequantises them to f16 in registers: the nibble becomes 1024+q by
-//     OR-ing it under the f16 exponent of 1024 (exact), a packed f16 add gives
-//     q-8 (exact) and a packed f16 multiply gives RNE_f16((q-8)·d) — one
-//     rounding of the exact weight, relative error <= 2^-11;
+//   * a workgroup computes a BM x BN tile of Y with WM x WN MMA waves, each
+//     owning a (BM/WM) x (BN/WN) sub-tile of v_mfma_f32_16x16x32_f16 blocks
+//     (one MFMA depth is exactly one Q4_0 block of 32);
+//   * the producer side (global loads, decode, LDS stores) either runs in the
+//     MMA waves themselves, or in PW waves of its own so that one wave's decode
+//     (VALU) overlaps another wave's MFMAs on each SIMD instead of all waves of
+//     the tile doing the same phase at once;
+//   * inside every 32-wide block, K is stored in LDS in the nibble decode order
+//     (for each 8 consecutive k from k0: k0, k0+2, k0+1, k0+3, k0+4, k0+6,
+//     k0+5, k0+7), for X and W alike, so the products pair up exactly as in
+//     natural order, an X load of 8 bf16 fills one such group, and one
+//     v_and_or_b32 decodes two weights (bytes j and j+2 of a dword): a low nibble under the f16
+//     exponent of 1024 is 1024+q, a high nibble (bits 4..7) under the exponent
+//     of 64 is 64+q, both exact; a packed f16 add gives q-8 (exact) and a packed
+//     f16 multiply RNE_f16((q-8)·d), a single rounding of the exact weight
+//     (relative error <= 2^-11);
 //   * X: bf16 is narrowed to f16 with v_cvt_pkrtz (exact for |x| in f16's
-//     normal range: bf16 carries 8 significant bits, f16 11);
-//   * both operands are staged through double-buffered LDS (rows padded by 16
-//     bytes so the 16 rows a fragment read touches fall in distinct banks);
-//     one barrier per stage;
+//     normal range: bf16 carries 8 significant bits, f16 11), placed in the
+//     same permuted order;
+//   * K advances BK per stage; the global loads run PF stages ahead in a
+//     register ring; LDS is double buffered (rows padded by 16 bytes), one
+//     barrier per stage;
 //   * tiles are ordered so that the tiles sharing W columns run on the same
 //     XCD (workgroup i goes to XCD i % 8), reading each W block into one L2.
 // Accuracy: |y - y_exact| <= 2^-11·Σ|w||x| + f32 accumulation error, inside
@@ -36,210 +42,340 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int BK = 64;          // K per LDS stage (two Q4_0 blocks)
-constexpr int PITCH = BK + 8;   // f16 elements per LDS row (+16 bytes)
-constexpr int PREFETCH = 3;     // stages of global loads in flight
-
-// 8 bf16 (one uint4) -> 8 f16 (4 dwords).
-__device__ __forceinline__ uint4 bf16x8_to_f16(const uint4& a) {
-    const uint32_t v[4] = {a.x, a.y, a.z, a.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float lo = __uint_as_float(v[i] << 16);
-        const float hi = __uint_as_float(v[i] & 0xFFFF0000u);
-        // round-toward-zero is exact here: a bf16 value in f16's normal range
-        // needs 8 significant bits.
-        o[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
-    }
-    return make_uint4(o[0], o[1], o[2], o[3]);
+// (a & m) | b as one v_and_or_b32 (mask in a scalar register: a VOP3 op takes
+// no literal operand on gfx9).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t b) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(b));
+    return r;
 }
 
-// Dequantise 16 weights of a Q4_0 block held in `e` (realigned block dwords):
-// half 0 = low nibbles (k 0..15), half 1 = high nibbles (k 16..31), as 8
-// dwords of consecutive f16 pairs.
-__device__ __forceinline__ void q4_0_half_to_f16(const uint32_t (&e)[5], uint32_t half, uint32_t (&o)[8]) {
-    const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)(e[0] & 0xFFFFu));
-    const h2 d2 = {dh, dh};
-    const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-    const uint32_t shift = half * 4u;
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const uint32_t q = __builtin_amdgcn_alignbyte(e[t + 1], e[t], 2) >> shift;
-        const uint32_t p0 = (__builtin_amdgcn_perm(q, q, 0x0C010C00u) & 0x000F000Fu) | 0x64006400u;
-        const uint32_t p1 = (__builtin_amdgcn_perm(q, q, 0x0C030C02u) & 0x000F000Fu) | 0x64006400u;
-        o[2 * t] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, p0) + off) * d2);
-        o[2 * t + 1] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, p1) + off) * d2);
-    }
+// Two f32 bit patterns (bf16 values) to packed f16, rounding toward zero
+// (exact for bf16 values in f16's normal range).
+__device__ __forceinline__ uint32_t pk_f16(uint32_t lo, uint32_t hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(lo), __uint_as_float(hi)));
 }
 
-}  // namespace
+// Global loads and decode of one tile's X and W stages, spread over NT threads.
+//
+// LDS order inside each 32-wide block: group g (g = 0..3) holds k = 8g..8g+7 as
+// the pairs (k0, k0+2), (k0+1, k0+3), (k0+4, k0+6), (k0+5, k0+7), k0 = 8g.
+//   X unit: one row's 8 consecutive bf16 (one 16-byte load) -> one group.
+//   W unit: half h of one row's block (the whole 18-byte block is loaded, two
+//           loads): quant dwords 2h, 2h+1 hold the low nibbles of k = 8h..8h+7
+//           (group h) and the high nibbles of k = 16+8h.. (group h+2); byte j of
+//           a dword pairs with byte j+2 under one v_and_or_b32.
+template <int BM, int BN, int NB, int PF, int NT>
+struct Producer {
+    static constexpr int PITCH = 32 * NB + 8;
+    static constexpr int XU = BM * 4 * NB / NT;  // X units per thread per stage
+    static constexpr int WU = BN * 2 * NB / NT;  // W units per thread per stage
+    static_assert(XU >= 1 && WU >= 1 && XU * NT == BM * 4 * NB && WU * NT == BN * 2 * NB, "unit split");
 
-template <int BM, int BN>
-__global__ __launch_bounds__(256) void gemm_q4_0_kernel(const uint8_t* __restrict__ W, const uint16_t* __restrict__ X,
-                                                        void* __restrict__ Y, uint32_t M, uint32_t N, uint32_t K,
-                                                        uint32_t y_bf16) {
-    static_assert(BM * BN == 8192, "tile must hold 8192 outputs (4 waves x 2048)");
-    // 2x2 waves: 64x128 -> waves of 32x64; 128x64 -> waves of 64x32
-    constexpr int TM = BM / 2 / 16;           // 16x16 tiles per wave along M
-    constexpr int TN = BN / 2 / 16;           // 16x16 tiles per wave along N
-    constexpr int XV = BM * BK * 2 / 16 / 256;  // uint4 of X per thread per stage
-    constexpr int XT = BK * 2 / 16;              // uint4 per X row (8)
-    // W blocks per stage: BN rows x 2 = 2*BN; each thread dequantises 32/WS weights of one block
-    constexpr int WS = 256 / (2 * BN);           // threads per block: 1 (BN=128) or 2 (BN=64)
-    constexpr int WW = 32 / WS;                  // weights per thread
+    uint32_t xraw[PF][XU][4];  // 8 bf16 at k = 8g..8g+7
+    uint32_t wraw[PF][WU][5];  // the block's dwords from the aligned dword holding its first byte
+    const uint16_t* xrow[XU];
+    const uint32_t* wrow[WU];
+    uint32_t wsh[WU], wback[WU];
+    uint32_t ptid, nkb;
 
-    __shared__ __attribute__((aligned(16))) _Float16 sX[2][BM * PITCH];
-    __shared__ __attribute__((aligned(16))) _Float16 sW[2][BN * PITCH];
+    __device__ __forceinline__ void xunit(int i, uint32_t& r, uint32_t& g8) const {
+        const uint32_t u = ptid + (uint32_t)i * NT;
+        r = u / (4u * NB);
+        g8 = u % (4u * NB);
+    }
+    __device__ __forceinline__ void wunit(int i, uint32_t& r, uint32_t& b, uint32_t& h) const {
+        const uint32_t u = ptid + (uint32_t)i * NT;
+        r = u / (2u * NB);
+        b = (u / 2u) % (uint32_t)NB;
+        h = u & 1u;
+    }
 
-    const uint32_t tid = threadIdx.x;
-    const uint32_t lane = tid & 63u, wave = tid >> 6;
-    const uint32_t wm = wave >> 1, wn = wave & 1u;
+    // Per-unit addresses, computed once: rows past M/N re-read the last row (in
+    // bounds; their outputs are never stored).  A stage advances X by 32·NB
+    // elements and W by NB 18-byte blocks (a multiple of 4 bytes, so a block's
+    // byte shift within its dword never changes).
+    __device__ __forceinline__ void init(const uint8_t* W, const uint16_t* X, uint32_t tid, uint32_t m0, uint32_t n0,
+                                         uint32_t M, uint32_t N, uint32_t K) {
+        ptid = tid;
+        nkb = K / 32u;
+        const size_t rowbytes = (size_t)nkb * 18u;
+#pragma unroll
+        for (int i = 0; i < XU; i++) {
+            uint32_t r, g8;
+            xunit(i, r, g8);
+            const uint32_t m = m0 + r < M ? m0 + r : M - 1u;
+            xrow[i] = X + (size_t)m * K + 8u * g8;
+        }
+#pragma unroll
+        for (int i = 0; i < WU; i++) {
+            uint32_t r, b, h;
+            wunit(i, r, b, h);
+            const uint32_t n = n0 + r < N ? n0 + r : N - 1u;
+            const uintptr_t a0 = (uintptr_t)W + (size_t)n * rowbytes;  // block 0 of stage 0
+            const uintptr_t a = a0 + b * 18u;
+            wsh[i] = (uint32_t)(a & 3u);
+            wrow[i] = reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
+            // dwords back from this block's aligned base to the stage's first block's
+            wback[i] = (uint32_t)(((a & ~(uintptr_t)3) - (a0 & ~(uintptr_t)3)) / 4u);
+        }
+    }
 
-    // XCD-aware tile order: tiles sharing the same N range go to the same XCD.
-    const uint32_t mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN, T = mt * nt;
-    uint32_t tau = blockIdx.x;
-    if (T % 8u == 0) tau = (blockIdx.x % 8u) * (T / 8u) + blockIdx.x / 8u;
-    const uint32_t n0 = (tau / mt) * BN, m0 = (tau % mt) * BM;
-    const uint32_t nkb = K / 32u;                         // Q4_0 blocks per row
-    const uint32_t nst = (K + (uint32_t)BK - 1) / (uint32_t)BK;  // stages; the last holds one block when K % 64 == 32
+    // Blocks of the last stage past K are missing when K % (32·NB) != 0: such
+    // a unit re-reads its stage's first block (which exists, in bounds) and
+    // lstore zeroes its d (X: the product with a zero weight is zero).
+    __device__ __forceinline__ bool blk_ok(uint32_t st, uint32_t b) const { return (uint32_t)NB * st + b < nkb; }
 
-    // X loader: thread covers XV consecutive uint4 of row xr starting at column xc (uint4 units)
-    const uint32_t xr = tid * XV / XT, xc = (tid * XV) % XT;
-    const bool xvalid = m0 + xr < M;
-    const uint16_t* xsrc = X + (size_t)(xvalid ? m0 + xr : 0u) * K + xc * 8u;
-    // W loader: thread covers weights [wh*WW, +WW) of block wb (0/1) of row wr
-    const uint32_t wr = tid / (2u * WS), wb = (tid / WS) & 1u, wh = tid % WS;
-    const bool wvalid = n0 + wr < N;
-    const uint8_t* wsrc = W + (size_t)(wvalid ? n0 + wr : 0u) * nkb * 18u + wb * 18u;
+    // Loads are unconditional so the wait counters can keep all PF stages in flight.
+    __device__ __forceinline__ void gload(int slot, uint32_t st) {
+#pragma unroll
+        for (int i = 0; i < XU; i++) {
+            uint32_t r, g8;
+            xunit(i, r, g8);
+            const uint32_t b = g8 / 4u;
+            const uint16_t* xp = xrow[i] + (size_t)st * (32 * NB) - (blk_ok(st, b) ? 0u : 32u * b);
+            const u32x4_a4 v = *gptr<u32x4_a4>(xp);
+            xraw[slot][i][0] = v.x;
+            xraw[slot][i][1] = v.y;
+            xraw[slot][i][2] = v.z;
+            xraw[slot][i][3] = v.w;
+        }
+#pragma unroll
+        for (int i = 0; i < WU; i++) {
+            uint32_t r, b, h;
+            wunit(i, r, b, h);
+            const uint32_t* al = wrow[i] + (size_t)st * (NB * 18 / 4) - (blk_ok(st, b) ? 0u : wback[i]);
+            load_dwords<5>(al, wraw[slot][i]);  // every dword overlaps the block's 18 bytes
+        }
+    }
 
+    // Decode/convert ring slot `slot` (stage st) into the LDS tiles dx, dw.
+    __device__ __forceinline__ void lstore(int slot, _Float16* dx, _Float16* dw, uint32_t st) {
+#pragma unroll
+        for (int i = 0; i < XU; i++) {
+            uint32_t r, g8;
+            xunit(i, r, g8);
+            const uint32_t* q = xraw[slot][i];  // bf16 pairs (k0, k0+1), (k0+2, k0+3), ...
+            const uint32_t p0 = pk_f16(q[0] << 16, q[1] << 16);                  // k0, k0+2
+            const uint32_t p1 = pk_f16(q[0] & 0xFFFF0000u, q[1] & 0xFFFF0000u);  // k0+1, k0+3
+            const uint32_t p2 = pk_f16(q[2] << 16, q[3] << 16);                  // k0+4, k0+6
+            const uint32_t p3 = pk_f16(q[2] & 0xFFFF0000u, q[3] & 0xFFFF0000u);  // k0+5, k0+7
+            *reinterpret_cast<uint4*>(&dx[r * PITCH + 8u * g8]) = make_uint4(p0, p1, p2, p3);
+        }
+        const h2 off_lo = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+        const h2 off_hi = {(_Float16)-72.0f, (_Float16)-72.0f};
+        const uint32_t mag_lo = 0x64006400u, mag_hi = 0x54005400u;
+#pragma unroll
+        for (int i = 0; i < WU; i++) {
+            uint32_t r, b, h;
+            wunit(i, r, b, h);
+            const uint32_t* q = wraw[slot][i];
+            const uint32_t sh = wsh[i];
+            const uint32_t dbits = blk_ok(st, b) ? (q[0] >> (8u * sh)) : 0u;  // a missing block weighs zero
+            const h2 d2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dbits, dbits, 0x01000100u));
+            const uint32_t sel = 0x05040302u + 0x01010101u * sh;  // quant dword t = block bytes 2+4t..5+4t
+            // quant dwords 2h and 2h+1 (raw dwords 2h..2h+2)
+            const uint32_t qa = __builtin_amdgcn_perm(h ? q[3] : q[1], h ? q[2] : q[0], sel);
+            const uint32_t qb = __builtin_amdgcn_perm(h ? q[4] : q[2], h ? q[3] : q[1], sel);
+            auto wv = [&](uint32_t c, h2 off) {
+                return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, c) + off) * d2);
+            };
+            const uint32_t a8 = qa >> 8, b8 = qb >> 8;
+            // low nibbles: group h (k0 = 8h): (k0, k0+2) (k0+1, k0+3) from qa, (k0+4, k0+6) (k0+5, k0+7) from qb
+            *reinterpret_cast<uint4*>(&dw[r * PITCH + b * 32u + 8u * h]) =
+                make_uint4(wv(and_or(qa, 0x000F000Fu, mag_lo), off_lo), wv(and_or(a8, 0x000F000Fu, mag_lo), off_lo),
+                           wv(and_or(qb, 0x000F000Fu, mag_lo), off_lo), wv(and_or(b8, 0x000F000Fu, mag_lo), off_lo));
+            // high nibbles: group h + 2 (k0 = 16 + 8h)
+            *reinterpret_cast<uint4*>(&dw[r * PITCH + b * 32u + 8u * h + 16u]) =
+                make_uint4(wv(and_or(qa, 0x00F000F0u, mag_hi), off_hi), wv(and_or(a8, 0x00F000F0u, mag_hi), off_hi),
+                           wv(and_or(qb, 0x00F000F0u, mag_hi), off_hi), wv(and_or(b8, 0x00F000F0u, mag_hi), off_hi));
+        }
+    }
+};
+
+// One MMA wave's sub-tile: TM x TN blocks of 16x16, fragments read from LDS.
+template <int BM, int BN, int WM, int WN, int NB>
+struct Consumer {
+    static constexpr int PITCH = 32 * NB + 8;
+    static constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+    static_assert(TM * 16 * WM == BM && TN * 16 * WN == BN, "tile must split into 16x16 blocks per wave");
     f4 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t fr, fk, arow, bcol, lane;
 
-    uint4 xreg[PREFETCH][XV];
-    uint32_t wreg[PREFETCH][5], wsh[PREFETCH];
-    // A thread's X columns and W block of a stage lie in one 32-wide Q4_0 block
-    // (column block 2*st + xc/4, W block 2*st + wb); past K they are zero and
-    // never loaded.
-    const uint32_t xblk = xc / 4u;
+    __device__ __forceinline__ void init(uint32_t lane_, uint32_t cw) {
+        lane = lane_;
+        fr = lane & 15u;
+        fk = (lane >> 4) * 8u;
+        arow = (cw / WN) * (BM / WM);
+        bcol = (cw % WN) * (BN / WN);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+    }
 
-    // Loads are unconditional (a block past K re-reads block 0 of the row, in
-    // bounds, and is zeroed in lstore) so that the wait counters can keep all
-    // PREFETCH stages in flight.
-    auto gload = [&](int slot, uint32_t st) {
-        const uint32_t xs = 2u * st + xblk < nkb ? st : 0u;
-        const uint4* xp = reinterpret_cast<const uint4*>(xsrc + (size_t)xs * BK);
+    __device__ __forceinline__ void mma(const _Float16* ax, const _Float16* bw) {
 #pragma unroll
-        for (int v = 0; v < XV; v++) {
-            const u32x4_a4 t = *gptr<u32x4_a4>(xp + v);
-            xreg[slot][v] = make_uint4(t.x, t.y, t.z, t.w);
-        }
-        const uint32_t wbk = 2u * st + wb < nkb ? 2u * st : 0u;
-        const uintptr_t a = (uintptr_t)(wsrc + (size_t)wbk * 18u);
-        wsh[slot] = (uint32_t)(a & 3u);
-        load_dwords<5>(reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3), wreg[slot]);
-    };
-    // Out-of-range rows/blocks are zeroed with bit masks rather than selects:
-    // a select lets the compiler branch around the conversion, and the branch
-    // makes its wait-counter analysis fall back to waiting for every load.
-    auto lstore = [&](int slot, int buf, uint32_t st) {
-        const uint32_t xm = (xvalid && 2u * st + xblk < nkb) ? 0xFFFFFFFFu : 0u;
-        const uint32_t wm_ = (wvalid && 2u * st + wb < nkb) ? 0xFFFFFFFFu : 0u;
-        uint4* dx = reinterpret_cast<uint4*>(&sX[buf][xr * PITCH + xc * 8u]);
-#pragma unroll
-        for (int v = 0; v < XV; v++) {
-            const uint4 c = bf16x8_to_f16(xreg[slot][v]);
-            dx[v] = make_uint4(c.x & xm, c.y & xm, c.z & xm, c.w & xm);
-        }
-        uint32_t e[5];
-        realign<5>(wreg[slot], wsh[slot], e);
-        uint4* dw = reinterpret_cast<uint4*>(&sW[buf][wr * PITCH + wb * 32u + wh * WW]);
-#pragma unroll
-        for (int h = 0; h < WW / 16; h++) {
-            uint32_t o[8];
-            q4_0_half_to_f16(e, wh * (WW / 16) + h, o);
-            dw[2 * h] = make_uint4(o[0] & wm_, o[1] & wm_, o[2] & wm_, o[3] & wm_);
-            dw[2 * h + 1] = make_uint4(o[4] & wm_, o[5] & wm_, o[6] & wm_, o[7] & wm_);
-        }
-    };
-
-#pragma unroll
-    for (int s = 0; s < PREFETCH; s++) gload(s, (uint32_t)s < nst ? (uint32_t)s : 0u);
-
-    const uint32_t fr = lane & 15u, fk = (lane >> 4) * 8u;
-    const uint32_t arow = wm * (BM / 2), bcol = wn * (BN / 2);
-    auto stage = [&](int slot, uint32_t st) {
-        const int buf = (int)(st & 1u);
-        lstore(slot, buf, st);
-        gload(slot, st + PREFETCH < nst ? st + PREFETCH : st);
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < BK / 32; kk++) {
+        for (int kk = 0; kk < NB; kk++) {
             h8 a[TM], b[TN];
 #pragma unroll
             for (int i = 0; i < TM; i++)
-                a[i] = *reinterpret_cast<const h8*>(&sX[buf][(arow + i * 16u + fr) * PITCH + kk * 32u + fk]);
+                a[i] = *reinterpret_cast<const h8*>(&ax[(arow + i * 16u + fr) * PITCH + kk * 32u + fk]);
 #pragma unroll
             for (int j = 0; j < TN; j++)
-                b[j] = *reinterpret_cast<const h8*>(&sW[buf][(bcol + j * 16u + fr) * PITCH + kk * 32u + fk]);
+                b[j] = *reinterpret_cast<const h8*>(&bw[(bcol + j * 16u + fr) * PITCH + kk * 32u + fk]);
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
-    };
-    uint32_t s0 = 0;
-    for (; s0 + PREFETCH <= nst; s0 += PREFETCH) {
-#pragma unroll
-        for (int slot = 0; slot < PREFETCH; slot++) stage(slot, s0 + (uint32_t)slot);
     }
-#pragma unroll
-    for (int slot = 0; slot < PREFETCH; slot++)
-        if (s0 + (uint32_t)slot < nst) stage(slot, s0 + (uint32_t)slot);
 
     // D layout of 16x16 MFMA: lane holds rows 4*(lane/16) + r, column lane%16.
-    const uint32_t col_l = lane & 15u, row_l = (lane >> 4) * 4u;
+    __device__ __forceinline__ void store(void* Y, uint32_t m0, uint32_t n0, uint32_t M, uint32_t N, uint32_t y_bf16) {
+        const uint32_t col_l = lane & 15u, row_l = (lane >> 4) * 4u;
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+        for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const uint32_t col = n0 + bcol + j * 16u + col_l;
+            for (int j = 0; j < TN; j++) {
+                const uint32_t col = n0 + bcol + j * 16u + col_l;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint32_t row = m0 + arow + i * 16u + row_l + r;
-                if (row < M && col < N) {
-                    const size_t idx = (size_t)row * N + col;
-                    if (y_bf16) static_cast<uint16_t*>(Y)[idx] = f32_to_bf16_bits(acc[i][j][r]);
-                    else static_cast<float*>(Y)[idx] = acc[i][j][r];
+                for (int r = 0; r < 4; r++) {
+                    const uint32_t row = m0 + arow + i * 16u + row_l + r;
+                    if (row < M && col < N) {
+                        const size_t idx = (size_t)row * N + col;
+                        if (y_bf16) gptr_mut<uint16_t>(Y)[idx] = f32_to_bf16_bits(acc[i][j][r]);
+                        else gptr_mut<float>(Y)[idx] = acc[i][j][r];
+                    }
                 }
             }
+    }
+};
+
+}  // namespace
+
+// WM x WN MMA waves plus PW producer waves (PW = 0: the MMA waves also
+// produce).  BK: K per LDS stage (a multiple of 32); PF: stages of global
+// loads in flight.
+template <int BM, int BN, int WM, int WN, int PW, int BK, int PF>
+__global__ __launch_bounds__((WM * WN + PW) * 64) void gemm_q4_0_kernel(const uint8_t* __restrict__ W,
+                                                                         const uint16_t* __restrict__ X,
+                                                                         void* __restrict__ Y, uint32_t M, uint32_t N,
+                                                                         uint32_t K, uint32_t y_bf16) {
+    constexpr int NB = BK / 32;
+    constexpr int PITCH = BK + 8;
+    constexpr int NT = (PW > 0 ? PW : WM * WN) * 64;  // producer threads
+    using P = Producer<BM, BN, NB, PF, NT>;
+    using C = Consumer<BM, BN, WM, WN, NB>;
+
+    extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
+    _Float16* sX = smem;                   // [2][BM * PITCH]
+    _Float16* sW = smem + 2 * BM * PITCH;  // [2][BN * PITCH]
+    auto bufx = [&](uint32_t s) { return sX + (s & 1u) * BM * PITCH; };
+    auto bufw = [&](uint32_t s) { return sW + (s & 1u) * BN * PITCH; };
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // XCD-aware tile order: tiles sharing the same N range go to the same XCD.
+    const uint32_t mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN, T = mt * nt;
+    uint32_t tau = blockIdx.x;
+    if (T % 8u == 0) tau = (blockIdx.x % 8u) * (T / 8u) + blockIdx.x / 8u;
+    const uint32_t n0 = (tau / mt) * BN, m0 = (tau % mt) * BM;
+    const uint32_t nst = (K + (uint32_t)BK - 1) / (uint32_t)BK;  // stages; the last may hold fewer than NB blocks
+
+    // Producer schedule.  Prologue: PF stages of loads in flight (stages past
+    // the end re-load the last one), stage 0 in LDS buffer 0, barrier.  Stage s:
+    // refill ring slot s % PF with stage s + PF, decode stage s + 1 into the
+    // other buffer (the MMA of stage s reads buffer s & 1), barrier.
+    auto produce = [&](P& p, auto&& during) {
+#pragma unroll
+        for (int s = 0; s < PF; s++) p.gload(s, (uint32_t)s < nst ? (uint32_t)s : nst - 1u);
+        p.lstore(0, bufx(0), bufw(0), 0);
+        __syncthreads();
+        auto iter = [&](int slot, uint32_t s) {
+            p.gload(slot, s + PF < nst ? s + PF : nst - 1u);
+            during(s);
+            if (s + 1 < nst) p.lstore((slot + 1) % PF, bufx(s + 1), bufw(s + 1), s + 1);
+            __syncthreads();
+        };
+        uint32_t s0 = 0;
+        for (; s0 + PF <= nst; s0 += PF) {
+#pragma unroll
+            for (int slot = 0; slot < PF; slot++) iter(slot, s0 + (uint32_t)slot);
         }
+#pragma unroll
+        for (int slot = 0; slot < PF; slot++)
+            if (s0 + (uint32_t)slot < nst) iter(slot, s0 + (uint32_t)slot);
+    };
+
+    if constexpr (PW == 0) {
+        P p;
+        C c;
+        p.init(W, X, tid, m0, n0, M, N, K);
+        c.init(lane, wave);
+        produce(p, [&](uint32_t s) { c.mma(bufx(s), bufw(s)); });
+        c.store(Y, m0, n0, M, N, y_bf16);
+    } else {
+        // wave-uniform split: every wave passes the same 1 + nst barriers
+        if (wave < (uint32_t)PW) {
+            P p;
+            p.init(W, X, tid, m0, n0, M, N, K);
+            produce(p, [](uint32_t) {});
+        } else {
+            C c;
+            c.init(lane, wave - PW);
+            __syncthreads();
+            for (uint32_t s = 0; s < nst; s++) {
+                c.mma(bufx(s), bufw(s));
+                __syncthreads();
+            }
+            c.store(Y, m0, n0, M, N, y_bf16);
+        }
+    }
 }
 
 bool gemm_q4_0_supported(uint32_t N, uint32_t K, uint32_t M) {
     return N > 0 && M > 0 && K > 0 && K % 32u == 0;
 }
 
+namespace {
+
+template <int BM, int BN, int WM, int WN, int PW, int BK, int PF>
+hipError_t launch_tile(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* x, uint32_t M, void* y, uint32_t yb,
+                       hipStream_t st) {
+    auto kernel = gemm_q4_0_kernel<BM, BN, WM, WN, PW, BK, PF>;
+    constexpr int kThreads = (WM * WN + PW) * 64;
+    constexpr size_t lds = (size_t)2 * (BM + BN) * (BK + 8) * sizeof(_Float16);
+    if constexpr (lds > 64u * 1024u) {
+        static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (attr != hipSuccess) return attr;
+    }
+    const uint32_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    hipLaunchKernelGGL(kernel, dim3(tiles), dim3(kThreads), lds, st, w, x, y, M, N, K, yb);
+    return hipGetLastError();
+}
+
+}  // namespace
+
 hipError_t gemm_q4_0_launch(const uint8_t* w, uint32_t N, uint32_t K, const void* x, uint32_t M, void* y,
                             bool y_bf16, hipStream_t stream) {
     if (!gemm_q4_0_supported(N, K, M)) return hipErrorInvalidValue;
-    // 64x128 tiles unless that leaves fewer workgroups than 128x64 would need
-    // waves for (tall X, narrow W); both hold 8192 outputs.
-    const uint32_t t_a = ((M + 63) / 64) * ((N + 127) / 128);
-    const uint32_t t_b = ((M + 127) / 128) * ((N + 63) / 64);
     const auto* xp = static_cast<const uint16_t*>(x);
-    if (M >= 2 * N || t_b < t_a) {
-        hipLaunchKernelGGL((gemm_q4_0_kernel<128, 64>), dim3(t_b), dim3(256), 0, stream, w, xp, y, M, N, K,
-                           y_bf16 ? 1u : 0u);
-    } else {
-        hipLaunchKernelGGL((gemm_q4_0_kernel<64, 128>), dim3(t_a), dim3(256), 0, stream, w, xp, y, M, N, K,
-                           y_bf16 ? 1u : 0u);
-    }
-    return hipGetLastError();
+    const uint32_t yb = y_bf16 ? 1u : 0u;
+    auto tiles = [&](uint32_t bm, uint32_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    // The largest tile (most reuse of each decoded weight and converted
+    // activation) that still gives most CUs a workgroup; smaller problems take
+    // the smallest tile.
+    constexpr uint32_t kCus = 256;
+    if (tiles(128, 128) >= kCus) return launch_tile<128, 128, 2, 4, 0, 64, 4>(w, N, K, xp, M, y, yb, stream);
+    if (M <= N && tiles(64, 128) >= kCus * 3 / 4)
+        return launch_tile<64, 128, 2, 4, 0, 64, 4>(w, N, K, xp, M, y, yb, stream);
+    if (tiles(128, 64) >= kCus * 3 / 4) return launch_tile<128, 64, 4, 2, 0, 128, 2>(w, N, K, xp, M, y, yb, stream);
+    return launch_tile<64, 64, 2, 4, 0, 128, 2>(w, N, K, xp, M, y, yb, stream);
 }
 
 }  // namespace dmx
