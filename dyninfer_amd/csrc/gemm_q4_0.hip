@@ -6,8 +6,9 @@
 //
 // Data path (no repack: W is read as GGUF blocks straight from HBM):
 //   * a workgroup computes a BM x BN tile of Y with WM x WN MMA waves, each
-//     owning a (BM/WM) x (BN/WN) sub-tile of v_mfma_f32_16x16x32_f16 blocks
-//     (one MFMA depth is exactly one Q4_0 block of 32);
+//     owning a (BM/WM) x (BN/WN) sub-tile of v_mfma_f32_32x32x16_f16 blocks
+//     (two MFMA depths per Q4_0 block of 32; the 32x32 shape reads half the
+//     LDS bytes per flop of the 16x16 one);
 //   * the producer side (global loads, decode, LDS stores) either runs in the
 //     MMA waves themselves, or in PW waves of its own so that one wave's decode
 //     (VALU) overlaps another wave's MFMAs on each SIMD instead of all waves of
@@ -38,7 +39,7 @@ namespace dmx {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 namespace {
 
@@ -71,6 +72,8 @@ struct Producer {
     static constexpr int XU = BM * 4 * NB / NT;  // X units per thread per stage
     static constexpr int WU = BN * 2 * NB / NT;  // W units per thread per stage
     static_assert(XU >= 1 && WU >= 1 && XU * NT == BM * 4 * NB && WU * NT == BN * 2 * NB, "unit split");
+    static constexpr int kLoads = XU + 2 * WU;        // global load instructions per stage
+    static constexpr int kValu = 8 * XU + 32 * WU;    // decode VALU instructions per stage (approximate)
 
     uint32_t xraw[PF][XU][4];  // 8 bf16 at k = 8g..8g+7
     uint32_t wraw[PF][WU][5];  // the block's dwords from the aligned dword holding its first byte
@@ -155,11 +158,15 @@ struct Producer {
         for (int i = 0; i < XU; i++) {
             uint32_t r, g8;
             xunit(i, r, g8);
-            const uint32_t* q = xraw[slot][i];  // bf16 pairs (k0, k0+1), (k0+2, k0+3), ...
-            const uint32_t p0 = pk_f16(q[0] << 16, q[1] << 16);                  // k0, k0+2
-            const uint32_t p1 = pk_f16(q[0] & 0xFFFF0000u, q[1] & 0xFFFF0000u);  // k0+1, k0+3
-            const uint32_t p2 = pk_f16(q[2] << 16, q[3] << 16);                  // k0+4, k0+6
-            const uint32_t p3 = pk_f16(q[2] & 0xFFFF0000u, q[3] & 0xFFFF0000u);  // k0+5, k0+7
+            // bf16 pairs (k0, k0+1), (k0+2, k0+3), ...  A dword read as f32 is
+            // its high bf16 plus low-order bits below f16 precision, which the
+            // round-toward-zero conversion discards, so the high halves need no
+            // masking.
+            const uint32_t* q = xraw[slot][i];
+            const uint32_t p0 = pk_f16(q[0] << 16, q[1] << 16);  // k0, k0+2
+            const uint32_t p1 = pk_f16(q[0], q[1]);              // k0+1, k0+3
+            const uint32_t p2 = pk_f16(q[2] << 16, q[3] << 16);  // k0+4, k0+6
+            const uint32_t p3 = pk_f16(q[2], q[3]);              // k0+5, k0+7
             *reinterpret_cast<uint4*>(&dx[r * PITCH + 8u * g8]) = make_uint4(p0, p1, p2, p3);
         }
         const h2 off_lo = {(_Float16)-1032.0f, (_Float16)-1032.0f};
@@ -193,56 +200,73 @@ struct Producer {
     }
 };
 
-// One MMA wave's sub-tile: TM x TN blocks of 16x16, fragments read from LDS.
+// One MMA wave's sub-tile: TM x TN blocks of 32x32 (v_mfma_f32_32x32x16_f16),
+// fragments read from LDS.  Operand layout: lane l holds row (or column)
+// l % 32 and the 8 k at 8·(l / 32) of the instruction's 16.
 template <int BM, int BN, int WM, int WN, int NB>
 struct Consumer {
     static constexpr int PITCH = 32 * NB + 8;
-    static constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
-    static_assert(TM * 16 * WM == BM && TN * 16 * WN == BN, "tile must split into 16x16 blocks per wave");
-    f4 acc[TM][TN];
+    static constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+    static_assert(TM * 32 * WM == BM && TN * 32 * WN == BN, "tile must split into 32x32 blocks per wave");
+    f32x16 acc[TM][TN];
     uint32_t fr, fk, arow, bcol, lane;
 
     __device__ __forceinline__ void init(uint32_t lane_, uint32_t cw) {
         lane = lane_;
-        fr = lane & 15u;
-        fk = (lane >> 4) * 8u;
+        fr = lane & 31u;
+        fk = (lane >> 5) * 8u;
         arow = (cw / WN) * (BM / WM);
         bcol = (cw % WN) * (BN / WN);
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < TN; j++) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
     }
 
-    __device__ __forceinline__ void mma(const _Float16* ax, const _Float16* bw) {
+    // A stage's fragments, all read before the first MFMA so that LDS latency
+    // is paid once per stage rather than once per MFMA depth.
+    struct Frags {
+        h8 a[2 * NB][TM], b[2 * NB][TN];
+    };
+
+    __device__ __forceinline__ void load(const _Float16* ax, const _Float16* bw, Frags& f) const {
 #pragma unroll
-        for (int kk = 0; kk < NB; kk++) {
-            h8 a[TM], b[TN];
+        for (int kk = 0; kk < 2 * NB; kk++) {
 #pragma unroll
             for (int i = 0; i < TM; i++)
-                a[i] = *reinterpret_cast<const h8*>(&ax[(arow + i * 16u + fr) * PITCH + kk * 32u + fk]);
+                f.a[kk][i] = *reinterpret_cast<const h8*>(&ax[(arow + i * 32u + fr) * PITCH + kk * 16u + fk]);
 #pragma unroll
             for (int j = 0; j < TN; j++)
-                b[j] = *reinterpret_cast<const h8*>(&bw[(bcol + j * 16u + fr) * PITCH + kk * 32u + fk]);
+                f.b[kk][j] = *reinterpret_cast<const h8*>(&bw[(bcol + j * 32u + fr) * PITCH + kk * 16u + fk]);
+        }
+    }
+
+    __device__ __forceinline__ void mma(const Frags& f) {
+#pragma unroll
+        for (int kk = 0; kk < 2 * NB; kk++)
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk][i], f.b[kk][j], acc[i][j], 0, 0, 0);
     }
 
-    // D layout of 16x16 MFMA: lane holds rows 4*(lane/16) + r, column lane%16.
+    static constexpr int kMfmas = 2 * NB * TM * TN;
+
+    // D layout of 32x32 MFMA: lane holds column lane%32 and, for r = 0..15,
+    // row 8·(r/4) + 4·(lane/32) + r%4.
     __device__ __forceinline__ void store(void* Y, uint32_t m0, uint32_t n0, uint32_t M, uint32_t N, uint32_t y_bf16) {
-        const uint32_t col_l = lane & 15u, row_l = (lane >> 4) * 4u;
+        const uint32_t col_l = lane & 31u, row_l = (lane >> 5) * 4u;
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int j = 0; j < TN; j++) {
-                const uint32_t col = n0 + bcol + j * 16u + col_l;
+                const uint32_t col = n0 + bcol + j * 32u + col_l;
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const uint32_t row = m0 + arow + i * 16u + row_l + r;
+                for (int r = 0; r < 16; r++) {
+                    const uint32_t row = m0 + arow + i * 32u + 8u * (r >> 2) + row_l + (r & 3);
                     if (row < M && col < N) {
                         const size_t idx = (size_t)row * N + col;
                         if (y_bf16) gptr_mut<uint16_t>(Y)[idx] = f32_to_bf16_bits(acc[i][j][r]);
@@ -286,19 +310,38 @@ __global__ __launch_bounds__((WM * WN + PW) * 64) void gemm_q4_0_kernel(const ui
     const uint32_t n0 = (tau / mt) * BN, m0 = (tau % mt) * BM;
     const uint32_t nst = (K + (uint32_t)BK - 1) / (uint32_t)BK;  // stages; the last may hold fewer than NB blocks
 
-    // Producer schedule.  Prologue: PF stages of loads in flight (stages past
-    // the end re-load the last one), stage 0 in LDS buffer 0, barrier.  Stage s:
-    // refill ring slot s % PF with stage s + PF, decode stage s + 1 into the
-    // other buffer (the MMA of stage s reads buffer s & 1), barrier.
-    auto produce = [&](P& p, auto&& during) {
+    auto last = [&](uint32_t t) { return t < nst ? t : nst - 1u; };
+
+    if constexpr (PW == 0) {
+        // Every wave loads, decodes and multiplies.  Prologue: PF stages of
+        // loads in flight (stages past the end re-load the last one), stage 0
+        // decoded into LDS buffer 0, barrier.  Stage s, branch-free: refill
+        // ring slot s % PF with stage s + PF, read all of stage s's fragments
+        // (buffer s & 1), then the MFMAs of stage s interleaved with
+        // the decode of stage s + 1 into the other buffer (past the end: the
+        // last stage again, never read), barrier.  The MFMAs run in the matrix
+        // core while the decode's VALU work issues between them.
+        P p;
+        C c;
+        p.init(W, X, tid, m0, n0, M, N, K);
+        c.init(lane, wave);
 #pragma unroll
-        for (int s = 0; s < PF; s++) p.gload(s, (uint32_t)s < nst ? (uint32_t)s : nst - 1u);
+        for (int s = 0; s < PF; s++) p.gload(s, last((uint32_t)s));
         p.lstore(0, bufx(0), bufw(0), 0);
         __syncthreads();
         auto iter = [&](int slot, uint32_t s) {
-            p.gload(slot, s + PF < nst ? s + PF : nst - 1u);
-            during(s);
-            if (s + 1 < nst) p.lstore((slot + 1) % PF, bufx(s + 1), bufw(s + 1), s + 1);
+            p.gload(slot, last(s + PF));
+            __builtin_amdgcn_sched_barrier(0);  // the loads leave first, before anything waits
+            typename C::Frags f;
+            c.load(bufx(s), bufw(s), f);
+            c.mma(f);
+            p.lstore((slot + 1) % PF, bufx(s + 1), bufw(s + 1), last(s + 1));
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * NB * (C::TM + C::TN), 0);  // DS reads
+#pragma unroll
+            for (int m = 0; m < C::kMfmas; m++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                     // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, P::kValu / C::kMfmas, 0);  // decode VALU
+            }
             __syncthreads();
         };
         uint32_t s0 = 0;
@@ -309,27 +352,39 @@ __global__ __launch_bounds__((WM * WN + PW) * 64) void gemm_q4_0_kernel(const ui
 #pragma unroll
         for (int slot = 0; slot < PF; slot++)
             if (s0 + (uint32_t)slot < nst) iter(slot, s0 + (uint32_t)slot);
-    };
-
-    if constexpr (PW == 0) {
-        P p;
-        C c;
-        p.init(W, X, tid, m0, n0, M, N, K);
-        c.init(lane, wave);
-        produce(p, [&](uint32_t s) { c.mma(bufx(s), bufw(s)); });
         c.store(Y, m0, n0, M, N, y_bf16);
     } else {
-        // wave-uniform split: every wave passes the same 1 + nst barriers
+        // PW producer waves load and decode stage s + 1 while the MMA waves
+        // multiply stage s; one barrier per stage (wave-uniform split: every
+        // wave passes the same 1 + nst barriers).
         if (wave < (uint32_t)PW) {
             P p;
             p.init(W, X, tid, m0, n0, M, N, K);
-            produce(p, [](uint32_t) {});
+#pragma unroll
+            for (int s = 0; s < PF; s++) p.gload(s, last((uint32_t)s));
+            p.lstore(0, bufx(0), bufw(0), 0);
+            __syncthreads();
+            auto iter = [&](int slot, uint32_t s) {
+                p.gload(slot, last(s + PF));
+                p.lstore((slot + 1) % PF, bufx(s + 1), bufw(s + 1), last(s + 1));
+                __syncthreads();
+            };
+            uint32_t s0 = 0;
+            for (; s0 + PF <= nst; s0 += PF) {
+#pragma unroll
+                for (int slot = 0; slot < PF; slot++) iter(slot, s0 + (uint32_t)slot);
+            }
+#pragma unroll
+            for (int slot = 0; slot < PF; slot++)
+                if (s0 + (uint32_t)slot < nst) iter(slot, s0 + (uint32_t)slot);
         } else {
             C c;
             c.init(lane, wave - PW);
             __syncthreads();
             for (uint32_t s = 0; s < nst; s++) {
-                c.mma(bufx(s), bufw(s));
+                typename C::Frags f;
+                c.load(bufx(s), bufw(s), f);
+                c.mma(f);
                 __syncthreads();
             }
             c.store(Y, m0, n0, M, N, y_bf16);
@@ -375,7 +430,7 @@ hipError_t gemm_q4_0_launch(const uint8_t* w, uint32_t N, uint32_t K, const void
     if (M <= N && tiles(64, 128) >= kCus * 3 / 4)
         return launch_tile<64, 128, 2, 4, 0, 64, 4>(w, N, K, xp, M, y, yb, stream);
     if (tiles(128, 64) >= kCus * 3 / 4) return launch_tile<128, 64, 4, 2, 0, 128, 2>(w, N, K, xp, M, y, yb, stream);
-    return launch_tile<64, 64, 2, 4, 0, 128, 2>(w, N, K, xp, M, y, yb, stream);
+    return launch_tile<64, 64, 2, 2, 0, 128, 2>(w, N, K, xp, M, y, yb, stream);
 }
 
 }  // namespace dmx

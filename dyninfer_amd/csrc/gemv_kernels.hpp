@@ -184,6 +184,129 @@ __device__ __forceinline__ void stage_x(uint8_t* lds, const void* __restrict__ x
     __syncthreads();
 }
 
+// Reduction over the GP (8 or 16) adjacent lanes of a scale group, all lanes
+// receiving the result: xor-1, xor-2 quad permutes, then the half-row and row
+// mirrors (each lane meets the other half of its 8, then of its 16).
+template <int GP, bool MAX>
+__device__ __forceinline__ float group_reduce(float v) {
+    static_assert(GP == 8 || GP == 16, "scale groups span 8 or 16 lanes");
+#define DMX_STEP(ctrl)                                                                                 \
+    {                                                                                                  \
+        const float o = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false)); \
+        v = MAX ? fmaxf(v, o) : v + o;                                                                 \
+    }
+    DMX_STEP(0xB1)   // quad_perm [1,0,3,2]
+    DMX_STEP(0x4E)   // quad_perm [2,3,0,1]
+    DMX_STEP(0x141)  // row_half_mirror
+    if constexpr (GP == 16) DMX_STEP(0x140)  // row_mirror
+#undef DMX_STEP
+    return v;
+}
+
+// Same tile as stage_x, staged with one thread per f16 pair (NT·PPT threads
+// per (row, chunk), PASSES rounds of the workgroup): for tiles of few chunks,
+// where one thread per chunk would leave most of the workgroup idle behind a
+// long serial chain.  A scale group's pairs sit on adjacent lanes inside one
+// DPP row, so its largest magnitude and its constants reduce across lanes.
+// The constants equal stage_x's up to the order of their f32 sums.
+template <class E, int B, bool XBF16, int PASSES>
+__device__ __forceinline__ void stage_x_pairs(uint8_t* lds, const void* __restrict__ x, uint32_t K, uint32_t ldx,
+                                              uint32_t batch) {
+    using XT = XTile<E>;
+    constexpr int NP = E::NT * E::PPT;  // pairs per chunk
+    constexpr int GP = NP / E::NG;      // pairs per scale group
+    const uint32_t nch = K / (uint32_t)E::CW;
+    const uint32_t items = (uint32_t)B * nch;
+    uint32_t* xp = reinterpret_cast<uint32_t*>(lds);
+    float* xc = reinterpret_cast<float*>(lds + (size_t)B * nch * XT::XPW * 4u);
+    // Pair (t, h) of lane j: the GP pairs of scale group g = j / GP.
+    const uint32_t j = threadIdx.x % (uint32_t)NP;  // blockDim is a multiple of NP
+    const uint32_t g = j / (uint32_t)GP, k = j % (uint32_t)GP;
+    uint32_t t, h;
+    if constexpr (E::NG == 1) {
+        t = j / (uint32_t)E::PPT;
+        h = j % (uint32_t)E::PPT;
+    } else {
+        static_assert(E::NG == 4 && E::NT == 4 && E::PPT == 8, "Q6_K groups: h in {g, g + 4}, t = 0..3");
+        t = k >> 1;
+        h = g + 4u * (k & 1u);
+    }
+    const uint32_t o0 = (uint32_t)E::xoff((int)t, (int)h, 0), o1 = (uint32_t)E::xoff((int)t, (int)h, 1);
+    const bool dv = E::dv((int)t, (int)h);
+    // All rounds' activations are loaded before any is used, so the rounds
+    // share one memory latency.
+    uint32_t item[PASSES];
+    bool live[PASSES];
+    float v0[PASSES], v1[PASSES];
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ps++) {
+        const uint32_t it = (threadIdx.x + (uint32_t)ps * blockDim.x) / (uint32_t)NP;
+        live[ps] = it < items;
+        item[ps] = live[ps] ? it : items - 1u;  // spare lanes redo the last chunk, unstored
+        const uint32_t b = B == 1 ? 0u : item[ps] / nch, u = item[ps] - b * nch;
+        const uint32_t base = (b < batch ? b : 0u) * ldx + E::xbase(u);  // the activations are < 4 GiB
+        if constexpr (XBF16) {
+            const uint16_t* xs = static_cast<const uint16_t*>(x);
+            v0[ps] = __uint_as_float((uint32_t)*gptr<uint16_t>(xs + (base + o0)) << 16);
+            v1[ps] = __uint_as_float((uint32_t)*gptr<uint16_t>(xs + (base + o1)) << 16);
+        } else {
+            const float* xs = static_cast<const float*>(x);
+            v0[ps] = *gptr<float>(xs + (base + o0));
+            v1[ps] = *gptr<float>(xs + (base + o1));
+        }
+        if (b >= batch) v0[ps] = v1[ps] = 0.0f;  // rows past the batch stage as zeros
+    }
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ps++) {
+        const float m = group_reduce<GP, true>(fmaxf(fabsf(v0[ps]), fabsf(v1[ps])));
+        int e = 0;
+        (void)frexpf(m, &e);
+        e = e < -110 ? -110 : e;  // keeps s = 2^(e-14) a normal f32
+        _Float16 lo = (_Float16)ldexpf(v0[ps], 14 - e);
+        _Float16 hi = (_Float16)ldexpf(v1[ps], 14 - e);
+        if (dv) {
+            lo = lo * (_Float16)0.0625f;
+            hi = hi * (_Float16)0.0625f;
+        }
+        const float fl = (float)lo, fh = (float)hi;
+        const float coef = dv ? E::coef(true) : E::coef(false);
+        const float C = group_reduce<GP, false>(fmaf(coef, fh, coef * fl));
+        const float S = group_reduce<GP, false>(dv ? 16.0f * (fl + fh) : fl + fh);
+        if (live[ps]) {
+            xp[(size_t)item[ps] * XT::XPW + t * (uint32_t)E::PPT + h] =
+                (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+            if (k == 0) {
+                const float s = ldexpf(1.0f, e - 14);
+                float* c = xc + ((size_t)item[ps] * E::NG + g) * XT::NCF;
+                if constexpr (XT::NCF == 4) {
+                    *reinterpret_cast<float4*>(c) = make_float4(-C, s, s * S, 0.0f);
+                } else {
+                    *reinterpret_cast<float2*>(c) = make_float2(-C, s);
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Stages the activation tile.  When every wave of the grid has at most one
+// row block the launch is latency-bound and the tile is staged one thread per
+// pair (up to four rounds of the workgroup); otherwise the weight stream is
+// long and the one-thread-per-chunk stager, which spends a fraction of the
+// instructions, is used.
+template <class E, int B, bool XBF16>
+__device__ __forceinline__ void stage_x_auto(uint8_t* lds, const GemvParams& p) {
+    const void* x = p.x;
+    const uint32_t K = p.K, ldx = p.ldx, batch = p.batch;
+    const uint32_t pairs = (uint32_t)B * (K / (uint32_t)E::CW) * (uint32_t)(E::NT * E::PPT);
+    const bool latency_bound = p.total_rb <= gridDim.x * (blockDim.x >> 6);
+    if (!latency_bound) stage_x<E, B, XBF16>(lds, x, K, ldx, batch);
+    else if (pairs <= blockDim.x) stage_x_pairs<E, B, XBF16, 1>(lds, x, K, ldx, batch);
+    else if (pairs <= 2u * blockDim.x) stage_x_pairs<E, B, XBF16, 2>(lds, x, K, ldx, batch);
+    else if (pairs <= 4u * blockDim.x) stage_x_pairs<E, B, XBF16, 4>(lds, x, K, ldx, batch);
+    else stage_x<E, B, XBF16>(lds, x, K, ldx, batch);
+}
+
 // ---------------------------------------------------------------- chunk dot product
 // Reads the (-C, s, s·Σx) constants of group g of chunk u for activation row b.
 template <class E>
@@ -487,7 +610,7 @@ __global__ __launch_bounds__(kGemvThreads) void gguf_gemv_kernel(const GemvParam
     extern __shared__ __align__(16) uint8_t xlds[];
     const uint32_t rowbytes = (p.K / (uint32_t)E::QK) * (uint32_t)E::BB;
     auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) { return E::load(rb.w, row * rowbytes, u); };
-    gemv_pipeline<E, R, B>(p, xlds, load, [&] { stage_x<E, B, XBF16>(xlds, p.x, p.K, p.ldx, p.batch); });
+    gemv_pipeline<E, R, B>(p, xlds, load, [&] { stage_x_auto<E, B, XBF16>(xlds, p); });
 }
 
 // ---------------------------------------------------------------- MLX affine U4
@@ -515,7 +638,7 @@ __global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_kernel(const GemvPar
         r.kind = p.sdtype;
         return r;
     };
-    gemv_pipeline<E, R, B>(p, xlds, load, [&] { stage_x<E, B, XBF16>(xlds, p.x, p.K, p.ldx, p.batch); });
+    gemv_pipeline<E, R, B>(p, xlds, load, [&] { stage_x_auto<E, B, XBF16>(xlds, p); });
 }
 
 // Rows per lane group for a register batch B: more rows amortise each
