@@ -25,7 +25,7 @@ __device__ __forceinline__ uint32_t load_u16le(const uint8_t* p) { return (uint3
 template <uint32_t ENC>
 __global__ __launch_bounds__(256) void gguf_dequant_kernel(const uint8_t* __restrict__ w, uint64_t nslices,
                                                            float* __restrict__ out) {
-    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t t = (uint64_t)blockIdx.x * 256u + threadIdx.x;  // launched with 256 threads
     if (t >= nslices) return;
     float* o = out + t * 32;
     if constexpr (ENC == ENC_Q4_0) {
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(256) void mlx_u4_dequant_kernel(const uint32_t* __r
                                                              const uint8_t* __restrict__ bi, uint64_t nwords,
                                                              uint32_t K, uint32_t group, uint32_t sdtype,
                                                              float* __restrict__ out) {
-    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t t = (uint64_t)blockIdx.x * 256u + threadIdx.x;  // launched with 256 threads
     if (t >= nwords) return;
     const uint64_t k0 = t * 8;  // flat index of the word's first weight
     const uint64_t row = k0 / K;

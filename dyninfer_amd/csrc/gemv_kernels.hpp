@@ -114,7 +114,7 @@ __device__ __forceinline__ void stage_x(uint8_t* lds, const void* __restrict__ x
     const uint32_t nch = K / (uint32_t)E::CW;
     uint32_t* xp = reinterpret_cast<uint32_t*>(lds);
     float* xc = reinterpret_cast<float*>(lds + (size_t)B * nch * XT::XPW * 4u);
-    for (uint32_t item = threadIdx.x; item < (uint32_t)B * nch; item += blockDim.x) {
+    for (uint32_t item = threadIdx.x; item < (uint32_t)B * nch; item += (uint32_t)kGemvThreads) {
         const uint32_t b = item / nch, u = item - b * nch;
         float v[E::NRUN][E::RUNLEN];
         if (b < batch) {
@@ -220,7 +220,7 @@ __device__ __forceinline__ void stage_x_pairs(uint8_t* lds, const void* __restri
     uint32_t* xp = reinterpret_cast<uint32_t*>(lds);
     float* xc = reinterpret_cast<float*>(lds + (size_t)B * nch * XT::XPW * 4u);
     // Pair (t, h) of lane j: the GP pairs of scale group g = j / GP.
-    const uint32_t j = threadIdx.x % (uint32_t)NP;  // blockDim is a multiple of NP
+    const uint32_t j = threadIdx.x % (uint32_t)NP;  // the workgroup size is a multiple of NP
     const uint32_t g = j / (uint32_t)GP, k = j % (uint32_t)GP;
     uint32_t t, h;
     if constexpr (E::NG == 1) {
@@ -240,7 +240,7 @@ __device__ __forceinline__ void stage_x_pairs(uint8_t* lds, const void* __restri
     float v0[PASSES], v1[PASSES];
 #pragma unroll
     for (int ps = 0; ps < PASSES; ps++) {
-        const uint32_t it = (threadIdx.x + (uint32_t)ps * blockDim.x) / (uint32_t)NP;
+        const uint32_t it = (threadIdx.x + (uint32_t)ps * (uint32_t)kGemvThreads) / (uint32_t)NP;
         live[ps] = it < items;
         item[ps] = live[ps] ? it : items - 1u;  // spare lanes redo the last chunk, unstored
         const uint32_t b = B == 1 ? 0u : item[ps] / nch, u = item[ps] - b * nch;
@@ -299,11 +299,11 @@ __device__ __forceinline__ void stage_x_auto(uint8_t* lds, const GemvParams& p) 
     const void* x = p.x;
     const uint32_t K = p.K, ldx = p.ldx, batch = p.batch;
     const uint32_t pairs = (uint32_t)B * (K / (uint32_t)E::CW) * (uint32_t)(E::NT * E::PPT);
-    const bool latency_bound = p.total_rb <= gridDim.x * (blockDim.x >> 6);
+    const bool latency_bound = p.total_rb <= p.grid * (uint32_t)(kGemvThreads / 64);
     if (!latency_bound) stage_x<E, B, XBF16>(lds, x, K, ldx, batch);
-    else if (pairs <= blockDim.x) stage_x_pairs<E, B, XBF16, 1>(lds, x, K, ldx, batch);
-    else if (pairs <= 2u * blockDim.x) stage_x_pairs<E, B, XBF16, 2>(lds, x, K, ldx, batch);
-    else if (pairs <= 4u * blockDim.x) stage_x_pairs<E, B, XBF16, 4>(lds, x, K, ldx, batch);
+    else if (pairs <= 1u * kGemvThreads) stage_x_pairs<E, B, XBF16, 1>(lds, x, K, ldx, batch);
+    else if (pairs <= 2u * kGemvThreads) stage_x_pairs<E, B, XBF16, 2>(lds, x, K, ldx, batch);
+    else if (pairs <= 4u * kGemvThreads) stage_x_pairs<E, B, XBF16, 4>(lds, x, K, ldx, batch);
     else stage_x<E, B, XBF16>(lds, x, K, ldx, batch);
 }
 
@@ -522,8 +522,11 @@ __device__ __forceinline__ void reduce_store(float (&acc)[R][B], const RowBlock&
 template <class E, int R, int B, class LOAD, class STAGE>
 __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const uint8_t* lds, LOAD&& load, STAGE&& stage) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
-    const uint32_t W = gridDim.x * (blockDim.x >> 6);
+    // The launch shape comes from compile-time constants and the parameters:
+    // reading blockDim/gridDim costs a load from the dispatch packet that the
+    // first weight loads would wait behind.
+    const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (uint32_t)(kGemvThreads / 64) + (threadIdx.x >> 6));
+    const uint32_t W = p.grid * (uint32_t)(kGemvThreads / 64);
     const uint32_t L = 1u << p.lanes_log2;
     const uint32_t j = lane & (L - 1u), g = lane >> p.lanes_log2;
     const uint32_t rows_per_rb = (64u >> p.lanes_log2) * (uint32_t)R;
@@ -670,7 +673,9 @@ hipError_t launch_persistent(KERNEL kernel, const GemvParams& p, size_t lds, hip
     const uint64_t want = ((uint64_t)p.total_rb + waves - 1) / waves;
     const uint64_t cap = (uint64_t)per_cu * (uint64_t)cus;
     const uint32_t blocks = (uint32_t)(want < cap ? want : cap);
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), lds, st, p);
+    GemvParams q = p;
+    q.grid = blocks;
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), lds, st, q);
     return hipGetLastError();
 }
 

@@ -12,22 +12,25 @@ constexpr int kMaxGemvBatch = 16;
 enum Enc : uint32_t { ENC_Q4_0 = 2, ENC_Q4_1 = 3, ENC_Q8_0 = 8, ENC_Q6_K = 14, ENC_MLX_U4 = 0x1004 };
 enum DType : uint32_t { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
 
-// Kernel parameters of one GEMV launch (passed by value as the kernel argument).
+// Kernel parameters of one GEMV launch (passed by value as the kernel
+// argument).  The fields that address the first weight loads lead, in the
+// first 96 bytes, so that they arrive in one round of scalar loads.
 struct GemvParams {
     const uint8_t* w[kMaxProblems];   // GGUF blocks, or MLX packed words
-    const uint8_t* sc[kMaxProblems];  // MLX scales
-    const uint8_t* bi[kMaxProblems];  // MLX biases
-    void* y[kMaxProblems];
     uint32_t n[kMaxProblems];
     uint32_t rb_begin[kMaxProblems];  // first row block of each problem
     uint32_t total_rb;                // row blocks over all problems
-    uint32_t nprob;
-    const void* x;
+    uint32_t grid;                    // workgroups launched (set by the launcher)
     uint32_t K;
+    uint32_t lanes_log2;  // lanes cooperating on one weight row (L = 2^lanes_log2 divides K/chunk)
+    uint32_t nprob;
     uint32_t ldx;         // activation row stride, elements
     uint32_t ldy;         // output row stride, elements (per problem: its N)
     uint32_t batch;       // activation rows actually present (<= kernel's B)
-    uint32_t lanes_log2;  // lanes cooperating on one weight row (L = 2^lanes_log2 divides K/chunk)
+    const void* x;
+    void* y[kMaxProblems];
+    const uint8_t* sc[kMaxProblems];  // MLX scales
+    const uint8_t* bi[kMaxProblems];  // MLX biases
     uint32_t y_bf16;      // store bf16 instead of f32
     uint32_t group;       // MLX group size
     uint32_t sdtype;      // MLX scale/bias dtype
