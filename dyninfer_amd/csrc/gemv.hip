@@ -8,11 +8,11 @@
 
 namespace dmx {
 
-hipError_t gemv_launch_q4_0(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st);
-hipError_t gemv_launch_q4_1(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st);
-hipError_t gemv_launch_q8_0(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st);
-hipError_t gemv_launch_q6_k(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st);
-hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q4_0(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q4_1(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q8_0(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q6_k(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16, hipStream_t st);
 
 hipError_t cached_occupancy(const void* kernel, size_t lds, int threads, int* per_cu, int* cus) {
     struct Entry {
@@ -97,13 +97,14 @@ uint32_t rows_per_group(const EncInfo& e, uint32_t B) {
     return B <= 4 ? 4 : 2;
 }
 
-hipError_t launch(uint32_t enc, const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st) {
+hipError_t launch(uint32_t enc, const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16,
+                  hipStream_t st) {
     switch (enc) {
-    case ENC_Q4_0: return gemv_launch_q4_0(p, B, R, xbf16, st);
-    case ENC_Q4_1: return gemv_launch_q4_1(p, B, R, xbf16, st);
-    case ENC_Q8_0: return gemv_launch_q8_0(p, B, R, xbf16, st);
-    case ENC_Q6_K: return gemv_launch_q6_k(p, B, R, xbf16, st);
-    case ENC_MLX_U4: return gemv_launch_mlx_u4(p, B, R, xbf16, st);
+    case ENC_Q4_0: return gemv_launch_q4_0(p, B, R, oneshot, xbf16, st);
+    case ENC_Q4_1: return gemv_launch_q4_1(p, B, R, oneshot, xbf16, st);
+    case ENC_Q8_0: return gemv_launch_q8_0(p, B, R, oneshot, xbf16, st);
+    case ENC_Q6_K: return gemv_launch_q6_k(p, B, R, oneshot, xbf16, st);
+    case ENC_MLX_U4: return gemv_launch_mlx_u4(p, B, R, oneshot, xbf16, st);
     default: return hipErrorInvalidValue;
     }
 }
@@ -149,14 +150,24 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     while (L < 64 && 2 * L <= nch) L *= 2;
     uint32_t lanes_log2 = 0;
     while ((1u << lanes_log2) < L) lanes_log2++;
-    // Rows per lane group: with one activation row, a single row when the
-    // matrices are too small to give every resident wave (~4096) two row
-    // blocks — more waves and a shorter per-task chain — else the wider tile.
+    // One activation row: latency mode (one wave per row block of one row per
+    // lane group, all of a lane's chunks loaded at once) when the matrices
+    // give at most 16384 such row blocks and a lane at most 4 chunks (Q6_K: 2;
+    // its wider raw chunks would otherwise cost waves per SIMD).
+    // Otherwise the persistent pipeline, with rows per lane group R as wide as
+    // the batch allows, or 1 when the wider tile would give fewer than 2048
+    // row blocks (more waves, shorter per-task chains).
+    auto count_rbs = [&](uint32_t rows) {
+        uint64_t n = 0;
+        for (int i = 0; i < nprob; i++) n += (probs[i].n + rows - 1) / rows;
+        return n;
+    };
+    const uint32_t cpl = (nch + L - 1) >> lanes_log2;
     uint32_t R = rows_per_group(info, B);
+    uint32_t oneshot = 0;
     if (B == 1) {
-        uint64_t rbs = 0;
-        for (int i = 0; i < nprob; i++) rbs += (probs[i].n + (64u >> lanes_log2) * R - 1) / ((64u >> lanes_log2) * R);
-        if (rbs < 8192) R = 1;
+        if (cpl <= (info.q6k ? 2u : 4u) && count_rbs(64u >> lanes_log2) <= 16384) oneshot = cpl;
+        if (oneshot || count_rbs((64u >> lanes_log2) * R) < 2048) R = 1;
     }
     const uint32_t rows_per_rb = (64u >> lanes_log2) * R;
 
@@ -183,7 +194,7 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     p.y_bf16 = y_bf16 ? 1u : 0u;
     p.group = group;
     p.sdtype = sdtype;
-    return launch(enc, p, B, R, x_bf16, stream);
+    return launch(enc, p, B, R, oneshot, x_bf16, stream);
 }
 
 }  // namespace dmx

@@ -605,6 +605,44 @@ __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const uint8_t
     if (t < T) compute(ba, nblk, nc);  // odd task count: the last task is in ba
 }
 
+// Latency mode, one activation row: every wave owns at most one row block
+// (total row blocks <= waves launched), so there is no task loop.  A lane
+// issues the loads of all CPL of its chunks before the activations are
+// staged, so the whole launch waits on one memory latency; then it
+// multiplies them, the L lanes reduce, and lane 0 stores.
+template <class E, int CPL, class LOAD, class STAGE>
+__device__ __forceinline__ void gemv_oneshot(const GemvParams& p, const uint8_t* lds, LOAD&& load, STAGE&& stage) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (uint32_t)(kGemvThreads / 64) + (threadIdx.x >> 6));
+    const uint32_t L = 1u << p.lanes_log2;
+    const uint32_t j = lane & (L - 1u), g = lane >> p.lanes_log2;
+    const uint32_t rows_per_rb = 64u >> p.lanes_log2;
+    const uint32_t nch = p.K / (uint32_t)E::CW;
+    const bool active = wid < p.total_rb;
+    const RowBlock blk = row_block(p, active ? wid : p.total_rb - 1u, rows_per_rb);
+    const uint32_t row = blk.base + g < blk.n ? blk.base + g : blk.n - 1u;
+    typename E::Raw buf[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+        const uint32_t u = j + (uint32_t)c * L;
+        buf[c] = load(blk, row, u < nch ? u : nch - 1u);
+    }
+    stage();
+    if (!active) return;
+    float acc[1][1] = {{0.0f}};
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+        const uint32_t u0 = j + (uint32_t)c * L;
+        const bool past = u0 >= nch;  // a lane past the last chunk: adds zero
+        const uint32_t u = past ? nch - 1u : u0;
+        typename E::Chunk ch[1];
+        ch[0] = E::unpack(buf[c], u);
+        E::zero_if(ch[0], past);
+        chunk_dot<E, 1, 1>(ch, lds, nch, u, acc);
+    }
+    reduce_store<1, 1>(acc, blk, blk.base + g, j, L, p);
+}
+
 // ---------------------------------------------------------------- GGUF
 // Weight offsets are 32-bit (the C ABI limits one weight to 4 GiB), so loads
 // use a uniform 64-bit base plus a per-lane 32-bit offset.
@@ -616,16 +654,25 @@ __global__ __launch_bounds__(kGemvThreads) void gguf_gemv_kernel(const GemvParam
     gemv_pipeline<E, R, B>(p, xlds, load, [&] { stage_x_auto<E, B, XBF16>(xlds, p); });
 }
 
-// ---------------------------------------------------------------- MLX affine U4
-template <int B, int R, bool XBF16>
-__global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_kernel(const GemvParams p) {
-    using E = EncMlxU4;
+template <class E, int CPL, bool XBF16>
+__global__ __launch_bounds__(kGemvThreads) void gguf_gemv_oneshot_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
-    const uint32_t ngroups = p.K / p.group;
-    const uint32_t chunks_per_group = p.group / 32u;
-    const bool f32s = p.sdtype == DT_F32;
-    auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) {
-        E::Raw r;
+    const uint32_t rowbytes = (p.K / (uint32_t)E::QK) * (uint32_t)E::BB;
+    auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) { return E::load(rb.w, row * rowbytes, u); };
+    gemv_oneshot<E, CPL>(p, xlds, load, [&] { stage_x_auto<E, 1, XBF16>(xlds, p); });
+}
+
+// ---------------------------------------------------------------- MLX affine U4
+// Raw bytes of chunk u of a row: 16 bytes of packed words plus the group's
+// scale and bias (f32, or f16/bf16 bits).
+struct MlxLoad {
+    const GemvParams& p;
+    uint32_t ngroups, chunks_per_group;
+    bool f32s;
+    __device__ __forceinline__ explicit MlxLoad(const GemvParams& q)
+        : p(q), ngroups(q.K / q.group), chunks_per_group(q.group / 32u), f32s(q.sdtype == DT_F32) {}
+    __device__ __forceinline__ EncMlxU4::Raw operator()(const RowBlock& rb, uint32_t row, uint32_t u) const {
+        EncMlxU4::Raw r;
         const uint8_t* wb = rb.w;
         load_dwords<4>(reinterpret_cast<const uint32_t*>(wb + (row * (p.K / 2u) + u * 16u)), r.w);
         const uint32_t gi = row * ngroups + u / chunks_per_group;
@@ -640,8 +687,19 @@ __global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_kernel(const GemvPar
         }
         r.kind = p.sdtype;
         return r;
-    };
-    gemv_pipeline<E, R, B>(p, xlds, load, [&] { stage_x_auto<E, B, XBF16>(xlds, p); });
+    }
+};
+
+template <int B, int R, bool XBF16>
+__global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_kernel(const GemvParams p) {
+    extern __shared__ __align__(16) uint8_t xlds[];
+    gemv_pipeline<EncMlxU4, R, B>(p, xlds, MlxLoad(p), [&] { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p); });
+}
+
+template <int CPL, bool XBF16>
+__global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_oneshot_kernel(const GemvParams p) {
+    extern __shared__ __align__(16) uint8_t xlds[];
+    gemv_oneshot<EncMlxU4, CPL>(p, xlds, MlxLoad(p), [&] { stage_x_auto<EncMlxU4, 1, XBF16>(xlds, p); });
 }
 
 // Rows per lane group for a register batch B: more rows amortise each
@@ -679,15 +737,46 @@ hipError_t launch_persistent(KERNEL kernel, const GemvParams& p, size_t lds, hip
     return hipGetLastError();
 }
 
+// Latency-mode launch: one wave per row block.
+template <class KERNEL>
+hipError_t launch_oneshot(KERNEL kernel, const GemvParams& p, size_t lds, hipStream_t st) {
+    if (lds > 64u * 1024u) {
+        int cus = 0, per_cu = 0;
+        hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, kGemvThreads, &per_cu, &cus);
+        if (e != hipSuccess) return e;
+    }
+    constexpr uint32_t waves = kGemvThreads / 64;
+    GemvParams q = p;
+    q.grid = (p.total_rb + waves - 1) / waves;
+    hipLaunchKernelGGL(kernel, dim3(q.grid), dim3(kGemvThreads), lds, st, q);
+    return hipGetLastError();
+}
+
 // Instantiates and launches the GEMV kernel of encoding E for a power-of-two
-// register batch B (the host has checked that its activation tile fits LDS).
+// register batch B (the host has checked that its activation tile fits LDS);
+// oneshot = chunks per lane (1..4) selects the latency-mode kernel.
 // GGUF decode takes f32 activations, the reference's precision contract for
 // quantized linears (crates/dyninfer-compiler/src/lib.rs:289-306); bf16
 // activations reach GGUF weights only through the Q4_0 MFMA path.
 template <class E>
-hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st) {
+hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16,
+                            hipStream_t st) {
     if (xbf16) return hipErrorInvalidValue;
     const size_t lds = (size_t)xtile_bytes(E::ENC, B, p.K);
+    if (oneshot) {
+        if (B != 1 || R != 1) return hipErrorInvalidValue;
+        switch (oneshot) {
+        case 1: return launch_oneshot(gguf_gemv_oneshot_kernel<E, 1, false>, p, lds, st);
+        case 2: return launch_oneshot(gguf_gemv_oneshot_kernel<E, 2, false>, p, lds, st);
+        case 3:
+            if constexpr (E::ENC != ENC_Q6_K) return launch_oneshot(gguf_gemv_oneshot_kernel<E, 3, false>, p, lds, st);
+            return hipErrorInvalidValue;
+        case 4:
+            if constexpr (E::ENC != ENC_Q6_K) return launch_oneshot(gguf_gemv_oneshot_kernel<E, 4, false>, p, lds, st);
+            return hipErrorInvalidValue;
+        default: return hipErrorInvalidValue;
+        }
+    }
     if (B == 1 && R == 1) return launch_persistent(gguf_gemv_kernel<E, 1, 1, false>, p, lds, st);
 #define DMX_CASE(b)                                                                                  \
     case b:                                                                                          \

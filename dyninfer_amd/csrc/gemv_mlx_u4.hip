@@ -2,9 +2,24 @@
 #include "gemv_kernels.hpp"
 
 namespace dmx {
-hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t R, bool xbf16, hipStream_t st) {
+hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16, hipStream_t st) {
     using E = EncMlxU4;
     const size_t lds = (size_t)xtile_bytes(E::ENC, B, p.K);
+    if (oneshot) {
+        if (B != 1 || R != 1) return hipErrorInvalidValue;
+#define DMX_ONESHOT(c)                                                                               \
+    case c:                                                                                          \
+        return xbf16 ? launch_oneshot(mlx_u4_gemv_oneshot_kernel<c, true>, p, lds, st)                \
+                     : launch_oneshot(mlx_u4_gemv_oneshot_kernel<c, false>, p, lds, st);
+        switch (oneshot) {
+            DMX_ONESHOT(1)
+            DMX_ONESHOT(2)
+            DMX_ONESHOT(3)
+            DMX_ONESHOT(4)
+        default: return hipErrorInvalidValue;
+        }
+#undef DMX_ONESHOT
+    }
     if (B == 1 && R == 1)
         return xbf16 ? launch_persistent(mlx_u4_gemv_kernel<1, 1, true>, p, lds, st)
                      : launch_persistent(mlx_u4_gemv_kernel<1, 1, false>, p, lds, st);
