@@ -394,6 +394,12 @@ def main() -> int:
             for (n, k) in [(3072, 1024), (1024, 3072), (2048, 1024)]:
                 c3[f"M{m}_N{n}_K{k}"] = {kk: round(v, 4) for kk, v in bench_gemm(torch, d, ctx, m, n, k).items()}
         extra["config3_q4_0_gemm"] = c3
+        g512 = c3["M512_N3072_K1024"]
+        extra["config3_roofline"] = {"bound": "mfma", "kernel": "gemm_q4_0 M512 N3072 K1024",
+                                     "achieved": round(g512["TFLOPs"], 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                                     "unit": "TFLOP/s", "frac": round(g512["mfma_frac"], 4),
+                                     "flops_per_launch": 2 * 512 * 3072 * 1024, "avg_launch_us": round(g512["us"], 3),
+                                     "timing": "HIP events around 50 back-to-back launches; includes the dispatch gap"}
         log("config 4 (Qwen3-8B step) ...")
         s4 = gguf_step_8b(torch, d, gen)
         c4 = {"weight_bytes_per_step": s4.weight_bytes}
