@@ -319,7 +319,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: one 64 MiB device copy (the counters' calibration), then one "
-                         "eager config-1 step; prints the step's launch labels in dispatch order")
+                         "eager config-1 step and one M512 config-3 GEMM; prints the launch labels in dispatch order")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -345,8 +345,16 @@ def main() -> int:
         with torch.cuda.stream(r1.stream):
             r1.step(r1.stream)
         torch.cuda.synchronize()
+        # then one config-3 GEMM launch (M512 N3072 K1024, bf16 X and Y)
+        wg = gguf_tensor(torch, d, d.ENC_Q4_0, 3072, 1024, gen)
+        xg = torch.randn(512, 1024, device="cuda", generator=gen).bfloat16()
+        yg = torch.empty(512, 3072, device="cuda", dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        ctx.qlinear(wg, xg, yg)
+        torch.cuda.synchronize()
         print(json.dumps({"calibration_bytes": src.numel() * 4,
-                          "launches": [[lab, sum(w.nbytes for w in ws)] for lab, ws, _, _ in s1.launches]}))
+                          "launches": [[lab, sum(w.nbytes for w in ws)] for lab, ws, _, _ in s1.launches]
+                          + [["gemm.q4_0.M512_N3072_K1024", wg.nbytes]]}))
         return 0
     g1 = r1.capture()
     ms = r1.time_graph(g1, args.steps, args.warmup)
