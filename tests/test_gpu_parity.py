@@ -229,6 +229,35 @@ def test_gemv_full_size_rows_subset(ctx, gtype, n, k, batch):
     assert torch.count_nonzero(z).item() == 0
 
 
+@pytest.mark.parametrize("gtype", oracle.GGUF_TYPES, ids=oracle.NAMES.get)
+@pytest.mark.parametrize("n,k", [
+    (300, 6144),    # one activation row: latency mode, 3 chunks per lane (Q6_K: 3, persistent)
+    (300, 8192),    # latency mode, 4 chunks per lane (Q6_K: 2)
+    (1024, 12288),  # persistent pipeline, one row per lane group (6 chunks per lane)
+    (8448, 12288),  # persistent pipeline, 4 rows per lane group (Q6_K: 2); rows subset checked
+])
+def test_gemv_gguf_kernel_paths(ctx, gtype, n, k):
+    """Batch-1 shapes that select each GEMV kernel path (latency mode with 3 and
+    4 chunks per lane, the persistent pipeline with 1 and 4 rows per lane
+    group), against the oracle on up to 512 output rows."""
+    w, data = gguf(gtype, n, k, seed=n * 7 + k + gtype)
+    x = oracle.randn(k, seed=n + k).reshape(1, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    rows = np.sort(np.random.default_rng(n).choice(n, size=min(512, n), replace=False))
+    wsub = oracle.dequant_gguf(gtype, _rows_subset(gtype, data, n, k, rows), len(rows), k)
+    assert gemv_err(np.ascontiguousarray(y[:, rows]), x, wsub) <= XF16
+
+
+@pytest.mark.parametrize("n,k", [(300, 6144), (300, 8192), (1024, 12288)])
+def test_gemv_mlx_kernel_paths(ctx, n, k):
+    g = 64
+    packed, sc, bi = oracle.synth_mlx_u4(n, k, g, oracle.D_BF16, seed=n + k)
+    w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), g, oracle.D_BF16)
+    x = oracle.randn(k, seed=k).reshape(1, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    assert gemv_err(y, x, oracle.dequant_mlx_u4(packed, sc, bi, oracle.D_BF16, n, k, g)) <= XF16
+
+
 # ----------------------------------------------------------------- activation range
 def _ranged_x(batch, k, seed, lo, hi, zero_block=True):
     """N(0,1) activations scaled by 10^u per 16-element run, u uniform in [lo, hi];
