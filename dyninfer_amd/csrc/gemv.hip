@@ -90,11 +90,11 @@ bool enc_info(uint32_t enc, EncInfo& e) {
 }
 
 // Rows per lane group for register batch B; must match rows_per_group<E, B>()
-// in gemv_kernels.hpp.  With one activation row, a single row per group is
-// also instantiated.
+// in gemv_kernels.hpp.  Half of it (rows_per_group_narrow) is instantiated
+// beside it for B > 1, and a single row for B = 1.
 uint32_t rows_per_group(const EncInfo& e, uint32_t B) {
     if (e.q6k) return B <= 2 ? 2 : 1;
-    return B <= 4 ? 4 : 2;
+    return B <= 2 ? 4 : 2;
 }
 
 hipError_t launch(uint32_t enc, const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16,
@@ -168,6 +168,8 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     if (B == 1) {
         if (cpl <= (info.q6k ? 2u : 4u) && count_rbs(64u >> lanes_log2) <= 16384) oneshot = cpl;
         if (oneshot || count_rbs((64u >> lanes_log2) * R) < 2048) R = 1;
+    } else if (R > 1 && count_rbs((64u >> lanes_log2) * R) < 2048) {
+        R /= 2;  // the narrower tile instantiated beside each batch's default
     }
     const uint32_t rows_per_rb = (64u >> lanes_log2) * R;
 

@@ -709,7 +709,15 @@ __global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_oneshot_kernel(const
 template <class E, int B>
 constexpr int rows_per_group() {
     if constexpr (E::ENC == ENC_Q6_K) return B <= 2 ? 2 : 1;
-    else return B <= 4 ? 4 : 2;
+    else return B <= 2 ? 4 : 2;
+}
+
+// The narrower tile instantiated beside it for activation rows > 1, taken by
+// the host when the wider one would leave too few row blocks for the GPU
+// (halving the rows gives twice the waves at fewer registers each).
+template <class E, int B>
+constexpr int rows_per_group_narrow() {
+    return rows_per_group<E, B>() > 1 ? rows_per_group<E, B>() / 2 : 1;
 }
 
 // Resident workgroups per CU for (kernel, dynamic LDS) on the current device
@@ -778,14 +786,17 @@ hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t R, uint32_
         }
     }
     if (B == 1 && R == 1) return launch_persistent(gguf_gemv_kernel<E, 1, 1, false>, p, lds, st);
-#define DMX_CASE(b)                                                                                  \
-    case b:                                                                                          \
-        if constexpr (b <= max_register_batch(E::ENC))                                               \
-            return R == (uint32_t)rows_per_group<E, b>()                                             \
-                       ? launch_persistent(gguf_gemv_kernel<E, b, rows_per_group<E, b>(), false>, p, lds, st) \
-                       : hipErrorInvalidValue;                                                       \
-        else                                                                                         \
-            return hipErrorInvalidValue;
+#define DMX_CASE(b)                                                                                       \
+    case b:                                                                                               \
+        if constexpr (b <= max_register_batch(E::ENC)) {                                                  \
+            if (R == (uint32_t)rows_per_group<E, b>())                                                    \
+                return launch_persistent(gguf_gemv_kernel<E, b, rows_per_group<E, b>(), false>, p, lds, st); \
+            if constexpr (b > 1)                                                                          \
+                if (R == (uint32_t)rows_per_group_narrow<E, b>())                                         \
+                    return launch_persistent(gguf_gemv_kernel<E, b, rows_per_group_narrow<E, b>(), false>, p, \
+                                             lds, st);                                                    \
+        }                                                                                                 \
+        return hipErrorInvalidValue;
     switch (B) {
         DMX_CASE(1)
         DMX_CASE(2)

@@ -23,11 +23,18 @@ hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t R, uint3
     if (B == 1 && R == 1)
         return xbf16 ? launch_persistent(mlx_u4_gemv_kernel<1, 1, true>, p, lds, st)
                      : launch_persistent(mlx_u4_gemv_kernel<1, 1, false>, p, lds, st);
-    if (R != (uint32_t)(B <= 4 ? 4 : 2)) return hipErrorInvalidValue;
 #define DMX_CASE(b)                                                                                        \
     case b:                                                                                                \
-        return xbf16 ? launch_persistent(mlx_u4_gemv_kernel<b, rows_per_group<E, b>(), true>, p, lds, st)  \
-                     : launch_persistent(mlx_u4_gemv_kernel<b, rows_per_group<E, b>(), false>, p, lds, st);
+        if (R == (uint32_t)rows_per_group<E, b>())                                                         \
+            return xbf16 ? launch_persistent(mlx_u4_gemv_kernel<b, rows_per_group<E, b>(), true>, p, lds, st)  \
+                         : launch_persistent(mlx_u4_gemv_kernel<b, rows_per_group<E, b>(), false>, p, lds, st); \
+        if constexpr (b > 1)                                                                               \
+            if (R == (uint32_t)rows_per_group_narrow<E, b>())                                              \
+            return xbf16 ? launch_persistent(mlx_u4_gemv_kernel<b, rows_per_group_narrow<E, b>(), true>, p, lds, \
+                                             st)                                                           \
+                         : launch_persistent(mlx_u4_gemv_kernel<b, rows_per_group_narrow<E, b>(), false>, p, lds, \
+                                             st);                                                          \
+        return hipErrorInvalidValue;
     switch (B) {
         DMX_CASE(1)
         DMX_CASE(2)
