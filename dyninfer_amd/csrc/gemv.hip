@@ -150,13 +150,16 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     while (L < 64 && 2 * L <= nch) L *= 2;
     uint32_t lanes_log2 = 0;
     while ((1u << lanes_log2) < L) lanes_log2++;
-    // One activation row: latency mode (one wave per row block of one row per
-    // lane group, all of a lane's chunks loaded at once) when the matrices
-    // give at most 16384 such row blocks and a lane at most 4 chunks (Q6_K: 2;
-    // its wider raw chunks would otherwise cost waves per SIMD).
+    // Latency mode (one wave per row block of one row per lane group, all of
+    // a lane's chunks loaded at once) when the matrices give at most 16384
+    // such row blocks and a lane few chunks: 4 for one activation row (Q6_K:
+    // 2, its wider raw chunks would otherwise cost waves per SIMD), 2 for 2
+    // rows, 1 for 4 (more chunks or rows cost more in registers, and waves
+    // per SIMD, than the latency saves; timed on the config-1/4 steps).
     // Otherwise the persistent pipeline, with rows per lane group R as wide as
-    // the batch allows, or 1 when the wider tile would give fewer than 2048
-    // row blocks (more waves, shorter per-task chains).
+    // the batch allows, or narrower (1 for one activation row, half for more)
+    // when the wider tile would give fewer than 2048 row blocks (more waves,
+    // shorter per-task chains).
     auto count_rbs = [&](uint32_t rows) {
         uint64_t n = 0;
         for (int i = 0; i < nprob; i++) n += (probs[i].n + rows - 1) / rows;
@@ -165,9 +168,12 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     const uint32_t cpl = (nch + L - 1) >> lanes_log2;
     uint32_t R = rows_per_group(info, B);
     uint32_t oneshot = 0;
-    if (B == 1) {
-        if (cpl <= (info.q6k ? 2u : 4u) && count_rbs(64u >> lanes_log2) <= 16384) oneshot = cpl;
-        if (oneshot || count_rbs((64u >> lanes_log2) * R) < 2048) R = 1;
+    const uint32_t max_cpl = B == 1 ? (info.q6k ? 2u : 4u) : B == 2 ? 2u : B == 4 ? 1u : 0u;
+    if (cpl >= 1 && cpl <= max_cpl && count_rbs(64u >> lanes_log2) <= 16384) {
+        oneshot = cpl;
+        R = 1;
+    } else if (B == 1) {
+        if (count_rbs((64u >> lanes_log2) * R) < 2048) R = 1;
     } else if (R > 1 && count_rbs((64u >> lanes_log2) * R) < 2048) {
         R /= 2;  // the narrower tile instantiated beside each batch's default
     }

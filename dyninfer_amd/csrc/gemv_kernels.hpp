@@ -605,12 +605,13 @@ __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const uint8_t
     if (t < T) compute(ba, nblk, nc);  // odd task count: the last task is in ba
 }
 
-// Latency mode, one activation row: every wave owns at most one row block
-// (total row blocks <= waves launched), so there is no task loop.  A lane
-// issues the loads of all CPL of its chunks before the activations are
+// Latency mode: every wave owns at most one row block of one row per lane
+// group (total row blocks <= waves launched), so there is no task loop.  A
+// lane issues the loads of all CPL of its chunks before the activations are
 // staged, so the whole launch waits on one memory latency; then it
-// multiplies them, the L lanes reduce, and lane 0 stores.
-template <class E, int CPL, class LOAD, class STAGE>
+// multiplies them for the B activation rows, the L lanes reduce, and lane 0
+// stores.
+template <class E, int CPL, int B, class LOAD, class STAGE>
 __device__ __forceinline__ void gemv_oneshot(const GemvParams& p, const uint8_t* lds, LOAD&& load, STAGE&& stage) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (uint32_t)(kGemvThreads / 64) + (threadIdx.x >> 6));
@@ -629,7 +630,9 @@ __device__ __forceinline__ void gemv_oneshot(const GemvParams& p, const uint8_t*
     }
     stage();
     if (!active) return;
-    float acc[1][1] = {{0.0f}};
+    float acc[1][B];
+#pragma unroll
+    for (int b = 0; b < B; b++) acc[0][b] = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPL; c++) {
         const uint32_t u0 = j + (uint32_t)c * L;
@@ -638,9 +641,9 @@ __device__ __forceinline__ void gemv_oneshot(const GemvParams& p, const uint8_t*
         typename E::Chunk ch[1];
         ch[0] = E::unpack(buf[c], u);
         E::zero_if(ch[0], past);
-        chunk_dot<E, 1, 1>(ch, lds, nch, u, acc);
+        chunk_dot<E, 1, B>(ch, lds, nch, u, acc);
     }
-    reduce_store<1, 1>(acc, blk, blk.base + g, j, L, p);
+    reduce_store<1, B>(acc, blk, blk.base + g, j, L, p);
 }
 
 // ---------------------------------------------------------------- GGUF
@@ -654,12 +657,12 @@ __global__ __launch_bounds__(kGemvThreads) void gguf_gemv_kernel(const GemvParam
     gemv_pipeline<E, R, B>(p, xlds, load, [&] { stage_x_auto<E, B, XBF16>(xlds, p); });
 }
 
-template <class E, int CPL, bool XBF16>
+template <class E, int CPL, int B, bool XBF16>
 __global__ __launch_bounds__(kGemvThreads) void gguf_gemv_oneshot_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
     const uint32_t rowbytes = (p.K / (uint32_t)E::QK) * (uint32_t)E::BB;
     auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) { return E::load(rb.w, row * rowbytes, u); };
-    gemv_oneshot<E, CPL>(p, xlds, load, [&] { stage_x_auto<E, 1, XBF16>(xlds, p); });
+    gemv_oneshot<E, CPL, B>(p, xlds, load, [&] { stage_x_auto<E, B, XBF16>(xlds, p); });
 }
 
 // ---------------------------------------------------------------- MLX affine U4
@@ -696,10 +699,10 @@ __global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_kernel(const GemvPar
     gemv_pipeline<EncMlxU4, R, B>(p, xlds, MlxLoad(p), [&] { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p); });
 }
 
-template <int CPL, bool XBF16>
+template <int CPL, int B, bool XBF16>
 __global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_oneshot_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
-    gemv_oneshot<EncMlxU4, CPL>(p, xlds, MlxLoad(p), [&] { stage_x_auto<EncMlxU4, 1, XBF16>(xlds, p); });
+    gemv_oneshot<EncMlxU4, CPL, B>(p, xlds, MlxLoad(p), [&] { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p); });
 }
 
 // Rows per lane group for a register batch B: more rows amortise each
@@ -762,7 +765,7 @@ hipError_t launch_oneshot(KERNEL kernel, const GemvParams& p, size_t lds, hipStr
 
 // Instantiates and launches the GEMV kernel of encoding E for a power-of-two
 // register batch B (the host has checked that its activation tile fits LDS);
-// oneshot = chunks per lane (1..4) selects the latency-mode kernel.
+// oneshot = chunks per lane selects the latency-mode kernel.
 // GGUF decode takes f32 activations, the reference's precision contract for
 // quantized linears (crates/dyninfer-compiler/src/lib.rs:289-306); bf16
 // activations reach GGUF weights only through the Q4_0 MFMA path.
@@ -772,18 +775,24 @@ hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t R, uint32_
     if (xbf16) return hipErrorInvalidValue;
     const size_t lds = (size_t)xtile_bytes(E::ENC, B, p.K);
     if (oneshot) {
-        if (B != 1 || R != 1) return hipErrorInvalidValue;
-        switch (oneshot) {
-        case 1: return launch_oneshot(gguf_gemv_oneshot_kernel<E, 1, false>, p, lds, st);
-        case 2: return launch_oneshot(gguf_gemv_oneshot_kernel<E, 2, false>, p, lds, st);
-        case 3:
-            if constexpr (E::ENC != ENC_Q6_K) return launch_oneshot(gguf_gemv_oneshot_kernel<E, 3, false>, p, lds, st);
-            return hipErrorInvalidValue;
-        case 4:
-            if constexpr (E::ENC != ENC_Q6_K) return launch_oneshot(gguf_gemv_oneshot_kernel<E, 4, false>, p, lds, st);
-            return hipErrorInvalidValue;
-        default: return hipErrorInvalidValue;
+        // chunks per lane (the host's limits): 1..4 for one activation row
+        // (Q6_K 1..2), 1..2 for 2 rows, 1 for 4
+        if (R != 1) return hipErrorInvalidValue;
+#define DMX_ONESHOT(b, c)                                                                             \
+    if (B == b && oneshot == c) return launch_oneshot(gguf_gemv_oneshot_kernel<E, c, b, false>, p, lds, st);
+        DMX_ONESHOT(1, 1)
+        DMX_ONESHOT(1, 2)
+        if constexpr (E::ENC != ENC_Q6_K) {
+            DMX_ONESHOT(1, 3)
+            DMX_ONESHOT(1, 4)
         }
+        if constexpr (max_register_batch(E::ENC) >= 2) {
+            DMX_ONESHOT(2, 1)
+            DMX_ONESHOT(2, 2)
+        }
+        if constexpr (max_register_batch(E::ENC) >= 4) DMX_ONESHOT(4, 1)
+#undef DMX_ONESHOT
+        return hipErrorInvalidValue;
     }
     if (B == 1 && R == 1) return launch_persistent(gguf_gemv_kernel<E, 1, 1, false>, p, lds, st);
 #define DMX_CASE(b)                                                                                       \

@@ -6,19 +6,20 @@ hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t R, uint3
     using E = EncMlxU4;
     const size_t lds = (size_t)xtile_bytes(E::ENC, B, p.K);
     if (oneshot) {
-        if (B != 1 || R != 1) return hipErrorInvalidValue;
-#define DMX_ONESHOT(c)                                                                               \
-    case c:                                                                                          \
-        return xbf16 ? launch_oneshot(mlx_u4_gemv_oneshot_kernel<c, true>, p, lds, st)                \
-                     : launch_oneshot(mlx_u4_gemv_oneshot_kernel<c, false>, p, lds, st);
-        switch (oneshot) {
-            DMX_ONESHOT(1)
-            DMX_ONESHOT(2)
-            DMX_ONESHOT(3)
-            DMX_ONESHOT(4)
-        default: return hipErrorInvalidValue;
-        }
+        if (R != 1) return hipErrorInvalidValue;
+#define DMX_ONESHOT(b, c)                                                                                 \
+    if (B == b && oneshot == c)                                                                           \
+        return xbf16 ? launch_oneshot(mlx_u4_gemv_oneshot_kernel<c, b, true>, p, lds, st)                \
+                     : launch_oneshot(mlx_u4_gemv_oneshot_kernel<c, b, false>, p, lds, st);
+        DMX_ONESHOT(1, 1)
+        DMX_ONESHOT(1, 2)
+        DMX_ONESHOT(1, 3)
+        DMX_ONESHOT(1, 4)
+        DMX_ONESHOT(2, 1)
+        DMX_ONESHOT(2, 2)
+        DMX_ONESHOT(4, 1)
 #undef DMX_ONESHOT
+        return hipErrorInvalidValue;
     }
     if (B == 1 && R == 1)
         return xbf16 ? launch_persistent(mlx_u4_gemv_kernel<1, 1, true>, p, lds, st)
