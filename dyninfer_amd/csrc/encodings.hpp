@@ -27,8 +27,12 @@
 //
 // Layout contract with the activation staging (gemv_kernels.hpp): for code
 // dword t of a chunk the lane reads PPT f16 pairs, pair h holding activations
-// xoff(t, h, 0) and xoff(t, h, 1) (offsets within the chunk's activation runs),
-// divided by 16 when dv(t, h), accumulated into group grp(t, h).
+// xoff(t, h, 0) and xoff(t, h, 1) (offsets from the chunk's first activation
+// xbase(u)), divided by 16 when dv(t, h), accumulated into group grp(t, h).
+// Those 2·PPT activations are exactly NXR runs of 4 consecutive ones, run r
+// starting at xrun0(r) + TSTRIDE·t, and xoff(t, h, e) = xoff(0, h, e) +
+// TSTRIDE·t, so one thread per code dword stages its pairs from NXR aligned
+// 4-element loads (checked at compile time by xruns_ok).
 #pragma once
 #include "device_common.hpp"
 #include "kernels.hpp"
@@ -119,6 +123,8 @@ struct EncQ40 {
     static constexpr int xoff(int t, int h, int e) { return 4 * t + (h >> 1) + 2 * e + 16 * (h & 1); }
     static constexpr bool dv(int, int h) { return (h & 1) != 0; }
     static constexpr int grp(int, int) { return 0; }
+    static constexpr int TSTRIDE = 4, NXR = 2;  // activations 4t..4t+3 and 16+4t..16+4t+3
+    static constexpr int xrun0(int r) { return 16 * r; }
     using Raw = RawBlock<NDW>;
     struct Chunk { uint32_t q[NT]; float d; };
     __device__ __forceinline__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u) {
@@ -151,6 +157,8 @@ struct EncQ41 {
     static constexpr int xoff(int t, int h, int e) { return EncQ40::xoff(t, h, e); }
     static constexpr bool dv(int t, int h) { return EncQ40::dv(t, h); }
     static constexpr int grp(int, int) { return 0; }
+    static constexpr int TSTRIDE = EncQ40::TSTRIDE, NXR = EncQ40::NXR;
+    static constexpr int xrun0(int r) { return EncQ40::xrun0(r); }
     struct Raw { uint32_t d[NDW]; };
     struct Chunk { uint32_t q[NT]; float d, m; };
     __device__ __forceinline__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u) {
@@ -188,6 +196,8 @@ struct EncQ80 {
     static constexpr int xoff(int t, int h, int e) { return 4 * t + h + 2 * e; }
     static constexpr bool dv(int, int) { return false; }
     static constexpr int grp(int, int) { return 0; }
+    static constexpr int TSTRIDE = 4, NXR = 1;  // activations 4t..4t+3
+    static constexpr int xrun0(int) { return 0; }
     using Raw = RawBlock<NDW>;
     struct Chunk { uint32_t q[NT]; float d; };
     __device__ __forceinline__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u) {
@@ -236,6 +246,8 @@ struct EncQ6K {
     static constexpr int xoff(int t, int h, int e) { return 32 * (h & 3) + 4 * t + (h >> 2) + 2 * e; }
     static constexpr bool dv(int, int h) { return (h & 3) >= 2; }
     static constexpr int grp(int, int h) { return h & 3; }
+    static constexpr int TSTRIDE = 4, NXR = 4;  // activations 32r+4t..32r+4t+3, run r = group r
+    static constexpr int xrun0(int r) { return 32 * r; }
     struct Raw { uint32_t a[5], b[5], h[5], s[5]; uint32_t sh; };
     struct Chunk { uint32_t a[NT], b[NT], h[NT]; float dsc[NG]; };
     __device__ __forceinline__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u) {
@@ -315,6 +327,8 @@ struct EncMlxU4 {
     static constexpr int xoff(int t, int h, int e) { return 8 * t + 2 * (h >> 1) + (h & 1) + 4 * e; }
     static constexpr bool dv(int, int h) { return (h & 1) != 0; }
     static constexpr int grp(int, int) { return 0; }
+    static constexpr int TSTRIDE = 8, NXR = 2;  // activations 8t..8t+7
+    static constexpr int xrun0(int r) { return 4 * r; }
     // packed words plus the scale/bias bit patterns (f32, or f16/bf16 in the
     // low half) and their dtype
     struct Raw { uint32_t w[4]; uint32_t s, b, kind; };
@@ -349,5 +363,32 @@ struct EncMlxU4 {
         c.b = z ? 0.0f : c.b;
     }
 };
+
+// The run description of an encoding matches its xoff(): run and position of
+// activation (h, e) of code dword 0, -1 if no run holds it.
+template <class E>
+constexpr int xrun_of(int h, int e) {
+    for (int r = 0; r < E::NXR; r++)
+        if (E::xoff(0, h, e) >= E::xrun0(r) && E::xoff(0, h, e) < E::xrun0(r) + 4) return r;
+    return -1;
+}
+template <class E>
+constexpr bool xruns_ok() {
+    int seen[64] = {};
+    for (int t = 0; t < E::NT; t++)
+        for (int h = 0; h < E::PPT; h++)
+            for (int e = 0; e < 2; e++) {
+                if (E::xoff(t, h, e) != E::xoff(0, h, e) + E::TSTRIDE * t) return false;
+                const int r = xrun_of<E>(h, e);
+                if (r < 0) return false;
+                seen[4 * r + E::xoff(0, h, e) - E::xrun0(r)]++;
+            }
+    for (int i = 0; i < 4 * E::NXR; i++)
+        if (seen[i] != E::NT) return false;  // every run element is one activation of each dword
+    return 4 * E::NXR == 2 * E::PPT;
+}
+static_assert(xruns_ok<EncQ40>() && xruns_ok<EncQ41>() && xruns_ok<EncQ80>() && xruns_ok<EncQ6K>() &&
+                  xruns_ok<EncMlxU4>(),
+              "activation runs disagree with xoff()");
 
 }  // namespace dmx

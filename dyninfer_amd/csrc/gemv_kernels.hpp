@@ -20,8 +20,9 @@
 //   * the grid is persistent (occupancy x CUs workgroups): wave w walks row
 //     blocks w, w+W, ... and the lane's (row block, chunk) tasks run as one
 //     software pipeline — the next task's weight bytes are loaded before the
-//     current task is computed, and the first task's before the activation
-//     staging, so HBM latency overlaps staging and arithmetic;
+//     current task is computed, and the first task's right after the
+//     activation loads (before the staging arithmetic), so HBM latency
+//     overlaps staging and arithmetic;
 //   * per weight: half a v_and_or_b32 and half a v_dot2_f32_f16 per
 //     activation row; per group and row: two or three f32 ops;
 //   * at the end of a row block the L lanes combine their R·B partial sums
@@ -71,240 +72,205 @@ struct XTile {
     static_assert(chunk_bytes == xtile_chunk_bytes(E::ENC), "host/device activation tile layouts differ");
 };
 
-// f32 [n] of activation row b at element k (f32 or bf16 source), 16-byte loads.
-template <bool XBF16, int N>
-__device__ __forceinline__ void load_xrun(const void* __restrict__ x, size_t off, float (&v)[N]) {
-    typedef float f32x4 __attribute__((ext_vector_type(4)));
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Activations off..off+3 of the source as f32 (f32 or bf16 source).  off is a
+// multiple of 4 and rows start 16-byte aligned, so this is one aligned 16-byte
+// (f32) or 8-byte (bf16) load.
+template <bool XBF16>
+__device__ __forceinline__ void load_x4(const void* __restrict__ x, uint32_t off, float (&v)[4]) {
     if constexpr (XBF16) {
-        static_assert(N % 8 == 0, "bf16 runs are read 8 at a time");
-        const uint16_t* xp = static_cast<const uint16_t*>(x) + off;
-#pragma unroll
-        for (int i = 0; i < N; i += 8) {
-            const u32x4 q = *gptr<u32x4>(xp + i);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                v[i + 2 * j] = __uint_as_float(q[j] << 16);
-                v[i + 2 * j + 1] = __uint_as_float(q[j] & 0xFFFF0000u);
-            }
-        }
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 q = *gptr<u32x2>(static_cast<const uint16_t*>(x) + off);
+        v[0] = __uint_as_float(q[0] << 16);
+        v[1] = __uint_as_float(q[0] & 0xFFFF0000u);
+        v[2] = __uint_as_float(q[1] << 16);
+        v[3] = __uint_as_float(q[1] & 0xFFFF0000u);
     } else {
-        static_assert(N % 4 == 0, "f32 runs are read 4 at a time");
-        const float* xp = static_cast<const float*>(x) + off;
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const f32x4 q = *gptr<f32x4>(static_cast<const float*>(x) + off);
 #pragma unroll
-        for (int i = 0; i < N; i += 4) {
-            const f32x4 q = *gptr<f32x4>(xp + i);
-#pragma unroll
-            for (int j = 0; j < 4; j++) v[i + j] = q[j];
-        }
+        for (int i = 0; i < 4; i++) v[i] = q[i];
     }
 }
 
-// Stages activation rows [0, batch) (rows up to B zero-filled) into the tile.
-// One thread per (row, chunk): it reads the chunk's activations, picks each
-// scale group's power of two s = 2^(e-14) from the group's largest magnitude
-// (frexp exponent e, so |x|/s < 2^14), writes the f16 pairs in decode order
-// (pairs meeting x16 codes divided by 16), and the group constants
-// -C = -Σ coef·v and s·Σx over the stored values v.  All threads of the
-// workgroup take part; ends with a barrier.
-template <class E, int B, bool XBF16>
-__device__ __forceinline__ void stage_x(uint8_t* lds, const void* __restrict__ x, uint32_t K, uint32_t ldx,
-                                        uint32_t batch) {
-    using XT = XTile<E>;
-    const uint32_t nch = K / (uint32_t)E::CW;
-    uint32_t* xp = reinterpret_cast<uint32_t*>(lds);
-    float* xc = reinterpret_cast<float*>(lds + (size_t)B * nch * XT::XPW * 4u);
-    for (uint32_t item = threadIdx.x; item < (uint32_t)B * nch; item += (uint32_t)kGemvThreads) {
-        const uint32_t b = item / nch, u = item - b * nch;
-        float v[E::NRUN][E::RUNLEN];
-        if (b < batch) {
-#pragma unroll
-            for (int r = 0; r < E::NRUN; r++)
-                load_xrun<XBF16>(x, (size_t)b * ldx + E::xbase(u) + (uint32_t)(r * E::RUNSTRIDE), v[r]);
-        } else {
-#pragma unroll
-            for (int r = 0; r < E::NRUN; r++)
-#pragma unroll
-                for (int i = 0; i < E::RUNLEN; i++) v[r][i] = 0.0f;
-        }
-        auto val = [&](int t, int h, int e) -> float {
-            const int o = E::xoff(t, h, e);
-            const int r = E::NRUN > 1 ? o / (E::NRUN > 1 ? E::RUNSTRIDE : 1) : 0;
-            return v[r][o - r * E::RUNSTRIDE];
-        };
-        int ex[E::NG];
-#pragma unroll
-        for (int g = 0; g < E::NG; g++) {
-            float m = 0.0f;
-#pragma unroll
-            for (int t = 0; t < E::NT; t++)
-#pragma unroll
-                for (int h = 0; h < E::PPT; h++)
-                    if (E::grp(t, h) == g) m = fmaxf(m, fmaxf(fabsf(val(t, h, 0)), fabsf(val(t, h, 1))));
-            int e = 0;
-            (void)frexpf(m, &e);
-            ex[g] = e < -110 ? -110 : e;  // keeps s = 2^(e-14) a normal f32
-        }
-        float C[E::NG], S[E::NG];
-#pragma unroll
-        for (int g = 0; g < E::NG; g++) C[g] = S[g] = 0.0f;
-        uint32_t pr[E::NT * E::PPT];
-#pragma unroll
-        for (int t = 0; t < E::NT; t++)
-#pragma unroll
-            for (int h = 0; h < E::PPT; h++) {
-                const int g = E::grp(t, h);
-                const bool dv = E::dv(t, h);
-                _Float16 lo = (_Float16)ldexpf(val(t, h, 0), 14 - ex[g]);
-                _Float16 hi = (_Float16)ldexpf(val(t, h, 1), 14 - ex[g]);
-                if (dv) {
-                    lo = lo * (_Float16)0.0625f;
-                    hi = hi * (_Float16)0.0625f;
-                }
-                pr[t * E::PPT + h] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
-                                     ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-                const float fl = (float)lo, fh = (float)hi;
-                C[g] = fmaf(E::coef(dv), fh, fmaf(E::coef(dv), fl, C[g]));
-                S[g] = fmaf(dv ? 16.0f : 1.0f, fh, fmaf(dv ? 16.0f : 1.0f, fl, S[g]));
-            }
-        uint4* dst = reinterpret_cast<uint4*>(xp + (size_t)item * XT::XPW);
-#pragma unroll
-        for (int i = 0; i < E::NT * E::PPT; i += 4) dst[i / 4] = make_uint4(pr[i], pr[i + 1], pr[i + 2], pr[i + 3]);
-#pragma unroll
-        for (int g = 0; g < E::NG; g++) {
-            const float s = ldexpf(1.0f, ex[g] - 14);
-            float* c = xc + ((size_t)item * E::NG + g) * XT::NCF;
-            if constexpr (XT::NCF == 4) {
-                *reinterpret_cast<float4*>(c) = make_float4(-C[g], s, s * S[g], 0.0f);
-            } else {
-                *reinterpret_cast<float2*>(c) = make_float2(-C[g], s);
-            }
-        }
-    }
-    __syncthreads();
-}
-
-// Reduction over the GP (8 or 16) adjacent lanes of a scale group, all lanes
-// receiving the result: xor-1, xor-2 quad permutes, then the half-row and row
-// mirrors (each lane meets the other half of its 8, then of its 16).
-template <int GP, bool MAX>
-__device__ __forceinline__ float group_reduce(float v) {
-    static_assert(GP == 8 || GP == 16, "scale groups span 8 or 16 lanes");
-#define DMX_STEP(ctrl)                                                                                 \
-    {                                                                                                  \
-        const float o = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false)); \
-        v = MAX ? fmaxf(v, o) : v + o;                                                                 \
-    }
-    DMX_STEP(0xB1)   // quad_perm [1,0,3,2]
-    DMX_STEP(0x4E)   // quad_perm [2,3,0,1]
-    DMX_STEP(0x141)  // row_half_mirror
-    if constexpr (GP == 16) DMX_STEP(0x140)  // row_mirror
-#undef DMX_STEP
+// Reduction over the N (4 or 8) adjacent lanes of one chunk, every lane
+// receiving the result: xor-1 and xor-2 quad permutes, then for 8 lanes the
+// half-row mirror (each quad meets the other quad of its 8).  Every lane adds
+// the same operands (commuted), so all hold the same value.
+template <int N, class OP>
+__device__ __forceinline__ uint32_t lanes_reduce(uint32_t v, OP op) {
+    static_assert(N == 4 || N == 8, "a chunk's code dwords span 4 or 8 lanes");
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    if constexpr (N == 8) v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
     return v;
 }
 
-// Same tile as stage_x, staged with one thread per f16 pair (NT·PPT threads
-// per (row, chunk), PASSES rounds of the workgroup): for tiles of few chunks,
-// where one thread per chunk would leave most of the workgroup idle behind a
-// long serial chain.  A scale group's pairs sit on adjacent lanes inside one
-// DPP row, so its largest magnitude and its constants reduce across lanes.
-// The constants equal stage_x's up to the order of their f32 sums.
-template <class E, int B, bool XBF16, int PASSES>
-__device__ __forceinline__ void stage_x_pairs(uint8_t* lds, const void* __restrict__ x, uint32_t K, uint32_t ldx,
-                                              uint32_t batch) {
-    using XT = XTile<E>;
-    constexpr int NP = E::NT * E::PPT;  // pairs per chunk
-    constexpr int GP = NP / E::NG;      // pairs per scale group
-    const uint32_t nch = K / (uint32_t)E::CW;
+// max(|a|, |b|, |c|) as one v_max3_f32 with abs modifiers (the compiler's
+// fmaxf would first canonicalise each loaded value).  A NaN operand can only
+// change the scale exponent it feeds.
+__device__ __forceinline__ float absmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, |%1|, |%2|, |%3|" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// One staging thread's share: code dword t = idx % NT of (activation row,
+// chunk) item = idx / NT; its NXR runs of 4 activations.
+template <class E>
+struct XStage {
+    float v[E::NXR][4];
+    uint32_t item;
+    bool live;  // item < B·nch: the thread stores
+};
+
+// Issues the loads of staging thread idx (no use of the loaded values, so
+// loads issued after it are not waited for).
+template <class E, int B, bool XBF16>
+__device__ __forceinline__ void xstage_load(const GemvParams& p, uint32_t nch, uint32_t idx, XStage<E>& s) {
     const uint32_t items = (uint32_t)B * nch;
+    const uint32_t it = idx / (uint32_t)E::NT, t = idx % (uint32_t)E::NT;
+    s.live = it < items;
+    s.item = s.live ? it : items - 1u;  // spare threads redo the last chunk, unstored
+    const uint32_t b = B == 1 ? 0u : s.item / nch, u = s.item - b * nch;
+    // Rows past the batch restage row 0: in bounds, and their sums are never
+    // stored.  Activation offsets are 32-bit (the activations are < 4 GiB).
+    const uint32_t base = (b < p.batch ? b : 0u) * p.ldx + E::xbase(u) + (uint32_t)E::TSTRIDE * t;
+#pragma unroll
+    for (int r = 0; r < E::NXR; r++) load_x4<XBF16>(p.x, base + (uint32_t)E::xrun0(r), s.v[r]);
+}
+
+// The rest of staging thread (t, s.item): picks each scale group's power of
+// two s = 2^(e-14) from the group's largest magnitude over the chunk (frexp
+// exponent e, so |x|/s < 2^14), writes the dword's PPT f16 pairs in decode
+// order (one RNE rounding of x/s, or of x/(16s) for pairs meeting x16 codes)
+// and, from lane t = 0, the group constants -C = -Σ coef·v and s·Σx over the
+// stored values v (their f32 sums reduced across the chunk's NT lanes).
+template <class E, int B>
+__device__ __forceinline__ void xstage_store(uint8_t* lds, uint32_t nch, uint32_t t, const XStage<E>& s) {
+    using XT = XTile<E>;
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
     uint32_t* xp = reinterpret_cast<uint32_t*>(lds);
     float* xc = reinterpret_cast<float*>(lds + (size_t)B * nch * XT::XPW * 4u);
-    // Pair (t, h) of lane j: the GP pairs of scale group g = j / GP.
-    const uint32_t j = threadIdx.x % (uint32_t)NP;  // the workgroup size is a multiple of NP
-    const uint32_t g = j / (uint32_t)GP, k = j % (uint32_t)GP;
-    uint32_t t, h;
-    if constexpr (E::NG == 1) {
-        t = j / (uint32_t)E::PPT;
-        h = j % (uint32_t)E::PPT;
-    } else {
-        static_assert(E::NG == 4 && E::NT == 4 && E::PPT == 8, "Q6_K groups: h in {g, g + 4}, t = 0..3");
-        t = k >> 1;
-        h = g + 4u * (k & 1u);
-    }
-    const uint32_t o0 = (uint32_t)E::xoff((int)t, (int)h, 0), o1 = (uint32_t)E::xoff((int)t, (int)h, 1);
-    const bool dv = E::dv((int)t, (int)h);
-    // All rounds' activations are loaded before any is used, so the rounds
-    // share one memory latency.
-    uint32_t item[PASSES];
-    bool live[PASSES];
-    float v0[PASSES], v1[PASSES];
+    auto val = [&](int h, int e) -> float {
+        const int r = xrun_of<E>(h, e);
+        return s.v[r][E::xoff(0, h, e) - E::xrun0(r)];
+    };
+    // each group's largest magnitude: its 2·PPT/NG activations folded three at
+    // a time (the running maximum is non-negative, so its abs is a no-op)
+    constexpr int NV = 2 * E::PPT / E::NG;
+    static_assert(NV >= 3, "a group holds at least 3 activations per dword");
+    uint32_t mx[E::NG];
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ps++) {
-        const uint32_t it = (threadIdx.x + (uint32_t)ps * (uint32_t)kGemvThreads) / (uint32_t)NP;
-        live[ps] = it < items;
-        item[ps] = live[ps] ? it : items - 1u;  // spare lanes redo the last chunk, unstored
-        const uint32_t b = B == 1 ? 0u : item[ps] / nch, u = item[ps] - b * nch;
-        const uint32_t base = (b < batch ? b : 0u) * ldx + E::xbase(u);  // the activations are < 4 GiB
-        if constexpr (XBF16) {
-            const uint16_t* xs = static_cast<const uint16_t*>(x);
-            v0[ps] = __uint_as_float((uint32_t)*gptr<uint16_t>(xs + (base + o0)) << 16);
-            v1[ps] = __uint_as_float((uint32_t)*gptr<uint16_t>(xs + (base + o1)) << 16);
-        } else {
-            const float* xs = static_cast<const float*>(x);
-            v0[ps] = *gptr<float>(xs + (base + o0));
-            v1[ps] = *gptr<float>(xs + (base + o1));
-        }
-        if (b >= batch) v0[ps] = v1[ps] = 0.0f;  // rows past the batch stage as zeros
-    }
+    for (int g = 0; g < E::NG; g++) {
+        float a[NV];
+        int n = 0;
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ps++) {
-        const float m = group_reduce<GP, true>(fmaxf(fabsf(v0[ps]), fabsf(v1[ps])));
+        for (int h = 0; h < E::PPT; h++)
+            if (E::grp(0, h) == g) {
+                a[n++] = val(h, 0);
+                a[n++] = val(h, 1);
+            }
+        float m = absmax3(a[0], a[1], a[2]);
+#pragma unroll
+        for (int i = 3; i < NV; i += 2) m = absmax3(m, a[i], a[i + 1 < NV ? i + 1 : i]);
+        mx[g] = __float_as_uint(m);  // non-negative floats order as integers
+    }
+    int ex[E::NG];
+#pragma unroll
+    for (int g = 0; g < E::NG; g++) {
+        mx[g] = lanes_reduce<E::NT>(mx[g], [](uint32_t a, uint32_t b) { return a > b ? a : b; });
         int e = 0;
-        (void)frexpf(m, &e);
-        e = e < -110 ? -110 : e;  // keeps s = 2^(e-14) a normal f32
-        _Float16 lo = (_Float16)ldexpf(v0[ps], 14 - e);
-        _Float16 hi = (_Float16)ldexpf(v1[ps], 14 - e);
-        if (dv) {
-            lo = lo * (_Float16)0.0625f;
-            hi = hi * (_Float16)0.0625f;
+        (void)frexpf(__uint_as_float(mx[g]), &e);
+        ex[g] = e < -110 ? -110 : e;  // keeps s = 2^(e-14) a normal f32
+    }
+    uint32_t pr[E::PPT];
+    float C[E::NG], S[E::NG];
+#pragma unroll
+    for (int g = 0; g < E::NG; g++) C[g] = S[g] = 0.0f;
+#pragma unroll
+    for (int h = 0; h < E::PPT; h++) {
+        const int g = E::grp(0, h);
+        const bool dv = E::dv(0, h);
+        const int sh = (dv ? 10 : 14) - ex[g];
+        const f32x2 f = {ldexpf(val(h, 0), sh), ldexpf(val(h, 1), sh)};
+        pr[h] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));  // v_cvt_pk_f16_f32 (RNE)
+        const uint32_t cf = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)E::coef(dv)) * 0x00010001u;
+        C[g] = dot2(pr[h], cf, C[g]);
+        if constexpr (XT::NCF == 4) S[g] = dot2(pr[h], dv ? 0x4C004C00u : 0x3C003C00u, S[g]);  // (16, 16) or (1, 1)
+    }
+    auto fadd = [](uint32_t a, uint32_t b) { return __float_as_uint(__uint_as_float(a) + __uint_as_float(b)); };
+#pragma unroll
+    for (int g = 0; g < E::NG; g++) {
+        C[g] = __uint_as_float(lanes_reduce<E::NT>(__float_as_uint(C[g]), fadd));
+        if constexpr (XT::NCF == 4) S[g] = __uint_as_float(lanes_reduce<E::NT>(__float_as_uint(S[g]), fadd));
+    }
+    if (s.live) {
+        uint32_t* dst = xp + (size_t)s.item * XT::XPW + t * (uint32_t)E::PPT;
+        if constexpr (E::PPT % 4 == 0) {
+#pragma unroll
+            for (int h = 0; h < E::PPT; h += 4)
+                *reinterpret_cast<uint4*>(dst + h) = make_uint4(pr[h], pr[h + 1], pr[h + 2], pr[h + 3]);
+        } else {
+            static_assert(E::PPT == 2, "pairs per code dword: 2, 4 or 8");
+            *reinterpret_cast<uint2*>(dst) = make_uint2(pr[0], pr[1]);
         }
-        const float fl = (float)lo, fh = (float)hi;
-        const float coef = dv ? E::coef(true) : E::coef(false);
-        const float C = group_reduce<GP, false>(fmaf(coef, fh, coef * fl));
-        const float S = group_reduce<GP, false>(dv ? 16.0f * (fl + fh) : fl + fh);
-        if (live[ps]) {
-            xp[(size_t)item[ps] * XT::XPW + t * (uint32_t)E::PPT + h] =
-                (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-            if (k == 0) {
-                const float s = ldexpf(1.0f, e - 14);
-                float* c = xc + ((size_t)item[ps] * E::NG + g) * XT::NCF;
+        if (t == 0) {
+#pragma unroll
+            for (int g = 0; g < E::NG; g++) {
+                const float sc = ldexpf(1.0f, ex[g] - 14);
+                float* c = xc + ((size_t)s.item * E::NG + g) * XT::NCF;
                 if constexpr (XT::NCF == 4) {
-                    *reinterpret_cast<float4*>(c) = make_float4(-C, s, s * S, 0.0f);
+                    *reinterpret_cast<float4*>(c) = make_float4(-C[g], sc, sc * S[g], 0.0f);
                 } else {
-                    *reinterpret_cast<float2*>(c) = make_float2(-C, s);
+                    *reinterpret_cast<float2*>(c) = make_float2(-C[g], sc);
                 }
             }
         }
     }
+}
+
+// Stages activation rows [0, batch) into the tile (rows up to B restage row 0),
+// one thread per code dword: B·nch·NT staging threads, P per workgroup thread
+// per round.  The first round's activation loads are issued, then mid() (the
+// caller's first weight loads), then the first round is computed: loads
+// return in issue order, so the activations arrive ahead of the weights and
+// the staging arithmetic runs while the weights are in flight.  Later rounds
+// (large batches) load after the weights.  Ends with a barrier.
+template <class E, int B, bool XBF16, int P, class MID>
+__device__ __forceinline__ void stage_x_rounds(uint8_t* lds, const GemvParams& p, MID&& mid) {
+    const uint32_t nch = p.K / (uint32_t)E::CW;
+    const uint32_t total = (uint32_t)B * nch * (uint32_t)E::NT;
+    const uint32_t t = threadIdx.x % (uint32_t)E::NT;  // the workgroup size is a multiple of NT
+    XStage<E> s[P];
+#pragma unroll
+    for (int ps = 0; ps < P; ps++) xstage_load<E, B, XBF16>(p, nch, threadIdx.x + (uint32_t)ps * kGemvThreads, s[ps]);
+    __builtin_amdgcn_sched_barrier(0);
+    mid();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ps = 0; ps < P; ps++) xstage_store<E, B>(lds, nch, t, s[ps]);
+    for (uint32_t base = (uint32_t)P * kGemvThreads; base < total; base += (uint32_t)P * kGemvThreads) {
+#pragma unroll
+        for (int ps = 0; ps < P; ps++)
+            xstage_load<E, B, XBF16>(p, nch, base + threadIdx.x + (uint32_t)ps * kGemvThreads, s[ps]);
+#pragma unroll
+        for (int ps = 0; ps < P; ps++) xstage_store<E, B>(lds, nch, t, s[ps]);
+    }
     __syncthreads();
 }
 
-// Stages the activation tile.  When every wave of the grid has at most one
-// row block the launch is latency-bound and the tile is staged one thread per
-// pair (up to four rounds of the workgroup); otherwise the weight stream is
-// long and the one-thread-per-chunk stager, which spends a fraction of the
-// instructions, is used.
-template <class E, int B, bool XBF16>
-__device__ __forceinline__ void stage_x_auto(uint8_t* lds, const GemvParams& p) {
-    const void* x = p.x;
-    const uint32_t K = p.K, ldx = p.ldx, batch = p.batch;
-    const uint32_t pairs = (uint32_t)B * (K / (uint32_t)E::CW) * (uint32_t)(E::NT * E::PPT);
-    const bool latency_bound = p.total_rb <= p.grid * (uint32_t)(kGemvThreads / 64);
-    if (!latency_bound) stage_x<E, B, XBF16>(lds, x, K, ldx, batch);
-    else if (pairs <= 1u * kGemvThreads) stage_x_pairs<E, B, XBF16, 1>(lds, x, K, ldx, batch);
-    else if (pairs <= 2u * kGemvThreads) stage_x_pairs<E, B, XBF16, 2>(lds, x, K, ldx, batch);
-    else if (pairs <= 4u * kGemvThreads) stage_x_pairs<E, B, XBF16, 4>(lds, x, K, ldx, batch);
-    else stage_x<E, B, XBF16>(lds, x, K, ldx, batch);
+// Rounds of P passes, P the power of two covering the staging threads, at
+// most 16 activations (registers) per thread in flight: every variant is
+// compiled into the kernel, so the widest one sets its register count.
+template <class E, int B, bool XBF16, class MID>
+__device__ __forceinline__ void stage_x_auto(uint8_t* lds, const GemvParams& p, MID&& mid) {
+    constexpr int PMAX = 4 / E::NXR > 0 ? 4 / E::NXR : 1;
+    const uint32_t passes = ((uint32_t)B * (p.K / (uint32_t)E::CW) * (uint32_t)E::NT + kGemvThreads - 1u) / kGemvThreads;
+    if (PMAX == 1 || passes <= 1u) stage_x_rounds<E, B, XBF16, 1>(lds, p, mid);
+    else if constexpr (PMAX >= 2) {
+        if (PMAX == 2 || passes <= 2u) stage_x_rounds<E, B, XBF16, 2>(lds, p, mid);
+        else stage_x_rounds<E, B, XBF16, (PMAX >= 4 ? 4 : 2)>(lds, p, mid);
+    }
 }
 
 // ---------------------------------------------------------------- chunk dot product
@@ -517,8 +483,9 @@ __device__ __forceinline__ void reduce_store(float (&acc)[R][B], const RowBlock&
 // unconditional — a wave without row blocks loads the last row block's first
 // task, and at the end of the sequence the current task is loaded again — so
 // the compiler's wait counters can keep a lane's loads in flight across one
-// task of compute.  stage() stages the activations (with a barrier); it runs
-// after the first task's loads are issued, in every wave.
+// task of compute.  stage(mid) stages the activations (with a barrier) in
+// every wave and calls mid(), which issues the first task's loads, between
+// issuing the activation loads and using them.
 template <class E, int R, int B, class LOAD, class STAGE>
 __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const uint8_t* lds, LOAD&& load, STAGE&& stage) {
     const uint32_t lane = threadIdx.x & 63u;
@@ -582,8 +549,7 @@ __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const uint8_t
                 for (int b = 0; b < B; b++) acc[i][b] = 0.0f;
         }
     };
-    load_task(ba, nblk, nc);
-    stage();
+    stage([&] { load_task(ba, nblk, nc); });
     if (T == 0) return;
     uint32_t t = 0;
     for (; t + 2 <= T; t += 2) {
@@ -607,10 +573,10 @@ __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const uint8_t
 
 // Latency mode: every wave owns at most one row block of one row per lane
 // group (total row blocks <= waves launched), so there is no task loop.  A
-// lane issues the loads of all CPL of its chunks before the activations are
-// staged, so the whole launch waits on one memory latency; then it
-// multiplies them for the B activation rows, the L lanes reduce, and lane 0
-// stores.
+// lane issues the loads of all CPL of its chunks right after the activation
+// loads, the activations are staged while they are in flight, so the whole
+// launch waits on one memory latency; then it multiplies them for the B
+// activation rows, the L lanes reduce, and lane 0 stores.
 template <class E, int CPL, int B, class LOAD, class STAGE>
 __device__ __forceinline__ void gemv_oneshot(const GemvParams& p, const uint8_t* lds, LOAD&& load, STAGE&& stage) {
     const uint32_t lane = threadIdx.x & 63u;
@@ -623,12 +589,13 @@ __device__ __forceinline__ void gemv_oneshot(const GemvParams& p, const uint8_t*
     const RowBlock blk = row_block(p, active ? wid : p.total_rb - 1u, rows_per_rb);
     const uint32_t row = blk.base + g < blk.n ? blk.base + g : blk.n - 1u;
     typename E::Raw buf[CPL];
+    stage([&] {
 #pragma unroll
-    for (int c = 0; c < CPL; c++) {
-        const uint32_t u = j + (uint32_t)c * L;
-        buf[c] = load(blk, row, u < nch ? u : nch - 1u);
-    }
-    stage();
+        for (int c = 0; c < CPL; c++) {
+            const uint32_t u = j + (uint32_t)c * L;
+            buf[c] = load(blk, row, u < nch ? u : nch - 1u);
+        }
+    });
     if (!active) return;
     float acc[1][B];
 #pragma unroll
@@ -654,7 +621,7 @@ __global__ __launch_bounds__(kGemvThreads) void gguf_gemv_kernel(const GemvParam
     extern __shared__ __align__(16) uint8_t xlds[];
     const uint32_t rowbytes = (p.K / (uint32_t)E::QK) * (uint32_t)E::BB;
     auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) { return E::load(rb.w, row * rowbytes, u); };
-    gemv_pipeline<E, R, B>(p, xlds, load, [&] { stage_x_auto<E, B, XBF16>(xlds, p); });
+    gemv_pipeline<E, R, B>(p, xlds, load, [&](auto&& mid) { stage_x_auto<E, B, XBF16>(xlds, p, mid); });
 }
 
 template <class E, int CPL, int B, bool XBF16>
@@ -662,7 +629,7 @@ __global__ __launch_bounds__(kGemvThreads) void gguf_gemv_oneshot_kernel(const G
     extern __shared__ __align__(16) uint8_t xlds[];
     const uint32_t rowbytes = (p.K / (uint32_t)E::QK) * (uint32_t)E::BB;
     auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) { return E::load(rb.w, row * rowbytes, u); };
-    gemv_oneshot<E, CPL, B>(p, xlds, load, [&] { stage_x_auto<E, B, XBF16>(xlds, p); });
+    gemv_oneshot<E, CPL, B>(p, xlds, load, [&](auto&& mid) { stage_x_auto<E, B, XBF16>(xlds, p, mid); });
 }
 
 // ---------------------------------------------------------------- MLX affine U4
@@ -696,13 +663,13 @@ struct MlxLoad {
 template <int B, int R, bool XBF16>
 __global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
-    gemv_pipeline<EncMlxU4, R, B>(p, xlds, MlxLoad(p), [&] { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p); });
+    gemv_pipeline<EncMlxU4, R, B>(p, xlds, MlxLoad(p), [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p, mid); });
 }
 
 template <int CPL, int B, bool XBF16>
 __global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_oneshot_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
-    gemv_oneshot<EncMlxU4, CPL, B>(p, xlds, MlxLoad(p), [&] { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p); });
+    gemv_oneshot<EncMlxU4, CPL, B>(p, xlds, MlxLoad(p), [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p, mid); });
 }
 
 // Rows per lane group for a register batch B: more rows amortise each
