@@ -8,11 +8,11 @@
 
 namespace dmx {
 
-hipError_t gemv_launch_q4_0(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16, hipStream_t st);
-hipError_t gemv_launch_q4_1(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16, hipStream_t st);
-hipError_t gemv_launch_q8_0(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16, hipStream_t st);
-hipError_t gemv_launch_q6_k(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16, hipStream_t st);
-hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q4_0(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q4_1(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q8_0(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q6_k(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
 
 hipError_t cached_occupancy(const void* kernel, size_t lds, int threads, int* per_cu, int* cus) {
     struct Entry {
@@ -75,7 +75,7 @@ namespace {
 
 struct EncInfo {
     uint32_t chunk_weights;  // weights one lane handles per step
-    bool q6k;                // 64-weight Q6_K chunks hold fewer rows per lane
+    bool q6k;                // 64-weight Q6_K chunks: fewer chunks per lane in latency mode
 };
 
 bool enc_info(uint32_t enc, EncInfo& e) {
@@ -89,22 +89,13 @@ bool enc_info(uint32_t enc, EncInfo& e) {
     }
 }
 
-// Rows per lane group for register batch B; must match rows_per_group<E, B>()
-// in gemv_kernels.hpp.  Half of it (rows_per_group_narrow) is instantiated
-// beside it for B > 1, and a single row for B = 1.
-uint32_t rows_per_group(const EncInfo& e, uint32_t B) {
-    if (e.q6k) return B <= 2 ? 2 : 1;
-    return B <= 2 ? 4 : 2;
-}
-
-hipError_t launch(uint32_t enc, const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16,
-                  hipStream_t st) {
+hipError_t launch(uint32_t enc, const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st) {
     switch (enc) {
-    case ENC_Q4_0: return gemv_launch_q4_0(p, B, R, oneshot, xbf16, st);
-    case ENC_Q4_1: return gemv_launch_q4_1(p, B, R, oneshot, xbf16, st);
-    case ENC_Q8_0: return gemv_launch_q8_0(p, B, R, oneshot, xbf16, st);
-    case ENC_Q6_K: return gemv_launch_q6_k(p, B, R, oneshot, xbf16, st);
-    case ENC_MLX_U4: return gemv_launch_mlx_u4(p, B, R, oneshot, xbf16, st);
+    case ENC_Q4_0: return gemv_launch_q4_0(p, B, oneshot, xbf16, st);
+    case ENC_Q4_1: return gemv_launch_q4_1(p, B, oneshot, xbf16, st);
+    case ENC_Q8_0: return gemv_launch_q8_0(p, B, oneshot, xbf16, st);
+    case ENC_Q6_K: return gemv_launch_q6_k(p, B, oneshot, xbf16, st);
+    case ENC_MLX_U4: return gemv_launch_mlx_u4(p, B, oneshot, xbf16, st);
     default: return hipErrorInvalidValue;
     }
 }
@@ -153,34 +144,18 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     // Latency mode (one wave per row block of one row per lane group, all of
     // a lane's chunks loaded at once) when the matrices give at most 16384
     // such row blocks and a lane few chunks: 4 for one activation row (Q6_K:
-    // 2, its wider raw chunks would otherwise cost waves per SIMD), 2 for 2
-    // rows, 1 for 4 (more chunks or rows cost more in registers, and waves
-    // per SIMD, than the latency saves; timed on the config-1/4 steps).
-    // Otherwise the persistent pipeline, with rows per lane group R as wide as
-    // the batch allows, or narrower (1 for one activation row, half for more)
-    // when the wider tile would give fewer than 2048 row blocks (more waves,
-    // shorter per-task chains).
-    auto count_rbs = [&](uint32_t rows) {
-        uint64_t n = 0;
-        for (int i = 0; i < nprob; i++) n += (probs[i].n + rows - 1) / rows;
-        return n;
-    };
+    // 2; at 3 the 8B down_proj ran slower than the pipeline), 2 for 2 rows, 1
+    // for 4 (more chunks or rows cost more in registers, and waves per SIMD,
+    // than the latency saves; timed on the config-1/4 steps).  Otherwise the
+    // persistent pipeline, whose rows per lane group the encoding's launcher
+    // picks from the occupancy of each instantiated tile.
+    uint64_t rbs1 = 0;
+    for (int i = 0; i < nprob; i++) rbs1 += (probs[i].n + (64u >> lanes_log2) - 1) / (64u >> lanes_log2);
     const uint32_t cpl = (nch + L - 1) >> lanes_log2;
-    uint32_t R = rows_per_group(info, B);
-    uint32_t oneshot = 0;
     const uint32_t max_cpl = B == 1 ? (info.q6k ? 2u : 4u) : B == 2 ? 2u : B == 4 ? 1u : 0u;
-    if (cpl >= 1 && cpl <= max_cpl && count_rbs(64u >> lanes_log2) <= 16384) {
-        oneshot = cpl;
-        R = 1;
-    } else if (B == 1) {
-        if (count_rbs((64u >> lanes_log2) * R) < 2048) R = 1;
-    } else if (R > 1 && count_rbs((64u >> lanes_log2) * R) < 2048) {
-        R /= 2;  // the narrower tile instantiated beside each batch's default
-    }
-    const uint32_t rows_per_rb = (64u >> lanes_log2) * R;
+    const uint32_t oneshot = cpl >= 1 && cpl <= max_cpl && rbs1 <= 16384 ? cpl : 0u;
 
     GemvParams p = {};
-    uint32_t rbs = 0;
     for (int i = 0; i < kMaxProblems; i++) {
         const GemvProblem& q = probs[i < nprob ? i : nprob - 1];
         p.w[i] = q.w;
@@ -188,10 +163,7 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
         p.bi[i] = q.bi;
         p.y[i] = q.y;
         p.n[i] = i < nprob ? q.n : 0;
-        p.rb_begin[i] = rbs;
-        if (i < nprob) rbs += (q.n + rows_per_rb - 1) / rows_per_rb;
     }
-    p.total_rb = rbs;
     p.nprob = (uint32_t)nprob;
     p.x = x;
     p.K = K;
@@ -202,7 +174,7 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     p.y_bf16 = y_bf16 ? 1u : 0u;
     p.group = group;
     p.sdtype = sdtype;
-    return launch(enc, p, B, R, oneshot, x_bf16, stream);
+    return launch(enc, p, B, oneshot, x_bf16, stream);  // lays out the row blocks per tile
 }
 
 }  // namespace dmx

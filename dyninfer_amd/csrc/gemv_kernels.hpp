@@ -672,22 +672,13 @@ __global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_oneshot_kernel(const
     gemv_oneshot<EncMlxU4, CPL, B>(p, xlds, MlxLoad(p), [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p, mid); });
 }
 
-// Rows per lane group for a register batch B: more rows amortise each
-// activation read from LDS and the per-task overhead, fewer keep the
-// accumulators in registers.  (With one activation row the host may pick a
-// single row per group instead, for matrices too small to fill the GPU.)
+// Widest rows per lane group instantiated for a register batch B: more rows
+// amortise each activation read from LDS and the per-task overhead, fewer
+// keep the accumulators in registers (gemv_tiles adds the narrower tiles).
 template <class E, int B>
 constexpr int rows_per_group() {
     if constexpr (E::ENC == ENC_Q6_K) return B <= 2 ? 2 : 1;
     else return B <= 2 ? 4 : 2;
-}
-
-// The narrower tile instantiated beside it for activation rows > 1, taken by
-// the host when the wider one would leave too few row blocks for the GPU
-// (halving the rows gives twice the waves at fewer registers each).
-template <class E, int B>
-constexpr int rows_per_group_narrow() {
-    return rows_per_group<E, B>() > 1 ? rows_per_group<E, B>() / 2 : 1;
 }
 
 // Resident workgroups per CU for (kernel, dynamic LDS) on the current device
@@ -695,56 +686,98 @@ constexpr int rows_per_group_narrow() {
 // Also raises the kernel's dynamic-LDS limit when lds needs it.
 hipError_t cached_occupancy(const void* kernel, size_t lds, int threads, int* per_cu, int* cus);
 
-// Launch of one kernel instantiation with a persistent grid: as many waves as
-// fit on the device at once (capped by the row-block count).  Fewer waves
-// would even out the row blocks per wave, but cost more in memory-level
-// parallelism than the tail they save.
-template <class KERNEL>
-hipError_t launch_persistent(KERNEL kernel, const GemvParams& p, size_t lds, hipStream_t st) {
-    int cus = 0, per_cu = 0;
-    hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, kGemvThreads, &per_cu, &cus);
-    if (e != hipSuccess) return e;
-    if (per_cu < 1) return hipErrorInvalidConfiguration;
+// Row blocks of rows_per_rb rows over the problems (rb_begin, total_rb).
+inline void layout_row_blocks(GemvParams& p, uint32_t rows_per_rb) {
+    uint32_t rbs = 0;
+    for (int i = 0; i < kMaxProblems; i++) {
+        p.rb_begin[i] = rbs;
+        if ((uint32_t)i < p.nprob) rbs += (p.n[i] + rows_per_rb - 1) / rows_per_rb;
+    }
+    p.total_rb = rbs;
+}
+
+typedef void (*GemvKernel)(GemvParams);
+
+// One persistent-pipeline instantiation: rows per lane group and its kernel.
+struct GemvTile {
+    uint32_t R;
+    GemvKernel kernel;
+};
+
+// Persistent launch over the instantiated tiles t[0..n) (widest first).  Each
+// tile's grid is as many workgroups as fit on the device at once (its
+// occupancy x CUs), capped by its row-block count.  The widest tile whose
+// row blocks cover every resident wave wins: on long weight streams wide
+// tiles amortise the per-task and per-row-block work (measured: the Q6_K and
+// MLX lm_heads and the 8B gate/up run fastest on the widest tile, uneven
+// row blocks per wave included).  When no tile covers the resident waves, the
+// one with the most row blocks (the narrowest) keeps the most waves busy.
+inline hipError_t launch_persistent_best(const GemvTile* t, int n, const GemvParams& p0, size_t lds,
+                                         hipStream_t st) {
     constexpr uint64_t waves = kGemvThreads / 64;
-    const uint64_t want = ((uint64_t)p.total_rb + waves - 1) / waves;
-    const uint64_t cap = (uint64_t)per_cu * (uint64_t)cus;
-    const uint32_t blocks = (uint32_t)(want < cap ? want : cap);
-    GemvParams q = p;
-    q.grid = blocks;
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), lds, st, q);
+    const uint32_t groups = 64u >> p0.lanes_log2;  // lane groups per wave
+    int pick = -1;
+    GemvParams q = p0;
+    for (int i = 0; i < n; i++) {
+        q = p0;
+        layout_row_blocks(q, groups * t[i].R);
+        int cus = 0, per_cu = 0;
+        hipError_t e = cached_occupancy(reinterpret_cast<const void*>(t[i].kernel), lds, kGemvThreads, &per_cu, &cus);
+        if (e != hipSuccess) return e;
+        if (per_cu < 1) continue;
+        const uint64_t cap = (uint64_t)per_cu * (uint64_t)cus;
+        const uint64_t want = ((uint64_t)q.total_rb + waves - 1) / waves;
+        q.grid = (uint32_t)(want < cap ? want : cap);
+        pick = i;
+        if ((uint64_t)q.total_rb >= cap * waves) break;
+    }
+    if (pick < 0) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(t[pick].kernel, dim3(q.grid), dim3(kGemvThreads), lds, st, q);
     return hipGetLastError();
 }
 
-// Latency-mode launch: one wave per row block.
+// The persistent tiles instantiated for register batch B: the default rows per
+// group W, half of it, and for one activation row every power of two down
+// to one row.  gemv_tile<R>() names the kernel of R rows.
+template <class E, int B, class MK>
+int gemv_tiles(GemvTile (&t)[3], MK&& gemv_tile) {
+    constexpr int W = rows_per_group<E, B>();
+    int n = 0;
+    t[n++] = {(uint32_t)W, gemv_tile(std::integral_constant<int, W>())};
+    if constexpr (W >= 2) t[n++] = {(uint32_t)(W / 2), gemv_tile(std::integral_constant<int, W / 2>())};
+    if constexpr (W >= 4 && B == 1) t[n++] = {(uint32_t)(W / 4), gemv_tile(std::integral_constant<int, W / 4>())};
+    return n;
+}
+
+// Latency-mode launch: one wave per row block of one row per lane group.
 template <class KERNEL>
-hipError_t launch_oneshot(KERNEL kernel, const GemvParams& p, size_t lds, hipStream_t st) {
+hipError_t launch_oneshot(KERNEL kernel, GemvParams p, size_t lds, hipStream_t st) {
     if (lds > 64u * 1024u) {
         int cus = 0, per_cu = 0;
         hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, kGemvThreads, &per_cu, &cus);
         if (e != hipSuccess) return e;
     }
+    layout_row_blocks(p, 64u >> p.lanes_log2);
     constexpr uint32_t waves = kGemvThreads / 64;
-    GemvParams q = p;
-    q.grid = (p.total_rb + waves - 1) / waves;
-    hipLaunchKernelGGL(kernel, dim3(q.grid), dim3(kGemvThreads), lds, st, q);
+    p.grid = (p.total_rb + waves - 1) / waves;
+    hipLaunchKernelGGL(kernel, dim3(p.grid), dim3(kGemvThreads), lds, st, p);
     return hipGetLastError();
 }
 
 // Instantiates and launches the GEMV kernel of encoding E for a power-of-two
 // register batch B (the host has checked that its activation tile fits LDS);
-// oneshot = chunks per lane selects the latency-mode kernel.
+// oneshot = chunks per lane selects the latency-mode kernel, 0 the
+// persistent pipeline.  The row-block layout is set here, per tile.
 // GGUF decode takes f32 activations, the reference's precision contract for
 // quantized linears (crates/dyninfer-compiler/src/lib.rs:289-306); bf16
 // activations reach GGUF weights only through the Q4_0 MFMA path.
 template <class E>
-hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16,
-                            hipStream_t st) {
+hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st) {
     if (xbf16) return hipErrorInvalidValue;
     const size_t lds = (size_t)xtile_bytes(E::ENC, B, p.K);
     if (oneshot) {
         // chunks per lane (the host's limits): 1..4 for one activation row
         // (Q6_K 1..2), 1..2 for 2 rows, 1 for 4
-        if (R != 1) return hipErrorInvalidValue;
 #define DMX_ONESHOT(b, c)                                                                             \
     if (B == b && oneshot == c) return launch_oneshot(gguf_gemv_oneshot_kernel<E, c, b, false>, p, lds, st);
         DMX_ONESHOT(1, 1)
@@ -761,26 +794,23 @@ hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t R, uint32_
 #undef DMX_ONESHOT
         return hipErrorInvalidValue;
     }
-    if (B == 1 && R == 1) return launch_persistent(gguf_gemv_kernel<E, 1, 1, false>, p, lds, st);
-#define DMX_CASE(b)                                                                                       \
-    case b:                                                                                               \
-        if constexpr (b <= max_register_batch(E::ENC)) {                                                  \
-            if (R == (uint32_t)rows_per_group<E, b>())                                                    \
-                return launch_persistent(gguf_gemv_kernel<E, b, rows_per_group<E, b>(), false>, p, lds, st); \
-            if constexpr (b > 1)                                                                          \
-                if (R == (uint32_t)rows_per_group_narrow<E, b>())                                         \
-                    return launch_persistent(gguf_gemv_kernel<E, b, rows_per_group_narrow<E, b>(), false>, p, \
-                                             lds, st);                                                    \
-        }                                                                                                 \
-        return hipErrorInvalidValue;
+    GemvTile t[3];
+    int n = 0;
+#define DMX_CASE(b)                                                                                            \
+    case b:                                                                                                    \
+        if constexpr (b <= max_register_batch(E::ENC))                                                         \
+            n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, b, decltype(r)::value, false>; }); \
+        break;
     switch (B) {
         DMX_CASE(1)
         DMX_CASE(2)
         DMX_CASE(4)
         DMX_CASE(8)
-    default: return hipErrorInvalidValue;
+    default: break;
     }
 #undef DMX_CASE
+    if (n == 0) return hipErrorInvalidValue;
+    return launch_persistent_best(t, n, p, lds, st);
 }
 
 }  // namespace dmx

@@ -2,7 +2,7 @@
 #include "gemv_kernels.hpp"
 
 namespace dmx {
-hipError_t gemv_launch_q4_0(const GemvParams& p, uint32_t B, uint32_t R, uint32_t oneshot, bool xbf16, hipStream_t st) {
-    return launch_gguf_gemv<EncQ40>(p, B, R, oneshot, xbf16, st);
+hipError_t gemv_launch_q4_0(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st) {
+    return launch_gguf_gemv<EncQ40>(p, B, oneshot, xbf16, st);
 }
 }  // namespace dmx
