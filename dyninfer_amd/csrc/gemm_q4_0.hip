@@ -73,7 +73,7 @@ struct Producer {
     static constexpr int WU = BN * 2 * NB / NT;  // W units per thread per stage
     static_assert(XU >= 1 && WU >= 1 && XU * NT == BM * 4 * NB && WU * NT == BN * 2 * NB, "unit split");
     static constexpr int kLoads = XU + 2 * WU;        // global load instructions per stage
-    static constexpr int kValu = 8 * XU + 32 * WU;    // decode VALU instructions per stage (approximate)
+    static constexpr int kValu = 10 * XU + 32 * WU;    // decode VALU instructions per stage (approximate)
 
     uint32_t xraw[PF][XU][4];  // 8 bf16 at k = 8g..8g+7
     uint32_t wraw[PF][WU][5];  // the block's dwords from the aligned dword holding its first byte
@@ -158,15 +158,17 @@ struct Producer {
         for (int i = 0; i < XU; i++) {
             uint32_t r, g8;
             xunit(i, r, g8);
-            // bf16 pairs (k0, k0+1), (k0+2, k0+3), ...  A dword read as f32 is
-            // its high bf16 plus low-order bits below f16 precision, which the
-            // round-toward-zero conversion discards, so the high halves need no
-            // masking.
+            // bf16 pairs (k0, k0+1), (k0+2, k0+3), ...  The high bf16 of a
+            // dword is only its f32 value once the low half is cleared: f32
+            // mantissa bits 13..15 (the low bf16's sign and top exponent bits)
+            // lie inside f16's 10-bit mantissa, so round-toward-zero would keep
+            // them.
             const uint32_t* q = xraw[slot][i];
+            constexpr uint32_t kHi = 0xFFFF0000u;
             const uint32_t p0 = pk_f16(q[0] << 16, q[1] << 16);  // k0, k0+2
-            const uint32_t p1 = pk_f16(q[0], q[1]);              // k0+1, k0+3
+            const uint32_t p1 = pk_f16(q[0] & kHi, q[1] & kHi);  // k0+1, k0+3
             const uint32_t p2 = pk_f16(q[2] << 16, q[3] << 16);  // k0+4, k0+6
-            const uint32_t p3 = pk_f16(q[2], q[3]);              // k0+5, k0+7
+            const uint32_t p3 = pk_f16(q[2] & kHi, q[3] & kHi);  // k0+5, k0+7
             *reinterpret_cast<uint4*>(&dx[r * PITCH + 8u * g8]) = make_uint4(p0, p1, p2, p3);
         }
         const h2 off_lo = {(_Float16)-1032.0f, (_Float16)-1032.0f};

@@ -192,6 +192,44 @@ def test_gemm_q4_0(ctx, m, n, k, ybf16):
     assert np.all(err <= TOL + extra), err.max()
 
 
+def _q4_0_blocks(codes: np.ndarray, d_bits: np.ndarray) -> np.ndarray:
+    """GGUF Q4_0 bytes from codes [n, k] (0..15) and f16 scale bits [n, k/32]:
+    byte l of a block holds k = l (low nibble) and k = 16 + l (high nibble)."""
+    n, k = codes.shape
+    c = codes.reshape(n, k // 32, 32).astype(np.uint8)
+    blk = np.empty((n, k // 32, 18), np.uint8)
+    blk[..., 0] = d_bits & 0xFF
+    blk[..., 1] = d_bits >> 8
+    blk[..., 2:] = c[..., :16] | (c[..., 16:] << 4)
+    return blk.reshape(-1)
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 256, 1024), (512, 3072, 1024), (2048, 3072, 1024)])
+def test_gemm_q4_0_bf16_neighbour_bits(ctx, m, n, k):
+    """Each activation must be narrowed from its own bf16 alone.  Even k hold
+    -3.0 (sign and top exponent bit set: the bits that sit just below an odd
+    neighbour's mantissa when a dword is read as f32), odd k hold positive
+    values, and only odd k carry weight (codes 15 against 8), so any leak of an
+    even activation's bits into its odd neighbour is a one-signed error of up
+    to 0.6% of Σ|w||x| in every output."""
+    rng = np.random.default_rng(5)
+    codes = np.full((n, k), 8, np.int64)
+    codes[:, 1::2] = rng.integers(9, 16, size=(n, k // 2))
+    d_bits = np.array([oracle.f32_to_f16(v) for v in rng.uniform(0.005, 0.02, 64)], np.uint16)
+    data = _q4_0_blocks(codes, d_bits[rng.integers(0, 64, size=(n, k // 32))])
+    x = np.empty((m, k), np.float32)
+    x[:, 0::2] = -3.0
+    x[:, 1::2] = rng.uniform(0.5, 2.0, size=(m, k // 2))
+    xb = oracle.f32_to_bf16_bits(x.reshape(-1)).reshape(m, k)
+    x = oracle.bf16_bits_to_f32(xb)
+    w = d.QWeight(d.ENC_Q4_0, n, k, dev(data))
+    y = ctx.qlinear(w, dev(xb).view(torch.bfloat16)).cpu().numpy()
+    wf = oracle.dequant_gguf(oracle.Q4_0, data, n, k)
+    y64, absdot = oracle.linear_f64(x, wf)
+    err = np.abs(y.astype(np.float64) - y64) / absdot
+    assert err.max() <= 2.0 ** -11 + 1e-5, err.max()
+
+
 # ----------------------------------------------------------------- BASELINE full sizes
 def _rows_subset(gtype, data, n, k, rows):
     bw, bb = oracle.BLOCK[gtype]
