@@ -493,13 +493,28 @@ __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const uint8_t
     // reading blockDim/gridDim costs a load from the dispatch packet that the
     // first weight loads would wait behind.
     const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (uint32_t)(kGemvThreads / 64) + (threadIdx.x >> 6));
-    const uint32_t W = p.grid * (uint32_t)(kGemvThreads / 64);
     const uint32_t L = 1u << p.lanes_log2;
     const uint32_t j = lane & (L - 1u), g = lane >> p.lanes_log2;
     const uint32_t rows_per_rb = (64u >> p.lanes_log2) * (uint32_t)R;
     const uint32_t nch = p.K / (uint32_t)E::CW;
     const uint32_t cpl = (nch + L - 1u) >> p.lanes_log2;  // chunks per lane per row block
-    const uint32_t T = wid < p.total_rb ? (p.total_rb - wid + W - 1) / W * cpl : 0u;  // tasks of this wave
+    // This wave's problem (fixed for the launch: the host gives each problem a
+    // range of waves in proportion to its row blocks) and its row blocks wi,
+    // wi + nw, ... of that problem: the problem's waves read neighbouring row
+    // blocks at a time, a compact front through the matrix (DRAM locality).
+    uint32_t pi = 0;
+#pragma unroll
+    for (int i = 0; i + 1 < kMaxProblems; i++) pi += ((uint32_t)i + 1u < p.nprob && wid >= p.wave_end[i]) ? 1u : 0u;
+    RowBlock blk0;
+    blk0.w = pick(pi, p.w);
+    blk0.sc = pick(pi, p.sc);
+    blk0.bi = pick(pi, p.bi);
+    blk0.y = pick(pi, p.y);
+    blk0.n = pick(pi, p.n);
+    const uint32_t wbeg = pi == 0 ? 0u : pick(pi - 1u, p.wave_end), wend = pick(pi, p.wave_end);
+    const uint32_t prb = (blk0.n + rows_per_rb - 1u) / rows_per_rb;  // the problem's row blocks
+    const uint32_t wi = wid - wbeg, nw = wend - wbeg;
+    const uint32_t T = wi < prb ? (prb - wi + nw - 1u) / nw * cpl : 0u;  // tasks of this wave
 
     float acc[R][B];
 #pragma unroll
@@ -520,15 +535,18 @@ __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const uint8_t
     // Two register buffers in ping-pong (no copies between them, so waiting
     // for one buffer never waits for the loads in flight into the other).
     typename E::Raw ba[R], bb[R];
-    uint32_t nrb = wid < p.total_rb ? wid : p.total_rb - 1u, nc = 0;  // the task loaded next
-    RowBlock nblk = row_block(p, nrb, rows_per_rb);
+    // the task loaded next: row block nrb (a wave without row blocks loads
+    // rows clamped into the matrix), chunk round nc
+    uint32_t nrb = wi, nc = 0;
+    RowBlock nblk = blk0;
+    nblk.base = nrb * rows_per_rb;
     // wave-uniform and branch-free; past the end the last task is loaded again
     auto advance = [&](uint32_t t) {
         const bool more = t + 1 < T;
         const bool wrap = more && nc + 1 == cpl;
         nc = wrap ? 0u : (more ? nc + 1 : nc);
-        nrb = wrap ? nrb + W : nrb;
-        nblk = row_block(p, nrb, rows_per_rb);
+        nrb = wrap ? nrb + nw : nrb;
+        nblk.base = nrb * rows_per_rb;
     };
     auto compute = [&](const typename E::Raw (&buf)[R], const RowBlock& blk, uint32_t c) {
         const uint32_t u0 = j + c * L;
@@ -696,6 +714,22 @@ inline void layout_row_blocks(GemvParams& p, uint32_t rows_per_rb) {
     p.total_rb = rbs;
 }
 
+// Waves of the persistent grid per problem (p.wave_end), in proportion to
+// each problem's row blocks, at least one each: problem i < nprob-1 gets
+// 1 + floor((W - nprob)·rb_i / rb_total) waves and the last the rest (at
+// least one, since the others take at most W - 1 together).
+inline void split_waves(GemvParams& p, uint32_t rows_per_rb) {
+    const uint64_t W = (uint64_t)p.grid * (kGemvThreads / 64);
+    uint64_t rb[kMaxProblems] = {}, total = 0;
+    for (uint32_t i = 0; i < p.nprob; i++) total += rb[i] = (p.n[i] + rows_per_rb - 1) / rows_per_rb;
+    uint64_t end = 0;
+    for (uint32_t i = 0; i < (uint32_t)kMaxProblems; i++) {
+        if (i + 1 < p.nprob) end += 1 + (W - p.nprob) * rb[i] / (total ? total : 1);
+        else end = W;
+        p.wave_end[i] = (uint32_t)end;
+    }
+}
+
 typedef void (*GemvKernel)(GemvParams);
 
 // One persistent-pipeline instantiation: rows per lane group and its kernel.
@@ -706,21 +740,24 @@ struct GemvTile {
 
 // Persistent launch over the instantiated tiles t[0..n) (widest first).  Each
 // tile's grid is as many workgroups as fit on the device at once (its
-// occupancy x CUs), capped by its row-block count.  The widest tile whose
-// row blocks cover every resident wave wins: on long weight streams wide
-// tiles amortise the per-task and per-row-block work (measured: the Q6_K and
-// MLX lm_heads and the 8B gate/up run fastest on the widest tile, uneven
-// row blocks per wave included).  When no tile covers the resident waves, the
-// one with the most row blocks (the narrowest) keeps the most waves busy.
+// occupancy x CUs), capped by its row-block count, and its waves are split
+// over the problems (split_waves).  The tile whose busiest wave has the
+// fewest rows wins (rows, not row blocks: a wave's time is its share of the
+// weight stream), ties going to the widest, which amortises the per-task and
+// per-row-block work over more weights.  Measured on the 8B gate/up (two
+// 12288-row problems): 4-row tiles leave half the waves 2 row blocks and
+// half 1 (49% of HBM peak), 1- and 2-row tiles split them evenly (54%).
 inline hipError_t launch_persistent_best(const GemvTile* t, int n, const GemvParams& p0, size_t lds,
                                          hipStream_t st) {
     constexpr uint64_t waves = kGemvThreads / 64;
     const uint32_t groups = 64u >> p0.lanes_log2;  // lane groups per wave
     int pick = -1;
-    GemvParams q = p0;
+    uint64_t best = ~(uint64_t)0;
+    GemvParams q = p0, chosen = p0;
     for (int i = 0; i < n; i++) {
         q = p0;
-        layout_row_blocks(q, groups * t[i].R);
+        const uint32_t rows_per_rb = groups * t[i].R;
+        layout_row_blocks(q, rows_per_rb);
         int cus = 0, per_cu = 0;
         hipError_t e = cached_occupancy(reinterpret_cast<const void*>(t[i].kernel), lds, kGemvThreads, &per_cu, &cus);
         if (e != hipSuccess) return e;
@@ -728,11 +765,22 @@ inline hipError_t launch_persistent_best(const GemvTile* t, int n, const GemvPar
         const uint64_t cap = (uint64_t)per_cu * (uint64_t)cus;
         const uint64_t want = ((uint64_t)q.total_rb + waves - 1) / waves;
         q.grid = (uint32_t)(want < cap ? want : cap);
-        pick = i;
-        if ((uint64_t)q.total_rb >= cap * waves) break;
+        split_waves(q, rows_per_rb);
+        uint64_t rows = 0;  // rows of the busiest wave
+        for (uint32_t k = 0; k < q.nprob; k++) {
+            const uint64_t nw = q.wave_end[k] - (k ? q.wave_end[k - 1] : 0u);
+            const uint64_t prb = (q.n[k] + rows_per_rb - 1) / rows_per_rb;
+            const uint64_t r = (prb + nw - 1) / nw * rows_per_rb;
+            rows = r > rows ? r : rows;
+        }
+        if (rows < best) {
+            best = rows;
+            pick = i;
+            chosen = q;
+        }
     }
     if (pick < 0) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL(t[pick].kernel, dim3(q.grid), dim3(kGemvThreads), lds, st, q);
+    hipLaunchKernelGGL(t[pick].kernel, dim3(chosen.grid), dim3(kGemvThreads), lds, st, chosen);
     return hipGetLastError();
 }
 

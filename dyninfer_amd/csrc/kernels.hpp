@@ -34,6 +34,10 @@ struct GemvParams {
     uint32_t y_bf16;      // store bf16 instead of f32
     uint32_t group;       // MLX group size
     uint32_t sdtype;      // MLX scale/bias dtype
+    // Persistent pipeline: waves [wave_end[i-1], wave_end[i]) serve problem i
+    // (wave_end[nprob-1] = all waves launched), each a contiguous run of the
+    // problem's row blocks.
+    uint32_t wave_end[kMaxProblems];
 };
 
 // Bytes of the GEMV activation tile in LDS per (activation row, chunk): the
