@@ -142,6 +142,41 @@ def test_gemv_multi_qkv(ctx, batch):
         assert err <= XF16, err
 
 
+# 5..16 activation rows on at least 384 tiles of 16 weight rows take the MFMA
+# GEMV (every weight decoded once for all rows): ragged rows, K needing
+# padding groups (1056 = 33 blocks), K split over LDS segments (12288: four
+# launches, the later ones adding with atomics), bf16 outputs.
+@pytest.mark.parametrize("n,k,batch,ybf16", [(6144, 1024, 5, False), (6144, 1024, 16, False), (6150, 1056, 9, False),
+                                             (6144, 4096, 16, True), (6144, 12288, 7, False), (8000, 2048, 12, True)])
+def test_gemv_mfma_q4_0(ctx, n, k, batch, ybf16):
+    w, data = gguf(oracle.Q4_0, n, k, seed=n + k + batch)
+    x = oracle.randn(batch * k, seed=batch).reshape(batch, k)
+    y = ctx.qlinear(w, dev(x), y_dtype=torch.bfloat16 if ybf16 else torch.float32)
+    if ybf16:
+        y = oracle.bf16_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16))
+    else:
+        y = y.cpu().numpy()
+    wf = oracle.dequant_gguf(oracle.Q4_0, data, n, k)
+    y64, absdot = oracle.linear_f64(x, wf)
+    den = np.where(absdot > 0, absdot, 1)
+    # f16 weight and activation roundings: 2·2^-11 of Σ|w||x|; bf16 outputs add 2^-8 of |y|
+    extra = np.abs(y64) * 2.0 ** -8 / den if ybf16 else 0.0
+    err = np.abs(y.astype(np.float64) - y64) / den
+    assert np.all(err <= 2.0 ** -10 + 2e-5 + extra), err.max()
+
+
+def test_gemv_mfma_q4_0_grouped(ctx):
+    # q/k/v of Qwen3-8B share one activation at batch 16: one MFMA launch, three outputs
+    k, batch = 4096, 16
+    shapes = [4096, 1024, 1024]
+    ws, datas = zip(*[gguf(oracle.Q4_0, n, k, seed=21 + i) for i, n in enumerate(shapes)])
+    x = oracle.randn(batch * k, seed=13).reshape(batch, k)
+    ys = ctx.qlinear_multi(list(ws), dev(x))
+    for y, data, n in zip(ys, datas, shapes):
+        err = gemv_err(y.cpu().numpy(), x, oracle.dequant_gguf(oracle.Q4_0, data, n, k))
+        assert err <= 2.0 ** -10 + 2e-5, err
+
+
 @pytest.mark.parametrize("sdtype", [oracle.D_BF16, oracle.D_F16, oracle.D_F32])
 @pytest.mark.parametrize("n,k,g", [(1, 64, 64), (1024, 1024, 64), (3072, 1024, 64), (1024, 3072, 64), (96, 512, 32),
                                    (40, 512, 128)])
