@@ -43,7 +43,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 namespace {
 
 constexpr int kMfmaThreads = 512;
-constexpr int kMfmaPF = 8;  // tasks of raw loads in flight per wave (a multiple of 2)
+constexpr int kMfmaPF = 8;  // tasks of raw loads in flight per wave (a multiple of 4)
 
 struct MfmaParams {
     const uint8_t* w[kMaxProblems];
@@ -70,6 +70,14 @@ __host__ __device__ constexpr uint32_t mfma_groups(uint32_t nblk) {
     return ((nblk + 3u) / 4u + kMfmaPF - 1u) / kMfmaPF * kMfmaPF;
 }
 __host__ __device__ constexpr uint32_t mfma_lds_bytes(uint32_t nblk) { return mfma_groups(nblk) * (4u * 64u * 16u + 64u); }
+
+// Slot of B-operand lane l (row b = l % 16, quarter q = l / 16) in the 64
+// slots of 16 bytes of one (group, j): l with its low three bits XORed by
+// (j + 4·(q & 1)) & 7.  A bijection within each 16-lane quarter, so a
+// fragment read (64 lanes, slots l) stays conflict-free, while the 16
+// staging threads of one (group, row) (j, q = 0..3) spread their writes over
+// all 8 16-byte bank groups instead of one.
+__device__ __forceinline__ uint32_t xslot(uint32_t l, uint32_t j) { return l ^ ((j + 4u * ((l >> 4) & 1u)) & 7u); }
 
 __device__ __forceinline__ uint32_t wq(uint32_t c, _Float16 off, h2 d2) {
     const h2 o = {off, off};
@@ -119,18 +127,28 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_q4_0_kernel(const Mfma
         r.row0 = (tile - pick(pi, p.tile_begin)) * 16u;
         return r;
     };
-    // raw loads of task (tile i, group g): block 4g + q of row m of the tile
-    auto load = [&](uint32_t i, uint32_t g) {
-        const Where wh = where(tile_at(i));
+    // a tile's weight base and the byte offset of this lane's row (rows past
+    // the problem re-read its last one: in bounds, never stored)
+    struct Rows {
+        const uint8_t* w;
+        uint32_t off;
+    };
+    auto rows_of = [&](const Where& wh) {
         const uint32_t row = wh.row0 + m < wh.n ? wh.row0 + m : wh.n - 1u;
+        return Rows{wh.w, row * rowbytes};
+    };
+    // raw loads of group g of a tile: block 4g + q of the lane's row
+    auto load = [&](const Rows& r, uint32_t g) {
         const uint32_t blk = 4u * g + q;
         const uint32_t kb = kb0 + (blk < p.nblk ? blk : p.nblk - 1u);  // past the segment: zeroed d
-        return load_raw_block<5>(wh.w, row * rowbytes + kb * 18u);
+        return load_raw_block<5>(r.w, r.off + kb * 18u);
     };
     // the first PF tasks' weight loads leave before the activations are staged
+    Where wcur = where(tile_at(0u));
+    Rows rcur = rows_of(wcur);
     RawBlock<5> ring[kMfmaPF];
 #pragma unroll
-    for (int s = 0; s < kMfmaPF; s++) ring[s] = load(0u, (uint32_t)s);  // ng >= PF: all in tile 0
+    for (int s = 0; s < kMfmaPF; s++) ring[s] = load(rcur, (uint32_t)s);  // ng >= PF: all in tile 0
 
     // ---- stage the activations: unit u = (group g, row b, e = 4q + j), the 16
     // units of (g, b) on one DPP row of 16 lanes.  Pass i + 1's loads are
@@ -174,13 +192,13 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_q4_0_kernel(const Mfma
         // block-relative k: (4j, 4j+2) (4j+1, 4j+3) (16+4j, 18+4j) (17+4j, 19+4j)
         const uint4 val = make_uint4(pk(v[0], v[2]), pk(v[1], v[3]), pk(v[4], v[6]), pk(v[5], v[7]));
         if (u < nunits) {
-            xl[(g * 4u + j) * 64u + b + 16u * q] = val;
+            xl[(g * 4u + j) * 64u + xslot(b + 16u * q, j)] = val;
             if (e == 0) inv[g * 16u + b] = ldexpf(1.0f, -sh);
         }
     };
-    // chunks of kStageChunk passes: all of a chunk's loads leave before the
-    // first is converted
-    constexpr uint32_t kStageChunk = 8;
+    // chunks of kStageChunk passes (K = 4096 at batch 16: one chunk): all of a
+    // chunk's loads leave before the first is converted
+    constexpr uint32_t kStageChunk = 16;
     for (uint32_t c0 = 0; c0 < npass; c0 += kStageChunk) {
         float v[kStageChunk][8];
 #pragma unroll
@@ -211,36 +229,44 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_q4_0_kernel(const Mfma
                                        wq(and_or(D8, 0x000F000Fu, 0x64006400u), (_Float16)-1032.0f, d2),
                                        wq(and_or(D, 0x00F000F0u, 0x54005400u), (_Float16)-72.0f, d2),
                                        wq(and_or(D8, 0x00F000F0u, 0x54005400u), (_Float16)-72.0f, d2));
-            const uint4 xb = xl[(g * 4u + (uint32_t)jj) * 64u + lane];
+            const uint4 xb = xl[(g * 4u + (uint32_t)jj) * 64u + xslot(lane, (uint32_t)jj)];
             tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, xb), tmp, 0, 0, 0);
         }
         return tmp;
     };
     // Tiles outer, groups inner (ng is a multiple of PF, so ring slot s of
-    // inner step g0 + s is static).  Two tasks at a time (two independent
+    // inner step g0 + s is static).  Four tasks at a time (four independent
     // MFMA chains); their slots are refilled, once decoded, with the tasks PF
     // later, which cross into the next tile at the end of one.  Each tile's outputs are
     // stored after its last group, outside the loop whose loads stay in
     // flight: no load sits under a branch.
     for (uint32_t i = 0; i < ntw; i++) {
+        const Where wnxt = where(tile_at(i + 1u));
+        const Rows rnxt = rows_of(wnxt);
         for (uint32_t g0 = 0; g0 < ng; g0 += kMfmaPF) {
 #pragma unroll
-            for (int s = 0; s < kMfmaPF; s += 2) {
+            for (int s = 0; s < kMfmaPF; s += 4) {
                 const uint32_t g = g0 + (uint32_t)s;
-                const f32x4 p0 = product(ring[s], g), p1 = product(ring[s + 1], g + 1u);
-                // refill the two slots in place once decoded (the same registers
+                f32x4 pr[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) pr[u] = product(ring[s + u], g + (uint32_t)u);
+                // refill the slots in place once decoded (the same registers
                 // across iterations: no copies that would wait for the loads)
                 const bool wrap = g + kMfmaPF >= ng;  // the refills belong to the next tile
-                const uint32_t ni = wrap ? i + 1u : i, ng0 = wrap ? g + kMfmaPF - ng : g + kMfmaPF;
-                ring[s] = load(ni, ng0);
-                ring[s + 1] = load(ni, ng0 + 1u);
-                const float s0 = inv[g * 16u + (lane & 15u)], s1 = inv[(g + 1u) * 16u + (lane & 15u)];
+                const Rows rr = wrap ? rnxt : rcur;
+                const uint32_t ng0 = wrap ? g + kMfmaPF - ng : g + kMfmaPF;
 #pragma unroll
-                for (int k = 0; k < 4; k++) acc[k] = fmaf(p1[k], s1, fmaf(p0[k], s0, acc[k]));
+                for (int u = 0; u < 4; u++) ring[s + u] = load(rr, ng0 + (uint32_t)u);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float sc = inv[(g + (uint32_t)u) * 16u + (lane & 15u)];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) acc[k] = fmaf(pr[u][k], sc, acc[k]);
+                }
             }
         }
         // lane l holds activation row b = l % 16 and weight rows 4q..4q+3
-        const Where wh = where(tile_at(i));
+        const Where wh = wcur;
         const uint32_t b = lane & 15u;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -253,6 +279,8 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_q4_0_kernel(const Mfma
             }
         }
         acc = zero;
+        wcur = wnxt;
+        rcur = rnxt;
     }
 }
 
@@ -307,9 +335,10 @@ hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, u
         hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, kMfmaThreads, &per_cu, &cus);
         if (e != hipSuccess) return e;
         if (per_cu < 1) return hipErrorInvalidConfiguration;
-        const uint32_t waves = kMfmaThreads / 64u;
-        const uint64_t cap = (uint64_t)per_cu * cus, want = (tiles + waves - 1u) / waves;
-        p.grid = (uint32_t)(want < cap ? want : cap);
+        // every CU gets a workgroup while there are tiles: the tiles spread over
+        // the workgroups first (wave numbering in the kernel)
+        const uint64_t cap = (uint64_t)per_cu * cus;
+        p.grid = (uint32_t)(tiles < cap ? tiles : cap);
         p.k0 = b0 * 32u;
         p.nblk = nb;
         p.accumulate = b0 > 0 ? 1u : 0u;
