@@ -264,26 +264,40 @@ struct EncQ6K {
         r.sh = sh;
         return r;
     }
-    __device__ __forceinline__ static Chunk unpack(const Raw& r, uint32_t u) {
-        Chunk c;
+    // The three code runs realigned: code dword t of each at a[t], b[t], h[t].
+    __device__ __forceinline__ static void codes(const Raw& r, uint32_t (&a)[NT], uint32_t (&b)[NT],
+                                                 uint32_t (&h)[NT]) {
         const uint32_t sel = realign_sel(r.sh, 0);
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            c.a[t] = __builtin_amdgcn_perm(r.a[t + 1], r.a[t], sel);
-            c.b[t] = __builtin_amdgcn_perm(r.b[t + 1], r.b[t], sel);
-            c.h[t] = __builtin_amdgcn_perm(r.h[t + 1], r.h[t], sel);
+            a[t] = __builtin_amdgcn_perm(r.a[t + 1], r.a[t], sel);
+            b[t] = __builtin_amdgcn_perm(r.b[t + 1], r.b[t], sel);
+            h[t] = __builtin_amdgcn_perm(r.h[t + 1], r.h[t], sel);
         }
+    }
+    // The int8 scales of chunk u's groups j = 0..3 and the super-block's d.
+    __device__ __forceinline__ static void scales(const Raw& r, uint32_t u, int32_t (&sc)[NG], float& d) {
+        const uint32_t sel = realign_sel(r.sh, 0);
         const bool n = ((u >> 1) & 1u) != 0;
         const uint32_t bs = 8u * (u & 1u);
         // sc bytes 8n + s + {0, 2} (groups 0, 1) and 8n + 4 + s + {0, 2} (groups 2, 3)
         const uint32_t s01 = __builtin_amdgcn_perm(n ? r.s[3] : r.s[1], n ? r.s[2] : r.s[0], sel);
         const uint32_t s23 = __builtin_amdgcn_perm(n ? r.s[4] : r.s[2], n ? r.s[3] : r.s[1], sel);
         // d = bytes 16..17 of the run
-        const float d = f16_bits_to_f32(r.sh ? (r.s[4] >> 16) : r.s[4]);
-        c.dsc[0] = (float)(int32_t)__builtin_amdgcn_sbfe(s01, bs, 8u) * d;
-        c.dsc[1] = (float)(int32_t)__builtin_amdgcn_sbfe(s01, bs + 16u, 8u) * d;
-        c.dsc[2] = (float)(int32_t)__builtin_amdgcn_sbfe(s23, bs, 8u) * d;
-        c.dsc[3] = (float)(int32_t)__builtin_amdgcn_sbfe(s23, bs + 16u, 8u) * d;
+        d = f16_bits_to_f32(r.sh ? (r.s[4] >> 16) : r.s[4]);
+        sc[0] = (int32_t)__builtin_amdgcn_sbfe(s01, bs, 8u);
+        sc[1] = (int32_t)__builtin_amdgcn_sbfe(s01, bs + 16u, 8u);
+        sc[2] = (int32_t)__builtin_amdgcn_sbfe(s23, bs, 8u);
+        sc[3] = (int32_t)__builtin_amdgcn_sbfe(s23, bs + 16u, 8u);
+    }
+    __device__ __forceinline__ static Chunk unpack(const Raw& r, uint32_t u) {
+        Chunk c;
+        codes(r, c.a, c.b, c.h);
+        int32_t sc[NG];
+        float d;
+        scales(r, u, sc, d);
+#pragma unroll
+        for (int g = 0; g < NG; g++) c.dsc[g] = (float)sc[g] * d;
         return c;
     }
     __device__ __forceinline__ static void pairs(const Chunk& c, int t, uint32_t (&p)[PPT]) {

@@ -1,33 +1,36 @@
-// Decode GEMV on MFMA for 5..16 activation rows, GGUF Q4_0 (y[b, o] =
+// Decode GEMV on MFMA for 5..16 activation rows, GGUF Q4_0 and Q6_K (y[b, o] =
 // Σ_k x[b, k]·w[o, k], f32 accumulation; gguf_codegen.rs:268-314 `emit_linear`
-// with the Q4_0 dequantisation of :412-472).
+// with the dequantisations of :412-472 (Q4_0) and :474-526 (Q6_K)).
 //
 // The VALU GEMV multiplies every decoded weight once per activation row (a
 // v_dot2 per pair per row), so above ~4 rows its VALU and LDS work grows with
 // the batch while the weight stream does not.  Here the activation rows are
-// the N side of v_mfma_f32_16x16x32_f16 (16 columns, zero-padded) and each
-// weight is decoded once, whatever the batch:
-//   * a wave owns tiles of 16 weight rows (the A side: lane l holds row l % 16
-//     and 8 k of the instruction's 32); per instruction, lane quarter
-//     q = l / 16 contributes 8 weights of its own block 4g + q of the row (the
-//     k slots of one MFMA may hold any k as long as the activation side holds
-//     the same ones, and the block scale is folded into each f16 weight), so
-//     the four lanes of a row read 72 contiguous bytes, and the four MFMAs of
-//     a 4-block group j = 0..3 take code dword j of every block: its 8 weights
-//     (4j, 4j+2), (4j+1, 4j+3), (16+4j, 18+4j), (17+4j, 19+4j), one
-//     v_and_or_b32 per pair (a low nibble under the f16 exponent of 1024 is
-//     1024+q, a high nibble under that of 64 is 64+q, both exact), a packed
-//     add giving q-8 (exact) and a packed multiply RNE_f16((q-8)·d), the only
-//     rounding of the weight (relative 2^-11);
-//   * the activations are staged once per workgroup in LDS as f16 in the B
-//     layout of each (group, j): lane (b, q) the 8 matching activations of
-//     row b, scaled by a power of two per (row, 128-k group) whose largest
-//     magnitude lands in [2^13, 2^14) (no overflow, no flush of the group's
-//     large values), rounded once to f16; the group's four MFMAs accumulate
-//     into a zeroed tile that is then added to the f32 total times the
-//     group's inverse scale;
-//   * weights stream through a ring of PF groups of raw block loads per
-//     wave (the next groups' loads in flight while one is multiplied);
+// one side of v_mfma_f32_16x16x32_f16 (16 rows, zero-padded) and each weight
+// is decoded once, whatever the batch:
+//   * a wave owns tiles of 16 weight rows (the B side: lane l holds row l % 16
+//     and 8 k of the instruction's 32; the result D[b][row] leaves lane l
+//     with weight row l % 16 of activation rows 4q..4q+3, q = l / 16).  A task
+//     is KT weights of each row of a tile in NM = KT/32 MFMAs, lane quarter q
+//     decoding a quarter of them (Q4_0: block 4t + q of task t, 128 weights a
+//     task; Q6_K: quarter q of super-block t, 256 weights a task) and feeding
+//     8 of its weights to each MFMA (the k slots of one MFMA may hold any k
+//     as long as the activation side holds the same ones).  The 8 weights of
+//     MFMA j are two runs of 4 k (run0, run1) in the pair order (r, r+2),
+//     (r+1, r+3) that one v_and_or_b32 decodes: a code at mantissa bits 0..
+//     under the f16 exponent of 1024 is 1024 + c, one at bits 4.. under that
+//     of 64 is 64 + c, both exact; a packed add removes the offset (exact)
+//     and a packed multiply by the f16 scale rounds once: Q4_0 folds its
+//     block scale, RNE_f16((q-8)·d); Q6_K folds its 16-weight group's int8
+//     scale, RNE_f16((q-32)·sc), and multiplies the super-block's d in f32
+//     afterwards (each lane's row has one d per super-block);
+//   * the activations are staged once per workgroup in LDS as f16 in the A
+//     layout of each (task, j): lane (b, q) the 8 matching activations of row
+//     b, scaled by a power of two per (row, task) whose largest magnitude
+//     lands in [2^13, 2^14) (no overflow, no flush of the task's large values),
+//     rounded once to f16; a task's MFMAs accumulate into a zeroed tile that
+//     is then added to the f32 total times the inverse scale;
+//   * weights stream through a ring of PF tasks of raw loads per wave, each
+//     slot refilled in place once decoded;
 //   * a K range too long for LDS runs as segments in consecutive launches,
 //     the later ones adding to the f32 outputs.
 // Accuracy: |y - y_exact| <= (2^-11 + 2^-11 + 2^-22)·Σ|w||x| + f32 accumulation
@@ -43,7 +46,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 namespace {
 
 constexpr int kMfmaThreads = 512;
-constexpr int kMfmaPF = 8;  // tasks of raw loads in flight per wave (a multiple of 4)
 
 struct MfmaParams {
     const uint8_t* w[kMaxProblems];
@@ -51,58 +53,150 @@ struct MfmaParams {
     uint32_t tile_begin[kMaxProblems];  // first 16-row tile of each problem
     uint32_t total_tiles;
     uint32_t grid;
-    uint32_t K;        // full reduction length (row bytes)
-    uint32_t k0;       // first k of this launch's segment
-    uint32_t nblk;     // Q4_0 blocks in the segment
+    uint32_t K;           // full reduction length
+    uint32_t k0;          // first k of this launch's segment
+    uint32_t nunit;       // blocks (Q4_0) or super-blocks (Q6_K) in the segment
     uint32_t nprob;
     uint32_t batch;
-    uint32_t y_bf16;
     uint32_t accumulate;  // add to y (later segments; f32 outputs only)
     const float* x;
     void* y[kMaxProblems];
 };
 
-// LDS: activations [group][j][64 lanes] x 16 bytes, then the inverse scales
-// [group][16 rows] f32.
-// 4-block groups of a segment, padded to a multiple of kMfmaPF (the padding
-// groups have zero weights and activations)
-__host__ __device__ constexpr uint32_t mfma_groups(uint32_t nblk) {
-    return ((nblk + 3u) / 4u + kMfmaPF - 1u) / kMfmaPF * kMfmaPF;
-}
-__host__ __device__ constexpr uint32_t mfma_lds_bytes(uint32_t nblk) { return mfma_groups(nblk) * (4u * 64u * 16u + 64u); }
-
-// Slot of B-operand lane l (row b = l % 16, quarter q = l / 16) in the 64
-// slots of 16 bytes of one (group, j): l with its low three bits XORed by
-// (j + 4·(q & 1)) & 7.  A bijection within each 16-lane quarter, so a
-// fragment read (64 lanes, slots l) stays conflict-free, while the 16
-// staging threads of one (group, row) (j, q = 0..3) spread their writes over
-// all 8 16-byte bank groups instead of one.
-__device__ __forceinline__ uint32_t xslot(uint32_t l, uint32_t j) { return l ^ ((j + 4u * ((l >> 4) & 1u)) & 7u); }
-
-__device__ __forceinline__ uint32_t wq(uint32_t c, _Float16 off, h2 d2) {
+// (c + off)·s for a packed pair (v_pk_add_f16, v_pk_mul_f16)
+__device__ __forceinline__ uint32_t wq(uint32_t c, _Float16 off, h2 s2) {
     const h2 o = {off, off};
-    return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, c) + o) * d2);
+    return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, c) + o) * s2);
 }
+
+// ---- encoding policies: task shape, raw loads, decode into the NM B operands
+// (uint4 = 4 f16 pairs) and the activation runs of each operand.
+
+// Q4_0: a task is 4 blocks (128 weights); lane quarter q decodes block 4t + q
+// and MFMA j takes its code dword j: low nibbles (4j, 4j+2), (4j+1, 4j+3),
+// high nibbles (16+4j, 18+4j), (17+4j, 19+4j).
+struct MfmaQ40 {
+    static constexpr int KT = 128, NM = 4, PF = 8, TPI = 4;  // weights, MFMAs per task; ring depth; tasks per step
+    static constexpr uint32_t UNIT = 32, UPT = 4;            // weights per block, blocks per task
+    static constexpr bool ROWSCALE = false;
+    static constexpr uint32_t STAGE = 16;  // staging passes per chunk of loads
+    using Raw = RawBlock<5>;
+    __device__ static uint32_t run0(uint32_t q, uint32_t j) { return 32u * q + 4u * j; }
+    __device__ static uint32_t run1(uint32_t q, uint32_t j) { return 32u * q + 16u + 4u * j; }
+    __device__ static uint32_t rowbytes(uint32_t K) { return (K / 32u) * 18u; }
+    // task t's raw loads (blocks past the segment re-read its last one)
+    __device__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u0, uint32_t nunit, uint32_t t,
+                               uint32_t q) {
+        const uint32_t blk = 4u * t + q;
+        return load_raw_block<5>(w, rowoff + (u0 + (blk < nunit ? blk : nunit - 1u)) * 18u);
+    }
+    __device__ static void decode(const Raw& r, uint32_t nunit, uint32_t t, uint32_t q, uint4 (&a)[NM], float&) {
+        const bool ok = 4u * t + q < nunit;  // past the segment: zero weights
+        const uint32_t sel = realign_sel(r.sh, 2);
+        const uint32_t db = (r.d[0] >> (8u * r.sh)) & (ok ? 0xFFFFu : 0u);
+        const h2 d2 = __builtin_bit_cast(h2, db * 0x00010001u);
+#pragma unroll
+        for (int j = 0; j < NM; j++) {
+            const uint32_t D = __builtin_amdgcn_perm(r.d[j + 1], r.d[j], sel), D8 = D >> 8;
+            a[j] = make_uint4(wq(and_or(D, 0x000F000Fu, 0x64006400u), (_Float16)-1032.0f, d2),
+                              wq(and_or(D8, 0x000F000Fu, 0x64006400u), (_Float16)-1032.0f, d2),
+                              wq(and_or(D, 0x00F000F0u, 0x54005400u), (_Float16)-72.0f, d2),
+                              wq(and_or(D8, 0x00F000F0u, 0x54005400u), (_Float16)-72.0f, d2));
+        }
+    }
+};
+
+// Q6_K: a task is one super-block (256 weights); lane quarter q decodes its
+// chunk (n, s) = (q >> 1, q & 1): weights n·128 + 32g + 16s + i of groups
+// g = 0..3, i < 16 (encodings.hpp EncQ6K, gguf_codegen.rs:499-521).  MFMA
+// j = 2t + h takes code dword t (i = 4t..4t+3) of groups 2h (run0) and 2h + 1
+// (run1 = run0 + 32); groups 2 and 3 hold their low bits in the high nibble,
+// decoded under the exponent of 64.
+struct MfmaQ6K {
+    static constexpr int KT = 256, NM = 8, PF = 4, TPI = 2;
+    static constexpr uint32_t UNIT = 256, UPT = 1;
+    static constexpr bool ROWSCALE = true;
+    static constexpr uint32_t STAGE = 8;  // 21-dword ring slots leave room for 8
+    using Raw = EncQ6K::Raw;
+    __device__ static uint32_t run0(uint32_t q, uint32_t j) {
+        return 128u * (q >> 1) + 64u * (j & 1u) + 16u * (q & 1u) + 4u * (j >> 1);
+    }
+    __device__ static uint32_t run1(uint32_t q, uint32_t j) { return run0(q, j) + 32u; }
+    __device__ static uint32_t rowbytes(uint32_t K) { return (K / 256u) * 210u; }
+    __device__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u0, uint32_t nunit, uint32_t t,
+                               uint32_t q) {
+        return EncQ6K::load(w, rowoff, 4u * (u0 + (t < nunit ? t : nunit - 1u)) + q);
+    }
+    __device__ static void decode(const Raw& r, uint32_t nunit, uint32_t t, uint32_t q, uint4 (&a)[NM], float& d) {
+        uint32_t A[4], B[4], H[4];
+        EncQ6K::codes(r, A, B, H);
+        int32_t sc[4];
+        EncQ6K::scales(r, q, sc, d);
+        d = t < nunit ? d : 0.0f;  // past the segment: zero weights
+        h2 s2[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const _Float16 v = (_Float16)sc[g];  // exact: |sc| <= 128
+            s2[g] = h2{v, v};
+        }
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) {
+            const uint32_t a0 = A[tt], b0 = B[tt], a8 = a0 >> 8, b8 = b0 >> 8;
+            const uint32_t hl4 = H[tt] << 4, hl2 = H[tt] << 2, hr4 = H[tt] >> 4, hr6 = H[tt] >> 6;
+            // groups 0, 1: low nibble + qh bits (0-1 | 2-3) at mantissa bits 0..5
+            a[2 * tt] =
+                make_uint4(wq(and_or(a0, 0x000F000Fu, and_or(hl4, 0x00300030u, 0x64006400u)), (_Float16)-1056.0f, s2[0]),
+                           wq(and_or(a8, 0x000F000Fu, and_or(hr4, 0x00300030u, 0x64006400u)), (_Float16)-1056.0f, s2[0]),
+                           wq(and_or(b0, 0x000F000Fu, and_or(hl2, 0x00300030u, 0x64006400u)), (_Float16)-1056.0f, s2[1]),
+                           wq(and_or(b8, 0x000F000Fu, and_or(hr6, 0x00300030u, 0x64006400u)), (_Float16)-1056.0f, s2[1]));
+            // groups 2, 3: high nibble + qh bits (4-5 | 6-7) at mantissa bits 4..9
+            a[2 * tt + 1] =
+                make_uint4(wq(and_or(a0, 0x00F000F0u, and_or(hl4, 0x03000300u, 0x54005400u)), (_Float16)-96.0f, s2[2]),
+                           wq(and_or(a8, 0x00F000F0u, and_or(hr4, 0x03000300u, 0x54005400u)), (_Float16)-96.0f, s2[2]),
+                           wq(and_or(b0, 0x00F000F0u, and_or(hl2, 0x03000300u, 0x54005400u)), (_Float16)-96.0f, s2[3]),
+                           wq(and_or(b8, 0x00F000F0u, and_or(hr6, 0x03000300u, 0x54005400u)), (_Float16)-96.0f, s2[3]));
+        }
+    }
+};
+
+// LDS: activations [task][j][64 lanes] x 16 bytes, then the inverse scales
+// [task][16 rows] f32.  Tasks of a segment are padded to a multiple of PF
+// (the padding tasks have zero weights and activations).
+template <class M>
+__host__ __device__ constexpr uint32_t mfma_tasks(uint32_t nunit) {
+    return ((nunit + M::UPT - 1u) / M::UPT + M::PF - 1u) / M::PF * M::PF;
+}
+template <class M>
+__host__ __device__ constexpr uint32_t mfma_lds_bytes(uint32_t nunit) {
+    return mfma_tasks<M>(nunit) * (M::NM * 64u * 16u + 64u);
+}
+
+// Slot of A-operand lane l (row b = l % 16, quarter q = l / 16) in the 64
+// slots of 16 bytes of one (task, j): l with its low three bits XORed by
+// (j + 4·(q & 1)) & 7.  A bijection within each 16-lane quarter, so a
+// fragment read (64 lanes, slots l) stays conflict-free, while the staging
+// threads of one (task, row) spread their writes over the LDS bank groups.
+__device__ __forceinline__ uint32_t xslot(uint32_t l, uint32_t j) { return l ^ ((j + 4u * ((l >> 4) & 1u)) & 7u); }
 
 }  // namespace
 
-template <bool YBF16>
-__global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_q4_0_kernel(const MfmaParams p) {
+template <class M, bool YBF16>
+__global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const uint32_t ng = mfma_groups(p.nblk);
+    constexpr uint32_t NM = M::NM, UPR = 4u * NM;  // staging units per (task, row): (q, j)
+    const uint32_t ng = mfma_tasks<M>(p.nunit);
     uint4* xl = reinterpret_cast<uint4*>(lds);
-    float* inv = reinterpret_cast<float*>(lds + ng * 4u * 64u * 16u);
+    float* inv = reinterpret_cast<float*>(lds + ng * NM * 64u * 16u);
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
 
     // ---- weight tiles: wave wid takes tiles wid, wid + W, ..., waves numbered
     // across workgroups first (wave i of workgroup w is wid = i·grid + w), so
-    // a few tiles still spread over all CUs; task = (tile, group), PF tasks of
-    // raw loads in flight
+    // a few tiles still spread over all CUs
     const uint32_t wid = __builtin_amdgcn_readfirstlane((tid >> 6) * p.grid + blockIdx.x);
     const uint32_t W = p.grid * (kMfmaThreads / 64u);
     const uint32_t m = lane & 15u, q = lane >> 4;
     const uint32_t ntw = wid < p.total_tiles ? (p.total_tiles - wid + W - 1u) / W : 0u;  // tiles of this wave
-    const uint32_t rowbytes = (p.K / 32u) * 18u, kb0 = p.k0 / 32u;
+    const uint32_t rowbytes = M::rowbytes(p.K), u0 = p.k0 / M::UNIT;
 
     // the wave's i-th tile (past the end: its last, or any tile for a wave
     // without tiles: loaded, never multiplied into a stored result)
@@ -137,32 +231,29 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_q4_0_kernel(const Mfma
         const uint32_t row = wh.row0 + m < wh.n ? wh.row0 + m : wh.n - 1u;
         return Rows{wh.w, row * rowbytes};
     };
-    // raw loads of group g of a tile: block 4g + q of the lane's row
-    auto load = [&](const Rows& r, uint32_t g) {
-        const uint32_t blk = 4u * g + q;
-        const uint32_t kb = kb0 + (blk < p.nblk ? blk : p.nblk - 1u);  // past the segment: zeroed d
-        return load_raw_block<5>(r.w, r.off + kb * 18u);
-    };
+    auto load = [&](const Rows& r, uint32_t t) { return M::load(r.w, r.off, u0, p.nunit, t, q); };
     // the first PF tasks' weight loads leave before the activations are staged
     Where wcur = where(tile_at(0u));
     Rows rcur = rows_of(wcur);
-    RawBlock<5> ring[kMfmaPF];
+    typename M::Raw ring[M::PF];
 #pragma unroll
-    for (int s = 0; s < kMfmaPF; s++) ring[s] = load(rcur, (uint32_t)s);  // ng >= PF: all in tile 0
+    for (int s = 0; s < M::PF; s++) ring[s] = load(rcur, (uint32_t)s);  // ng >= PF: all in tile 0
 
-    // ---- stage the activations: unit u = (group g, row b, e = 4q + j), the 16
-    // units of (g, b) on one DPP row of 16 lanes.  Pass i + 1's loads are
-    // issued before pass i is converted, so the passes share one latency.
-    const uint32_t nunits = ng * 256u, npass = (nunits + kMfmaThreads - 1u) / kMfmaThreads;
+    // ---- stage the activations: unit u = (task g, row b, e = q·NM + j); the
+    // UPR units of (g, b) lie on consecutive lanes (16 or 32), their maximum
+    // reduced by DPP within rows of 16 lanes and v_permlane16_swap across two.
+    // Chunks of passes: all of a chunk's loads leave before the first is
+    // converted.
+    const uint32_t nunits = ng * 16u * UPR, npass = (nunits + kMfmaThreads - 1u) / kMfmaThreads;
     auto xload = [&](uint32_t pass, float (&v)[8]) {
         const uint32_t u = pass * kMfmaThreads + tid;
-        const uint32_t g = u >> 8, b = (u >> 4) & 15u, e = u & 15u, q = e >> 2, j = e & 3u;
-        const uint32_t blk = 4u * g + q;
+        const uint32_t g = u / (16u * UPR), b = (u / UPR) % 16u, e = u % UPR, qq = e / NM, j = e % NM;
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = 0.0f;
-        if (u < nunits && b < p.batch && blk < p.nblk) {
-            const float* xr = p.x + (size_t)b * p.K + p.k0 + 32u * blk + 4u * j;
-            const f32x4 lo = *gptr<f32x4>(xr), hi = *gptr<f32x4>(xr + 16);
+        const bool ok = M::UPT * g + (M::UPT == 1 ? 0u : qq) < p.nunit;  // the unit holding these k
+        if (u < nunits && b < p.batch && ok) {
+            const float* xr = p.x + (size_t)b * p.K + p.k0 + M::KT * g;
+            const f32x4 lo = *gptr<f32x4>(xr + M::run0(qq, j)), hi = *gptr<f32x4>(xr + M::run1(qq, j));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 v[i] = lo[i];
@@ -172,14 +263,18 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_q4_0_kernel(const Mfma
     };
     auto xstore = [&](uint32_t pass, const float (&v)[8]) {
         const uint32_t u = pass * kMfmaThreads + tid;
-        const uint32_t g = u >> 8, b = (u >> 4) & 15u, e = u & 15u, q = e >> 2, j = e & 3u;
-        float m = absmax3(v[0], v[1], v[2]);
-        m = absmax3(m, v[3], v[4]);
-        m = absmax3(m, v[5], v[6]);
-        m = absmax3(m, v[7], v[7]);
-        uint32_t mx = __float_as_uint(m);  // non-negative floats order as integers
+        const uint32_t g = u / (16u * UPR), b = (u / UPR) % 16u, e = u % UPR, qq = e / NM, j = e % NM;
+        float mv = absmax3(v[0], v[1], v[2]);
+        mv = absmax3(mv, v[3], v[4]);
+        mv = absmax3(mv, v[5], v[6]);
+        mv = absmax3(mv, v[7], v[7]);
+        uint32_t mx = __float_as_uint(mv);  // non-negative floats order as integers
         mx = lanes_reduce<8>(mx, [](uint32_t a, uint32_t c) { return a > c ? a : c; });
-        mx = max(mx, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0x140, 0xF, 0xF, false));  // row_mirror: all 16
+        mx = max(mx, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0x140, 0xF, 0xF, false));  // row_mirror: 16 lanes
+        if constexpr (UPR == 32) {  // and the neighbouring row of 16
+            const auto r = __builtin_amdgcn_permlane16_swap(mx, mx, false, false);
+            mx = max(r[0], r[1]);
+        }
         int ex = 0;
         (void)frexpf(__uint_as_float(mx), &ex);
         ex = ex < -110 ? -110 : ex;  // keeps the scale a normal f32
@@ -189,16 +284,14 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_q4_0_kernel(const Mfma
             const f32x2 f = {ldexpf(a, sh), ldexpf(c, sh)};
             return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));  // RNE
         };
-        // block-relative k: (4j, 4j+2) (4j+1, 4j+3) (16+4j, 18+4j) (17+4j, 19+4j)
+        // pair order (r, r+2) (r+1, r+3) of each run
         const uint4 val = make_uint4(pk(v[0], v[2]), pk(v[1], v[3]), pk(v[4], v[6]), pk(v[5], v[7]));
         if (u < nunits) {
-            xl[(g * 4u + j) * 64u + xslot(b + 16u * q, j)] = val;
+            xl[(g * NM + j) * 64u + xslot(b + 16u * qq, j)] = val;
             if (e == 0) inv[g * 16u + b] = ldexpf(1.0f, -sh);
         }
     };
-    // chunks of kStageChunk passes (K = 4096 at batch 16: one chunk): all of a
-    // chunk's loads leave before the first is converted
-    constexpr uint32_t kStageChunk = 16;
+    constexpr uint32_t kStageChunk = M::STAGE;
     for (uint32_t c0 = 0; c0 < npass; c0 += kStageChunk) {
         float v[kStageChunk][8];
 #pragma unroll
@@ -211,71 +304,73 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_q4_0_kernel(const Mfma
 
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 acc = zero;
-    // one task's product: decode block 4g + q's four code dwords and run the
-    // group's four MFMAs into a zeroed tile
-    auto product = [&](const RawBlock<5>& r, uint32_t g) {
-        const bool ok = 4u * g + q < p.nblk;
-        const uint32_t sel = realign_sel(r.sh, 2);
-        uint32_t cd[4];
+    // one task's product: decode the lane's quarter and run the task's MFMAs
+    // into a zeroed tile; rs = the lane's row scale (Q6_K's d)
+    auto product = [&](const typename M::Raw& r, uint32_t t, float& rs) {
+        // the activation fragments' LDS reads leave before the decode, so
+        // their latency hides behind it
+        uint4 xa[NM];
 #pragma unroll
-        for (int c = 0; c < 4; c++) cd[c] = __builtin_amdgcn_perm(r.d[c + 1], r.d[c], sel);
-        const uint32_t db = ok ? (r.d[0] >> (8u * r.sh)) & 0xFFFFu : 0u;  // past the segment: zero weights
-        const h2 d2 = __builtin_bit_cast(h2, db * 0x00010001u);
+        for (uint32_t j = 0; j < NM; j++) xa[j] = xl[(t * NM + j) * 64u + xslot(lane, j)];
+        uint4 a[NM];
+        M::decode(r, p.nunit, t, q, a, rs);
         f32x4 tmp = zero;
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-            const uint32_t D = cd[jj], D8 = D >> 8;
-            const uint4 a = make_uint4(wq(and_or(D, 0x000F000Fu, 0x64006400u), (_Float16)-1032.0f, d2),
-                                       wq(and_or(D8, 0x000F000Fu, 0x64006400u), (_Float16)-1032.0f, d2),
-                                       wq(and_or(D, 0x00F000F0u, 0x54005400u), (_Float16)-72.0f, d2),
-                                       wq(and_or(D8, 0x00F000F0u, 0x54005400u), (_Float16)-72.0f, d2));
-            const uint4 xb = xl[(g * 4u + (uint32_t)jj) * 64u + xslot(lane, (uint32_t)jj)];
-            tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, xb), tmp, 0, 0, 0);
-        }
+        for (uint32_t j = 0; j < NM; j++)
+            tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, xa[j]), __builtin_bit_cast(h8, a[j]), tmp, 0, 0, 0);
         return tmp;
     };
-    // Tiles outer, groups inner (ng is a multiple of PF, so ring slot s of
-    // inner step g0 + s is static).  Four tasks at a time (four independent
-    // MFMA chains); their slots are refilled, once decoded, with the tasks PF
-    // later, which cross into the next tile at the end of one.  Each tile's outputs are
-    // stored after its last group, outside the loop whose loads stay in
-    // flight: no load sits under a branch.
+    // Tiles outer, tasks inner (ng is a multiple of PF, so ring slot s of
+    // inner step g0 + s is static).  TPI tasks at a time (independent MFMA
+    // chains); their slots are refilled, once decoded, with the tasks PF
+    // later, which cross into the next tile at the end of one.  Each tile's
+    // outputs are stored after its last task, outside the loop whose loads
+    // stay in flight: no load sits under a branch.
     for (uint32_t i = 0; i < ntw; i++) {
         const Where wnxt = where(tile_at(i + 1u));
         const Rows rnxt = rows_of(wnxt);
-        for (uint32_t g0 = 0; g0 < ng; g0 += kMfmaPF) {
+        for (uint32_t g0 = 0; g0 < ng; g0 += M::PF) {
 #pragma unroll
-            for (int s = 0; s < kMfmaPF; s += 4) {
+            for (int s = 0; s < M::PF; s += M::TPI) {
                 const uint32_t g = g0 + (uint32_t)s;
-                f32x4 pr[4];
+                f32x4 pr[M::TPI];
+                float rs[M::TPI];
 #pragma unroll
-                for (int u = 0; u < 4; u++) pr[u] = product(ring[s + u], g + (uint32_t)u);
+                for (int k = 0; k < M::TPI; k++) pr[k] = product(ring[s + k], g + (uint32_t)k, rs[k]);
                 // refill the slots in place once decoded (the same registers
                 // across iterations: no copies that would wait for the loads)
-                const bool wrap = g + kMfmaPF >= ng;  // the refills belong to the next tile
+                const bool wrap = g + M::PF >= ng;  // the refills belong to the next tile
                 const Rows rr = wrap ? rnxt : rcur;
-                const uint32_t ng0 = wrap ? g + kMfmaPF - ng : g + kMfmaPF;
+                const uint32_t gn = wrap ? g + M::PF - ng : g + M::PF;
 #pragma unroll
-                for (int u = 0; u < 4; u++) ring[s + u] = load(rr, ng0 + (uint32_t)u);
+                for (int k = 0; k < M::TPI; k++) ring[s + k] = load(rr, gn + (uint32_t)k);
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const float sc = inv[(g + (uint32_t)u) * 16u + (lane & 15u)];
+                for (int k = 0; k < M::TPI; k++) {
+                    // inverse activation scales of rows 4q..4q+3
+                    f32x4 sc = *reinterpret_cast<const f32x4*>(inv + (g + (uint32_t)k) * 16u + 4u * q);
+                    if constexpr (M::ROWSCALE) sc *= rs[k];
 #pragma unroll
-                    for (int k = 0; k < 4; k++) acc[k] = fmaf(pr[u][k], sc, acc[k]);
+                    for (int c = 0; c < 4; c++) acc[c] = fmaf(pr[k][c], sc[c], acc[c]);
                 }
             }
         }
-        // lane l holds activation row b = l % 16 and weight rows 4q..4q+3
-        const Where wh = wcur;
-        const uint32_t b = lane & 15u;
+        // lane l holds weight row l % 16 of activation rows 4q..4q+3
+        const uint32_t row = wcur.row0 + m;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t row = wh.row0 + 4u * q + (uint32_t)k;
-            if (b < p.batch && row < wh.n) {
-                const size_t idx = (size_t)b * wh.n + row;
-                if constexpr (YBF16) gptr_mut<uint16_t>(wh.y)[idx] = f32_to_bf16_bits(acc[k]);
-                else if (p.accumulate) unsafeAtomicAdd(&static_cast<float*>(wh.y)[idx], acc[k]);  // later K segments
-                else gptr_mut<float>(wh.y)[idx] = acc[k];
+        for (int c = 0; c < 4; c++) {
+            const uint32_t b = 4u * q + (uint32_t)c;
+            if (b < p.batch && row < wcur.n) {
+                const size_t idx = (size_t)b * wcur.n + row;
+                if constexpr (YBF16) gptr_mut<uint16_t>(wcur.y)[idx] = f32_to_bf16_bits(acc[c]);
+                else if (p.accumulate) {  // later K segments
+                    // through a global pointer (global_atomic_add_f32): a flat
+                    // atomic would make every vmcnt wait of the loop a full drain
+                    [[clang::atomic(ignore_denormal_mode)]] {
+                        (void)__hip_atomic_fetch_add(gptr_mut<float>(wcur.y) + idx, acc[c], __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+                else gptr_mut<float>(wcur.y)[idx] = acc[c];
             }
         }
         acc = zero;
@@ -284,26 +379,31 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_q4_0_kernel(const Mfma
     }
 }
 
+namespace {
+
 // Launches with fewer than kMfmaMinTiles 16-row tiles stay on the VALU GEMV:
-// each workgroup stages all activations (~6-8 us at K = 4096, batch 16)
-// and a wave multiplies its tile's groups in sequence, which only pays off
-// when the weights are many (measured on the 8B shapes at batch 16: 4096
-// rows 28 us on MFMA against 22 us on VALU, 6144 rows 28 against 32,
-// 24576 rows 31 against 76).
+// each workgroup stages all activations (~6-9 us at K = 4096, batch 16)
+// and a wave multiplies its tile's tasks in sequence, which only pays off
+// when the weights are many (measured on the 8B Q4_0 shapes at batch 16:
+// 4096 rows 28 us on MFMA against 22 us on VALU, 6144 rows 21 against 32,
+// 24576 rows 28 against 76).
 constexpr uint32_t kMfmaMinTiles = 384;
 
-bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool x_bf16,
-                       bool y_bf16) {
-    if (enc != ENC_Q4_0 || x_bf16 || batch < 5 || batch > 16) return false;
-    uint32_t tiles = 0;
-    for (int i = 0; i < nprob; i++) tiles += (probs[i].n + 15u) / 16u;
-    if (tiles < kMfmaMinTiles) return false;
-    return !y_bf16 || mfma_lds_bytes(K / 32u) <= kLdsBytes;  // bf16 outputs cannot add up segments
+// Units per launch: the fewest segments whose LDS fits, whole tasks each
+// except the last.
+template <class M>
+uint32_t mfma_segment(uint32_t units) {
+    for (uint32_t nseg = 1; nseg <= units; nseg++) {
+        uint32_t seg = (units + nseg - 1u) / nseg;
+        seg = nseg > 1 ? (seg + M::UPT - 1u) / M::UPT * M::UPT : seg;
+        if (mfma_lds_bytes<M>(seg) <= kLdsBytes) return seg;
+    }
+    return 0;
 }
 
-hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x,
-                            uint32_t batch, bool y_bf16, hipStream_t st) {
-    if (enc != ENC_Q4_0 || nprob < 1 || nprob > kMaxProblems) return hipErrorInvalidValue;
+template <class M>
+hipError_t launch_mfma(const GemvProblem* probs, int nprob, uint32_t K, const void* x, uint32_t batch, bool y_bf16,
+                       hipStream_t st) {
     MfmaParams p = {};
     uint32_t tiles = 0;
     for (int i = 0; i < kMaxProblems; i++) {
@@ -318,19 +418,13 @@ hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, u
     p.nprob = (uint32_t)nprob;
     p.K = K;
     p.batch = batch;
-    p.y_bf16 = y_bf16 ? 1u : 0u;
     p.x = static_cast<const float*>(x);
-    // segments of at most kSegBlocks blocks (a multiple of 4: whole groups)
-    uint32_t seg = K / 32u;
-    while (mfma_lds_bytes(seg) > kLdsBytes) seg = (seg + 1u) / 2u;
-    seg = seg < K / 32u ? (seg + 3u) / 4u * 4u : seg;
-    while (mfma_lds_bytes(seg) > kLdsBytes) seg -= 4u;
-    if (seg == 0) return hipErrorInvalidValue;
-    if (y_bf16 && seg < K / 32u) return hipErrorInvalidValue;
-    auto kernel = y_bf16 ? gemv_mfma_q4_0_kernel<true> : gemv_mfma_q4_0_kernel<false>;
-    for (uint32_t b0 = 0; b0 < K / 32u; b0 += seg) {
-        const uint32_t nb = K / 32u - b0 < seg ? K / 32u - b0 : seg;
-        const size_t lds = mfma_lds_bytes(nb);
+    const uint32_t units = K / M::UNIT, seg = mfma_segment<M>(units);
+    if (seg == 0 || (y_bf16 && seg < units)) return hipErrorInvalidValue;
+    auto kernel = y_bf16 ? gemv_mfma_kernel<M, true> : gemv_mfma_kernel<M, false>;
+    for (uint32_t b0 = 0; b0 < units; b0 += seg) {
+        const uint32_t nu = units - b0 < seg ? units - b0 : seg;
+        const size_t lds = mfma_lds_bytes<M>(nu);
         int cus = 0, per_cu = 0;
         hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, kMfmaThreads, &per_cu, &cus);
         if (e != hipSuccess) return e;
@@ -339,14 +433,36 @@ hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, u
         // the workgroups first (wave numbering in the kernel)
         const uint64_t cap = (uint64_t)per_cu * cus;
         p.grid = (uint32_t)(tiles < cap ? tiles : cap);
-        p.k0 = b0 * 32u;
-        p.nblk = nb;
+        p.k0 = b0 * M::UNIT;
+        p.nunit = nu;
         p.accumulate = b0 > 0 ? 1u : 0u;
         hipLaunchKernelGGL(kernel, dim3(p.grid), dim3(kMfmaThreads), lds, st, p);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+}  // namespace
+
+bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool x_bf16,
+                       bool y_bf16) {
+    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K) || x_bf16 || batch < 5 || batch > 16) return false;
+    uint32_t tiles = 0;
+    for (int i = 0; i < nprob; i++) tiles += (probs[i].n + 15u) / 16u;
+    if (tiles < kMfmaMinTiles) return false;
+    // bf16 outputs cannot add up segments
+    const uint32_t units = enc == ENC_Q4_0 ? K / MfmaQ40::UNIT : K / MfmaQ6K::UNIT;
+    const uint32_t seg = enc == ENC_Q4_0 ? mfma_segment<MfmaQ40>(units) : mfma_segment<MfmaQ6K>(units);
+    return seg > 0 && (!y_bf16 || seg == units);
+}
+
+hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x,
+                            uint32_t batch, bool y_bf16, hipStream_t st) {
+    if (nprob < 1 || nprob > kMaxProblems) return hipErrorInvalidValue;
+    if (enc == ENC_Q4_0) return launch_mfma<MfmaQ40>(probs, nprob, K, x, batch, y_bf16, st);
+    if (enc == ENC_Q6_K) return launch_mfma<MfmaQ6K>(probs, nprob, K, x, batch, y_bf16, st);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace dmx

@@ -144,19 +144,32 @@ def test_gemv_multi_qkv(ctx, batch):
 
 # 5..16 activation rows on at least 384 tiles of 16 weight rows take the MFMA
 # GEMV (every weight decoded once for all rows): ragged rows, K needing
-# padding groups (1056 = 33 blocks), K split over LDS segments (12288: four
-# launches, the later ones adding with atomics), bf16 outputs.
-@pytest.mark.parametrize("n,k,batch,ybf16", [(6144, 1024, 5, False), (6144, 1024, 16, False), (6150, 1056, 9, False),
-                                             (6144, 4096, 16, True), (6144, 12288, 7, False), (8000, 2048, 12, True)])
-def test_gemv_mfma_q4_0(ctx, n, k, batch, ybf16):
-    w, data = gguf(oracle.Q4_0, n, k, seed=n + k + batch)
+# padding tasks (Q4_0 1056 = 33 blocks, Q6_K 2304 = 9 super-blocks, rows
+# alternating 4- and 2-byte alignment), K split over LDS segments (12288:
+# three launches, the later ones adding with atomics), bf16 outputs, a
+# weight base 2 bytes past a 4-byte boundary.
+MFMA_CASES = [
+    (oracle.Q4_0, 6144, 1024, 5, False, 0), (oracle.Q4_0, 6144, 1024, 16, False, 0),
+    (oracle.Q4_0, 6150, 1056, 9, False, 2), (oracle.Q4_0, 6144, 4096, 16, True, 0),
+    (oracle.Q4_0, 6144, 12288, 7, False, 0), (oracle.Q4_0, 8000, 2048, 12, True, 0),
+    (oracle.Q6_K, 6144, 1024, 5, False, 0), (oracle.Q6_K, 6144, 4096, 16, True, 0),
+    (oracle.Q6_K, 6150, 2304, 9, False, 2), (oracle.Q6_K, 6144, 12288, 7, False, 0),
+    (oracle.Q6_K, 8000, 4096, 12, True, 2),
+]
+
+
+@pytest.mark.parametrize("gtype,n,k,batch,ybf16,off", MFMA_CASES,
+                         ids=[f"{oracle.NAMES[c[0]]}-{c[1]}x{c[2]}-b{c[3]}{'-bf16' if c[4] else ''}{'-off2' if c[5] else ''}"
+                              for c in MFMA_CASES])
+def test_gemv_mfma(ctx, gtype, n, k, batch, ybf16, off):
+    w, data = gguf(gtype, n, k, seed=n + k + batch, off=off)
     x = oracle.randn(batch * k, seed=batch).reshape(batch, k)
     y = ctx.qlinear(w, dev(x), y_dtype=torch.bfloat16 if ybf16 else torch.float32)
     if ybf16:
         y = oracle.bf16_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16))
     else:
         y = y.cpu().numpy()
-    wf = oracle.dequant_gguf(oracle.Q4_0, data, n, k)
+    wf = oracle.dequant_gguf(gtype, data, n, k)
     y64, absdot = oracle.linear_f64(x, wf)
     den = np.where(absdot > 0, absdot, 1)
     # f16 weight and activation roundings: 2·2^-11 of Σ|w||x|; bf16 outputs add 2^-8 of |y|
@@ -165,16 +178,31 @@ def test_gemv_mfma_q4_0(ctx, n, k, batch, ybf16):
     assert np.all(err <= 2.0 ** -10 + 2e-5 + extra), err.max()
 
 
-def test_gemv_mfma_q4_0_grouped(ctx):
+@pytest.mark.parametrize("gtype", [oracle.Q4_0, oracle.Q6_K], ids=oracle.NAMES.get)
+def test_gemv_mfma_grouped(ctx, gtype):
     # q/k/v of Qwen3-8B share one activation at batch 16: one MFMA launch, three outputs
     k, batch = 4096, 16
     shapes = [4096, 1024, 1024]
-    ws, datas = zip(*[gguf(oracle.Q4_0, n, k, seed=21 + i) for i, n in enumerate(shapes)])
+    ws, datas = zip(*[gguf(gtype, n, k, seed=21 + i) for i, n in enumerate(shapes)])
     x = oracle.randn(batch * k, seed=13).reshape(batch, k)
     ys = ctx.qlinear_multi(list(ws), dev(x))
     for y, data, n in zip(ys, datas, shapes):
-        err = gemv_err(y.cpu().numpy(), x, oracle.dequant_gguf(oracle.Q4_0, data, n, k))
+        err = gemv_err(y.cpu().numpy(), x, oracle.dequant_gguf(gtype, data, n, k))
         assert err <= 2.0 ** -10 + 2e-5, err
+
+
+@pytest.mark.parametrize("gtype", [oracle.Q4_0, oracle.Q6_K], ids=oracle.NAMES.get)
+@pytest.mark.parametrize("lo,hi", [(6, 8), (-30, -28), (-8, 8)])
+def test_gemv_mfma_activation_range(ctx, gtype, lo, hi):
+    """The MFMA path's per-(row, task) power-of-two scaling over magnitudes f16
+    cannot hold unscaled, mixed within a task, and a zero run."""
+    n, k, batch = 6144, 2048, 8
+    w, data = gguf(gtype, n, k, seed=17 + gtype)
+    x = _ranged_x(batch, k, seed=(lo + 100) * 7 + (hi + 100), lo=lo, hi=hi)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    assert np.all(np.isfinite(y))
+    err = gemv_err(y, x, oracle.dequant_gguf(gtype, data, n, k))
+    assert err <= 2.0 ** -10 + 2e-5, err
 
 
 @pytest.mark.parametrize("sdtype", [oracle.D_BF16, oracle.D_F16, oracle.D_F32])
@@ -274,6 +302,7 @@ def _rows_subset(gtype, data, n, k, rows):
 
 @pytest.mark.parametrize("gtype,n,k,batch", [
     (oracle.Q6_K, 151936, 1024, 1),   # Qwen3-0.6B tied lm_head
+    (oracle.Q6_K, 151936, 1024, 16),  # the same at batch 16 (MFMA path)
     (oracle.Q6_K, 4096, 12288, 4),    # Qwen3-8B down_proj
     (oracle.Q4_0, 12288, 4096, 16),   # Qwen3-8B gate/up
     (oracle.Q8_0, 1024, 3072, 4),     # Qwen3-0.6B down_proj
@@ -288,7 +317,9 @@ def test_gemv_full_size_rows_subset(ctx, gtype, n, k, batch):
     rows = np.sort(np.random.default_rng(0).choice(n, size=min(512, n), replace=False))
     sub = _rows_subset(gtype, data, n, k, rows)
     wsub = oracle.dequant_gguf(gtype, sub, len(rows), k)
-    assert gemv_err(np.ascontiguousarray(y1[:, rows]), x1, wsub) <= XF16
+    # 5..16 rows on Q4_0/Q6_K take the MFMA path: f16 weights add 2^-11
+    tol = 2.0 ** -10 + 2e-5 if batch >= 5 and gtype in (oracle.Q4_0, oracle.Q6_K) else XF16
+    assert gemv_err(np.ascontiguousarray(y1[:, rows]), x1, wsub) <= tol
     # linearity over every output: y(2 x1 - x2) == 2 y(x1) - y(x2) up to the
     # activation rounding of each of the three products
     x3 = (2 * x1 - x2).astype(np.float32)
