@@ -29,8 +29,14 @@
 //     lands in [2^13, 2^14) (no overflow, no flush of the task's large values),
 //     rounded once to f16; a task's MFMAs accumulate into a zeroed tile that
 //     is then added to the f32 total times the inverse scale;
-//   * weights stream through a ring of PF tasks of raw loads per wave, each
-//     slot refilled in place once decoded;
+//   * weights stream coalesced: a task's bytes of the tile's 16 rows (one
+//     4-byte-aligned window per row) are loaded as 16-byte pieces with
+//     consecutive lanes on consecutive pieces of a row, so a load
+//     instruction touches a few cache lines rather than one per lane (the
+//     vector cache's tag rate, one line per clock, bounds lane-per-row
+//     loads at ~3.5 TB/s), through a ring of PF tasks in registers; each
+//     task's pieces then pass through a per-wave LDS window of 16 rows, from
+//     which every lane reads its row's quarter in the B layout;
 //   * a K range too long for LDS runs as segments in consecutive launches,
 //     the later ones adding to the f32 outputs.
 // Accuracy: |y - y_exact| <= (2^-11 + 2^-11 + 2^-22)·Σ|w||x| + f32 accumulation
@@ -42,6 +48,8 @@ namespace dmx {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef half2_t h2;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t __attribute__((may_alias)) u32a;  // window dwords, written as u32x4
 
 namespace {
 
@@ -69,70 +77,91 @@ __device__ __forceinline__ uint32_t wq(uint32_t c, _Float16 off, h2 s2) {
     return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, c) + o) * s2);
 }
 
-// ---- encoding policies: task shape, raw loads, decode into the NM B operands
-// (uint4 = 4 f16 pairs) and the activation runs of each operand.
+// ---- encoding policies: task shape, row windows, decode from the window
+// into the NM B operands (uint4 = 4 f16 pairs) and the activation runs of
+// each operand.  A task is 256 weights of each row (8 MFMAs); its row window
+// starts at the task's first byte rounded down to 4 (sh = the remainder, 0 or
+// 2), is loaded as NP pieces of 16 bytes, each touching only dwords that hold
+// bytes of the task (so no load leaves a page the task touches), and is kept
+// in LDS rows of WB bytes (WB / 16 odd: rows at distinct bank groups).
 
-// Q4_0: a task is 4 blocks (128 weights); lane quarter q decodes block 4t + q
-// and MFMA j takes its code dword j: low nibbles (4j, 4j+2), (4j+1, 4j+3),
-// high nibbles (16+4j, 18+4j), (17+4j, 19+4j).
+// Q4_0: a task is 8 blocks (144 bytes of a row); lane quarter q decodes
+// blocks 2q and 2q + 1, MFMA j taking code dword j & 3 of block 2q + (j >> 2):
+// low nibbles (4j', 4j'+2), (4j'+1, 4j'+3), high nibbles (16+4j', 18+4j'),
+// (17+4j', 19+4j'), j' = j & 3.
 struct MfmaQ40 {
-    static constexpr int KT = 128, NM = 4, PF = 8, TPI = 4;  // weights, MFMAs per task; ring depth; tasks per step
-    static constexpr uint32_t UNIT = 32, UPT = 4;            // weights per block, blocks per task
+    static constexpr int KT = 256, NM = 8, PF = 4, TPI = 2;  // weights, MFMAs per task; ring depth; tasks per step
+    static constexpr uint32_t UNIT = 32, UPT = 8, UB = 18;   // weights, bytes per block; blocks per task
+    static constexpr uint32_t TB = UPT * UB;                 // bytes of a row per task
+    static constexpr uint32_t NP = 10, WB = 176;             // window pieces, LDS row bytes
     static constexpr bool ROWSCALE = false;
-    static constexpr uint32_t STAGE = 16;  // staging passes per chunk of loads
-    using Raw = RawBlock<5>;
-    __device__ static uint32_t run0(uint32_t q, uint32_t j) { return 32u * q + 4u * j; }
-    __device__ static uint32_t run1(uint32_t q, uint32_t j) { return 32u * q + 16u + 4u * j; }
-    __device__ static uint32_t rowbytes(uint32_t K) { return (K / 32u) * 18u; }
-    // task t's raw loads (blocks past the segment re-read its last one)
-    __device__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u0, uint32_t nunit, uint32_t t,
-                               uint32_t q) {
-        const uint32_t blk = 4u * t + q;
-        return load_raw_block<5>(w, rowoff + (u0 + (blk < nunit ? blk : nunit - 1u)) * 18u);
-    }
-    __device__ static void decode(const Raw& r, uint32_t nunit, uint32_t t, uint32_t q, uint4 (&a)[NM], float&) {
-        const bool ok = 4u * t + q < nunit;  // past the segment: zero weights
-        const uint32_t sel = realign_sel(r.sh, 2);
-        const uint32_t db = (r.d[0] >> (8u * r.sh)) & (ok ? 0xFFFFu : 0u);
-        const h2 d2 = __builtin_bit_cast(h2, db * 0x00010001u);
+    static constexpr uint32_t STAGE = 8;  // staging passes per chunk of loads
+    // Pieces 0..8 hold window bytes [0, 144) at LDS 16i; piece 9 is [128, 144)
+    // (sh = 0) or [132, 148) (sh = 2) at LDS [144, 160), so window dword 36
+    // (sh = 2 only) sits at LDS dword 39.
+    __device__ static uint32_t goff(uint32_t piece, uint32_t sh) { return piece < 9u ? 16u * piece : 128u + 2u * sh; }
+    __device__ static uint32_t run0(uint32_t q, uint32_t j) { return 64u * q + 32u * (j >> 2) + 4u * (j & 3u); }
+    __device__ static uint32_t run1(uint32_t q, uint32_t j) { return run0(q, j) + 16u; }
+    __device__ static void decode(const u32a* win, uint32_t sh, bool ok, uint32_t q, uint4 (&a)[NM], float&) {
 #pragma unroll
-        for (int j = 0; j < NM; j++) {
-            const uint32_t D = __builtin_amdgcn_perm(r.d[j + 1], r.d[j], sel), D8 = D >> 8;
-            a[j] = make_uint4(wq(and_or(D, 0x000F000Fu, 0x64006400u), (_Float16)-1032.0f, d2),
-                              wq(and_or(D8, 0x000F000Fu, 0x64006400u), (_Float16)-1032.0f, d2),
-                              wq(and_or(D, 0x00F000F0u, 0x54005400u), (_Float16)-72.0f, d2),
-                              wq(and_or(D8, 0x00F000F0u, 0x54005400u), (_Float16)-72.0f, d2));
+        for (int h = 0; h < 2; h++) {
+            const uint32_t o = sh + UB * (2u * q + (uint32_t)h), k0 = o >> 2;  // block start in the window
+            uint32_t d[5];
+#pragma unroll
+            for (int i = 0; i < 4; i++) d[i] = win[k0 + (uint32_t)i];
+            d[4] = win[k0 + 4u == 36u ? 39u : k0 + 4u];
+            const uint32_t bsh = o & 3u, sel = realign_sel(bsh, 2);
+            const uint32_t db = (d[0] >> (8u * bsh)) & (ok ? 0xFFFFu : 0u);  // padding task: zero weights
+            const h2 d2 = __builtin_bit_cast(h2, db * 0x00010001u);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t D = __builtin_amdgcn_perm(d[j + 1], d[j], sel), D8 = D >> 8;
+                a[4 * h + j] = make_uint4(wq(and_or(D, 0x000F000Fu, 0x64006400u), (_Float16)-1032.0f, d2),
+                                          wq(and_or(D8, 0x000F000Fu, 0x64006400u), (_Float16)-1032.0f, d2),
+                                          wq(and_or(D, 0x00F000F0u, 0x54005400u), (_Float16)-72.0f, d2),
+                                          wq(and_or(D8, 0x00F000F0u, 0x54005400u), (_Float16)-72.0f, d2));
+            }
         }
     }
 };
 
-// Q6_K: a task is one super-block (256 weights); lane quarter q decodes its
-// chunk (n, s) = (q >> 1, q & 1): weights n·128 + 32g + 16s + i of groups
-// g = 0..3, i < 16 (encodings.hpp EncQ6K, gguf_codegen.rs:499-521).  MFMA
-// j = 2t + h takes code dword t (i = 4t..4t+3) of groups 2h (run0) and 2h + 1
-// (run1 = run0 + 32); groups 2 and 3 hold their low bits in the high nibble,
-// decoded under the exponent of 64.
+// Q6_K: a task is one super-block (210 bytes of a row); lane quarter q
+// decodes its chunk (n, s) = (q >> 1, q & 1): weights n·128 + 32g + 16s + i
+// of groups g = 0..3, i < 16 (encodings.hpp EncQ6K, gguf_codegen.rs:499-521).
+// MFMA j = 2t + h takes code dword t (i = 4t..4t+3) of groups 2h (run0) and
+// 2h + 1 (run1 = run0 + 32); groups 2 and 3 hold their low bits in the high
+// nibble, decoded under the exponent of 64.
 struct MfmaQ6K {
     static constexpr int KT = 256, NM = 8, PF = 4, TPI = 2;
-    static constexpr uint32_t UNIT = 256, UPT = 1;
+    static constexpr uint32_t UNIT = 256, UPT = 1, UB = 210;
+    static constexpr uint32_t TB = UB;
+    static constexpr uint32_t NP = 14, WB = 240;
     static constexpr bool ROWSCALE = true;
-    static constexpr uint32_t STAGE = 8;  // 21-dword ring slots leave room for 8
-    using Raw = EncQ6K::Raw;
+    static constexpr uint32_t STAGE = 8;
+    // Pieces 0..12 hold window bytes [0, 208) at LDS 16i; piece 13 is
+    // [196, 212) at LDS [208, 224), so window dword 52 (d) sits at LDS dword 55.
+    __device__ static uint32_t goff(uint32_t piece, uint32_t) { return piece < 13u ? 16u * piece : 196u; }
     __device__ static uint32_t run0(uint32_t q, uint32_t j) {
         return 128u * (q >> 1) + 64u * (j & 1u) + 16u * (q & 1u) + 4u * (j >> 1);
     }
     __device__ static uint32_t run1(uint32_t q, uint32_t j) { return run0(q, j) + 32u; }
-    __device__ static uint32_t rowbytes(uint32_t K) { return (K / 256u) * 210u; }
-    __device__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u0, uint32_t nunit, uint32_t t,
-                               uint32_t q) {
-        return EncQ6K::load(w, rowoff, 4u * (u0 + (t < nunit ? t : nunit - 1u)) + q);
-    }
-    __device__ static void decode(const Raw& r, uint32_t nunit, uint32_t t, uint32_t q, uint4 (&a)[NM], float& d) {
+    __device__ static void decode(const u32a* win, uint32_t sh, bool ok, uint32_t q, uint4 (&a)[NM], float& d) {
+        EncQ6K::Raw r;
+        const uint32_t n = q >> 1, s = q & 1u;
+        const uint32_t oa = (64u * n + 16u * s) >> 2, oh = (128u + 32u * n + 16u * s) >> 2;
+#pragma unroll
+        for (int i = 0; i < 5; i++) {
+            r.a[i] = win[oa + (uint32_t)i];
+            r.b[i] = win[oa + 8u + (uint32_t)i];
+            r.h[i] = win[oh + (uint32_t)i];
+            r.s[i] = win[i < 4 ? 48u + (uint32_t)i : 55u];  // sc[0..16), d
+        }
+        r.sh = sh;
         uint32_t A[4], B[4], H[4];
         EncQ6K::codes(r, A, B, H);
         int32_t sc[4];
         EncQ6K::scales(r, q, sc, d);
-        d = t < nunit ? d : 0.0f;  // past the segment: zero weights
+        d = ok ? d : 0.0f;  // padding task: zero weights
         h2 s2[4];
 #pragma unroll
         for (int g = 0; g < 4; g++) {
@@ -159,16 +188,17 @@ struct MfmaQ6K {
     }
 };
 
-// LDS: activations [task][j][64 lanes] x 16 bytes, then the inverse scales
-// [task][16 rows] f32.  Tasks of a segment are padded to a multiple of PF
-// (the padding tasks have zero weights and activations).
+// LDS: activations [task][j][64 lanes] x 16 bytes, the inverse scales
+// [task][16 rows] f32, then each wave's window of 16 rows x WB bytes.  Tasks
+// of a segment are padded to a multiple of PF (the padding tasks have zero
+// weights and activations).
 template <class M>
 __host__ __device__ constexpr uint32_t mfma_tasks(uint32_t nunit) {
     return ((nunit + M::UPT - 1u) / M::UPT + M::PF - 1u) / M::PF * M::PF;
 }
 template <class M>
 __host__ __device__ constexpr uint32_t mfma_lds_bytes(uint32_t nunit) {
-    return mfma_tasks<M>(nunit) * (M::NM * 64u * 16u + 64u);
+    return mfma_tasks<M>(nunit) * (M::NM * 64u * 16u + 64u) + (kMfmaThreads / 64u) * 16u * M::WB;
 }
 
 // Slot of A-operand lane l (row b = l % 16, quarter q = l / 16) in the 64
@@ -184,10 +214,12 @@ template <class M, bool YBF16>
 __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr uint32_t NM = M::NM, UPR = 4u * NM;  // staging units per (task, row): (q, j)
-    const uint32_t ng = mfma_tasks<M>(p.nunit);
+    constexpr uint32_t NSLOT = 16u * M::NP, NLD = (NSLOT + 63u) / 64u;  // window pieces, loads per lane
+    const uint32_t ng = mfma_tasks<M>(p.nunit), nt = p.nunit / M::UPT;  // tasks with padding, without
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
     uint4* xl = reinterpret_cast<uint4*>(lds);
     float* inv = reinterpret_cast<float*>(lds + ng * NM * 64u * 16u);
-    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    uint8_t* win = lds + ng * (NM * 64u * 16u + 64u) + (tid >> 6) * 16u * M::WB;  // this wave's window
 
     // ---- weight tiles: wave wid takes tiles wid, wid + W, ..., waves numbered
     // across workgroups first (wave i of workgroup w is wid = i·grid + w), so
@@ -196,7 +228,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     const uint32_t W = p.grid * (kMfmaThreads / 64u);
     const uint32_t m = lane & 15u, q = lane >> 4;
     const uint32_t ntw = wid < p.total_tiles ? (p.total_tiles - wid + W - 1u) / W : 0u;  // tiles of this wave
-    const uint32_t rowbytes = M::rowbytes(p.K), u0 = p.k0 / M::UNIT;
+    const uint32_t rowbytes = (p.K / M::UNIT) * M::UB, seg0 = (p.k0 / M::UNIT) * M::UB;
 
     // the wave's i-th tile (past the end: its last, or any tile for a wave
     // without tiles: loaded, never multiplied into a stored result)
@@ -221,43 +253,69 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
         r.row0 = (tile - pick(pi, p.tile_begin)) * 16u;
         return r;
     };
-    // a tile's weight base and the byte offset of this lane's row (rows past
+    // Window pieces of this lane: piece slot 64i + lane (the slots past the
+    // last re-load it) is piece pc[i] of tile row pr[i], stored at LDS
+    // lo[i] of the window.
+    uint32_t pr[NLD], pc[NLD], lo[NLD];
+#pragma unroll
+    for (uint32_t i = 0; i < NLD; i++) {
+        const uint32_t sl = 64u * i + lane < NSLOT ? 64u * i + lane : NSLOT - 1u;
+        pr[i] = sl / M::NP;
+        pc[i] = sl % M::NP;
+        lo[i] = pr[i] * M::WB + 16u * pc[i];
+    }
+    // a tile's 4-byte-aligned weight base and the byte offsets (from it) of
+    // the segment's start in this lane's decode row and load rows (rows past
     // the problem re-read its last one: in bounds, never stored)
     struct Rows {
-        const uint8_t* w;
-        uint32_t off;
+        const uint8_t* abase;
+        uint32_t om;
+        uint32_t oi[NLD];
     };
     auto rows_of = [&](const Where& wh) {
-        const uint32_t row = wh.row0 + m < wh.n ? wh.row0 + m : wh.n - 1u;
-        return Rows{wh.w, row * rowbytes};
+        const uint32_t bsh = (uint32_t)((uintptr_t)wh.w & 3u);
+        auto off = [&](uint32_t r) { return (wh.row0 + r < wh.n ? wh.row0 + r : wh.n - 1u) * rowbytes + bsh + seg0; };
+        Rows r;
+        r.abase = wh.w - bsh;
+        r.om = off(m);
+#pragma unroll
+        for (uint32_t i = 0; i < NLD; i++) r.oi[i] = off(pr[i]);
+        return r;
     };
-    auto load = [&](const Rows& r, uint32_t t) { return M::load(r.w, r.off, u0, p.nunit, t, q); };
+    // task t's window start from a row's segment offset (padding tasks
+    // re-read the last task)
+    auto task_off = [&](uint32_t o, uint32_t t) { return o + (t < nt ? t : nt - 1u) * M::TB; };
+    auto load = [&](const Rows& r, uint32_t t, u32x4 (&v)[NLD]) {
+#pragma unroll
+        for (uint32_t i = 0; i < NLD; i++) {
+            const uint32_t o = task_off(r.oi[i], t);
+            v[i] = *gptr<u32x4>(r.abase + (o & ~3u) + M::goff(pc[i], o & 3u));
+        }
+    };
     // the first PF tasks' weight loads leave before the activations are staged
     Where wcur = where(tile_at(0u));
     Rows rcur = rows_of(wcur);
-    typename M::Raw ring[M::PF];
+    u32x4 ring[M::PF][NLD];
 #pragma unroll
-    for (int s = 0; s < M::PF; s++) ring[s] = load(rcur, (uint32_t)s);  // ng >= PF: all in tile 0
+    for (int s = 0; s < M::PF; s++) load(rcur, (uint32_t)s, ring[s]);  // ng >= PF: all in tile 0
 
     // ---- stage the activations: unit u = (task g, row b, e = q·NM + j); the
-    // UPR units of (g, b) lie on consecutive lanes (16 or 32), their maximum
-    // reduced by DPP within rows of 16 lanes and v_permlane16_swap across two.
-    // Chunks of passes: all of a chunk's loads leave before the first is
-    // converted.
+    // 32 units of (g, b) lie on consecutive lanes, their maximum reduced by
+    // DPP within rows of 16 lanes and v_permlane16_swap across two.  Chunks
+    // of passes: all of a chunk's loads leave before the first is converted.
     const uint32_t nunits = ng * 16u * UPR, npass = (nunits + kMfmaThreads - 1u) / kMfmaThreads;
     auto xload = [&](uint32_t pass, float (&v)[8]) {
         const uint32_t u = pass * kMfmaThreads + tid;
         const uint32_t g = u / (16u * UPR), b = (u / UPR) % 16u, e = u % UPR, qq = e / NM, j = e % NM;
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = 0.0f;
-        const bool ok = M::UPT * g + (M::UPT == 1 ? 0u : qq) < p.nunit;  // the unit holding these k
-        if (u < nunits && b < p.batch && ok) {
+        if (u < nunits && b < p.batch && g < nt) {
             const float* xr = p.x + (size_t)b * p.K + p.k0 + M::KT * g;
-            const f32x4 lo = *gptr<f32x4>(xr + M::run0(qq, j)), hi = *gptr<f32x4>(xr + M::run1(qq, j));
+            const f32x4 lo4 = *gptr<f32x4>(xr + M::run0(qq, j)), hi4 = *gptr<f32x4>(xr + M::run1(qq, j));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                v[i] = lo[i];
-                v[4 + i] = hi[i];
+                v[i] = lo4[i];
+                v[4 + i] = hi4[i];
             }
         }
     };
@@ -271,7 +329,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
         uint32_t mx = __float_as_uint(mv);  // non-negative floats order as integers
         mx = lanes_reduce<8>(mx, [](uint32_t a, uint32_t c) { return a > c ? a : c; });
         mx = max(mx, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0x140, 0xF, 0xF, false));  // row_mirror: 16 lanes
-        if constexpr (UPR == 32) {  // and the neighbouring row of 16
+        {  // and the neighbouring row of 16
             const auto r = __builtin_amdgcn_permlane16_swap(mx, mx, false, false);
             mx = max(r[0], r[1]);
         }
@@ -291,6 +349,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
             if (e == 0) inv[g * 16u + b] = ldexpf(1.0f, -sh);
         }
     };
+    static_assert(UPR == 32, "a (task, row) spans two rows of 16 lanes");
     constexpr uint32_t kStageChunk = M::STAGE;
     for (uint32_t c0 = 0; c0 < npass; c0 += kStageChunk) {
         float v[kStageChunk][8];
@@ -304,16 +363,19 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
 
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 acc = zero;
-    // one task's product: decode the lane's quarter and run the task's MFMAs
-    // into a zeroed tile; rs = the lane's row scale (Q6_K's d)
-    auto product = [&](const typename M::Raw& r, uint32_t t, float& rs) {
-        // the activation fragments' LDS reads leave before the decode, so
-        // their latency hides behind it
+    // One task's product: its pieces into the wave's window (a wave's LDS
+    // accesses complete in order, so the reads below see them and the next
+    // task's writes wait for these reads), the lane's quarter decoded from
+    // its row, and the task's MFMAs into a zeroed tile; rs = the row scale
+    // (Q6_K's d).
+    auto product = [&](const u32x4 (&v)[NLD], const Rows& r, uint32_t t, float& rs) {
+#pragma unroll
+        for (uint32_t i = 0; i < NLD; i++) *reinterpret_cast<u32x4*>(win + lo[i]) = v[i];
         uint4 xa[NM];
 #pragma unroll
         for (uint32_t j = 0; j < NM; j++) xa[j] = xl[(t * NM + j) * 64u + xslot(lane, j)];
         uint4 a[NM];
-        M::decode(r, p.nunit, t, q, a, rs);
+        M::decode(reinterpret_cast<const u32a*>(win + m * M::WB), task_off(r.om, t) & 3u, t < nt, q, a, rs);
         f32x4 tmp = zero;
 #pragma unroll
         for (uint32_t j = 0; j < NM; j++)
@@ -322,10 +384,10 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     };
     // Tiles outer, tasks inner (ng is a multiple of PF, so ring slot s of
     // inner step g0 + s is static).  TPI tasks at a time (independent MFMA
-    // chains); their slots are refilled, once decoded, with the tasks PF
-    // later, which cross into the next tile at the end of one.  Each tile's
-    // outputs are stored after its last task, outside the loop whose loads
-    // stay in flight: no load sits under a branch.
+    // chains); their slots are refilled, once stored to the window, with the
+    // tasks PF later, which cross into the next tile at the end of one.  Each
+    // tile's outputs are stored after its last task, outside the loop whose
+    // loads stay in flight: no load sits under a branch.
     for (uint32_t i = 0; i < ntw; i++) {
         const Where wnxt = where(tile_at(i + 1u));
         const Rows rnxt = rows_of(wnxt);
@@ -333,24 +395,23 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
 #pragma unroll
             for (int s = 0; s < M::PF; s += M::TPI) {
                 const uint32_t g = g0 + (uint32_t)s;
-                f32x4 pr[M::TPI];
+                f32x4 prd[M::TPI];
                 float rs[M::TPI];
 #pragma unroll
-                for (int k = 0; k < M::TPI; k++) pr[k] = product(ring[s + k], g + (uint32_t)k, rs[k]);
-                // refill the slots in place once decoded (the same registers
-                // across iterations: no copies that would wait for the loads)
+                for (int k = 0; k < M::TPI; k++) prd[k] = product(ring[s + k], rcur, g + (uint32_t)k, rs[k]);
+                // refill the slots in place (the same registers across
+                // iterations: no copies that would wait for the loads)
                 const bool wrap = g + M::PF >= ng;  // the refills belong to the next tile
-                const Rows rr = wrap ? rnxt : rcur;
                 const uint32_t gn = wrap ? g + M::PF - ng : g + M::PF;
 #pragma unroll
-                for (int k = 0; k < M::TPI; k++) ring[s + k] = load(rr, gn + (uint32_t)k);
+                for (int k = 0; k < M::TPI; k++) load(wrap ? rnxt : rcur, gn + (uint32_t)k, ring[s + k]);
 #pragma unroll
                 for (int k = 0; k < M::TPI; k++) {
                     // inverse activation scales of rows 4q..4q+3
                     f32x4 sc = *reinterpret_cast<const f32x4*>(inv + (g + (uint32_t)k) * 16u + 4u * q);
                     if constexpr (M::ROWSCALE) sc *= rs[k];
 #pragma unroll
-                    for (int c = 0; c < 4; c++) acc[c] = fmaf(pr[k][c], sc[c], acc[c]);
+                    for (int c = 0; c < 4; c++) acc[c] = fmaf(prd[k][c], sc[c], acc[c]);
                 }
             }
         }
@@ -369,8 +430,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
                         (void)__hip_atomic_fetch_add(gptr_mut<float>(wcur.y) + idx, acc[c], __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
                     }
-                }
-                else gptr_mut<float>(wcur.y)[idx] = acc[c];
+                } else gptr_mut<float>(wcur.y)[idx] = acc[c];
             }
         }
         acc = zero;
@@ -447,7 +507,7 @@ hipError_t launch_mfma(const GemvProblem* probs, int nprob, uint32_t K, const vo
 
 bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool x_bf16,
                        bool y_bf16) {
-    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K) || x_bf16 || batch < 5 || batch > 16) return false;
+    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K) || x_bf16 || batch < 5 || batch > 16 || K % 256u) return false;
     uint32_t tiles = 0;
     for (int i = 0; i < nprob; i++) tiles += (probs[i].n + 15u) / 16u;
     if (tiles < kMfmaMinTiles) return false;

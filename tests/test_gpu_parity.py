@@ -142,15 +142,17 @@ def test_gemv_multi_qkv(ctx, batch):
         assert err <= XF16, err
 
 
-# 5..16 activation rows on at least 384 tiles of 16 weight rows take the MFMA
-# GEMV (every weight decoded once for all rows): ragged rows, K needing
-# padding tasks (Q4_0 1056 = 33 blocks, Q6_K 2304 = 9 super-blocks, rows
-# alternating 4- and 2-byte alignment), K split over LDS segments (12288:
-# three launches, the later ones adding with atomics), bf16 outputs, a
-# weight base 2 bytes past a 4-byte boundary.
+# 5..16 activation rows on at least 384 tiles of 16 weight rows (K a
+# multiple of 256) take the MFMA GEMV (every weight decoded once for all
+# rows): ragged rows, task counts needing padding tasks (Q4_0 1280 = 5 tasks
+# of 8 blocks, Q6_K 2304 = 9 super-blocks, rows alternating 4- and 2-byte
+# alignment), K split over LDS segments (12288: three launches, the later
+# ones adding with atomics), bf16 outputs, a weight base 2 bytes past a
+# 4-byte boundary; K = 1056 (not whole tasks) stays on the VALU GEMV.
 MFMA_CASES = [
     (oracle.Q4_0, 6144, 1024, 5, False, 0), (oracle.Q4_0, 6144, 1024, 16, False, 0),
-    (oracle.Q4_0, 6150, 1056, 9, False, 2), (oracle.Q4_0, 6144, 4096, 16, True, 0),
+    (oracle.Q4_0, 6150, 1280, 9, False, 2), (oracle.Q4_0, 6150, 1056, 9, False, 2),
+    (oracle.Q4_0, 6144, 4096, 16, True, 0),
     (oracle.Q4_0, 6144, 12288, 7, False, 0), (oracle.Q4_0, 8000, 2048, 12, True, 0),
     (oracle.Q6_K, 6144, 1024, 5, False, 0), (oracle.Q6_K, 6144, 4096, 16, True, 0),
     (oracle.Q6_K, 6150, 2304, 9, False, 2), (oracle.Q6_K, 6144, 12288, 7, False, 0),
