@@ -425,13 +425,17 @@ hipError_t gemm_q4_0_launch(const uint8_t* w, uint32_t N, uint32_t K, const void
     const uint32_t yb = y_bf16 ? 1u : 0u;
     auto tiles = [&](uint32_t bm, uint32_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     // The largest tile (most reuse of each decoded weight and converted
-    // activation) that still gives most CUs a workgroup; smaller problems take
-    // the smallest tile.  The 128x128 tile runs eight producer waves beside its
-    // eight MMA waves.  (Chosen from timing sweeps of M in {128, 512, 2048} at
-    // the Qwen3-0.6B FFN shapes.)
+    // activation) that still gives most CUs a workgroup.  The 128x128 tile
+    // runs eight producer waves beside its eight MMA waves.  Launches too small
+    // for these tiles take the K-split kernel (K a multiple of 256), whose four
+    // waves per tile each multiply a quarter of K.  (Chosen from timing sweeps
+    // of M in {128, 512, 2048} at the Qwen3-0.6B FFN shapes: at M = 128 and
+    // for K = 3072 the K-split kernel takes 40-60% less time, at M = 512 with
+    // 192 tiles of 128x64 5% more.)
     constexpr uint32_t kCus = 256;
     if (tiles(128, 128) >= kCus) return launch_tile<128, 128, 2, 4, 8, 64, 2>(w, N, K, xp, M, y, yb, stream);
     if (tiles(128, 64) >= kCus * 3 / 4) return launch_tile<128, 64, 4, 2, 0, 128, 2>(w, N, K, xp, M, y, yb, stream);
+    if (gemm_q4_0_ks_supported(N, K, M)) return gemm_q4_0_ks_launch(w, N, K, x, M, y, y_bf16, stream);
     return launch_tile<64, 64, 2, 2, 0, 128, 2>(w, N, K, xp, M, y, yb, stream);
 }
 

@@ -93,4 +93,10 @@ hipError_t gemm_q4_0_launch(const uint8_t* w, uint32_t N, uint32_t K, const void
 // Shape limits of the GEMM kernel (checked by the C ABI before launching).
 bool gemm_q4_0_supported(uint32_t N, uint32_t K, uint32_t M);
 
+// The K-split GEMM (K a multiple of 256): each wave of a workgroup multiplies
+// a quarter of K for the whole tile; gemm_q4_0_launch routes to it.
+bool gemm_q4_0_ks_supported(uint32_t N, uint32_t K, uint32_t M);
+hipError_t gemm_q4_0_ks_launch(const uint8_t* w, uint32_t N, uint32_t K, const void* x, uint32_t M, void* y,
+                               bool y_bf16, hipStream_t stream);
+
 }  // namespace dmx

@@ -257,6 +257,18 @@ def test_gemm_q4_0(ctx, m, n, k, ybf16):
     assert np.all(err <= TOL + extra), err.max()
 
 
+@pytest.mark.parametrize("m,n,k", [(200, 384, 1024), (512, 3072, 1024), (96, 1040, 2048), (512, 1024, 3072), (130, 2000, 768)])
+def test_gemm_q4_0_offset_weights(ctx, m, n, k):
+    # weight blocks starting 2 bytes past a 4-byte boundary (GGUF tensors are
+    # only 2-byte aligned); ragged row and column tiles
+    w, data = gguf(oracle.Q4_0, n, k, seed=m * 3 + n + k, off=2)
+    xb = oracle.f32_to_bf16_bits(oracle.randn(m * k, seed=m + 1)).reshape(m, k)
+    x = oracle.bf16_bits_to_f32(xb)
+    y = ctx.qlinear(w, dev(xb).view(torch.bfloat16)).cpu().numpy()
+    err = gemv_err(y, x, oracle.dequant_gguf(oracle.Q4_0, data, n, k))
+    assert err <= 2.0 ** -11 + 1e-5, err
+
+
 def _q4_0_blocks(codes: np.ndarray, d_bits: np.ndarray) -> np.ndarray:
     """GGUF Q4_0 bytes from codes [n, k] (0..15) and f16 scale bits [n, k/32]:
     byte l of a block holds k = l (low nibble) and k = 16 + l (high nibble)."""
