@@ -192,13 +192,16 @@ struct MfmaQ6K {
 // [task][16 rows] f32, then each wave's window of 16 rows x WB bytes.  Tasks
 // of a segment are padded to a multiple of PF (the padding tasks have zero
 // weights and activations).
-template <class M>
+// Split mode (few tiles): the 8 waves of a workgroup share each tile, wave w
+// taking tasks [w·T/8, (w+1)·T/8) with a ring of 2, so T is a multiple of 16.
+template <class M, bool SPLIT>
 __host__ __device__ constexpr uint32_t mfma_tasks(uint32_t nunit) {
-    return ((nunit + M::UPT - 1u) / M::UPT + M::PF - 1u) / M::PF * M::PF;
+    constexpr uint32_t pad = SPLIT ? 16u : (uint32_t)M::PF;
+    return ((nunit + M::UPT - 1u) / M::UPT + pad - 1u) / pad * pad;
 }
-template <class M>
+template <class M, bool SPLIT>
 __host__ __device__ constexpr uint32_t mfma_lds_bytes(uint32_t nunit) {
-    return mfma_tasks<M>(nunit) * (M::NM * 64u * 16u + 64u) + (kMfmaThreads / 64u) * 16u * M::WB;
+    return mfma_tasks<M, SPLIT>(nunit) * (M::NM * 64u * 16u + 64u) + (kMfmaThreads / 64u) * 16u * M::WB;
 }
 
 // Slot of A-operand lane l (row b = l % 16, quarter q = l / 16) in the 64
@@ -210,22 +213,29 @@ __device__ __forceinline__ uint32_t xslot(uint32_t l, uint32_t j) { return l ^ (
 
 }  // namespace
 
-template <class M, bool YBF16>
+template <class M, bool YBF16, bool SPLIT>
 __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr uint32_t NM = M::NM, UPR = 4u * NM;  // staging units per (task, row): (q, j)
     constexpr uint32_t NSLOT = 16u * M::NP, NLD = (NSLOT + 63u) / 64u;  // window pieces, loads per lane
-    const uint32_t ng = mfma_tasks<M>(p.nunit), nt = p.nunit / M::UPT;  // tasks with padding, without
+    constexpr int PF = SPLIT ? 2 : M::PF;  // tasks of raw loads in flight per wave
+    constexpr uint32_t NW = kMfmaThreads / 64u;
+    const uint32_t ng = mfma_tasks<M, SPLIT>(p.nunit), nt = p.nunit / M::UPT;  // tasks with padding, without
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint4* xl = reinterpret_cast<uint4*>(lds);
     float* inv = reinterpret_cast<float*>(lds + ng * NM * 64u * 16u);
-    uint8_t* win = lds + ng * (NM * 64u * 16u + 64u) + (tid >> 6) * 16u * M::WB;  // this wave's window
+    uint8_t* wins = lds + ng * (NM * 64u * 16u + 64u);  // the waves' windows
+    uint8_t* win = wins + wv * 16u * M::WB;             // this wave's window
 
-    // ---- weight tiles: wave wid takes tiles wid, wid + W, ..., waves numbered
-    // across workgroups first (wave i of workgroup w is wid = i·grid + w), so
-    // a few tiles still spread over all CUs
-    const uint32_t wid = __builtin_amdgcn_readfirstlane((tid >> 6) * p.grid + blockIdx.x);
-    const uint32_t W = p.grid * (kMfmaThreads / 64u);
+    // ---- weight tiles.  Whole tiles per wave: wave wid takes tiles wid,
+    // wid + W, ..., waves numbered across workgroups first (wave i of
+    // workgroup w is wid = i·grid + w), so a few tiles still spread over all
+    // CUs.  Split mode: workgroup w takes tiles w, w + grid, ... and its waves
+    // split each tile's tasks (wave v: tasks t0 = v·tpw .. t0 + tpw - 1).
+    const uint32_t wid = SPLIT ? blockIdx.x : __builtin_amdgcn_readfirstlane(wv * p.grid + blockIdx.x);
+    const uint32_t W = SPLIT ? p.grid : p.grid * NW;
+    const uint32_t tpw = SPLIT ? ng / NW : ng, t0 = SPLIT ? wv * tpw : 0u;
     const uint32_t m = lane & 15u, q = lane >> 4;
     const uint32_t ntw = wid < p.total_tiles ? (p.total_tiles - wid + W - 1u) / W : 0u;  // tiles of this wave
     const uint32_t rowbytes = (p.K / M::UNIT) * M::UB, seg0 = (p.k0 / M::UNIT) * M::UB;
@@ -295,9 +305,9 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     // the first PF tasks' weight loads leave before the activations are staged
     Where wcur = where(tile_at(0u));
     Rows rcur = rows_of(wcur);
-    u32x4 ring[M::PF][NLD];
+    u32x4 ring[PF][NLD];
 #pragma unroll
-    for (int s = 0; s < M::PF; s++) load(rcur, (uint32_t)s, ring[s]);  // ng >= PF: all in tile 0
+    for (int s = 0; s < PF; s++) load(rcur, t0 + (uint32_t)s, ring[s]);  // tpw >= PF: all in tile 0
 
     // ---- stage the activations: unit u = (task g, row b, e = q·NM + j); the
     // 32 units of (g, b) lie on consecutive lanes, their maximum reduced by
@@ -382,27 +392,27 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
             tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, xa[j]), __builtin_bit_cast(h8, a[j]), tmp, 0, 0, 0);
         return tmp;
     };
-    // Tiles outer, tasks inner (ng is a multiple of PF, so ring slot s of
-    // inner step g0 + s is static).  TPI tasks at a time (independent MFMA
-    // chains); their slots are refilled, once stored to the window, with the
-    // tasks PF later, which cross into the next tile at the end of one.  Each
-    // tile's outputs are stored after its last task, outside the loop whose
-    // loads stay in flight: no load sits under a branch.
+    // Tiles outer, the wave's tasks inner (tpw is a multiple of PF, so ring
+    // slot s of inner step g0 + s is static).  TPI tasks at a time
+    // (independent MFMA chains); their slots are refilled, once stored to the
+    // window, with the tasks PF later, which cross into the next tile at the
+    // end of one.  Each tile's outputs are stored after its last task, outside
+    // the loop whose loads stay in flight: no load sits under a branch.
     for (uint32_t i = 0; i < ntw; i++) {
         const Where wnxt = where(tile_at(i + 1u));
         const Rows rnxt = rows_of(wnxt);
-        for (uint32_t g0 = 0; g0 < ng; g0 += M::PF) {
+        for (uint32_t g0 = 0; g0 < tpw; g0 += PF) {
 #pragma unroll
-            for (int s = 0; s < M::PF; s += M::TPI) {
-                const uint32_t g = g0 + (uint32_t)s;
+            for (int s = 0; s < PF; s += M::TPI) {
+                const uint32_t g = t0 + g0 + (uint32_t)s;
                 f32x4 prd[M::TPI];
                 float rs[M::TPI];
 #pragma unroll
                 for (int k = 0; k < M::TPI; k++) prd[k] = product(ring[s + k], rcur, g + (uint32_t)k, rs[k]);
                 // refill the slots in place (the same registers across
                 // iterations: no copies that would wait for the loads)
-                const bool wrap = g + M::PF >= ng;  // the refills belong to the next tile
-                const uint32_t gn = wrap ? g + M::PF - ng : g + M::PF;
+                const bool wrap = g0 + (uint32_t)s + PF >= tpw;  // the refills belong to the next tile
+                const uint32_t gn = wrap ? g + PF - tpw : g + PF;
 #pragma unroll
                 for (int k = 0; k < M::TPI; k++) load(wrap ? rnxt : rcur, gn + (uint32_t)k, ring[s + k]);
 #pragma unroll
@@ -415,12 +425,23 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
                 }
             }
         }
+        if constexpr (SPLIT) {
+            // the waves' partial tiles meet in their windows (a wave's last
+            // window reads precede these writes: in order); wave 0 adds and
+            // stores, then every window may be refilled
+            *reinterpret_cast<f32x4*>(win + 16u * lane) = acc;
+            __syncthreads();
+            if (wv == 0u) {
+#pragma unroll
+                for (uint32_t v = 1; v < NW; v++) acc += *reinterpret_cast<const f32x4*>(wins + v * 16u * M::WB + 16u * lane);
+            }
+        }
         // lane l holds weight row l % 16 of activation rows 4q..4q+3
         const uint32_t row = wcur.row0 + m;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const uint32_t b = 4u * q + (uint32_t)c;
-            if (b < p.batch && row < wcur.n) {
+            if ((!SPLIT || wv == 0u) && b < p.batch && row < wcur.n) {
                 const size_t idx = (size_t)b * wcur.n + row;
                 if constexpr (YBF16) gptr_mut<uint16_t>(wcur.y)[idx] = f32_to_bf16_bits(acc[c]);
                 else if (p.accumulate) {  // later K segments
@@ -433,6 +454,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
                 } else gptr_mut<float>(wcur.y)[idx] = acc[c];
             }
         }
+        if constexpr (SPLIT) __syncthreads();
         acc = zero;
         wcur = wnxt;
         rcur = rnxt;
@@ -441,25 +463,57 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
 
 namespace {
 
-// Launches with fewer than kMfmaMinTiles 16-row tiles stay on the VALU GEMV:
-// each workgroup stages all activations (~6-9 us at K = 4096, batch 16)
-// and a wave multiplies its tile's tasks in sequence, which only pays off
-// when the weights are many (measured on the 8B Q4_0 shapes at batch 16:
-// 4096 rows 28 us on MFMA against 22 us on VALU, 6144 rows 21 against 32,
-// 24576 rows 28 against 76).
+// Modes (measured on the 8B shapes at batch 16, split / whole tiles / VALU):
+// below kMfmaSplitTiles 16-row tiles the eight waves of a workgroup share
+// each tile (split mode: 4096x12288 Q6_K 41 / 57 / 80 us, 4096x4096 Q4_0
+// 11.7 / 15.3 / 22.7 us, q/k/v 13.9 / 15.9 / 32.8 us) when a segment has at
+// least 8 tasks (one per wave); otherwise a wave takes whole tiles, which
+// pays from kMfmaMinTiles tiles on (each workgroup stages all activations, a
+// few microseconds, before its first product: lm_head 124 us whole tiles,
+// 148 us split, 690 us VALU).
 constexpr uint32_t kMfmaMinTiles = 384;
+constexpr uint32_t kMfmaSplitTiles = 1024;
 
 // Units per launch: the fewest segments whose LDS fits, whole tasks each
 // except the last.
-template <class M>
+template <class M, bool SPLIT>
 uint32_t mfma_segment(uint32_t units) {
     for (uint32_t nseg = 1; nseg <= units; nseg++) {
         uint32_t seg = (units + nseg - 1u) / nseg;
         seg = nseg > 1 ? (seg + M::UPT - 1u) / M::UPT * M::UPT : seg;
-        if (mfma_lds_bytes<M>(seg) <= kLdsBytes) return seg;
+        if (mfma_lds_bytes<M, SPLIT>(seg) <= kLdsBytes) return seg;
     }
     return 0;
 }
+
+template <class M, bool SPLIT>
+hipError_t launch_mode(MfmaParams p, uint32_t units, bool y_bf16, hipStream_t st) {
+    const uint32_t seg = mfma_segment<M, SPLIT>(units);
+    if (seg == 0 || (y_bf16 && seg < units)) return hipErrorInvalidValue;
+    auto kernel = y_bf16 ? gemv_mfma_kernel<M, true, SPLIT> : gemv_mfma_kernel<M, false, SPLIT>;
+    for (uint32_t b0 = 0; b0 < units; b0 += seg) {
+        const uint32_t nu = units - b0 < seg ? units - b0 : seg;
+        const size_t lds = mfma_lds_bytes<M, SPLIT>(nu);
+        int cus = 0, per_cu = 0;
+        hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, kMfmaThreads, &per_cu, &cus);
+        if (e != hipSuccess) return e;
+        if (per_cu < 1) return hipErrorInvalidConfiguration;
+        // every CU gets a workgroup while there are tiles: the tiles spread over
+        // the workgroups first
+        const uint64_t cap = (uint64_t)per_cu * cus;
+        p.grid = (uint32_t)(p.total_tiles < cap ? p.total_tiles : cap);
+        p.k0 = b0 * M::UNIT;
+        p.nunit = nu;
+        p.accumulate = b0 > 0 ? 1u : 0u;
+        hipLaunchKernelGGL(kernel, dim3(p.grid), dim3(kMfmaThreads), lds, st, p);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+template <class M>
+int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16);
 
 template <class M>
 hipError_t launch_mfma(const GemvProblem* probs, int nprob, uint32_t K, const void* x, uint32_t batch, bool y_bf16,
@@ -479,28 +533,22 @@ hipError_t launch_mfma(const GemvProblem* probs, int nprob, uint32_t K, const vo
     p.K = K;
     p.batch = batch;
     p.x = static_cast<const float*>(x);
-    const uint32_t units = K / M::UNIT, seg = mfma_segment<M>(units);
-    if (seg == 0 || (y_bf16 && seg < units)) return hipErrorInvalidValue;
-    auto kernel = y_bf16 ? gemv_mfma_kernel<M, true> : gemv_mfma_kernel<M, false>;
-    for (uint32_t b0 = 0; b0 < units; b0 += seg) {
-        const uint32_t nu = units - b0 < seg ? units - b0 : seg;
-        const size_t lds = mfma_lds_bytes<M>(nu);
-        int cus = 0, per_cu = 0;
-        hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, kMfmaThreads, &per_cu, &cus);
-        if (e != hipSuccess) return e;
-        if (per_cu < 1) return hipErrorInvalidConfiguration;
-        // every CU gets a workgroup while there are tiles: the tiles spread over
-        // the workgroups first (wave numbering in the kernel)
-        const uint64_t cap = (uint64_t)per_cu * cus;
-        p.grid = (uint32_t)(tiles < cap ? tiles : cap);
-        p.k0 = b0 * M::UNIT;
-        p.nunit = nu;
-        p.accumulate = b0 > 0 ? 1u : 0u;
-        hipLaunchKernelGGL(kernel, dim3(p.grid), dim3(kMfmaThreads), lds, st, p);
-        e = hipGetLastError();
-        if (e != hipSuccess) return e;
+    const uint32_t units = K / M::UNIT;
+    return mfma_mode<M>(K, tiles, y_bf16) == 2 ? launch_mode<M, true>(p, units, y_bf16, st)
+                                       : launch_mode<M, false>(p, units, y_bf16, st);
+}
+
+// 2: split mode, 1: whole tiles per wave, 0: not on MFMA (with bf16 outputs
+// only a single segment)
+template <class M>
+int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16) {
+    const uint32_t units = K / M::UNIT;
+    if (tiles < kMfmaSplitTiles) {
+        const uint32_t seg = mfma_segment<M, true>(units);
+        if (seg / M::UPT >= 8u && (!y_bf16 || seg == units)) return 2;
     }
-    return hipSuccess;
+    const uint32_t seg = mfma_segment<M, false>(units);
+    return tiles >= kMfmaMinTiles && seg > 0 && (!y_bf16 || seg == units) ? 1 : 0;
 }
 
 }  // namespace
@@ -510,11 +558,7 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     if ((enc != ENC_Q4_0 && enc != ENC_Q6_K) || x_bf16 || batch < 5 || batch > 16 || K % 256u) return false;
     uint32_t tiles = 0;
     for (int i = 0; i < nprob; i++) tiles += (probs[i].n + 15u) / 16u;
-    if (tiles < kMfmaMinTiles) return false;
-    // bf16 outputs cannot add up segments
-    const uint32_t units = enc == ENC_Q4_0 ? K / MfmaQ40::UNIT : K / MfmaQ6K::UNIT;
-    const uint32_t seg = enc == ENC_Q4_0 ? mfma_segment<MfmaQ40>(units) : mfma_segment<MfmaQ6K>(units);
-    return seg > 0 && (!y_bf16 || seg == units);
+    return (enc == ENC_Q4_0 ? mfma_mode<MfmaQ40>(K, tiles, y_bf16) : mfma_mode<MfmaQ6K>(K, tiles, y_bf16)) != 0;
 }
 
 hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x,

@@ -157,6 +157,10 @@ MFMA_CASES = [
     (oracle.Q6_K, 6144, 1024, 5, False, 0), (oracle.Q6_K, 6144, 4096, 16, True, 0),
     (oracle.Q6_K, 6150, 2304, 9, False, 2), (oracle.Q6_K, 6144, 12288, 7, False, 0),
     (oracle.Q6_K, 8000, 4096, 12, True, 2),
+    # whole tiles per wave (>= 1024 tiles) and few tiles shared by a workgroup's waves
+    (oracle.Q4_0, 20480, 1024, 9, False, 0), (oracle.Q6_K, 17000, 1024, 16, True, 2),
+    (oracle.Q6_K, 1040, 4096, 16, False, 0), (oracle.Q6_K, 4096, 12288, 16, False, 0),
+    (oracle.Q4_0, 4096, 4096, 8, True, 0),
 ]
 
 
