@@ -108,8 +108,8 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     if (!enc_info(enc, info) || nprob < 1 || nprob > kMaxProblems || batch < 1 || batch > (uint32_t)kMaxGemvBatch)
         return hipErrorInvalidValue;
     // 5..16 activation rows: every weight decoded once for all rows, on MFMA
-    if (gemv_mfma_applies(enc, probs, nprob, batch, K, x_bf16, y_bf16))
-        return gemv_mfma_launch(enc, probs, nprob, K, x, batch, y_bf16, stream);
+    if (gemv_mfma_applies(enc, probs, nprob, batch, K, y_bf16, group))
+        return gemv_mfma_launch(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, stream);
     // Register batch: the next power of two, halved while its activation tile
     // does not fit one workgroup's LDS; larger batches run as several passes.
     uint32_t lim = 0;

@@ -1,6 +1,7 @@
-// Decode GEMV on MFMA for 5..16 activation rows, GGUF Q4_0 and Q6_K (y[b, o] =
-// Σ_k x[b, k]·w[o, k], f32 accumulation; gguf_codegen.rs:268-314 `emit_linear`
-// with the dequantisations of :412-472 (Q4_0) and :474-526 (Q6_K)).
+// Decode GEMV on MFMA for 5..16 activation rows, GGUF Q4_0 and Q6_K and MLX
+// affine U4 (y[b, o] = Σ_k x[b, k]·w[o, k], f32 accumulation;
+// gguf_codegen.rs:268-314 `emit_linear` with the dequantisations of :412-472
+// (Q4_0) and :474-526 (Q6_K), mlx_affine.rs:557-626 `emit_linear_u4`).
 //
 // The VALU GEMV multiplies every decoded weight once per activation row (a
 // v_dot2 per pair per row), so above ~4 rows its VALU and LDS work grows with
@@ -67,8 +68,13 @@ struct MfmaParams {
     uint32_t nprob;
     uint32_t batch;
     uint32_t accumulate;  // add to y (later segments; f32 outputs only)
-    const float* x;
+    uint32_t x_bf16;      // activations bf16 (else f32)
+    uint32_t group;       // MLX group size
+    uint32_t sdtype;      // MLX scale/bias dtype
+    const void* x;
     void* y[kMaxProblems];
+    const uint8_t* sc[kMaxProblems];  // MLX scales
+    const uint8_t* bi[kMaxProblems];  // MLX biases
 };
 
 // (c + off)·s for a packed pair (v_pk_add_f16, v_pk_mul_f16)
@@ -94,7 +100,7 @@ struct MfmaQ40 {
     static constexpr uint32_t UNIT = 32, UPT = 8, UB = 18;   // weights, bytes per block; blocks per task
     static constexpr uint32_t TB = UPT * UB;                 // bytes of a row per task
     static constexpr uint32_t NP = 10, WB = 176;             // window pieces, LDS row bytes
-    static constexpr bool ROWSCALE = false;
+    static constexpr bool ROWSCALE = false, MLX = false, PAIR4 = false;
     static constexpr uint32_t STAGE = 8;  // staging passes per chunk of loads
     // Pieces 0..8 hold window bytes [0, 144) at LDS 16i; piece 9 is [128, 144)
     // (sh = 0) or [132, 148) (sh = 2) at LDS [144, 160), so window dword 36
@@ -136,7 +142,7 @@ struct MfmaQ6K {
     static constexpr uint32_t UNIT = 256, UPT = 1, UB = 210;
     static constexpr uint32_t TB = UB;
     static constexpr uint32_t NP = 14, WB = 240;
-    static constexpr bool ROWSCALE = true;
+    static constexpr bool ROWSCALE = true, MLX = false, PAIR4 = false;
     static constexpr uint32_t STAGE = 8;
     // Pieces 0..12 hold window bytes [0, 208) at LDS 16i; piece 13 is
     // [196, 212) at LDS [208, 224), so window dword 52 (d) sits at LDS dword 55.
@@ -184,6 +190,50 @@ struct MfmaQ6K {
                            wq(and_or(a8, 0x00F000F0u, and_or(hr4, 0x03000300u, 0x54005400u)), (_Float16)-96.0f, s2[2]),
                            wq(and_or(b0, 0x00F000F0u, and_or(hl2, 0x03000300u, 0x54005400u)), (_Float16)-96.0f, s2[3]),
                            wq(and_or(b8, 0x00F000F0u, and_or(hr6, 0x03000300u, 0x54005400u)), (_Float16)-96.0f, s2[3]));
+        }
+    }
+};
+
+// MLX affine U4 (mlx_affine.rs:557-626, fixture.rs:307-311): a task is 256
+// weights of a row, 32 packed words (128 bytes, 16-byte aligned rows, so no
+// realignment); lane quarter q decodes words 8q..8q+7 (k 64q..64q+63), MFMA j
+// taking word j: nibbles (0,4), (1,5), (2,6), (3,7), i.e. the activation pairs
+// (r, r+4) of one run of 8.  w = q·s + b with the group's scale and bias:
+// q exact in f16, one fused packed multiply-add rounds once, RNE_f16(q·s + b)
+// (bf16 and f16 scales and biases are exact in f16's normal range).
+struct MfmaMlxU4 {
+    static constexpr int KT = 256, NM = 8, PF = 4, TPI = 2;
+    static constexpr uint32_t UNIT = 256, UPT = 1, UB = 128;
+    static constexpr uint32_t TB = UB;
+    static constexpr uint32_t NP = 8, WB = 144;
+    static constexpr bool ROWSCALE = false, MLX = true, PAIR4 = true;
+    static constexpr uint32_t STAGE = 8;
+    __device__ static uint32_t goff(uint32_t piece, uint32_t) { return 16u * piece; }
+    __device__ static uint32_t run0(uint32_t q, uint32_t j) { return 64u * q + 8u * j; }
+    __device__ static uint32_t run1(uint32_t q, uint32_t j) { return run0(q, j) + 4u; }
+    // a scale or bias bit pattern (f32, or f16/bf16 in the low half) to f16
+    __device__ static _Float16 sb_f16(uint32_t bits, uint32_t sdtype) {
+        if (sdtype == DT_F32) return (_Float16)__uint_as_float(bits);
+        if (sdtype == DT_F16) return __builtin_bit_cast(_Float16, (uint16_t)bits);
+        return (_Float16)__uint_as_float(bits << 16);  // bf16
+    }
+    // aux = (s, b) of the group of words 0..3 and of words 4..7
+    __device__ static void decode(const u32a* win, uint32_t q, const uint32_t (&aux)[4], uint32_t sdtype,
+                                  uint4 (&a)[NM]) {
+        const _Float16 s0 = sb_f16(aux[0], sdtype), b0 = sb_f16(aux[1], sdtype);
+        const _Float16 s1 = sb_f16(aux[2], sdtype), b1 = sb_f16(aux[3], sdtype);
+        const h2 o1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f}, o64 = {(_Float16)-64.0f, (_Float16)-64.0f};
+#pragma unroll
+        for (int j = 0; j < NM; j++) {
+            const uint32_t w = win[8u * q + (uint32_t)j], w8 = w >> 8;
+            const h2 s2 = j < 4 ? h2{s0, s0} : h2{s1, s1}, b2 = j < 4 ? h2{b0, b0} : h2{b1, b1};
+            auto wq = [&](uint32_t c, h2 o) {
+                return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, c) + o, s2, b2));
+            };
+            a[j] = make_uint4(wq(and_or(w, 0x000F000Fu, 0x64006400u), o1024),   // nibbles 0, 4
+                              wq(and_or(w, 0x00F000F0u, 0x54005400u), o64),     // 1, 5
+                              wq(and_or(w8, 0x000F000Fu, 0x64006400u), o1024),  // 2, 6
+                              wq(and_or(w8, 0x00F000F0u, 0x54005400u), o64));   // 3, 7
         }
     }
 };
@@ -249,6 +299,8 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     };
     struct Where {
         const uint8_t* w;
+        const uint8_t* sc;
+        const uint8_t* bi;
         void* y;
         uint32_t n, row0;
     };
@@ -258,6 +310,10 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
         for (int i = 1; i < kMaxProblems; i++) pi += ((uint32_t)i < p.nprob && tile >= p.tile_begin[i]) ? 1u : 0u;
         Where r;
         r.w = pick(pi, p.w);
+        if constexpr (M::MLX) {
+            r.sc = pick(pi, p.sc);
+            r.bi = pick(pi, p.bi);
+        }
         r.y = pick(pi, p.y);
         r.n = pick(pi, p.n);
         r.row0 = (tile - pick(pi, p.tile_begin)) * 16u;
@@ -279,14 +335,22 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     // the problem re-read its last one: in bounds, never stored)
     struct Rows {
         const uint8_t* abase;
-        uint32_t om;
+        const uint8_t* sc;
+        const uint8_t* bi;
+        uint32_t om, rowm;
         uint32_t oi[NLD];
     };
     auto rows_of = [&](const Where& wh) {
         const uint32_t bsh = (uint32_t)((uintptr_t)wh.w & 3u);
-        auto off = [&](uint32_t r) { return (wh.row0 + r < wh.n ? wh.row0 + r : wh.n - 1u) * rowbytes + bsh + seg0; };
+        auto row = [&](uint32_t r) { return wh.row0 + r < wh.n ? wh.row0 + r : wh.n - 1u; };
+        auto off = [&](uint32_t r) { return row(r) * rowbytes + bsh + seg0; };
         Rows r;
         r.abase = wh.w - bsh;
+        if constexpr (M::MLX) {
+            r.sc = wh.sc;
+            r.bi = wh.bi;
+            r.rowm = row(m);
+        }
         r.om = off(m);
 #pragma unroll
         for (uint32_t i = 0; i < NLD; i++) r.oi[i] = off(pr[i]);
@@ -295,19 +359,38 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     // task t's window start from a row's segment offset (padding tasks
     // re-read the last task)
     auto task_off = [&](uint32_t o, uint32_t t) { return o + (t < nt ? t : nt - 1u) * M::TB; };
-    auto load = [&](const Rows& r, uint32_t t, u32x4 (&v)[NLD]) {
+    // MLX scales and biases of the lane's row: the dword holding each value
+    // (bits shifted down for 16-bit types; it holds a byte of the value, so
+    // it stays in the value's page)
+    const uint32_t es = p.sdtype == DT_F32 ? 4u : 2u, gpr = p.K / (p.group ? p.group : 1u);
+    auto sbload = [&](const uint8_t* base, uint32_t idx) {
+        const uint32_t o = idx * es;
+        const uint32_t v = *gptr<uint32_t>(base + (o & ~3u));
+        return es == 4u ? v : (v >> (8u * (o & 3u))) & 0xFFFFu;
+    };
+    auto load = [&](const Rows& r, uint32_t t, u32x4 (&v)[NLD], uint32_t (&aux)[4]) {
 #pragma unroll
         for (uint32_t i = 0; i < NLD; i++) {
             const uint32_t o = task_off(r.oi[i], t);
             v[i] = *gptr<u32x4>(r.abase + (o & ~3u) + M::goff(pc[i], o & 3u));
+        }
+        if constexpr (M::MLX) {
+            // groups of the lane's k 64q..64q+31 and 64q+32..64q+63
+            const uint32_t kl = p.k0 + (t < nt ? t : nt - 1u) * M::KT + 64u * q;
+            const uint32_t g0 = r.rowm * gpr + kl / p.group, g1 = r.rowm * gpr + (kl + 32u) / p.group;
+            aux[0] = sbload(r.sc, g0);
+            aux[1] = sbload(r.bi, g0);
+            aux[2] = sbload(r.sc, g1);
+            aux[3] = sbload(r.bi, g1);
         }
     };
     // the first PF tasks' weight loads leave before the activations are staged
     Where wcur = where(tile_at(0u));
     Rows rcur = rows_of(wcur);
     u32x4 ring[PF][NLD];
+    uint32_t rx[PF][4];
 #pragma unroll
-    for (int s = 0; s < PF; s++) load(rcur, t0 + (uint32_t)s, ring[s]);  // tpw >= PF: all in tile 0
+    for (int s = 0; s < PF; s++) load(rcur, t0 + (uint32_t)s, ring[s], rx[s]);  // tpw >= PF: all in tile 0
 
     // ---- stage the activations: unit u = (task g, row b, e = q·NM + j); the
     // 32 units of (g, b) lie on consecutive lanes, their maximum reduced by
@@ -320,12 +403,26 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = 0.0f;
         if (u < nunits && b < p.batch && g < nt) {
-            const float* xr = p.x + (size_t)b * p.K + p.k0 + M::KT * g;
-            const f32x4 lo4 = *gptr<f32x4>(xr + M::run0(qq, j)), hi4 = *gptr<f32x4>(xr + M::run1(qq, j));
+            const size_t k0 = (size_t)b * p.K + p.k0 + M::KT * g;
+            if (p.x_bf16) {  // two runs of 4 bf16: 8 bytes each
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                const uint16_t* xr = static_cast<const uint16_t*>(p.x) + k0;
+                const u32x2 lo2 = *gptr<u32x2>(xr + M::run0(qq, j)), hi2 = *gptr<u32x2>(xr + M::run1(qq, j));
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                v[i] = lo4[i];
-                v[4 + i] = hi4[i];
+                for (int i = 0; i < 2; i++) {
+                    v[2 * i] = __uint_as_float(lo2[i] << 16);
+                    v[2 * i + 1] = __uint_as_float(lo2[i] & 0xFFFF0000u);
+                    v[4 + 2 * i] = __uint_as_float(hi2[i] << 16);
+                    v[5 + 2 * i] = __uint_as_float(hi2[i] & 0xFFFF0000u);
+                }
+            } else {
+                const float* xr = static_cast<const float*>(p.x) + k0;
+                const f32x4 lo4 = *gptr<f32x4>(xr + M::run0(qq, j)), hi4 = *gptr<f32x4>(xr + M::run1(qq, j));
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    v[i] = lo4[i];
+                    v[4 + i] = hi4[i];
+                }
             }
         }
     };
@@ -352,8 +449,10 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
             const f32x2 f = {ldexpf(a, sh), ldexpf(c, sh)};
             return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));  // RNE
         };
-        // pair order (r, r+2) (r+1, r+3) of each run
-        const uint4 val = make_uint4(pk(v[0], v[2]), pk(v[1], v[3]), pk(v[4], v[6]), pk(v[5], v[7]));
+        // pair order: (r, r+2) (r+1, r+3) of each run, or (r, r+4) ... (r+3, r+7)
+        // of one run of 8 (MLX words)
+        const uint4 val = M::PAIR4 ? make_uint4(pk(v[0], v[4]), pk(v[1], v[5]), pk(v[2], v[6]), pk(v[3], v[7]))
+                                   : make_uint4(pk(v[0], v[2]), pk(v[1], v[3]), pk(v[4], v[6]), pk(v[5], v[7]));
         if (u < nunits) {
             xl[(g * NM + j) * 64u + xslot(b + 16u * qq, j)] = val;
             if (e == 0) inv[g * 16u + b] = ldexpf(1.0f, -sh);
@@ -378,14 +477,21 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     // task's writes wait for these reads), the lane's quarter decoded from
     // its row, and the task's MFMAs into a zeroed tile; rs = the row scale
     // (Q6_K's d).
-    auto product = [&](const u32x4 (&v)[NLD], const Rows& r, uint32_t t, float& rs) {
+    auto product = [&](const u32x4 (&v)[NLD], const uint32_t (&aux)[4], const Rows& r, uint32_t t, float& rs) {
 #pragma unroll
         for (uint32_t i = 0; i < NLD; i++) *reinterpret_cast<u32x4*>(win + lo[i]) = v[i];
         uint4 xa[NM];
 #pragma unroll
         for (uint32_t j = 0; j < NM; j++) xa[j] = xl[(t * NM + j) * 64u + xslot(lane, j)];
         uint4 a[NM];
-        M::decode(reinterpret_cast<const u32a*>(win + m * M::WB), task_off(r.om, t) & 3u, t < nt, q, a, rs);
+        if constexpr (M::MLX) {
+            uint32_t ax[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) ax[i] = t < nt ? aux[i] : 0u;  // padding task: zero scale and bias
+            M::decode(reinterpret_cast<const u32a*>(win + m * M::WB), q, ax, p.sdtype, a);
+        } else {
+            M::decode(reinterpret_cast<const u32a*>(win + m * M::WB), task_off(r.om, t) & 3u, t < nt, q, a, rs);
+        }
         f32x4 tmp = zero;
 #pragma unroll
         for (uint32_t j = 0; j < NM; j++)
@@ -406,15 +512,15 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
             for (int s = 0; s < PF; s += M::TPI) {
                 const uint32_t g = t0 + g0 + (uint32_t)s;
                 f32x4 prd[M::TPI];
-                float rs[M::TPI];
+                float rs[M::TPI] = {};
 #pragma unroll
-                for (int k = 0; k < M::TPI; k++) prd[k] = product(ring[s + k], rcur, g + (uint32_t)k, rs[k]);
+                for (int k = 0; k < M::TPI; k++) prd[k] = product(ring[s + k], rx[s + k], rcur, g + (uint32_t)k, rs[k]);
                 // refill the slots in place (the same registers across
                 // iterations: no copies that would wait for the loads)
                 const bool wrap = g0 + (uint32_t)s + PF >= tpw;  // the refills belong to the next tile
                 const uint32_t gn = wrap ? g + PF - tpw : g + PF;
 #pragma unroll
-                for (int k = 0; k < M::TPI; k++) load(wrap ? rnxt : rcur, gn + (uint32_t)k, ring[s + k]);
+                for (int k = 0; k < M::TPI; k++) load(wrap ? rnxt : rcur, gn + (uint32_t)k, ring[s + k], rx[s + k]);
 #pragma unroll
                 for (int k = 0; k < M::TPI; k++) {
                     // inverse activation scales of rows 4q..4q+3
@@ -516,13 +622,15 @@ template <class M>
 int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16);
 
 template <class M>
-hipError_t launch_mfma(const GemvProblem* probs, int nprob, uint32_t K, const void* x, uint32_t batch, bool y_bf16,
-                       hipStream_t st) {
+hipError_t launch_mfma(const GemvProblem* probs, int nprob, uint32_t K, const void* x, bool x_bf16, uint32_t batch,
+                       bool y_bf16, uint32_t group, uint32_t sdtype, hipStream_t st) {
     MfmaParams p = {};
     uint32_t tiles = 0;
     for (int i = 0; i < kMaxProblems; i++) {
         const GemvProblem& g = probs[i < nprob ? i : nprob - 1];
         p.w[i] = g.w;
+        p.sc[i] = g.sc;
+        p.bi[i] = g.bi;
         p.y[i] = g.y;
         p.n[i] = i < nprob ? g.n : 0u;
         p.tile_begin[i] = tiles;
@@ -532,7 +640,10 @@ hipError_t launch_mfma(const GemvProblem* probs, int nprob, uint32_t K, const vo
     p.nprob = (uint32_t)nprob;
     p.K = K;
     p.batch = batch;
-    p.x = static_cast<const float*>(x);
+    p.x = x;
+    p.x_bf16 = x_bf16 ? 1u : 0u;
+    p.group = group;
+    p.sdtype = sdtype;
     const uint32_t units = K / M::UNIT;
     return mfma_mode<M>(K, tiles, y_bf16) == 2 ? launch_mode<M, true>(p, units, y_bf16, st)
                                        : launch_mode<M, false>(p, units, y_bf16, st);
@@ -553,19 +664,37 @@ int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16) {
 
 }  // namespace
 
-bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool x_bf16,
-                       bool y_bf16) {
-    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K) || x_bf16 || batch < 5 || batch > 16 || K % 256u) return false;
+bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool y_bf16,
+                       uint32_t group) {
+    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K && enc != ENC_MLX_U4) || batch < 5 || batch > 16 || K % 256u) return false;
+    if (enc == ENC_MLX_U4 && (group == 0 || group % 32u)) return false;
     uint32_t tiles = 0;
-    for (int i = 0; i < nprob; i++) tiles += (probs[i].n + 15u) / 16u;
-    return (enc == ENC_Q4_0 ? mfma_mode<MfmaQ40>(K, tiles, y_bf16) : mfma_mode<MfmaQ6K>(K, tiles, y_bf16)) != 0;
+    uint64_t rows = 0;
+    for (int i = 0; i < nprob; i++) {
+        tiles += (probs[i].n + 15u) / 16u;
+        rows += probs[i].n;
+    }
+    // The MFMA path's fixed costs (staging every activation row per
+    // workgroup, a wave's first products) outweigh the VALU GEMV's per-row
+    // work on small launches that the VALU GEMV serves in one register pass:
+    // it takes launches with more rows than one pass holds, launches of at
+    // least 8 MB of weights, or at least kMfmaSplitTiles tiles (measured at
+    // the Qwen3-0.6B MLX shapes: 1-4 MB launches take ~13 us on MFMA against
+    // 7-9 us on VALU at 5-8 rows, 13-15 against 14-18 us at 16 rows).
+    const uint64_t bytes = rows * (enc == ENC_Q4_0 ? K / 32u * 18u : enc == ENC_Q6_K ? K / 256u * 210u : K / 2u);
+    if (batch <= max_register_batch(enc) && bytes < (8ull << 20) && tiles < kMfmaSplitTiles) return false;
+    const int mode = enc == ENC_Q4_0   ? mfma_mode<MfmaQ40>(K, tiles, y_bf16)
+                   : enc == ENC_Q6_K   ? mfma_mode<MfmaQ6K>(K, tiles, y_bf16)
+                                       : mfma_mode<MfmaMlxU4>(K, tiles, y_bf16);
+    return mode != 0;
 }
 
-hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x,
-                            uint32_t batch, bool y_bf16, hipStream_t st) {
+hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x, bool x_bf16,
+                            uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype, hipStream_t st) {
     if (nprob < 1 || nprob > kMaxProblems) return hipErrorInvalidValue;
-    if (enc == ENC_Q4_0) return launch_mfma<MfmaQ40>(probs, nprob, K, x, batch, y_bf16, st);
-    if (enc == ENC_Q6_K) return launch_mfma<MfmaQ6K>(probs, nprob, K, x, batch, y_bf16, st);
+    if (enc == ENC_Q4_0) return launch_mfma<MfmaQ40>(probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
+    if (enc == ENC_Q6_K) return launch_mfma<MfmaQ6K>(probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
+    if (enc == ENC_MLX_U4) return launch_mfma<MfmaMlxU4>(probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     return hipErrorInvalidValue;
 }
 

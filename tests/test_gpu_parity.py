@@ -231,6 +231,41 @@ def test_gemv_mlx_bf16_io(ctx, sdtype, n, k, g, batch):
     assert np.all(err <= TOL + rounding), err.max()
 
 
+# MLX affine U4 on the MFMA GEMV (more than 8 rows, K a multiple of 256):
+# whole tiles per wave (>= 1024 tiles, or >= 384 with fewer than 8 tasks),
+# split mode, group sizes 32 / 64 / 128, every scale dtype, bf16 and f32
+# activations.
+MLX_MFMA_CASES = [
+    (6144, 1024, 64, oracle.D_BF16, 16, True), (20000, 1024, 64, oracle.D_F16, 12, True),
+    (1024, 3072, 64, oracle.D_F16, 12, True), (3072, 2048, 32, oracle.D_F32, 16, True),
+    (2048, 4096, 128, oracle.D_BF16, 9, False), (4100, 2048, 64, oracle.D_BF16, 9, False),
+]
+
+
+@pytest.mark.parametrize("n,k,g,sdtype,batch,xbf16", MLX_MFMA_CASES,
+                         ids=[f"{c[0]}x{c[1]}-g{c[2]}-s{c[3]}-b{c[4]}{'-bf16io' if c[5] else '-f32io'}"
+                              for c in MLX_MFMA_CASES])
+def test_gemv_mfma_mlx(ctx, n, k, g, sdtype, batch, xbf16):
+    packed, sc, bi = oracle.synth_mlx_u4(n, k, g, sdtype, seed=n + k + g + batch)
+    w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), g, sdtype)
+    wf = oracle.dequant_mlx_u4(packed, sc, bi, sdtype, n, k, g)
+    if xbf16:
+        xb = oracle.f32_to_bf16_bits(oracle.randn(batch * k, seed=batch + 7)).reshape(batch, k)
+        x = oracle.bf16_bits_to_f32(xb)
+        y = ctx.qlinear(w, dev(xb).view(torch.bfloat16), y_dtype=torch.bfloat16)
+        y = oracle.bf16_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(batch, n)
+    else:
+        x = oracle.randn(batch * k, seed=batch + 7).reshape(batch, k)
+        y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    y64, absdot = oracle.linear_f64(x, wf)
+    den = np.where(absdot > 0, absdot, 1)
+    # f16 weights (one rounding of q·s + b; f32 scales and biases also rounded
+    # to f16 first) and activations: 2^-10 plus slack; bf16 outputs 2^-8 of |y|
+    extra = np.abs(y64) * 2.0 ** -8 / den if xbf16 else 0.0
+    err = np.abs(y.astype(np.float64) - y64) / den
+    assert np.all(err <= 2.0 ** -10 + 1e-4 + extra), err.max()
+
+
 def test_gemv_mlx_f32_io(ctx):
     n, k, g = 257, 2048, 64
     packed, sc, bi = oracle.synth_mlx_u4(n, k, g, oracle.D_BF16, seed=4)
