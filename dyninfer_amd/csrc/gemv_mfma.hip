@@ -1,4 +1,4 @@
-// Decode GEMV on MFMA for 5..16 activation rows, GGUF Q4_0 and Q6_K and MLX
+// Decode GEMV on MFMA for 3..16 activation rows, GGUF Q4_0 and Q6_K and MLX
 // affine U4 (y[b, o] = Σ_k x[b, k]·w[o, k], f32 accumulation;
 // gguf_codegen.rs:268-314 `emit_linear` with the dequantisations of :412-472
 // (Q4_0) and :474-526 (Q6_K), mlx_affine.rs:557-626 `emit_linear_u4`).
@@ -666,7 +666,7 @@ int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16) {
 
 bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool y_bf16,
                        uint32_t group) {
-    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K && enc != ENC_MLX_U4) || batch < 5 || batch > 16 || K % 256u) return false;
+    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K && enc != ENC_MLX_U4) || batch < 3 || batch > 16 || K % 256u) return false;
     if (enc == ENC_MLX_U4 && (group == 0 || group % 32u)) return false;
     uint32_t tiles = 0;
     uint64_t rows = 0;
@@ -681,7 +681,10 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     // least 8 MB of weights, or at least kMfmaSplitTiles tiles (measured at
     // the Qwen3-0.6B MLX shapes: 1-4 MB launches take ~13 us on MFMA against
     // 7-9 us on VALU at 5-8 rows, 13-15 against 14-18 us at 16 rows).
+    // At 3-4 rows only the largest launches gain (8B lm_head at 4 rows: 114 us on MFMA against 181 us;
+    // at 2 rows both take ~111 us).
     const uint64_t bytes = rows * (enc == ENC_Q4_0 ? K / 32u * 18u : enc == ENC_Q6_K ? K / 256u * 210u : K / 2u);
+    if (batch < 5 && tiles < kMfmaSplitTiles) return false;
     if (batch <= max_register_batch(enc) && bytes < (8ull << 20) && tiles < kMfmaSplitTiles) return false;
     const int mode = enc == ENC_Q4_0   ? mfma_mode<MfmaQ40>(K, tiles, y_bf16)
                    : enc == ENC_Q6_K   ? mfma_mode<MfmaQ6K>(K, tiles, y_bf16)

@@ -161,6 +161,8 @@ MFMA_CASES = [
     (oracle.Q4_0, 20480, 1024, 9, False, 0), (oracle.Q6_K, 17000, 1024, 16, True, 2),
     (oracle.Q6_K, 1040, 4096, 16, False, 0), (oracle.Q6_K, 4096, 12288, 16, False, 0),
     (oracle.Q4_0, 4096, 4096, 8, True, 0),
+    # 3-4 rows: only launches of >= 1024 tiles
+    (oracle.Q6_K, 17000, 1024, 4, False, 0), (oracle.Q4_0, 20480, 1024, 3, True, 2),
 ]
 
 
@@ -231,7 +233,8 @@ def test_gemv_mlx_bf16_io(ctx, sdtype, n, k, g, batch):
     assert np.all(err <= TOL + rounding), err.max()
 
 
-# MLX affine U4 on the MFMA GEMV (more than 8 rows, K a multiple of 256):
+# MLX affine U4 on the MFMA GEMV (more than 8 rows, or 3-4 on >= 1024 tiles;
+# K a multiple of 256):
 # whole tiles per wave (>= 1024 tiles, or >= 384 with fewer than 8 tasks),
 # split mode, group sizes 32 / 64 / 128, every scale dtype, bf16 and f32
 # activations.
@@ -239,6 +242,7 @@ MLX_MFMA_CASES = [
     (6144, 1024, 64, oracle.D_BF16, 16, True), (20000, 1024, 64, oracle.D_F16, 12, True),
     (1024, 3072, 64, oracle.D_F16, 12, True), (3072, 2048, 32, oracle.D_F32, 16, True),
     (2048, 4096, 128, oracle.D_BF16, 9, False), (4100, 2048, 64, oracle.D_BF16, 9, False),
+    (20000, 1024, 64, oracle.D_BF16, 4, True),
 ]
 
 
