@@ -236,23 +236,23 @@ __device__ __forceinline__ void xstage_store(uint8_t* lds, uint32_t nch, uint32_
 // return in issue order, so the activations arrive ahead of the weights and
 // the staging arithmetic runs while the weights are in flight.  Later rounds
 // (large batches) load after the weights.  Ends with a barrier.
-template <class E, int B, bool XBF16, int P, class MID>
+template <class E, int B, bool XBF16, int P, int TH, class MID>
 __device__ __forceinline__ void stage_x_rounds(uint8_t* lds, const GemvParams& p, MID&& mid) {
     const uint32_t nch = p.K / (uint32_t)E::CW;
     const uint32_t total = (uint32_t)B * nch * (uint32_t)E::NT;
     const uint32_t t = threadIdx.x % (uint32_t)E::NT;  // the workgroup size is a multiple of NT
     XStage<E> s[P];
 #pragma unroll
-    for (int ps = 0; ps < P; ps++) xstage_load<E, B, XBF16>(p, nch, threadIdx.x + (uint32_t)ps * kGemvThreads, s[ps]);
+    for (int ps = 0; ps < P; ps++) xstage_load<E, B, XBF16>(p, nch, threadIdx.x + (uint32_t)ps * TH, s[ps]);
     __builtin_amdgcn_sched_barrier(0);
     mid();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ps = 0; ps < P; ps++) xstage_store<E, B>(lds, nch, t, s[ps]);
-    for (uint32_t base = (uint32_t)P * kGemvThreads; base < total; base += (uint32_t)P * kGemvThreads) {
+    for (uint32_t base = (uint32_t)P * TH; base < total; base += (uint32_t)P * TH) {
 #pragma unroll
         for (int ps = 0; ps < P; ps++)
-            xstage_load<E, B, XBF16>(p, nch, base + threadIdx.x + (uint32_t)ps * kGemvThreads, s[ps]);
+            xstage_load<E, B, XBF16>(p, nch, base + threadIdx.x + (uint32_t)ps * TH, s[ps]);
 #pragma unroll
         for (int ps = 0; ps < P; ps++) xstage_store<E, B>(lds, nch, t, s[ps]);
     }
@@ -261,15 +261,16 @@ __device__ __forceinline__ void stage_x_rounds(uint8_t* lds, const GemvParams& p
 
 // Rounds of P passes, P the power of two covering the staging threads, at
 // most 16 activations (registers) per thread in flight: every variant is
-// compiled into the kernel, so the widest one sets its register count.
-template <class E, int B, bool XBF16, class MID>
+// compiled into the kernel, so the widest one sets its register count.  TH is
+// the workgroup size.
+template <class E, int B, bool XBF16, int TH = kGemvThreads, class MID>
 __device__ __forceinline__ void stage_x_auto(uint8_t* lds, const GemvParams& p, MID&& mid) {
     constexpr int PMAX = 4 / E::NXR > 0 ? 4 / E::NXR : 1;
-    const uint32_t passes = ((uint32_t)B * (p.K / (uint32_t)E::CW) * (uint32_t)E::NT + kGemvThreads - 1u) / kGemvThreads;
-    if (PMAX == 1 || passes <= 1u) stage_x_rounds<E, B, XBF16, 1>(lds, p, mid);
+    const uint32_t passes = ((uint32_t)B * (p.K / (uint32_t)E::CW) * (uint32_t)E::NT + TH - 1u) / TH;
+    if (PMAX == 1 || passes <= 1u) stage_x_rounds<E, B, XBF16, 1, TH>(lds, p, mid);
     else if constexpr (PMAX >= 2) {
-        if (PMAX == 2 || passes <= 2u) stage_x_rounds<E, B, XBF16, 2>(lds, p, mid);
-        else stage_x_rounds<E, B, XBF16, (PMAX >= 4 ? 4 : 2)>(lds, p, mid);
+        if (PMAX == 2 || passes <= 2u) stage_x_rounds<E, B, XBF16, 2, TH>(lds, p, mid);
+        else stage_x_rounds<E, B, XBF16, (PMAX >= 4 ? 4 : 2), TH>(lds, p, mid);
     }
 }
 
@@ -594,11 +595,12 @@ __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const uint8_t
 // lane issues the loads of all CPL of its chunks right after the activation
 // loads, the activations are staged while they are in flight, so the whole
 // launch waits on one memory latency; then it multiplies them for the B
-// activation rows, the L lanes reduce, and lane 0 stores.
-template <class E, int CPL, int B, class LOAD, class STAGE>
+// activation rows, the L lanes reduce, and lane 0 stores.  TH is the
+// workgroup size.
+template <class E, int CPL, int B, int TH, class LOAD, class STAGE>
 __device__ __forceinline__ void gemv_oneshot(const GemvParams& p, const uint8_t* lds, LOAD&& load, STAGE&& stage) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (uint32_t)(kGemvThreads / 64) + (threadIdx.x >> 6));
+    const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (uint32_t)(TH / 64) + (threadIdx.x >> 6));
     const uint32_t L = 1u << p.lanes_log2;
     const uint32_t j = lane & (L - 1u), g = lane >> p.lanes_log2;
     const uint32_t rows_per_rb = 64u >> p.lanes_log2;
@@ -642,12 +644,12 @@ __global__ __launch_bounds__(kGemvThreads) void gguf_gemv_kernel(const GemvParam
     gemv_pipeline<E, R, B>(p, xlds, load, [&](auto&& mid) { stage_x_auto<E, B, XBF16>(xlds, p, mid); });
 }
 
-template <class E, int CPL, int B, bool XBF16>
-__global__ __launch_bounds__(kGemvThreads) void gguf_gemv_oneshot_kernel(const GemvParams p) {
+template <class E, int CPL, int B, bool XBF16, int TH>
+__global__ __launch_bounds__(TH) void gguf_gemv_oneshot_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
     const uint32_t rowbytes = (p.K / (uint32_t)E::QK) * (uint32_t)E::BB;
     auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) { return E::load(rb.w, row * rowbytes, u); };
-    gemv_oneshot<E, CPL, B>(p, xlds, load, [&](auto&& mid) { stage_x_auto<E, B, XBF16>(xlds, p, mid); });
+    gemv_oneshot<E, CPL, B, TH>(p, xlds, load, [&](auto&& mid) { stage_x_auto<E, B, XBF16, TH>(xlds, p, mid); });
 }
 
 // ---------------------------------------------------------------- MLX affine U4
@@ -684,10 +686,11 @@ __global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_kernel(const GemvPar
     gemv_pipeline<EncMlxU4, R, B>(p, xlds, MlxLoad(p), [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p, mid); });
 }
 
-template <int CPL, int B, bool XBF16>
-__global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_oneshot_kernel(const GemvParams p) {
+template <int CPL, int B, bool XBF16, int TH>
+__global__ __launch_bounds__(TH) void mlx_u4_gemv_oneshot_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
-    gemv_oneshot<EncMlxU4, CPL, B>(p, xlds, MlxLoad(p), [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p, mid); });
+    gemv_oneshot<EncMlxU4, CPL, B, TH>(p, xlds, MlxLoad(p),
+                                        [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XBF16, TH>(xlds, p, mid); });
 }
 
 // Widest rows per lane group instantiated for a register batch B: more rows
@@ -741,19 +744,30 @@ struct GemvTile {
 // Persistent launch over the instantiated tiles t[0..n) (widest first).  Each
 // tile's grid is as many workgroups as fit on the device at once (its
 // occupancy x CUs), capped by its row-block count, and its waves are split
-// over the problems (split_waves).  The tile whose busiest wave has the
-// fewest rows wins (rows, not row blocks: a wave's time is its share of the
-// weight stream), ties going to the widest, which amortises the per-task and
-// per-row-block work over more weights.  Measured on the 8B gate/up (two
-// 12288-row problems): 4-row tiles leave half the waves 2 row blocks and
+// over the problems (split_waves).  Long streams (the busiest wave has at
+// least 8 tasks; cpl = chunks per lane per row block): the widest tile whose
+// busiest CU holds within 5% of an even split of all rows over the CUs (its
+// busiest wave's rows times its waves), since wider tiles amortise the
+// per-task and per-row-block work over more weights.  Otherwise, or when no
+// tile splits that evenly, the tile whose busiest wave has the fewest rows
+// (rows, not row blocks: a wave's time is its share of the weight stream),
+// ties to the widest; for short streams this also keeps more waves, and
+// loads, in flight.  Measured: the 8B lm_head (Q6_K 151936x4096) 109 us on
+// 1-row tiles (6 waves per SIMD, the fewest rows per wave) against 99 us on
+// 2-row tiles (4 per SIMD, 2% over the even split); the 8B down (Q6_K
+// 4096x12288, 3 tasks per wave) 13.1 us on 1-row tiles against 13.8 us on
+// 2-row tiles (both split evenly, 16 and 8 waves per CU); the 8B gate/up (two
+// 12288-row problems) on 4-row tiles left half the waves 2 row blocks and
 // half 1 (49% of HBM peak), 1- and 2-row tiles split them evenly (54%).
 inline hipError_t launch_persistent_best(const GemvTile* t, int n, const GemvParams& p0, size_t lds,
-                                         hipStream_t st) {
+                                         uint32_t cpl, hipStream_t st) {
     constexpr uint64_t waves = kGemvThreads / 64;
     const uint32_t groups = 64u >> p0.lanes_log2;  // lane groups per wave
-    int pick = -1;
+    uint64_t total_rows = 0;
+    for (uint32_t k = 0; k < p0.nprob; k++) total_rows += p0.n[k];
+    int pick = -1, even = -1;
     uint64_t best = ~(uint64_t)0;
-    GemvParams q = p0, chosen = p0;
+    GemvParams q = p0, chosen = p0, chosen_even = p0;
     for (int i = 0; i < n; i++) {
         q = p0;
         const uint32_t rows_per_rb = groups * t[i].R;
@@ -761,23 +775,33 @@ inline hipError_t launch_persistent_best(const GemvTile* t, int n, const GemvPar
         int cus = 0, per_cu = 0;
         hipError_t e = cached_occupancy(reinterpret_cast<const void*>(t[i].kernel), lds, kGemvThreads, &per_cu, &cus);
         if (e != hipSuccess) return e;
-        if (per_cu < 1) continue;
+        if (per_cu < 1 || cus < 1) continue;
         const uint64_t cap = (uint64_t)per_cu * (uint64_t)cus;
         const uint64_t want = ((uint64_t)q.total_rb + waves - 1) / waves;
         q.grid = (uint32_t)(want < cap ? want : cap);
         split_waves(q, rows_per_rb);
-        uint64_t rows = 0;  // rows of the busiest wave
+        uint64_t rbs = 0;  // row blocks of the busiest wave
         for (uint32_t k = 0; k < q.nprob; k++) {
             const uint64_t nw = q.wave_end[k] - (k ? q.wave_end[k - 1] : 0u);
             const uint64_t prb = (q.n[k] + rows_per_rb - 1) / rows_per_rb;
-            const uint64_t r = (prb + nw - 1) / nw * rows_per_rb;
-            rows = r > rows ? r : rows;
+            const uint64_t r = (prb + nw - 1) / nw;
+            rbs = r > rbs ? r : rbs;
+        }
+        const uint64_t rows = rbs * rows_per_rb;
+        const uint64_t load = rows * waves * (((uint64_t)q.grid + (uint64_t)cus - 1) / (uint64_t)cus);
+        if (even < 0 && rbs * cpl >= 8 && load * 100 <= total_rows * 105 / (uint64_t)cus) {
+            even = i;
+            chosen_even = q;
         }
         if (rows < best) {
             best = rows;
             pick = i;
             chosen = q;
         }
+    }
+    if (even >= 0) {
+        pick = even;
+        chosen = chosen_even;
     }
     if (pick < 0) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(t[pick].kernel, dim3(chosen.grid), dim3(kGemvThreads), lds, st, chosen);
@@ -797,18 +821,32 @@ int gemv_tiles(GemvTile (&t)[3], MK&& gemv_tile) {
     return n;
 }
 
-// Latency-mode launch: one wave per row block of one row per lane group.
+// Latency-mode launch: one wave per row block of one row per lane group, in
+// workgroups of 512 threads (k512) or 256 (k256): the size whose busiest CU
+// holds fewer waves, ties to 512 (each workgroup stages the activations once).
+// Every workgroup lands on a CU of its own while the grid is at most the CU
+// count, so 1,024 waves fill all 256 CUs in 256-thread groups and half of
+// them in 512-thread groups; measured on the Qwen3-0.6B projections (1,024
+// and 3,072 waves) 256 threads took 5-15% less time per launch, and on
+// launches that split evenly either way (2,048, 4,096, 6,144 waves) it cost
+// up to 12%.
 template <class KERNEL>
-hipError_t launch_oneshot(KERNEL kernel, GemvParams p, size_t lds, hipStream_t st) {
-    if (lds > 64u * 1024u) {
-        int cus = 0, per_cu = 0;
-        hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, kGemvThreads, &per_cu, &cus);
-        if (e != hipSuccess) return e;
-    }
+hipError_t launch_oneshot(KERNEL k512, KERNEL k256, GemvParams p, size_t lds, hipStream_t st) {
+    int cus = 0, per_cu = 0;
+    hipError_t e = cached_occupancy(reinterpret_cast<const void*>(k512), lds, 512, &per_cu, &cus);
+    if (e != hipSuccess) return e;
+    e = cached_occupancy(reinterpret_cast<const void*>(k256), lds, 256, &per_cu, &cus);
+    if (e != hipSuccess) return e;
+    if (cus < 1) return hipErrorInvalidConfiguration;
     layout_row_blocks(p, 64u >> p.lanes_log2);
-    constexpr uint32_t waves = kGemvThreads / 64;
+    auto busiest = [&](uint32_t waves) {  // waves on the busiest CU, groups of `waves`
+        const uint64_t wgs = ((uint64_t)p.total_rb + waves - 1) / waves;
+        return (wgs + (uint64_t)cus - 1) / (uint64_t)cus * waves;
+    };
+    const bool small = busiest(4) < busiest(8);
+    const uint32_t waves = small ? 4u : 8u;
     p.grid = (p.total_rb + waves - 1) / waves;
-    hipLaunchKernelGGL(kernel, dim3(p.grid), dim3(kGemvThreads), lds, st, p);
+    hipLaunchKernelGGL(small ? k256 : k512, dim3(p.grid), dim3(waves * 64u), lds, st, p);
     return hipGetLastError();
 }
 
@@ -827,7 +865,9 @@ hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t oneshot, b
         // chunks per lane (the host's limits): 1..4 for one activation row
         // (Q6_K 1..2), 1..2 for 2 rows, 1 for 4
 #define DMX_ONESHOT(b, c)                                                                             \
-    if (B == b && oneshot == c) return launch_oneshot(gguf_gemv_oneshot_kernel<E, c, b, false>, p, lds, st);
+    if (B == b && oneshot == c)                                                                       \
+        return launch_oneshot(gguf_gemv_oneshot_kernel<E, c, b, false, 512>, gguf_gemv_oneshot_kernel<E, c, b, false, 256>, \
+                              p, lds, st);
         DMX_ONESHOT(1, 1)
         DMX_ONESHOT(1, 2)
         if constexpr (E::ENC != ENC_Q6_K) {
@@ -858,7 +898,8 @@ hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t oneshot, b
     }
 #undef DMX_CASE
     if (n == 0) return hipErrorInvalidValue;
-    return launch_persistent_best(t, n, p, lds, st);
+    const uint32_t nch = p.K / (uint32_t)E::CW;
+    return launch_persistent_best(t, n, p, lds, (nch + (1u << p.lanes_log2) - 1u) >> p.lanes_log2, st);
 }
 
 }  // namespace dmx

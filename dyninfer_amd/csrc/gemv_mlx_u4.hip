@@ -8,8 +8,10 @@ hipError_t launch_mlx(const GemvParams& p, uint32_t B, uint32_t oneshot, hipStre
     using E = EncMlxU4;
     const size_t lds = (size_t)xtile_bytes(E::ENC, B, p.K);
     if (oneshot) {
-#define DMX_ONESHOT(b, c) \
-    if (B == b && oneshot == c) return launch_oneshot(mlx_u4_gemv_oneshot_kernel<c, b, XBF16>, p, lds, st);
+#define DMX_ONESHOT(b, c)                                                                                  \
+    if (B == b && oneshot == c)                                                                            \
+        return launch_oneshot(mlx_u4_gemv_oneshot_kernel<c, b, XBF16, 512>, mlx_u4_gemv_oneshot_kernel<c, b, XBF16, 256>, \
+                              p, lds, st);
         DMX_ONESHOT(1, 1)
         DMX_ONESHOT(1, 2)
         DMX_ONESHOT(1, 3)
@@ -35,7 +37,8 @@ hipError_t launch_mlx(const GemvParams& p, uint32_t B, uint32_t oneshot, hipStre
     }
 #undef DMX_CASE
     if (n == 0) return hipErrorInvalidValue;
-    return launch_persistent_best(t, n, p, lds, st);
+    const uint32_t nch = p.K / (uint32_t)E::CW;
+    return launch_persistent_best(t, n, p, lds, (nch + (1u << p.lanes_log2) - 1u) >> p.lanes_log2, st);
 }
 }  // namespace
 
