@@ -487,13 +487,13 @@ __device__ __forceinline__ void reduce_store(float (&acc)[R][B], const RowBlock&
 // task of compute.  stage(mid) stages the activations (with a barrier) in
 // every wave and calls mid(), which issues the first task's loads, between
 // issuing the activation loads and using them.
-template <class E, int R, int B, class LOAD, class STAGE>
+template <class E, int R, int B, int TH, class LOAD, class STAGE>
 __device__ __forceinline__ void gemv_pipeline(const GemvParams& p, const uint8_t* lds, LOAD&& load, STAGE&& stage) {
     const uint32_t lane = threadIdx.x & 63u;
-    // The launch shape comes from compile-time constants and the parameters:
-    // reading blockDim/gridDim costs a load from the dispatch packet that the
-    // first weight loads would wait behind.
-    const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (uint32_t)(kGemvThreads / 64) + (threadIdx.x >> 6));
+    // The launch shape comes from compile-time constants (TH: the workgroup
+    // size) and the parameters: reading blockDim/gridDim costs a load from the
+    // dispatch packet that the first weight loads would wait behind.
+    const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (uint32_t)(TH / 64) + (threadIdx.x >> 6));
     const uint32_t L = 1u << p.lanes_log2;
     const uint32_t j = lane & (L - 1u), g = lane >> p.lanes_log2;
     const uint32_t rows_per_rb = (64u >> p.lanes_log2) * (uint32_t)R;
@@ -636,12 +636,12 @@ __device__ __forceinline__ void gemv_oneshot(const GemvParams& p, const uint8_t*
 // ---------------------------------------------------------------- GGUF
 // Weight offsets are 32-bit (the C ABI limits one weight to 4 GiB), so loads
 // use a uniform 64-bit base plus a per-lane 32-bit offset.
-template <class E, int B, int R, bool XBF16>
-__global__ __launch_bounds__(kGemvThreads) void gguf_gemv_kernel(const GemvParams p) {
+template <class E, int B, int R, bool XBF16, int TH = kGemvThreads>
+__global__ __launch_bounds__(TH) void gguf_gemv_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
     const uint32_t rowbytes = (p.K / (uint32_t)E::QK) * (uint32_t)E::BB;
     auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) { return E::load(rb.w, row * rowbytes, u); };
-    gemv_pipeline<E, R, B>(p, xlds, load, [&](auto&& mid) { stage_x_auto<E, B, XBF16>(xlds, p, mid); });
+    gemv_pipeline<E, R, B, TH>(p, xlds, load, [&](auto&& mid) { stage_x_auto<E, B, XBF16, TH>(xlds, p, mid); });
 }
 
 template <class E, int CPL, int B, bool XBF16, int TH>
@@ -683,7 +683,8 @@ struct MlxLoad {
 template <int B, int R, bool XBF16>
 __global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
-    gemv_pipeline<EncMlxU4, R, B>(p, xlds, MlxLoad(p), [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p, mid); });
+    gemv_pipeline<EncMlxU4, R, B, kGemvThreads>(p, xlds, MlxLoad(p),
+                                                [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p, mid); });
 }
 
 template <int CPL, int B, bool XBF16, int TH>
@@ -721,8 +722,8 @@ inline void layout_row_blocks(GemvParams& p, uint32_t rows_per_rb) {
 // each problem's row blocks, at least one each: problem i < nprob-1 gets
 // 1 + floor((W - nprob)·rb_i / rb_total) waves and the last the rest (at
 // least one, since the others take at most W - 1 together).
-inline void split_waves(GemvParams& p, uint32_t rows_per_rb) {
-    const uint64_t W = (uint64_t)p.grid * (kGemvThreads / 64);
+inline void split_waves(GemvParams& p, uint32_t rows_per_rb, uint32_t threads) {
+    const uint64_t W = (uint64_t)p.grid * (threads / 64);
     uint64_t rb[kMaxProblems] = {}, total = 0;
     for (uint32_t i = 0; i < p.nprob; i++) total += rb[i] = (p.n[i] + rows_per_rb - 1) / rows_per_rb;
     uint64_t end = 0;
@@ -739,6 +740,7 @@ typedef void (*GemvKernel)(GemvParams);
 struct GemvTile {
     uint32_t R;
     GemvKernel kernel;
+    uint32_t threads;  // workgroup size
 };
 
 // Persistent launch over the instantiated tiles t[0..n) (widest first).  Each
@@ -761,7 +763,6 @@ struct GemvTile {
 // half 1 (49% of HBM peak), 1- and 2-row tiles split them evenly (54%).
 inline hipError_t launch_persistent_best(const GemvTile* t, int n, const GemvParams& p0, size_t lds,
                                          uint32_t cpl, hipStream_t st) {
-    constexpr uint64_t waves = kGemvThreads / 64;
     const uint32_t groups = 64u >> p0.lanes_log2;  // lane groups per wave
     uint64_t total_rows = 0;
     for (uint32_t k = 0; k < p0.nprob; k++) total_rows += p0.n[k];
@@ -771,15 +772,16 @@ inline hipError_t launch_persistent_best(const GemvTile* t, int n, const GemvPar
     for (int i = 0; i < n; i++) {
         q = p0;
         const uint32_t rows_per_rb = groups * t[i].R;
+        const uint64_t waves = t[i].threads / 64;
         layout_row_blocks(q, rows_per_rb);
         int cus = 0, per_cu = 0;
-        hipError_t e = cached_occupancy(reinterpret_cast<const void*>(t[i].kernel), lds, kGemvThreads, &per_cu, &cus);
+        hipError_t e = cached_occupancy(reinterpret_cast<const void*>(t[i].kernel), lds, (int)t[i].threads, &per_cu, &cus);
         if (e != hipSuccess) return e;
         if (per_cu < 1 || cus < 1) continue;
         const uint64_t cap = (uint64_t)per_cu * (uint64_t)cus;
         const uint64_t want = ((uint64_t)q.total_rb + waves - 1) / waves;
         q.grid = (uint32_t)(want < cap ? want : cap);
-        split_waves(q, rows_per_rb);
+        split_waves(q, rows_per_rb, t[i].threads);
         uint64_t rbs = 0;  // row blocks of the busiest wave
         for (uint32_t k = 0; k < q.nprob; k++) {
             const uint64_t nw = q.wave_end[k] - (k ? q.wave_end[k - 1] : 0u);
@@ -804,20 +806,21 @@ inline hipError_t launch_persistent_best(const GemvTile* t, int n, const GemvPar
         chosen = chosen_even;
     }
     if (pick < 0) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL(t[pick].kernel, dim3(chosen.grid), dim3(kGemvThreads), lds, st, chosen);
+    hipLaunchKernelGGL(t[pick].kernel, dim3(chosen.grid), dim3(t[pick].threads), lds, st, chosen);
     return hipGetLastError();
 }
 
 // The persistent tiles instantiated for register batch B: the default rows per
 // group W, half of it, and for one activation row every power of two down
-// to one row.  gemv_tile<R>() names the kernel of R rows.
+// to one row.  gemv_tile<R>() names the kernel of R rows, of `threads`
+// threads per workgroup.
 template <class E, int B, class MK>
-int gemv_tiles(GemvTile (&t)[3], MK&& gemv_tile) {
+int gemv_tiles(GemvTile (&t)[3], MK&& gemv_tile, uint32_t threads = kGemvThreads) {
     constexpr int W = rows_per_group<E, B>();
     int n = 0;
-    t[n++] = {(uint32_t)W, gemv_tile(std::integral_constant<int, W>())};
-    if constexpr (W >= 2) t[n++] = {(uint32_t)(W / 2), gemv_tile(std::integral_constant<int, W / 2>())};
-    if constexpr (W >= 4 && B == 1) t[n++] = {(uint32_t)(W / 4), gemv_tile(std::integral_constant<int, W / 4>())};
+    t[n++] = {(uint32_t)W, gemv_tile(std::integral_constant<int, W>()), threads};
+    if constexpr (W >= 2) t[n++] = {(uint32_t)(W / 2), gemv_tile(std::integral_constant<int, W / 2>()), threads};
+    if constexpr (W >= 4 && B == 1) t[n++] = {(uint32_t)(W / 4), gemv_tile(std::integral_constant<int, W / 4>()), threads};
     return n;
 }
 
@@ -884,13 +887,26 @@ hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t oneshot, b
     }
     GemvTile t[3];
     int n = 0;
+    // One activation row and K > 8192: 1024-thread workgroups, one per CU,
+    // stage the activations half as often per CU, in one round of loads.
+    // Staging is VALU work per workgroup (~7.5 instructions per activation
+    // for Q6_K) and a launch's waves all stage before their first product: on
+    // the 8B down_proj (Q6_K 4096x12288, 3 tasks per wave) it ended ~8,000
+    // cycles in (two rounds of 512 threads, the second queued behind the
+    // first task's weights), and 1024 threads took 12.1-12.4 us against
+    // 13.0-13.5 us.  At K = 4096 1024 threads measured 1-2% slower.
+    const uint32_t nch = p.K / (uint32_t)E::CW;
+    const bool big = B == 1 && p.K > 8192u;
 #define DMX_CASE(b)                                                                                            \
     case b:                                                                                                    \
         if constexpr (b <= max_register_batch(E::ENC))                                                         \
             n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, b, decltype(r)::value, false>; }); \
         break;
     switch (B) {
-        DMX_CASE(1)
+    case 1:
+        n = big ? gemv_tiles<E, 1>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, 1, decltype(r)::value, false, 1024>; }, 1024u)
+                : gemv_tiles<E, 1>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, 1, decltype(r)::value, false>; });
+        break;
         DMX_CASE(2)
         DMX_CASE(4)
         DMX_CASE(8)
@@ -898,7 +914,6 @@ hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t oneshot, b
     }
 #undef DMX_CASE
     if (n == 0) return hipErrorInvalidValue;
-    const uint32_t nch = p.K / (uint32_t)E::CW;
     return launch_persistent_best(t, n, p, lds, (nch + (1u << p.lanes_log2) - 1u) >> p.lanes_log2, st);
 }
 

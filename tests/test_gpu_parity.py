@@ -281,7 +281,8 @@ def test_gemv_mlx_f32_io(ctx):
 
 # ----------------------------------------------------------------- GEMM (Q4_0 MFMA)
 @pytest.mark.parametrize("m,n,k", [(1, 128, 64), (17, 130, 96), (128, 256, 512), (200, 384, 1024), (512, 3072, 1024),
-                                   (512, 1024, 3072), (128, 2048, 1024), (2048, 1024, 1024)])
+                                   (512, 1024, 3072), (128, 2048, 1024), (2048, 1024, 1024),
+                                   (2000, 3000, 1024)])  # 384 tiles of 128x128, ragged rows and columns
 @pytest.mark.parametrize("ybf16", [False, True])
 def test_gemm_q4_0(ctx, m, n, k, ybf16):
     w, data = gguf(oracle.Q4_0, n, k, seed=m + n + k)
@@ -300,7 +301,8 @@ def test_gemm_q4_0(ctx, m, n, k, ybf16):
     assert np.all(err <= TOL + extra), err.max()
 
 
-@pytest.mark.parametrize("m,n,k", [(200, 384, 1024), (512, 3072, 1024), (96, 1040, 2048), (512, 1024, 3072), (130, 2000, 768)])
+@pytest.mark.parametrize("m,n,k", [(200, 384, 1024), (512, 3072, 1024), (96, 1040, 2048), (512, 1024, 3072), (130, 2000, 768),
+                                   (2048, 3072, 768)])
 def test_gemm_q4_0_offset_weights(ctx, m, n, k):
     # weight blocks starting 2 bytes past a 4-byte boundary (GGUF tensors are
     # only 2-byte aligned); ragged row and column tiles
@@ -396,6 +398,7 @@ def test_gemv_full_size_rows_subset(ctx, gtype, n, k, batch):
     (300, 8192),    # latency mode, 4 chunks per lane (Q6_K: 2)
     (1024, 12288),  # persistent pipeline, one row per lane group (6 chunks per lane)
     (8448, 12288),  # persistent pipeline, 4 rows per lane group (Q6_K: 2); rows subset checked
+                    # (K = 12288: 1024-thread workgroups)
 ])
 def test_gemv_gguf_kernel_paths(ctx, gtype, n, k):
     """Batch-1 shapes that select each GEMV kernel path (latency mode with 3 and
