@@ -273,6 +273,32 @@ def bench_gemm(torch, d, ctx, m, n, k, iters=50):
 
 
 # ------------------------------------------------------------------ CPU baseline
+def bench_embedding(torch, d, ctx, enc, vocab, k, n, iters=50):
+    """Embedding gather of n token rows from a [vocab, k] weight (the tied Qwen3
+    embedding).  Algorithmic HBM bytes per launch: the n gathered rows' on-disk
+    bytes plus their f32 output (4 k bytes each) plus the ids."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    w = gguf_tensor(torch, d, enc, vocab, k, gen)
+    ids = torch.randint(0, vocab, (n,), device="cuda", generator=gen, dtype=torch.int64)
+    out = torch.empty(n, k, device="cuda")
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        for _ in range(3):
+            ctx.embedding(w, ids, out, stream=st)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(iters):
+            ctx.embedding(w, ids, out, stream=st)
+        b.record(st)
+        torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / iters
+    nbytes = n * (w.nbytes // vocab + 4 * k + 8)
+    return {"us": round(us, 3), "bytes_per_launch": nbytes, "GBps": round(nbytes / us / 1e3, 1),
+            "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
 def cpu_baseline(seconds: float = 12.0):
     """The oracle's CPU contraction (dequantisation adjacent to an f32 dot, the
     reference's CPU semantics) timed on this host over config 1's matmuls, for a
@@ -416,9 +442,18 @@ def main() -> int:
             ms8 = r.time_graph(r.capture(), max(3, args.steps // 5), 2)
             c4[f"batch{b}"] = {"us_per_step": round(ms8 * 1e3, 1), "weight_GBps": round(s4.weight_bytes / ms8 / 1e6, 1),
                                "hbm_frac": round(s4.weight_bytes / ms8 / 1e6 / HBM_PEAK_GBS, 4),
-                               "tokens_per_s": round(b / (ms8 * 1e-3), 1)}
+                               "tokens_per_s": round(b / (ms8 * 1e-3), 1),
+                               "breakdown": {k: {"launches_per_step": n, "us_per_launch": round(us, 3),
+                                                 "GBps": round(nb / (us * 1e-6) / 1e9, 1)}
+                                             for k, (n, us, nb) in sorted(r.label_times(reps=5).items())}}
+            del r
         extra["config4_qwen3_8b_step"] = c4
         del s4
+        log("embedding gather (tied Qwen3 embeddings) ...")
+        extra["embedding_gather"] = {
+            f"{name}_n{n}": bench_embedding(torch, d, ctx, enc, 151936, k, n)
+            for name, enc, k in (("q6_k_151936x1024", d.ENC_Q6_K, 1024), ("q4_0_151936x4096", d.ENC_Q4_0, 4096))
+            for n in (1, 512, 4096)}
 
     cpu = None
     if not args.no_cpu:

@@ -44,7 +44,7 @@ _GGUF_BLOCK = {ENC_Q4_0: (32, 18), ENC_Q4_1: (32, 20), ENC_Q8_0: (32, 34), ENC_Q
 
 EXPORTED_SYMBOLS = (
     "dyninfer_mi355x_open", "dyninfer_mi355x_close", "dyninfer_mi355x_last_error", "dyninfer_mi355x_qlinear",
-    "dyninfer_mi355x_qlinear_multi", "dyninfer_mi355x_dequant", "dyninfer_mi355x_supports",
+    "dyninfer_mi355x_qlinear_multi", "dyninfer_mi355x_dequant", "dyninfer_mi355x_embedding", "dyninfer_mi355x_supports",
     "dyninfer_mi355x_candidates_json", "dyninfer_mi355x_registry_select", "dyninfer_mi355x_registry_require",
     "dyninfer_mi355x_version",
 )
@@ -88,6 +88,7 @@ def library() -> ctypes.CDLL:
         "dyninfer_mi355x_qlinear": (I, [P, W, P, U32, U32, P, U32, P]),
         "dyninfer_mi355x_qlinear_multi": (I, [P, W, U32, P, U32, U32, ctypes.POINTER(P), U32, P]),
         "dyninfer_mi355x_dequant": (I, [P, W, P, P]),
+        "dyninfer_mi355x_embedding": (I, [P, W, P, U32, P, P]),
         "dyninfer_mi355x_supports": (I, [W, U32, U32, U32]),
         "dyninfer_mi355x_candidates_json": (ctypes.c_char_p, []),
         "dyninfer_mi355x_registry_select": (I, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, P, SZ,
@@ -236,6 +237,19 @@ class Context:
             out = torch.empty((w.rows, w.cols), dtype=torch.float32, device=dev)
         wc = w.c()
         _check(self._lib.dyninfer_mi355x_dequant(self._h, ctypes.byref(wc), out.data_ptr(), self._stream(stream)))
+        return out
+
+    def embedding(self, w: QWeight, ids, out=None, stream=None):
+        """Gather rows ids (device int64 [n]) of W and dequantise them -> f32 [n, cols]."""
+        import torch
+        if ids.dtype != torch.int64 or not ids.is_cuda or not ids.is_contiguous():
+            raise DyninferError(ERR_INVALID_ARGUMENT, "ids must be a contiguous int64 device tensor")
+        n = ids.numel()
+        if out is None:
+            out = torch.empty((n, w.cols), dtype=torch.float32, device=ids.device)
+        wc = w.c()
+        _check(self._lib.dyninfer_mi355x_embedding(self._h, ctypes.byref(wc), ids.data_ptr() if n else None, n,
+                                                   out.data_ptr() if n else None, self._stream(stream)))
         return out
 
 

@@ -274,6 +274,27 @@ int dyninfer_mi355x_dequant(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t
     return DYNINFER_MI355X_OK;
 }
 
+int dyninfer_mi355x_embedding(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* w, const int64_t* ids,
+                              uint32_t n_ids, float* out, void* stream) {
+    if (int rc = check_ctx(ctx)) return rc;
+    if (int rc = check_weight(w)) return rc;
+    if (n_ids == 0) return DYNINFER_MI355X_OK;  // an empty batch gathers nothing
+    if (!ids || !aligned(ids, 8)) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "ids is NULL or not 8-byte aligned");
+    if (!out || !aligned(out, 16))
+        return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "output is NULL or not 16-byte aligned");
+    const uint64_t per_row = (w->cols / 4 + 255) / 256;
+    if ((uint64_t)n_ids * per_row > 0x7FFFFFFFull)
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "n_ids * ceil(K / 1024) must stay below 2^31");
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipError_t e = dmx::gather_launch(w->encoding, static_cast<const uint8_t*>(w->data),
+                                      static_cast<const uint8_t*>(w->scales), static_cast<const uint8_t*>(w->biases),
+                                      (uint32_t)w->rows, (uint32_t)w->cols, w->group_size, w->scale_dtype, ids, n_ids,
+                                      out, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "embedding launch");
+    return DYNINFER_MI355X_OK;
+}
+
 const char* dyninfer_mi355x_candidates_json(void) { return dmx::candidates_json().c_str(); }
 
 static int registry_call(const char* c, const char* r, const char* t, char* out, size_t cap, size_t* len, bool req) {

@@ -86,6 +86,12 @@ bool gemv_k_supported(uint32_t enc, uint32_t K);
 hipError_t dequant_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, const uint8_t* bi, uint32_t N,
                           uint32_t K, uint32_t group, uint32_t sdtype, float* out, hipStream_t stream);
 
+// Embedding gather: out[i, :] = dequant(W[ids[i], :]) in f32, [n_ids, K]; ids outside
+// [0, vocab) give a NaN row.  out must be 16-byte aligned.
+hipError_t gather_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, const uint8_t* bi, uint32_t vocab,
+                         uint32_t K, uint32_t group, uint32_t sdtype, const int64_t* ids, uint32_t n_ids, float* out,
+                         hipStream_t stream);
+
 // Q4_0 prefill GEMM on MFMA: Y[M, N] = X[M, K] · Wᵀ, X bf16, Y f32 or bf16.
 hipError_t gemm_q4_0_launch(const uint8_t* w, uint32_t N, uint32_t K, const void* x, uint32_t M,
                             void* y, bool y_bf16, hipStream_t stream);

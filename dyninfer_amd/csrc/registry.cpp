@@ -80,11 +80,17 @@ const std::string& candidates_json() {
                                        ? "; prefill GEMM dequantises into LDS and feeds f16 MFMA"
                                        : "") +
                                   "; f32 or bf16 activations";
+            all.push(candidate(g.codec, "embedding", "gather", g.block,
+                               std::string("Gathers rows of official GGML ") + g.codec +
+                                   " blocks in place on gfx950 and dequantises them to f32 (bit-exact)"));
             all.push(candidate(g.codec, "linear", "matmul", g.block, n));
             all.push(candidate(g.codec, "output_projection", "output", g.block, n));
         }
         const std::string mlx = "Direct MLX U4 words with groupwise scale/bias on gfx950 (group size a multiple "
                                 "of 32), dequantised in registers next to the contraction; f32 or bf16 activations";
+        all.push(candidate("mlx.affine.u4", "embedding", "embedding", 32,
+                           "Gathers rows of MLX U4 words with groupwise scale/bias on gfx950 and dequantises them "
+                           "to f32 (bit-exact)"));
         all.push(candidate("mlx.affine.u4", "linear", "matmul", 32, mlx));
         all.push(candidate("mlx.affine.u4", "output_projection", "output", 32, mlx));
         return json::dump(all);

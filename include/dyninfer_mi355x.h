@@ -128,6 +128,20 @@ int dyninfer_mi355x_dequant(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t
                             float* out, void* stream);
 
 /*
+ * Quantized embedding gather: out[i, :] = dequant(W[ids[i], :]) as f32, out [n_ids, K]
+ * row-major, W [vocab = N, K] as for qlinear.  Replaces the Embedding lowering's
+ * gather helper, one row per call there (gguf_codegen.rs:316-348 `emit_gather` with
+ * the dequant body of :350-526, called from `emit_embedding_call` :214-232;
+ * mlx_affine.rs:628-675 `emit_gather_u4`, called from :438-462); here n_ids rows in
+ * one launch.  Values are bit-identical to dyninfer_mi355x_dequant's rows.
+ * ids: device int64 [n_ids], 8-byte aligned; an id outside [0, vocab) yields a row
+ * of NaN and reads no weight bytes (the reference leaves it undefined).  out: device,
+ * 16-byte aligned.  n_ids == 0 is a no-op.
+ */
+int dyninfer_mi355x_embedding(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* w,
+                              const int64_t* ids, uint32_t n_ids, float* out, void* stream);
+
+/*
  * 1 if (w, rows, x_dtype, y_dtype) is inside the qualified envelope, else 0 (and
  * last_error says why).  Host-only; same rules as the validation in
  * q4_0.rs:40-113 / gguf_block.rs:66-156 / mlx_affine.rs:55-155 plus this

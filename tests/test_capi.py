@@ -40,7 +40,7 @@ def test_nm_exports_are_c_linkage():
 
 def test_version_and_candidates_json():
     assert b"gfx950" in d.library().dyninfer_mi355x_version()
-    assert len(d.candidates()) == 10
+    assert len(d.candidates()) == 15
 
 
 def w(enc, rows=64, cols=256, data=0x1000, **kw):
@@ -87,6 +87,8 @@ def test_calls_without_context_fail_cleanly():
     assert rc == d.ERR_INVALID_ARGUMENT
     assert "context" in lib.dyninfer_mi355x_last_error().decode()
     rc = lib.dyninfer_mi355x_dequant(None, ctypes.byref(wc), 0x1000, None)
+    assert rc == d.ERR_INVALID_ARGUMENT
+    rc = lib.dyninfer_mi355x_embedding(None, ctypes.byref(wc), 0x1000, 1, 0x2000, None)
     assert rc == d.ERR_INVALID_ARGUMENT
 
 

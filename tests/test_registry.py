@@ -195,9 +195,16 @@ def test_axis_not_divisible_rejects():
     assert ours["reasons"] == [{"reason": "axis_not_divisible", "axis": 1, "dimension": 300, "multiple_of": 256}]
 
 
-def test_embedding_has_no_mi355x_candidate():
-    rep = d.registry_select(gguf_request("gguf.q4_0", 151936, 1024, op="embedding"), hip("gfx950"), full_registry())
-    assert rep["selected"]["descriptor"]["id"] == "gguf.q4_0.gather.iree_block_hip"
+@pytest.mark.parametrize("codec,block,suffix", [("gguf.q4_0", 32, "gather"), ("gguf.q4_1", 32, "gather"),
+                                                ("gguf.q8_0", 32, "gather"), ("gguf.q6_k", 256, "gather"),
+                                                ("mlx.affine.u4", 32, "embedding")])
+def test_embedding_selects_mi355x_gather_on_gfx950(codec, block, suffix):
+    req = gguf_request(codec, 151936, 4 * block, op="embedding", mode="prefill")
+    sel = d.registry_require(req, hip("gfx950"), full_registry())
+    assert sel["descriptor"]["id"] == f"{codec}.{suffix}.mi355x_hip" and sel["score"] == 1400
+    rep = d.registry_select(req, hip("gfx1151"), full_registry())
+    assert rep["selected"]["descriptor"]["id"] in (f"{codec}.gather.iree_block_hip",
+                                                   "mlx.affine.u4.embedding.iree_grouped_hip")
 
 
 def test_duplicate_candidate_ids_are_rejected():
@@ -212,10 +219,10 @@ def test_candidates_match_the_serde_schema():
     keys = {"id", "operation", "encoding", "input_types", "output_types", "accumulator_types", "shape",
             "orientations", "target", "modes", "lowering", "deterministic_score", "readiness", "notes"}
     cands = d.candidates()
-    assert len(cands) == 10 and len({c["id"] for c in cands}) == 10
+    assert len(cands) == 15 and len({c["id"] for c in cands}) == 15
     for c in cands:
         assert set(c) == keys
-        assert c["operation"] in ("linear", "output_projection")
+        assert c["operation"] in ("embedding", "linear", "output_projection")
         assert c["readiness"] == "production"
         assert c["orientations"] == ["native"]
         assert set(c["modes"]) == {"prefill", "decode"}
