@@ -61,10 +61,12 @@ struct MfmaParams {
     uint32_t n[kMaxProblems];
     uint32_t tile_begin[kMaxProblems];  // first 16-row tile of each problem
     uint32_t total_tiles;
-    uint32_t grid;
+    uint32_t grid;        // workgroups per K segment (the launch has grid * nseg)
     uint32_t K;           // full reduction length
-    uint32_t k0;          // first k of this launch's segment
-    uint32_t nunit;       // blocks (Q4_0) or super-blocks (Q6_K) in the segment
+    uint32_t k0;          // first k of this launch's first segment
+    uint32_t nunit;       // blocks (Q4_0) or super-blocks (Q6_K) over all of the launch's segments
+    uint32_t seg_units;   // units per segment (the last may have fewer)
+    uint32_t nseg;        // K segments in this launch: workgroup w serves segment w / grid
     uint32_t nprob;
     uint32_t batch;
     uint32_t accumulate;  // add to y (later segments; f32 outputs only)
@@ -270,7 +272,11 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     constexpr uint32_t NSLOT = 16u * M::NP, NLD = (NSLOT + 63u) / 64u;  // window pieces, loads per lane
     constexpr int PF = SPLIT ? 2 : M::PF;  // tasks of raw loads in flight per wave
     constexpr uint32_t NW = kMfmaThreads / 64u;
-    const uint32_t ng = mfma_tasks<M, SPLIT>(p.nunit), nt = p.nunit / M::UPT;  // tasks with padding, without
+    // this workgroup's K segment: units [sidx·seg_units, ...) of the launch's range
+    const uint32_t sidx = p.nseg > 1u ? blockIdx.x / p.grid : 0u, bid = blockIdx.x - sidx * p.grid;
+    const uint32_t k0 = p.k0 + sidx * p.seg_units * M::UNIT;
+    const uint32_t nunit = p.nunit - sidx * p.seg_units < p.seg_units ? p.nunit - sidx * p.seg_units : p.seg_units;
+    const uint32_t ng = mfma_tasks<M, SPLIT>(nunit), nt = nunit / M::UPT;  // tasks with padding, without
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint4* xl = reinterpret_cast<uint4*>(lds);
@@ -283,12 +289,12 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     // workgroup w is wid = i·grid + w), so a few tiles still spread over all
     // CUs.  Split mode: workgroup w takes tiles w, w + grid, ... and its waves
     // split each tile's tasks (wave v: tasks t0 = v·tpw .. t0 + tpw - 1).
-    const uint32_t wid = SPLIT ? blockIdx.x : __builtin_amdgcn_readfirstlane(wv * p.grid + blockIdx.x);
+    const uint32_t wid = SPLIT ? bid : __builtin_amdgcn_readfirstlane(wv * p.grid + bid);
     const uint32_t W = SPLIT ? p.grid : p.grid * NW;
     const uint32_t tpw = SPLIT ? ng / NW : ng, t0 = SPLIT ? wv * tpw : 0u;
     const uint32_t m = lane & 15u, q = lane >> 4;
     const uint32_t ntw = wid < p.total_tiles ? (p.total_tiles - wid + W - 1u) / W : 0u;  // tiles of this wave
-    const uint32_t rowbytes = (p.K / M::UNIT) * M::UB, seg0 = (p.k0 / M::UNIT) * M::UB;
+    const uint32_t rowbytes = (p.K / M::UNIT) * M::UB, seg0 = (k0 / M::UNIT) * M::UB;
 
     // the wave's i-th tile (past the end: its last, or any tile for a wave
     // without tiles: loaded, never multiplied into a stored result)
@@ -376,7 +382,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
         }
         if constexpr (M::MLX) {
             // groups of the lane's k 64q..64q+31 and 64q+32..64q+63
-            const uint32_t kl = p.k0 + (t < nt ? t : nt - 1u) * M::KT + 64u * q;
+            const uint32_t kl = k0 + (t < nt ? t : nt - 1u) * M::KT + 64u * q;
             const uint32_t g0 = r.rowm * gpr + kl / p.group, g1 = r.rowm * gpr + (kl + 32u) / p.group;
             aux[0] = sbload(r.sc, g0);
             aux[1] = sbload(r.bi, g0);
@@ -403,10 +409,10 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = 0.0f;
         if (u < nunits && b < p.batch && g < nt) {
-            const size_t k0 = (size_t)b * p.K + p.k0 + M::KT * g;
+            const size_t xk0 = (size_t)b * p.K + k0 + M::KT * g;
             if (p.x_bf16) {  // two runs of 4 bf16: 8 bytes each
                 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-                const uint16_t* xr = static_cast<const uint16_t*>(p.x) + k0;
+                const uint16_t* xr = static_cast<const uint16_t*>(p.x) + xk0;
                 const u32x2 lo2 = *gptr<u32x2>(xr + M::run0(qq, j)), hi2 = *gptr<u32x2>(xr + M::run1(qq, j));
 #pragma unroll
                 for (int i = 0; i < 2; i++) {
@@ -416,7 +422,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
                     v[5 + 2 * i] = __uint_as_float(hi2[i] & 0xFFFF0000u);
                 }
             } else {
-                const float* xr = static_cast<const float*>(p.x) + k0;
+                const float* xr = static_cast<const float*>(p.x) + xk0;
                 const f32x4 lo4 = *gptr<f32x4>(xr + M::run0(qq, j)), hi4 = *gptr<f32x4>(xr + M::run1(qq, j));
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -592,30 +598,64 @@ uint32_t mfma_segment(uint32_t units) {
     return 0;
 }
 
+// Zeroes the f32 outputs [batch, n_i] of every problem (before a launch whose
+// K segments all add into them).
+__global__ __launch_bounds__(256) void mfma_zero_outputs_kernel(const MfmaParams p) {
+    const uint32_t i = blockIdx.y;
+    const uint64_t e = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (i < p.nprob && e < (uint64_t)p.batch * pick(i, p.n)) gptr_mut<float>(pick(i, p.y))[e] = 0.0f;
+}
+
 template <class M, bool SPLIT>
 hipError_t launch_mode(MfmaParams p, uint32_t units, bool y_bf16, hipStream_t st) {
-    const uint32_t seg = mfma_segment<M, SPLIT>(units);
+    uint32_t seg = mfma_segment<M, SPLIT>(units);
     if (seg == 0 || (y_bf16 && seg < units)) return hipErrorInvalidValue;
     auto kernel = y_bf16 ? gemv_mfma_kernel<M, true, SPLIT> : gemv_mfma_kernel<M, false, SPLIT>;
-    for (uint32_t b0 = 0; b0 < units; b0 += seg) {
-        const uint32_t nu = units - b0 < seg ? units - b0 : seg;
-        const size_t lds = mfma_lds_bytes<M, SPLIT>(nu);
-        int cus = 0, per_cu = 0;
-        hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, kMfmaThreads, &per_cu, &cus);
-        if (e != hipSuccess) return e;
-        if (per_cu < 1) return hipErrorInvalidConfiguration;
-        // every CU gets a workgroup while there are tiles: the tiles spread over
-        // the workgroups first
-        const uint64_t cap = (uint64_t)per_cu * cus;
-        p.grid = (uint32_t)(p.total_tiles < cap ? p.total_tiles : cap);
-        p.k0 = b0 * M::UNIT;
-        p.nunit = nu;
-        p.accumulate = b0 > 0 ? 1u : 0u;
-        hipLaunchKernelGGL(kernel, dim3(p.grid), dim3(kMfmaThreads), lds, st, p);
+    int cus = 0, per_cu = 0;
+    hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), mfma_lds_bytes<M, SPLIT>(seg), kMfmaThreads,
+                                    &per_cu, &cus);
+    if (e != hipSuccess) return e;
+    if (per_cu < 1 || cus < 1) return hipErrorInvalidConfiguration;
+    // K too long for LDS on a launch of at most one 16-row tile per CU: each
+    // workgroup takes nseg tiles of one segment (segments of whole rounds of
+    // tasks, a task per wave in split mode), so it stages a segment's
+    // activations once for nseg tiles instead of once per tile (8B down_proj,
+    // 4096 x 12288 Q6_K at 16 rows: 38.8 -> 35.2 us; cutting K where LDS does
+    // not force it measured slower: o_proj 4096 x 4096 Q4_0 11.3 -> 14.6 us).
+    bool shared_tiles = false;
+    if (!y_bf16 && seg < units && p.total_tiles <= (uint32_t)cus) {
+        const uint32_t step = SPLIT ? 8u * M::UPT : M::UPT;
+        if (seg / step * step >= step) {
+            seg = seg / step * step;
+            shared_tiles = true;
+        }
+    }
+    const uint32_t nseg = (units + seg - 1u) / seg;
+    const size_t lds = mfma_lds_bytes<M, SPLIT>(seg);
+    e = cached_occupancy(reinterpret_cast<const void*>(kernel), lds, kMfmaThreads, &per_cu, &cus);
+    if (e != hipSuccess) return e;
+    if (per_cu < 1) return hipErrorInvalidConfiguration;
+    // every CU gets a workgroup while there are tiles: the tiles spread over
+    // the workgroups first
+    const uint64_t cap = (uint64_t)per_cu * cus;
+    p.grid = (uint32_t)(p.total_tiles < cap ? p.total_tiles : cap);
+    if (shared_tiles) p.grid = (p.total_tiles + nseg - 1u) / nseg;  // about nseg tiles per workgroup
+    p.k0 = 0;
+    p.nunit = units;
+    p.seg_units = seg;
+    p.nseg = nseg;
+    p.accumulate = nseg > 1u ? 1u : 0u;
+    if (nseg > 1u) {  // every segment adds into y (f32): clear it first
+        uint32_t nmax = 0;
+        for (uint32_t i = 0; i < p.nprob; i++) nmax = p.n[i] > nmax ? p.n[i] : nmax;
+        const uint64_t elems = (uint64_t)p.batch * nmax;
+        hipLaunchKernelGGL(mfma_zero_outputs_kernel, dim3((unsigned)((elems + 255u) / 256u), p.nprob), dim3(256), 0, st,
+                           p);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    return hipSuccess;
+    hipLaunchKernelGGL(kernel, dim3(p.grid * nseg), dim3(kMfmaThreads), lds, st, p);
+    return hipGetLastError();
 }
 
 template <class M>
