@@ -186,6 +186,38 @@ def test_gemv_mfma(ctx, gtype, n, k, batch, ybf16, off):
     assert np.all(err <= 2.0 ** -10 + 2e-5 + extra), err.max()
 
 
+@pytest.mark.parametrize("gtype,n,k", [(oracle.Q6_K, 4096, 12288), (oracle.Q4_0, 2048, 16384)],
+                         ids=["q6_k-4096x12288", "q4_0-2048x16384"])
+def test_gemv_mfma_segments_graph_replays(ctx, gtype, n, k):
+    """Long K at 16 rows: a fill kernel zeroes y, then every K segment adds into
+    it atomically.  Captured in a HIP graph and replayed three times with eager
+    launches between: every replay must clear and re-accumulate (agreeing with
+    the eager result up to the order of the atomic adds) and stay in the f16 bound."""
+    w, data = gguf(gtype, n, k, seed=n + k)
+    x = dev(oracle.randn(16 * k, seed=5).reshape(16, k))
+    eager = ctx.qlinear(w, x).cpu().numpy()
+    y64, absdot = oracle.linear_f64(x.cpu().numpy(), oracle.dequant_gguf(gtype, data, n, k))
+    assert oracle.normalized_error(eager, y64, absdot) <= 2.0 ** -10 + 2e-5
+    y = torch.full((16, n), 7.0, device="cuda")
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        ctx.qlinear(w, x, y, stream=st)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            ctx.qlinear(w, x, y, stream=st)
+    torch.cuda.synchronize()
+    den = np.where(absdot > 0, absdot, 1)
+    for _ in range(3):
+        y.fill_(7.0)
+        ctx.qlinear(w, x * 0.5)  # eager work between the replays
+        g.replay()
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        assert np.max(np.abs(got.astype(np.float64) - eager) / den) <= 1e-6
+    del g
+
+
 @pytest.mark.parametrize("gtype", [oracle.Q4_0, oracle.Q6_K], ids=oracle.NAMES.get)
 def test_gemv_mfma_grouped(ctx, gtype):
     # q/k/v of Qwen3-8B share one activation at batch 16: one MFMA launch, three outputs
