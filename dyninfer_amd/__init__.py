@@ -45,6 +45,9 @@ _GGUF_BLOCK = {ENC_Q4_0: (32, 18), ENC_Q4_1: (32, 20), ENC_Q8_0: (32, 34), ENC_Q
 EXPORTED_SYMBOLS = (
     "dyninfer_mi355x_open", "dyninfer_mi355x_close", "dyninfer_mi355x_last_error", "dyninfer_mi355x_qlinear",
     "dyninfer_mi355x_qlinear_multi", "dyninfer_mi355x_dequant", "dyninfer_mi355x_embedding", "dyninfer_mi355x_supports",
+    "dyninfer_mi355x_gguf_open", "dyninfer_mi355x_gguf_open_memory", "dyninfer_mi355x_gguf_close",
+    "dyninfer_mi355x_gguf_tensor_count", "dyninfer_mi355x_gguf_metadata_json", "dyninfer_mi355x_gguf_tensor",
+    "dyninfer_mi355x_gguf_find", "dyninfer_mi355x_gguf_upload", "dyninfer_mi355x_gguf_qweight",
     "dyninfer_mi355x_candidates_json", "dyninfer_mi355x_registry_select", "dyninfer_mi355x_registry_require",
     "dyninfer_mi355x_version",
 )
@@ -70,6 +73,11 @@ class _QWeightC(ctypes.Structure):
 _lib: Optional[ctypes.CDLL] = None
 
 
+class _GgufTensorC(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("type_code", ctypes.c_uint32), ("n_dims", ctypes.c_uint32),
+                ("dims", ctypes.c_uint64 * 16), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
+
+
 def library() -> ctypes.CDLL:
     """Load the built library (raises if it has not been built)."""
     global _lib
@@ -89,6 +97,15 @@ def library() -> ctypes.CDLL:
         "dyninfer_mi355x_qlinear_multi": (I, [P, W, U32, P, U32, U32, ctypes.POINTER(P), U32, P]),
         "dyninfer_mi355x_dequant": (I, [P, W, P, P]),
         "dyninfer_mi355x_embedding": (I, [P, W, P, U32, P, P]),
+        "dyninfer_mi355x_gguf_open": (I, [ctypes.c_char_p, ctypes.POINTER(P)]),
+        "dyninfer_mi355x_gguf_open_memory": (I, [P, ctypes.c_uint64, ctypes.POINTER(P)]),
+        "dyninfer_mi355x_gguf_close": (I, [P]),
+        "dyninfer_mi355x_gguf_tensor_count": (ctypes.c_uint64, [P]),
+        "dyninfer_mi355x_gguf_metadata_json": (ctypes.c_char_p, [P]),
+        "dyninfer_mi355x_gguf_tensor": (I, [P, ctypes.c_uint64, ctypes.POINTER(_GgufTensorC)]),
+        "dyninfer_mi355x_gguf_find": (I, [P, ctypes.c_char_p, ctypes.POINTER(_GgufTensorC)]),
+        "dyninfer_mi355x_gguf_upload": (I, [P, ctypes.c_char_p, P, ctypes.c_uint64, P]),
+        "dyninfer_mi355x_gguf_qweight": (I, [P, ctypes.c_char_p, P, W]),
         "dyninfer_mi355x_supports": (I, [W, U32, U32, U32]),
         "dyninfer_mi355x_candidates_json": (ctypes.c_char_p, []),
         "dyninfer_mi355x_registry_select": (I, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, P, SZ,
@@ -279,3 +296,82 @@ def registry_select(request: dict, target: dict, cands=None) -> dict:
 def registry_require(request: dict, target: dict, cands=None) -> dict:
     """KernelRegistry::require -> SelectedKernelCandidate, or DyninferError(ERR_UNSUPPORTED, E_KERNEL_COVERAGE…)."""
     return _registry("dyninfer_mi355x_registry_require", request, target, cands)
+
+
+@dataclass
+class GgufTensor:
+    name: str
+    type_code: int
+    shape: tuple
+    offset: int
+    nbytes: int
+
+
+class GgufFile:
+    """Index of a GGUF file: exact byte ranges of its tensors (dyninfer_mi355x_gguf_*).
+    ``GgufFile(path)`` maps the file; ``GgufFile.from_bytes(b)`` indexes bytes in memory."""
+
+    def __init__(self, path: Optional[str] = None, _data=None):
+        self._lib = library()
+        self._h = ctypes.c_void_p()
+        self._keep = None
+        if _data is not None:
+            self._keep = ctypes.create_string_buffer(bytes(_data), len(_data))
+            _check(self._lib.dyninfer_mi355x_gguf_open_memory(ctypes.addressof(self._keep), len(_data),
+                                                              ctypes.byref(self._h)))
+        else:
+            _check(self._lib.dyninfer_mi355x_gguf_open(os.fsencode(path), ctypes.byref(self._h)))
+
+    @classmethod
+    def from_bytes(cls, data: bytes) -> "GgufFile":
+        return cls(_data=data)
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.dyninfer_mi355x_gguf_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def _py(t: "_GgufTensorC") -> GgufTensor:
+        return GgufTensor(t.name.decode(), t.type_code, tuple(t.dims[:t.n_dims]), t.offset, t.nbytes)
+
+    @property
+    def tensors(self) -> list:
+        out = []
+        for i in range(self._lib.dyninfer_mi355x_gguf_tensor_count(self._h)):
+            t = _GgufTensorC()
+            _check(self._lib.dyninfer_mi355x_gguf_tensor(self._h, i, ctypes.byref(t)))
+            out.append(self._py(t))
+        return out
+
+    @property
+    def metadata(self) -> dict:
+        return json.loads(self._lib.dyninfer_mi355x_gguf_metadata_json(self._h).decode())
+
+    def find(self, name: str) -> GgufTensor:
+        t = _GgufTensorC()
+        _check(self._lib.dyninfer_mi355x_gguf_find(self._h, name.encode(), ctypes.byref(t)))
+        return self._py(t)
+
+    def upload(self, name: str, dst=None, stream=None):
+        """Copy the tensor's exact bytes to the device (a new uint8 tensor unless dst is given)."""
+        import torch
+        if dst is None:
+            dst = torch.empty(self.find(name).nbytes, dtype=torch.uint8, device="cuda")
+        cap = dst.numel() * dst.element_size()
+        _check(self._lib.dyninfer_mi355x_gguf_upload(self._h, name.encode(), dst.data_ptr(), cap,
+                                                     Context._stream(stream)))
+        return dst
+
+    def qweight(self, name: str, device_data) -> QWeight:
+        """QWeight of a rank-2 Q4_0/Q4_1/Q8_0/Q6_K tensor whose bytes are at device_data."""
+        wc = _QWeightC()
+        _check(self._lib.dyninfer_mi355x_gguf_qweight(self._h, name.encode(), _ptr(device_data), ctypes.byref(wc)))
+        w = QWeight(wc.encoding, wc.rows, wc.cols, device_data)
+        return w

@@ -8,10 +8,18 @@
 
 #include <hip/hip_runtime.h>
 
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cerrno>
 #include <cstdio>
 #include <cstring>
 #include <string>
 
+#include "gguf.hpp"
 #include "kernels.hpp"
 #include "registry.hpp"
 
@@ -293,6 +301,118 @@ int dyninfer_mi355x_embedding(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight
                                       out, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "embedding launch");
     return DYNINFER_MI355X_OK;
+}
+
+struct dyninfer_gguf {
+    dmx::GgufIndex idx;
+};
+
+static int gguf_finish(const uint8_t* base, uint64_t len, void* map, dyninfer_gguf_t** out) {
+    auto* g = new dyninfer_gguf();
+    const std::string err = dmx::gguf_index(base, len, g->idx);
+    g->idx.map = map;
+    if (!err.empty()) {
+        dyninfer_mi355x_gguf_close(g);
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "invalid GGUF: " + err);
+    }
+    *out = g;
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_gguf_open(const char* path, dyninfer_gguf_t** out) {
+    if (!path || !out) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "path / out is NULL");
+    *out = nullptr;
+    const int fd = ::open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string("cannot open ") + path + ": " + std::strerror(errno));
+    struct stat st;
+    if (::fstat(fd, &st) != 0 || st.st_size <= 0) {
+        ::close(fd);
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, std::string("invalid GGUF: empty or unreadable file ") + path);
+    }
+    void* m = ::mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);
+    if (m == MAP_FAILED) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string("mmap failed: ") + std::strerror(errno));
+    return gguf_finish(static_cast<const uint8_t*>(m), (uint64_t)st.st_size, m, out);
+}
+
+int dyninfer_mi355x_gguf_open_memory(const void* data, uint64_t len, dyninfer_gguf_t** out) {
+    if (!data || !out) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "data / out is NULL");
+    *out = nullptr;
+    return gguf_finish(static_cast<const uint8_t*>(data), len, nullptr, out);
+}
+
+int dyninfer_mi355x_gguf_close(dyninfer_gguf_t* g) {
+    if (!g) return DYNINFER_MI355X_OK;
+    if (g->idx.map) ::munmap(g->idx.map, (size_t)g->idx.len);
+    delete g;
+    return DYNINFER_MI355X_OK;
+}
+
+uint64_t dyninfer_mi355x_gguf_tensor_count(const dyninfer_gguf_t* g) { return g ? g->idx.tensors.size() : 0; }
+
+const char* dyninfer_mi355x_gguf_metadata_json(const dyninfer_gguf_t* g) { return g ? g->idx.metadata_json.c_str() : "{}"; }
+
+static void gguf_fill(const dmx::GgufTensor& t, dyninfer_gguf_tensor_t* out) {
+    std::memset(out, 0, sizeof *out);
+    out->name = t.name.c_str();
+    out->type_code = t.type_code;
+    out->n_dims = (uint32_t)t.shape.size();
+    for (size_t i = 0; i < t.shape.size(); i++) out->dims[i] = t.shape[i];
+    out->offset = t.offset;
+    out->nbytes = t.nbytes;
+}
+
+static const dmx::GgufTensor* gguf_lookup(const dyninfer_gguf_t* g, const char* name) {
+    auto it = std::lower_bound(g->idx.tensors.begin(), g->idx.tensors.end(), name,
+                               [](const dmx::GgufTensor& t, const char* n) { return t.name < n; });
+    return it != g->idx.tensors.end() && it->name == name ? &*it : nullptr;
+}
+
+int dyninfer_mi355x_gguf_tensor(const dyninfer_gguf_t* g, uint64_t index, dyninfer_gguf_tensor_t* out) {
+    if (!g || !out) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "index / out is NULL");
+    if (index >= g->idx.tensors.size()) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "tensor index out of range");
+    gguf_fill(g->idx.tensors[index], out);
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_gguf_find(const dyninfer_gguf_t* g, const char* name, dyninfer_gguf_tensor_t* out) {
+    if (!g || !name || !out) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "index / name / out is NULL");
+    const dmx::GgufTensor* t = gguf_lookup(g, name);
+    if (!t) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string("no tensor named ") + name);
+    gguf_fill(*t, out);
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_gguf_upload(const dyninfer_gguf_t* g, const char* name, void* dst, uint64_t dst_bytes, void* stream) {
+    if (!g || !name || !dst) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "index / name / dst is NULL");
+    const dmx::GgufTensor* t = gguf_lookup(g, name);
+    if (!t) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string("no tensor named ") + name);
+    if (dst_bytes < t->nbytes)
+        return fail(DYNINFER_MI355X_ERR_BUFFER_TOO_SMALL, "destination needs " + std::to_string(t->nbytes) + " bytes");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = hipMemcpyAsync(dst, g->idx.base + t->offset, (size_t)t->nbytes, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync");
+    e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_gguf_qweight(const dyninfer_gguf_t* g, const char* name, const void* device_data,
+                                 dyninfer_qweight_t* out) {
+    if (!g || !name || !out) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "index / name / out is NULL");
+    const dmx::GgufTensor* t = gguf_lookup(g, name);
+    if (!t) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string("no tensor named ") + name);
+    if (t->shape.size() != 2) return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "tensor " + t->name + " is not rank 2");
+    if (t->type_code != dmx::ENC_Q4_0 && t->type_code != dmx::ENC_Q4_1 && t->type_code != dmx::ENC_Q8_0 &&
+        t->type_code != dmx::ENC_Q6_K)
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
+                    "tensor " + t->name + " has GGUF type " + std::to_string(t->type_code) + ", not Q4_0/Q4_1/Q8_0/Q6_K");
+    std::memset(out, 0, sizeof *out);
+    out->encoding = t->type_code;
+    out->rows = t->shape[0];
+    out->cols = t->shape[1];
+    out->data = device_data;
+    return check_weight(out);
 }
 
 const char* dyninfer_mi355x_candidates_json(void) { return dmx::candidates_json().c_str(); }

@@ -142,6 +142,47 @@ int dyninfer_mi355x_embedding(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight
                               const int64_t* ids, uint32_t n_ids, float* out, void* stream);
 
 /*
+ * GGUF container index: the exact byte range of every tensor of a GGUF file, so a
+ * weight reaches the device as a plain copy of its on-disk bytes (no repack).
+ * Restates the reference's indexer (crates/dyninfer-checkpoint-gguf/src/container.rs:179-340:
+ * magic, version 2..3, metadata, tensor directory with dims reversed to row-major,
+ * data section at the header end rounded up to general.alignment, default 32, :16)
+ * under its default inspection limits (crates/dyninfer-checkpoint/src/limits.rs), and
+ * the provider plan's exact (file, offset, length) ranges (crates/dyninfer-checkpoint/src/provider.rs:9-60).
+ * Tensors are listed sorted by name, as the reference's entries.  Duplicate tensor
+ * names are rejected.
+ */
+typedef struct dyninfer_gguf dyninfer_gguf_t;
+
+typedef struct dyninfer_gguf_tensor {
+    const char* name;   /* NUL-terminated, owned by the index */
+    uint32_t type_code; /* GgufType code (types.rs:10-45) */
+    uint32_t n_dims;    /* logical rank */
+    uint64_t dims[16];  /* row-major logical shape, dims[0] outermost */
+    uint64_t offset;    /* absolute byte offset of the tensor's data in the file */
+    uint64_t nbytes;    /* exact byte length */
+} dyninfer_gguf_tensor_t;
+
+/* Maps the file read-only and indexes it.  */
+int dyninfer_mi355x_gguf_open(const char* path, dyninfer_gguf_t** out);
+/* Indexes caller-owned bytes (they must outlive the index).  */
+int dyninfer_mi355x_gguf_open_memory(const void* data, uint64_t len, dyninfer_gguf_t** out);
+int dyninfer_mi355x_gguf_close(dyninfer_gguf_t* g);
+uint64_t dyninfer_mi355x_gguf_tensor_count(const dyninfer_gguf_t* g);
+/* Metadata key/values as one JSON object (keys sorted; f32/f64 as numbers, non-finite as null). */
+const char* dyninfer_mi355x_gguf_metadata_json(const dyninfer_gguf_t* g);
+int dyninfer_mi355x_gguf_tensor(const dyninfer_gguf_t* g, uint64_t index, dyninfer_gguf_tensor_t* out);
+int dyninfer_mi355x_gguf_find(const dyninfer_gguf_t* g, const char* name, dyninfer_gguf_tensor_t* out);
+/* Copies the tensor's exact bytes to device memory dst (dst_bytes >= nbytes) on `stream`,
+ * then waits for the copy (the source is pageable mapped memory).  */
+int dyninfer_mi355x_gguf_upload(const dyninfer_gguf_t* g, const char* name, void* dst, uint64_t dst_bytes,
+                                void* stream);
+/* Describes a rank-2 Q4_0/Q4_1/Q8_0/Q6_K tensor whose bytes are at device_data as a
+ * dyninfer_qweight_t (rows = dims[0], cols = dims[1]); other types are unsupported. */
+int dyninfer_mi355x_gguf_qweight(const dyninfer_gguf_t* g, const char* name, const void* device_data,
+                                 dyninfer_qweight_t* out);
+
+/*
  * 1 if (w, rows, x_dtype, y_dtype) is inside the qualified envelope, else 0 (and
  * last_error says why).  Host-only; same rules as the validation in
  * q4_0.rs:40-113 / gguf_block.rs:66-156 / mlx_affine.rs:55-155 plus this
