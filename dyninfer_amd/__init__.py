@@ -67,6 +67,7 @@ class _QWeightC(ctypes.Structure):
         ("encoding", ctypes.c_uint32), ("group_size", ctypes.c_uint32), ("rows", ctypes.c_uint64),
         ("cols", ctypes.c_uint64), ("data", ctypes.c_void_p), ("scales", ctypes.c_void_p),
         ("biases", ctypes.c_void_p), ("scale_dtype", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+        ("data_bytes", ctypes.c_uint64), ("scales_bytes", ctypes.c_uint64), ("biases_bytes", ctypes.c_uint64),
     ]
 
 
@@ -146,6 +147,13 @@ def _ptr(t) -> Optional[int]:
     return t.data_ptr() if hasattr(t, "data_ptr") else int(t)
 
 
+def _nbytes(t) -> Optional[int]:
+    """Byte length of a tensor (None for a raw address)."""
+    if t is None or not hasattr(t, "data_ptr"):
+        return None
+    return t.numel() * t.element_size()
+
+
 @dataclass
 class QWeight:
     """A quantized weight [rows = N out, cols = K in] in its on-disk bytes.
@@ -153,6 +161,10 @@ class QWeight:
     GGUF: ``data`` holds the interleaved blocks.  MLX U4: ``data`` = packed u32
     words, ``scales``/``biases`` = [N, K/group] of ``scale_dtype``.  Tensors (or
     raw device addresses) must stay alive while kernels use them.
+
+    Component byte lengths (``*_bytes``) default to the tensors' own sizes, so
+    the C ABI checks the buffers actually bound against the encoding's byte
+    totals; for a raw address they default to the encoding's expected length.
     """
     encoding: int
     rows: int
@@ -162,10 +174,24 @@ class QWeight:
     biases: object = None
     group_size: int = 0
     scale_dtype: int = DTYPE_BF16
+    data_bytes: Optional[int] = None
+    scales_bytes: Optional[int] = None
+    biases_bytes: Optional[int] = None
+
+    def _expected(self):
+        if self.encoding in _GGUF_BLOCK:
+            bw, bb = _GGUF_BLOCK[self.encoding]
+            return self.rows * (self.cols // bw) * bb, 0, 0
+        es = 4 if self.scale_dtype == DTYPE_F32 else 2
+        g = self.rows * (self.cols // self.group_size) * es if self.group_size else 0
+        return self.rows * self.cols // 2, g, g
 
     def c(self) -> _QWeightC:
+        ed, es, eb = self._expected()
+        pick = lambda given, t, exp: given if given is not None else (_nbytes(t) if _nbytes(t) is not None else exp)
         return _QWeightC(self.encoding, self.group_size, self.rows, self.cols, _ptr(self.data), _ptr(self.scales),
-                         _ptr(self.biases), self.scale_dtype, 0)
+                         _ptr(self.biases), self.scale_dtype, 0, pick(self.data_bytes, self.data, ed),
+                         pick(self.scales_bytes, self.scales, es), pick(self.biases_bytes, self.biases, eb))
 
     @property
     def nbytes(self) -> int:
@@ -373,5 +399,4 @@ class GgufFile:
         """QWeight of a rank-2 Q4_0/Q4_1/Q8_0/Q6_K tensor whose bytes are at device_data."""
         wc = _QWeightC()
         _check(self._lib.dyninfer_mi355x_gguf_qweight(self._h, name.encode(), _ptr(device_data), ctypes.byref(wc)))
-        w = QWeight(wc.encoding, wc.rows, wc.cols, device_data)
-        return w
+        return QWeight(wc.encoding, wc.rows, wc.cols, device_data, data_bytes=wc.data_bytes)

@@ -106,7 +106,12 @@ int check_weight(const dyninfer_qweight_t* w) {
             return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string(enc_name(w->encoding)) +
                                                                   ": block data must be " + std::to_string(need) +
                                                                   "-byte aligned");
-        if (w->rows * (w->cols / bw) * block_bytes(w->encoding) > 0xFFFFFFF0ull)
+        const uint64_t expect = w->rows * (w->cols / bw) * block_bytes(w->encoding);
+        if (w->data_bytes != expect)
+            return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
+                        std::string(enc_name(w->encoding)) + " requires one interleaved data component of " +
+                            std::to_string(expect) + " bytes, got " + std::to_string(w->data_bytes) + " bytes");
+        if (expect > 0xFFFFFFF0ull)
             return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, std::string(enc_name(w->encoding)) +
                                                              ": one weight tensor is limited to 4 GiB (32-bit offsets)");
         if (!dmx::gemv_k_supported(w->encoding, (uint32_t)w->cols))
@@ -131,7 +136,14 @@ int check_weight(const dyninfer_qweight_t* w) {
     }
     if (!aligned(w->data, 4) || !aligned(w->scales, es) || !aligned(w->biases, es))
         return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "mlx.affine.u4: component pointers are misaligned");
-    if (w->rows * w->cols / 2 > 0xFFFFFFF0ull || w->rows * (w->cols / w->group_size) * es > 0xFFFFFFF0ull)
+    const uint64_t packed = w->rows * w->cols / 2, grouped = w->rows * (w->cols / w->group_size) * es;
+    if (w->data_bytes != packed || w->scales_bytes != grouped || w->biases_bytes != grouped)
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
+                    "mlx.affine.u4: MLX component byte length is invalid (packed " + std::to_string(packed) +
+                        ", scales/biases " + std::to_string(grouped) + " bytes expected; got " +
+                        std::to_string(w->data_bytes) + ", " + std::to_string(w->scales_bytes) + ", " +
+                        std::to_string(w->biases_bytes) + ")");
+    if (packed > 0xFFFFFFF0ull || grouped > 0xFFFFFFF0ull)
         return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "mlx.affine.u4: one weight tensor is limited to 4 GiB (32-bit offsets)");
     if (!dmx::gemv_k_supported(w->encoding, (uint32_t)w->cols))
         return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "mlx.affine.u4: logical axis 1 (" + std::to_string(w->cols) +
@@ -139,21 +151,15 @@ int check_weight(const dyninfer_qweight_t* w) {
     return 0;
 }
 
-// Activation/output dtype rules.  GGUF weights take f32 activations (the
-// reference's all-f32 contract for quantized linears,
-// crates/dyninfer-compiler/src/lib.rs:289-306); Q4_0 additionally takes bf16
-// activations on its MFMA path.  MLX U4 takes f32 or bf16.
-int check_io(uint32_t enc, uint32_t count, uint32_t x_dtype, uint32_t y_dtype, uint32_t rows) {
+// Activation/output dtype rules: f32 (the reference's all-f32 contract for
+// quantized linears, crates/dyninfer-compiler/src/lib.rs:289-306) or bf16
+// activations for every encoding, f32 or bf16 outputs.
+int check_io(uint32_t x_dtype, uint32_t y_dtype, uint32_t rows) {
     if (rows == 0) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "rows must be >= 1");
     if (x_dtype != DYNINFER_DTYPE_F32 && x_dtype != DYNINFER_DTYPE_BF16)
         return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "activations must be f32 or bf16");
     if (y_dtype != DYNINFER_DTYPE_F32 && y_dtype != DYNINFER_DTYPE_BF16)
         return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "outputs must be f32 or bf16");
-    if (x_dtype == DYNINFER_DTYPE_BF16 && enc != DYNINFER_ENC_MLX_AFFINE_U4 &&
-        !(enc == DYNINFER_ENC_GGUF_Q4_0 && count == 1))
-        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
-                    std::string(enc_name(enc)) + ": bf16 activations are supported for single gguf.q4_0 weights "
-                                                 "(MFMA path) and mlx.affine.u4 only; pass f32 activations");
     return 0;
 }
 
@@ -173,6 +179,35 @@ dmx::GemvProblem problem_of(const dyninfer_qweight_t* w, void* y) {
 }
 
 size_t esize(uint32_t dt) { return dt == DYNINFER_DTYPE_F32 ? 4 : 2; }
+
+// Whether rows >= 17 of this encoding run the prefill GEMM (else GEMV chunks).
+bool has_prefill_gemm(uint32_t enc, uint32_t N, uint32_t K, uint32_t rows) {
+    return enc == DYNINFER_ENC_GGUF_Q4_0 && dmx::gemm_q4_0_supported(N, K, rows);
+}
+
+// Device memory of one prefill call: transient (hipMallocAsync on the stream,
+// released with hipFreeAsync after the launches that use it).
+struct Workspace {
+    uint8_t* p = nullptr;
+    hipStream_t st = nullptr;
+    bool owned = false;
+    ~Workspace() {
+        if (owned) (void)hipFreeAsync(p, st);
+    }
+};
+
+// The prefill path: x staged once (xprep), then one GEMM per weight.
+hipError_t prefill(const dyninfer_qweight_t* ws, uint32_t count, const void* x, uint32_t x_dtype, uint32_t rows,
+                   void* const* ys, uint32_t y_dtype, uint8_t* work, hipStream_t st) {
+    const uint32_t K = (uint32_t)ws[0].cols;
+    uint16_t* xh = reinterpret_cast<uint16_t*>(work);
+    float* rs = reinterpret_cast<float*>(work + dmx::prefill_xh_bytes(rows, K));
+    hipError_t e = dmx::xprep_launch(x, x_dtype == DYNINFER_DTYPE_BF16, rows, K, dmx::XPERM_PAIR2, xh, rs, st);
+    for (uint32_t i = 0; i < count && e == hipSuccess; i++)
+        e = dmx::gemm_q4_0_launch(static_cast<const uint8_t*>(ws[i].data), (uint32_t)ws[i].rows, K, xh, rs, rows,
+                                  ys[i], y_dtype == DYNINFER_DTYPE_BF16, st);
+    return e;
+}
 
 // Runs rows > 16 through the GEMV kernels 16 activation rows at a time.
 hipError_t gemv_rows(const dyninfer_qweight_t* ws, uint32_t count, const void* x, uint32_t x_dtype, uint32_t rows,
@@ -224,7 +259,7 @@ int dyninfer_mi355x_close(dyninfer_mi355x_ctx_t* ctx) {
 }
 
 int dyninfer_mi355x_supports(const dyninfer_qweight_t* w, uint32_t rows, uint32_t x_dtype, uint32_t y_dtype) {
-    if (check_weight(w) || check_io(w->encoding, 1, x_dtype, y_dtype, rows)) return 0;
+    if (check_weight(w) || check_io(x_dtype, y_dtype, rows)) return 0;
     return 1;
 }
 
@@ -245,16 +280,24 @@ int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qwe
             return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT,
                         "grouped weights must share encoding, K, group size and scale dtype");
     }
-    if (int rc = check_io(ws[0].encoding, count, x_dtype, y_dtype, rows)) return rc;
+    if (int rc = check_io(x_dtype, y_dtype, rows)) return rc;
     if (!aligned(x, 16)) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "activations must be 16-byte aligned");
+    bool gemm = rows > (uint32_t)dmx::kMaxGemvBatch;
+    for (uint32_t i = 0; i < count && gemm; i++)
+        gemm = has_prefill_gemm(ws[i].encoding, (uint32_t)ws[i].rows, (uint32_t)ws[i].cols, rows);
+    if (gemm && (uint64_t)rows * ws[0].cols >= (1ull << 31))
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "prefill: rows * K must stay below 2^31 (32-bit activation offsets)");
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e;
-    if (ws[0].encoding == DYNINFER_ENC_GGUF_Q4_0 && x_dtype == DYNINFER_DTYPE_BF16) {
-        // Q4_0 with bf16 activations: dequant-to-LDS + f16 MFMA for any row count.
-        e = dmx::gemm_q4_0_launch(static_cast<const uint8_t*>(ws[0].data), (uint32_t)ws[0].rows,
-                                  (uint32_t)ws[0].cols, x, rows, ys[0], y_dtype == DYNINFER_DTYPE_BF16, st);
+    if (gemm) {
+        Workspace wk;
+        wk.st = st;
+        e = hipMallocAsync(reinterpret_cast<void**>(&wk.p), (size_t)dmx::prefill_workspace_bytes(rows, (uint32_t)ws[0].cols), st);
+        if (e != hipSuccess) return hip_fail(e, "hipMallocAsync (prefill staging workspace)");
+        wk.owned = true;
+        e = prefill(ws, count, x, x_dtype, rows, ys, y_dtype, wk.p, st);
     } else {
         e = gemv_rows(ws, count, x, x_dtype, rows, ys, y_dtype, st);
     }
@@ -309,8 +352,9 @@ struct dyninfer_gguf {
 
 static int gguf_finish(const uint8_t* base, uint64_t len, void* map, dyninfer_gguf_t** out) {
     auto* g = new dyninfer_gguf();
-    const std::string err = dmx::gguf_index(base, len, g->idx);
     g->idx.map = map;
+    g->idx.len = len;  // the mapping's length, so a failed index still unmaps it
+    const std::string err = dmx::gguf_index(base, len, g->idx);
     if (!err.empty()) {
         dyninfer_mi355x_gguf_close(g);
         return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "invalid GGUF: " + err);
@@ -412,6 +456,7 @@ int dyninfer_mi355x_gguf_qweight(const dyninfer_gguf_t* g, const char* name, con
     out->rows = t->shape[0];
     out->cols = t->shape[1];
     out->data = device_data;
+    out->data_bytes = t->nbytes;
     return check_weight(out);
 }
 

@@ -16,22 +16,24 @@
 //   * inside every 32-wide block, K is stored in LDS in the nibble decode order
 //     (for each 8 consecutive k from k0: k0, k0+2, k0+1, k0+3, k0+4, k0+6,
 //     k0+5, k0+7), for X and W alike, so the products pair up exactly as in
-//     natural order, an X load of 8 bf16 fills one such group, and one
+//     natural order, an X load of 8 staged f16 fills one such group, and one
 //     v_and_or_b32 decodes two weights (bytes j and j+2 of a dword): a low nibble under the f16
 //     exponent of 1024 is 1024+q, a high nibble (bits 4..7) under the exponent
 //     of 64 is 64+q, both exact; a packed f16 add gives q-8 (exact) and a packed
 //     f16 multiply RNE_f16((q-8)·d), a single rounding of the exact weight
 //     (relative error <= 2^-11);
-//   * X: bf16 is narrowed to f16 with v_cvt_pkrtz (exact for |x| in f16's
-//     normal range: bf16 carries 8 significant bits, f16 11), placed in the
-//     same permuted order;
+//   * X arrives as f16 from the prefill staging kernel (xprep.hip): each row
+//     scaled by a power of two so that its largest magnitude is below 2^15,
+//     rounded once (RNE), already in the permuted k order; the tile loads it
+//     into LDS unchanged and the epilogue multiplies row m by rs[m];
 //   * K advances BK per stage; the global loads run PF stages ahead in a
 //     register ring; LDS is double buffered (rows padded by 16 bytes), one
 //     barrier per stage;
 //   * tiles are ordered so that the tiles sharing W columns run on the same
 //     XCD (workgroup i goes to XCD i % 8), reading each W block into one L2.
-// Accuracy: |y - y_exact| <= 2^-11·Σ|w||x| + f32 accumulation error, inside
-// the 2e-3 normalised tolerance.
+// Accuracy: |y - y_exact| <= 2^-10·Σ|w||x| (one f16 rounding of each weight and
+// of each activation) + f32 accumulation error, inside the 2e-3 normalised
+// tolerance.
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -40,6 +42,7 @@ namespace dmx {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -51,17 +54,11 @@ __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t b) {
     return r;
 }
 
-// Two f32 bit patterns (bf16 values) to packed f16, rounding toward zero
-// (exact for bf16 values in f16's normal range).
-__device__ __forceinline__ uint32_t pk_f16(uint32_t lo, uint32_t hi) {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(lo), __uint_as_float(hi)));
-}
-
 // Global loads and decode of one tile's X and W stages, spread over NT threads.
 //
 // LDS order inside each 32-wide block: group g (g = 0..3) holds k = 8g..8g+7 as
 // the pairs (k0, k0+2), (k0+1, k0+3), (k0+4, k0+6), (k0+5, k0+7), k0 = 8g.
-//   X unit: one row's 8 consecutive bf16 (one 16-byte load) -> one group.
+//   X unit: one row's 8 staged f16 of one group (one 16-byte load), copied.
 //   W unit: half h of one row's block (the whole 18-byte block is loaded, two
 //           loads): quant dwords 2h, 2h+1 hold the low nibbles of k = 8h..8h+7
 //           (group h) and the high nibbles of k = 16+8h.. (group h+2); byte j of
@@ -73,9 +70,9 @@ struct Producer {
     static constexpr int WU = BN * 2 * NB / NT;  // W units per thread per stage
     static_assert(XU >= 1 && WU >= 1 && XU * NT == BM * 4 * NB && WU * NT == BN * 2 * NB, "unit split");
     static constexpr int kLoads = XU + 2 * WU;        // global load instructions per stage
-    static constexpr int kValu = 10 * XU + 32 * WU;    // decode VALU instructions per stage (approximate)
+    static constexpr int kValu = 32 * WU;              // decode VALU instructions per stage (approximate)
 
-    uint32_t xraw[PF][XU][4];  // 8 bf16 at k = 8g..8g+7
+    uint32_t xraw[PF][XU][4];  // the 8 staged f16 of group g
     uint32_t wraw[PF][WU][5];  // the block's dwords from the aligned dword holding its first byte
     const uint16_t* xrow[XU];
     const uint32_t* wrow[WU];
@@ -158,18 +155,8 @@ struct Producer {
         for (int i = 0; i < XU; i++) {
             uint32_t r, g8;
             xunit(i, r, g8);
-            // bf16 pairs (k0, k0+1), (k0+2, k0+3), ...  The high bf16 of a
-            // dword is only its f32 value once the low half is cleared: f32
-            // mantissa bits 13..15 (the low bf16's sign and top exponent bits)
-            // lie inside f16's 10-bit mantissa, so round-toward-zero would keep
-            // them.
             const uint32_t* q = xraw[slot][i];
-            constexpr uint32_t kHi = 0xFFFF0000u;
-            const uint32_t p0 = pk_f16(q[0] << 16, q[1] << 16);  // k0, k0+2
-            const uint32_t p1 = pk_f16(q[0] & kHi, q[1] & kHi);  // k0+1, k0+3
-            const uint32_t p2 = pk_f16(q[2] << 16, q[3] << 16);  // k0+4, k0+6
-            const uint32_t p3 = pk_f16(q[2] & kHi, q[3] & kHi);  // k0+5, k0+7
-            *reinterpret_cast<uint4*>(&dx[r * PITCH + 8u * g8]) = make_uint4(p0, p1, p2, p3);
+            *reinterpret_cast<uint4*>(&dx[r * PITCH + 8u * g8]) = make_uint4(q[0], q[1], q[2], q[3]);
         }
         const h2 off_lo = {(_Float16)-1032.0f, (_Float16)-1032.0f};
         const h2 off_hi = {(_Float16)-72.0f, (_Float16)-72.0f};
@@ -258,11 +245,19 @@ struct Consumer {
     static constexpr int kMfmas = 2 * NB * TM * TN;
 
     // D layout of 32x32 MFMA: lane holds column lane%32 and, for r = 0..15,
-    // row 8·(r/4) + 4·(lane/32) + r%4.
-    __device__ __forceinline__ void store(void* Y, uint32_t m0, uint32_t n0, uint32_t M, uint32_t N, uint32_t y_bf16) {
+    // row 8·(r/4) + 4·(lane/32) + r%4.  Row m's sums are multiplied by its
+    // staging factor rs[m] (rs covers the rows of every tile, past M too).
+    __device__ __forceinline__ void store(void* Y, const float* rs, uint32_t m0, uint32_t n0, uint32_t M, uint32_t N,
+                                          uint32_t y_bf16) {
         const uint32_t col_l = lane & 31u, row_l = (lane >> 5) * 4u;
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+        for (int i = 0; i < TM; i++) {
+            float f[16];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const f32x4 v = *gptr<f32x4>(rs + m0 + arow + i * 32u + 8u * q + row_l);
+                f[4 * q] = v[0]; f[4 * q + 1] = v[1]; f[4 * q + 2] = v[2]; f[4 * q + 3] = v[3];
+            }
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const uint32_t col = n0 + bcol + j * 32u + col_l;
@@ -271,11 +266,13 @@ struct Consumer {
                     const uint32_t row = m0 + arow + i * 32u + 8u * (r >> 2) + row_l + (r & 3);
                     if (row < M && col < N) {
                         const size_t idx = (size_t)row * N + col;
-                        if (y_bf16) gptr_mut<uint16_t>(Y)[idx] = f32_to_bf16_bits(acc[i][j][r]);
-                        else gptr_mut<float>(Y)[idx] = acc[i][j][r];
+                        const float v = acc[i][j][r] * f[r];
+                        if (y_bf16) gptr_mut<uint16_t>(Y)[idx] = f32_to_bf16_bits(v);
+                        else gptr_mut<float>(Y)[idx] = v;
                     }
                 }
             }
+        }
     }
 };
 
@@ -287,6 +284,7 @@ struct Consumer {
 template <int BM, int BN, int WM, int WN, int PW, int BK, int PF>
 __global__ __launch_bounds__((WM * WN + PW) * 64) void gemm_q4_0_kernel(const uint8_t* __restrict__ W,
                                                                          const uint16_t* __restrict__ X,
+                                                                         const float* __restrict__ rs,
                                                                          void* __restrict__ Y, uint32_t M, uint32_t N,
                                                                          uint32_t K, uint32_t y_bf16) {
     constexpr int NB = BK / 32;
@@ -354,7 +352,7 @@ __global__ __launch_bounds__((WM * WN + PW) * 64) void gemm_q4_0_kernel(const ui
 #pragma unroll
         for (int slot = 0; slot < PF; slot++)
             if (s0 + (uint32_t)slot < nst) iter(slot, s0 + (uint32_t)slot);
-        c.store(Y, m0, n0, M, N, y_bf16);
+        c.store(Y, rs, m0, n0, M, N, y_bf16);
     } else {
         // PW producer waves load and decode stage s + 1 while the MMA waves
         // multiply stage s; one barrier per stage (wave-uniform split: every
@@ -389,7 +387,7 @@ __global__ __launch_bounds__((WM * WN + PW) * 64) void gemm_q4_0_kernel(const ui
                 c.mma(f);
                 __syncthreads();
             }
-            c.store(Y, m0, n0, M, N, y_bf16);
+            c.store(Y, rs, m0, n0, M, N, y_bf16);
         }
     }
 }
@@ -401,8 +399,8 @@ bool gemm_q4_0_supported(uint32_t N, uint32_t K, uint32_t M) {
 namespace {
 
 template <int BM, int BN, int WM, int WN, int PW, int BK, int PF>
-hipError_t launch_tile(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* x, uint32_t M, void* y, uint32_t yb,
-                       hipStream_t st) {
+hipError_t launch_tile(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* x, const float* rs, uint32_t M,
+                       void* y, uint32_t yb, hipStream_t st) {
     auto kernel = gemm_q4_0_kernel<BM, BN, WM, WN, PW, BK, PF>;
     constexpr int kThreads = (WM * WN + PW) * 64;
     constexpr size_t lds = (size_t)2 * (BM + BN) * (BK + 8) * sizeof(_Float16);
@@ -412,16 +410,15 @@ hipError_t launch_tile(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t*
         if (attr != hipSuccess) return attr;
     }
     const uint32_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    hipLaunchKernelGGL(kernel, dim3(tiles), dim3(kThreads), lds, st, w, x, y, M, N, K, yb);
+    hipLaunchKernelGGL(kernel, dim3(tiles), dim3(kThreads), lds, st, w, x, rs, y, M, N, K, yb);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t gemm_q4_0_launch(const uint8_t* w, uint32_t N, uint32_t K, const void* x, uint32_t M, void* y,
-                            bool y_bf16, hipStream_t stream) {
+hipError_t gemm_q4_0_launch(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* xp, const float* rs, uint32_t M,
+                            void* y, bool y_bf16, hipStream_t stream) {
     if (!gemm_q4_0_supported(N, K, M)) return hipErrorInvalidValue;
-    const auto* xp = static_cast<const uint16_t*>(x);
     const uint32_t yb = y_bf16 ? 1u : 0u;
     auto tiles = [&](uint32_t bm, uint32_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     // The largest tile (most reuse of each decoded weight and converted
@@ -433,10 +430,10 @@ hipError_t gemm_q4_0_launch(const uint8_t* w, uint32_t N, uint32_t K, const void
     // for K = 3072 the K-split kernel takes 40-60% less time, at M = 512 with
     // 192 tiles of 128x64 5% more.)
     constexpr uint32_t kCus = 256;
-    if (tiles(128, 128) >= kCus) return launch_tile<128, 128, 2, 4, 8, 64, 2>(w, N, K, xp, M, y, yb, stream);
-    if (tiles(128, 64) >= kCus * 3 / 4) return launch_tile<128, 64, 4, 2, 0, 128, 2>(w, N, K, xp, M, y, yb, stream);
-    if (gemm_q4_0_ks_supported(N, K, M)) return gemm_q4_0_ks_launch(w, N, K, x, M, y, y_bf16, stream);
-    return launch_tile<64, 64, 2, 2, 0, 128, 2>(w, N, K, xp, M, y, yb, stream);
+    if (tiles(128, 128) >= kCus) return launch_tile<128, 128, 2, 4, 8, 64, 2>(w, N, K, xp, rs, M, y, yb, stream);
+    if (tiles(128, 64) >= kCus * 3 / 4) return launch_tile<128, 64, 4, 2, 0, 128, 2>(w, N, K, xp, rs, M, y, yb, stream);
+    if (gemm_q4_0_ks_supported(N, K, M)) return gemm_q4_0_ks_launch(w, N, K, xp, rs, M, y, y_bf16, stream);
+    return launch_tile<64, 64, 2, 2, 0, 128, 2>(w, N, K, xp, rs, M, y, yb, stream);
 }
 
 }  // namespace dmx

@@ -1,7 +1,9 @@
 // Prefill GEMM, GGUF Q4_0, K split over the waves of a workgroup:
-// Y[M, N] = X[M, K] · Wᵀ with X bf16 row-major, W Q4_0 blocks (N rows of K/32
-// blocks), f32 accumulation (gguf_codegen.rs:268-314 `emit_linear`, the Q4_0
-// dequantisation of :412-472).
+// Y[M, N] = X[M, K] · Wᵀ with W Q4_0 blocks (N rows of K/32 blocks), f32
+// accumulation (gguf_codegen.rs:268-314 `emit_linear`, the Q4_0 dequantisation
+// of :412-472).  X arrives staged by xprep.hip: f16 rows scaled by a power of
+// two (factor rs[m] applied in the epilogue), k permuted as 0,2,1,3,4,6,5,7
+// inside every group of 8.
 //
 // A workgroup owns one BM×BN tile of Y and splits K into four quarters, one
 // per wave, so each wave is an independent pipeline with no barrier until the
@@ -17,8 +19,8 @@
 //     from window bytes 0, 16, 20 + 2·sh (each touching only dwords that hold
 //     bytes of the chunk, so no load leaves a page the chunk touches);
 //   * each lane reads its v_mfma_f32_16x16x32_f16 operands from LDS: an X
-//     fragment (8 k of one row) narrowed from bf16 to f16 with k reordered as
-//     0,2,1,3,4,6,5,7 (the order one v_and_or_b32 decodes nibbles in), a W
+//     fragment (8 staged f16 of one row, in the order one v_and_or_b32
+//     decodes nibbles in: 0,2,1,3,4,6,5,7) used as it is, a W
 //     fragment 8 weights of one row from 8 qs bytes (low nibbles under the f16
 //     exponent of 1024, high nibbles under that of 64, a packed add giving q-8
 //     exactly, a packed multiply by d: RNE_f16((q-8)·d), a weight's one
@@ -26,9 +28,10 @@
 //   * one block's operands are decoded while the previous block's MFMAs run
 //     (scheduling-group barriers interleave them);
 //   * the four K-partials meet in LDS: each wave owns every fourth 16×16 tile,
-//     the others hand it theirs, the owner adds and stores.
-// Error: 2^-11·Σ|w||x| (f16 weights; bf16 activations are exact in f16's
-// normal range) plus f32 accumulation.
+//     the others hand it theirs, the owner adds, scales row m by rs[m] and
+//     stores.
+// Error: 2^-10·Σ|w||x| (one f16 rounding of each weight and of each staged
+// activation) plus f32 accumulation.
 #include <type_traits>
 
 #include "encodings.hpp"
@@ -47,12 +50,6 @@ constexpr int kKsWaves = 4;      // K quarters, one per wave
 constexpr uint32_t kKsKC = 64;   // k per chunk: two Q4_0 blocks
 constexpr uint32_t kKsBufs = 3;  // LDS chunk buffers per wave
 constexpr uint32_t kWPitch = 48; // LDS bytes per W row window: three 16-byte pieces
-
-// Two f32 bit patterns holding bf16 values to packed f16, rounding toward zero
-// (exact for bf16 values in f16's normal range; the low 16 bits must be zero).
-__device__ __forceinline__ uint32_t pk_f16(uint32_t lo, uint32_t hi) {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(lo), __uint_as_float(hi)));
-}
 
 // (a & m) | b, every operand a vector register (m and b differ between lanes)
 __device__ __forceinline__ uint32_t and_or_v(uint32_t a, uint32_t m, uint32_t b) {
@@ -93,7 +90,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 template <int BM, int BN, int BSH>
 __global__ __launch_bounds__(kKsWaves * 64) void gemm_q4_0_ks_kernel(const uint8_t* __restrict__ w,
-                                                                       const uint16_t* __restrict__ x, void* y,
+                                                                       const uint16_t* __restrict__ x,
+                                                                       const float* __restrict__ rs, void* y,
                                                                        uint32_t M, uint32_t N, uint32_t K,
                                                                        uint32_t y_bf16) {
     using T = Ks<BM, BN>;
@@ -167,8 +165,8 @@ __global__ __launch_bounds__(kKsWaves * 64) void gemm_q4_0_ks_kernel(const uint8
         for (int i = 0; i < NWL; i++) dma16(wb + wg[i], d + T::XB + 1024u * (uint32_t)i);
     };
     // One 32-k step (one block of each W row) in two stages: fetch() reads
-    // the LDS words (raw X pieces, the W qs dwords and d), decode() narrows X
-    // and decodes W into the MFMA operands.
+    // the LDS words (X pieces, the W qs dwords and d), decode() decodes W into
+    // the MFMA operands (the X pieces are operands as they are).
     struct Raw {
         u32x4 x[TM];
         uint32_t q[TN][3], d[TN];
@@ -192,15 +190,10 @@ __global__ __launch_bounds__(kKsWaves * 64) void gemm_q4_0_ks_kernel(const uint8
     };
     auto decode = [&](auto step, const Raw& r, Frags& f) {
         constexpr uint32_t s = decltype(step)::value;
-        constexpr uint32_t kHi = 0xFFFF0000u;
         constexpr uint32_t dob = BSH + 18u * s;
         constexpr uint32_t sel = 0x03020100u + 0x01010101u * ((dob + 2u) & 3u);  // realigns the qs dwords
 #pragma unroll
-        for (int mg = 0; mg < TM; mg++) {
-            const u32x4 q = r.x[mg];
-            f.a[mg] = u32x4{pk_f16(q[0] << 16, q[1] << 16), pk_f16(q[0] & kHi, q[1] & kHi),   // k0,k2  k1,k3
-                            pk_f16(q[2] << 16, q[3] << 16), pk_f16(q[2] & kHi, q[3] & kHi)};  // k4,k6  k5,k7
-        }
+        for (int mg = 0; mg < TM; mg++) f.a[mg] = r.x[mg];  // k0,k2 k1,k3 k4,k6 k5,k7
 #pragma unroll
         for (int g = 0; g < TN; g++) {
             const h2 d2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(r.d[g], r.d[g], (dob & 3u) ? 0x07060706u : 0x05040504u));
@@ -226,7 +219,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void gemm_q4_0_ks_kernel(const uint8
                                                                     __builtin_bit_cast(h8, f.b[g]), acc[mg][g], 0, 0, 0);
     };
     constexpr int kMfmas = TM * TN;
-    constexpr int kValu = 12 * TM + 17 * TN;  // one step's narrowing and decode
+    constexpr int kValu = 17 * TN;            // one step's decode
     constexpr int kReads = TM + 4 * TN;       // one step's LDS reads
     auto interleave = [&]() {
 #pragma unroll
@@ -303,13 +296,17 @@ __global__ __launch_bounds__(kKsWaves * 64) void gemm_q4_0_ks_kernel(const uint8
                 if (o != wv) v += red[(o * (uint32_t)(TM * TN) + t) * 64u + lane];
             // lane l holds rows 4(l/16)..+3 of column l % 16
             const uint32_t n = n0 + 16u * (uint32_t)g + (lane & 15u);
+            const uint32_t mb = m0 + 16u * (uint32_t)mg + 4u * (lane >> 4);
+            const f32x4 f = *gptr<f32x4>(rs + mb);  // rs covers whole row groups past M
+            const float fr[4] = {f[0], f[1], f[2], f[3]};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const uint32_t m = m0 + 16u * (uint32_t)mg + 4u * (lane >> 4) + (uint32_t)e;
+                const uint32_t m = mb + (uint32_t)e;
                 if (m < M && n < N) {
                     const size_t idx = (size_t)m * N + n;
-                    if (y_bf16) gptr_mut<uint16_t>(y)[idx] = f32_to_bf16_bits(v[e]);
-                    else gptr_mut<float>(y)[idx] = v[e];
+                    const float o = v[e] * fr[e];
+                    if (y_bf16) gptr_mut<uint16_t>(y)[idx] = f32_to_bf16_bits(o);
+                    else gptr_mut<float>(y)[idx] = o;
                 }
             }
         }
@@ -318,8 +315,8 @@ __global__ __launch_bounds__(kKsWaves * 64) void gemm_q4_0_ks_kernel(const uint8
 namespace {
 
 template <int BM, int BN>
-hipError_t launch_ks(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* x, uint32_t M, void* y, uint32_t yb,
-                     hipStream_t st) {
+hipError_t launch_ks(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* x, const float* rs, uint32_t M, void* y,
+                     uint32_t yb, hipStream_t st) {
     auto kernel = ((uintptr_t)w & 3u) ? gemm_q4_0_ks_kernel<BM, BN, 2> : gemm_q4_0_ks_kernel<BM, BN, 0>;
     constexpr size_t lds = Ks<BM, BN>::LDS;
     if constexpr (lds > 64u * 1024u) {
@@ -331,7 +328,7 @@ hipError_t launch_ks(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* x
         if (attr2 != hipSuccess) return attr2;
     }
     const uint32_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    hipLaunchKernelGGL(kernel, dim3(tiles), dim3(kKsWaves * 64), lds, st, w, x, y, M, N, K, yb);
+    hipLaunchKernelGGL(kernel, dim3(tiles), dim3(kKsWaves * 64), lds, st, w, x, rs, y, M, N, K, yb);
     return hipGetLastError();
 }
 
@@ -342,17 +339,16 @@ bool gemm_q4_0_ks_supported(uint32_t N, uint32_t K, uint32_t M) {
     return N > 0 && M > 0 && K > 0 && K % (kKsWaves * kKsKC) == 0 && (uint64_t)M * K < (1ull << 31);
 }
 
-hipError_t gemm_q4_0_ks_launch(const uint8_t* w, uint32_t N, uint32_t K, const void* x, uint32_t M, void* y,
-                               bool y_bf16, hipStream_t stream) {
+hipError_t gemm_q4_0_ks_launch(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* xp, const float* rs,
+                               uint32_t M, void* y, bool y_bf16, hipStream_t stream) {
     if (!gemm_q4_0_ks_supported(N, K, M)) return hipErrorInvalidValue;
-    const auto* xp = static_cast<const uint16_t*>(x);
     const uint32_t yb = y_bf16 ? 1u : 0u;
     auto tiles = [&](uint32_t bm, uint32_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     constexpr uint32_t kCus = 256;
-    if (tiles(64, 96) >= kCus) return launch_ks<64, 96>(w, N, K, xp, M, y, yb, stream);
-    if (tiles(64, 64) >= kCus) return launch_ks<64, 64>(w, N, K, xp, M, y, yb, stream);
-    if (tiles(32, 64) >= kCus) return launch_ks<32, 64>(w, N, K, xp, M, y, yb, stream);
-    return launch_ks<32, 32>(w, N, K, xp, M, y, yb, stream);
+    if (tiles(64, 96) >= kCus) return launch_ks<64, 96>(w, N, K, xp, rs, M, y, yb, stream);
+    if (tiles(64, 64) >= kCus) return launch_ks<64, 64>(w, N, K, xp, rs, M, y, yb, stream);
+    if (tiles(32, 64) >= kCus) return launch_ks<32, 64>(w, N, K, xp, rs, M, y, yb, stream);
+    return launch_ks<32, 32>(w, N, K, xp, rs, M, y, yb, stream);
 }
 
 }  // namespace dmx

@@ -857,19 +857,17 @@ hipError_t launch_oneshot(KERNEL k512, KERNEL k256, GemvParams p, size_t lds, hi
 // register batch B (the host has checked that its activation tile fits LDS);
 // oneshot = chunks per lane selects the latency-mode kernel, 0 the
 // persistent pipeline.  The row-block layout is set here, per tile.
-// GGUF decode takes f32 activations, the reference's precision contract for
-// quantized linears (crates/dyninfer-compiler/src/lib.rs:289-306); bf16
-// activations reach GGUF weights only through the Q4_0 MFMA path.
-template <class E>
-hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st) {
-    if (xbf16) return hipErrorInvalidValue;
+// Activations are f32 (the reference's precision contract for quantized
+// linears, crates/dyninfer-compiler/src/lib.rs:289-306) or bf16 (XBF16).
+template <class E, bool XBF16>
+hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot, hipStream_t st) {
     const size_t lds = (size_t)xtile_bytes(E::ENC, B, p.K);
     if (oneshot) {
         // chunks per lane (the host's limits): 1..4 for one activation row
         // (Q6_K 1..2), 1..2 for 2 rows, 1 for 4
 #define DMX_ONESHOT(b, c)                                                                             \
     if (B == b && oneshot == c)                                                                       \
-        return launch_oneshot(gguf_gemv_oneshot_kernel<E, c, b, false, 512>, gguf_gemv_oneshot_kernel<E, c, b, false, 256>, \
+        return launch_oneshot(gguf_gemv_oneshot_kernel<E, c, b, XBF16, 512>, gguf_gemv_oneshot_kernel<E, c, b, XBF16, 256>, \
                               p, lds, st);
         DMX_ONESHOT(1, 1)
         DMX_ONESHOT(1, 2)
@@ -900,12 +898,12 @@ hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t oneshot, b
 #define DMX_CASE(b)                                                                                            \
     case b:                                                                                                    \
         if constexpr (b <= max_register_batch(E::ENC))                                                         \
-            n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, b, decltype(r)::value, false>; }); \
+            n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, b, decltype(r)::value, XBF16>; }); \
         break;
     switch (B) {
     case 1:
-        n = big ? gemv_tiles<E, 1>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, 1, decltype(r)::value, false, 1024>; }, 1024u)
-                : gemv_tiles<E, 1>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, 1, decltype(r)::value, false>; });
+        n = big ? gemv_tiles<E, 1>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, 1, decltype(r)::value, XBF16, 1024>; }, 1024u)
+                : gemv_tiles<E, 1>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, 1, decltype(r)::value, XBF16>; });
         break;
         DMX_CASE(2)
         DMX_CASE(4)
@@ -915,6 +913,11 @@ hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t oneshot, b
 #undef DMX_CASE
     if (n == 0) return hipErrorInvalidValue;
     return launch_persistent_best(t, n, p, lds, (nch + (1u << p.lanes_log2) - 1u) >> p.lanes_log2, st);
+}
+
+template <class E>
+hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st) {
+    return xbf16 ? launch_gguf_gemv_x<E, true>(p, B, oneshot, st) : launch_gguf_gemv_x<E, false>(p, B, oneshot, st);
 }
 
 }  // namespace dmx

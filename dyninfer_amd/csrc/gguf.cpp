@@ -21,6 +21,30 @@ namespace {
 constexpr uint64_t kMaxHeaderBytes = 64ull << 20, kMaxTensors = 1000000, kMaxEntries = 1000000;
 constexpr uint64_t kMaxKeyLen = 16 * 1024, kMaxRank = 16, kMaxDim = 1ull << 40;
 
+// Well-formed UTF-8 (RFC 3629: no overlong forms, no surrogates, at most
+// U+10FFFF), the check Rust's String::from_utf8 makes (container.rs:62-81).
+bool valid_utf8(const uint8_t* s, uint64_t n) {
+    uint64_t i = 0;
+    while (i < n) {
+        const uint8_t c = s[i];
+        if (c < 0x80) { i++; continue; }
+        uint32_t len, cp;
+        if (c >= 0xC2 && c <= 0xDF) { len = 2; cp = c & 0x1Fu; }
+        else if (c >= 0xE0 && c <= 0xEF) { len = 3; cp = c & 0x0Fu; }
+        else if (c >= 0xF0 && c <= 0xF4) { len = 4; cp = c & 0x07u; }
+        else return false;
+        if (n - i < len) return false;
+        for (uint32_t k = 1; k < len; k++) {
+            if ((s[i + k] & 0xC0u) != 0x80u) return false;
+            cp = (cp << 6) | (s[i + k] & 0x3Fu);
+        }
+        if ((len == 3 && (cp < 0x800 || (cp >= 0xD800 && cp <= 0xDFFF))) || (len == 4 && (cp < 0x10000 || cp > 0x10FFFF)))
+            return false;
+        i += len;
+    }
+    return true;
+}
+
 struct Cursor {
     const uint8_t* p;
     uint64_t len, pos = 0;
@@ -42,6 +66,7 @@ struct Cursor {
         if (!err.empty()) return {};
         if (n > kMaxKeyLen) { err = "GGUF string length " + std::to_string(n) + " exceeds limit"; return {}; }
         if (!need(n)) return {};
+        if (!valid_utf8(p + pos, n)) { err = "GGUF string is not UTF-8"; return {}; }
         std::string s(reinterpret_cast<const char*>(p + pos), (size_t)n);
         pos += n;
         return s;
@@ -158,7 +183,15 @@ std::string gguf_index(const uint8_t* base, uint64_t len, GgufIndex& idx) {
             if (dim > kMaxDim) return "dimension " + std::to_string(dim) + " exceeds limit (" + d.name + ")";
         dirs.push_back(std::move(d));
     }
-    const uint64_t data = alignment ? (c.pos + alignment - 1) / alignment * alignment : c.pos;
+    // align_up as the reference computes it (div_ceil, then the multiple):
+    // the quotient is at least 1, so the multiple overflows only for an
+    // alignment beyond any file length, which is then reported as such
+    uint64_t data = c.pos;
+    if (alignment) {
+        const uint64_t q = c.pos / alignment + (c.pos % alignment ? 1u : 0u);
+        if (q > UINT64_MAX / alignment) return "GGUF data section offset overflows (general.alignment " + std::to_string(alignment) + ")";
+        data = q * alignment;
+    }
     idx.tensors.clear();
     for (Dir& d : dirs) {
         uint64_t block = 0, bytes = 0, numel = 1;

@@ -92,9 +92,27 @@ hipError_t gather_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, cons
                          uint32_t K, uint32_t group, uint32_t sdtype, const int64_t* ids, uint32_t n_ids, float* out,
                          hipStream_t stream);
 
-// Q4_0 prefill GEMM on MFMA: Y[M, N] = X[M, K] · Wᵀ, X bf16, Y f32 or bf16.
-hipError_t gemm_q4_0_launch(const uint8_t* w, uint32_t N, uint32_t K, const void* x, uint32_t M,
-                            void* y, bool y_bf16, hipStream_t stream);
+// Prefill activations as the GEMMs read them (xprep.hip): xh [M, K] f16 =
+// RNE(x · 2^(15 - e_m)) with k permuted inside every group of 8, and the row
+// factors rs[m] = 2^(e_m - 15) the GEMM epilogues multiply by.
+enum XPerm : uint32_t {
+    XPERM_PAIR2 = 0,  // 0,2,1,3,4,6,5,7: GGUF codes (bytes j and j+2 of a dword decode together)
+    XPERM_PAIR4 = 1,  // 0,4,1,5,2,6,3,7: MLX U4 (nibbles i and i+4 of a word)
+};
+hipError_t xprep_launch(const void* x, bool x_bf16, uint32_t M, uint32_t K, uint32_t perm, uint16_t* xh, float* rs,
+                        hipStream_t stream);
+
+// Device workspace of one prefill GEMM call: xh (M·K f16) then rs (f32 for M
+// rows rounded up to 256, so epilogues may read whole row groups past M).
+inline uint64_t prefill_xh_bytes(uint32_t M, uint32_t K) { return ((uint64_t)M * K * 2u + 255u) & ~(uint64_t)255u; }
+inline uint64_t prefill_workspace_bytes(uint32_t M, uint32_t K) {
+    return prefill_xh_bytes(M, K) + (((uint64_t)M + 255u) & ~(uint64_t)255u) * 4u;
+}
+
+// Q4_0 prefill GEMM on MFMA: Y[M, N] = diag(rs) · (Xh[M, K] · Wᵀ), Xh/rs from
+// xprep_launch(XPERM_PAIR2); Y f32 or bf16.
+hipError_t gemm_q4_0_launch(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs,
+                            uint32_t M, void* y, bool y_bf16, hipStream_t stream);
 
 // Shape limits of the GEMM kernel (checked by the C ABI before launching).
 bool gemm_q4_0_supported(uint32_t N, uint32_t K, uint32_t M);
@@ -102,7 +120,7 @@ bool gemm_q4_0_supported(uint32_t N, uint32_t K, uint32_t M);
 // The K-split GEMM (K a multiple of 256): each wave of a workgroup multiplies
 // a quarter of K for the whole tile; gemm_q4_0_launch routes to it.
 bool gemm_q4_0_ks_supported(uint32_t N, uint32_t K, uint32_t M);
-hipError_t gemm_q4_0_ks_launch(const uint8_t* w, uint32_t N, uint32_t K, const void* x, uint32_t M, void* y,
-                               bool y_bf16, hipStream_t stream);
+hipError_t gemm_q4_0_ks_launch(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs,
+                               uint32_t M, void* y, bool y_bf16, hipStream_t stream);
 
 }  // namespace dmx

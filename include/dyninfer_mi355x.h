@@ -19,7 +19,9 @@
  *   - opaque context handle with open/close pair (wrapper.h:39-60);
  *   - all buffers are caller-owned device memory; the library never repacks or
  *     copies weights and keeps no allocation between calls (README.md:5-9,
- *     crates/dyninfer-compiler/src/lib.rs:630);
+ *     crates/dyninfer-compiler/src/lib.rs:630); its one device allocation is the
+ *     transient prefill staging workspace of qlinear with rows >= 17, allocated
+ *     and freed in stream order on the caller's stream;
  *   - work is enqueued asynchronously on the caller's HIP stream (`stream` is a
  *     hipStream_t passed as void*; NULL = the null stream); concurrent calls on
  *     distinct streams are allowed; there is no CPU fallback (README.md:83-84).
@@ -69,6 +71,14 @@ enum { DYNINFER_DTYPE_F32 = 0, DYNINFER_DTYPE_F16 = 1, DYNINFER_DTYPE_BF16 = 2 }
  * MLX affine U4 (PhysicalEncoding::GroupQuantized, crates/dyninfer-checkpoint-safetensors/src/mlx.rs:152-261):
  *   `data` = packed u32 [N, K/8] (lane i = bits 4i..4i+3), `scales`, `biases` = [N, K/group_size]
  *   of `scale_dtype` (f32/f16/bf16), each aligned to its element size.
+ *
+ * The *_bytes fields give each component's byte length, the sum of its byte ranges in
+ * the reference's parameter binding.  Every call validates them as the reference's
+ * encodings do: GGUF `data_bytes` must equal N*(K/B)*bytes_per_block
+ * ("one interleaved data component", gguf_block.rs:111-155, q4_0.rs:82-119); MLX
+ * `data_bytes` must equal N*K/2 and `scales_bytes` = `biases_bytes` = N*(K/g)*sizeof(scale)
+ * ("MLX component byte length", mlx_affine.rs:137-153).  A mismatch is
+ * DYNINFER_MI355X_ERR_UNSUPPORTED (E_UNSUPPORTED_ENCODING); no kernel reads a short buffer.
  */
 typedef struct dyninfer_qweight {
     uint32_t encoding;
@@ -80,6 +90,9 @@ typedef struct dyninfer_qweight {
     const void* biases;   /* MLX only */
     uint32_t scale_dtype; /* MLX only */
     uint32_t reserved;
+    uint64_t data_bytes;
+    uint64_t scales_bytes; /* MLX only (0 for GGUF) */
+    uint64_t biases_bytes; /* MLX only (0 for GGUF) */
 } dyninfer_qweight_t;
 
 typedef struct dyninfer_mi355x_ctx dyninfer_mi355x_ctx_t;
@@ -99,10 +112,20 @@ const char* dyninfer_mi355x_last_error(void);
  * reference's dequantised value (gguf_codegen.rs:268-314 `emit_linear`;
  * mlx_affine.rs:557-626 `emit_linear_u4`; output projection = the same helper,
  * gguf_codegen.rs:157-159).  `rows` = activation rows (1..16 for decode; any for prefill).
- * x: [rows, K] row-major, dtype x_dtype (f32 or bf16); y: [rows, N], dtype y_dtype
- * (f32 or bf16).  rows <= 16 runs the decode GEMV kernels (VALU, HBM-bound);
- * rows >= 17 runs the prefill path (Q4_0: dequant-to-LDS + MFMA; other encodings: the
- * GEMV kernels over row chunks).
+ * x: [rows, K] row-major, 16-byte aligned, dtype x_dtype (f32 or bf16, every encoding);
+ * y: [rows, N], dtype y_dtype (f32 or bf16).
+ *   rows <= 16: the decode GEMV kernels (HBM-bound; 5..16 rows of large Q4_0, Q6_K and
+ *     MLX weights on MFMA), activations rounded to f16 after a power-of-two scaling per
+ *     scale group;
+ *   rows >= 17: the prefill path.  x is staged once per call as f16 rows scaled by a
+ *     power of two per row (RNE), then a dequant-to-LDS + MFMA GEMM per weight.  The
+ *     staging needs a transient device workspace of about rows*K*2 bytes, allocated and
+ *     freed on `stream` (hipMallocAsync / hipFreeAsync, stream-ordered); encodings
+ *     without a prefill GEMM run the GEMV kernels over 16-row chunks instead and need
+ *     no workspace.
+ * Error bound: |y - y_exact| <= 2^-10 * sum_k |w||x| plus f32 accumulation, where a
+ * prefill activation more than 2^29 below its row's largest magnitude may also be
+ * flushed to f16 subnormals (absolute 2^-40 * max|x| each).
  */
 int dyninfer_mi355x_qlinear(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* w,
                             const void* x, uint32_t x_dtype, uint32_t rows,
@@ -111,7 +134,8 @@ int dyninfer_mi355x_qlinear(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t
 /*
  * Several weights that share one activation (q/k/v, gate/up) in a single launch:
  * y_i = x · W_iᵀ for i < count.  All weights must have the same encoding (and group
- * size / scale dtype) and the same K; N may differ.  count <= 4, rows <= 16.
+ * size / scale dtype) and the same K; N may differ.  count <= 4, any rows (prefill
+ * stages x once and runs one GEMM per weight).
  * No reference counterpart as one call: the reference emits one helper call per
  * linear (parameter.rs:141-183); this is the same arithmetic batched into one launch.
  */

@@ -72,12 +72,46 @@ def test_supports_mlx_rules():
 
 
 def test_supports_dtype_rules():
-    assert d.supports(w(d.ENC_Q4_0), 512, d.DTYPE_BF16, d.DTYPE_BF16)   # MFMA path
-    assert not d.supports(w(d.ENC_Q6_K), 1, d.DTYPE_BF16)              # GGUF decode takes f32 activations
+    # f32 or bf16 activations for every encoding, any row count; f16 activations are not qualified
+    for enc in (d.ENC_Q4_0, d.ENC_Q4_1, d.ENC_Q8_0, d.ENC_Q6_K):
+        for rows in (1, 4, 16, 17, 512):
+            assert d.supports(w(enc), rows, d.DTYPE_BF16, d.DTYPE_BF16)
+            assert d.supports(w(enc), rows, d.DTYPE_F32, d.DTYPE_F32)
     assert not d.supports(w(d.ENC_Q4_0), 1, d.DTYPE_F16)
-    assert not d.supports(w(d.ENC_Q6_K), 1, d.DTYPE_BF16)
-    assert "bf16 activations" in d.library().dyninfer_mi355x_last_error().decode()
+    assert "activations must be f32 or bf16" in d.library().dyninfer_mi355x_last_error().decode()
+    assert not d.supports(w(d.ENC_Q4_0), 1, d.DTYPE_F32, d.DTYPE_F16)
     assert not d.supports(w(d.ENC_Q4_0), 0)
+
+
+@pytest.mark.parametrize("enc,rows,cols,nbytes", [
+    (d.ENC_Q4_0, 64, 256, 64 * 8 * 18), (d.ENC_Q4_1, 3, 64, 3 * 2 * 20), (d.ENC_Q8_0, 5, 96, 5 * 3 * 34),
+    (d.ENC_Q6_K, 7, 512, 7 * 2 * 210)])
+def test_gguf_data_component_byte_total(enc, rows, cols, nbytes):
+    """One interleaved data component of N·(K/B)·bytes_per_block bytes
+    (gguf_block.rs:124-155): a short or long buffer is E_UNSUPPORTED_ENCODING."""
+    assert d.supports(w(enc, rows, cols, data_bytes=nbytes), 1)
+    for bad in (nbytes - 1, nbytes + 1, nbytes - 18, 0):
+        assert not d.supports(w(enc, rows, cols, data_bytes=bad), 1)
+        msg = d.library().dyninfer_mi355x_last_error().decode()
+        assert f"requires one interleaved data component of {nbytes} bytes, got {bad} bytes" in msg
+    lib = d.library()
+    wc = w(enc, rows, cols, data_bytes=nbytes - 2).c()
+    rc = lib.dyninfer_mi355x_qlinear(ctypes.c_void_p(1), ctypes.byref(wc), 0x1000, d.DTYPE_F32, 1, 0x2000,
+                                     d.DTYPE_F32, None)
+    assert rc == d.ERR_UNSUPPORTED  # rejected host-side before any launch
+
+
+def test_mlx_component_byte_lengths():
+    """packed N·K/2, scales and biases N·(K/g)·sizeof(scale) (mlx_affine.rs:137-153)."""
+    kw = dict(data=0x1000, scales=0x2000, biases=0x3000, group_size=64)
+    n, k = 16, 256
+    for dt, es in ((d.DTYPE_BF16, 2), (d.DTYPE_F16, 2), (d.DTYPE_F32, 4)):
+        g = n * (k // 64) * es
+        assert d.supports(w(d.ENC_MLX_U4, n, k, scale_dtype=dt, data_bytes=n * k // 2, scales_bytes=g,
+                            biases_bytes=g, **kw), 1)
+        for bad in (dict(data_bytes=n * k // 2 - 4), dict(scales_bytes=g - es), dict(biases_bytes=g + es)):
+            assert not d.supports(w(d.ENC_MLX_U4, n, k, scale_dtype=dt, **kw, **bad), 1)
+            assert "MLX component byte length is invalid" in d.library().dyninfer_mi355x_last_error().decode()
 
 
 def test_calls_without_context_fail_cleanly():

@@ -106,7 +106,8 @@ def test_general_alignment_and_metadata_types():
     assert g2.metadata["nan"] is None  # serde_json: non-finite f32 -> null
 
 
-@pytest.mark.parametrize("case", ["magic", "version", "truncated", "past_end", "block", "type", "value_type", "dup"])
+@pytest.mark.parametrize("case", ["magic", "version", "truncated", "past_end", "block", "type", "value_type", "dup",
+                                  "utf8_key", "utf8_value", "utf8_surrogate", "utf8_overlong", "align_overflow"])
 def test_invalid_files_are_rejected(case):
     good = {"w": ((2, 32), Q4_0, bytes(36))}
     if case == "magic":
@@ -123,15 +124,46 @@ def test_invalid_files_are_rejected(case):
         blob = write_gguf({"w": ((2, 32), 99, bytes(36))}, {})
     elif case == "value_type":
         blob = write_gguf(good, {}, extra_meta=_s("k") + struct.pack("<I", 13))
+    elif case.startswith("utf8"):
+        # container.rs read_string: String::from_utf8 rejects the bytes
+        bad = {"utf8_key": b"\xff", "utf8_value": b"\xc3\x28", "utf8_surrogate": b"\xed\xa0\x80",
+               "utf8_overlong": b"\xc0\xaf"}[case]
+        raw = struct.pack("<Q", len(bad)) + bad
+        extra = raw + struct.pack("<I", 4) + struct.pack("<I", 1) if case == "utf8_key" else \
+            _s("k") + struct.pack("<I", 8) + raw
+        blob = write_gguf(good, {}, extra_meta=extra)
+    elif case == "align_overflow":
+        # align_up(pos, 2^64 - 1) = 2^64 - 1: the data section lies past the end of the file
+        blob = write_gguf(good, {"general.alignment": ("u64", (1 << 64) - 1)}, alignment=32)
     else:
         blob = write_gguf({"wa": ((2, 32), Q4_0, bytes(36)), "wb": ((2, 32), Q4_0, bytes(36))}, {})
         blob = blob.replace(_s("wb"), _s("wa"), 1)
     msg = {"magic": "bad magic", "version": "version 4", "truncated": "truncated", "past_end": "past end",
            "block": "not divisible", "type": "unknown GGUF tensor type", "value_type": "value type 13",
-           "dup": "duplicate"}[case]
+           "dup": "duplicate", "utf8_key": "not UTF-8", "utf8_value": "not UTF-8", "utf8_surrogate": "not UTF-8",
+           "utf8_overlong": "not UTF-8", "align_overflow": "past end"}[case]
     with pytest.raises(d.DyninferError) as e:
         d.GgufFile.from_bytes(blob)
     assert e.value.code == d.ERR_UNSUPPORTED and msg in e.value.message
+
+
+def test_valid_utf8_metadata_is_kept():
+    txt = "Größe ✓ \U0001F600"
+    g = d.GgufFile.from_bytes(write_gguf({"w": ((2, 32), Q4_0, bytes(36))}, {"name": ("str", txt)}))
+    assert g.metadata["name"] == txt
+
+
+def test_invalid_file_opened_by_path_is_unmapped(tmp_path):
+    """A file that fails indexing is reported and its mapping released (no
+    mapping of it is left in the process after repeated failed opens)."""
+    path = tmp_path / "bad_version.gguf"
+    path.write_bytes(write_gguf({"w": ((2, 32), Q4_0, bytes(36))}, {}, version=4))
+    for _ in range(20):
+        with pytest.raises(d.DyninferError) as e:
+            d.GgufFile(str(path))
+        assert e.value.code == d.ERR_UNSUPPORTED and "version 4" in e.value.message
+    maps = open("/proc/self/maps").read()
+    assert str(path) not in maps
 
 
 @pytest.mark.gpu

@@ -394,9 +394,16 @@ def _rows_subset(gtype, data, n, k, rows):
 @pytest.mark.parametrize("gtype,n,k,batch", [
     (oracle.Q6_K, 151936, 1024, 1),   # Qwen3-0.6B tied lm_head
     (oracle.Q6_K, 151936, 1024, 16),  # the same at batch 16 (MFMA path)
+    (oracle.Q6_K, 151936, 4096, 1),   # Qwen3-8B lm_head (510 MB)
+    (oracle.Q6_K, 151936, 4096, 4),
+    (oracle.Q6_K, 151936, 4096, 16),
     (oracle.Q6_K, 4096, 12288, 4),    # Qwen3-8B down_proj
     (oracle.Q4_0, 12288, 4096, 16),   # Qwen3-8B gate/up
     (oracle.Q8_0, 1024, 3072, 4),     # Qwen3-0.6B down_proj
+    (oracle.Q4_0, 1024, 2048, 1),     # Qwen3-0.6B o_proj (K = 2048), every GGUF type
+    (oracle.Q4_1, 1024, 2048, 1),
+    (oracle.Q8_0, 1024, 2048, 1),
+    (oracle.Q6_K, 1024, 2048, 1),
 ])
 def test_gemv_full_size_rows_subset(ctx, gtype, n, k, batch):
     """Full BASELINE shapes: 512 random output rows checked against the oracle,
@@ -442,6 +449,33 @@ def test_gemv_gguf_kernel_paths(ctx, gtype, n, k):
     rows = np.sort(np.random.default_rng(n).choice(n, size=min(512, n), replace=False))
     wsub = oracle.dequant_gguf(gtype, _rows_subset(gtype, data, n, k, rows), len(rows), k)
     assert gemv_err(np.ascontiguousarray(y[:, rows]), x, wsub) <= XF16
+
+
+@pytest.mark.parametrize("batch", [1, 8, 16])
+def test_gemv_mlx_lm_head_full_size(ctx, batch):
+    """Qwen3-0.6B tied lm_head in MLX U4 g64 (151936 x 1024):
+    512 random output rows against the oracle, linearity and zero input over
+    every output."""
+    n, k, g = 151936, 1024, 64
+    packed, sc, bi = oracle.synth_mlx_u4(n, k, g, oracle.D_BF16, seed=151)
+    w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), g, oracle.D_BF16)
+    x1 = oracle.randn(batch * k, seed=1).reshape(batch, k)
+    x2 = oracle.randn(batch * k, seed=2).reshape(batch, k)
+    y1 = ctx.qlinear(w, dev(x1)).cpu().numpy()
+    rows = np.sort(np.random.default_rng(1).choice(n, size=512, replace=False))
+    gpr = k // g
+    sub = oracle.dequant_mlx_u4(packed.reshape(n, -1)[rows], sc.reshape(n, -1)[rows], bi.reshape(n, -1)[rows],
+                                oracle.D_BF16, len(rows), k, g)
+    tol = 2.0 ** -10 + 1e-4 if batch >= 5 else XF16
+    assert gpr == 16 and gemv_err(np.ascontiguousarray(y1[:, rows]), x1, sub) <= tol
+    x3 = (2 * x1 - x2).astype(np.float32)
+    y2 = ctx.qlinear(w, dev(x2)).cpu().numpy()
+    y3 = ctx.qlinear(w, dev(x3)).cpu().numpy()
+    wabs = ctx.dequant(w).abs()
+    bound = sum(c * (torch.abs(dev(xi)) @ wabs.T).cpu().numpy() for c, xi in ((2, x1), (1, x2), (1, x3)))
+    assert np.all(np.abs(y3 - (2 * y1 - y2)) <= 2.0 ** -10 * bound + 1e-30)
+    z = ctx.qlinear(w, torch.zeros((batch, k), dtype=torch.float32, device="cuda"))
+    assert torch.count_nonzero(z).item() == 0
 
 
 @pytest.mark.parametrize("n,k", [(300, 6144), (300, 8192), (1024, 12288)])

@@ -1,0 +1,240 @@
+"""GPU parity for the routes a quantized linear takes beyond single-weight f32
+decode, through the C ABI, against the CPU oracle:
+
+  * prefill (rows >= 17) with f32 and bf16 activations for every encoding,
+    through qlinear and qlinear_multi: Q4_0 runs the staged-activation MFMA
+    GEMM (x rounded once to f16 after a power-of-two scaling per row), the
+    other encodings the GEMV kernels over 16-row chunks (the chunks' x and y
+    pointer arithmetic is what the 17/32/200/512 row counts check);
+  * bf16 activations on the decode GEMV for every encoding;
+  * grouped launches (q/k/v, gate/up) for every encoding at the Qwen3-0.6B
+    shapes of BASELINE config 1, batches 1, 4 and 16;
+  * the GEMM over activation magnitudes f16 cannot hold unscaled;
+  * rows whose codes all sit at the zero point (w == 0 exactly, d != 0).
+
+Tolerances, as max over outputs of |y - y64| / sum_k |w||x| (y64 the f64
+contraction of the exactly dequantised weights): 2^-10 + 2e-5 (one f16
+rounding of each weight and each activation, plus f32 accumulation), within
+the 2e-3 north-star tolerance; bf16 outputs add their own rounding, 2^-8 of |y|.
+"""
+import numpy as np
+import pytest
+import torch
+
+import dyninfer_amd as d
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+ENC = {oracle.Q4_0: d.ENC_Q4_0, oracle.Q4_1: d.ENC_Q4_1, oracle.Q8_0: d.ENC_Q8_0, oracle.Q6_K: d.ENC_Q6_K}
+MLX = "mlx"
+ALL = list(oracle.GGUF_TYPES) + [MLX]
+IDS = {**oracle.NAMES, MLX: "mlx_u4"}
+F16X2 = 2.0 ** -10 + 2e-5
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def make(kind, n, k, seed):
+    """(QWeight, exactly dequantised f32 [n, k]) for a GGUF type or MLX U4 g64 bf16."""
+    if kind == MLX:
+        packed, sc, bi = oracle.synth_mlx_u4(n, k, 64, oracle.D_BF16, seed=seed)
+        w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), 64, d.DTYPE_BF16)
+        return w, oracle.dequant_mlx_u4(packed, sc, bi, oracle.D_BF16, n, k, 64)
+    data = oracle.synth_gguf(kind, n, k, seed)
+    return d.QWeight(ENC[kind], n, k, dev(data)), oracle.dequant_gguf(kind, data, n, k)
+
+
+def xs(rows, k, seed, bf16):
+    """Activations as the device sees them (bf16 bits or f32) and their f32 values."""
+    x = oracle.randn(rows * k, seed=seed).reshape(rows, k)
+    if not bf16:
+        return dev(x), x
+    xb = oracle.f32_to_bf16_bits(x.reshape(-1)).reshape(rows, k)
+    return dev(xb).view(torch.bfloat16), oracle.bf16_bits_to_f32(xb).reshape(rows, k)
+
+
+def err_of(y, x, wf, ybf16=False):
+    if ybf16:
+        y = oracle.bf16_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(y.shape)
+    else:
+        y = y.cpu().numpy()
+    y64, absdot = oracle.linear_f64(x, wf)
+    den = np.where(absdot > 0, absdot, 1)
+    err = np.abs(y.astype(np.float64) - y64) / den
+    if ybf16:
+        err = err - np.abs(y64) * 2.0 ** -8 / den
+    return float(err.max())
+
+
+# ----------------------------------------------------------------- prefill, every encoding
+@pytest.mark.parametrize("kind", ALL, ids=IDS.get)
+@pytest.mark.parametrize("rows", [17, 32, 200, 512])
+@pytest.mark.parametrize("xbf16", [False, True], ids=["xf32", "xbf16"])
+def test_prefill_rows(ctx, kind, rows, xbf16):
+    n, k = 384, 1024
+    w, wf = make(kind, n, k, seed=rows + 3)
+    xd, x = xs(rows, k, seed=rows, bf16=xbf16)
+    assert err_of(ctx.qlinear(w, xd), x, wf) <= F16X2
+
+
+@pytest.mark.parametrize("kind", ALL, ids=IDS.get)
+@pytest.mark.parametrize("rows", [17, 200])
+def test_prefill_multi(ctx, kind, rows):
+    """q/k/v sharing one activation, rows > 16: one staging of x, then one
+    GEMM (or GEMV chunk sequence) per weight, outputs of different N."""
+    k, shapes = 1024, [512, 256, 256]
+    made = [make(kind, n, k, seed=40 + i) for i, n in enumerate(shapes)]
+    xd, x = xs(rows, k, seed=9, bf16=False)
+    ys = ctx.qlinear_multi([m[0] for m in made], xd)
+    for y, (_, wf) in zip(ys, made):
+        assert err_of(y, x, wf) <= F16X2
+
+
+@pytest.mark.parametrize("m,n,k", [(17, 256, 1024), (128, 3072, 1024), (512, 3072, 1024), (512, 1024, 3072),
+                                   (2048, 3072, 1024), (300, 1000, 768)])
+@pytest.mark.parametrize("ybf16", [False, True], ids=["yf32", "ybf16"])
+def test_gemm_q4_0_f32_activations(ctx, m, n, k, ybf16):
+    """The Q4_0 GEMM with f32 activations (the candidates' advertised input
+    type): each kernel path (K-split at M=128, 128x64 and 128x128 tiles),
+    ragged tiles."""
+    w, wf = make(oracle.Q4_0, n, k, seed=m + n)
+    xd, x = xs(m, k, seed=m * 3 + k, bf16=False)
+    y = ctx.qlinear(w, xd, y_dtype=torch.bfloat16 if ybf16 else torch.float32)
+    assert err_of(y, x, wf, ybf16) <= F16X2
+
+
+def _ranged_x(rows, k, seed, lo, hi):
+    """N(0,1) activations scaled by 10^u per 16-element run, u uniform in
+    [lo, hi], and one all-zero run."""
+    rng = np.random.default_rng(seed)
+    x = oracle.randn(rows * k, seed=seed).reshape(rows, k).astype(np.float64)
+    x *= np.repeat(10.0 ** rng.uniform(lo, hi, size=(rows, k // 16)), 16, axis=1)
+    x[:, 32:48] = 0.0
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("m", [128, 512, 2048])
+@pytest.mark.parametrize("lo,hi", [(6, 8), (-30, -28), (-8, 8), (-36, 32)])
+def test_gemm_q4_0_activation_range(ctx, m, lo, hi):
+    """Magnitudes f16 cannot hold unscaled (above 65504, below 6e-8) and up to
+    68 decades within a row: the per-row power-of-two staging keeps the large
+    values at full f16 precision; values more than 2^29 below their row's
+    largest become f16 subnormals, each at most 2^-40·max|x| off, a vanishing
+    share of sum|w||x| here.  f32 and bf16 activations."""
+    n, k = 512, 1024
+    w, wf = make(oracle.Q4_0, n, k, seed=m + lo)
+    x = _ranged_x(m, k, seed=(lo + 100) * 7 + hi + m, lo=lo, hi=hi)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    assert np.all(np.isfinite(y))
+    y64, absdot = oracle.linear_f64(x, wf)
+    assert oracle.normalized_error(y, y64, absdot) <= F16X2
+    xb = oracle.f32_to_bf16_bits(x.reshape(-1)).reshape(m, k)
+    y = ctx.qlinear(w, dev(xb).view(torch.bfloat16))
+    assert err_of(y, oracle.bf16_bits_to_f32(xb).reshape(m, k), wf) <= F16X2
+
+
+def test_gemm_q4_0_nonfinite_row_stays_in_its_row(ctx):
+    n, k, m = 256, 1024, 64
+    w, wf = make(oracle.Q4_0, n, k, seed=5)
+    x = oracle.randn(m * k, seed=6).reshape(m, k)
+    x[3, 10] = np.nan
+    x[40, 900] = np.inf
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    assert not np.any(np.isfinite(y[3])) and not np.any(np.isfinite(y[40]))
+    keep = [r for r in range(m) if r not in (3, 40)]
+    y64, absdot = oracle.linear_f64(x[keep], wf)
+    assert oracle.normalized_error(y[keep], y64, absdot) <= F16X2
+
+
+# ----------------------------------------------------------------- decode with bf16 activations
+@pytest.mark.parametrize("kind", ALL, ids=IDS.get)
+@pytest.mark.parametrize("n,k", [(1024, 1024), (3072, 1024), (1024, 3072), (6144, 4096)])
+@pytest.mark.parametrize("batch", [1, 2, 4, 8, 16])
+def test_gemv_bf16_activations(ctx, kind, n, k, batch):
+    w, wf = make(kind, n, k, seed=n + k + batch)
+    xd, x = xs(batch, k, seed=batch + 17, bf16=True)
+    assert err_of(ctx.qlinear(w, xd), x, wf) <= F16X2
+
+
+# ----------------------------------------------------------------- grouped launches, every encoding
+@pytest.mark.parametrize("kind", ALL, ids=IDS.get)
+@pytest.mark.parametrize("batch", [1, 4, 16])
+@pytest.mark.parametrize("group", ["qkv", "gate_up"])
+def test_multi_config1_shapes(ctx, kind, batch, group):
+    """Qwen3-0.6B q/k/v (2048, 1024, 1024 x 1024) and gate/up (2 x 3072 x 1024)
+    in one launch, as BASELINE config 1's step issues them."""
+    k = 1024
+    shapes = [2048, 1024, 1024] if group == "qkv" else [3072, 3072]
+    made = [make(kind, n, k, seed=100 + 7 * i + batch) for i, n in enumerate(shapes)]
+    xd, x = xs(batch, k, seed=batch + 5, bf16=kind == MLX)
+    ys = ctx.qlinear_multi([m[0] for m in made], xd)
+    for y, (_, wf) in zip(ys, made):
+        assert err_of(y, x, wf) <= F16X2
+
+
+# ----------------------------------------------------------------- zero-point rows
+def _zero_point(kind, n, k, seed):
+    """Weights whose first 64 rows dequantise to exactly 0 everywhere, with
+    non-zero scales: Q4_0 code 8, Q8_0 code 0, Q6_K q = 32 (ql 0, qh 2), Q4_1
+    and MLX code 0 with a zero offset."""
+    zr = 64
+    if kind == MLX:
+        packed, sc, bi = oracle.synth_mlx_u4(n, k, 64, oracle.D_BF16, seed=seed)
+        packed.reshape(n, -1)[:zr] = 0
+        bi.reshape(n, -1)[:zr] = 0
+        wf = oracle.dequant_mlx_u4(packed, sc, bi, oracle.D_BF16, n, k, 64)
+        w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), 64, d.DTYPE_BF16)
+        dmax = np.abs(oracle.bf16_bits_to_f32(sc).reshape(n, -1)).max(axis=1)
+    else:
+        data = oracle.synth_gguf(kind, n, k, seed)
+        bw, bb = oracle.BLOCK[kind]
+        blk = data.reshape(n, k // bw, bb)
+        if kind == oracle.Q4_0:
+            blk[:zr, :, 2:] = 0x88
+        elif kind == oracle.Q4_1:
+            blk[:zr, :, 2:4] = 0  # m = +0
+            blk[:zr, :, 4:] = 0
+        elif kind == oracle.Q8_0:
+            blk[:zr, :, 2:] = 0
+        else:
+            blk[:zr, :, 0:128] = 0      # low 4 bits 0
+            blk[:zr, :, 128:192] = 0xAA  # high 2 bits 2 in every field
+        wf = oracle.dequant_gguf(kind, data, n, k)
+        w = d.QWeight(ENC[kind], n, k, dev(data))
+        dpos = 208 if kind == oracle.Q6_K else 0
+        dbits = blk[:, :, dpos].astype(np.uint16) | (blk[:, :, dpos + 1].astype(np.uint16) << 8)
+        dv = np.abs(dbits.view(np.float16).astype(np.float64))
+        if kind == oracle.Q6_K:
+            dv = dv * 128.0  # |d·sc| <= 128 |d|
+        dmax = dv.max(axis=1)
+    assert not np.any(wf[:zr]) and np.all(dmax[:zr] > 0)
+    return w, wf, zr, dmax
+
+
+@pytest.mark.parametrize("kind", ALL, ids=IDS.get)
+@pytest.mark.parametrize("rows", [1, 4, 16, 200])
+def test_zero_point_rows(ctx, kind, rows):
+    """Rows that dequantise to exactly 0 give y = 0 in the reference.  Paths
+    that decode each weight before multiplying (MFMA GEMV at 5..16 rows on
+    large Q4_0/Q6_K/MLX weights, the Q4_0 GEMM) return exactly 0.  The VALU
+    GEMV computes sum P·v - C with C = sum coef·v formed in another order, so
+    it leaves an f32 rounding residue, bounded in absolute terms by
+    2^-8 · sum_k |x_k| · |scale of k's block| (|d·sc| for Q6_K): at most ~56
+    roundings (two per v_dot2 if it rounds its product sum and its addition
+    separately) of partial sums no larger than 1152·sum|v| per chunk.  x has
+    magnitude ~1e3 so that any residue is visible."""
+    n, k = 6144, 1024
+    w, wf, zr, dmax = _zero_point(kind, n, k, seed=rows + 11)
+    x = (oracle.randn(rows * k, seed=rows) * 1000.0).reshape(rows, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    y64, absdot = oracle.linear_f64(x, wf)
+    assert oracle.normalized_error(y[:, zr:], y64[:, zr:], absdot[:, zr:]) <= F16X2
+    bound = 2.0 ** -8 * np.abs(x).sum(axis=1, keepdims=True) * dmax[None, :zr]
+    print(f"zero-point residue / bound: {np.max(np.abs(y[:, :zr]) / bound):.3e}")
+    assert np.all(np.abs(y[:, :zr]) <= bound)
+    exact = (kind == oracle.Q4_0 and rows > 16) or (rows >= 5 and rows <= 16 and kind in (oracle.Q4_0, oracle.Q6_K, MLX))
+    if exact:
+        assert not np.any(y[:, :zr]), np.abs(y[:, :zr]).max()
