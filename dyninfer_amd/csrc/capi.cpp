@@ -17,14 +17,27 @@
 #include <cerrno>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "gguf.hpp"
 #include "kernels.hpp"
 #include "registry.hpp"
 
+// A context's prefill staging workspace for one stream: grown in stream order
+// (the old buffer released with hipFreeAsync behind the work that used it),
+// kept for the next call on that stream, released at close.
+struct StreamWorkspace {
+    hipStream_t st;
+    uint8_t* p;
+    uint64_t bytes;
+};
+
 struct dyninfer_mi355x_ctx {
     int device;
+    std::mutex mu;     // held from workspace lookup until the call's launches are enqueued
+    std::vector<StreamWorkspace> work;
 };
 
 namespace {
@@ -185,8 +198,11 @@ bool has_prefill_gemm(uint32_t enc, uint32_t N, uint32_t K, uint32_t rows) {
     return enc == DYNINFER_ENC_GGUF_Q4_0 && dmx::gemm_q4_0_supported(N, K, rows);
 }
 
-// Device memory of one prefill call: transient (hipMallocAsync on the stream,
-// released with hipFreeAsync after the launches that use it).
+// Device memory of one prefill call.  Normally the context's workspace for the
+// stream (grown when too small).  Under stream capture the call never uses a
+// context workspace, which a later regrowth could free while the graph still
+// names it: it takes a transient stream-ordered allocation, released after its
+// launches, that the captured graph allocates and frees on each replay.
 struct Workspace {
     uint8_t* p = nullptr;
     hipStream_t st = nullptr;
@@ -195,6 +211,39 @@ struct Workspace {
         if (owned) (void)hipFreeAsync(p, st);
     }
 };
+
+hipError_t acquire_workspace(dyninfer_mi355x_ctx_t* ctx, hipStream_t st, uint64_t need, Workspace& wk) {
+    wk.st = st;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(st, &cap);
+    if (e != hipSuccess) return e;
+    if (cap != hipStreamCaptureStatusNone) {
+        e = hipMallocAsync(reinterpret_cast<void**>(&wk.p), (size_t)need, st);
+        wk.owned = e == hipSuccess;
+        return e;
+    }
+    StreamWorkspace* sw = nullptr;
+    for (StreamWorkspace& w : ctx->work)
+        if (w.st == st) sw = &w;
+    if (sw && sw->bytes >= need) {
+        wk.p = sw->p;
+        return hipSuccess;
+    }
+    uint64_t bytes = 1u << 20;  // powers of two from 1 MiB: few regrowths as prefill lengths vary
+    while (bytes < need) bytes *= 2;
+    uint8_t* p = nullptr;
+    e = hipMallocAsync(reinterpret_cast<void**>(&p), (size_t)bytes, st);
+    if (e != hipSuccess) return e;
+    if (sw) {
+        (void)hipFreeAsync(sw->p, st);  // after the work already queued on st that uses it
+        sw->p = p;
+        sw->bytes = bytes;
+    } else {
+        ctx->work.push_back({st, p, bytes});
+    }
+    wk.p = p;
+    return hipSuccess;
+}
 
 // The prefill path: x staged once (xprep), then one GEMM per weight.
 hipError_t prefill(const dyninfer_qweight_t* ws, uint32_t count, const void* x, uint32_t x_dtype, uint32_t rows,
@@ -249,12 +298,25 @@ int dyninfer_mi355x_open(int device, dyninfer_mi355x_ctx_t** out_ctx) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(DYNINFER_MI355X_ERR_DEVICE,
                     std::string("device is ") + prop.gcnArchName + "; this library's kernels are built for gfx950 only");
-    *out_ctx = new dyninfer_mi355x_ctx{device};
+    auto* c = new dyninfer_mi355x_ctx();
+    c->device = device;
+    *out_ctx = c;
     return DYNINFER_MI355X_OK;
 }
 
 int dyninfer_mi355x_close(dyninfer_mi355x_ctx_t* ctx) {
+    if (!ctx) return DYNINFER_MI355X_OK;
+    hipError_t first = hipSuccess;
+    {
+        DeviceGuard g(ctx->device);
+        // hipFree waits for the device, so work still using a workspace completes first
+        for (StreamWorkspace& w : ctx->work) {
+            const hipError_t e = hipFree(w.p);
+            if (first == hipSuccess) first = e;
+        }
+    }
     delete ctx;
+    if (first != hipSuccess) return hip_fail(first, "hipFree (prefill staging workspace)");
     return DYNINFER_MI355X_OK;
 }
 
@@ -287,6 +349,7 @@ int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qwe
         gemm = has_prefill_gemm(ws[i].encoding, (uint32_t)ws[i].rows, (uint32_t)ws[i].cols, rows);
     if (gemm && (uint64_t)rows * ws[0].cols >= (1ull << 31))
         return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "prefill: rows * K must stay below 2^31 (32-bit activation offsets)");
+    const uint64_t need = gemm ? dmx::prefill_workspace_bytes(rows, (uint32_t)ws[0].cols) : 0;
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -294,9 +357,9 @@ int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qwe
     if (gemm) {
         Workspace wk;
         wk.st = st;
-        e = hipMallocAsync(reinterpret_cast<void**>(&wk.p), (size_t)dmx::prefill_workspace_bytes(rows, (uint32_t)ws[0].cols), st);
+        std::lock_guard<std::mutex> lock(ctx->mu);
+        e = acquire_workspace(ctx, st, need, wk);
         if (e != hipSuccess) return hip_fail(e, "hipMallocAsync (prefill staging workspace)");
-        wk.owned = true;
         e = prefill(ws, count, x, x_dtype, rows, ys, y_dtype, wk.p, st);
     } else {
         e = gemv_rows(ws, count, x, x_dtype, rows, ys, y_dtype, st);

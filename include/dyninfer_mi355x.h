@@ -17,11 +17,11 @@
  *     thread (thread-local, unlike the wrapper's process-global g_last_error,
  *     wrapper.c:238);
  *   - opaque context handle with open/close pair (wrapper.h:39-60);
- *   - all buffers are caller-owned device memory; the library never repacks or
- *     copies weights and keeps no allocation between calls (README.md:5-9,
- *     crates/dyninfer-compiler/src/lib.rs:630); its one device allocation is the
- *     transient prefill staging workspace of qlinear with rows >= 17, allocated
- *     and freed in stream order on the caller's stream;
+ *   - weights, activations and outputs are caller-owned device memory; the library
+ *     never repacks or copies weights and derives no parameters from them
+ *     (README.md:5-9, crates/dyninfer-compiler/src/lib.rs:630); its one device
+ *     allocation is the prefill staging workspace of qlinear with rows >= 17 (see
+ *     there), owned by the context;
  *   - work is enqueued asynchronously on the caller's HIP stream (`stream` is a
  *     hipStream_t passed as void*; NULL = the null stream); concurrent calls on
  *     distinct streams are allowed; there is no CPU fallback (README.md:83-84).
@@ -119,10 +119,16 @@ const char* dyninfer_mi355x_last_error(void);
  *     scale group;
  *   rows >= 17: the prefill path.  x is staged once per call as f16 rows scaled by a
  *     power of two per row (RNE), then a dequant-to-LDS + MFMA GEMM per weight.  The
- *     staging needs a transient device workspace of about rows*K*2 bytes, allocated and
- *     freed on `stream` (hipMallocAsync / hipFreeAsync, stream-ordered); encodings
- *     without a prefill GEMM run the GEMV kernels over 16-row chunks instead and need
- *     no workspace.
+ *     staging needs a device workspace of about rows*K*2 bytes.  The context keeps one
+ *     per stream handle, allocated on first use and grown in stream order
+ *     (hipMallocAsync; the old one hipFreeAsync'd behind the work that used it), and
+ *     releases them at dyninfer_mi355x_close.  Under stream capture the call uses no
+ *     context workspace (a later regrowth could free it while the graph names it): it
+ *     allocates and frees a transient one in stream order, which the captured graph
+ *     then does on every replay.
+ *     A stream that is destroyed while the context lives must have finished its work
+ *     first (its handle may be reused by a new stream).  Encodings without a prefill
+ *     GEMM run the GEMV kernels over 16-row chunks instead and need no workspace.
  * Error bound: |y - y_exact| <= 2^-10 * sum_k |w||x| plus f32 accumulation, where a
  * prefill activation more than 2^29 below its row's largest magnitude may also be
  * flushed to f16 subnormals (absolute 2^-40 * max|x| each).

@@ -238,3 +238,51 @@ def test_zero_point_rows(ctx, kind, rows):
     exact = (kind == oracle.Q4_0 and rows > 16) or (rows >= 5 and rows <= 16 and kind in (oracle.Q4_0, oracle.Q6_K, MLX))
     if exact:
         assert not np.any(y[:, :zr]), np.abs(y[:, :zr]).max()
+
+
+# ----------------------------------------------------------------- the prefill staging workspace
+def test_prefill_workspace_growth_across_calls_and_streams(ctx):
+    """The context's staging workspace per stream: grown in stream order when a
+    longer prefill arrives (the old one released behind the work using it),
+    reused by shorter ones; two streams keep distinct workspaces."""
+    n, k = 512, 1024
+    w, wf = make(oracle.Q4_0, n, k, seed=31)
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    cases = []
+    for i, (rows, st) in enumerate([(17, sa), (2048, sa), (64, sa), (1500, sb), (33, sb), (3000, sa)]):
+        xd, x = xs(rows, k, seed=100 + i, bf16=i % 2 == 1)
+        with torch.cuda.stream(st):
+            y = ctx.qlinear(w, xd, stream=st)
+        cases.append((y, x))
+    torch.cuda.synchronize()
+    for y, x in cases:
+        assert err_of(y, x, wf) <= F16X2
+
+
+def test_prefill_graph_capture_replays(ctx):
+    """A prefill captured in a HIP graph (its staging a transient stream-ordered
+    allocation owned by the graph) and replayed three times, with eager prefill
+    calls of other sizes between the replays: every replay equals the eager result."""
+    n, k, rows = 768, 1024, 200
+    w, wf = make(oracle.Q4_0, n, k, seed=41)
+    xd, x = xs(rows, k, seed=42, bf16=False)
+    eager = ctx.qlinear(w, xd).cpu().numpy()
+    assert err_of(torch.from_numpy(eager), x, wf) <= F16X2
+    y = torch.empty((rows, n), device="cuda")
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        ctx.qlinear(w, xd, y, stream=st)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            ctx.qlinear(w, xd, y, stream=st)
+    torch.cuda.synchronize()
+    for i in range(3):
+        y.fill_(float("nan"))
+        other, _ = xs(300 + 100 * i, k, seed=50 + i, bf16=True)
+        ctx.qlinear(w, other)  # eager work between the replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), eager.view(np.uint32)), i
+    del g
