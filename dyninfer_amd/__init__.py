@@ -37,6 +37,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdyninfer
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_HIP, ERR_DEVICE, ERR_BUFFER_TOO_SMALL = 0, 1, 2, 3, 4, 5
 ENC_Q4_0, ENC_Q4_1, ENC_Q8_0, ENC_Q6_K, ENC_MLX_U4 = 2, 3, 8, 14, 0x1004
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+NOALLOC_SCRATCH_BYTES = 32 << 20  # DYNINFER_MI355X_NOALLOC_SCRATCH_BYTES
 ENCODING_IDS = {ENC_Q4_0: "gguf.q4_0", ENC_Q4_1: "gguf.q4_1", ENC_Q8_0: "gguf.q8_0", ENC_Q6_K: "gguf.q6_k",
                 ENC_MLX_U4: "mlx.affine.u4"}
 # (weights per block, bytes per block): gguf_codegen.rs:23-38
@@ -49,7 +50,7 @@ EXPORTED_SYMBOLS = (
     "dyninfer_mi355x_gguf_tensor_count", "dyninfer_mi355x_gguf_metadata_json", "dyninfer_mi355x_gguf_tensor",
     "dyninfer_mi355x_gguf_find", "dyninfer_mi355x_gguf_upload", "dyninfer_mi355x_gguf_qweight",
     "dyninfer_mi355x_candidates_json", "dyninfer_mi355x_registry_select", "dyninfer_mi355x_registry_require",
-    "dyninfer_mi355x_version",
+    "dyninfer_mi355x_version", "dyninfer_mi355x_qlinear_multi_noalloc",
 )
 
 
@@ -96,6 +97,7 @@ def library() -> ctypes.CDLL:
         "dyninfer_mi355x_last_error": (ctypes.c_char_p, []),
         "dyninfer_mi355x_qlinear": (I, [P, W, P, U32, U32, P, U32, P]),
         "dyninfer_mi355x_qlinear_multi": (I, [P, W, U32, P, U32, U32, ctypes.POINTER(P), U32, P]),
+        "dyninfer_mi355x_qlinear_multi_noalloc": (I, [P, W, U32, P, U32, U32, ctypes.POINTER(P), U32, P]),
         "dyninfer_mi355x_dequant": (I, [P, W, P, P]),
         "dyninfer_mi355x_embedding": (I, [P, W, P, U32, P, P]),
         "dyninfer_mi355x_gguf_open": (I, [ctypes.c_char_p, ctypes.POINTER(P)]),
@@ -260,16 +262,19 @@ class Context:
                                                  y.data_ptr(), _dtype_code(y), self._stream(stream)))
         return y
 
-    def qlinear_multi(self, ws: Sequence[QWeight], x, ys=None, y_dtype=None, stream=None):
-        """One launch for several weights sharing activation x (same encoding and K)."""
+    def qlinear_multi(self, ws: Sequence[QWeight], x, ys=None, y_dtype=None, stream=None, noalloc=False):
+        """One launch for several weights sharing activation x (same encoding and K).
+        noalloc: dyninfer_mi355x_qlinear_multi_noalloc (prefill staging in the
+        device's static scratch; the caller passes the outputs)."""
         import torch
         rows = x.shape[0] if x.dim() == 2 else 1
         if ys is None:
             ys = [torch.empty((rows, w.rows), dtype=y_dtype or torch.float32, device=x.device) for w in ws]
         arr = (_QWeightC * len(ws))(*[w.c() for w in ws])
         yp = (ctypes.c_void_p * len(ws))(*[y.data_ptr() for y in ys])
-        _check(self._lib.dyninfer_mi355x_qlinear_multi(self._h, arr, len(ws), x.data_ptr(), _dtype_code(x), rows,
-                                                       yp, _dtype_code(ys[0]), self._stream(stream)))
+        fn = self._lib.dyninfer_mi355x_qlinear_multi_noalloc if noalloc else self._lib.dyninfer_mi355x_qlinear_multi
+        _check(fn(self._h, arr, len(ws), x.data_ptr(), _dtype_code(x), rows, yp, _dtype_code(ys[0]),
+                  self._stream(stream)))
         return ys
 
     def dequant(self, w: QWeight, out=None, stream=None):

@@ -25,6 +25,13 @@
 #include "kernels.hpp"
 #include "registry.hpp"
 
+// Prefill staging workspace of the no-allocation entry point: one array per
+// device, allocated when the code object loads and held until the process
+// ends.  In host code `scratch` only names the symbol; the device address is
+// taken once per context with hipGetSymbolAddress (ctx->scratch).
+constexpr size_t kScratchBytes = DYNINFER_MI355X_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
 // A context's prefill staging workspace for one stream: grown in stream order
 // (the old buffer released with hipFreeAsync behind the work that used it),
 // kept for the next call on that stream, released at close.
@@ -36,6 +43,7 @@ struct StreamWorkspace {
 
 struct dyninfer_mi355x_ctx {
     int device;
+    uint8_t* scratch;  // this device's copy of `scratch`
     std::mutex mu;     // held from workspace lookup until the call's launches are enqueued
     std::vector<StreamWorkspace> work;
 };
@@ -298,8 +306,15 @@ int dyninfer_mi355x_open(int device, dyninfer_mi355x_ctx_t** out_ctx) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(DYNINFER_MI355X_ERR_DEVICE,
                     std::string("device is ") + prop.gcnArchName + "; this library's kernels are built for gfx950 only");
+    // the device's copy of the no-allocation scratch array, with that device current
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    void* sp = nullptr;
+    e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress (no-allocation scratch)");
     auto* c = new dyninfer_mi355x_ctx();
     c->device = device;
+    c->scratch = static_cast<uint8_t*>(sp);
     *out_ctx = c;
     return DYNINFER_MI355X_OK;
 }
@@ -325,9 +340,11 @@ int dyninfer_mi355x_supports(const dyninfer_qweight_t* w, uint32_t rows, uint32_
     return 1;
 }
 
-int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws, uint32_t count,
-                                  const void* x, uint32_t x_dtype, uint32_t rows, void* const* ys, uint32_t y_dtype,
-                                  void* stream) {
+// qlinear_multi; noalloc takes the prefill workspace from the device's static
+// scratch array instead of a stream-ordered allocation.
+static int qlinear_multi_impl(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws, uint32_t count, const void* x,
+                              uint32_t x_dtype, uint32_t rows, void* const* ys, uint32_t y_dtype, void* stream,
+                              bool noalloc) {
     if (int rc = check_ctx(ctx)) return rc;
     if (!ws || count == 0 || count > (uint32_t)dmx::kMaxProblems)
         return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "count must be 1..4 with a weight array");
@@ -350,6 +367,12 @@ int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qwe
     if (gemm && (uint64_t)rows * ws[0].cols >= (1ull << 31))
         return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "prefill: rows * K must stay below 2^31 (32-bit activation offsets)");
     const uint64_t need = gemm ? dmx::prefill_workspace_bytes(rows, (uint32_t)ws[0].cols) : 0;
+    if (noalloc && need > kScratchBytes)
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
+                    "qlinear_multi_noalloc: the prefill staging of " + std::to_string(rows) + " rows x K " +
+                        std::to_string(ws[0].cols) + " needs " + std::to_string(need) +
+                        " bytes, more than the static scratch of " + std::to_string(kScratchBytes) +
+                        " bytes; split the rows or call dyninfer_mi355x_qlinear_multi");
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -357,15 +380,32 @@ int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qwe
     if (gemm) {
         Workspace wk;
         wk.st = st;
-        std::lock_guard<std::mutex> lock(ctx->mu);
-        e = acquire_workspace(ctx, st, need, wk);
-        if (e != hipSuccess) return hip_fail(e, "hipMallocAsync (prefill staging workspace)");
-        e = prefill(ws, count, x, x_dtype, rows, ys, y_dtype, wk.p, st);
+        if (noalloc) {
+            wk.p = ctx->scratch;
+            e = prefill(ws, count, x, x_dtype, rows, ys, y_dtype, wk.p, st);
+        } else {
+            std::lock_guard<std::mutex> lock(ctx->mu);
+            e = acquire_workspace(ctx, st, need, wk);
+            if (e != hipSuccess) return hip_fail(e, "hipMallocAsync (prefill staging workspace)");
+            e = prefill(ws, count, x, x_dtype, rows, ys, y_dtype, wk.p, st);
+        }
     } else {
         e = gemv_rows(ws, count, x, x_dtype, rows, ys, y_dtype, st);
     }
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws, uint32_t count,
+                                  const void* x, uint32_t x_dtype, uint32_t rows, void* const* ys, uint32_t y_dtype,
+                                  void* stream) {
+    return qlinear_multi_impl(ctx, ws, count, x, x_dtype, rows, ys, y_dtype, stream, false);
+}
+
+int dyninfer_mi355x_qlinear_multi_noalloc(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws, uint32_t count,
+                                          const void* x, uint32_t x_dtype, uint32_t rows, void* const* ys,
+                                          uint32_t y_dtype, void* stream) {
+    return qlinear_multi_impl(ctx, ws, count, x, x_dtype, rows, ys, y_dtype, stream, true);
 }
 
 int dyninfer_mi355x_qlinear(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* w, const void* x, uint32_t x_dtype,

@@ -125,7 +125,7 @@ const char* dyninfer_mi355x_last_error(void);
  *     releases them at dyninfer_mi355x_close.  Under stream capture the call uses no
  *     context workspace (a later regrowth could free it while the graph names it): it
  *     allocates and frees a transient one in stream order, which the captured graph
- *     then does on every replay.
+ *     then does on every replay (the no-allocation variant below avoids that).
  *     A stream that is destroyed while the context lives must have finished its work
  *     first (its handle may be reused by a new stream).  Encodings without a prefill
  *     GEMM run the GEMV kernels over 16-row chunks instead and need no workspace.
@@ -148,6 +148,26 @@ int dyninfer_mi355x_qlinear(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t
 int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws,
                                   uint32_t count, const void* x, uint32_t x_dtype, uint32_t rows,
                                   void* const* ys, uint32_t y_dtype, void* stream);
+
+/*
+ * No counterpart in the reference.  For callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops or harnesses that forbid hipMalloc):
+ * dyninfer_mi355x_qlinear_multi with the prefill staging workspace (rows >= 17 on a
+ * weight with a prefill GEMM: round_up(rows*K*2, 256) + 4*round_up(rows, 256) bytes)
+ * taken from a static device array of DYNINFER_MI355X_NOALLOC_SCRATCH_BYTES per device
+ * (allocated when the library's code object loads on a device, held until the process
+ * ends) instead of a stream-ordered allocation.  A larger staging is rejected with
+ * DYNINFER_MI355X_ERR_UNSUPPORTED (2048 rows fit K <= 8160, 512 rows K <= 32736).
+ * Calls no hipMalloc/hipFree or allocating routine.  Every call on one device shares
+ * that device's array and leaves it holding the last staging: calls that overlap on
+ * one device (concurrent streams, or threads without ordering) race and may return
+ * wrong results; calls ordered on one stream are safe.  Decode calls (rows <= 16) use
+ * no scratch and are identical to dyninfer_mi355x_qlinear_multi.
+ */
+#define DYNINFER_MI355X_NOALLOC_SCRATCH_BYTES (32u << 20)
+int dyninfer_mi355x_qlinear_multi_noalloc(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws,
+                                          uint32_t count, const void* x, uint32_t x_dtype, uint32_t rows,
+                                          void* const* ys, uint32_t y_dtype, void* stream);
 
 /*
  * Dequantise W to f32 [N, K] on the device, bit-exactly as the reference's

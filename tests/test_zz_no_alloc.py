@@ -1,0 +1,74 @@
+"""dyninfer_mi355x_qlinear_multi_noalloc against dyninfer_mi355x_qlinear_multi,
+through the C ABI: the same kernels with the prefill staging taken from the
+device's static scratch array instead of a stream-ordered allocation, so the
+outputs must be bit-identical, and both within the f16 bound of the oracle.
+Two prefill calls in a row (the second smaller, over the first call's
+leftover staging), a decode call, and a staging beyond the scratch size
+(rejected host-side, after which calls still work)."""
+import numpy as np
+import pytest
+import torch
+
+import dyninfer_amd as d
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+F16X2 = 2.0 ** -10 + 2e-5
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def _weights(k, shapes, seed):
+    datas = [oracle.synth_gguf(oracle.Q4_0, n, k, seed + i) for i, n in enumerate(shapes)]
+    return [d.QWeight(d.ENC_Q4_0, n, k, dev(x)) for n, x in zip(shapes, datas)], datas
+
+
+def _both(ctx, ws, x):
+    ref = ctx.qlinear_multi(ws, x)
+    outs = [torch.full_like(r, float("nan")) for r in ref]
+    ctx.qlinear_multi(ws, x, outs, noalloc=True)
+    torch.cuda.synchronize()
+    return [r.cpu().numpy() for r in ref], [o.cpu().numpy() for o in outs]
+
+
+def test_noalloc_matches_qlinear_multi_on_consecutive_calls(ctx):
+    k, shapes = 1024, [512, 256, 256]
+    ws, datas = _weights(k, shapes, seed=3)
+    for rows, xbf16 in ((512, False), (100, True)):  # the second call smaller than the first
+        x = oracle.randn(rows * k, seed=rows).reshape(rows, k)
+        if xbf16:
+            xb = oracle.f32_to_bf16_bits(x.reshape(-1)).reshape(rows, k)
+            xd, x = dev(xb).view(torch.bfloat16), oracle.bf16_bits_to_f32(xb).reshape(rows, k)
+        else:
+            xd = dev(x)
+        ref, got = _both(ctx, ws, xd)
+        for r, g, data, n in zip(ref, got, datas, shapes):
+            assert np.array_equal(r.view(np.uint32), g.view(np.uint32)), (rows, n)
+            y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(oracle.Q4_0, data, n, k))
+            assert oracle.normalized_error(g, y64, absdot) <= F16X2
+
+
+def test_noalloc_decode_and_size_limit(ctx):
+    k = 1024
+    ws, _ = _weights(k, [384], seed=9)
+    x = dev(oracle.randn(8 * k, seed=1).reshape(8, k))
+    ref, got = _both(ctx, ws, x)
+    assert np.array_equal(ref[0].view(np.uint32), got[0].view(np.uint32))
+    # 2048 rows x K 8192: a staging of 32 MiB + 8 KiB, beyond the scratch array
+    kb = 8192
+    wb, _ = _weights(kb, [64], seed=11)
+    xb = torch.zeros((2048, kb), dtype=torch.float32, device="cuda")
+    yb = [torch.empty((2048, 64), dtype=torch.float32, device="cuda")]
+    with pytest.raises(d.DyninferError) as e:
+        ctx.qlinear_multi(wb, xb, yb, noalloc=True)
+    assert e.value.code == d.ERR_UNSUPPORTED and "static scratch" in e.value.message
+    # the largest staging that fits (2048 rows x K 8160) runs, and calls keep working
+    wf, dataf = _weights(8160, [64], seed=12)
+    xf = oracle.randn(2048 * 8160, seed=2).reshape(2048, 8160)
+    ref, got = _both(ctx, wf, dev(xf))
+    assert np.array_equal(ref[0].view(np.uint32), got[0].view(np.uint32))
+    ref, got = _both(ctx, ws, x)
+    assert np.array_equal(ref[0].view(np.uint32), got[0].view(np.uint32))
