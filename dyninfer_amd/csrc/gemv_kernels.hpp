@@ -860,8 +860,15 @@ hipError_t launch_oneshot(KERNEL k512, KERNEL k256, GemvParams p, size_t lds, hi
 // Activations are f32 (the reference's precision contract for quantized
 // linears, crates/dyninfer-compiler/src/lib.rs:289-306) or bf16 (XBF16).
 template <class E, bool XBF16>
+hipError_t launch_gguf_gemv_stream(GemvParams p, size_t lds, hipStream_t st);  // gemv_stream.hpp
+
+template <class E, bool XBF16>
 hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot, hipStream_t st) {
     const size_t lds = (size_t)xtile_bytes(E::ENC, B, p.K);
+    if (B == 1 && !oneshot) {  // long stream of one activation row: the streaming kernel where it fits
+        const hipError_t e = launch_gguf_gemv_stream<E, XBF16>(p, lds, st);
+        if (e != hipErrorNotSupported) return e;
+    }
     if (oneshot) {
         // chunks per lane (the host's limits): 1..4 for one activation row
         // (Q6_K 1..2), 1..2 for 2 rows, 1 for 4
@@ -915,9 +922,6 @@ hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot,
     return launch_persistent_best(t, n, p, lds, (nch + (1u << p.lanes_log2) - 1u) >> p.lanes_log2, st);
 }
 
-template <class E>
-hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st) {
-    return xbf16 ? launch_gguf_gemv_x<E, true>(p, B, oneshot, st) : launch_gguf_gemv_x<E, false>(p, B, oneshot, st);
-}
+
 
 }  // namespace dmx

@@ -1,5 +1,5 @@
 // Decode GEMV instantiations for GGUF Q6_K (kernel templates in gemv_kernels.hpp).
-#include "gemv_kernels.hpp"
+#include "gemv_stream.hpp"
 
 namespace dmx {
 hipError_t gemv_launch_q6_k(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st) {

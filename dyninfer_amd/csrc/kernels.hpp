@@ -38,6 +38,9 @@ struct GemvParams {
     // (wave_end[nprob-1] = all waves launched), each a contiguous run of the
     // problem's row blocks.
     uint32_t wave_end[kMaxProblems];
+    // Streaming kernel: row steps per wave whose row sums the LDS holds until
+    // the wave's stream ends (the busiest wave's count).
+    uint32_t res_steps;
 };
 
 // Bytes of the GEMV activation tile in LDS per (activation row, chunk): the
