@@ -201,9 +201,13 @@ dmx::GemvProblem problem_of(const dyninfer_qweight_t* w, void* y) {
 
 size_t esize(uint32_t dt) { return dt == DYNINFER_DTYPE_F32 ? 4 : 2; }
 
-// Whether rows >= 17 of this encoding run the prefill GEMM (else GEMV chunks).
+// Whether `rows` activation rows run the prefill GEMM (else the GEMV kernels
+// over 16-row chunks).  Q4_0's 16-row GEMV runs on MFMA, and two or three of
+// its chunks take less time than staging plus a GEMM launch below 48 rows;
+// Q4_1 and Q8_0 take the GEMM from 17 rows.
 bool has_prefill_gemm(uint32_t enc, uint32_t N, uint32_t K, uint32_t rows) {
-    return enc == DYNINFER_ENC_GGUF_Q4_0 && dmx::gemm_q4_0_supported(N, K, rows);
+    const uint32_t min_rows = enc == DYNINFER_ENC_GGUF_Q4_0 ? 48u : (uint32_t)dmx::kMaxGemvBatch + 1u;
+    return rows >= min_rows && dmx::gemm_supported(enc, N, K, rows);
 }
 
 // Device memory of one prefill call.  Normally the context's workspace for the
@@ -259,10 +263,11 @@ hipError_t prefill(const dyninfer_qweight_t* ws, uint32_t count, const void* x, 
     const uint32_t K = (uint32_t)ws[0].cols;
     uint16_t* xh = reinterpret_cast<uint16_t*>(work);
     float* rs = reinterpret_cast<float*>(work + dmx::prefill_xh_bytes(rows, K));
-    hipError_t e = dmx::xprep_launch(x, x_dtype == DYNINFER_DTYPE_BF16, rows, K, dmx::XPERM_PAIR2, xh, rs, st);
+    const uint32_t enc = ws[0].encoding;
+    hipError_t e = dmx::xprep_launch(x, x_dtype == DYNINFER_DTYPE_BF16, rows, K, dmx::gemm_layout(enc), xh, rs, st);
     for (uint32_t i = 0; i < count && e == hipSuccess; i++)
-        e = dmx::gemm_q4_0_launch(static_cast<const uint8_t*>(ws[i].data), (uint32_t)ws[i].rows, K, xh, rs, rows,
-                                  ys[i], y_dtype == DYNINFER_DTYPE_BF16, st);
+        e = dmx::gemm_launch(enc, static_cast<const uint8_t*>(ws[i].data), (uint32_t)ws[i].rows, K, xh, rs, rows, ys[i],
+                             y_dtype == DYNINFER_DTYPE_BF16, st);
     return e;
 }
 
@@ -361,7 +366,7 @@ static int qlinear_multi_impl(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight
     }
     if (int rc = check_io(x_dtype, y_dtype, rows)) return rc;
     if (!aligned(x, 16)) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "activations must be 16-byte aligned");
-    bool gemm = rows > (uint32_t)dmx::kMaxGemvBatch;
+    bool gemm = true;
     for (uint32_t i = 0; i < count && gemm; i++)
         gemm = has_prefill_gemm(ws[i].encoding, (uint32_t)ws[i].rows, (uint32_t)ws[i].cols, rows);
     if (gemm && (uint64_t)rows * ws[0].cols >= (1ull << 31))

@@ -1,0 +1,571 @@
+// Prefill GEMM on gfx950 MFMA for the GGUF block encodings Q4_0, Q4_1 and
+// Q8_0: Y[M, N] = X[M, K] · Wᵀ with f32 accumulation.
+//
+// Reference semantics: the same `emit_linear` contraction as decode
+// (gguf_codegen.rs:268-314, dequantisations :412-472 Q4_0, :382-410 Q8_0,
+// q4.rs Q4_1) with rows = the prefill window/chunk (512 when paged,
+// parameter.rs:107-121, dense_decoder.rs:53-56).
+//
+// Data path.  W is read as GGUF blocks straight from HBM (no repack); X
+// arrives staged by xprep.hip as f16 fragments of the MFMA operand, each row
+// scaled by a power of two that rs[m] undoes.
+//   * A workgroup of four waves owns a (32·TM) x (64·4/S) tile of Y: each
+//     wave a (32·TM) x 64 tile (TM x 2 blocks of v_mfma_f32_32x32x16_f16),
+//     the four waves split over S slices of K and 4/S column subtiles.
+//   * K advances in chunks of two weight blocks (64 k, four MFMA k steps)
+//     through an LDS ring of R chunks, one barrier per chunk.  Each chunk's
+//     activation fragments (1 KiB each, contiguous in HBM) are copied by
+//     global_load_lds_dwordx4 once per slice and read by every wave of the
+//     slice; each wave's 64 weight rows are copied the same way into a window
+//     per wave: the row's two blocks from their 4-byte-aligned start, as
+//     16-byte pieces (consecutive lanes on consecutive pieces, the last piece
+//     moved back so that no read passes the blocks' last dword).  Copies run
+//     R - 1 chunks ahead and hold no registers.
+//   * Every lane decodes one whole block straight into B operands: lane l
+//     takes weight row l % 32 of a 32-row block and block h = l / 32 of the
+//     chunk, so an MFMA k step pairs 8 k of the chunk's first block (lanes
+//     0..31) with 8 k of its second (lanes 32..63), and xprep stages the
+//     activations in that order.  A code at mantissa bits 0.. under the f16
+//     exponent of 1024 is 1024 + c, one at bits 4.. under that of 64 is
+//     64 + c (one v_and_or_b32 per two codes, both exact); a packed add removes
+//     the offset (exact) and a packed multiply by the block scale rounds once
+//     (Q4_0 RNE_f16((q-8)·d), Q8_0 RNE_f16(q·d)); Q4_1 a packed fma,
+//     RNE_f16(q·d + m).
+//   * The weights are the MFMA's A operand and the activations its B, so each
+//     lane ends with 4 consecutive output columns of one row per block and
+//     stores them as one 16-byte (f32) or 8-byte (bf16) write.  K slices meet
+//     in LDS after the loop, summed in slice order by one wave per output
+//     (deterministic), then scaled by rs[m].
+//   * Workgroups that read the same weight rows run on the same XCD
+//     (workgroup i goes to XCD i % 8).
+// Accuracy: |y - y_exact| <= 2^-10·Σ|w||x| (one f16 rounding of each weight and
+// of each activation) + f32 accumulation error, inside the 2e-3 normalised
+// tolerance.  Weights must be finite in f16 (|w| <= 65504, e.g. |d| <= 8188
+// for Q4_0).
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace dmx {
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWaves = 4;
+constexpr uint32_t kLdsMax = 160u * 1024u;
+
+struct GemmArgs {
+    const uint8_t* w;
+    const uint16_t* xh;
+    const float* rs;
+    void* y;
+    uint64_t rowbytes;
+    uint32_t M, N, K;
+    uint32_t mt, nt;  // workgroup tiles along M and N
+    uint32_t y_bf16;
+};
+
+// (a & m) | b as one v_and_or_b32 (mask in a scalar register: a VOP3 op takes
+// no literal operand on gfx9).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t b) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(b));
+    return r;
+}
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ uint32_t as_u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ h8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return __builtin_bit_cast(h8, u32x4{a, b, c, d});
+}
+
+// 16 bytes per lane from global memory into LDS at dst + 16·lane (dst
+// wave-uniform): global_load_lds_dwordx4, counted by vmcnt.
+__device__ __forceinline__ void dma16(const void* src, void* dst) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n), other counters unconstrained.
+template <uint32_t n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((n & 15u) | ((n >> 4) << 14) | (7u << 4) | (15u << 8));
+}
+
+// The ring's step barrier: this wave's copies older than its last n have
+// landed in LDS and its LDS reads are done (s_waitcnt vmcnt(n) lgkmcnt(0)),
+// then s_barrier.  __syncthreads() would also wait for the copies still in
+// flight (its fence waits for vmcnt(0)); the empty asm statements keep the
+// compiler from moving memory accesses across the barrier.
+template <uint32_t n>
+__device__ __forceinline__ void ring_barrier() {
+    static_assert(n < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((n & 15u) | ((n >> 4) << 14) | (7u << 4));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// ring_barrier<k·PER>() for a wave-uniform k in [0, KMAX]: the copies of the
+// k newest chunks may stay in flight.
+template <uint32_t PER, uint32_t KMAX>
+__device__ __forceinline__ void ring_barrier_k(uint32_t k) {
+    if constexpr (KMAX == 0) {
+        ring_barrier<0>();
+    } else {
+        if (k >= KMAX) ring_barrier<KMAX * PER>();
+        else ring_barrier_k<PER, KMAX - 1>(k);
+    }
+}
+
+// Per-encoding block geometry and decode.  A lane reads kDw dwords from the
+// 4-byte-aligned dword holding its block's first byte (sh = the block start's
+// offset in that dword, 0 or 2); scale() takes the block's f16 scale(s) from
+// them and step(t) decodes the MFMA operand of the chunk's k step t: 8 k of
+// the block, as 4 packed f16 pairs.
+template <uint32_t ENC>
+struct Blk;
+
+template <>
+struct Blk<ENC_Q4_0> {
+    // d (2 B) then 16 code bytes; byte j: k = j (low nibble), k = j + 16 (high).
+    // Step t: code bytes 4t..4t+3 -> k = 4t+(0,2), 4t+(1,3), 16+4t+(0,2), 16+4t+(1,3).
+    static constexpr uint32_t kBytes = 18, kDw = 5, kLayout = XFRAG_NIB;
+    struct Scale {
+        h2 d;
+        uint32_t sel;
+    };
+    __device__ static Scale scale(const uint32_t* r, uint32_t sh) {
+        return {as_h2(__builtin_amdgcn_perm(r[0], r[0], 0x01000100u + 0x01010101u * sh)),
+                0x05040302u + 0x01010101u * sh};  // block bytes 2+4t..5+4t from dwords t, t+1
+    }
+    __device__ static h8 step(const uint32_t* r, const Scale& s, int t) {
+        const h2 ol = {(_Float16)-1032.0f, (_Float16)-1032.0f}, oh = {(_Float16)-72.0f, (_Float16)-72.0f};
+        const uint32_t ml = 0x64006400u, mh = 0x54005400u;
+        auto lo = [&](uint32_t v) { return as_u((as_h2(and_or(v, 0x000F000Fu, ml)) + ol) * s.d); };
+        auto hi = [&](uint32_t v) { return as_u((as_h2(and_or(v, 0x00F000F0u, mh)) + oh) * s.d); };
+        const uint32_t q = __builtin_amdgcn_perm(r[t + 1], r[t], s.sel), q8 = q >> 8;
+        return as_h8(lo(q), lo(q8), hi(q), hi(q8));
+    }
+};
+
+template <>
+struct Blk<ENC_Q4_1> {
+    // d, m (2 B each) then 16 code bytes (4-byte-aligned blocks): w = q·d + m;
+    // k order as Q4_0.
+    static constexpr uint32_t kBytes = 20, kDw = 5, kLayout = XFRAG_NIB;
+    struct Scale {
+        h2 d, m;
+    };
+    __device__ static Scale scale(const uint32_t* r, uint32_t) {
+        return {as_h2(__builtin_amdgcn_perm(r[0], r[0], 0x01000100u)),
+                as_h2(__builtin_amdgcn_perm(r[0], r[0], 0x03020302u))};
+    }
+    __device__ static h8 step(const uint32_t* r, const Scale& s, int t) {
+        const h2 ol = {(_Float16)-1024.0f, (_Float16)-1024.0f}, oh = {(_Float16)-64.0f, (_Float16)-64.0f};
+        const uint32_t ml = 0x64006400u, mh = 0x54005400u;
+        auto lo = [&](uint32_t v) {
+            return as_u(__builtin_elementwise_fma(as_h2(and_or(v, 0x000F000Fu, ml)) + ol, s.d, s.m));
+        };
+        auto hi = [&](uint32_t v) {
+            return as_u(__builtin_elementwise_fma(as_h2(and_or(v, 0x00F000F0u, mh)) + oh, s.d, s.m));
+        };
+        const uint32_t q = r[t + 1], q8 = q >> 8;
+        return as_h8(lo(q), lo(q8), hi(q), hi(q8));
+    }
+};
+
+template <>
+struct Blk<ENC_Q8_0> {
+    // d (2 B) then 32 int8 codes; step t: codes 8t..8t+7 in the order
+    // (0,2) (1,3) (4,6) (5,7): a code c as (c ^ 0x80) under the exponent of 1024
+    // is 1152 + c.
+    static constexpr uint32_t kBytes = 34, kDw = 9, kLayout = XFRAG_BYTE;
+    struct Scale {
+        h2 d;
+        uint32_t sel;
+    };
+    __device__ static Scale scale(const uint32_t* r, uint32_t sh) {
+        return {as_h2(__builtin_amdgcn_perm(r[0], r[0], 0x01000100u + 0x01010101u * sh)),
+                0x05040302u + 0x01010101u * sh};
+    }
+    __device__ static h8 step(const uint32_t* r, const Scale& s, int t) {
+        const h2 o = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+        const uint32_t ml = 0x64006400u;
+        auto p = [&](uint32_t v) { return as_u((as_h2(and_or(v, 0x00FF00FFu, ml)) + o) * s.d); };
+        const uint32_t c0 = __builtin_amdgcn_perm(r[2 * t + 1], r[2 * t], s.sel) ^ 0x80808080u;
+        const uint32_t c1 = __builtin_amdgcn_perm(r[2 * t + 2], r[2 * t + 1], s.sel) ^ 0x80808080u;
+        return as_h8(p(c0), p(c0 >> 8), p(c1), p(c1 >> 8));
+    }
+};
+
+// LDS geometry of one kernel configuration.
+template <uint32_t ENC, int TM, int S>
+struct Geo {
+    static constexpr uint32_t WN = kWaves / S;                        // column subtiles per workgroup
+    static constexpr uint32_t kSpanMax = (2u * Blk<ENC>::kBytes + 2u + 3u) & ~3u;  // a row's two blocks, aligned
+    static constexpr uint32_t NP = (kSpanMax + 15u) / 16u;             // 16-byte pieces per row window
+    static constexpr uint32_t kWinBytes = 64u * NP * 16u;              // a wave's 64-row window
+    static constexpr uint32_t kABytes = (uint32_t)S * 4u * TM * 1024u;  // activation fragments of a chunk
+    static constexpr uint32_t kSlot = kABytes + kWaves * kWinBytes;
+    static constexpr uint32_t kRs = 32u * TM * 4u;                      // the tile's row factors
+    static constexpr uint32_t kEpiPitch = 68u;                          // floats per output row in LDS
+    static constexpr uint32_t kEpi = (uint32_t)kWaves * 32u * TM * kEpiPitch * 4u;  // every wave's whole tile
+    static constexpr uint32_t kRoom = kLdsMax - kRs;
+    static constexpr uint32_t R = 4u * kSlot <= kRoom ? 4u : 3u * kSlot <= kRoom ? 3u : 2u;
+    static constexpr uint32_t kRing = R * kSlot > kEpi ? R * kSlot : kEpi;  // the epilogue reuses the ring
+    static constexpr uint32_t kLds = kRing + kRs;
+    static constexpr uint32_t kDmaA = 4u * TM / WN;  // activation copies per wave per chunk
+    static constexpr uint32_t kDma = kDmaA + NP;      // all copies per wave per chunk
+    static constexpr bool kFits = 2u * kSlot <= kRoom;
+    static_assert((4u * TM) % WN == 0, "activation fragments split evenly over the slice's waves");
+};
+
+template <uint32_t ENC, int TM, int S>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_kernel(const GemmArgs a) {
+    using B = Blk<ENC>;
+    using G = Geo<ENC, TM, S>;
+    constexpr uint32_t R = G::R, NP = G::NP;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t ks = wave % (uint32_t)S, ns = wave / (uint32_t)S;
+
+    // XCD-aware tile order: consecutive tile indices (tiles sharing N columns)
+    // on the workgroups that land on one XCD (workgroup i on XCD i % 8).
+    const uint32_t T = a.mt * a.nt;
+    const uint32_t q8 = T / 8u, r8 = T % 8u, xcd = blockIdx.x % 8u;
+    const uint32_t tau = (xcd < r8 ? xcd * (q8 + 1u) : r8 * (q8 + 1u) + (xcd - r8) * q8) + blockIdx.x / 8u;
+    const uint32_t mtile = tau % a.mt, ntile = tau / a.mt;
+    const uint32_t n0 = (ntile * G::WN + ns) * 64u;  // this wave's 64 columns
+    const uint32_t mb0 = mtile * TM;                 // first 32-row block
+    const uint32_t mbs = (a.M + 31u) / 32u;
+
+    // K slice: chunks [c0, c0 + nc) of two blocks; S divides the chunk count,
+    // so every wave runs the same steps and meets the same barriers
+    const uint32_t nchk = a.K / 64u, ksteps = a.K / 16u;
+    const uint32_t nc = nchk / S, c0 = nc * ks;
+
+    // Activation copies: this wave copies fragments f = ns, ns + WN, ... of its
+    // slice's 4·TM per chunk (f = 4·i + t: row block i, k step t).
+    const uint16_t* xsrc[G::kDmaA];
+    uint32_t xdst[G::kDmaA];
+#pragma unroll
+    for (uint32_t q = 0; q < G::kDmaA; q++) {
+        const uint32_t f = ns + q * G::WN, i = f / 4u, t = f % 4u;
+        const uint32_t mb = mb0 + i < mbs ? mb0 + i : mbs - 1u;  // past M: re-read the last block (never stored)
+        xsrc[q] = a.xh + (((size_t)mb * ksteps + 4u * c0 + t) * 64u + lane) * 8u;
+        xdst[q] = (ks * 4u * TM + f) * 1024u;
+    }
+    // Weight copies: piece p of row r of the window, for lane index 64·q + lane.
+    const uint8_t* wsrc[NP];
+#pragma unroll
+    for (uint32_t q = 0; q < NP; q++) {
+        const uint32_t li = 64u * q + lane, r = li / NP, p = li % NP;
+        const uint32_t n = n0 + r < a.N ? n0 + r : a.N - 1u;  // past N: re-read the last row (never stored)
+        const uintptr_t start = (uintptr_t)a.w + (uintptr_t)n * a.rowbytes + (uintptr_t)B::kBytes * 2u * c0;
+        const uintptr_t al = start & ~(uintptr_t)3;
+        const uint32_t span = (uint32_t)(((start + 2u * B::kBytes + 3u) & ~(uintptr_t)3) - al);
+        const uint32_t off = p + 1u < NP ? 16u * p : span - 16u;
+        wsrc[q] = reinterpret_cast<const uint8_t*>(al + off);
+    }
+    auto slot_a = [&](uint32_t slot) { return lds + slot * G::kSlot; };
+    auto slot_w = [&](uint32_t slot, uint32_t wv) { return lds + slot * G::kSlot + G::kABytes + wv * G::kWinBytes; };
+    auto issue = [&](uint32_t c, uint32_t slot) {  // chunk c of the slice (c < nc) into a ring slot
+#pragma unroll
+        for (uint32_t q = 0; q < G::kDmaA; q++) dma16(xsrc[q] + (size_t)c * 4u * 512u, slot_a(slot) + xdst[q]);
+#pragma unroll
+        for (uint32_t q = 0; q < NP; q++)
+            dma16(wsrc[q] + (size_t)c * 2u * B::kBytes, slot_w(slot, wave) + 64u * 16u * q);
+    };
+
+    // This lane's block in the window: row l % 32 of each 32-row block j, block
+    // h = l / 32 of the chunk; dword k of the block's aligned start at window
+    // offset wrd[j][k] (span bytes past the first NP - 1 pieces sit in the
+    // last piece, moved back by span - 16·NP).
+    const uint32_t h = lane >> 5;
+    uint32_t sh[2], wrd[2][B::kDw];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t r = 32u * j + (lane & 31u);
+        const uint32_t n = n0 + r < a.N ? n0 + r : a.N - 1u;
+        const uintptr_t start = (uintptr_t)a.w + (uintptr_t)n * a.rowbytes + (uintptr_t)B::kBytes * 2u * c0;
+        const uint32_t s0 = (uint32_t)(start & 3u);
+        const uint32_t span = (2u * B::kBytes + s0 + 3u) & ~3u;
+        const uint32_t bstart = s0 + B::kBytes * h;  // block h's first byte in the span
+        sh[j] = bstart & 3u;
+#pragma unroll
+        for (uint32_t k = 0; k < B::kDw; k++) {
+            const uint32_t o = (bstart & ~3u) + 4u * k;
+            wrd[j][k] = r * NP * 16u + (o < 16u * (NP - 1u) ? o : o - span + 16u * NP);
+        }
+    }
+
+    // Row factors of the tile's 32·TM rows, copied into LDS ahead of the ring
+    // (the oldest copy in flight, so the first ring wait covers it).
+    float* rs_lds = reinterpret_cast<float*>(lds + G::kRing);
+    if (wave == 0 && lane < 8u * TM) dma16(a.rs + (size_t)mb0 * 32u + 4u * lane, rs_lds);
+
+    f32x16 acc[TM][2];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    // Registers: the activation fragments of the chunk being multiplied (each
+    // refilled from the next chunk's slot once its MFMAs have issued), and the
+    // raw and decoded weights of the current and the next chunk.
+    h8 xa[TM][4];
+    uint32_t raw[B::kDw * 2];
+    h8 wf[2][2][4];
+    auto read_w = [&](uint32_t slot) {
+        const uint8_t* sw = slot_w(slot, wave);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (uint32_t k = 0; k < B::kDw; k++) raw[j * B::kDw + k] = *reinterpret_cast<const uint32_t*>(sw + wrd[j][k]);
+    };
+    auto read_a = [&](uint32_t slot, int t) {
+        const uint8_t* sa = slot_a(slot) + ks * 4u * TM * 1024u + lane * 16u;
+#pragma unroll
+        for (int i = 0; i < TM; i++) xa[i][t] = *reinterpret_cast<const h8*>(sa + (4u * i + t) * 1024u);
+    };
+    auto decode_all = [&](int p) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const typename B::Scale sc = B::scale(raw + j * B::kDw, sh[j]);
+#pragma unroll
+            for (int t = 0; t < 4; t++) wf[p][j][t] = B::step(raw + j * B::kDw, sc, t);
+        }
+    };
+
+    // One step of the pipeline, chunk c with weights wf[p]: barrier (chunk c + 1
+    // landed for every wave; every wave done reading chunk c), copy chunk c + R
+    // into chunk c's slot, read chunk c + 1's weights, then the MFMAs of chunk
+    // c in k-step order, each k step followed by the next chunk's activation
+    // reads of that step, with chunk c + 1's decode into wf[1 - p] spread
+    // between the MFMAs of k steps 1..3 (the MFMAs run in the matrix core while
+    // the decode issues).  Scheduling barriers keep the k steps in order.
+    // The last step reads a slot no chunk was copied into; its decode is
+    // never multiplied.
+    constexpr int kValuPerMfma = (int)(3u * 16u + 2u * TM - 1u) / (2 * TM);  // ~3 decode pieces of ~16 VALU per k step
+    auto step = [&](uint32_t c, int p) {
+        // copies issued so far: chunks up to min(c + R, nc) - 1; chunk c + 1 must
+        // have landed, the newer ones may stay in flight
+        const uint32_t last = c + R - 1u < nc - 1u ? c + R - 1u : nc - 1u;
+        ring_barrier_k<G::kDma, R - 2u>(last > c + 1u ? last - c - 1u : 0u);
+        const uint32_t cn = c + R;
+        if (cn < nc) issue(cn, c % R);
+        const uint32_t nxt = (c + 1u) % R;
+        read_w(nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        typename B::Scale sc[2];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+            for (int m = 0; m < 2 * TM; m++) {
+                const int i = m >> 1, j = m & 1;
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[p][j][t], xa[i][t], acc[i][j], 0, 0, 0);
+            }
+            if (t > 0) {
+                // decode pieces (weight block kj, k step kt) k = 3(t-1) .. (steps 1, 2, 3 take 3, 3, 2)
+#pragma unroll
+                for (int k = 3 * (t - 1); k < 3 * t && k < 8; k++) {
+                    const int kj = k >> 2, kt = k & 3;
+                    if (kt == 0) sc[kj] = B::scale(raw + kj * B::kDw, sh[kj]);
+                    wf[1 - p][kj][kt] = B::step(raw + kj * B::kDw, sc[kj], kt);
+                }
+            }
+            read_a(nxt, t);
+            // one MFMA, then a share of the decode VALU, ...; the step's
+            // activation reads after its last MFMA
+#pragma unroll
+            for (int m = 0; m < 2 * TM; m++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (t > 0) __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, TM, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+#pragma unroll
+    for (uint32_t c = 0; c < R; c++)
+        if (c < nc) issue(c, c);
+    ring_barrier_k<G::kDma, R - 1u>((nc < R ? nc : R) - 1u);  // chunk 0 landed for every wave
+    read_w(0);
+#pragma unroll
+    for (int t = 0; t < 4; t++) read_a(0, t);
+    decode_all(0);
+    uint32_t c = 0;
+    for (; c + 2u <= nc; c += 2u) {
+        step(c, 0);
+        step(c + 1u, 1);
+    }
+    if (c < nc) step(c, 0);
+    wait_vmcnt<0>();
+    __syncthreads();  // every wave past its last chunk: the ring is free
+
+    // Epilogue.  D = W-block x X-block: lane l holds activation row l % 32
+    // of the row block and, for r = 0..15, column 8·(r/4) + 4·(l/32) + r%4.
+    // Every wave writes its whole partial tile (32·TM rows x 64 columns, f32)
+    // to its LDS rows; then the S waves of a column subtile each take 32·TM/S
+    // of the rows, add the S partials in slice order (deterministic), scale by
+    // rs[m] and store whole rows, 16 lanes per 64-column row.  All LDS reads
+    // of a wave are issued before its first store.
+    float* epi = reinterpret_cast<float*>(lds);
+    {
+        float* mine = epi + wave * 32u * TM * G::kEpiPitch;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    *reinterpret_cast<f32x4*>(mine + (32u * i + (lane & 31u)) * G::kEpiPitch + 32u * j + 8u * q +
+                                              4u * (lane >> 5)) =
+                        f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+    }
+    if constexpr (S > 1) __syncthreads();
+    constexpr uint32_t RPT = 32u * TM / S, NI = RPT / 4u;  // rows per wave, store instructions per wave
+    f32x4 v[NI];
+#pragma unroll
+    for (uint32_t s4 = 0; s4 < NI; s4++) {
+        const uint32_t ml = ks * RPT + 4u * s4 + (lane >> 4), c4 = lane & 15u;
+        v[s4] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < S; k++)  // slice order, the same for every output
+            v[s4] += *reinterpret_cast<const f32x4*>(epi + ((ns * S + k) * 32u * TM + ml) * G::kEpiPitch + 4u * c4);
+        v[s4] *= rs_lds[ml];
+    }
+    const uint32_t mrow0 = mb0 * 32u + ks * RPT + (lane >> 4), ncol = n0 + 4u * (lane & 15u);
+    const bool vec_ok = (a.N & 3u) == 0 && ((uintptr_t)a.y & (a.y_bf16 ? 7u : 15u)) == 0;
+    if (vec_ok && mb0 * 32u + ks * RPT + RPT <= a.M && n0 + 64u <= a.N) {  // whole rows in range: no per-lane tests
+#pragma unroll
+        for (uint32_t s4 = 0; s4 < NI; s4++) {
+            const size_t idx = (size_t)(mrow0 + 4u * s4) * a.N + ncol;
+            if (a.y_bf16) {
+                const uint32_t lo = (uint32_t)f32_to_bf16_bits(v[s4][0]) | ((uint32_t)f32_to_bf16_bits(v[s4][1]) << 16);
+                const uint32_t hi = (uint32_t)f32_to_bf16_bits(v[s4][2]) | ((uint32_t)f32_to_bf16_bits(v[s4][3]) << 16);
+                *gptr_mut<u32x2>(static_cast<uint16_t*>(a.y) + idx) = u32x2{lo, hi};
+            } else {
+                *gptr_mut<f32x4>(static_cast<float*>(a.y) + idx) = v[s4];
+            }
+        }
+    } else {
+#pragma unroll
+        for (uint32_t s4 = 0; s4 < NI; s4++) {
+            const uint32_t m = mrow0 + 4u * s4;
+            if (m >= a.M) continue;
+            const size_t idx = (size_t)m * a.N + ncol;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (ncol + (uint32_t)e >= a.N) break;
+                if (a.y_bf16) gptr_mut<uint16_t>(a.y)[idx + e] = f32_to_bf16_bits(v[s4][e]);
+                else gptr_mut<float>(a.y)[idx + e] = v[s4][e];
+            }
+        }
+    }
+}
+
+template <uint32_t ENC, int TM, int S>
+hipError_t launch(const GemmArgs& a, hipStream_t st) {
+    static_assert(Geo<ENC, TM, S>::kFits, "LDS of one workgroup");
+    auto kernel = gemm_kernel<ENC, TM, S>;
+    constexpr uint32_t lds = Geo<ENC, TM, S>::kLds;
+    if constexpr (lds > 64u * 1024u) {
+        static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (attr != hipSuccess) return attr;
+    }
+    hipLaunchKernelGGL(kernel, dim3(a.mt * a.nt), dim3(kWaves * 64), lds, st, a);
+    return hipGetLastError();
+}
+
+template <uint32_t ENC, int TM>
+hipError_t launch_s(GemmArgs a, int S, hipStream_t st) {
+    a.mt = ((a.M + 31u) / 32u + TM - 1u) / TM;
+    a.nt = (a.N + 64u * (kWaves / S) - 1u) / (64u * (kWaves / S));
+    if constexpr (Geo<ENC, TM, 4>::kFits)
+        if (S == 4) return launch<ENC, TM, 4>(a, st);
+    if (S >= 2) return launch<ENC, TM, 2>(a, st);
+    return launch<ENC, TM, 1>(a, st);
+}
+
+template <uint32_t ENC>
+hipError_t launch_enc(GemmArgs a, hipStream_t st) {
+    // Wave tile (TM row blocks) and K split (S slices per workgroup) from a
+    // cost model fitted to timing sweeps (M in {128, 512, 2048}, N in {1024,
+    // 3072, 12288}, K in {1024, 3072, 4096}), in units of about 0.1 us:
+    // rounds of 256 workgroups (one per CU) x (chunks per slice x time per
+    // chunk + start-up and stores), where a chunk takes ~2·TM + 4 and the
+    // four-slice ring, only two chunks deep, ~4 more.  TM = 4 only when M
+    // fills more than 64 rows; S divides the chunk count (the slices, and so
+    // the waves' ring barriers, are equal in number) and leaves >= 2 chunks
+    // per slice.
+    const uint32_t mb = (a.M + 31u) / 32u;
+    const uint32_t nchk = a.K / 64u;
+    int best_tm = 2, best_s = 1;
+    uint64_t best_cost = ~0ull;
+    for (int TM : {4, 2}) {  // ties keep the larger tile
+        if (TM == 4 && mb <= 2u) continue;
+        const uint64_t mt = (mb + TM - 1u) / TM;
+        for (int S : {1, 2, 4}) {
+            // equal slices: every wave of a workgroup passes the same barriers
+            if (S > 1 && (nchk % S != 0 || nchk < 2u * S)) continue;
+            if (S == 4 && !(TM == 2 ? Geo<ENC, 2, 4>::kFits : Geo<ENC, 4, 4>::kFits)) continue;
+            const uint64_t nt = (a.N + 64u * (kWaves / S) - 1u) / (64u * (kWaves / S));
+            const uint64_t rounds = (mt * nt + 255u) / 256u;
+            const uint64_t cost = rounds * ((nchk / S) * (2u * TM + 4u + (S == 4 ? 4u : 0u)) + 24u);
+            if (cost < best_cost) best_cost = cost, best_tm = TM, best_s = S;
+        }
+    }
+    if (best_tm == 2) return launch_s<ENC, 2>(a, best_s, st);
+    return launch_s<ENC, 4>(a, best_s, st);
+}
+
+}  // namespace
+
+uint32_t gemm_layout(uint32_t enc) {
+    switch (enc) {
+        case ENC_Q4_0: return Blk<ENC_Q4_0>::kLayout;
+        case ENC_Q4_1: return Blk<ENC_Q4_1>::kLayout;
+        case ENC_Q8_0: return Blk<ENC_Q8_0>::kLayout;
+        default: return ~0u;
+    }
+}
+
+bool gemm_supported(uint32_t enc, uint32_t N, uint32_t K, uint32_t M) {
+    return gemm_layout(enc) != ~0u && N > 0 && M > 0 && K >= 64u && K % 64u == 0;
+}
+
+hipError_t gemm_launch(uint32_t enc, const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs,
+                       uint32_t M, void* y, bool y_bf16, hipStream_t st) {
+    if (!gemm_supported(enc, N, K, M)) return hipErrorInvalidValue;
+    GemmArgs a{};
+    a.w = w;
+    a.xh = xh;
+    a.rs = rs;
+    a.y = y;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.y_bf16 = y_bf16 ? 1u : 0u;
+    switch (enc) {
+        case ENC_Q4_0: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q4_0>::kBytes; return launch_enc<ENC_Q4_0>(a, st);
+        case ENC_Q4_1: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q4_1>::kBytes; return launch_enc<ENC_Q4_1>(a, st);
+        case ENC_Q8_0: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q8_0>::kBytes; return launch_enc<ENC_Q8_0>(a, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace dmx

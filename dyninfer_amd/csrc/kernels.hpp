@@ -95,35 +95,34 @@ hipError_t gather_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, cons
                          uint32_t K, uint32_t group, uint32_t sdtype, const int64_t* ids, uint32_t n_ids, float* out,
                          hipStream_t stream);
 
-// Prefill activations as the GEMMs read them (xprep.hip): xh [M, K] f16 =
-// RNE(x · 2^(15 - e_m)) with k permuted inside every group of 8, and the row
-// factors rs[m] = 2^(e_m - 15) the GEMM epilogues multiply by.
-enum XPerm : uint32_t {
-    XPERM_PAIR2 = 0,  // 0,2,1,3,4,6,5,7: GGUF codes (bytes j and j+2 of a dword decode together)
-    XPERM_PAIR4 = 1,  // 0,4,1,5,2,6,3,7: MLX U4 (nibbles i and i+4 of a word)
+// Prefill activations staged for the MFMA GEMM (xprep.hip): f16 operand
+// fragments of v_mfma_f32_32x32x16_f16, row m scaled by 2^(15 - e_m) (rs[m] =
+// 2^(e_m - 15) undoes it), k ordered inside every 64-k chunk as the GEMM's
+// weight decode produces the weights; rows padded with zeros to a multiple of
+// 32.  Lane half h of k step 4c + t holds 8 k of k = 64c + 32h + (0..31):
+enum XFrag : uint32_t {
+    XFRAG_NIB = 2,   // Q4_0, Q4_1: 4t, 4t+2, 4t+1, 4t+3, 16+4t, 18+4t, 17+4t, 19+4t
+    XFRAG_BYTE = 3,  // Q8_0:       8t + (0, 2, 1, 3, 4, 6, 5, 7)
 };
-hipError_t xprep_launch(const void* x, bool x_bf16, uint32_t M, uint32_t K, uint32_t perm, uint16_t* xh, float* rs,
+hipError_t xprep_launch(const void* x, bool x_bf16, uint32_t M, uint32_t K, uint32_t layout, uint16_t* xh, float* rs,
                         hipStream_t stream);
 
-// Device workspace of one prefill GEMM call: xh (M·K f16) then rs (f32 for M
-// rows rounded up to 256, so epilogues may read whole row groups past M).
-inline uint64_t prefill_xh_bytes(uint32_t M, uint32_t K) { return ((uint64_t)M * K * 2u + 255u) & ~(uint64_t)255u; }
+// Device workspace of one prefill GEMM call: xh (M rounded up to 32 rows of K
+// f16) then rs (f32 for M rows rounded up to 256, so epilogues may read whole
+// row groups past M).
+inline uint64_t prefill_xh_bytes(uint32_t M, uint32_t K) {
+    return (((uint64_t)M + 31u) / 32u * 32u * K * 2u + 255u) & ~(uint64_t)255u;
+}
 inline uint64_t prefill_workspace_bytes(uint32_t M, uint32_t K) {
     return prefill_xh_bytes(M, K) + (((uint64_t)M + 255u) & ~(uint64_t)255u) * 4u;
 }
 
-// Q4_0 prefill GEMM on MFMA: Y[M, N] = diag(rs) · (Xh[M, K] · Wᵀ), Xh/rs from
-// xprep_launch(XPERM_PAIR2); Y f32 or bf16.
-hipError_t gemm_q4_0_launch(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs,
-                            uint32_t M, void* y, bool y_bf16, hipStream_t stream);
-
-// Shape limits of the GEMM kernel (checked by the C ABI before launching).
-bool gemm_q4_0_supported(uint32_t N, uint32_t K, uint32_t M);
-
-// The K-split GEMM (K a multiple of 256): each wave of a workgroup multiplies
-// a quarter of K for the whole tile; gemm_q4_0_launch routes to it.
-bool gemm_q4_0_ks_supported(uint32_t N, uint32_t K, uint32_t M);
-hipError_t gemm_q4_0_ks_launch(const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs,
-                               uint32_t M, void* y, bool y_bf16, hipStream_t stream);
+// Prefill GEMM on MFMA (gemm.hip): Y[M, N] = diag(rs) · (Xh[M, K] · Wᵀ), Xh/rs
+// from xprep_launch(gemm_layout(enc)); Y f32 or bf16.  gemm_layout returns ~0u
+// for encodings without a GEMM.
+uint32_t gemm_layout(uint32_t enc);
+bool gemm_supported(uint32_t enc, uint32_t N, uint32_t K, uint32_t M);
+hipError_t gemm_launch(uint32_t enc, const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs,
+                       uint32_t M, void* y, bool y_bf16, hipStream_t stream);
 
 }  // namespace dmx

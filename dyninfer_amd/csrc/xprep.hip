@@ -1,7 +1,7 @@
-// Prefill activation staging for the MFMA GEMMs: X [M, K] (f32 or bf16) to
-// f16 once per call, in the k order the GEMMs' weight decode produces.
+// Prefill activation staging for the MFMA GEMM: X [M, K] (f32 or bf16) to f16
+// once per call, laid out as the GEMM's MFMA operands.
 //
-//   xh[m, :] = RNE_f16(x[m, :] · 2^(15 - e_m)),   rs[m] = 2^(e_m - 15),
+//   xh value of (m, k) = RNE_f16(x[m, k] · 2^(15 - e_m)),   rs[m] = 2^(e_m - 15),
 //
 // e_m the binary exponent of the row's largest magnitude (max |x| < 2^e_m),
 // so every scaled value is below 2^15 (no f16 overflow) and the row's large
@@ -9,20 +9,29 @@
 // two); the one rounding is RNE to f16, relative 2^-11 for scaled magnitudes
 // in f16's normal range.  A value more than 2^29 below its row's largest
 // lands among f16's subnormals (absolute error <= 2^-25 scaled, i.e.
-// 2^-40·max|x| per activation).  The GEMMs accumulate x_h·w in f32 and
-// multiply the tile by rs[m] in the epilogue.
+// 2^-40·max|x| per activation).  The GEMM accumulates x_h·w in f32 and
+// multiplies each output row by rs[m].
 //
-// k order inside every group of 8 (the permutation is applied identically to
-// the weights' LDS tiles, so products pair up as in natural order):
-//   XPERM_PAIR2: 0, 2, 1, 3, 4, 6, 5, 7   one v_and_or_b32 decodes bytes j and
-//                j+2 of a dword (GGUF Q4_0/Q4_1/Q8_0 codes, Q6_K ql/qh);
-//   XPERM_PAIR4: 0, 4, 1, 5, 2, 6, 3, 7   nibbles i and i+4 of an MLX u32 word.
+// Layout: fragments of a v_mfma_f32_32x32x16_f16 operand, 1 KiB each:
+//   fragment (mb, ks) = rows 32·mb .. 32·mb+31, k step ks (16 k), at element
+//   offset ((mb·K/16 + ks)·64 + lane)·8; lane l holds row 32·mb + l % 32 and
+//   8 k for lane half h = l / 32.
+// The GEMM advances K in chunks of 64 (k steps 4c .. 4c+3), lane half h
+// decoding the chunk's weight block h, so half h of step 4c+t holds 8 k of
+// k = 64c + 32h .. 64c + 32h + 31, in the order the block's decode produces:
+//   XFRAG_NIB  (Q4_0, Q4_1: code byte j holds k = j and k = j + 16):
+//              4t, 4t+2, 4t+1, 4t+3, 16+4t, 18+4t, 17+4t, 19+4t
+//   XFRAG_BYTE (Q8_0: one code byte per k):
+//              8t, 8t+2, 8t+1, 8t+3, 8t+4, 8t+6, 8t+5, 8t+7
+// (pairs (j, j+2) of a dword decode together).  Rows M .. roundup(M, 32) - 1
+// are written as zeros, so the GEMM reads whole fragments.
 //
 // Mapping: one wave per row (4 rows per 256-thread workgroup); lane l takes
-// the 8-element groups l, l+64, ...  Rows with K <= 2048 keep their values in
-// registers between the max pass and the conversion pass; longer rows reload
-// them (cache hits).  NaN and inf: the row's scale is taken as 2^15 and the
-// non-finite values propagate to the row's outputs.
+// the 8-element output slots l, l+64, ... (slot 8c + 2t + h: chunk c, step t,
+// half h).  Rows with K <= 8192 keep their values in registers between the
+// max pass and the conversion pass; longer rows reload them (cache hits).
+// NaN and inf: the row's scale is taken as 2^15 and the non-finite values
+// propagate to the row's outputs.
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -36,18 +45,30 @@ typedef float xf4 __attribute__((ext_vector_type(4)));
 
 constexpr int kXprepWaves = 4;
 
-template <bool XBF16>
-__device__ __forceinline__ void load8(const void* x, size_t off, float (&v)[8]) {
+// The 8 activations of output slot `slot` of a row: two runs of 4 k, at
+// k0 and k0 + RUN2 (NIB: 16, BYTE: 4).
+template <uint32_t LAYOUT>
+__device__ __forceinline__ uint32_t slot_k0(uint32_t slot) {
+    const uint32_t c = slot >> 3, t = (slot >> 1) & 3u, h = slot & 1u;
+    return 64u * c + 32u * h + (LAYOUT == XFRAG_NIB ? 4u * t : 8u * t);
+}
+template <bool XBF16, uint32_t LAYOUT>
+__device__ __forceinline__ void load8(const void* x, size_t row, uint32_t slot, float (&v)[8]) {
+    constexpr uint32_t RUN2 = LAYOUT == XFRAG_NIB ? 16u : 4u;
+    const size_t k0 = row + slot_k0<LAYOUT>(slot);
     if constexpr (XBF16) {
-        const u32x4_a4 q = *gptr<u32x4_a4>(static_cast<const uint16_t*>(x) + off);
+        typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+        const u32x2_a4 p = *gptr<u32x2_a4>(static_cast<const uint16_t*>(x) + k0);
+        const u32x2_a4 q = *gptr<u32x2_a4>(static_cast<const uint16_t*>(x) + k0 + RUN2);
+        const uint32_t w[4] = {p.x, p.y, q.x, q.y};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            v[2 * i] = __uint_as_float(q[i] << 16);
-            v[2 * i + 1] = __uint_as_float(q[i] & 0xFFFF0000u);
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
         }
     } else {
-        const xf4 a = *gptr<xf4>(static_cast<const float*>(x) + off);
-        const xf4 b = *gptr<xf4>(static_cast<const float*>(x) + off + 4);
+        const xf4 a = *gptr<xf4>(static_cast<const float*>(x) + k0);
+        const xf4 b = *gptr<xf4>(static_cast<const float*>(x) + k0 + RUN2);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             v[i] = a[i];
@@ -70,16 +91,16 @@ __device__ __forceinline__ uint32_t pk(float a, float b, int sh) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, xh2));  // RNE
 }
 
-template <uint32_t PERM>
+// Element offset in xh of row m's output slot (chunk c, step t, half h).
+__device__ __forceinline__ size_t frag_offset(uint32_t m, uint32_t slot, uint32_t ksteps) {
+    const uint32_t c = slot >> 3, t = (slot >> 1) & 3u, h = slot & 1u;
+    return (((size_t)(m >> 5) * ksteps + 4u * c + t) * 64u + (m & 31u) + 32u * h) * 8u;
+}
+
+// Both layouts pair (v0, v2), (v1, v3), (v4, v6), (v5, v7).
 __device__ __forceinline__ void store8(uint16_t* xh, size_t off, const float (&v)[8], int sh) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    u32x4 o;
-    if constexpr (PERM == XPERM_PAIR2) {
-        o = u32x4{pk(v[0], v[2], sh), pk(v[1], v[3], sh), pk(v[4], v[6], sh), pk(v[5], v[7], sh)};
-    } else {
-        o = u32x4{pk(v[0], v[4], sh), pk(v[1], v[5], sh), pk(v[2], v[6], sh), pk(v[3], v[7], sh)};
-    }
-    *gptr_mut<u32x4>(xh + off) = o;
+    *gptr_mut<u32x4>(xh + off) = u32x4{pk(v[0], v[2], sh), pk(v[1], v[3], sh), pk(v[4], v[6], sh), pk(v[5], v[7], sh)};
 }
 
 // Maximum over the wave (unsigned), every lane receiving it.
@@ -92,14 +113,21 @@ __device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
     return v;
 }
 
-// NR > 0: up to NR groups per lane held in registers (K <= 512·NR); NR = 0: reload.
-template <bool XBF16, uint32_t PERM, int NR>
-__global__ __launch_bounds__(kXprepWaves * 64) void xprep_kernel(const void* __restrict__ x, uint32_t M, uint32_t K,
-                                                                  uint16_t* __restrict__ xh, float* __restrict__ rs) {
+// NR > 0: up to NR slots per lane held in registers (K <= 512·NR); NR = 0: reload.
+template <bool XBF16, uint32_t LAYOUT, int NR>
+__global__ __launch_bounds__(kXprepWaves * 64) void xprep_kernel(const void* __restrict__ x, uint32_t M, uint32_t Mp,
+                                                                  uint32_t K, uint16_t* __restrict__ xh,
+                                                                  float* __restrict__ rs) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t m = blockIdx.x * (uint32_t)kXprepWaves + (threadIdx.x >> 6);
-    if (m >= M) return;
-    const uint32_t groups = K / 8u;
+    if (m >= Mp) return;
+    const uint32_t slots = K / 8u, ksteps = K / 16u;
+    if (m >= M) {  // padding row: zeros
+        const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (uint32_t g = lane; g < slots; g += 64u) store8(xh, frag_offset(m, g, ksteps), z, 0);
+        if (lane == 0) gptr_mut<float>(rs)[m] = 0.0f;
+        return;
+    }
     const size_t row = (size_t)m * K;
     uint32_t mx = 0;
     float v[NR > 0 ? NR : 1][8];
@@ -107,15 +135,15 @@ __global__ __launch_bounds__(kXprepWaves * 64) void xprep_kernel(const void* __r
 #pragma unroll
         for (int i = 0; i < NR; i++) {
             const uint32_t g = lane + 64u * (uint32_t)i;
-            if (g < groups) {
-                load8<XBF16>(x, row + 8u * g, v[i]);
+            if (g < slots) {
+                load8<XBF16, LAYOUT>(x, row, g, v[i]);
                 mx = absbits_max8(v[i], mx);
             }
         }
     } else {
-        for (uint32_t g = lane; g < groups; g += 64u) {
+        for (uint32_t g = lane; g < slots; g += 64u) {
             float t[8];
-            load8<XBF16>(x, row + 8u * g, t);
+            load8<XBF16, LAYOUT>(x, row, g, t);
             mx = absbits_max8(t, mx);
         }
     }
@@ -130,39 +158,47 @@ __global__ __launch_bounds__(kXprepWaves * 64) void xprep_kernel(const void* __r
 #pragma unroll
         for (int i = 0; i < NR; i++) {
             const uint32_t g = lane + 64u * (uint32_t)i;
-            if (g < groups) store8<PERM>(xh, row + 8u * g, v[i], sh);
+            if (g < slots) store8(xh, frag_offset(m, g, ksteps), v[i], sh);
         }
     } else {
-        for (uint32_t g = lane; g < groups; g += 64u) {
+        for (uint32_t g = lane; g < slots; g += 64u) {
             float t[8];
-            load8<XBF16>(x, row + 8u * g, t);
-            store8<PERM>(xh, row + 8u * g, t, sh);
+            load8<XBF16, LAYOUT>(x, row, g, t);
+            store8(xh, frag_offset(m, g, ksteps), t, sh);
         }
     }
     if (lane == 0) gptr_mut<float>(rs)[m] = ldexpf(1.0f, e - 15);
 }
 
-template <bool XBF16, uint32_t PERM>
+template <bool XBF16, uint32_t LAYOUT>
 hipError_t launch_xprep(const void* x, uint32_t M, uint32_t K, uint16_t* xh, float* rs, hipStream_t st) {
-    const dim3 grid((M + kXprepWaves - 1) / kXprepWaves), block(kXprepWaves * 64);
-    const uint32_t groups = K / 8u;
-    if (groups <= 64u) hipLaunchKernelGGL((xprep_kernel<XBF16, PERM, 1>), grid, block, 0, st, x, M, K, xh, rs);
-    else if (groups <= 128u) hipLaunchKernelGGL((xprep_kernel<XBF16, PERM, 2>), grid, block, 0, st, x, M, K, xh, rs);
-    else if (groups <= 256u) hipLaunchKernelGGL((xprep_kernel<XBF16, PERM, 4>), grid, block, 0, st, x, M, K, xh, rs);
-    else hipLaunchKernelGGL((xprep_kernel<XBF16, PERM, 0>), grid, block, 0, st, x, M, K, xh, rs);
+    const uint32_t Mp = (M + 31u) & ~31u;
+    const dim3 grid((Mp + kXprepWaves - 1) / kXprepWaves), block(kXprepWaves * 64);
+    const uint32_t slots = K / 8u;
+    if (slots <= 64u) hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 1>), grid, block, 0, st, x, M, Mp, K, xh, rs);
+    else if (slots <= 128u) hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 2>), grid, block, 0, st, x, M, Mp, K, xh, rs);
+    else if (slots <= 256u) hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 4>), grid, block, 0, st, x, M, Mp, K, xh, rs);
+    else if (slots <= 512u) hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 8>), grid, block, 0, st, x, M, Mp, K, xh, rs);
+    else if (slots <= 1024u) hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 16>), grid, block, 0, st, x, M, Mp, K, xh, rs);
+    else hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 0>), grid, block, 0, st, x, M, Mp, K, xh, rs);
     return hipGetLastError();
+}
+
+template <uint32_t LAYOUT>
+hipError_t launch_xprep(const void* x, bool x_bf16, uint32_t M, uint32_t K, uint16_t* xh, float* rs, hipStream_t st) {
+    return x_bf16 ? launch_xprep<true, LAYOUT>(x, M, K, xh, rs, st) : launch_xprep<false, LAYOUT>(x, M, K, xh, rs, st);
 }
 
 }  // namespace
 
-hipError_t xprep_launch(const void* x, bool x_bf16, uint32_t M, uint32_t K, uint32_t perm, uint16_t* xh, float* rs,
+hipError_t xprep_launch(const void* x, bool x_bf16, uint32_t M, uint32_t K, uint32_t layout, uint16_t* xh, float* rs,
                         hipStream_t st) {
-    if (M == 0 || K == 0 || K % 8u || (perm != XPERM_PAIR2 && perm != XPERM_PAIR4)) return hipErrorInvalidValue;
-    if (perm == XPERM_PAIR2)
-        return x_bf16 ? launch_xprep<true, XPERM_PAIR2>(x, M, K, xh, rs, st)
-                      : launch_xprep<false, XPERM_PAIR2>(x, M, K, xh, rs, st);
-    return x_bf16 ? launch_xprep<true, XPERM_PAIR4>(x, M, K, xh, rs, st)
-                  : launch_xprep<false, XPERM_PAIR4>(x, M, K, xh, rs, st);
+    if (M == 0 || K == 0 || K % 64u) return hipErrorInvalidValue;
+    switch (layout) {
+        case XFRAG_NIB: return launch_xprep<XFRAG_NIB>(x, x_bf16, M, K, xh, rs, st);
+        case XFRAG_BYTE: return launch_xprep<XFRAG_BYTE>(x, x_bf16, M, K, xh, rs, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace dmx

@@ -20,8 +20,8 @@
  *   - weights, activations and outputs are caller-owned device memory; the library
  *     never repacks or copies weights and derives no parameters from them
  *     (README.md:5-9, crates/dyninfer-compiler/src/lib.rs:630); its one device
- *     allocation is the prefill staging workspace of qlinear with rows >= 17 (see
- *     there), owned by the context;
+ *     allocation is the prefill staging workspace of a prefill GEMM call (see
+ *     dyninfer_mi355x_qlinear), owned by the context;
  *   - work is enqueued asynchronously on the caller's HIP stream (`stream` is a
  *     hipStream_t passed as void*; NULL = the null stream); concurrent calls on
  *     distinct streams are allowed; there is no CPU fallback (README.md:83-84).
@@ -117,9 +117,13 @@ const char* dyninfer_mi355x_last_error(void);
  *   rows <= 16: the decode GEMV kernels (HBM-bound; 5..16 rows of large Q4_0, Q6_K and
  *     MLX weights on MFMA), activations rounded to f16 after a power-of-two scaling per
  *     scale group;
- *   rows >= 17: the prefill path.  x is staged once per call as f16 rows scaled by a
- *     power of two per row (RNE), then a dequant-to-LDS + MFMA GEMM per weight.  The
- *     staging needs a device workspace of about rows*K*2 bytes.  The context keeps one
+ *   rows >= 17: the prefill path.  Q4_1 and Q8_0 from 17 rows, Q4_0 from 48 rows
+ *     (below that its 16-row MFMA GEMV chunks are faster), K a multiple of 64: x is
+ *     staged once per call as f16 MFMA operand fragments, each row scaled by a power of
+ *     two (RNE) and the rows padded with zeros to a multiple of 32; then one MFMA GEMM
+ *     per weight decodes the GGUF blocks straight into MFMA operands.  The staging
+ *     needs a device workspace of round_up(round_up(rows, 32)*K*2, 256) +
+ *     4*round_up(rows, 256) bytes.  The context keeps one
  *     per stream handle, allocated on first use and grown in stream order
  *     (hipMallocAsync; the old one hipFreeAsync'd behind the work that used it), and
  *     releases them at dyninfer_mi355x_close.  Under stream capture the call uses no
@@ -127,8 +131,9 @@ const char* dyninfer_mi355x_last_error(void);
  *     allocates and frees a transient one in stream order, which the captured graph
  *     then does on every replay (the no-allocation variant below avoids that).
  *     A stream that is destroyed while the context lives must have finished its work
- *     first (its handle may be reused by a new stream).  Encodings without a prefill
- *     GEMM run the GEMV kernels over 16-row chunks instead and need no workspace.
+ *     first (its handle may be reused by a new stream).  Every other case (Q6_K, MLX
+ *     U4, K not a multiple of 64, Q4_0 below 48 rows) runs the GEMV kernels over 16-row
+ *     chunks and needs no workspace.
  * Error bound: |y - y_exact| <= 2^-10 * sum_k |w||x| plus f32 accumulation, where a
  * prefill activation more than 2^29 below its row's largest magnitude may also be
  * flushed to f16 subnormals (absolute 2^-40 * max|x| each).
@@ -152,12 +157,12 @@ int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qwe
 /*
  * No counterpart in the reference.  For callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops or harnesses that forbid hipMalloc):
- * dyninfer_mi355x_qlinear_multi with the prefill staging workspace (rows >= 17 on a
- * weight with a prefill GEMM: round_up(rows*K*2, 256) + 4*round_up(rows, 256) bytes)
+ * dyninfer_mi355x_qlinear_multi with the prefill staging workspace (a call that runs the
+ * prefill GEMM: round_up(round_up(rows, 32)*K*2, 256) + 4*round_up(rows, 256) bytes)
  * taken from a static device array of DYNINFER_MI355X_NOALLOC_SCRATCH_BYTES per device
  * (allocated when the library's code object loads on a device, held until the process
  * ends) instead of a stream-ordered allocation.  A larger staging is rejected with
- * DYNINFER_MI355X_ERR_UNSUPPORTED (2048 rows fit K <= 8160, 512 rows K <= 32736).
+ * DYNINFER_MI355X_ERR_UNSUPPORTED (2048 rows fit K <= 8128, 512 rows K <= 32704).
  * Calls no hipMalloc/hipFree or allocating routine.  Every call on one device shares
  * that device's array and leaves it holding the last staging: calls that overlap on
  * one device (concurrent streams, or threads without ordering) race and may return

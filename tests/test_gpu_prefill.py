@@ -2,10 +2,11 @@
 decode, through the C ABI, against the CPU oracle:
 
   * prefill (rows >= 17) with f32 and bf16 activations for every encoding,
-    through qlinear and qlinear_multi: Q4_0 runs the staged-activation MFMA
-    GEMM (x rounded once to f16 after a power-of-two scaling per row), the
-    other encodings the GEMV kernels over 16-row chunks (the chunks' x and y
-    pointer arithmetic is what the 17/32/200/512 row counts check);
+    through qlinear and qlinear_multi: Q4_0, Q4_1 and Q8_0 run the
+    staged-activation MFMA GEMM (x rounded once to f16 after a power-of-two
+    scaling per row), Q6_K and MLX the GEMV kernels over 16-row chunks (the
+    chunks' x and y pointer arithmetic is what the 17/32/200/512 row counts
+    check);
   * bf16 activations on the decode GEMV for every encoding;
   * grouped launches (q/k/v, gate/up) for every encoding at the Qwen3-0.6B
     shapes of BASELINE config 1, batches 1, 4 and 16;
@@ -235,7 +236,10 @@ def test_zero_point_rows(ctx, kind, rows):
     bound = 2.0 ** -8 * np.abs(x).sum(axis=1, keepdims=True) * dmax[None, :zr]
     print(f"zero-point residue / bound: {np.max(np.abs(y[:, :zr]) / bound):.3e}")
     assert np.all(np.abs(y[:, :zr]) <= bound)
-    exact = (kind == oracle.Q4_0 and rows > 16) or (rows >= 5 and rows <= 16 and kind in (oracle.Q4_0, oracle.Q6_K, MLX))
+    # the prefill GEMM (Q4_0, Q4_1, Q8_0 at 200 rows) and the MFMA GEMV (5..16 rows)
+    # multiply exact zeros
+    exact = (kind in (oracle.Q4_0, oracle.Q4_1, oracle.Q8_0) and rows >= 48) or \
+        (rows >= 5 and rows <= 16 and kind in (oracle.Q4_0, oracle.Q6_K, MLX))
     if exact:
         assert not np.any(y[:, :zr]), np.abs(y[:, :zr]).max()
 

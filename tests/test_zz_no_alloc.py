@@ -65,9 +65,10 @@ def test_noalloc_decode_and_size_limit(ctx):
     with pytest.raises(d.DyninferError) as e:
         ctx.qlinear_multi(wb, xb, yb, noalloc=True)
     assert e.value.code == d.ERR_UNSUPPORTED and "static scratch" in e.value.message
-    # the largest staging that fits (2048 rows x K 8160) runs, and calls keep working
-    wf, dataf = _weights(8160, [64], seed=12)
-    xf = oracle.randn(2048 * 8160, seed=2).reshape(2048, 8160)
+    # the largest staging that fits (2048 rows x K 8128, K a multiple of 64) runs,
+    # and calls keep working
+    wf, dataf = _weights(8128, [64], seed=12)
+    xf = oracle.randn(2048 * 8128, seed=2).reshape(2048, 8128)
     ref, got = _both(ctx, wf, dev(xf))
     assert np.array_equal(ref[0].view(np.uint32), got[0].view(np.uint32))
     ref, got = _both(ctx, ws, x)
