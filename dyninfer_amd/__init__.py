@@ -27,7 +27,7 @@ from typing import Optional, Sequence
 
 __all__ = [
     "LIB_PATH", "DyninferError", "QWeight", "Context", "library", "candidates", "registry_select",
-    "registry_require", "supports", "ENC_Q4_0", "ENC_Q4_1", "ENC_Q8_0", "ENC_Q6_K", "ENC_MLX_U4",
+    "registry_require", "precision_check", "supports", "ENC_Q4_0", "ENC_Q4_1", "ENC_Q8_0", "ENC_Q6_K", "ENC_MLX_U4",
     "DTYPE_F32", "DTYPE_F16", "DTYPE_BF16", "block_geometry", "weight_bytes", "ERR_INVALID_ARGUMENT",
     "ERR_UNSUPPORTED", "ERR_HIP", "ERR_DEVICE", "ERR_BUFFER_TOO_SMALL",
 ]
@@ -50,7 +50,7 @@ EXPORTED_SYMBOLS = (
     "dyninfer_mi355x_gguf_tensor_count", "dyninfer_mi355x_gguf_metadata_json", "dyninfer_mi355x_gguf_tensor",
     "dyninfer_mi355x_gguf_find", "dyninfer_mi355x_gguf_upload", "dyninfer_mi355x_gguf_qweight",
     "dyninfer_mi355x_candidates_json", "dyninfer_mi355x_registry_select", "dyninfer_mi355x_registry_require",
-    "dyninfer_mi355x_version", "dyninfer_mi355x_qlinear_multi_noalloc",
+    "dyninfer_mi355x_version", "dyninfer_mi355x_qlinear_multi_noalloc", "dyninfer_mi355x_precision_check",
 )
 
 
@@ -116,6 +116,7 @@ def library() -> ctypes.CDLL:
         "dyninfer_mi355x_registry_require": (I, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, P, SZ,
                                                  ctypes.POINTER(SZ)]),
         "dyninfer_mi355x_version": (ctypes.c_char_p, []),
+        "dyninfer_mi355x_precision_check": (I, [ctypes.c_char_p, ctypes.c_char_p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -327,6 +328,13 @@ def registry_select(request: dict, target: dict, cands=None) -> dict:
 def registry_require(request: dict, target: dict, cands=None) -> dict:
     """KernelRegistry::require -> SelectedKernelCandidate, or DyninferError(ERR_UNSUPPORTED, E_KERNEL_COVERAGE…)."""
     return _registry("dyninfer_mi355x_registry_require", request, target, cands)
+
+
+def precision_check(selected: dict, activation_type: str = "f32") -> None:
+    """The compiler's lower.precision gate (crates/dyninfer-compiler/src/lib.rs:289-306),
+    relaxed for bf16 activations on this library's lowerings; raises DyninferError
+    (ERR_UNSUPPORTED) when the selected kernel is not qualified."""
+    _check(library().dyninfer_mi355x_precision_check(json.dumps(selected).encode(), activation_type.encode()))
 
 
 @dataclass

@@ -593,4 +593,15 @@ int dyninfer_mi355x_registry_require(const char* candidates_json, const char* re
     return registry_call(candidates_json, request_json, target_json, out, out_cap, out_len, true);
 }
 
+int dyninfer_mi355x_precision_check(const char* selected_json, const char* activation_type) {
+    if (!selected_json) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "selected kernel JSON is NULL");
+    if (activation_type && std::strcmp(activation_type, "f32") != 0 && std::strcmp(activation_type, "bf16") != 0)
+        return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "activation_type must be \"f32\" or \"bf16\"");
+    std::string err;
+    const int rc = dmx::precision_check(selected_json, activation_type, err);
+    if (rc == 1) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, err);
+    if (rc == 2) return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, err);
+    return DYNINFER_MI355X_OK;
+}
+
 }  // extern "C"

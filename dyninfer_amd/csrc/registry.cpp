@@ -8,7 +8,10 @@
 //   rejection_reasons <- rejection_reasons (lib.rs:499-584)
 //   score             <- DeterministicCostModel::score (lib.rs:249-268)
 //   require error     <- KernelRegistry::require's E_KERNEL_COVERAGE (lib.rs:350-399)
+//   precision_check   <- the compiler's precision gate (crates/dyninfer-compiler/src/lib.rs:289-306),
+//                        relaxed for bf16-activation candidates of this library
 #include <algorithm>
+#include <cctype>
 #include <string>
 #include <vector>
 
@@ -27,9 +30,10 @@ Value strings(std::initializer_list<const char*> xs) {
     return a;
 }
 
-// One serde KernelCandidateDescriptor (lib.rs:132-149) for a gfx950 kernel.
+// One serde KernelCandidateDescriptor (lib.rs:132-149) for a gfx950 kernel;
+// `act` is its activation type (input and output), accumulation is f32.
 Value candidate(const std::string& codec, const char* op_kind, const char* op_suffix, long long block,
-                const std::string& notes) {
+                const std::string& notes, const char* act = "f32") {
     Value c = Value::object();
     const std::string id = codec + "." + op_suffix + ".mi355x_hip";
     c.set("id", Value::string(id));
@@ -38,8 +42,8 @@ Value candidate(const std::string& codec, const char* op_kind, const char* op_su
     enc.set("id", Value::string(codec));
     enc.set("version", Value::integer(1));
     c.set("encoding", enc);
-    c.set("input_types", strings({"f32"}));
-    c.set("output_types", strings({"f32"}));
+    c.set("input_types", strings({act}));
+    c.set("output_types", strings({act}));
     c.set("accumulator_types", strings({"f32"}));
     Value shape = Value::object();
     shape.set("logical_rank", Value::integer(2));
@@ -59,7 +63,9 @@ Value candidate(const std::string& codec, const char* op_kind, const char* op_su
     c.set("lowering", Value::string(id));
     // 400 > the IREE HIP entries' 300: both earn the +1000 exact-backend bonus
     // on driver "hip", so this entry wins on gfx950 and is rejected elsewhere.
-    c.set("deterministic_score", Value::integer(400));
+    // The bf16-activation entries score 390: a request that names no activation
+    // type (every request the reference makes) keeps selecting the f32 entry.
+    c.set("deterministic_score", Value::integer(std::string(act) == "f32" ? 400 : 390));
     c.set("readiness", Value::string("production"));
     c.set("notes", Value::string(notes));
     return c;
@@ -73,26 +79,31 @@ const std::string& candidates_json() {
         struct G { const char* codec; long long block; };
         const G gguf[] = {{"gguf.q4_0", 32}, {"gguf.q4_1", 32}, {"gguf.q8_0", 32}, {"gguf.q6_k", 256}};
         for (const G& g : gguf) {
+            const bool gemm = std::string(g.codec) != "gguf.q6_k";
             const std::string n = std::string("Consumes official GGML ") + g.codec +
                                   " interleaved blocks in place on gfx950: wave64 GEMV for 1-16 rows "
                                   "(in-register dequantisation, f32 accumulation)" +
-                                  (std::string(g.codec) == "gguf.q4_0"
-                                       ? "; prefill GEMM dequantises into LDS and feeds f16 MFMA"
-                                       : "") +
-                                  "; f32 or bf16 activations";
+                                  (gemm ? "; prefill GEMM decodes the blocks in registers straight into f16 MFMA "
+                                          "operands"
+                                        : "") +
+                                  "; activations rounded to f16 after a power-of-two scaling";
             all.push(candidate(g.codec, "embedding", "gather", g.block,
                                std::string("Gathers rows of official GGML ") + g.codec +
                                    " blocks in place on gfx950 and dequantises them to f32 (bit-exact)"));
-            all.push(candidate(g.codec, "linear", "matmul", g.block, n));
-            all.push(candidate(g.codec, "output_projection", "output", g.block, n));
+            all.push(candidate(g.codec, "linear", "matmul", g.block, n + "; f32 in/out"));
+            all.push(candidate(g.codec, "output_projection", "output", g.block, n + "; f32 in/out"));
+            all.push(candidate(g.codec, "linear", "matmul_bf16", g.block, n + "; bf16 in/out", "bf16"));
+            all.push(candidate(g.codec, "output_projection", "output_bf16", g.block, n + "; bf16 in/out", "bf16"));
         }
         const std::string mlx = "Direct MLX U4 words with groupwise scale/bias on gfx950 (group size a multiple "
-                                "of 32), dequantised in registers next to the contraction; f32 or bf16 activations";
+                                "of 32), dequantised in registers next to the contraction";
         all.push(candidate("mlx.affine.u4", "embedding", "embedding", 32,
                            "Gathers rows of MLX U4 words with groupwise scale/bias on gfx950 and dequantises them "
                            "to f32 (bit-exact)"));
-        all.push(candidate("mlx.affine.u4", "linear", "matmul", 32, mlx));
-        all.push(candidate("mlx.affine.u4", "output_projection", "output", 32, mlx));
+        all.push(candidate("mlx.affine.u4", "linear", "matmul", 32, mlx + "; f32 in/out"));
+        all.push(candidate("mlx.affine.u4", "output_projection", "output", 32, mlx + "; f32 in/out"));
+        all.push(candidate("mlx.affine.u4", "linear", "matmul_bf16", 32, mlx + "; bf16 in/out", "bf16"));
+        all.push(candidate("mlx.affine.u4", "output_projection", "output_bf16", 32, mlx + "; bf16 in/out", "bf16"));
         return json::dump(all);
     }();
     return s;
@@ -212,6 +223,16 @@ Value rejection_reasons(const Value& c, const Value& request, const Value& targe
     const Value& ot = need(c, "output_types", "candidate");
     const Value& at = need(c, "accumulator_types", "candidate");
     const std::string op = need(request, "operation", "request").as_str();
+    // Extension (no reference counterpart): a request may name the model's
+    // activation type; a linear or output candidate must then take it.
+    const Value* act = opt(request, "activation_type");
+    if (act && (op == "linear" || op == "output_projection") && !it.arr.empty() &&
+        it.arr[0].as_str() != act->as_str()) {
+        Value r = reason("activation_type_mismatch");
+        r.set("required", *act);
+        r.set("supported", it);
+        reasons.push(r);
+    }
     if (it.arr.empty() || ot.arr.empty() || at.arr.empty()) {
         reasons.push(reason("missing_type_choice"));
     } else if (precision_sensitive(op) && !contains(&at, sensitive_type(request))) {
@@ -309,6 +330,52 @@ int registry_select(const char* candidates, const char* request_json, const char
         report.set("rejected", rejected);
         out = json::dump(report);
         return 0;
+    } catch (const std::exception& e) {
+        err = e.what();
+        return 1;
+    }
+}
+
+namespace {
+
+// Rust Debug spelling of a serde ScalarType (crates/dyninfer-core/src/scalar.rs:9-23).
+std::string scalar_debug(const std::string& t) {
+    if (t == "bf16") return "Bf16";
+    if (t == "bool") return "Bool";
+    std::string d = t;
+    if (!d.empty()) d[0] = (char)std::toupper((unsigned char)d[0]);
+    return d;
+}
+
+}  // namespace
+
+int precision_check(const char* selected_json, const char* activation_type, std::string& err) {
+    try {
+        const Value sel = json::Parser(selected_json).parse();
+        const std::string in = need(sel, "input_type", "selected kernel").as_str();
+        const std::string out = need(sel, "output_type", "selected kernel").as_str();
+        const std::string act = need(sel, "activation_type", "selected kernel").as_str();
+        const std::string acc = need(sel, "accumulator_type", "selected kernel").as_str();
+        const Value& desc = need(sel, "descriptor", "selected kernel");
+        const std::string id = need(desc, "id", "descriptor").as_str();
+        const std::string lowering = need(desc, "lowering", "descriptor").as_str();
+        const std::string model_act = activation_type ? activation_type : "f32";
+        // lib.rs:289-306: an i64 input (token ids) or f32 throughout
+        if (in == "i64" || (in == "f32" && out == "f32" && act == "f32" && acc == "f32")) return 0;
+        // relaxed: bf16 activations in and out with f32 accumulation, for a model whose
+        // activations are bf16 and a lowering of this library (qualified for them)
+        const std::string suffix = ".mi355x_hip";
+        const bool ours = lowering.size() > suffix.size() &&
+                          lowering.compare(lowering.size() - suffix.size(), suffix.size(), suffix) == 0;
+        if (model_act == "bf16" && ours && in == "bf16" && out == "bf16" && act == "bf16" && acc == "f32") return 0;
+        err = "selected kernel `" + id + "` requires " + scalar_debug(in) + "/" + scalar_debug(out) + "/" +
+              scalar_debug(act) + "/" + scalar_debug(acc) +
+              (model_act == "bf16"
+                   ? ", but the shared lowering is qualified only for f32 compute, or bf16 activations with f32 "
+                     "accumulation on a .mi355x_hip lowering"
+                   : ", but the current shared lowering is qualified only for f32 compute") +
+              " (lower.precision)";
+        return 2;
     } catch (const std::exception& e) {
         err = e.what();
         return 1;

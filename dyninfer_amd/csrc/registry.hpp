@@ -13,4 +13,9 @@ const std::string& candidates_json();
 int registry_select(const char* candidates, const char* request_json, const char* target_json, bool require,
                     std::string& out, std::string& err);
 
+// The compiler's precision gate over a SelectedKernelCandidate, relaxed for
+// bf16 activations: 0 = accepted, 1 = malformed input, 2 = rejected (err =
+// the lower.precision message).
+int precision_check(const char* selected_json, const char* activation_type, std::string& err);
+
 }  // namespace dmx

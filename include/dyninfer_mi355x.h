@@ -277,6 +277,22 @@ int dyninfer_mi355x_registry_require(const char* candidates_json, const char* re
                                      const char* target_json, char* out, size_t out_cap,
                                      size_t* out_len);
 
+/*
+ * The compiler's precision gate for a selected lowering (crates/dyninfer-compiler/src/
+ * lib.rs:289-306), restated and relaxed for bf16 activations.  selected_json is a
+ * SelectedKernelCandidate (as registry_require writes); activation_type is the model's
+ * activation dtype, "f32" (NULL) or "bf16".  Accepted, as in the reference: an i64 input
+ * (embedding ids), or f32 input/output/activation/accumulator.  Also accepted when
+ * activation_type is "bf16": bf16 input/output/activation with f32 accumulation on a
+ * ".mi355x_hip" lowering (this library's kernels take and return bf16 activations).
+ * Anything else returns DYNINFER_MI355X_ERR_UNSUPPORTED with the reference's
+ * lower.precision message in last_error.
+ * Registry extension used with it: a KernelRequest may carry "activation_type"; linear and
+ * output_projection candidates whose first input type differs are then rejected with
+ * reason "activation_type_mismatch" (requests without the field select as the reference).
+ */
+int dyninfer_mi355x_precision_check(const char* selected_json, const char* activation_type);
+
 /* Library version string and the KernelRegistry::VERSION this registry expects ("6"). */
 const char* dyninfer_mi355x_version(void);
 

@@ -219,7 +219,7 @@ def test_candidates_match_the_serde_schema():
     keys = {"id", "operation", "encoding", "input_types", "output_types", "accumulator_types", "shape",
             "orientations", "target", "modes", "lowering", "deterministic_score", "readiness", "notes"}
     cands = d.candidates()
-    assert len(cands) == 15 and len({c["id"] for c in cands}) == 15
+    assert len(cands) == 25 and len({c["id"] for c in cands}) == 25
     for c in cands:
         assert set(c) == keys
         assert c["operation"] in ("embedding", "linear", "output_projection")
@@ -231,4 +231,78 @@ def test_candidates_match_the_serde_schema():
         assert c["encoding"]["version"] == 1
         assert c["shape"]["logical_rank"] == 2
         assert c["id"] == c["lowering"] and c["id"].endswith(".mi355x_hip")
+        assert c["accumulator_types"] == ["f32"]
+        bf16 = c["id"].split(".")[-2].endswith("_bf16")
+        assert c["input_types"] == c["output_types"] == (["bf16"] if bf16 else ["f32"])
+        assert c["deterministic_score"] == (390 if bf16 else 400)
     json.dumps(cands)
+
+
+# ---------------------------------------------------------------- bf16 activations (compiler precision gate)
+CODECS = [("gguf.q4_0", 32), ("gguf.q4_1", 32), ("gguf.q8_0", 32), ("gguf.q6_k", 256), ("mlx.affine.u4", 32)]
+
+
+@pytest.mark.parametrize("codec,block", CODECS)
+@pytest.mark.parametrize("op,suffix", [("linear", "matmul"), ("output_projection", "output")])
+def test_request_without_activation_type_selects_as_the_reference(codec, block, op, suffix):
+    """The bf16 entries score below the f32 ones, so the reference's own select
+    (which ignores activation types) keeps the f32 entry, and the reference's
+    all-f32 precision gate (lib.rs:289-306) accepts it."""
+    sel = d.registry_require(gguf_request(codec, 1024, 4 * block, op), hip("gfx950"), full_registry())
+    assert sel["descriptor"]["id"] == f"{codec}.{suffix}.mi355x_hip" and sel["input_type"] == "f32"
+    d.precision_check(sel)
+    d.precision_check(sel, "bf16")
+
+
+@pytest.mark.parametrize("codec,block", CODECS)
+@pytest.mark.parametrize("op,suffix", [("linear", "matmul_bf16"), ("output_projection", "output_bf16")])
+def test_bf16_activations_select_the_bf16_entry(codec, block, op, suffix):
+    req = dict(gguf_request(codec, 1024, 4 * block, op), activation_type="bf16")
+    sel = d.registry_require(req, hip("gfx950"), full_registry())
+    assert sel["descriptor"]["id"] == f"{codec}.{suffix}.mi355x_hip"
+    assert (sel["input_type"], sel["output_type"], sel["activation_type"], sel["accumulator_type"]) == \
+        ("bf16", "bf16", "bf16", "f32")
+    assert sel["score"] == 1390
+    # the f32-only gate of the reference rejects it; the relaxed gate accepts it
+    with pytest.raises(d.DyninferError) as e:
+        d.precision_check(sel)
+    assert e.value.code == d.ERR_UNSUPPORTED
+    assert f"selected kernel `{codec}.{suffix}.mi355x_hip` requires Bf16/Bf16/Bf16/F32" in e.value.message
+    assert "qualified only for f32 compute" in e.value.message
+    d.precision_check(sel, "bf16")
+    # the f32 entry is rejected for a bf16 request, with the extension's reason
+    rep = d.registry_select(req, hip("gfx950"), full_registry())
+    f32 = [r for r in rep["rejected"] if r["candidate_id"] == f"{codec}.{suffix.replace('_bf16', '')}.mi355x_hip"][0]
+    assert f32["reasons"] == [{"reason": "activation_type_mismatch", "required": "bf16", "supported": ["f32"]}]
+
+
+def test_activation_type_leaves_embeddings_alone_and_unknown_types_uncovered():
+    req = dict(gguf_request("gguf.q4_0", 151936, 1024, op="embedding"), activation_type="bf16")
+    assert d.registry_require(req, hip("gfx950"), full_registry())["descriptor"]["id"] == "gguf.q4_0.gather.mi355x_hip"
+    req = dict(gguf_request("gguf.q4_0", 1024, 1024), activation_type="f16")
+    with pytest.raises(d.DyninferError) as e:
+        d.registry_require(req, hip("gfx950"), d.candidates())
+    assert e.value.code == d.ERR_UNSUPPORTED and e.value.message.startswith("E_KERNEL_COVERAGE")
+
+
+def test_precision_gate_cases():
+    sel = d.registry_require(dict(gguf_request("gguf.q4_0", 64, 64), activation_type="bf16"), hip("gfx950"),
+                             d.candidates())
+    # a bf16 kernel that is not this library's (an IREE lowering) stays rejected
+    other = copy.deepcopy(sel)
+    other["descriptor"]["id"] = other["descriptor"]["lowering"] = "gguf.q4_0.matmul.iree_block_hip"
+    with pytest.raises(d.DyninferError):
+        d.precision_check(other, "bf16")
+    # bf16 accumulation stays rejected
+    acc = copy.deepcopy(sel)
+    acc["accumulator_type"] = "bf16"
+    with pytest.raises(d.DyninferError) as e:
+        d.precision_check(acc, "bf16")
+    assert "requires Bf16/Bf16/Bf16/Bf16" in e.value.message
+    # i64 inputs (token ids) pass, as in the reference
+    ids = copy.deepcopy(sel)
+    ids["input_type"] = "i64"
+    d.precision_check(ids)
+    with pytest.raises(d.DyninferError) as e:
+        d.precision_check(sel, "f16")
+    assert e.value.code == d.ERR_INVALID_ARGUMENT
