@@ -202,11 +202,12 @@ dmx::GemvProblem problem_of(const dyninfer_qweight_t* w, void* y) {
 size_t esize(uint32_t dt) { return dt == DYNINFER_DTYPE_F32 ? 4 : 2; }
 
 // Whether `rows` activation rows run the prefill GEMM (else the GEMV kernels
-// over 16-row chunks).  Q4_0's 16-row GEMV runs on MFMA, and two or three of
-// its chunks take less time than staging plus a GEMM launch below 48 rows;
-// Q4_1 and Q8_0 take the GEMM from 17 rows.
+// over 16-row chunks).  The 16-row GEMV of Q4_0 and Q6_K runs on MFMA, and
+// two or three of its chunks take less time than staging plus a GEMM launch
+// below 48 rows; Q4_1 and Q8_0 take the GEMM from 17 rows.
 bool has_prefill_gemm(uint32_t enc, uint32_t N, uint32_t K, uint32_t rows) {
-    const uint32_t min_rows = enc == DYNINFER_ENC_GGUF_Q4_0 ? 48u : (uint32_t)dmx::kMaxGemvBatch + 1u;
+    const bool mfma_gemv = enc == DYNINFER_ENC_GGUF_Q4_0 || enc == DYNINFER_ENC_GGUF_Q6_K;
+    const uint32_t min_rows = mfma_gemv ? 48u : (uint32_t)dmx::kMaxGemvBatch + 1u;
     return rows >= min_rows && dmx::gemm_supported(enc, N, K, rows);
 }
 

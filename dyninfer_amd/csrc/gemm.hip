@@ -1,9 +1,9 @@
-// Prefill GEMM on gfx950 MFMA for the GGUF block encodings Q4_0, Q4_1 and
-// Q8_0: Y[M, N] = X[M, K] · Wᵀ with f32 accumulation.
+// Prefill GEMM on gfx950 MFMA for the GGUF encodings Q4_0, Q4_1, Q8_0 and
+// Q6_K: Y[M, N] = X[M, K] · Wᵀ with f32 accumulation.
 //
 // Reference semantics: the same `emit_linear` contraction as decode
 // (gguf_codegen.rs:268-314, dequantisations :412-472 Q4_0, :382-410 Q8_0,
-// q4.rs Q4_1) with rows = the prefill window/chunk (512 when paged,
+// :474-526 Q6_K, q4.rs Q4_1) with rows = the prefill window/chunk (512 when paged,
 // parameter.rs:107-121, dense_decoder.rs:53-56).
 //
 // Data path.  W is read as GGUF blocks straight from HBM (no repack); X
@@ -30,7 +30,8 @@
 //     64 + c (one v_and_or_b32 per two codes, both exact); a packed add removes
 //     the offset (exact) and a packed multiply by the block scale rounds once
 //     (Q4_0 RNE_f16((q-8)·d), Q8_0 RNE_f16(q·d)); Q4_1 a packed fma,
-//     RNE_f16(q·d + m).
+//     RNE_f16(q·d + m); Q6_K RNE_f16((q-32)·RNE_f16(d·sc)) (its window and
+//     decode are described at WinQ6K).
 //   * The weights are the MFMA's A operand and the activations its B, so each
 //     lane ends with 4 consecutive output columns of one row per block and
 //     stores them as one 16-byte (f32) or 8-byte (bf16) write.  K slices meet
@@ -39,9 +40,10 @@
 //   * Workgroups that read the same weight rows run on the same XCD
 //     (workgroup i goes to XCD i % 8).
 // Accuracy: |y - y_exact| <= 2^-10·Σ|w||x| (one f16 rounding of each weight and
-// of each activation) + f32 accumulation error, inside the 2e-3 normalised
-// tolerance.  Weights must be finite in f16 (|w| <= 65504, e.g. |d| <= 8188
-// for Q4_0).
+// of each activation; Q6_K's weights round twice: (2^-10 + 2^-11)·Σ|w||x|) +
+// f32 accumulation error, inside the 2e-3 normalised tolerance.  Weights must
+// be finite in f16 (|w| <= 65504: |d| <= 8188 for Q4_0, |d·sc| <= 2047 for
+// Q6_K).
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -90,6 +92,12 @@ __device__ __forceinline__ void dma16(const void* src, void* dst) {
                                      (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
 }
 
+// 4 bytes per lane into LDS at dst + 4·lane: global_load_lds_dword.
+__device__ __forceinline__ void dma4(const void* src, void* dst) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
+}
+
 // s_waitcnt vmcnt(n), other counters unconstrained.
 template <uint32_t n>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -135,7 +143,7 @@ template <>
 struct Blk<ENC_Q4_0> {
     // d (2 B) then 16 code bytes; byte j: k = j (low nibble), k = j + 16 (high).
     // Step t: code bytes 4t..4t+3 -> k = 4t+(0,2), 4t+(1,3), 16+4t+(0,2), 16+4t+(1,3).
-    static constexpr uint32_t kBytes = 18, kDw = 5, kLayout = XFRAG_NIB;
+    static constexpr uint32_t kBytes = 18, kDw = 5, kLayout = XFRAG_NIB, kValuPerStep = 16;
     struct Scale {
         h2 d;
         uint32_t sel;
@@ -158,7 +166,7 @@ template <>
 struct Blk<ENC_Q4_1> {
     // d, m (2 B each) then 16 code bytes (4-byte-aligned blocks): w = q·d + m;
     // k order as Q4_0.
-    static constexpr uint32_t kBytes = 20, kDw = 5, kLayout = XFRAG_NIB;
+    static constexpr uint32_t kBytes = 20, kDw = 5, kLayout = XFRAG_NIB, kValuPerStep = 16;
     struct Scale {
         h2 d, m;
     };
@@ -185,7 +193,7 @@ struct Blk<ENC_Q8_0> {
     // d (2 B) then 32 int8 codes; step t: codes 8t..8t+7 in the order
     // (0,2) (1,3) (4,6) (5,7): a code c as (c ^ 0x80) under the exponent of 1024
     // is 1152 + c.
-    static constexpr uint32_t kBytes = 34, kDw = 9, kLayout = XFRAG_BYTE;
+    static constexpr uint32_t kBytes = 34, kDw = 9, kLayout = XFRAG_BYTE, kValuPerStep = 20;
     struct Scale {
         h2 d;
         uint32_t sel;
@@ -204,13 +212,207 @@ struct Blk<ENC_Q8_0> {
     }
 };
 
+// A wave's weight window: its 64 rows' bytes of one 64-k chunk, copied into
+// LDS, and each lane's reads and decode of its block.
+//
+// GGUF blocks of 32 weights: a row's two blocks of the chunk are contiguous;
+// they are copied from their 4-byte-aligned start as NP 16-byte pieces
+// (consecutive lanes on consecutive pieces of a row), the last piece moved
+// back so that no read passes the blocks' last dword.  Lane l decodes row
+// l % 32 of each 32-row half j, block h = l / 32 of the chunk.
+template <uint32_t ENC>
+struct WinBlocks {
+    using B = Blk<ENC>;
+    using Scale = typename B::Scale;
+    static constexpr uint32_t kSpanMax = (2u * B::kBytes + 2u + 3u) & ~3u;  // a row's two blocks, aligned
+    static constexpr uint32_t NP = (kSpanMax + 15u) / 16u;                   // 16-byte pieces per row
+    static constexpr uint32_t kCopies = NP;                                  // copy instructions per chunk
+    static constexpr uint32_t kBytes = 64u * NP * 16u;
+    static constexpr uint32_t kDw = B::kDw;
+    static constexpr uint32_t kValuPerStep = B::kValuPerStep;
+    const uint8_t* src[NP];       // copy lane's piece for the slice's first chunk
+    uint32_t off[2][kDw], sh[2];  // this lane's block dwords in the window, its block's start offset
+
+    __device__ void init(const GemmArgs& a, uint32_t n0, uint32_t lane, uint32_t c0) {
+#pragma unroll
+        for (uint32_t q = 0; q < NP; q++) {
+            const uint32_t li = 64u * q + lane, r = li / NP, p = li % NP;
+            const uint32_t n = n0 + r < a.N ? n0 + r : a.N - 1u;  // past N: re-read the last row (never stored)
+            const uintptr_t start = (uintptr_t)a.w + (uintptr_t)n * a.rowbytes + (uintptr_t)B::kBytes * 2u * c0;
+            const uintptr_t al = start & ~(uintptr_t)3;
+            const uint32_t span = (uint32_t)(((start + 2u * B::kBytes + 3u) & ~(uintptr_t)3) - al);
+            src[q] = reinterpret_cast<const uint8_t*>(al + (p + 1u < NP ? 16u * p : span - 16u));
+        }
+        // dword k of the lane's block (from its aligned start) at window offset
+        // off[j][k]: span bytes past the first NP - 1 pieces sit in the last
+        // piece, moved back by span - 16·NP
+        const uint32_t h = lane >> 5;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t r = 32u * j + (lane & 31u);
+            const uint32_t n = n0 + r < a.N ? n0 + r : a.N - 1u;
+            const uintptr_t start = (uintptr_t)a.w + (uintptr_t)n * a.rowbytes + (uintptr_t)B::kBytes * 2u * c0;
+            const uint32_t s0 = (uint32_t)(start & 3u);
+            const uint32_t span = (2u * B::kBytes + s0 + 3u) & ~3u;
+            const uint32_t bstart = s0 + B::kBytes * h;
+            sh[j] = bstart & 3u;
+#pragma unroll
+            for (uint32_t k = 0; k < kDw; k++) {
+                const uint32_t o = (bstart & ~3u) + 4u * k;
+                off[j][k] = r * NP * 16u + (o < 16u * (NP - 1u) ? o : o - span + 16u * NP);
+            }
+        }
+    }
+    __device__ void issue(uint32_t c, uint8_t* win) const {
+#pragma unroll
+        for (uint32_t q = 0; q < NP; q++) dma16(src[q] + (size_t)c * 2u * B::kBytes, win + 1024u * q);
+    }
+    __device__ void read(uint32_t, const uint8_t* win, uint32_t* raw) const {
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (uint32_t k = 0; k < kDw; k++) raw[j * kDw + k] = *reinterpret_cast<const uint32_t*>(win + off[j][k]);
+    }
+    __device__ Scale scale(uint32_t, int j, const uint32_t* r) const { return B::scale(r, sh[j]); }
+    __device__ h8 step(const uint32_t* r, const Scale& s, int t) const { return B::step(r, s, t); }
+};
+
+// GGUF Q6_K (super-blocks of 256 weights, 210 bytes: ql[128], qh[64], int8
+// scales[16], f16 d; gguf_codegen.rs:474-526).  Chunk g of a row covers
+// quarter q = g % 4 of super-block g / 4: weights 128·(q/2) + 64·(q%2) + 0..63,
+// lane half h the 32 of them with l = 0..31 at 128·(q/2) + 32·(2·(q%2) + h) + l,
+// whose 6-bit codes are the (q%2) nibble of ql[64·(q/2) + 32h + l] under bits
+// 2·(2·(q%2) + h) of qh[32·(q/2) + l], scaled by d·scales[8·(q/2) + 2·(2(q%2) + h)
+// + l/16].  The window per row: ql[64·(q/2) .. +64) and qh[32·(q/2) .. +32) as
+// six 16-byte pieces, then five dwords: the ql and qh dwords past those (a
+// super-block starting 2 bytes into its dword), the two scale dwords the
+// chunk's scales lie in, and the dword of d.  Every copy lies within the
+// super-block's dwords.  The codes' pairs (l, l+2) decode with one
+// v_and_or_b32 each for the nibble and one for the qh bits (moved under the
+// nibble), so an MFMA k step takes l = 8t .. 8t+7 in the order of Q8_0.
+struct WinQ6K {
+    static constexpr uint32_t kX16 = 6, kX4 = 5, kCopies = kX16 + kX4;
+    static constexpr uint32_t kPitch16 = 16u * kX16, kPitch4 = 4u * kX4;
+    static constexpr uint32_t kBytes = 64u * (kPitch16 + kPitch4);
+    static constexpr uint32_t kDw = 20;  // ql 9, qh 9, scale dword, d dword
+    static constexpr uint32_t kValuPerStep = 32;
+    struct Scale {
+        uint32_t sel, mN, magic, mH, sL;
+        h2 off, ds0, ds1;
+    };
+    uintptr_t rb16[kX16], rb4[kX4];  // row of each copy lane (its first super-block)
+    uint32_t p16[kX16], p4[kX4];     // piece of each copy lane
+    uintptr_t row[2];                // this lane's rows
+    uint32_t c0, h, lane;
+
+    __device__ void init(const GemmArgs& a, uint32_t n0, uint32_t lane_, uint32_t c0_) {
+        lane = lane_;
+        c0 = c0_;
+        h = lane >> 5;
+        auto rowp = [&](uint32_t r) {
+            const uint32_t n = n0 + r < a.N ? n0 + r : a.N - 1u;  // past N: re-read the last row (never stored)
+            return (uintptr_t)a.w + (uintptr_t)n * a.rowbytes;
+        };
+#pragma unroll
+        for (uint32_t q = 0; q < kX16; q++) {
+            const uint32_t li = 64u * q + lane;
+            rb16[q] = rowp(li / kX16);
+            p16[q] = li % kX16;
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < kX4; q++) {
+            const uint32_t li = 64u * q + lane;
+            rb4[q] = rowp(li / kX4);
+            p4[q] = li % kX4;
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) row[j] = rowp(32u * j + (lane & 31u));
+    }
+    __device__ void issue(uint32_t c, uint8_t* win) const {
+        const uint32_t g = c0 + c, sb = g >> 2, hn = (g >> 1) & 1u, ph = g & 1u;
+#pragma unroll
+        for (uint32_t q = 0; q < kX16; q++) {
+            const uintptr_t al = (rb16[q] + (uintptr_t)sb * 210u) & ~(uintptr_t)3;
+            const uint32_t p = p16[q];
+            const uint32_t o = p < 4u ? 64u * hn + 16u * p : 128u + 32u * hn + 16u * (p - 4u);
+            dma16(reinterpret_cast<const void*>(al + o), win + 1024u * q);
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < kX4; q++) {
+            const uintptr_t al = (rb4[q] + (uintptr_t)sb * 210u) & ~(uintptr_t)3;
+            const uint32_t p = p4[q];
+            const uint32_t o = p == 0u ? 64u * hn + 64u
+                             : p == 1u ? 160u + 32u * hn
+                             : p == 2u ? 192u + 8u * hn + 4u * ph
+                             : p == 3u ? 196u + 8u * hn + 4u * ph
+                                       : 208u;
+            dma4(reinterpret_cast<const void*>(al + o), win + 64u * kPitch16 + 256u * q);
+        }
+    }
+    __device__ uint32_t shift_of(uint32_t c, int j) const { return (uint32_t)((row[j] + (uintptr_t)((c0 + c) >> 2) * 210u) & 3u); }
+    __device__ void read(uint32_t c, const uint8_t* win, uint32_t* raw) const {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t r = 32u * j + (lane & 31u);
+            const uint8_t* w16 = win + r * kPitch16;
+            const uint8_t* w4 = win + 64u * kPitch16 + r * kPitch4;
+            uint32_t* o = raw + j * kDw;
+#pragma unroll
+            for (uint32_t k = 0; k < 9; k++) {
+                const uint32_t rel = 32u * h + 4u * k;  // ql dword k of the lane's 32 codes
+                o[k] = *reinterpret_cast<const uint32_t*>(rel < 64u ? w16 + rel : w4);
+                o[9 + k] = *reinterpret_cast<const uint32_t*>(k < 8u ? w16 + 64u + 4u * k : w4 + 4u);  // qh
+            }
+            o[18] = *reinterpret_cast<const uint32_t*>(w4 + (2u * h + shift_of(c, j) < 4u ? 8u : 12u));
+            o[19] = *reinterpret_cast<const uint32_t*>(w4 + 16u);
+        }
+    }
+    __device__ Scale scale(uint32_t c, int j, const uint32_t* r) const {
+        const uint32_t sh = shift_of(c, j), ph = (c0 + c) & 1u;
+        const float d = f16_bits_to_f32(r[19] >> (8u * sh));
+        const uint32_t bp = 8u * ((2u * h + sh) & 3u);
+        const float s0 = (float)(int8_t)(r[18] >> bp), s1 = (float)(int8_t)(r[18] >> (bp + 8u));
+        const _Float16 d0 = (_Float16)(d * s0), d1 = (_Float16)(d * s1);  // exact f32 product, one rounding
+        Scale s;
+        s.sel = 0x03020100u + 0x01010101u * sh;
+        s.mN = ph ? 0x00F000F0u : 0x000F000Fu;
+        s.magic = ph ? 0x54005400u : 0x64006400u;  // code bits under the exponent of 64 / 1024
+        s.mH = ph ? 0x03000300u : 0x00300030u;
+        s.sL = 4u - 2u * h;
+        const _Float16 o = ph ? (_Float16)-96.0f : (_Float16)-1056.0f;
+        s.off = h2{o, o};
+        s.ds0 = h2{d0, d0};
+        s.ds1 = h2{d1, d1};
+        return s;
+    }
+    __device__ h8 step(const uint32_t* r, const Scale& s, int t) const {
+        const uint32_t c = __builtin_amdgcn_perm(r[2 * t + 1], r[2 * t], s.sel);
+        const uint32_t c2 = __builtin_amdgcn_perm(r[2 * t + 2], r[2 * t + 1], s.sel);
+        const uint32_t e = __builtin_amdgcn_perm(r[9 + 2 * t + 1], r[9 + 2 * t], s.sel);
+        const uint32_t e2 = __builtin_amdgcn_perm(r[9 + 2 * t + 2], r[9 + 2 * t + 1], s.sel);
+        const h2 ds = t < 2 ? s.ds0 : s.ds1;
+        auto f = [&](uint32_t cv, uint32_t ev) {
+            return as_u((as_h2(and_or(ev << s.sL, s.mH, and_or(cv, s.mN, s.magic))) + s.off) * ds);
+        };
+        return as_h8(f(c, e), f(c >> 8, e >> 8), f(c2, e2), f(c2 >> 8, e2 >> 8));
+    }
+};
+
+template <uint32_t ENC>
+struct WinOf {
+    using type = WinBlocks<ENC>;
+};
+template <>
+struct WinOf<ENC_Q6_K> {
+    using type = WinQ6K;
+};
+
 // LDS geometry of one kernel configuration.
 template <uint32_t ENC, int TM, int S>
 struct Geo {
-    static constexpr uint32_t WN = kWaves / S;                        // column subtiles per workgroup
-    static constexpr uint32_t kSpanMax = (2u * Blk<ENC>::kBytes + 2u + 3u) & ~3u;  // a row's two blocks, aligned
-    static constexpr uint32_t NP = (kSpanMax + 15u) / 16u;             // 16-byte pieces per row window
-    static constexpr uint32_t kWinBytes = 64u * NP * 16u;              // a wave's 64-row window
+    using W = typename WinOf<ENC>::type;
+    static constexpr uint32_t WN = kWaves / S;                         // column subtiles per workgroup
+    static constexpr uint32_t kWinBytes = W::kBytes;                    // a wave's 64-row window
     static constexpr uint32_t kABytes = (uint32_t)S * 4u * TM * 1024u;  // activation fragments of a chunk
     static constexpr uint32_t kSlot = kABytes + kWaves * kWinBytes;
     static constexpr uint32_t kRs = 32u * TM * 4u;                      // the tile's row factors
@@ -221,7 +423,7 @@ struct Geo {
     static constexpr uint32_t kRing = R * kSlot > kEpi ? R * kSlot : kEpi;  // the epilogue reuses the ring
     static constexpr uint32_t kLds = kRing + kRs;
     static constexpr uint32_t kDmaA = 4u * TM / WN;  // activation copies per wave per chunk
-    static constexpr uint32_t kDma = kDmaA + NP;      // all copies per wave per chunk
+    static constexpr uint32_t kDma = kDmaA + W::kCopies;  // all copies per wave per chunk
     static constexpr bool kFits = 2u * kSlot <= kRoom;
     static_assert((4u * TM) % WN == 0, "activation fragments split evenly over the slice's waves");
 };
@@ -229,9 +431,8 @@ struct Geo {
 template <uint32_t ENC, int TM, int S>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_kernel(const GemmArgs a) {
-    using B = Blk<ENC>;
     using G = Geo<ENC, TM, S>;
-    constexpr uint32_t R = G::R, NP = G::NP;
+    constexpr uint32_t R = G::R;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
     const uint32_t lane = threadIdx.x & 63u;
@@ -264,49 +465,16 @@ void gemm_kernel(const GemmArgs a) {
         xsrc[q] = a.xh + (((size_t)mb * ksteps + 4u * c0 + t) * 64u + lane) * 8u;
         xdst[q] = (ks * 4u * TM + f) * 1024u;
     }
-    // Weight copies: piece p of row r of the window, for lane index 64·q + lane.
-    const uint8_t* wsrc[NP];
-#pragma unroll
-    for (uint32_t q = 0; q < NP; q++) {
-        const uint32_t li = 64u * q + lane, r = li / NP, p = li % NP;
-        const uint32_t n = n0 + r < a.N ? n0 + r : a.N - 1u;  // past N: re-read the last row (never stored)
-        const uintptr_t start = (uintptr_t)a.w + (uintptr_t)n * a.rowbytes + (uintptr_t)B::kBytes * 2u * c0;
-        const uintptr_t al = start & ~(uintptr_t)3;
-        const uint32_t span = (uint32_t)(((start + 2u * B::kBytes + 3u) & ~(uintptr_t)3) - al);
-        const uint32_t off = p + 1u < NP ? 16u * p : span - 16u;
-        wsrc[q] = reinterpret_cast<const uint8_t*>(al + off);
-    }
+    using W = typename G::W;
+    W win;
+    win.init(a, n0, lane, c0);
     auto slot_a = [&](uint32_t slot) { return lds + slot * G::kSlot; };
     auto slot_w = [&](uint32_t slot, uint32_t wv) { return lds + slot * G::kSlot + G::kABytes + wv * G::kWinBytes; };
     auto issue = [&](uint32_t c, uint32_t slot) {  // chunk c of the slice (c < nc) into a ring slot
 #pragma unroll
         for (uint32_t q = 0; q < G::kDmaA; q++) dma16(xsrc[q] + (size_t)c * 4u * 512u, slot_a(slot) + xdst[q]);
-#pragma unroll
-        for (uint32_t q = 0; q < NP; q++)
-            dma16(wsrc[q] + (size_t)c * 2u * B::kBytes, slot_w(slot, wave) + 64u * 16u * q);
+        win.issue(c, slot_w(slot, wave));
     };
-
-    // This lane's block in the window: row l % 32 of each 32-row block j, block
-    // h = l / 32 of the chunk; dword k of the block's aligned start at window
-    // offset wrd[j][k] (span bytes past the first NP - 1 pieces sit in the
-    // last piece, moved back by span - 16·NP).
-    const uint32_t h = lane >> 5;
-    uint32_t sh[2], wrd[2][B::kDw];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const uint32_t r = 32u * j + (lane & 31u);
-        const uint32_t n = n0 + r < a.N ? n0 + r : a.N - 1u;
-        const uintptr_t start = (uintptr_t)a.w + (uintptr_t)n * a.rowbytes + (uintptr_t)B::kBytes * 2u * c0;
-        const uint32_t s0 = (uint32_t)(start & 3u);
-        const uint32_t span = (2u * B::kBytes + s0 + 3u) & ~3u;
-        const uint32_t bstart = s0 + B::kBytes * h;  // block h's first byte in the span
-        sh[j] = bstart & 3u;
-#pragma unroll
-        for (uint32_t k = 0; k < B::kDw; k++) {
-            const uint32_t o = (bstart & ~3u) + 4u * k;
-            wrd[j][k] = r * NP * 16u + (o < 16u * (NP - 1u) ? o : o - span + 16u * NP);
-        }
-    }
 
     // Row factors of the tile's 32·TM rows, copied into LDS ahead of the ring
     // (the oldest copy in flight, so the first ring wait covers it).
@@ -325,26 +493,20 @@ void gemm_kernel(const GemmArgs a) {
     // refilled from the next chunk's slot once its MFMAs have issued), and the
     // raw and decoded weights of the current and the next chunk.
     h8 xa[TM][4];
-    uint32_t raw[B::kDw * 2];
+    uint32_t raw[W::kDw * 2];
     h8 wf[2][2][4];
-    auto read_w = [&](uint32_t slot) {
-        const uint8_t* sw = slot_w(slot, wave);
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (uint32_t k = 0; k < B::kDw; k++) raw[j * B::kDw + k] = *reinterpret_cast<const uint32_t*>(sw + wrd[j][k]);
-    };
+    auto read_w = [&](uint32_t c) { win.read(c, slot_w(c % R, wave), raw); };  // chunk c's weights
     auto read_a = [&](uint32_t slot, int t) {
         const uint8_t* sa = slot_a(slot) + ks * 4u * TM * 1024u + lane * 16u;
 #pragma unroll
         for (int i = 0; i < TM; i++) xa[i][t] = *reinterpret_cast<const h8*>(sa + (4u * i + t) * 1024u);
     };
-    auto decode_all = [&](int p) {
+    auto decode_all = [&](uint32_t c, int p) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const typename B::Scale sc = B::scale(raw + j * B::kDw, sh[j]);
+            const typename W::Scale sc = win.scale(c, j, raw + j * W::kDw);
 #pragma unroll
-            for (int t = 0; t < 4; t++) wf[p][j][t] = B::step(raw + j * B::kDw, sc, t);
+            for (int t = 0; t < 4; t++) wf[p][j][t] = win.step(raw + j * W::kDw, sc, t);
         }
     };
 
@@ -357,7 +519,7 @@ void gemm_kernel(const GemmArgs a) {
     // the decode issues).  Scheduling barriers keep the k steps in order.
     // The last step reads a slot no chunk was copied into; its decode is
     // never multiplied.
-    constexpr int kValuPerMfma = (int)(3u * 16u + 2u * TM - 1u) / (2 * TM);  // ~3 decode pieces of ~16 VALU per k step
+    constexpr int kValuPerMfma = (int)(3u * W::kValuPerStep + 2u * TM - 1u) / (2 * TM);  // ~3 decode pieces per k step
     auto step = [&](uint32_t c, int p) {
         // copies issued so far: chunks up to min(c + R, nc) - 1; chunk c + 1 must
         // have landed, the newer ones may stay in flight
@@ -366,9 +528,9 @@ void gemm_kernel(const GemmArgs a) {
         const uint32_t cn = c + R;
         if (cn < nc) issue(cn, c % R);
         const uint32_t nxt = (c + 1u) % R;
-        read_w(nxt);
+        read_w(c + 1u);
         __builtin_amdgcn_sched_barrier(0);
-        typename B::Scale sc[2];
+        typename W::Scale sc[2];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
 #pragma unroll
@@ -381,8 +543,8 @@ void gemm_kernel(const GemmArgs a) {
 #pragma unroll
                 for (int k = 3 * (t - 1); k < 3 * t && k < 8; k++) {
                     const int kj = k >> 2, kt = k & 3;
-                    if (kt == 0) sc[kj] = B::scale(raw + kj * B::kDw, sh[kj]);
-                    wf[1 - p][kj][kt] = B::step(raw + kj * B::kDw, sc[kj], kt);
+                    if (kt == 0) sc[kj] = win.scale(c + 1u, kj, raw + kj * W::kDw);
+                    wf[1 - p][kj][kt] = win.step(raw + kj * W::kDw, sc[kj], kt);
                 }
             }
             read_a(nxt, t);
@@ -405,7 +567,7 @@ void gemm_kernel(const GemmArgs a) {
     read_w(0);
 #pragma unroll
     for (int t = 0; t < 4; t++) read_a(0, t);
-    decode_all(0);
+    decode_all(0, 0);
     uint32_t c = 0;
     for (; c + 2u <= nc; c += 2u) {
         step(c, 0);
@@ -540,12 +702,13 @@ uint32_t gemm_layout(uint32_t enc) {
         case ENC_Q4_0: return Blk<ENC_Q4_0>::kLayout;
         case ENC_Q4_1: return Blk<ENC_Q4_1>::kLayout;
         case ENC_Q8_0: return Blk<ENC_Q8_0>::kLayout;
+        case ENC_Q6_K: return XFRAG_BYTE;  // a lane's 32 codes in order, as Q8_0
         default: return ~0u;
     }
 }
 
 bool gemm_supported(uint32_t enc, uint32_t N, uint32_t K, uint32_t M) {
-    return gemm_layout(enc) != ~0u && N > 0 && M > 0 && K >= 64u && K % 64u == 0;
+    return gemm_layout(enc) != ~0u && N > 0 && M > 0 && K >= 64u && K % (enc == ENC_Q6_K ? 256u : 64u) == 0;
 }
 
 hipError_t gemm_launch(uint32_t enc, const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs,
@@ -564,6 +727,7 @@ hipError_t gemm_launch(uint32_t enc, const uint8_t* w, uint32_t N, uint32_t K, c
         case ENC_Q4_0: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q4_0>::kBytes; return launch_enc<ENC_Q4_0>(a, st);
         case ENC_Q4_1: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q4_1>::kBytes; return launch_enc<ENC_Q4_1>(a, st);
         case ENC_Q8_0: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q8_0>::kBytes; return launch_enc<ENC_Q8_0>(a, st);
+        case ENC_Q6_K: a.rowbytes = (uint64_t)(K / 256u) * 210u; return launch_enc<ENC_Q6_K>(a, st);
         default: return hipErrorInvalidValue;
     }
 }

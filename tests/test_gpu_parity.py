@@ -355,7 +355,40 @@ def test_gemm(ctx, gtype, m, n, k, ybf16):
     assert np.all(err <= 2.0 ** -11 + 1e-5 + extra), err.max()
 
 
-@pytest.mark.parametrize("gtype", [oracle.Q4_0, oracle.Q8_0], ids=oracle.NAMES.get)
+# Q6_K: K a multiple of 256, the GEMM from 48 rows (shape -> TM, S)
+GEMM_SHAPES_Q6K = [(50, 20000, 256),   # TM2 S1/2
+                   (64, 1000, 512),
+                   (100, 300, 512),    # TM4
+                   (200, 384, 1024),
+                   (512, 3072, 1024),
+                   (512, 1024, 3072),  # TM2 S4
+                   (512, 6144, 1024),
+                   (2048, 3072, 1024),  # TM4 S1
+                   (2000, 3000, 1024),  # ragged
+                   (300, 200, 4096)]
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES_Q6K)
+@pytest.mark.parametrize("ybf16", [False, True])
+def test_gemm_q6_k(ctx, m, n, k, ybf16):
+    """Q6_K weights round twice (d·sc, then (q-32)·ds): 2^-10 with exact bf16
+    activations."""
+    w, data = gguf(oracle.Q6_K, n, k, seed=m + n + k + 1)
+    xb = oracle.f32_to_bf16_bits(oracle.randn(m * k, seed=m + 3)).reshape(m, k)
+    x = oracle.bf16_bits_to_f32(xb)
+    y = ctx.qlinear(w, dev(xb).view(torch.bfloat16), y_dtype=torch.bfloat16 if ybf16 else torch.float32)
+    if ybf16:
+        y = oracle.bf16_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16))
+    else:
+        y = y.cpu().numpy()
+    y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(oracle.Q6_K, data, n, k))
+    den = np.where(absdot > 0, absdot, 1)
+    extra = np.abs(y64) * 2.0 ** -8 / den if ybf16 else 0.0
+    err = np.abs(y.astype(np.float64) - y64) / den
+    assert np.all(err <= 2.0 ** -10 + 1e-5 + extra), err.max()
+
+
+@pytest.mark.parametrize("gtype", [oracle.Q4_0, oracle.Q8_0, oracle.Q6_K], ids=oracle.NAMES.get)
 @pytest.mark.parametrize("m,n,k", [(200, 384, 1024), (512, 3072, 1024), (96, 1040, 2048), (512, 1024, 3072), (130, 2000, 768),
                                    (2048, 3072, 768), (20, 20000, 256), (33, 512, 2048)])
 def test_gemm_offset_weights(ctx, gtype, m, n, k):
@@ -366,7 +399,7 @@ def test_gemm_offset_weights(ctx, gtype, m, n, k):
     x = oracle.bf16_bits_to_f32(xb)
     y = ctx.qlinear(w, dev(xb).view(torch.bfloat16)).cpu().numpy()
     err = gemv_err(y, x, oracle.dequant_gguf(gtype, data, n, k))
-    assert err <= 2.0 ** -11 + 1e-5, err
+    assert err <= (2.0 ** -10 if gtype == oracle.Q6_K else 2.0 ** -11) + 1e-5, err
 
 
 def test_gemm_deterministic(ctx):
