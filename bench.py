@@ -251,15 +251,15 @@ def bench_rotating_gemv(torch, d, ctx, enc, n, k, batch, pool_bytes=1.2e9, iters
             "hbm_frac": w0.nbytes / ms / 1e6 / HBM_PEAK_GBS}
 
 
-def bench_gemm(torch, d, ctx, m, n, k, xdtype, iters=50):
-    """Config 3: Q4_0 prefill GEMM (f16 MFMA, f32 accumulate, bf16 Y), x f32 or
-    bf16.  One call = the activation staging kernel (x to f16 with a per-row
-    power-of-two scale) plus the GEMM, both inside the timed region (HIP events
-    on the launch stream); the GEMM kernel's own duration is in the rocprofv3
-    summary under profiles/."""
+def bench_gemm(torch, d, ctx, m, n, k, xdtype, iters=50, enc=None):
+    """Config 3: prefill GEMM (f16 MFMA, f32 accumulate, bf16 Y; Q4_0 unless
+    `enc`), x f32 or bf16.  One call = the activation staging kernel (x to f16
+    operand fragments with a per-row power-of-two scale) plus the GEMM, both
+    inside the timed region (HIP events on the launch stream); the GEMM
+    kernel's own duration is in the rocprofv3 summary under profiles/."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(3)
-    w = gguf_tensor(torch, d, d.ENC_Q4_0, n, k, gen)
+    w = gguf_tensor(torch, d, d.ENC_Q4_0 if enc is None else enc, n, k, gen)
     x = torch.randn(m, k, device="cuda", generator=gen).to(xdtype)
     y = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
     st = torch.cuda.Stream()
@@ -360,9 +360,15 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--no-extra", action="store_true", help="skip configs 0/1/2/3 and config 4 at batch 4/16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--gemm-probe", action="store_true",
+                    help="for rocprofv3: 30 prefill calls (staging + GEMM, Q4_0, bf16 X and Y) at M512 N3072 K1024, "
+                         "then 30 at M2048 N3072 K1024, then 30 each of Q4_1, Q8_0, Q6_K at M512 N3072 K1024")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: one 64 MiB device copy (the counters' calibration), then one "
-                         "eager config-4 step and one M512 config-3 GEMM; prints the launch labels in dispatch order")
+                         "eager decode step (--probe-config) and one M512 config-3 GEMM; prints the launch labels "
+                         "in dispatch order")
+    ap.add_argument("--probe-config", type=int, default=4, choices=(1, 4),
+                    help="the decode step --pmc-probe runs: config 4 (Qwen3-8B) or config 1 (Qwen3-0.6B mixed GGUF)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -376,8 +382,23 @@ def main() -> int:
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0)
 
-    log("building config 4 weights (Qwen3-8B GGUF, 4.88 GB) ...")
-    s4 = gguf_step_8b(torch, d, gen)
+    if args.gemm_probe:
+        for enc, m in ((d.ENC_Q4_0, 512), (d.ENC_Q4_0, 2048), (d.ENC_Q4_1, 512), (d.ENC_Q8_0, 512), (d.ENC_Q6_K, 512)):
+            wg = gguf_tensor(torch, d, enc, 3072, 1024, gen)
+            xg = torch.randn(m, 1024, device="cuda", generator=gen).bfloat16()
+            yg = torch.empty(m, 3072, device="cuda", dtype=torch.bfloat16)
+            torch.cuda.synchronize()
+            for _ in range(30):
+                ctx.qlinear(wg, xg, yg)
+            torch.cuda.synchronize()
+        print("gemm probe: Q4_0 M512, Q4_0 M2048, Q4_1, Q8_0, Q6_K M512 (N3072 K1024), 30 calls each", flush=True)
+        return 0
+
+    if args.pmc_probe and args.probe_config == 1:
+        s4 = gguf_step_06b(torch, d, gen)
+    else:
+        log("building config 4 weights (Qwen3-8B GGUF, 4.88 GB) ...")
+        s4 = gguf_step_8b(torch, d, gen)
     r4 = StepRunner(torch, d, ctx, s4, args.batch, torch.float32, torch.float32)
     if args.pmc_probe:
         src = torch.ones(16 << 20, dtype=torch.float32, device="cuda")
@@ -476,8 +497,14 @@ def main() -> int:
                     c3[f"M{m}_N{n}_K{k}_{xn}"] = {kk: round(v, 4) for kk, v in
                                                   bench_gemm(torch, d, ctx, m, n, k, xdt).items()}
         extra["config3_q4_0_gemm"] = c3
+        log("prefill GEMM, other encodings ...")
+        extra["config3_other_encodings_gemm"] = {
+            f"{name}_M512_N{n}_K{k}_xbf16": {kk: round(v, 4) for kk, v in
+                                             bench_gemm(torch, d, ctx, 512, n, k, torch.bfloat16, enc=enc).items()}
+            for name, enc in (("q4_1", d.ENC_Q4_1), ("q8_0", d.ENC_Q8_0), ("q6_k", d.ENC_Q6_K))
+            for (n, k) in [(3072, 1024), (1024, 3072)]}
         g512 = c3["M512_N3072_K1024_xbf16"]
-        extra["config3_roofline"] = {"bound": "mfma", "kernel": "xprep + gemm_q4_0, M512 N3072 K1024, bf16 X",
+        extra["config3_roofline"] = {"bound": "mfma", "kernel": "xprep + gemm (Q4_0), M512 N3072 K1024, bf16 X",
                                      "achieved": round(g512["TFLOPs"], 1), "peak": MFMA_F16_PEAK_TFLOPS,
                                      "unit": "TFLOP/s", "frac": round(g512["mfma_frac"], 4),
                                      "flops_per_launch": 2 * 512 * 3072 * 1024, "avg_call_us": round(g512["us"], 3),

@@ -28,8 +28,9 @@
 //
 // Mapping: one wave per row (4 rows per 256-thread workgroup); lane l takes
 // the 8-element output slots l, l+64, ... (slot 8c + 2t + h: chunk c, step t,
-// half h).  Rows with K <= 8192 keep their values in registers between the
-// max pass and the conversion pass; longer rows reload them (cache hits).
+// half h).  Rows with K <= 12288 keep their values in registers between the
+// max pass and the conversion pass; longer rows reload them (cache hits), four
+// slots in flight per lane.
 // NaN and inf: the row's scale is taken as 2^15 and the non-finite values
 // propagate to the row's outputs.
 #include "device_common.hpp"
@@ -141,10 +142,15 @@ __global__ __launch_bounds__(kXprepWaves * 64) void xprep_kernel(const void* __r
             }
         }
     } else {
-        for (uint32_t g = lane; g < slots; g += 64u) {
-            float t[8];
-            load8<XBF16, LAYOUT>(x, row, g, t);
-            mx = absbits_max8(t, mx);
+        // four slots in flight per lane (cache hits on the second pass)
+        for (uint32_t g0 = lane; g0 < slots; g0 += 256u) {
+            float t[4][8];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (g0 + 64u * i < slots) load8<XBF16, LAYOUT>(x, row, g0 + 64u * i, t[i]);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (g0 + 64u * i < slots) mx = absbits_max8(t[i], mx);
         }
     }
     mx = wave_umax(mx);
@@ -161,10 +167,14 @@ __global__ __launch_bounds__(kXprepWaves * 64) void xprep_kernel(const void* __r
             if (g < slots) store8(xh, frag_offset(m, g, ksteps), v[i], sh);
         }
     } else {
-        for (uint32_t g = lane; g < slots; g += 64u) {
-            float t[8];
-            load8<XBF16, LAYOUT>(x, row, g, t);
-            store8(xh, frag_offset(m, g, ksteps), t, sh);
+        for (uint32_t g0 = lane; g0 < slots; g0 += 256u) {
+            float t[4][8];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (g0 + 64u * i < slots) load8<XBF16, LAYOUT>(x, row, g0 + 64u * i, t[i]);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (g0 + 64u * i < slots) store8(xh, frag_offset(m, g0 + 64u * i, ksteps), t[i], sh);
         }
     }
     if (lane == 0) gptr_mut<float>(rs)[m] = ldexpf(1.0f, e - 15);
@@ -180,6 +190,7 @@ hipError_t launch_xprep(const void* x, uint32_t M, uint32_t K, uint16_t* xh, flo
     else if (slots <= 256u) hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 4>), grid, block, 0, st, x, M, Mp, K, xh, rs);
     else if (slots <= 512u) hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 8>), grid, block, 0, st, x, M, Mp, K, xh, rs);
     else if (slots <= 1024u) hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 16>), grid, block, 0, st, x, M, Mp, K, xh, rs);
+    else if (slots <= 1536u) hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 24>), grid, block, 0, st, x, M, Mp, K, xh, rs);
     else hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 0>), grid, block, 0, st, x, M, Mp, K, xh, rs);
     return hipGetLastError();
 }

@@ -329,7 +329,9 @@ GEMM_SHAPES = [(17, 130, 96),      # TM1 S1, K of three blocks
                (2048, 3072, 1024),  # TM4 S1
                (2000, 3000, 1024),  # ragged rows and columns
                (2048, 64, 8128),   # 127 chunks of 64 k: no K split divides them
-               (300, 200, 4032)]   # 63 chunks
+               (300, 200, 4032),   # 63 chunks
+               (48, 256, 12288),   # activation staging: 24 register slots per lane
+               (40, 128, 16384)]   # activation staging: second pass reloads the row
 GEMM_TYPES = [oracle.Q4_0, oracle.Q4_1, oracle.Q8_0]
 
 
