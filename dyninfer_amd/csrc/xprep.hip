@@ -98,10 +98,14 @@ __device__ __forceinline__ size_t frag_offset(uint32_t m, uint32_t slot, uint32_
     return (((size_t)(m >> 5) * ksteps + 4u * c + t) * 64u + (m & 31u) + 32u * h) * 8u;
 }
 
-// Both layouts pair (v0, v2), (v1, v3), (v4, v6), (v5, v7).
+// Both layouts pair (v0, v2), (v1, v3), (v4, v6), (v5, v7).  Non-temporal
+// stores: the staged operand is read by the next kernel, not by this one, and
+// streaming it out during the kernel rather than leaving dirty L2 lines for the
+// end-of-kernel write-back measured 7.3 -> 6.1 us at M = 2048, K = 1024.
 __device__ __forceinline__ void store8(uint16_t* xh, size_t off, const float (&v)[8], int sh) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    *gptr_mut<u32x4>(xh + off) = u32x4{pk(v[0], v[2], sh), pk(v[1], v[3], sh), pk(v[4], v[6], sh), pk(v[5], v[7], sh)};
+    __builtin_nontemporal_store(u32x4{pk(v[0], v[2], sh), pk(v[1], v[3], sh), pk(v[4], v[6], sh), pk(v[5], v[7], sh)},
+                                gptr_mut<u32x4>(xh + off));
 }
 
 // Maximum over the wave (unsigned), every lane receiving it.
