@@ -1,9 +1,10 @@
 // Prefill GEMM on gfx950 MFMA for the GGUF encodings Q4_0, Q4_1, Q8_0 and
-// Q6_K: Y[M, N] = X[M, K] · Wᵀ with f32 accumulation.
+// Q6_K and for MLX affine U4: Y[M, N] = X[M, K] · Wᵀ with f32 accumulation.
 //
 // Reference semantics: the same `emit_linear` contraction as decode
 // (gguf_codegen.rs:268-314, dequantisations :412-472 Q4_0, :382-410 Q8_0,
-// :474-526 Q6_K, q4.rs Q4_1) with rows = the prefill window/chunk (512 when paged,
+// :474-526 Q6_K, q4.rs Q4_1; mlx_affine.rs:557-626 `emit_linear_u4`) with
+// rows = the prefill window/chunk (512 when paged,
 // parameter.rs:107-121, dense_decoder.rs:53-56).
 //
 // Data path.  W is read as GGUF blocks straight from HBM (no repack); X
@@ -31,7 +32,7 @@
 //     the offset (exact) and a packed multiply by the block scale rounds once
 //     (Q4_0 RNE_f16((q-8)·d), Q8_0 RNE_f16(q·d)); Q4_1 a packed fma,
 //     RNE_f16(q·d + m); Q6_K RNE_f16((q-32)·RNE_f16(d·sc)) (its window and
-//     decode are described at WinQ6K).
+//     decode are described at WinQ6K); MLX U4 RNE_f16(q·s + b) (WinMlx).
 //   * The weights are the MFMA's A operand and the activations its B, so each
 //     lane ends with 4 consecutive output columns of one row per block and
 //     stores them as one 16-byte (f32) or 8-byte (bf16) write.  K slices meet
@@ -71,6 +72,9 @@ struct GemmArgs {
     uint32_t mt, nt;  // workgroup tiles along M and N
     uint32_t y_bf16;
     uint32_t mmajor;  // tile order: 1 = M-major (consecutive tiles share activation rows)
+    const uint8_t* sc;  // MLX U4: scales and biases [N, K/group] of dtype sdtype
+    const uint8_t* bi;
+    uint32_t group, sdtype;
 };
 
 // (a & m) | b as one v_and_or_b32 (mask in a scalar register: a VOP3 op takes
@@ -399,9 +403,107 @@ struct WinQ6K {
     }
 };
 
+// MLX affine U4 (mlx_affine.rs:557-626; packed u32 [N, K/8], nibble i of a
+// word = k offset i, fixture.rs:307-311): a row's chunk is 8 words (32 bytes,
+// 4-byte-aligned rows of K/2 bytes) copied as two 16-byte pieces, plus, per
+// row, the dwords holding the scale and the bias of the chunk's two 32-k
+// halves (the same group unless group = 32).  Lane l decodes row l % 32 of
+// each 32-row half j, words 4h .. 4h+3 (h = l / 32): k step t takes word
+// 4h + t, nibbles (0,4) (1,5) (2,6) (3,7) as packed pairs (XFRAG_WORD), code q
+// exact in f16 and w = RNE_f16(q·s + b) by one packed fma, s and b taken to
+// f16 first (bf16 and f16 values exact in f16's normal range; f32 rounded).
+struct WinMlx {
+    static constexpr uint32_t kPieces = 2, kAux = 4, kCopies = kPieces + kAux;
+    static constexpr uint32_t kAuxOff = 64u * 16u * kPieces;  // aux dwords after the 64 rows' pieces
+    static constexpr uint32_t kBytes = kAuxOff + 256u * kAux;
+    static constexpr uint32_t kDw = 6;  // 4 code words, scale dword, bias dword
+    static constexpr uint32_t kValuPerStep = 14;
+    struct Scale {
+        h2 s, b;
+    };
+    const uint8_t* src[kPieces];  // copy lane's piece of the slice's first chunk
+    uintptr_t srow, brow;         // copy lane's row (= lane) of scales and biases
+    uint32_t ssh[2], bsh[2];      // this lane's rows' scale and bias row starts mod 4 (per 32-row half j)
+    uint32_t c0, es, group, sdtype, lane;
+
+    __device__ void init(const GemmArgs& a, uint32_t n0, uint32_t lane_, uint32_t c0_) {
+        lane = lane_;
+        c0 = c0_;
+        group = a.group;
+        sdtype = a.sdtype;
+        es = a.sdtype == DT_F32 ? 4u : 2u;
+        const uint32_t rbytes = a.K / 2u, sbytes = a.K / a.group * es;
+        auto rowc = [&](uint32_t r) { return n0 + r < a.N ? n0 + r : a.N - 1u; };  // past N: re-read the last row
+#pragma unroll
+        for (uint32_t q = 0; q < kPieces; q++) {
+            const uint32_t li = 64u * q + lane;
+            src[q] = a.w + (size_t)rowc(li / 2u) * rbytes + 32u * c0 + 16u * (li % 2u);
+        }
+        srow = (uintptr_t)a.sc + (uintptr_t)rowc(lane) * sbytes;
+        brow = (uintptr_t)a.bi + (uintptr_t)rowc(lane) * sbytes;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uintptr_t o = (uintptr_t)rowc(32u * j + (lane & 31u)) * sbytes;
+            ssh[j] = (uint32_t)(((uintptr_t)a.sc + o) & 3u);
+            bsh[j] = (uint32_t)(((uintptr_t)a.bi + o) & 3u);
+        }
+    }
+    // byte offset in a scale row of the group of the chunk's 32-k half hh
+    __device__ uint32_t goff(uint32_t c, uint32_t hh) const { return (64u * (c0 + c) + 32u * hh) / group * es; }
+    __device__ void issue(uint32_t c, uint8_t* win) const {
+#pragma unroll
+        for (uint32_t q = 0; q < kPieces; q++) dma16(src[q] + (size_t)c * 32u, win + 1024u * q);
+#pragma unroll
+        for (uint32_t hh = 0; hh < 2; hh++) {
+            const uint32_t o = goff(c, hh);
+            dma4(reinterpret_cast<const void*>((srow + o) & ~(uintptr_t)3), win + kAuxOff + 256u * hh);
+            dma4(reinterpret_cast<const void*>((brow + o) & ~(uintptr_t)3), win + kAuxOff + 256u * (2u + hh));
+        }
+    }
+    __device__ void read(uint32_t, const uint8_t* win, uint32_t* raw) const {
+        const uint32_t h = lane >> 5;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t r = 32u * j + (lane & 31u);
+            const u32x4 q = *reinterpret_cast<const u32x4*>(win + 32u * r + 16u * h);
+            uint32_t* o = raw + j * kDw;
+            o[0] = q.x;
+            o[1] = q.y;
+            o[2] = q.z;
+            o[3] = q.w;
+            o[4] = *reinterpret_cast<const uint32_t*>(win + kAuxOff + 256u * h + 4u * r);
+            o[5] = *reinterpret_cast<const uint32_t*>(win + kAuxOff + 256u * (2u + h) + 4u * r);
+        }
+    }
+    __device__ Scale scale(uint32_t c, int j, const uint32_t* r) const {
+        // 16-bit values may sit 2 bytes into their dword
+        const uint32_t go = goff(c, lane >> 5);
+        auto f16of = [&](uint32_t bits, uint32_t base_mod4) -> _Float16 {
+            if (sdtype == DT_F32) return (_Float16)__uint_as_float(bits);
+            const uint32_t v = (bits >> (8u * ((base_mod4 + go) & 3u))) & 0xFFFFu;
+            if (sdtype == DT_F16) return __builtin_bit_cast(_Float16, (uint16_t)v);
+            return (_Float16)__uint_as_float(v << 16);  // bf16
+        };
+        const _Float16 sv = f16of(r[4], ssh[j]), bv = f16of(r[5], bsh[j]);
+        return {h2{sv, sv}, h2{bv, bv}};
+    }
+    __device__ h8 step(const uint32_t* r, const Scale& s, int t) const {
+        const h2 ol = {(_Float16)-1024.0f, (_Float16)-1024.0f}, oh = {(_Float16)-64.0f, (_Float16)-64.0f};
+        const uint32_t ml = 0x64006400u, mh = 0x54005400u;
+        auto lo = [&](uint32_t v) { return as_u(__builtin_elementwise_fma(as_h2(and_or(v, 0x000F000Fu, ml)) + ol, s.s, s.b)); };
+        auto hi = [&](uint32_t v) { return as_u(__builtin_elementwise_fma(as_h2(and_or(v, 0x00F000F0u, mh)) + oh, s.s, s.b)); };
+        const uint32_t w = r[t], w8 = w >> 8;
+        return as_h8(lo(w), hi(w), lo(w8), hi(w8));
+    }
+};
+
 template <uint32_t ENC>
 struct WinOf {
     using type = WinBlocks<ENC>;
+};
+template <>
+struct WinOf<ENC_MLX_U4> {
+    using type = WinMlx;
 };
 template <>
 struct WinOf<ENC_Q6_K> {
@@ -709,6 +811,7 @@ uint32_t gemm_layout(uint32_t enc) {
         case ENC_Q4_1: return Blk<ENC_Q4_1>::kLayout;
         case ENC_Q8_0: return Blk<ENC_Q8_0>::kLayout;
         case ENC_Q6_K: return XFRAG_BYTE;  // a lane's 32 codes in order, as Q8_0
+        case ENC_MLX_U4: return XFRAG_WORD;
         default: return ~0u;
     }
 }
@@ -717,11 +820,14 @@ bool gemm_supported(uint32_t enc, uint32_t N, uint32_t K, uint32_t M) {
     return gemm_layout(enc) != ~0u && N > 0 && M > 0 && K >= 64u && K % (enc == ENC_Q6_K ? 256u : 64u) == 0;
 }
 
-hipError_t gemm_launch(uint32_t enc, const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs,
-                       uint32_t M, void* y, bool y_bf16, hipStream_t st) {
+hipError_t gemm_launch(const GemmWeight& wt, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs, uint32_t M,
+                       void* y, bool y_bf16, hipStream_t st) {
+    const uint32_t enc = wt.enc;
     if (!gemm_supported(enc, N, K, M)) return hipErrorInvalidValue;
+    if (enc == ENC_MLX_U4 && (wt.group == 0 || wt.group % 32u || K % wt.group || wt.sdtype > DT_BF16 || !wt.sc || !wt.bi))
+        return hipErrorInvalidValue;
     GemmArgs a{};
-    a.w = w;
+    a.w = wt.w;
     a.xh = xh;
     a.rs = rs;
     a.y = y;
@@ -729,18 +835,26 @@ hipError_t gemm_launch(uint32_t enc, const uint8_t* w, uint32_t N, uint32_t K, c
     a.N = N;
     a.K = K;
     a.y_bf16 = y_bf16 ? 1u : 0u;
+    a.sc = wt.sc;
+    a.bi = wt.bi;
+    a.group = wt.group;
+    a.sdtype = wt.sdtype;
+    switch (enc) {
+        case ENC_Q4_0: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q4_0>::kBytes; break;
+        case ENC_Q4_1: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q4_1>::kBytes; break;
+        case ENC_Q8_0: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q8_0>::kBytes; break;
+        case ENC_Q6_K: a.rowbytes = (uint64_t)(K / 256u) * 210u; break;
+        default: a.rowbytes = (uint64_t)K / 2u; break;  // MLX packed words (scales and biases besides)
+    }
     // M-major tile order when the staged activations (2 bytes per element)
     // outweigh the weights (M2048 N3072 K1024: 34.3 against 35.9 us per call)
-    const uint64_t wbytes = (uint64_t)N * (enc == ENC_Q6_K ? (uint64_t)(K / 256u) * 210u
-                                                            : (uint64_t)(K / 32u) * (enc == ENC_Q4_0   ? Blk<ENC_Q4_0>::kBytes
-                                                                                     : enc == ENC_Q4_1 ? Blk<ENC_Q4_1>::kBytes
-                                                                                                       : Blk<ENC_Q8_0>::kBytes));
-    a.mmajor = (uint64_t)M * K * 2u > wbytes ? 1u : 0u;
+    a.mmajor = (uint64_t)M * K * 2u > (uint64_t)N * a.rowbytes ? 1u : 0u;
     switch (enc) {
-        case ENC_Q4_0: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q4_0>::kBytes; return launch_enc<ENC_Q4_0>(a, st);
-        case ENC_Q4_1: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q4_1>::kBytes; return launch_enc<ENC_Q4_1>(a, st);
-        case ENC_Q8_0: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q8_0>::kBytes; return launch_enc<ENC_Q8_0>(a, st);
-        case ENC_Q6_K: a.rowbytes = (uint64_t)(K / 256u) * 210u; return launch_enc<ENC_Q6_K>(a, st);
+        case ENC_Q4_0: return launch_enc<ENC_Q4_0>(a, st);
+        case ENC_Q4_1: return launch_enc<ENC_Q4_1>(a, st);
+        case ENC_Q8_0: return launch_enc<ENC_Q8_0>(a, st);
+        case ENC_Q6_K: return launch_enc<ENC_Q6_K>(a, st);
+        case ENC_MLX_U4: return launch_enc<ENC_MLX_U4>(a, st);
         default: return hipErrorInvalidValue;
     }
 }

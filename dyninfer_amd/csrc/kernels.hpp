@@ -102,7 +102,8 @@ hipError_t gather_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, cons
 // 32.  Lane half h of k step 4c + t holds 8 k of k = 64c + 32h + (0..31):
 enum XFrag : uint32_t {
     XFRAG_NIB = 2,   // Q4_0, Q4_1: 4t, 4t+2, 4t+1, 4t+3, 16+4t, 18+4t, 17+4t, 19+4t
-    XFRAG_BYTE = 3,  // Q8_0:       8t + (0, 2, 1, 3, 4, 6, 5, 7)
+    XFRAG_BYTE = 3,  // Q8_0, Q6_K: 8t + (0, 2, 1, 3, 4, 6, 5, 7)
+    XFRAG_WORD = 4,  // MLX U4:     8t + (0, 4, 1, 5, 2, 6, 3, 7)
 };
 hipError_t xprep_launch(const void* x, bool x_bf16, uint32_t M, uint32_t K, uint32_t layout, uint16_t* xh, float* rs,
                         hipStream_t stream);
@@ -119,10 +120,18 @@ inline uint64_t prefill_workspace_bytes(uint32_t M, uint32_t K) {
 
 // Prefill GEMM on MFMA (gemm.hip): Y[M, N] = diag(rs) · (Xh[M, K] · Wᵀ), Xh/rs
 // from xprep_launch(gemm_layout(enc)); Y f32 or bf16.  gemm_layout returns ~0u
-// for encodings without a GEMM.
+// for encodings without a GEMM.  The weight: GGUF blocks at w, or MLX U4
+// packed words at w with scales sc and biases bi [N, K/group] of dtype sdtype.
+struct GemmWeight {
+    uint32_t enc;
+    const uint8_t* w;
+    const uint8_t* sc;
+    const uint8_t* bi;
+    uint32_t group, sdtype;
+};
 uint32_t gemm_layout(uint32_t enc);
 bool gemm_supported(uint32_t enc, uint32_t N, uint32_t K, uint32_t M);
-hipError_t gemm_launch(uint32_t enc, const uint8_t* w, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs,
-                       uint32_t M, void* y, bool y_bf16, hipStream_t stream);
+hipError_t gemm_launch(const GemmWeight& wt, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs, uint32_t M,
+                       void* y, bool y_bf16, hipStream_t stream);
 
 }  // namespace dmx

@@ -21,9 +21,12 @@
 // k = 64c + 32h .. 64c + 32h + 31, in the order the block's decode produces:
 //   XFRAG_NIB  (Q4_0, Q4_1: code byte j holds k = j and k = j + 16):
 //              4t, 4t+2, 4t+1, 4t+3, 16+4t, 18+4t, 17+4t, 19+4t
-//   XFRAG_BYTE (Q8_0: one code byte per k):
+//   XFRAG_BYTE (Q8_0, Q6_K: one code byte per k):
 //              8t, 8t+2, 8t+1, 8t+3, 8t+4, 8t+6, 8t+5, 8t+7
-// (pairs (j, j+2) of a dword decode together).  Rows M .. roundup(M, 32) - 1
+//              (pairs (j, j+2) of a dword decode together)
+//   XFRAG_WORD (MLX U4: packed word t of the block holds k = 8t .. 8t+7, LSB
+//              first): 8t, 8t+4, 8t+1, 8t+5, 8t+2, 8t+6, 8t+3, 8t+7
+//              (nibbles j and j+4 of a word decode together).  Rows M .. roundup(M, 32) - 1
 // are written as zeros, so the GEMM reads whole fragments.
 //
 // Mapping: one wave per row (4 rows per 256-thread workgroup); lane l takes
@@ -47,7 +50,7 @@ typedef float xf4 __attribute__((ext_vector_type(4)));
 constexpr int kXprepWaves = 4;
 
 // The 8 activations of output slot `slot` of a row: two runs of 4 k, at
-// k0 and k0 + RUN2 (NIB: 16, BYTE: 4).
+// k0 and k0 + RUN2 (NIB: 16, BYTE and WORD: 4, i.e. one run of 8).
 template <uint32_t LAYOUT>
 __device__ __forceinline__ uint32_t slot_k0(uint32_t slot) {
     const uint32_t c = slot >> 3, t = (slot >> 1) & 3u, h = slot & 1u;
@@ -98,14 +101,18 @@ __device__ __forceinline__ size_t frag_offset(uint32_t m, uint32_t slot, uint32_
     return (((size_t)(m >> 5) * ksteps + 4u * c + t) * 64u + (m & 31u) + 32u * h) * 8u;
 }
 
-// Both layouts pair (v0, v2), (v1, v3), (v4, v6), (v5, v7).  Non-temporal
-// stores: the staged operand is read by the next kernel, not by this one, and
-// streaming it out during the kernel rather than leaving dirty L2 lines for the
-// end-of-kernel write-back measured 7.3 -> 6.1 us at M = 2048, K = 1024.
+// NIB and BYTE pair (v0, v2), (v1, v3), (v4, v6), (v5, v7); WORD pairs (v0, v4),
+// (v1, v5), (v2, v6), (v3, v7).  Non-temporal stores: the staged operand is
+// read by the next kernel, not by this one, and streaming it out during the
+// kernel rather than leaving dirty L2 lines for the end-of-kernel write-back
+// measured 7.3 -> 6.1 us at M = 2048, K = 1024.
+template <uint32_t LAYOUT>
 __device__ __forceinline__ void store8(uint16_t* xh, size_t off, const float (&v)[8], int sh) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    __builtin_nontemporal_store(u32x4{pk(v[0], v[2], sh), pk(v[1], v[3], sh), pk(v[4], v[6], sh), pk(v[5], v[7], sh)},
-                                gptr_mut<u32x4>(xh + off));
+    const u32x4 q = LAYOUT == XFRAG_WORD
+                        ? u32x4{pk(v[0], v[4], sh), pk(v[1], v[5], sh), pk(v[2], v[6], sh), pk(v[3], v[7], sh)}
+                        : u32x4{pk(v[0], v[2], sh), pk(v[1], v[3], sh), pk(v[4], v[6], sh), pk(v[5], v[7], sh)};
+    __builtin_nontemporal_store(q, gptr_mut<u32x4>(xh + off));
 }
 
 // Maximum over the wave (unsigned), every lane receiving it.
@@ -129,7 +136,7 @@ __global__ __launch_bounds__(kXprepWaves * 64) void xprep_kernel(const void* __r
     const uint32_t slots = K / 8u, ksteps = K / 16u;
     if (m >= M) {  // padding row: zeros
         const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        for (uint32_t g = lane; g < slots; g += 64u) store8(xh, frag_offset(m, g, ksteps), z, 0);
+        for (uint32_t g = lane; g < slots; g += 64u) store8<LAYOUT>(xh, frag_offset(m, g, ksteps), z, 0);
         if (lane == 0) gptr_mut<float>(rs)[m] = 0.0f;
         return;
     }
@@ -168,7 +175,7 @@ __global__ __launch_bounds__(kXprepWaves * 64) void xprep_kernel(const void* __r
 #pragma unroll
         for (int i = 0; i < NR; i++) {
             const uint32_t g = lane + 64u * (uint32_t)i;
-            if (g < slots) store8(xh, frag_offset(m, g, ksteps), v[i], sh);
+            if (g < slots) store8<LAYOUT>(xh, frag_offset(m, g, ksteps), v[i], sh);
         }
     } else {
         for (uint32_t g0 = lane; g0 < slots; g0 += 256u) {
@@ -178,7 +185,7 @@ __global__ __launch_bounds__(kXprepWaves * 64) void xprep_kernel(const void* __r
                 if (g0 + 64u * i < slots) load8<XBF16, LAYOUT>(x, row, g0 + 64u * i, t[i]);
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                if (g0 + 64u * i < slots) store8(xh, frag_offset(m, g0 + 64u * i, ksteps), t[i], sh);
+                if (g0 + 64u * i < slots) store8<LAYOUT>(xh, frag_offset(m, g0 + 64u * i, ksteps), t[i], sh);
         }
     }
     if (lane == 0) gptr_mut<float>(rs)[m] = ldexpf(1.0f, e - 15);
@@ -212,6 +219,7 @@ hipError_t xprep_launch(const void* x, bool x_bf16, uint32_t M, uint32_t K, uint
     switch (layout) {
         case XFRAG_NIB: return launch_xprep<XFRAG_NIB>(x, x_bf16, M, K, xh, rs, st);
         case XFRAG_BYTE: return launch_xprep<XFRAG_BYTE>(x, x_bf16, M, K, xh, rs, st);
+        case XFRAG_WORD: return launch_xprep<XFRAG_WORD>(x, x_bf16, M, K, xh, rs, st);
         default: return hipErrorInvalidValue;
     }
 }

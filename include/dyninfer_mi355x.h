@@ -117,11 +117,12 @@ const char* dyninfer_mi355x_last_error(void);
  *   rows <= 16: the decode GEMV kernels (HBM-bound; 5..16 rows of large Q4_0, Q6_K and
  *     MLX weights on MFMA), activations rounded to f16 after a power-of-two scaling per
  *     scale group;
- *   rows >= 17: the prefill path.  Q4_1 and Q8_0 from 17 rows, Q4_0 from 48 rows
- *     (below that its 16-row MFMA GEMV chunks are faster), K a multiple of 64: x is
- *     staged once per call as f16 MFMA operand fragments, each row scaled by a power of
- *     two (RNE) and the rows padded with zeros to a multiple of 32; then one MFMA GEMM
- *     per weight decodes the GGUF blocks straight into MFMA operands.  The staging
+ *   rows >= 17: the prefill path.  Q4_1, Q8_0 and MLX U4 from 17 rows, Q4_0 and Q6_K
+ *     from 48 rows (below that their 16-row MFMA GEMV chunks are faster), K a multiple
+ *     of 64 (256 for Q6_K): x is staged once per call as f16 MFMA operand fragments,
+ *     each row scaled by a power of two (RNE) and the rows padded with zeros to a
+ *     multiple of 32; then one MFMA GEMM per weight decodes the GGUF blocks or MLX words
+ *     straight into MFMA operands.  The staging
  *     needs a device workspace of round_up(round_up(rows, 32)*K*2, 256) +
  *     4*round_up(rows, 256) bytes.  The context keeps one
  *     per stream handle, allocated on first use and grown in stream order
@@ -131,8 +132,8 @@ const char* dyninfer_mi355x_last_error(void);
  *     allocates and frees a transient one in stream order, which the captured graph
  *     then does on every replay (the no-allocation variant below avoids that).
  *     A stream that is destroyed while the context lives must have finished its work
- *     first (its handle may be reused by a new stream).  Every other case (Q6_K, MLX
- *     U4, K not a multiple of 64, Q4_0 below 48 rows) runs the GEMV kernels over 16-row
+ *     first (its handle may be reused by a new stream).  Every other case (K not a
+ *     multiple of 64, Q4_0 and Q6_K below 48 rows) runs the GEMV kernels over 16-row
  *     chunks and needs no workspace.
  * Error bound: |y - y_exact| <= 2^-10 * sum_k |w||x| plus f32 accumulation, where a
  * prefill activation more than 2^29 below its row's largest magnitude may also be

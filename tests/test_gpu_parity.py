@@ -404,6 +404,53 @@ def test_gemm_offset_weights(ctx, gtype, m, n, k):
     assert err <= (2.0 ** -10 if gtype == oracle.Q6_K else 2.0 ** -11) + 1e-5, err
 
 
+# MLX affine U4 on the prefill GEMM: every wave tile and K split, group sizes
+# 32 / 64 / 128, every scale dtype, scale and bias rows that start 2 bytes into
+# a dword (K / group odd with 16-bit scales) and component bases 2 bytes into a
+# dword.
+GEMM_MLX_CASES = [
+    (17, 256, 1024, 64, oracle.D_BF16), (33, 512, 2048, 32, oracle.D_F16), (50, 20000, 256, 128, oracle.D_BF16),
+    (100, 300, 1088, 64, oracle.D_BF16), (200, 384, 1024, 32, oracle.D_F32), (512, 3072, 1024, 64, oracle.D_BF16),
+    (512, 1024, 3072, 64, oracle.D_F16), (2048, 3072, 1024, 128, oracle.D_BF16), (2000, 3000, 1024, 64, oracle.D_F32),
+    (300, 200, 4032, 64, oracle.D_BF16),
+]
+
+
+def _mlx_offset(packed, sc, bi, off):
+    """Device copies of the three components, each starting `off` bytes past a
+    4-byte boundary (the packed words stay 4-byte aligned)."""
+    keep = []
+    def place(a, o):
+        buf = torch.zeros(a.nbytes + 16, dtype=torch.uint8, device="cuda")
+        buf[o:o + a.nbytes] = dev(a.view(np.uint8).reshape(-1))
+        keep.append(buf)
+        return buf.data_ptr() + o
+    return place(packed, 0), place(sc, off), place(bi, off), keep
+
+
+@pytest.mark.parametrize("m,n,k,g,sdtype", GEMM_MLX_CASES,
+                         ids=[f"{c[0]}x{c[1]}x{c[2]}-g{c[3]}-s{c[4]}" for c in GEMM_MLX_CASES])
+@pytest.mark.parametrize("off", [0, 2])
+def test_gemm_mlx(ctx, m, n, k, g, sdtype, off):
+    """w = RNE_f16(q·s + b) (s, b taken to f16: exact for bf16/f16 scales in
+    f16's range, one more rounding for f32): 2^-11 with exact bf16
+    activations, 2^-10 with f32 scales."""
+    if off and sdtype == oracle.D_F32:
+        pytest.skip("f32 scales and biases are 4-byte aligned by contract")
+    packed, sc, bi = oracle.synth_mlx_u4(n, k, g, sdtype, seed=m + n + k + g)
+    if off:
+        pw, ps, pb, keep = _mlx_offset(packed, sc, bi, off)
+        w = d.QWeight(d.ENC_MLX_U4, n, k, pw, ps, pb, g, sdtype)
+        w._keep = keep
+    else:
+        w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), g, sdtype)
+    xb = oracle.f32_to_bf16_bits(oracle.randn(m * k, seed=m + 5)).reshape(m, k)
+    x = oracle.bf16_bits_to_f32(xb)
+    y = ctx.qlinear(w, dev(xb).view(torch.bfloat16)).cpu().numpy()
+    err = gemv_err(y, x, oracle.dequant_mlx_u4(packed, sc, bi, sdtype, n, k, g))
+    assert err <= (2.0 ** -10 + 1e-4 if sdtype == oracle.D_F32 else 2.0 ** -11 + 1e-5), err
+
+
 def test_gemm_deterministic(ctx):
     """K-split partial tiles are summed in a fixed slice order: two calls give
     identical bits."""
