@@ -51,6 +51,10 @@ EXPORTED_SYMBOLS = (
     "dyninfer_mi355x_gguf_find", "dyninfer_mi355x_gguf_upload", "dyninfer_mi355x_gguf_qweight",
     "dyninfer_mi355x_candidates_json", "dyninfer_mi355x_registry_select", "dyninfer_mi355x_registry_require",
     "dyninfer_mi355x_version", "dyninfer_mi355x_qlinear_multi_noalloc", "dyninfer_mi355x_precision_check",
+    "dyninfer_mi355x_safetensors_open", "dyninfer_mi355x_safetensors_open_memory", "dyninfer_mi355x_safetensors_close",
+    "dyninfer_mi355x_safetensors_tensor_count", "dyninfer_mi355x_safetensors_metadata_json",
+    "dyninfer_mi355x_safetensors_tensor", "dyninfer_mi355x_safetensors_find", "dyninfer_mi355x_safetensors_upload",
+    "dyninfer_mi355x_safetensors_mlx_qweight",
 )
 
 
@@ -77,6 +81,11 @@ _lib: Optional[ctypes.CDLL] = None
 
 class _GgufTensorC(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("type_code", ctypes.c_uint32), ("n_dims", ctypes.c_uint32),
+                ("dims", ctypes.c_uint64 * 16), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
+
+
+class _StTensorC(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_char_p), ("n_dims", ctypes.c_uint32),
                 ("dims", ctypes.c_uint64 * 16), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
 
 
@@ -117,6 +126,15 @@ def library() -> ctypes.CDLL:
                                                  ctypes.POINTER(SZ)]),
         "dyninfer_mi355x_version": (ctypes.c_char_p, []),
         "dyninfer_mi355x_precision_check": (I, [ctypes.c_char_p, ctypes.c_char_p]),
+        "dyninfer_mi355x_safetensors_open": (I, [ctypes.c_char_p, ctypes.POINTER(P)]),
+        "dyninfer_mi355x_safetensors_open_memory": (I, [P, ctypes.c_uint64, ctypes.c_char_p, ctypes.POINTER(P)]),
+        "dyninfer_mi355x_safetensors_close": (I, [P]),
+        "dyninfer_mi355x_safetensors_tensor_count": (ctypes.c_uint64, [P]),
+        "dyninfer_mi355x_safetensors_metadata_json": (ctypes.c_char_p, [P]),
+        "dyninfer_mi355x_safetensors_tensor": (I, [P, ctypes.c_uint64, ctypes.POINTER(_StTensorC)]),
+        "dyninfer_mi355x_safetensors_find": (I, [P, ctypes.c_char_p, ctypes.POINTER(_StTensorC)]),
+        "dyninfer_mi355x_safetensors_upload": (I, [P, ctypes.c_char_p, P, ctypes.c_uint64, P]),
+        "dyninfer_mi355x_safetensors_mlx_qweight": (I, [P, ctypes.c_char_p, P, P, P, W]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -413,3 +431,87 @@ class GgufFile:
         wc = _QWeightC()
         _check(self._lib.dyninfer_mi355x_gguf_qweight(self._h, name.encode(), _ptr(device_data), ctypes.byref(wc)))
         return QWeight(wc.encoding, wc.rows, wc.cols, device_data, data_bytes=wc.data_bytes)
+
+
+@dataclass
+class StTensor:
+    name: str
+    dtype: str
+    shape: tuple
+    offset: int
+    nbytes: int
+
+
+class SafeTensorsFile:
+    """Index of a .safetensors file (dyninfer_mi355x_safetensors_*): exact byte ranges of its
+    tensors and MLX affine weights from their three components.  ``SafeTensorsFile(path)``
+    maps the file and reads config.json beside it; ``SafeTensorsFile.from_bytes(b, config)``
+    indexes bytes in memory with the text of a config.json (or None)."""
+
+    def __init__(self, path: Optional[str] = None, _data=None, _config: Optional[str] = None):
+        self._lib = library()
+        self._h = ctypes.c_void_p()
+        self._keep = None
+        if _data is not None:
+            self._keep = ctypes.create_string_buffer(bytes(_data), len(_data))
+            cfg = _config.encode() if _config is not None else None
+            _check(self._lib.dyninfer_mi355x_safetensors_open_memory(ctypes.addressof(self._keep), len(_data), cfg,
+                                                                     ctypes.byref(self._h)))
+        else:
+            _check(self._lib.dyninfer_mi355x_safetensors_open(os.fsencode(path), ctypes.byref(self._h)))
+
+    @classmethod
+    def from_bytes(cls, data: bytes, config: Optional[str] = None) -> "SafeTensorsFile":
+        return cls(_data=data, _config=config)
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.dyninfer_mi355x_safetensors_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def _py(t: "_StTensorC") -> StTensor:
+        return StTensor(t.name.decode(), t.dtype.decode(), tuple(t.dims[:t.n_dims]), t.offset, t.nbytes)
+
+    @property
+    def tensors(self) -> list:
+        out = []
+        for i in range(self._lib.dyninfer_mi355x_safetensors_tensor_count(self._h)):
+            t = _StTensorC()
+            _check(self._lib.dyninfer_mi355x_safetensors_tensor(self._h, i, ctypes.byref(t)))
+            out.append(self._py(t))
+        return out
+
+    @property
+    def metadata(self) -> dict:
+        return json.loads(self._lib.dyninfer_mi355x_safetensors_metadata_json(self._h).decode())
+
+    def find(self, name: str) -> StTensor:
+        t = _StTensorC()
+        _check(self._lib.dyninfer_mi355x_safetensors_find(self._h, name.encode(), ctypes.byref(t)))
+        return self._py(t)
+
+    def upload(self, name: str, dst=None, stream=None):
+        """Copy the tensor's exact bytes to the device (a new uint8 tensor unless dst is given)."""
+        import torch
+        if dst is None:
+            dst = torch.empty(max(self.find(name).nbytes, 1), dtype=torch.uint8, device="cuda")
+        cap = dst.numel() * dst.element_size()
+        _check(self._lib.dyninfer_mi355x_safetensors_upload(self._h, name.encode(), dst.data_ptr(), cap,
+                                                            Context._stream(stream)))
+        return dst
+
+    def mlx_qweight(self, weight_name: str, packed, scales, biases) -> QWeight:
+        """QWeight of the MLX affine weight `weight_name` whose three components' bytes are at
+        packed / scales / biases on the device (validated as the reference's MLX convention)."""
+        wc = _QWeightC()
+        _check(self._lib.dyninfer_mi355x_safetensors_mlx_qweight(self._h, weight_name.encode(), _ptr(packed),
+                                                                 _ptr(scales), _ptr(biases), ctypes.byref(wc)))
+        return QWeight(wc.encoding, wc.rows, wc.cols, packed, scales, biases, wc.group_size, wc.scale_dtype,
+                       data_bytes=wc.data_bytes, scales_bytes=wc.scales_bytes, biases_bytes=wc.biases_bytes)

@@ -21,7 +21,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 SOURCES = [
     "gemv_q6_k.hip", "gemv_q4_0.hip", "gemv_q4_1.hip", "gemv_q8_0.hip", "gemv_mlx_u4.hip",
     "gemv.hip", "gemv_mfma.hip", "gemm.hip", "xprep.hip", "dequant.hip", "embedding.hip",
-    "capi.cpp", "registry.cpp", "gguf.cpp",
+    "capi.cpp", "registry.cpp", "gguf.cpp", "safetensors.cpp",
 ]
 COMMON = [
     "--offload-arch=gfx950",

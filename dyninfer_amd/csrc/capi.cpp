@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "gguf.hpp"
+#include "safetensors.hpp"
 #include "kernels.hpp"
 #include "registry.hpp"
 
@@ -569,6 +570,137 @@ int dyninfer_mi355x_gguf_qweight(const dyninfer_gguf_t* g, const char* name, con
     out->cols = t->shape[1];
     out->data = device_data;
     out->data_bytes = t->nbytes;
+    return check_weight(out);
+}
+
+struct dyninfer_safetensors {
+    dmx::StIndex idx;
+};
+
+static int st_finish(const uint8_t* base, uint64_t len, void* map, const char* config, dyninfer_safetensors_t** out) {
+    auto* t = new dyninfer_safetensors();
+    t->idx.map = map;
+    t->idx.len = len;  // the mapping's length, so a failed index still unmaps it
+    const std::string err = dmx::st_index(base, len, t->idx);
+    if (!err.empty()) {
+        dyninfer_mi355x_safetensors_close(t);
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "invalid SafeTensors: " + err);
+    }
+    if (config) dmx::st_merge_config(t->idx, config);
+    *out = t;
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_safetensors_open(const char* path, dyninfer_safetensors_t** out) {
+    if (!path || !out) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "path / out is NULL");
+    *out = nullptr;
+    const int fd = ::open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string("cannot open ") + path + ": " + std::strerror(errno));
+    struct stat st;
+    if (::fstat(fd, &st) != 0 || st.st_size <= 0) {
+        ::close(fd);
+        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, std::string("invalid SafeTensors: empty or unreadable file ") + path);
+    }
+    void* m = ::mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);
+    if (m == MAP_FAILED) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string("mmap failed: ") + std::strerror(errno));
+    // the sibling config.json (config_json.rs:10-20); an unreadable one is ignored
+    std::string cfg_path(path), cfg;
+    const size_t slash = cfg_path.rfind('/');
+    cfg_path = (slash == std::string::npos ? std::string() : cfg_path.substr(0, slash + 1)) + "config.json";
+    bool have_cfg = false;
+    if (FILE* f = std::fopen(cfg_path.c_str(), "rb")) {
+        char buf[4096];
+        size_t got;
+        while ((got = std::fread(buf, 1, sizeof buf, f)) > 0) cfg.append(buf, got);
+        have_cfg = !std::ferror(f);
+        std::fclose(f);
+    }
+    return st_finish(static_cast<const uint8_t*>(m), (uint64_t)st.st_size, m, have_cfg ? cfg.c_str() : nullptr, out);
+}
+
+int dyninfer_mi355x_safetensors_open_memory(const void* data, uint64_t len, const char* config_json,
+                                            dyninfer_safetensors_t** out) {
+    if (!data || !out) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "data / out is NULL");
+    *out = nullptr;
+    return st_finish(static_cast<const uint8_t*>(data), len, nullptr, config_json, out);
+}
+
+int dyninfer_mi355x_safetensors_close(dyninfer_safetensors_t* t) {
+    if (!t) return DYNINFER_MI355X_OK;
+    if (t->idx.map) ::munmap(t->idx.map, (size_t)t->idx.len);
+    delete t;
+    return DYNINFER_MI355X_OK;
+}
+
+uint64_t dyninfer_mi355x_safetensors_tensor_count(const dyninfer_safetensors_t* t) { return t ? t->idx.tensors.size() : 0; }
+
+const char* dyninfer_mi355x_safetensors_metadata_json(const dyninfer_safetensors_t* t) {
+    return t ? t->idx.metadata_json.c_str() : "{}";
+}
+
+static void st_fill(const dmx::StTensor& t, dyninfer_st_tensor_t* out) {
+    std::memset(out, 0, sizeof *out);
+    out->name = t.name.c_str();
+    out->dtype = t.dtype.c_str();
+    out->n_dims = (uint32_t)t.shape.size();
+    for (size_t i = 0; i < t.shape.size(); i++) out->dims[i] = t.shape[i];
+    out->offset = t.offset;
+    out->nbytes = t.nbytes;
+}
+
+int dyninfer_mi355x_safetensors_tensor(const dyninfer_safetensors_t* t, uint64_t index, dyninfer_st_tensor_t* out) {
+    if (!t || !out) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "index / out is NULL");
+    if (index >= t->idx.tensors.size()) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "tensor index out of range");
+    st_fill(t->idx.tensors[index], out);
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_safetensors_find(const dyninfer_safetensors_t* t, const char* name, dyninfer_st_tensor_t* out) {
+    if (!t || !name || !out) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "index / name / out is NULL");
+    const dmx::StTensor* e = dmx::st_find(t->idx, name);
+    if (!e) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string("no tensor named ") + name);
+    st_fill(*e, out);
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_safetensors_upload(const dyninfer_safetensors_t* t, const char* name, void* dst, uint64_t dst_bytes,
+                                       void* stream) {
+    if (!t || !name || !dst) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "index / name / dst is NULL");
+    const dmx::StTensor* e = dmx::st_find(t->idx, name);
+    if (!e) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string("no tensor named ") + name);
+    if (dst_bytes < e->nbytes)
+        return fail(DYNINFER_MI355X_ERR_BUFFER_TOO_SMALL, "destination needs " + std::to_string(e->nbytes) + " bytes");
+    if (e->nbytes == 0) return DYNINFER_MI355X_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t err = hipMemcpyAsync(dst, t->idx.base + e->offset, (size_t)e->nbytes, hipMemcpyHostToDevice, st);
+    if (err != hipSuccess) return hip_fail(err, "hipMemcpyAsync");
+    err = hipStreamSynchronize(st);
+    if (err != hipSuccess) return hip_fail(err, "hipStreamSynchronize");
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_safetensors_mlx_qweight(const dyninfer_safetensors_t* t, const char* weight_name,
+                                            const void* device_packed, const void* device_scales,
+                                            const void* device_biases, dyninfer_qweight_t* out) {
+    if (!t || !weight_name || !out) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "index / name / out is NULL");
+    const dmx::StTensor *p = nullptr, *s = nullptr, *b = nullptr;
+    uint64_t n = 0, k = 0, g = 0;
+    const std::string err = dmx::st_mlx_weight(t->idx, weight_name, &p, &s, &b, &n, &k, &g);
+    if (!err.empty()) return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, err);
+    if (g > UINT32_MAX) return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "group size out of range");
+    std::memset(out, 0, sizeof *out);
+    out->encoding = DYNINFER_ENC_MLX_AFFINE_U4;
+    out->group_size = (uint32_t)g;
+    out->rows = n;
+    out->cols = k;
+    out->data = device_packed;
+    out->scales = device_scales;
+    out->biases = device_biases;
+    out->scale_dtype = s->dtype == "F32" ? DYNINFER_DTYPE_F32 : s->dtype == "F16" ? DYNINFER_DTYPE_F16 : DYNINFER_DTYPE_BF16;
+    out->data_bytes = p->nbytes;
+    out->scales_bytes = s->nbytes;
+    out->biases_bytes = b->nbytes;
     return check_weight(out);
 }
 

@@ -15,12 +15,6 @@
 
 namespace dmx {
 
-namespace {
-
-// InspectionLimits::default() (crates/dyninfer-checkpoint/src/limits.rs)
-constexpr uint64_t kMaxHeaderBytes = 64ull << 20, kMaxTensors = 1000000, kMaxEntries = 1000000;
-constexpr uint64_t kMaxKeyLen = 16 * 1024, kMaxRank = 16, kMaxDim = 1ull << 40;
-
 // Well-formed UTF-8 (RFC 3629: no overlong forms, no surrogates, at most
 // U+10FFFF), the check Rust's String::from_utf8 makes (container.rs:62-81).
 bool valid_utf8(const uint8_t* s, uint64_t n) {
@@ -44,6 +38,13 @@ bool valid_utf8(const uint8_t* s, uint64_t n) {
     }
     return true;
 }
+
+namespace {
+
+// InspectionLimits::default() (crates/dyninfer-checkpoint/src/limits.rs)
+constexpr uint64_t kMaxHeaderBytes = 64ull << 20, kMaxTensors = 1000000, kMaxEntries = 1000000;
+constexpr uint64_t kMaxKeyLen = 16 * 1024, kMaxRank = 16, kMaxDim = 1ull << 40;
+
 
 struct Cursor {
     const uint8_t* p;

@@ -30,6 +30,9 @@ struct GgufIndex {
 // (1 for plain scalar types) and bytes per block; false for an unknown code.
 bool gguf_type_geometry(uint32_t code, uint64_t* block, uint64_t* bytes);
 
+// Well-formed UTF-8 (RFC 3629), the check Rust's String::from_utf8 makes.
+bool valid_utf8(const uint8_t* s, uint64_t n);
+
 // Parses base[0, len) into idx (tensors, metadata).  Returns "" or an error message.
 std::string gguf_index(const uint8_t* base, uint64_t len, GgufIndex& idx);
 

@@ -239,6 +239,57 @@ int dyninfer_mi355x_gguf_qweight(const dyninfer_gguf_t* g, const char* name, con
                                  dyninfer_qweight_t* out);
 
 /*
+ * SafeTensors container index and the MLX affine convention: the exact byte range of
+ * every tensor of a .safetensors file, and an MLX quantized weight described from its
+ * three components (`<stem>.weight` packed u32, `<stem>.scales`, `<stem>.biases`), so
+ * each reaches the device as a plain copy of its on-disk bytes.  Restates the
+ * reference's indexer (crates/dyninfer-checkpoint-safetensors/src/container.rs: 8-byte
+ * little-endian header length of 1..64 MiB, JSON object header with "__metadata__",
+ * dtype/shape/data_offsets per tensor, byte length = numel x element size, ranges inside
+ * the file and not overlapping, the default inspection limits of
+ * crates/dyninfer-checkpoint/src/limits.rs) and the MLX convention
+ * (crates/dyninfer-checkpoint-safetensors/src/mlx.rs:17-261: metadata `format` "mlx",
+ * mlx.quantization.bits / group_size from __metadata__ or from the sibling config.json's
+ * quantization(_config) object, config_json.rs:129-143).  Tensors are listed sorted by
+ * name.  A repeated tensor name is rejected (the reference's JSON map keeps the last).
+ */
+typedef struct dyninfer_safetensors dyninfer_safetensors_t;
+
+typedef struct dyninfer_st_tensor {
+    const char* name;   /* NUL-terminated, owned by the index */
+    const char* dtype;  /* SafeTensors dtype string ("U32", "BF16", ...), owned by the index */
+    uint32_t n_dims;
+    uint64_t dims[16];  /* row-major shape */
+    uint64_t offset;    /* absolute byte offset of the tensor's data in the file */
+    uint64_t nbytes;    /* exact byte length */
+} dyninfer_st_tensor_t;
+
+/* Maps the file read-only, indexes it, and reads config.json beside it if present.  */
+int dyninfer_mi355x_safetensors_open(const char* path, dyninfer_safetensors_t** out);
+/* Indexes caller-owned bytes (they must outlive the index); config_json is the text of
+ * the checkpoint's config.json, or NULL.  */
+int dyninfer_mi355x_safetensors_open_memory(const void* data, uint64_t len, const char* config_json,
+                                            dyninfer_safetensors_t** out);
+int dyninfer_mi355x_safetensors_close(dyninfer_safetensors_t* t);
+uint64_t dyninfer_mi355x_safetensors_tensor_count(const dyninfer_safetensors_t* t);
+/* __metadata__ plus the config.json quantization keys, one JSON object (keys sorted). */
+const char* dyninfer_mi355x_safetensors_metadata_json(const dyninfer_safetensors_t* t);
+int dyninfer_mi355x_safetensors_tensor(const dyninfer_safetensors_t* t, uint64_t index, dyninfer_st_tensor_t* out);
+int dyninfer_mi355x_safetensors_find(const dyninfer_safetensors_t* t, const char* name, dyninfer_st_tensor_t* out);
+/* Copies the tensor's exact bytes to device memory dst (dst_bytes >= nbytes) on `stream`,
+ * then waits for the copy (the source is pageable mapped memory).  */
+int dyninfer_mi355x_safetensors_upload(const dyninfer_safetensors_t* t, const char* name, void* dst,
+                                       uint64_t dst_bytes, void* stream);
+/* Validates the MLX weight `weight_name` (a ".weight" tensor) as decode_affine_weight
+ * (mlx.rs:152-261: u32 storage, scales and biases of one float type f16/bf16/f32, shapes
+ * [N, K/group] with K = packed_last * 32 / bits) plus this library's limits (4-bit codes,
+ * rank 2), and describes the three components uploaded at device_packed / device_scales /
+ * device_biases as a dyninfer_qweight_t (rows N, cols K, byte lengths the tensors'). */
+int dyninfer_mi355x_safetensors_mlx_qweight(const dyninfer_safetensors_t* t, const char* weight_name,
+                                            const void* device_packed, const void* device_scales,
+                                            const void* device_biases, dyninfer_qweight_t* out);
+
+/*
  * 1 if (w, rows, x_dtype, y_dtype) is inside the qualified envelope, else 0 (and
  * last_error says why).  Host-only; same rules as the validation in
  * q4_0.rs:40-113 / gguf_block.rs:66-156 / mlx_affine.rs:55-155 plus this
