@@ -369,10 +369,14 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     // (bits shifted down for 16-bit types; it holds a byte of the value, so
     // it stays in the value's page)
     const uint32_t es = p.sdtype == DT_F32 ? 4u : 2u, gpr = p.K / (p.group ? p.group : 1u);
-    auto sbload = [&](const uint8_t* base, uint32_t idx) {
-        const uint32_t o = idx * es;
-        const uint32_t v = *gptr<uint32_t>(base + (o & ~3u));
-        return es == 4u ? v : (v >> (8u * (o & 3u))) & 0xFFFFu;
+    // (the raw dword: the 16-bit value is shifted out where it is used, so a
+    // refill load is not waited for at its issue)
+    auto sbload = [&](const uint8_t* base, uint32_t idx) { return *gptr<uint32_t>(base + ((idx * es) & ~3u)); };
+    // the scale/bias groups of task t for this lane: k 64q..64q+31 and 64q+32..64q+63
+    auto sbgroups = [&](const Rows& r, uint32_t t, uint32_t& g0, uint32_t& g1) {
+        const uint32_t kl = k0 + (t < nt ? t : nt - 1u) * M::KT + 64u * q;
+        g0 = r.rowm * gpr + kl / p.group;
+        g1 = r.rowm * gpr + (kl + 32u) / p.group;
     };
     auto load = [&](const Rows& r, uint32_t t, u32x4 (&v)[NLD], uint32_t (&aux)[4]) {
 #pragma unroll
@@ -381,56 +385,68 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
             v[i] = *gptr<u32x4>(r.abase + (o & ~3u) + M::goff(pc[i], o & 3u));
         }
         if constexpr (M::MLX) {
-            // groups of the lane's k 64q..64q+31 and 64q+32..64q+63
-            const uint32_t kl = k0 + (t < nt ? t : nt - 1u) * M::KT + 64u * q;
-            const uint32_t g0 = r.rowm * gpr + kl / p.group, g1 = r.rowm * gpr + (kl + 32u) / p.group;
+            uint32_t g0, g1;
+            sbgroups(r, t, g0, g1);
             aux[0] = sbload(r.sc, g0);
             aux[1] = sbload(r.bi, g0);
             aux[2] = sbload(r.sc, g1);
             aux[3] = sbload(r.bi, g1);
         }
     };
-    // the first PF tasks' weight loads leave before the activations are staged
-    Where wcur = where(tile_at(0u));
-    Rows rcur = rows_of(wcur);
-    u32x4 ring[PF][NLD];
-    uint32_t rx[PF][4];
-#pragma unroll
-    for (int s = 0; s < PF; s++) load(rcur, t0 + (uint32_t)s, ring[s], rx[s]);  // tpw >= PF: all in tile 0
-
     // ---- stage the activations: unit u = (task g, row b, e = q·NM + j); the
     // 32 units of (g, b) lie on consecutive lanes, their maximum reduced by
     // DPP within rows of 16 lanes and v_permlane16_swap across two.  Chunks
     // of passes: all of a chunk's loads leave before the first is converted.
-    const uint32_t nunits = ng * 16u * UPR, npass = (nunits + kMfmaThreads - 1u) / kMfmaThreads;
-    auto xload = [&](uint32_t pass, float (&v)[8]) {
+    // only the segment's real tasks: padding tasks are never multiplied
+    const uint32_t nunits = nt * 16u * UPR, npass = (nunits + kMfmaThreads - 1u) / kMfmaThreads;
+    // A unit's raw activations, loaded unconditionally (a unit past the tasks
+    // or the batch reads row 0, in bounds, and stages zeros): a load under a
+    // per-lane branch would make its wave wait for it where the branch joins,
+    // before the weight loads that follow are issued.
+    struct XRaw {
+        uint32_t w[8];  // bf16: two runs of 4 in w[0..3]; f32: w[0..7]
+        bool ok;
+    };
+    auto xload = [&](auto xb, uint32_t pass, XRaw& r) {
+        constexpr bool XB = decltype(xb)::value;
         const uint32_t u = pass * kMfmaThreads + tid;
         const uint32_t g = u / (16u * UPR), b = (u / UPR) % 16u, e = u % UPR, qq = e / NM, j = e % NM;
+        r.ok = u < nunits && b < p.batch && g < nt;
+        const size_t xk0 = r.ok ? (size_t)b * p.K + k0 + M::KT * g : 0u;
+        if constexpr (XB) {  // two runs of 4 bf16: 8 bytes each
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            const uint16_t* xr = static_cast<const uint16_t*>(p.x) + xk0;
+            const u32x2 lo2 = *gptr<u32x2>(xr + M::run0(qq, j)), hi2 = *gptr<u32x2>(xr + M::run1(qq, j));
+            r.w[0] = lo2[0];
+            r.w[1] = lo2[1];
+            r.w[2] = hi2[0];
+            r.w[3] = hi2[1];
+        } else {
+            const float* xr = static_cast<const float*>(p.x) + xk0;
+            const f32x4 lo4 = *gptr<f32x4>(xr + M::run0(qq, j)), hi4 = *gptr<f32x4>(xr + M::run1(qq, j));
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = 0.0f;
-        if (u < nunits && b < p.batch && g < nt) {
-            const size_t xk0 = (size_t)b * p.K + k0 + M::KT * g;
-            if (p.x_bf16) {  // two runs of 4 bf16: 8 bytes each
-                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-                const uint16_t* xr = static_cast<const uint16_t*>(p.x) + xk0;
-                const u32x2 lo2 = *gptr<u32x2>(xr + M::run0(qq, j)), hi2 = *gptr<u32x2>(xr + M::run1(qq, j));
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    v[2 * i] = __uint_as_float(lo2[i] << 16);
-                    v[2 * i + 1] = __uint_as_float(lo2[i] & 0xFFFF0000u);
-                    v[4 + 2 * i] = __uint_as_float(hi2[i] << 16);
-                    v[5 + 2 * i] = __uint_as_float(hi2[i] & 0xFFFF0000u);
-                }
-            } else {
-                const float* xr = static_cast<const float*>(p.x) + xk0;
-                const f32x4 lo4 = *gptr<f32x4>(xr + M::run0(qq, j)), hi4 = *gptr<f32x4>(xr + M::run1(qq, j));
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    v[i] = lo4[i];
-                    v[4 + i] = hi4[i];
-                }
+            for (int i = 0; i < 4; i++) {
+                r.w[i] = __float_as_uint(lo4[i]);
+                r.w[4 + i] = __float_as_uint(hi4[i]);
             }
         }
+    };
+    // the unit's 8 activations as f32 (zeros for a unit staged as padding)
+    auto xvals = [&](auto xb, const XRaw& r, float (&v)[8]) {
+        if constexpr (decltype(xb)::value) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                v[2 * i] = __uint_as_float(r.w[i] << 16);
+                v[2 * i + 1] = __uint_as_float(r.w[i] & 0xFFFF0000u);
+                v[4 + 2 * i] = __uint_as_float(r.w[2 + i] << 16);
+                v[5 + 2 * i] = __uint_as_float(r.w[2 + i] & 0xFFFF0000u);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = __uint_as_float(r.w[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = r.ok ? v[i] : 0.0f;
     };
     auto xstore = [&](uint32_t pass, const float (&v)[8]) {
         const uint32_t u = pass * kMfmaThreads + tid;
@@ -466,14 +482,47 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     };
     static_assert(UPR == 32, "a (task, row) spans two rows of 16 lanes");
     constexpr uint32_t kStageChunk = M::STAGE;
-    for (uint32_t c0 = 0; c0 < npass; c0 += kStageChunk) {
-        float v[kStageChunk][8];
+    // The first chunk's activation loads leave first, then the first PF
+    // tasks' weight loads: loads complete in issue order, so the staging
+    // converts while the weights are in flight (weights first made every wave
+    // wait for its weights before its first conversion: 1024x2048 MLX at 16
+    // rows staged in 4.0 us).
+    Where wcur = where(tile_at(0u));
+    Rows rcur = rows_of(wcur);
+    u32x4 ring[PF][NLD];
+    uint32_t rx[PF][4];
+    // one copy of the staging per activation dtype (a dtype test per load
+    // would join its two arms, and wait for the loads, at every unit)
+    auto stage = [&](auto xb) {
+        {
+            XRaw r[kStageChunk];
 #pragma unroll
-        for (uint32_t i = 0; i < kStageChunk; i++) xload(c0 + i < npass ? c0 + i : npass - 1u, v[i]);
+            for (uint32_t i = 0; i < kStageChunk; i++) xload(xb, i < npass ? i : npass - 1u, r[i]);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (uint32_t i = 0; i < kStageChunk; i++)
-            if (c0 + i < npass) xstore(c0 + i, v[i]);
-    }
+            for (int s = 0; s < PF; s++) load(rcur, t0 + (uint32_t)s, ring[s], rx[s]);  // tpw >= PF: all in tile 0
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (uint32_t i = 0; i < kStageChunk; i++) {
+                float v[8];
+                xvals(xb, r[i], v);
+                if (i < npass) xstore(i, v);
+            }
+        }
+        for (uint32_t c0 = kStageChunk; c0 < npass; c0 += kStageChunk) {
+            XRaw r[kStageChunk];
+#pragma unroll
+            for (uint32_t i = 0; i < kStageChunk; i++) xload(xb, c0 + i < npass ? c0 + i : npass - 1u, r[i]);
+#pragma unroll
+            for (uint32_t i = 0; i < kStageChunk; i++) {
+                float v[8];
+                xvals(xb, r[i], v);
+                if (c0 + i < npass) xstore(c0 + i, v);
+            }
+        }
+    };
+    if (p.x_bf16) stage(std::true_type{});
+    else stage(std::false_type{});
     __syncthreads();
 
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -491,9 +540,11 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
         for (uint32_t j = 0; j < NM; j++) xa[j] = xl[(t * NM + j) * 64u + xslot(lane, j)];
         uint4 a[NM];
         if constexpr (M::MLX) {
-            uint32_t ax[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) ax[i] = t < nt ? aux[i] : 0u;  // padding task: zero scale and bias
+            uint32_t g0, g1;
+            sbgroups(r, t, g0, g1);
+            const uint32_t sh0 = 8u * ((g0 * es) & 3u), sh1 = 8u * ((g1 * es) & 3u);
+            auto val = [&](uint32_t raw, uint32_t sh) { return es == 4u ? raw : (raw >> sh) & 0xFFFFu; };
+            const uint32_t ax[4] = {val(aux[0], sh0), val(aux[1], sh0), val(aux[2], sh1), val(aux[3], sh1)};
             M::decode(reinterpret_cast<const u32a*>(win + m * M::WB), q, ax, p.sdtype, a);
         } else {
             M::decode(reinterpret_cast<const u32a*>(win + m * M::WB), task_off(r.om, t) & 3u, t < nt, q, a, rs);
@@ -510,33 +561,48 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     // window, with the tasks PF later, which cross into the next tile at the
     // end of one.  Each tile's outputs are stored after its last task, outside
     // the loop whose loads stay in flight: no load sits under a branch.
-    for (uint32_t i = 0; i < ntw; i++) {
-        const Where wnxt = where(tile_at(i + 1u));
-        const Rows rnxt = rows_of(wnxt);
-        for (uint32_t g0 = 0; g0 < tpw; g0 += PF) {
+    // One round: the PF tasks from g0 of the current tile (padding tasks, past
+    // the segment's last and wave-uniform, are loaded like the others but
+    // neither staged nor multiplied), then, with REFILL, their slots reloaded
+    // in place (the same registers across rounds: no copies that would wait
+    // for the loads) with the tasks PF later, which cross into the next tile
+    // at the end of one.  The wave's last round loads nothing: a wave's end
+    // waits for its loads in flight, which on launches of one tile per wave
+    // were a whole extra round of loads (it is peeled, not branched around,
+    // so every wait of the loop keeps its count).
+    auto round = [&](uint32_t g0, const Rows& rnxt, auto refill) {
 #pragma unroll
-            for (int s = 0; s < PF; s += M::TPI) {
-                const uint32_t g = t0 + g0 + (uint32_t)s;
-                f32x4 prd[M::TPI];
-                float rs[M::TPI] = {};
+        for (int s = 0; s < PF; s += M::TPI) {
+            const uint32_t g = t0 + g0 + (uint32_t)s;
+            f32x4 prd[M::TPI];
+            float rs[M::TPI] = {};
 #pragma unroll
-                for (int k = 0; k < M::TPI; k++) prd[k] = product(ring[s + k], rx[s + k], rcur, g + (uint32_t)k, rs[k]);
-                // refill the slots in place (the same registers across
-                // iterations: no copies that would wait for the loads)
+            for (int k = 0; k < M::TPI; k++)
+                if (g + (uint32_t)k < nt) prd[k] = product(ring[s + k], rx[s + k], rcur, g + (uint32_t)k, rs[k]);
+            if constexpr (decltype(refill)::value) {
                 const bool wrap = g0 + (uint32_t)s + PF >= tpw;  // the refills belong to the next tile
                 const uint32_t gn = wrap ? g + PF - tpw : g + PF;
 #pragma unroll
                 for (int k = 0; k < M::TPI; k++) load(wrap ? rnxt : rcur, gn + (uint32_t)k, ring[s + k], rx[s + k]);
+            }
 #pragma unroll
-                for (int k = 0; k < M::TPI; k++) {
-                    // inverse activation scales of rows 4q..4q+3
-                    f32x4 sc = *reinterpret_cast<const f32x4*>(inv + (g + (uint32_t)k) * 16u + 4u * q);
-                    if constexpr (M::ROWSCALE) sc *= rs[k];
+            for (int k = 0; k < M::TPI; k++) {
+                if (g + (uint32_t)k >= nt) continue;
+                // inverse activation scales of rows 4q..4q+3
+                f32x4 sc = *reinterpret_cast<const f32x4*>(inv + (g + (uint32_t)k) * 16u + 4u * q);
+                if constexpr (M::ROWSCALE) sc *= rs[k];
 #pragma unroll
-                    for (int c = 0; c < 4; c++) acc[c] = fmaf(prd[k][c], sc[c], acc[c]);
-                }
+                for (int c = 0; c < 4; c++) acc[c] = fmaf(prd[k][c], sc[c], acc[c]);
             }
         }
+    };
+    for (uint32_t i = 0; i < ntw; i++) {
+        const Where wnxt = where(tile_at(i + 1u));
+        const Rows rnxt = rows_of(wnxt);
+        const bool last = i + 1u == ntw;
+        const uint32_t gend = last ? tpw - PF : tpw;  // rounds that reload
+        for (uint32_t g0 = 0; g0 < gend; g0 += PF) round(g0, rnxt, std::true_type{});
+        if (last) round(tpw - PF, rnxt, std::false_type{});
         if constexpr (SPLIT) {
             // the waves' partial tiles meet in their windows (a wave's last
             // window reads precede these writes: in order); wave 0 adds and
