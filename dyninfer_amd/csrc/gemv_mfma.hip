@@ -650,6 +650,10 @@ namespace {
 // few microseconds, before its first product: lm_head 124 us whole tiles,
 // 148 us split, 690 us VALU).
 constexpr uint32_t kMfmaMinTiles = 384;
+// When the VALU GEMV would take two register passes (more rows than one
+// holds), whole tiles pay from fewer tiles: MLX q/k/v (4096 x 1024, 256
+// tiles) at 16 rows 14.4 us on VALU (two launches), 11.4 us on MFMA.
+constexpr uint32_t kMfmaMinTilesTwoPasses = 128;
 constexpr uint32_t kMfmaSplitTiles = 1024;
 
 // Units per launch: the fewest segments whose LDS fits, whole tasks each
@@ -725,11 +729,16 @@ hipError_t launch_mode(MfmaParams p, uint32_t units, bool y_bf16, hipStream_t st
 }
 
 template <class M>
-int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16);
+int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16, uint32_t min_tiles);
+
+uint32_t mfma_min_tiles(uint32_t enc, uint32_t batch) {
+    return batch > max_register_batch(enc) ? kMfmaMinTilesTwoPasses : kMfmaMinTiles;
+}
 
 template <class M>
-hipError_t launch_mfma(const GemvProblem* probs, int nprob, uint32_t K, const void* x, bool x_bf16, uint32_t batch,
-                       bool y_bf16, uint32_t group, uint32_t sdtype, hipStream_t st) {
+hipError_t launch_mfma(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x, bool x_bf16,
+                       uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype, hipStream_t st) {
+    const uint32_t min_tiles = mfma_min_tiles(enc, batch);
     MfmaParams p = {};
     uint32_t tiles = 0;
     for (int i = 0; i < kMaxProblems; i++) {
@@ -751,21 +760,21 @@ hipError_t launch_mfma(const GemvProblem* probs, int nprob, uint32_t K, const vo
     p.group = group;
     p.sdtype = sdtype;
     const uint32_t units = K / M::UNIT;
-    return mfma_mode<M>(K, tiles, y_bf16) == 2 ? launch_mode<M, true>(p, units, y_bf16, st)
-                                       : launch_mode<M, false>(p, units, y_bf16, st);
+    return mfma_mode<M>(K, tiles, y_bf16, min_tiles) == 2 ? launch_mode<M, true>(p, units, y_bf16, st)
+                                                  : launch_mode<M, false>(p, units, y_bf16, st);
 }
 
 // 2: split mode, 1: whole tiles per wave, 0: not on MFMA (with bf16 outputs
 // only a single segment)
 template <class M>
-int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16) {
+int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16, uint32_t min_tiles) {
     const uint32_t units = K / M::UNIT;
     if (tiles < kMfmaSplitTiles) {
         const uint32_t seg = mfma_segment<M, true>(units);
         if (seg / M::UPT >= 8u && (!y_bf16 || seg == units)) return 2;
     }
     const uint32_t seg = mfma_segment<M, false>(units);
-    return tiles >= kMfmaMinTiles && seg > 0 && (!y_bf16 || seg == units) ? 1 : 0;
+    return tiles >= min_tiles && seg > 0 && (!y_bf16 || seg == units) ? 1 : 0;
 }
 
 }  // namespace
@@ -792,18 +801,19 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     const uint64_t bytes = rows * (enc == ENC_Q4_0 ? K / 32u * 18u : enc == ENC_Q6_K ? K / 256u * 210u : K / 2u);
     if (batch < 5 && tiles < kMfmaSplitTiles) return false;
     if (batch <= max_register_batch(enc) && bytes < (8ull << 20) && tiles < kMfmaSplitTiles) return false;
-    const int mode = enc == ENC_Q4_0   ? mfma_mode<MfmaQ40>(K, tiles, y_bf16)
-                   : enc == ENC_Q6_K   ? mfma_mode<MfmaQ6K>(K, tiles, y_bf16)
-                                       : mfma_mode<MfmaMlxU4>(K, tiles, y_bf16);
+    const uint32_t min_tiles = mfma_min_tiles(enc, batch);
+    const int mode = enc == ENC_Q4_0   ? mfma_mode<MfmaQ40>(K, tiles, y_bf16, min_tiles)
+                   : enc == ENC_Q6_K   ? mfma_mode<MfmaQ6K>(K, tiles, y_bf16, min_tiles)
+                                       : mfma_mode<MfmaMlxU4>(K, tiles, y_bf16, min_tiles);
     return mode != 0;
 }
 
 hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x, bool x_bf16,
                             uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype, hipStream_t st) {
     if (nprob < 1 || nprob > kMaxProblems) return hipErrorInvalidValue;
-    if (enc == ENC_Q4_0) return launch_mfma<MfmaQ40>(probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
-    if (enc == ENC_Q6_K) return launch_mfma<MfmaQ6K>(probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
-    if (enc == ENC_MLX_U4) return launch_mfma<MfmaMlxU4>(probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
+    if (enc == ENC_Q4_0) return launch_mfma<MfmaQ40>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
+    if (enc == ENC_Q6_K) return launch_mfma<MfmaQ6K>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
+    if (enc == ENC_MLX_U4) return launch_mfma<MfmaMlxU4>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     return hipErrorInvalidValue;
 }
 

@@ -163,6 +163,8 @@ MFMA_CASES = [
     (oracle.Q4_0, 4096, 4096, 8, True, 0),
     # 3-4 rows: only launches of >= 1024 tiles
     (oracle.Q6_K, 17000, 1024, 4, False, 0), (oracle.Q4_0, 20480, 1024, 3, True, 2),
+    # more rows than one VALU register pass: whole tiles from 128 tiles
+    (oracle.Q4_0, 2048, 1024, 12, False, 0), (oracle.Q6_K, 2570, 1024, 8, True, 2),
 ]
 
 
@@ -275,6 +277,7 @@ MLX_MFMA_CASES = [
     (1024, 3072, 64, oracle.D_F16, 12, True), (3072, 2048, 32, oracle.D_F32, 16, True),
     (2048, 4096, 128, oracle.D_BF16, 9, False), (4100, 2048, 64, oracle.D_BF16, 9, False),
     (20000, 1024, 64, oracle.D_BF16, 4, True),
+    (4096, 1024, 64, oracle.D_BF16, 16, True),  # 256 tiles, whole tiles (two VALU passes at 16 rows)
 ]
 
 
