@@ -2,7 +2,7 @@
  * CPU oracle for the quantized weight-matmul path — TEST INFRASTRUCTURE ONLY.
  *
  * This file restates, in plain C, the arithmetic the reference (goniz/dyninfer)
- * defines for GGUF Q4_0 / Q4_1 / Q8_0 / Q6_K blocks and MLX affine-U4 groups,
+ * defines for GGUF Q4_0 / Q4_1 / Q8_0 / Q6_K (and Q4_K) blocks and MLX affine-U4 groups,
  * plus the reference's deterministic fixture helpers (LCG fill, packers).
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
  * it, and only as the checker (or the timed CPU baseline).  The product path
@@ -21,7 +21,7 @@
 #include <omp.h>
 
 /* GGML type codes, crates/dyninfer-checkpoint-gguf/src/types.rs:10-43. */
-enum { T_Q4_0 = 2, T_Q4_1 = 3, T_Q8_0 = 8, T_Q6_K = 14 };
+enum { T_Q4_0 = 2, T_Q4_1 = 3, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
 /* Scale / activation dtypes used by this oracle. */
 enum { D_F32 = 0, D_F16 = 1, D_BF16 = 2 };
 
@@ -269,11 +269,52 @@ static void dq_q6_k(const uint8_t* blk, float* out) {
                     }
 }
 
+/* Q4_K (GGUF type 12; the reference declares its schema only,
+ * gguf_block.rs:183-316 SCHEMA_ONLY_DEFINITIONS "q4_k" 256 weights / 144 bytes
+ * [scale_min_f16, scales_and_mins_u6, quants_u4]).  Restated from GGML's
+ * published layout (block_q4_K, dequantize_row_q4_K): d = f16 bytes 0..2,
+ * dmin = f16 bytes 2..4, scales[12] = bytes 4..16, qs[128] = bytes 16..144.
+ * Sub-block j (32 weights) has a 6-bit scale sc_j and min m_j:
+ *   j < 4:  sc = scales[j] & 63,  m = scales[j + 4] & 63
+ *   j >= 4: sc = (scales[j + 4] & 15) | ((scales[j - 4] >> 6) << 4),
+ *           m  = (scales[j + 4] >> 4) | ((scales[j] >> 6) << 4)
+ * Weights 64i + l and 64i + 32 + l (i < 4, l < 32) are the low and high
+ * nibbles of qs[32i + l], in sub-blocks 2i and 2i + 1:
+ *   w = (d * sc_j) * q - (dmin * m_j)
+ * d * sc and dmin * m are exact in f32 (11-bit x 6-bit significands), so is
+ * their product with q (4 more bits): one rounding, at the subtraction. */
+static void q4_k_scale_min(const uint8_t* sc12, int j, int* sc, int* m) {
+    if (j < 4) {
+        *sc = sc12[j] & 63;
+        *m = sc12[j + 4] & 63;
+    } else {
+        *sc = (sc12[j + 4] & 15) | ((sc12[j - 4] >> 6) << 4);
+        *m = (sc12[j + 4] >> 4) | ((sc12[j] >> 6) << 4);
+    }
+}
+
+static void dq_q4_k(const uint8_t* blk, float* out) {
+    const float d = load_f16(blk), dmin = load_f16(blk + 2);
+    const uint8_t* qs = blk + 16;
+    for (int i = 0; i < 4; i++) {
+        int sc0, m0, sc1, m1;
+        q4_k_scale_min(blk + 4, 2 * i, &sc0, &m0);
+        q4_k_scale_min(blk + 4, 2 * i + 1, &sc1, &m1);
+        volatile float d0 = d * (float)sc0, o0 = dmin * (float)m0, d1 = d * (float)sc1, o1 = dmin * (float)m1;
+        for (int l = 0; l < 32; l++) {
+            volatile float a = d0 * (float)(qs[32 * i + l] & 15), b = d1 * (float)(qs[32 * i + l] >> 4);
+            out[64 * i + l] = a - o0;
+            out[64 * i + 32 + l] = b - o1;
+        }
+    }
+}
+
 static int block_geom(int type, int* bw, int* bb) {
     switch (type) {
     case T_Q4_0: *bw = 32; *bb = 18; return 0;
     case T_Q4_1: *bw = 32; *bb = 20; return 0;
     case T_Q8_0: *bw = 32; *bb = 34; return 0;
+    case T_Q4_K: *bw = 256; *bb = 144; return 0;
     case T_Q6_K: *bw = 256; *bb = 210; return 0;
     default: return -1;
     }
@@ -289,6 +330,7 @@ static void dq_block(int type, const uint8_t* blk, float* out) {
     case T_Q4_0: dq_q4_0(blk, out); break;
     case T_Q4_1: dq_q4_1(blk, out); break;
     case T_Q8_0: dq_q8_0(blk, out); break;
+    case T_Q4_K: dq_q4_k(blk, out); break;
     case T_Q6_K: dq_q6_k(blk, out); break;
     }
 }
@@ -426,7 +468,8 @@ void oracle_randn_f32(float* out, uint64_t n, uint64_t seed, float scale) {
  *   Q4_0: d = f16(|N(0,1)|*0.01), codes uniform 0..15
  *   Q4_1: as Q4_0 plus m = f16(N(0,1)*0.01)
  *   Q8_0: d as Q4_0, int8 codes uniform -127..127
- *   Q6_K: d as Q4_0, 16 int8 sub-scales uniform -32..31, 6-bit codes uniform 0..63 */
+ *   Q6_K: d as Q4_0, 16 int8 sub-scales uniform -32..31, 6-bit codes uniform 0..63
+ *   Q4_K: d as Q4_0, dmin = f16(|N(0,1)|*0.005), the 12 scale bytes and the codes uniform */
 int oracle_synth_gguf(int type, uint64_t rows, uint64_t cols, uint64_t seed, uint8_t* out) {
     int bw, bb;
     if (block_geom(type, &bw, &bb) || cols % (uint64_t)bw) return -1;
@@ -448,6 +491,13 @@ int oracle_synth_gguf(int type, uint64_t rows, uint64_t cols, uint64_t seed, uin
         case T_Q8_0:
             store_f16(o, d);
             for (int i = 0; i < 32; i++) o[2 + i] = (uint8_t)(int8_t)((int)(splitmix64(&s) % 255u) - 127);
+            break;
+        case T_Q4_K:
+            /* GGML-like: d, dmin small positive; 6-bit scales and mins uniform 0..63; codes 0..15 */
+            store_f16(o, d);
+            store_f16(o + 2, fabsf(normal(&s)) * 0.005f);
+            for (int i = 0; i < 12; i++) o[4 + i] = (uint8_t)(splitmix64(&s) & 0xFF);
+            for (int i = 0; i < 128; i++) o[16 + i] = (uint8_t)(splitmix64(&s) & 0xFF);
             break;
         case T_Q6_K: {
             /* draw each 6-bit code, then place its 4+2 bits per the layout */

@@ -10,6 +10,10 @@ independent source —
     (docs/quantization/gguf-q4.md:10-20; gguf_codegen.rs lane maps);
   * GGML's loop-form Q6_K decoder (a different formulation of the same
     layout) against the oracle's index-map form;
+  * GGML's Q4_K scale/min packer (quantize_row_q4_K's 12-byte packing, the
+    inverse of the decoder's unpacking) and the closed form
+    f32(d*sc*q - dmin*m) with one rounding, on blocks built from chosen
+    scales, mins and codes;
   * a numpy vectorised MLX decoder (LSB-first nibbles) and numpy f64 matmul.
 A planted mistake (swapped nibble halves) is shown to fail the known answer.
 """
@@ -250,6 +254,81 @@ def test_q6_k_known_answer_extremes():
     assert np.array_equal(w, (31 * sc[n * 8 + h * 4 + p * 2 + s] * 0.5).astype(np.float32))
 
 
+def pack_q4_k_scales(sc, m) -> np.ndarray:
+    """GGML's packing of eight 6-bit sub-block scales and mins into a Q4_K
+    block's 12 scale bytes (quantize_row_q4_K): the inverse direction of the
+    decoder's get_scale_min_k4, written from the packer's side."""
+    out = np.zeros(12, np.uint8)
+    for j in range(8):
+        if j < 4:
+            out[j] |= sc[j]
+            out[j + 4] |= m[j]
+        else:
+            out[j + 4] |= (sc[j] & 0xF) | ((m[j] & 0xF) << 4)
+            out[j - 4] |= (sc[j] >> 4) << 6
+            out[j] |= (m[j] >> 4) << 6
+    return out
+
+
+def q4_k_block(d, dmin, sc, m, q) -> np.ndarray:
+    """A Q4_K block from its fields: weight 64i + l is the low nibble of
+    qs[32i + l] and weight 64i + 32 + l its high nibble."""
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    blk[2:4] = np.frombuffer(np.float16(dmin).tobytes(), np.uint8)
+    blk[4:16] = pack_q4_k_scales(sc, m)
+    q = np.asarray(q, np.uint8).reshape(4, 2, 32)
+    blk[16:144] = (q[:, 0, :] | (q[:, 1, :] << 4)).ravel()
+    return blk
+
+
+def test_q4_k_closed_form_from_chosen_fields():
+    rng = np.random.default_rng(12)
+    blocks, want = [], []
+    for b in range(24):
+        d = np.float16(rng.uniform(1e-4, 0.05) * (1 if b % 5 else 1e-3))  # some subnormal d
+        dmin = np.float16(rng.uniform(0, 0.02)) if b % 7 else np.float16(0)
+        sc = rng.integers(0, 64, 8)
+        m = rng.integers(0, 64, 8)
+        if b == 0:
+            sc[:], m[:] = 63, 63  # every high bit set
+        q = rng.integers(0, 16, 256)
+        blocks.append(q4_k_block(d, dmin, sc, m, q))
+        j = np.arange(256) // 32
+        exact = float(d) * sc[j].astype(np.float64) * q - float(dmin) * m[j].astype(np.float64)
+        want.append(exact.astype(np.float32))  # each term exact: one RNE rounding
+    got = oracle.dequant_gguf(oracle.Q4_K, np.concatenate(blocks), 24, 256)
+    assert np.array_equal(got.view(np.uint32), np.stack(want).view(np.uint32))
+
+
+def test_q4_k_known_answer_block():
+    # sc_j = j + 1, m_j = 2j (j < 8), codes = weight index mod 16, d = 0.5, dmin = 0.25
+    sc, m = np.arange(1, 9), 2 * np.arange(8)
+    q = np.arange(256) % 16
+    blk = q4_k_block(0.5, 0.25, sc, m, q)
+    w = oracle.dequant_gguf(oracle.Q4_K, blk, 1, 256).ravel()
+    j = np.arange(256) // 32
+    assert np.array_equal(w, (0.5 * (j + 1) * q - 0.25 * 2 * j).astype(np.float32))
+    # the packed bytes themselves, from the layout: j<4 in the low 6 bits of bytes j / j+4,
+    # j>=4 split into a nibble of byte j+4 and the top two bits of bytes j-4 / j
+    assert list(blk[4:16]) == [1, 2, 3, 4, 0, 2, 4, 6, 5 | (8 << 4), 6 | (10 << 4), 7 | (12 << 4), 8 | (14 << 4)]
+
+
+def test_q4_k_planted_scale_min_swap_fails():
+    """A decoder that swaps the j >= 4 scale and min sources (a plausible
+    slip) disagrees with the closed form on a block built by the packer."""
+    rng = np.random.default_rng(3)
+    sc, m = rng.integers(16, 64, 8), rng.integers(16, 64, 8)
+    q = rng.integers(0, 16, 256)
+    blk = q4_k_block(0.01, 0.005, sc, m, q)
+    s = blk[4:16].astype(np.int64)
+    wrong_sc = [(s[j + 4] >> 4) | ((s[j] >> 6) << 4) for j in range(4, 8)]
+    assert wrong_sc != list(sc[4:])
+    got = oracle.dequant_gguf(oracle.Q4_K, blk, 1, 256).ravel()
+    j = np.arange(256) // 32
+    assert np.array_equal(got, (np.float64(np.float16(0.01)) * sc[j] * q - np.float64(np.float16(0.005)) * m[j]).astype(np.float32))
+
+
 def test_mlx_u4_numpy_decoder():
     rows, cols, g = 5, 256, 64
     for sdt in (oracle.D_BF16, oracle.D_F16, oracle.D_F32):
@@ -286,7 +365,7 @@ def test_linear_f32_sequential_within_f32_bound():
     assert np.all(np.abs(y - y64) <= 1000 * 2.0 ** -24 * a)
 
 
-@pytest.mark.parametrize("gtype", oracle.GGUF_TYPES, ids=oracle.NAMES.get)
+@pytest.mark.parametrize("gtype", oracle.GGUF_TYPES + (oracle.Q4_K,), ids=oracle.NAMES.get)
 def test_cpu_baseline_contraction_within_tolerance(gtype):
     bw, _ = oracle.BLOCK[gtype]
     n, k = 40, 4 * bw * (2 if bw == 32 else 1)
@@ -316,6 +395,9 @@ def test_synth_distributions():
                       np.repeat(q6[:, 208:210].copy().view(np.float16).astype(np.float32), 256, axis=0).reshape(256, 256)))
     ok = np.isfinite(q)
     assert q[ok].min() == -32 and q[ok].max() == 31
+    q4k = oracle.synth_gguf(oracle.Q4_K, 256, 256, 5).reshape(-1, 144)
+    dd = q4k[:, 0:4].copy().view(np.float16).astype(np.float32)
+    assert np.all(dd >= 0) and 0.005 < dd[:, 0].mean() < 0.011 and 0.0025 < dd[:, 1].mean() < 0.0055
     q41 = oracle.synth_gguf(oracle.Q4_1, 256, 256, 4).reshape(-1, 20)
     m = q41[:, 2:4].copy().view(np.float16).astype(np.float32)
     assert abs(m.mean()) < 0.002 and 0.007 < m.std() < 0.013
