@@ -3,6 +3,8 @@
 // Encodings are consumed in their on-disk byte layout (no repack):
 //   GGUF blocks (gguf_codegen.rs:15-48): Q4_0 18 B / 32 w, Q4_1 20 B / 32 w,
 //   Q8_0 34 B / 32 w, Q6_K 210 B / 256 w; row o, block b at (o*K/B + b)*bytes.
+//   GGUF Q4_K super-blocks (GGML layout; the reference declares the schema,
+//   gguf_block.rs:183-316): 144 B / 256 w.
 //   MLX affine U4: packed u32 [N, K/8] + scales/biases [N, K/g].
 #pragma once
 #include <hip/hip_runtime.h>
@@ -82,6 +84,20 @@ __device__ __forceinline__ void realign(const uint32_t (&raw)[NDW], uint32_t sh,
 #pragma unroll
     for (int i = 0; i + 1 < NDW; i++) e[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
     e[NDW - 1] = __builtin_amdgcn_alignbyte(raw[NDW - 1], raw[NDW - 1], sh);
+}
+
+// Q4_K sub-block j's (0..7) 6-bit scale and min from the super-block's 12
+// scale bytes s12 (GGML get_scale_min_k4): j < 4 in the low 6 bits of bytes j
+// and j + 4; j >= 4 split into a nibble of byte j + 4 (scale low, min high)
+// and the top two bits of bytes j - 4 (scale) and j (min).
+__device__ __forceinline__ void q4k_scale_min(const uint8_t* s12, uint32_t j, uint32_t& sc, uint32_t& m) {
+    if (j < 4u) {
+        sc = s12[j] & 63u;
+        m = s12[j + 4u] & 63u;
+    } else {
+        sc = (s12[j + 4u] & 15u) | ((uint32_t)(s12[j - 4u] >> 6) << 4);
+        m = (uint32_t)(s12[j + 4u] >> 4) | ((uint32_t)(s12[j] >> 6) << 4);
+    }
 }
 
 }  // namespace dmx

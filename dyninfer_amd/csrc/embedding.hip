@@ -4,7 +4,9 @@
 // interleaved bytes followed by the same dequant body as the matmul
 // (gguf_codegen.rs:316-348 `emit_gather`, body gguf_codegen.rs:350-526), and on
 // an MLX U4 weight to row slices of packed/scales/biases with
-// f32(q) * s + b (mlx_affine.rs:628-675 `emit_gather_u4`).  Each value here is
+// f32(q) * s + b (mlx_affine.rs:628-675 `emit_gather_u4`); GGUF Q4_K rows
+// (a schema-only encoding in the reference) dequantize as GGML's
+// dequantize_row_q4_K.  Each value here is
 // computed with the same f32 operations in the same order, so the rows are
 // bit-identical to the dequant hook's rows.
 //
@@ -46,6 +48,16 @@ __device__ __forceinline__ float4 gguf_four(const uint8_t* __restrict__ row, uin
         const float d = f16_bits_to_f32(ld16(blk));
         const uint8_t* q = blk + 2 + (k & 31u);
         for (int i = 0; i < 4; i++) v[i] = (float)(int8_t)ld8(q + i) * d;
+    } else if constexpr (ENC == ENC_Q4_K) {  // idx = 64i + 32h + l: nibble h of qs[32i + l], sub-block 2i + h
+        const uint8_t* blk = row + (size_t)(k >> 8) * 144u;
+        const uint32_t idx = k & 255u, jsub = idx >> 5;
+        const float d = f16_bits_to_f32(ld16(blk)), dmin = f16_bits_to_f32(ld16(blk + 2));
+        uint32_t sc, m;
+        q4k_scale_min(blk + 4, jsub, sc, m);
+        const float ds = d * (float)sc, dm = dmin * (float)m;
+        const uint8_t* q = blk + 16 + 32 * (jsub >> 1) + (idx & 31u);
+        const uint32_t sh = 4u * (jsub & 1u);
+        for (int i = 0; i < 4; i++) v[i] = ds * (float)((ld8(q + i) >> sh) & 15u) - dm;
     } else {  // Q6_K: idx = n*128 + h*64 + p*32 + s*16 + l (gguf_codegen.rs:499-503)
         const uint8_t* blk = row + (size_t)(k >> 8) * 210u;
         const uint32_t idx = k & 255u;
@@ -142,6 +154,10 @@ hipError_t gather_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, cons
         break;
     case ENC_Q6_K:
         hipLaunchKernelGGL(gguf_gather_kernel<ENC_Q6_K>, grid, block, 0, stream, w, (uint64_t)(K / 256) * 210u, vocab,
+                           K, per_row, ids, out);
+        break;
+    case ENC_Q4_K:
+        hipLaunchKernelGGL(gguf_gather_kernel<ENC_Q4_K>, grid, block, 0, stream, w, (uint64_t)(K / 256) * 144u, vocab,
                            K, per_row, ids, out);
         break;
     default: return hipErrorInvalidValue;

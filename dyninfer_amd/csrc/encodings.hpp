@@ -23,6 +23,7 @@
 //   Q4_1  w = q·d + m            code q,          off 0, + m·Σx
 //   Q8_0  w = q·d                code q+128 (xor 0x80), off 128
 //   Q6_K  w = (q-32)·sc·d        6-bit code q,    off 32, per 16-weight group
+//   Q4_K  w = q·(d·sc) - dmin·m  code q,          off 0, - dmin·m·Σx, per 32-weight group
 //   MLX   w = q·s + b            code q,          off 0, + b·Σx
 //
 // Layout contract with the activation staging (gemv_kernels.hpp): for code
@@ -327,6 +328,73 @@ struct EncQ6K {
     }
 };
 
+// ------------------------------------------------------------------ GGUF Q4_K
+// 144-byte super-block of 256 (GGML block_q4_K; the reference's schema
+// gguf_block.rs:183-316 "q4_k" and convention.rs:210,240: scale_min_f16 4 B,
+// scales_and_mins_u6 12 B, quants_u4 128 B): d = f16 bytes 0..2, dmin = f16
+// 2..4, packed 6-bit scales and mins 4..16, qs = 16..144.  Weights 64i + l and
+// 64i + 32 + l (i < 4, l < 32) are the low and high nibbles of qs[32i + l], in
+// sub-blocks 2i and 2i + 1: w = q·(d·sc_j) - dmin·m_j (q4k_scale_min).
+// Chunk u is step i = u & 3 of super-block u >> 2: two scale groups, the low
+// nibbles (weights 64i..64i+31) and the high nibbles (x16).  Code dword t =
+// qs bytes 32i + 4t..4t+3; its pairs (4t, 4t+2), (32+4t, 34+4t) x16,
+// (4t+1, 4t+3), (33+4t, 35+4t) x16.  Super-blocks are 4-byte aligned (the C
+// ABI requires a 4-byte-aligned base; 144 = 36 dwords).
+struct EncQ4K {
+    static constexpr uint32_t ENC = ENC_Q4_K;
+    static constexpr int CW = 64, QK = 256, NT = 8, PPT = 4, NG = 2, BB = 144;
+    static constexpr bool AFFINE = true;
+    static constexpr int NRUN = 2, RUNLEN = 32, RUNSTRIDE = 32;  // activation runs of group g at 32g
+    __device__ __forceinline__ static uint32_t xbase(uint32_t u) { return 64u * u; }
+    static constexpr float coef(bool) { return 1024.0f; }
+    static constexpr int xoff(int t, int h, int e) { return 4 * t + (h >> 1) + 2 * e + 32 * (h & 1); }
+    static constexpr bool dv(int, int h) { return (h & 1) != 0; }
+    static constexpr int grp(int, int h) { return h & 1; }
+    static constexpr int TSTRIDE = 4, NXR = 2;  // activations 4t..4t+3 and 32+4t..32+4t+3
+    static constexpr int xrun0(int r) { return 32 * r; }
+    // header dwords (d | dmin, scale bytes 0..11) and the step's 8 qs dwords
+    struct Raw { uint32_t h[4]; uint32_t q[NT]; };
+    struct Chunk { uint32_t q[NT]; float ds[NG], dm[NG]; };
+    __device__ __forceinline__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u) {
+        const uint32_t* sb = reinterpret_cast<const uint32_t*>(w + (rowoff + (u >> 2) * (uint32_t)BB));
+        Raw r;
+        load_dwords<4>(sb, r.h);
+        load_dwords<NT>(sb + 4u + 8u * (u & 3u), r.q);
+        return r;
+    }
+    // Sub-blocks 2i and 2i + 1 sit at scale-byte positions 2(i & 1) and
+    // 2(i & 1) + 1 of the three scale dwords: bytes 0..3 (scales j < 4, top
+    // bits of j >= 4), 4..7 (mins j < 4, top bits of j >= 4 mins), 8..11 (the
+    // low nibbles of j >= 4).
+    __device__ __forceinline__ static Chunk unpack(const Raw& r, uint32_t u) {
+        Chunk c;
+#pragma unroll
+        for (int t = 0; t < NT; t++) c.q[t] = r.q[t];
+        const float d = f16_bits_to_f32(r.h[0]), dmin = f16_bits_to_f32(r.h[0] >> 16);
+        const uint32_t i = u & 3u, sh = 16u * (i & 1u);
+        const uint32_t A = r.h[1] >> sh, M = r.h[2] >> sh, L = r.h[3] >> sh;
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            const uint32_t a = (A >> (8 * g)) & 0xFFu, m = (M >> (8 * g)) & 0xFFu, l = (L >> (8 * g)) & 0xFFu;
+            const uint32_t sc = i < 2u ? (a & 63u) : ((l & 15u) | ((a >> 6) << 4));
+            const uint32_t mn = i < 2u ? (m & 63u) : ((l >> 4) | ((m >> 6) << 4));
+            c.ds[g] = d * (float)sc;
+            c.dm[g] = -(dmin * (float)mn);
+        }
+        return c;
+    }
+    __device__ __forceinline__ static void pairs(const Chunk& c, int t, uint32_t (&p)[PPT]) { nibble_pairs(c.q[t], p); }
+    __device__ __forceinline__ static float gscale(const Chunk& c, int g) { return c.ds[g]; }
+    __device__ __forceinline__ static float goffset(const Chunk& c, int g) { return c.dm[g]; }
+    __device__ __forceinline__ static void zero_if(Chunk& c, bool z) {
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            c.ds[g] = z ? 0.0f : c.ds[g];
+            c.dm[g] = z ? 0.0f : c.dm[g];
+        }
+    }
+};
+
 // ------------------------------------------------------------------ MLX affine U4
 // One chunk = 32 weights = 4 packed u32 words (weight i of a word = bits
 // 4i..4i+3, fixture.rs:307-311) sharing one scale and bias (group size is a
@@ -402,7 +470,7 @@ constexpr bool xruns_ok() {
     return 4 * E::NXR == 2 * E::PPT;
 }
 static_assert(xruns_ok<EncQ40>() && xruns_ok<EncQ41>() && xruns_ok<EncQ80>() && xruns_ok<EncQ6K>() &&
-                  xruns_ok<EncMlxU4>(),
+                  xruns_ok<EncQ4K>() && xruns_ok<EncMlxU4>(),
               "activation runs disagree with xoff()");
 
 }  // namespace dmx

@@ -699,7 +699,7 @@ __global__ __launch_bounds__(TH) void mlx_u4_gemv_oneshot_kernel(const GemvParam
 // keep the accumulators in registers (gemv_tiles adds the narrower tiles).
 template <class E, int B>
 constexpr int rows_per_group() {
-    if constexpr (E::ENC == ENC_Q6_K) return B <= 2 ? 2 : 1;
+    if constexpr (E::ENC == ENC_Q6_K || E::ENC == ENC_Q4_K) return B <= 2 ? 2 : 1;  // 64-weight chunks
     else return B <= 2 ? 4 : 2;
 }
 

@@ -76,10 +76,13 @@ Value candidate(const std::string& codec, const char* op_kind, const char* op_su
 const std::string& candidates_json() {
     static const std::string s = [] {
         Value all = Value::array();
-        struct G { const char* codec; long long block; };
-        const G gguf[] = {{"gguf.q4_0", 32}, {"gguf.q4_1", 32}, {"gguf.q8_0", 32}, {"gguf.q6_k", 256}};
+        // gguf.q4_k is a schema-only encoding in the reference (gguf_block.rs:183-316): these
+        // entries give it its first kernels, decoding GGML's block_q4_K.
+        struct G { const char* codec; long long block; bool gemm; };
+        const G gguf[] = {{"gguf.q4_0", 32, true}, {"gguf.q4_1", 32, true}, {"gguf.q8_0", 32, true},
+                          {"gguf.q6_k", 256, true}, {"gguf.q4_k", 256, false}};
         for (const G& g : gguf) {
-            const bool gemm = std::string(g.codec) != "gguf.q6_k";
+            const bool gemm = g.gemm;
             const std::string n = std::string("Consumes official GGML ") + g.codec +
                                   " interleaved blocks in place on gfx950: wave64 GEMV for 1-16 rows "
                                   "(in-register dequantisation, f32 accumulation)" +

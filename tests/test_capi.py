@@ -40,7 +40,7 @@ def test_nm_exports_are_c_linkage():
 
 def test_version_and_candidates_json():
     assert b"gfx950" in d.library().dyninfer_mi355x_version()
-    assert len(d.candidates()) == 25  # f32 and bf16-activation entries
+    assert len(d.candidates()) == 30  # f32 and bf16-activation entries
 
 
 def w(enc, rows=64, cols=256, data=0x1000, **kw):
@@ -49,7 +49,8 @@ def w(enc, rows=64, cols=256, data=0x1000, **kw):
 
 @pytest.mark.parametrize("enc,cols,ok", [
     (d.ENC_Q4_0, 256, True), (d.ENC_Q4_0, 100, False), (d.ENC_Q4_1, 64, True), (d.ENC_Q8_0, 96, True),
-    (d.ENC_Q6_K, 256, True), (d.ENC_Q6_K, 384, False), (99, 256, False)])
+    (d.ENC_Q6_K, 256, True), (d.ENC_Q6_K, 384, False), (d.ENC_Q4_K, 512, True), (d.ENC_Q4_K, 288, False),
+    (99, 256, False)])
 def test_supports_block_multiples(enc, cols, ok):
     assert d.supports(w(enc, cols=cols), 1) == ok
 
@@ -58,6 +59,8 @@ def test_supports_alignment_rules():
     assert d.supports(w(d.ENC_Q4_0, data=0x1002), 1)          # GGUF: 2-byte aligned is enough
     assert not d.supports(w(d.ENC_Q4_0, data=0x1001), 1)
     assert not d.supports(w(d.ENC_Q4_1, data=0x1002), 1)      # Q4_1 blocks are 20 bytes: 4-byte base
+    assert not d.supports(w(d.ENC_Q4_K, data=0x1002), 1)      # Q4_K super-blocks are 144 bytes: 4-byte base
+    assert d.supports(w(d.ENC_Q4_K, data=0x1004), 1)
     assert not d.supports(w(d.ENC_Q4_0, data=0), 1)           # NULL
 
 
@@ -73,7 +76,7 @@ def test_supports_mlx_rules():
 
 def test_supports_dtype_rules():
     # f32 or bf16 activations for every encoding, any row count; f16 activations are not qualified
-    for enc in (d.ENC_Q4_0, d.ENC_Q4_1, d.ENC_Q8_0, d.ENC_Q6_K):
+    for enc in (d.ENC_Q4_0, d.ENC_Q4_1, d.ENC_Q8_0, d.ENC_Q6_K, d.ENC_Q4_K):
         for rows in (1, 4, 16, 17, 512):
             assert d.supports(w(enc), rows, d.DTYPE_BF16, d.DTYPE_BF16)
             assert d.supports(w(enc), rows, d.DTYPE_F32, d.DTYPE_F32)
@@ -85,7 +88,7 @@ def test_supports_dtype_rules():
 
 @pytest.mark.parametrize("enc,rows,cols,nbytes", [
     (d.ENC_Q4_0, 64, 256, 64 * 8 * 18), (d.ENC_Q4_1, 3, 64, 3 * 2 * 20), (d.ENC_Q8_0, 5, 96, 5 * 3 * 34),
-    (d.ENC_Q6_K, 7, 512, 7 * 2 * 210)])
+    (d.ENC_Q6_K, 7, 512, 7 * 2 * 210), (d.ENC_Q4_K, 3, 512, 3 * 2 * 144)])
 def test_gguf_data_component_byte_total(enc, rows, cols, nbytes):
     """One interleaved data component of N·(K/B)·bytes_per_block bytes
     (gguf_block.rs:124-155): a short or long buffer is E_UNSUPPORTED_ENCODING."""

@@ -1,0 +1,207 @@
+"""GGUF Q4_K (GGML's block_q4_K) through the C ABI.
+
+The reference declares Q4_K's schema only (gguf_block.rs:183-316: type 12,
+256 weights, 144 bytes, components scale_min_f16 / scales_and_mins_u6 /
+quants_u4; convention.rs:210,240), so its kernels here decode GGML's layout,
+which the oracle restates and pins (tests/test_oracle.py: the packer-side
+scale/min layout, a known-answer block, the one-rounding closed form).
+
+Bars, as for the other encodings:
+  * dequantisation and embedding rows: bit-exact (every f32 bit pattern)
+    with the oracle, w = f32(d·sc)·q - f32(dmin·m) with one rounding;
+  * GEMV outputs: max |y - y_ref| / Σ_k |w||x| <= 2e-3 and <= 2^-11 + 2e-5
+    (one f16 rounding per activation after a power-of-two scaling per
+    32-weight group, f32 accumulation), y_ref the f64 contraction of the
+    exactly dequantised weights.
+"""
+import struct
+
+import numpy as np
+import pytest
+
+import dyninfer_amd as d
+import oracle
+
+TOL = 2e-3
+XF16 = 2.0 ** -11 + 2e-5
+Q4K = oracle.Q4_K
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def weight(n, k, seed, off=0):
+    """A Q4_K weight of synthetic super-blocks, `off` bytes into a device buffer."""
+    import torch
+    data = oracle.synth_gguf(Q4K, n, k, seed)
+    buf = torch.zeros(data.size + 16, dtype=torch.uint8, device="cuda")
+    buf[off:off + data.size] = dev(data)
+    w = d.QWeight(d.ENC_Q4_K, n, k, buf.data_ptr() + off, data_bytes=data.size)
+    w._keep = buf
+    return w, data
+
+
+def assert_bits_equal(got, ref):
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    bad = (got.view(np.uint32) != ref.view(np.uint32)) & ~nan
+    assert not bad.any(), f"{bad.sum()} differing, first at {np.argwhere(bad)[0]}"
+
+
+def err_of(y, x, wf):
+    y64, absdot = oracle.linear_f64(x, wf)
+    return oracle.normalized_error(y, y64, absdot)
+
+
+# ---------------------------------------------------------------- host-side (no GPU)
+def test_q4_k_weight_rules():
+    w = lambda **kw: d.QWeight(d.ENC_Q4_K, kw.pop("n", 8), kw.pop("k", 512), kw.pop("data", 0x1000), **kw)
+    assert d.supports(w(), 1) and d.supports(w(), 16) and d.supports(w(), 512, d.DTYPE_BF16, d.DTYPE_BF16)
+    assert not d.supports(w(k=384), 1)          # K a multiple of 256
+    assert "multiple of the block size 256" in d.library().dyninfer_mi355x_last_error().decode()
+    assert not d.supports(w(data=0x1002), 1)    # 4-byte-aligned super-blocks
+    assert "4-byte aligned" in d.library().dyninfer_mi355x_last_error().decode()
+    assert d.supports(w(data_bytes=8 * 2 * 144), 1)
+    assert not d.supports(w(data_bytes=8 * 2 * 144 - 4), 1)
+    assert d.block_geometry(d.ENC_Q4_K) == (256, 144)
+
+
+def _s(x: str) -> bytes:
+    b = x.encode()
+    return struct.pack("<Q", len(b)) + b
+
+
+def test_gguf_q4_k_tensor_indexed_and_described():
+    """A GGUF file holding a type-12 tensor: its exact byte range, and a QWeight
+    of it (the reference indexes such tensors but has no kernel for them)."""
+    n, k = 6, 512
+    raw = oracle.synth_gguf(Q4K, n, k, 4).tobytes()
+    body = b"GGUF" + struct.pack("<IQQ", 3, 1, 1) + _s("general.architecture") + struct.pack("<I", 8) + _s("llama")
+    body += _s("blk.0.ffn_up.weight") + struct.pack("<I", 2) + struct.pack("<QQ", k, n) + struct.pack("<IQ", 12, 0)
+    body += b"\0" * ((32 - len(body) % 32) % 32)
+    g = d.GgufFile.from_bytes(body + raw)
+    t = g.tensors[0]
+    assert (t.type_code, t.nbytes, t.offset) == (12, len(raw), len(body))
+    w = g.qweight("blk.0.ffn_up.weight", 0x1000)
+    assert (w.encoding, w.rows, w.cols, w.data_bytes) == (d.ENC_Q4_K, n, k, len(raw))
+    with pytest.raises(d.DyninferError):
+        g.qweight("blk.0.ffn_up.weight", 0x1002)
+
+
+# ---------------------------------------------------------------- dequant / embedding
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,k,off", [(1, 256, 0), (3, 512, 4), (64, 1024, 0), (33, 4096, 12)])
+def test_dequant_bit_exact(ctx, n, k, off):
+    w, data = weight(n, k, seed=n + k, off=off)
+    assert_bits_equal(ctx.dequant(w).cpu().numpy(), oracle.dequant_gguf(Q4K, data, n, k))
+
+
+@pytest.mark.gpu
+def test_dequant_special_fields(ctx):
+    """d, dmin over signed zeros, subnormals, max, inf and NaN; every scale and
+    min byte pattern (0x00 / 0xFF / random) so the top-two-bit paths of
+    sub-blocks 4..7 are all exercised."""
+    specials = [0x8000, 0x0000, 0x0001, 0x03FF, 0x3C00, 0xC100, 0x7BFF, 0x7C00, 0xFC00, 0x7E00]
+    rng = np.random.default_rng(9)
+    blocks = []
+    for i, dbits in enumerate(specials):
+        for j, mbits in enumerate((0x0000, 0x3C00, specials[(i + 3) % len(specials)])):
+            b = rng.integers(0, 256, 144, dtype=np.uint8)
+            b[0:2] = [dbits & 0xFF, dbits >> 8]
+            b[2:4] = [mbits & 0xFF, mbits >> 8]
+            if j == 0:
+                b[4:16] = 0xFF
+            blocks.append(b)
+    data = np.concatenate(blocks)
+    rows = len(blocks)
+    w = d.QWeight(d.ENC_Q4_K, rows, 256, dev(data))
+    assert_bits_equal(ctx.dequant(w).cpu().numpy(), oracle.dequant_gguf(Q4K, data, rows, 256))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("vocab,k,n", [(1, 256, 1), (37, 512, 5), (300, 1024, 64), (9, 4096, 17)])
+def test_embedding_bit_exact(ctx, vocab, k, n):
+    w, data = weight(vocab, k, seed=vocab * 3 + k)
+    rng = np.random.default_rng(n)
+    ids = rng.integers(0, vocab, n).astype(np.int64)
+    ids[:min(n, 2)] = [0, vocab - 1][:min(n, 2)]
+    out = ctx.embedding(w, dev(ids)).cpu().numpy()
+    assert np.array_equal(out.view(np.uint32), oracle.dequant_gguf(Q4K, data, vocab, k)[ids].view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_embedding_out_of_range_ids_are_nan_rows(ctx):
+    w, data = weight(12, 512, seed=2)
+    ids = np.array([3, -1, 12, 11], np.int64)
+    out = ctx.embedding(w, dev(ids)).cpu().numpy()
+    ref = oracle.dequant_gguf(Q4K, data, 12, 512)
+    assert np.array_equal(out[0], ref[3]) and np.array_equal(out[3], ref[11])
+    assert np.isnan(out[1]).all() and np.isnan(out[2]).all()
+
+
+# ---------------------------------------------------------------- GEMV
+# shapes reach every launch form: latency mode (few chunks per lane), the
+# persistent pipeline, the batch-1 streaming kernel, 1024-thread workgroups
+# for K > 8192, and several register passes for batches above 4
+SHAPES = [(1, 256), (67, 512), (1024, 1024), (3072, 1024), (1024, 3072), (513, 4096), (4096, 4096), (1024, 12288)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,k", SHAPES)
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 8, 16])
+def test_gemv(ctx, n, k, batch):
+    w, data = weight(n, k, seed=100 + n + k + batch)
+    x = oracle.randn(batch * k, seed=n * 7 + batch).reshape(batch, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    err = err_of(y, x, oracle.dequant_gguf(Q4K, data, n, k))
+    assert err <= TOL and err <= XF16, err
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [17, 40])
+def test_more_than_16_rows(ctx, rows):
+    n, k = 768, 2048
+    w, data = weight(n, k, seed=rows)
+    x = oracle.randn(rows * k, seed=rows + 1).reshape(rows, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    err = err_of(y, x, oracle.dequant_gguf(Q4K, data, n, k))
+    assert err <= TOL and err <= XF16, err
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch", [1, 4])
+def test_bf16_activations_and_outputs_offset_base(ctx, batch):
+    import torch
+    n, k = 2048, 4096
+    w, data = weight(n, k, seed=77, off=4)
+    x = torch.from_numpy(oracle.randn(batch * k, seed=5).reshape(batch, k)).to(torch.bfloat16)
+    xr = x.float().numpy()
+    y = ctx.qlinear(w, x.cuda(), y_dtype=torch.bfloat16).float().cpu().numpy()
+    y64, absdot = oracle.linear_f64(xr, oracle.dequant_gguf(Q4K, data, n, k))
+    # bf16 outputs add one bf16 rounding of |y| (relative 2^-9)
+    bound = XF16 + 2.0 ** -9 * np.max(np.abs(y64) / absdot)
+    err = oracle.normalized_error(y, y64, absdot)
+    assert err <= TOL and err <= bound, err
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch", [1, 2, 16])
+def test_multi_weights_share_activations(ctx, batch):
+    k = 4096
+    ws = [weight(n, k, seed=n + batch) for n in (4096, 1024, 1024)]
+    x = oracle.randn(batch * k, seed=batch).reshape(batch, k)
+    ys = ctx.qlinear_multi([w for w, _ in ws], dev(x))
+    for (w, data), y in zip(ws, ys):
+        err = err_of(y.cpu().numpy(), x, oracle.dequant_gguf(Q4K, data, w.rows, k))
+        assert err <= TOL and err <= XF16, err
+
+
+@pytest.mark.gpu
+def test_deterministic(ctx):
+    w, _ = weight(4096, 4096, seed=1)
+    x = dev(oracle.randn(4096, seed=2).reshape(1, 4096))
+    a = ctx.qlinear(w, x).cpu().numpy()
+    for _ in range(3):
+        assert np.array_equal(ctx.qlinear(w, x).cpu().numpy().view(np.uint32), a.view(np.uint32))

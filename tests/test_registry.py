@@ -154,7 +154,7 @@ def gguf_request(codec, n, k, op="linear", mode="decode"):
 
 
 @pytest.mark.parametrize("codec,block", [("gguf.q4_0", 32), ("gguf.q4_1", 32), ("gguf.q8_0", 32), ("gguf.q6_k", 256),
-                                         ("mlx.affine.u4", 32)])
+                                         ("gguf.q4_k", 256), ("mlx.affine.u4", 32)])
 @pytest.mark.parametrize("op,suffix", [("linear", "matmul"), ("output_projection", "output")])
 @pytest.mark.parametrize("mode", ["decode", "prefill"])
 def test_mi355x_entry_wins_on_gfx950(codec, block, op, suffix, mode):
@@ -173,6 +173,17 @@ def test_mi355x_entry_rejected_off_gfx950(codec):
         rep["selected"]["descriptor"]["id"].endswith("iree_grouped_hip")
     ours = [r for r in rep["rejected"] if r["candidate_id"] == f"{codec}.matmul.mi355x_hip"][0]
     assert ours["reasons"] == [{"reason": "architecture_mismatch", "selected": "gfx1151"}]
+
+
+def test_q4_k_is_covered_only_on_gfx950():
+    """gguf.q4_k is declared without kernels in the reference (gguf_block.rs:183-316):
+    on gfx950 this library's entry is selected, elsewhere the request stays a
+    coverage error (E_KERNEL_COVERAGE, lib.rs:350-399)."""
+    req = gguf_request("gguf.q4_k", 4096, 4096)
+    assert d.registry_require(req, hip("gfx950"), full_registry())["descriptor"]["id"] == "gguf.q4_k.matmul.mi355x_hip"
+    with pytest.raises(d.DyninferError) as e:
+        d.registry_require(req, hip("gfx1151"), full_registry())
+    assert e.value.code == d.ERR_UNSUPPORTED
 
 
 def test_cpu_target_keeps_iree_cpu_kernel_and_missing_avx2_is_coverage_error():
@@ -197,14 +208,17 @@ def test_axis_not_divisible_rejects():
 
 @pytest.mark.parametrize("codec,block,suffix", [("gguf.q4_0", 32, "gather"), ("gguf.q4_1", 32, "gather"),
                                                 ("gguf.q8_0", 32, "gather"), ("gguf.q6_k", 256, "gather"),
-                                                ("mlx.affine.u4", 32, "embedding")])
+                                                ("gguf.q4_k", 256, "gather"), ("mlx.affine.u4", 32, "embedding")])
 def test_embedding_selects_mi355x_gather_on_gfx950(codec, block, suffix):
     req = gguf_request(codec, 151936, 4 * block, op="embedding", mode="prefill")
     sel = d.registry_require(req, hip("gfx950"), full_registry())
     assert sel["descriptor"]["id"] == f"{codec}.{suffix}.mi355x_hip" and sel["score"] == 1400
     rep = d.registry_select(req, hip("gfx1151"), full_registry())
-    assert rep["selected"]["descriptor"]["id"] in (f"{codec}.gather.iree_block_hip",
-                                                   "mlx.affine.u4.embedding.iree_grouped_hip")
+    if codec == "gguf.q4_k":  # schema-only in the reference: no other kernel exists
+        assert "selected" not in rep
+    else:
+        assert rep["selected"]["descriptor"]["id"] in (f"{codec}.gather.iree_block_hip",
+                                                       "mlx.affine.u4.embedding.iree_grouped_hip")
 
 
 def test_duplicate_candidate_ids_are_rejected():
@@ -219,7 +233,7 @@ def test_candidates_match_the_serde_schema():
     keys = {"id", "operation", "encoding", "input_types", "output_types", "accumulator_types", "shape",
             "orientations", "target", "modes", "lowering", "deterministic_score", "readiness", "notes"}
     cands = d.candidates()
-    assert len(cands) == 25 and len({c["id"] for c in cands}) == 25
+    assert len(cands) == 30 and len({c["id"] for c in cands}) == 30
     for c in cands:
         assert set(c) == keys
         assert c["operation"] in ("embedding", "linear", "output_projection")
