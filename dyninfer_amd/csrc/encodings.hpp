@@ -362,24 +362,33 @@ struct EncQ4K {
         load_dwords<NT>(sb + 4u + 8u * (u & 3u), r.q);
         return r;
     }
-    // Sub-blocks 2i and 2i + 1 sit at scale-byte positions 2(i & 1) and
-    // 2(i & 1) + 1 of the three scale dwords: bytes 0..3 (scales j < 4, top
-    // bits of j >= 4), 4..7 (mins j < 4, top bits of j >= 4 mins), 8..11 (the
-    // low nibbles of j >= 4).
+    // The 6-bit scales and mins of sub-blocks 2i and 2i + 1 (i = step 0..3)
+    // from the header dwords h[1..3]: they sit at scale-byte positions
+    // 2(i & 1) and 2(i & 1) + 1 of bytes 0..3 (scales j < 4, top bits of the
+    // scales j >= 4), 4..7 (mins j < 4, top bits of the mins j >= 4) and
+    // 8..11 (the low nibbles of j >= 4: scale low, min high).
+    __device__ __forceinline__ static void scale_min(const uint32_t (&h)[4], uint32_t i, uint32_t (&sc)[NG],
+                                                     uint32_t (&mn)[NG]) {
+        const uint32_t sh = 16u * (i & 1u);
+        const uint32_t A = h[1] >> sh, M = h[2] >> sh, L = h[3] >> sh;
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            const uint32_t a = (A >> (8 * g)) & 0xFFu, m = (M >> (8 * g)) & 0xFFu, l = (L >> (8 * g)) & 0xFFu;
+            sc[g] = i < 2u ? (a & 63u) : ((l & 15u) | ((a >> 6) << 4));
+            mn[g] = i < 2u ? (m & 63u) : ((l >> 4) | ((m >> 6) << 4));
+        }
+    }
     __device__ __forceinline__ static Chunk unpack(const Raw& r, uint32_t u) {
         Chunk c;
 #pragma unroll
         for (int t = 0; t < NT; t++) c.q[t] = r.q[t];
         const float d = f16_bits_to_f32(r.h[0]), dmin = f16_bits_to_f32(r.h[0] >> 16);
-        const uint32_t i = u & 3u, sh = 16u * (i & 1u);
-        const uint32_t A = r.h[1] >> sh, M = r.h[2] >> sh, L = r.h[3] >> sh;
+        uint32_t sc[NG], mn[NG];
+        scale_min(r.h, u & 3u, sc, mn);
 #pragma unroll
         for (int g = 0; g < NG; g++) {
-            const uint32_t a = (A >> (8 * g)) & 0xFFu, m = (M >> (8 * g)) & 0xFFu, l = (L >> (8 * g)) & 0xFFu;
-            const uint32_t sc = i < 2u ? (a & 63u) : ((l & 15u) | ((a >> 6) << 4));
-            const uint32_t mn = i < 2u ? (m & 63u) : ((l >> 4) | ((m >> 6) << 4));
-            c.ds[g] = d * (float)sc;
-            c.dm[g] = -(dmin * (float)mn);
+            c.ds[g] = d * (float)sc[g];
+            c.dm[g] = -(dmin * (float)mn[g]);
         }
         return c;
     }

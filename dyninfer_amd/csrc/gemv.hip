@@ -76,7 +76,7 @@ namespace {
 
 struct EncInfo {
     uint32_t chunk_weights;  // weights one lane handles per step
-    bool q6k;                // Q6_K's 20-dword chunks: fewer chunks per lane in latency mode
+    bool wide;               // 64-weight chunks (Q6_K, Q4_K): fewer chunks per lane in latency mode
 };
 
 bool enc_info(uint32_t enc, EncInfo& e) {
@@ -86,7 +86,7 @@ bool enc_info(uint32_t enc, EncInfo& e) {
     case ENC_Q8_0:
     case ENC_MLX_U4: e = {32, false}; return true;
     case ENC_Q6_K: e = {64, true}; return true;
-    case ENC_Q4_K: e = {64, false}; return true;
+    case ENC_Q4_K: e = {64, true}; return true;
     default: return false;
     }
 }
@@ -149,17 +149,21 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     while ((1u << lanes_log2) < L) lanes_log2++;
     // Latency mode (one wave per row block of one row per lane group, all of
     // a lane's chunks loaded at once) when the matrices give at most 16384
-    // such row blocks and a lane few chunks: 4 for one activation row (Q6_K:
-    // 2; at 3 the 8B down_proj ran slower than the pipeline), 2 for 2 rows, 1
-    // for 4 (more chunks or rows cost more in registers, and waves per SIMD,
-    // than the latency saves; timed on the config-1/4 steps).  Otherwise the
-    // persistent pipeline, whose rows per lane group the encoding's launcher
-    // picks from the occupancy of each instantiated tile.
+    // such row blocks and a lane few chunks: 4 for one activation row (64-
+    // weight chunks: 2; at 3 the 8B down_proj ran slower than the pipeline,
+    // Q4_K 4096 x 12288 12.6 against 9.1 us), 2 for 2 rows, 1 for 4 (64-weight
+    // chunks: at most 2048 row blocks; 12288 x 4096 Q4_K 28.6 us against 17.7
+    // us in the pipeline, 1024 x 4096 6.3 against 6.7 us).  More chunks or
+    // rows cost more in registers, and waves per SIMD, than the latency
+    // saves (timed on the config-1/4 steps).  Otherwise the persistent
+    // pipeline, whose rows per lane group the encoding's launcher picks from
+    // the occupancy of each instantiated tile.
     uint64_t rbs1 = 0;
     for (int i = 0; i < nprob; i++) rbs1 += (probs[i].n + (64u >> lanes_log2) - 1) / (64u >> lanes_log2);
     const uint32_t cpl = (nch + L - 1) >> lanes_log2;
-    const uint32_t max_cpl = B == 1 ? (info.q6k ? 2u : 4u) : B == 2 ? 2u : B == 4 ? 1u : 0u;
-    const uint32_t oneshot = cpl >= 1 && cpl <= max_cpl && rbs1 <= 16384 ? cpl : 0u;
+    const uint32_t max_cpl = B == 1 ? (info.wide ? 2u : 4u) : B == 2 ? 2u : B == 4 ? 1u : 0u;
+    const uint64_t max_rbs = B == 4 && info.wide ? 2048u : 16384u;
+    const uint32_t oneshot = cpl >= 1 && cpl <= max_cpl && rbs1 <= max_rbs ? cpl : 0u;
 
     GemvParams p = {};
     for (int i = 0; i < kMaxProblems; i++) {

@@ -871,14 +871,14 @@ hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot,
     }
     if (oneshot) {
         // chunks per lane (the host's limits): 1..4 for one activation row
-        // (Q6_K 1..2), 1..2 for 2 rows, 1 for 4
+        // (Q6_K, Q4_K 1..2), 1..2 for 2 rows, 1 for 4
 #define DMX_ONESHOT(b, c)                                                                             \
     if (B == b && oneshot == c)                                                                       \
         return launch_oneshot(gguf_gemv_oneshot_kernel<E, c, b, XBF16, 512>, gguf_gemv_oneshot_kernel<E, c, b, XBF16, 256>, \
                               p, lds, st);
         DMX_ONESHOT(1, 1)
         DMX_ONESHOT(1, 2)
-        if constexpr (E::ENC != ENC_Q6_K) {
+        if constexpr (E::ENC != ENC_Q6_K && E::ENC != ENC_Q4_K) {
             DMX_ONESHOT(1, 3)
             DMX_ONESHOT(1, 4)
         }

@@ -1,5 +1,5 @@
-// Decode GEMV on MFMA for 3..16 activation rows, GGUF Q4_0 and Q6_K and MLX
-// affine U4 (y[b, o] = Σ_k x[b, k]·w[o, k], f32 accumulation;
+// Decode GEMV on MFMA for 3..16 activation rows, GGUF Q4_0, Q6_K and Q4_K and
+// MLX affine U4 (y[b, o] = Σ_k x[b, k]·w[o, k], f32 accumulation;
 // gguf_codegen.rs:268-314 `emit_linear` with the dequantisations of :412-472
 // (Q4_0) and :474-526 (Q6_K), mlx_affine.rs:557-626 `emit_linear_u4`).
 //
@@ -102,7 +102,7 @@ struct MfmaQ40 {
     static constexpr uint32_t UNIT = 32, UPT = 8, UB = 18;   // weights, bytes per block; blocks per task
     static constexpr uint32_t TB = UPT * UB;                 // bytes of a row per task
     static constexpr uint32_t NP = 10, WB = 176;             // window pieces, LDS row bytes
-    static constexpr bool ROWSCALE = false, MLX = false, PAIR4 = false;
+    static constexpr bool ROWSCALE = false, MLX = false, PAIR4 = false, BIAS = false;
     static constexpr uint32_t STAGE = 8;  // staging passes per chunk of loads
     // Pieces 0..8 hold window bytes [0, 144) at LDS 16i; piece 9 is [128, 144)
     // (sh = 0) or [132, 148) (sh = 2) at LDS [144, 160), so window dword 36
@@ -144,7 +144,7 @@ struct MfmaQ6K {
     static constexpr uint32_t UNIT = 256, UPT = 1, UB = 210;
     static constexpr uint32_t TB = UB;
     static constexpr uint32_t NP = 14, WB = 240;
-    static constexpr bool ROWSCALE = true, MLX = false, PAIR4 = false;
+    static constexpr bool ROWSCALE = true, MLX = false, PAIR4 = false, BIAS = false;
     static constexpr uint32_t STAGE = 8;
     // Pieces 0..12 hold window bytes [0, 208) at LDS 16i; piece 13 is
     // [196, 212) at LDS [208, 224), so window dword 52 (d) sits at LDS dword 55.
@@ -196,6 +196,49 @@ struct MfmaQ6K {
     }
 };
 
+// Q4_K (GGML block_q4_K; the reference's schema gguf_block.rs:183-316): a
+// task is one super-block (144 bytes of a row, 4-byte aligned, so no
+// realignment); lane quarter q decodes step q (encodings.hpp EncQ4K): MFMA j
+// takes code dword j, the low nibbles of weights 64q + 4j.. (sub-block 2q,
+// run0) and the high nibbles of 64q + 32 + 4j.. (sub-block 2q + 1, run1).
+// w = d·(sc·q) - dmin·m: the B operand is sc·q (exact in f16, <= 945) and d
+// multiplies the task's product per weight row in f32; the offsets take a
+// ninth MFMA (BIAS): B holds 32·m of the lane's two sub-blocks in k slots
+// 8q, 8q + 1 (exact), A the matching activation sums X/32 of each row
+// (staged with the activations, one f16 rounding), and that product is
+// subtracted times dmin.
+struct MfmaQ4K {
+    static constexpr int KT = 256, NM = 8, PF = 4, TPI = 2;
+    static constexpr uint32_t UNIT = 256, UPT = 1, UB = 144;
+    static constexpr uint32_t TB = UB;
+    static constexpr uint32_t NP = 9, WB = 144;
+    static constexpr bool ROWSCALE = false, MLX = false, PAIR4 = false, BIAS = true;
+    static constexpr uint32_t STAGE = 8;
+    __device__ static uint32_t goff(uint32_t piece, uint32_t) { return 16u * piece; }
+    __device__ static uint32_t run0(uint32_t q, uint32_t j) { return 64u * q + 4u * j; }
+    __device__ static uint32_t run1(uint32_t q, uint32_t j) { return run0(q, j) + 32u; }
+    // mb = the f16 pair (32·m_2q, 32·m_2q+1); d, dmin zero for a padding task
+    __device__ static void decode(const u32a* win, bool ok, uint32_t q, uint4 (&a)[NM], uint32_t& mb, float& d,
+                                  float& dmin) {
+        const uint32_t h[4] = {win[0], win[1], win[2], win[3]};
+        uint32_t sc[2], mn[2];
+        EncQ4K::scale_min(h, q, sc, mn);
+        d = ok ? f16_bits_to_f32(h[0]) : 0.0f;
+        dmin = ok ? f16_bits_to_f32(h[0] >> 16) : 0.0f;
+        const _Float16 s0 = (_Float16)sc[0], s1 = (_Float16)sc[1];  // exact: < 64
+        const h2 s2lo = {s0, s0}, s2hi = {s1, s1};
+        mb = __builtin_bit_cast(uint32_t, h2{(_Float16)(32u * mn[0]), (_Float16)(32u * mn[1])});  // exact: <= 2016
+#pragma unroll
+        for (int j = 0; j < NM; j++) {
+            const uint32_t D = win[4u + 8u * q + (uint32_t)j], D8 = D >> 8;
+            a[j] = make_uint4(wq(and_or(D, 0x000F000Fu, 0x64006400u), (_Float16)-1024.0f, s2lo),
+                              wq(and_or(D8, 0x000F000Fu, 0x64006400u), (_Float16)-1024.0f, s2lo),
+                              wq(and_or(D, 0x00F000F0u, 0x54005400u), (_Float16)-64.0f, s2hi),
+                              wq(and_or(D8, 0x00F000F0u, 0x54005400u), (_Float16)-64.0f, s2hi));
+        }
+    }
+};
+
 // MLX affine U4 (mlx_affine.rs:557-626, fixture.rs:307-311): a task is 256
 // weights of a row, 32 packed words (128 bytes, 16-byte aligned rows, so no
 // realignment); lane quarter q decodes words 8q..8q+7 (k 64q..64q+63), MFMA j
@@ -208,7 +251,7 @@ struct MfmaMlxU4 {
     static constexpr uint32_t UNIT = 256, UPT = 1, UB = 128;
     static constexpr uint32_t TB = UB;
     static constexpr uint32_t NP = 8, WB = 144;
-    static constexpr bool ROWSCALE = false, MLX = true, PAIR4 = true;
+    static constexpr bool ROWSCALE = false, MLX = true, PAIR4 = true, BIAS = false;
     static constexpr uint32_t STAGE = 8;
     __device__ static uint32_t goff(uint32_t piece, uint32_t) { return 16u * piece; }
     __device__ static uint32_t run0(uint32_t q, uint32_t j) { return 64u * q + 8u * j; }
@@ -241,7 +284,9 @@ struct MfmaMlxU4 {
 };
 
 // LDS: activations [task][j][64 lanes] x 16 bytes, the inverse scales
-// [task][16 rows] f32, then each wave's window of 16 rows x WB bytes.  Tasks
+// [task][16 rows] f32, for BIAS encodings the activation sums [task][16
+// rows][4 quarters] as f16 pairs, then each wave's window of 16 rows x WB
+// bytes.  Tasks
 // of a segment are padded to a multiple of PF (the padding tasks have zero
 // weights and activations).
 // Split mode (few tiles): the 8 waves of a workgroup share each tile, wave w
@@ -251,9 +296,13 @@ __host__ __device__ constexpr uint32_t mfma_tasks(uint32_t nunit) {
     constexpr uint32_t pad = SPLIT ? 16u : (uint32_t)M::PF;
     return ((nunit + M::UPT - 1u) / M::UPT + pad - 1u) / pad * pad;
 }
+template <class M>
+__host__ __device__ constexpr uint32_t mfma_task_lds() {
+    return M::NM * 64u * 16u + 64u + (M::BIAS ? 256u : 0u);
+}
 template <class M, bool SPLIT>
 __host__ __device__ constexpr uint32_t mfma_lds_bytes(uint32_t nunit) {
-    return mfma_tasks<M, SPLIT>(nunit) * (M::NM * 64u * 16u + 64u) + (kMfmaThreads / 64u) * 16u * M::WB;
+    return mfma_tasks<M, SPLIT>(nunit) * mfma_task_lds<M>() + (kMfmaThreads / 64u) * 16u * M::WB;
 }
 
 // Slot of A-operand lane l (row b = l % 16, quarter q = l / 16) in the 64
@@ -281,7 +330,8 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint4* xl = reinterpret_cast<uint4*>(lds);
     float* inv = reinterpret_cast<float*>(lds + ng * NM * 64u * 16u);
-    uint8_t* wins = lds + ng * (NM * 64u * 16u + 64u);  // the waves' windows
+    uint32_t* xs = reinterpret_cast<uint32_t*>(lds + ng * (NM * 64u * 16u + 64u));  // BIAS: activation sums
+    uint8_t* wins = lds + ng * mfma_task_lds<M>();      // the waves' windows
     uint8_t* win = wins + wv * 16u * M::WB;             // this wave's window
 
     // ---- weight tiles.  Whole tiles per wave: wave wid takes tiles wid,
@@ -475,6 +525,20 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
         // of one run of 8 (MLX words)
         const uint4 val = M::PAIR4 ? make_uint4(pk(v[0], v[4]), pk(v[1], v[5]), pk(v[2], v[6]), pk(v[3], v[7]))
                                    : make_uint4(pk(v[0], v[2]), pk(v[1], v[3]), pk(v[4], v[6]), pk(v[5], v[7]));
+        if constexpr (M::BIAS) {
+            // the unit's two runs summed as stored (f16 values, exact in f32
+            // but for the last bits of 32-term sums), over the NM units of
+            // its quarter (8 consecutive lanes), stored / 32 as f16 (below
+            // 2^14) for the offset MFMA
+            const uint32_t one2 = 0x3C003C00u;
+            float s0 = dot2(val.x, one2, dot2(val.y, one2, 0.0f)), s1 = dot2(val.z, one2, dot2(val.w, one2, 0.0f));
+            auto fadd = [](uint32_t a, uint32_t c) { return __float_as_uint(__uint_as_float(a) + __uint_as_float(c)); };
+            s0 = __uint_as_float(lanes_reduce<8>(__float_as_uint(s0), fadd));
+            s1 = __uint_as_float(lanes_reduce<8>(__float_as_uint(s1), fadd));
+            typedef float f32x2 __attribute__((ext_vector_type(2)));
+            const f32x2 f = {s0 * 0.03125f, s1 * 0.03125f};
+            if (u < nunits && j == 0) xs[(g * 16u + b) * 4u + qq] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));
+        }
         if (u < nunits) {
             xl[(g * NM + j) * 64u + xslot(b + 16u * qq, j)] = val;
             if (e == 0) inv[g * 16u + b] = ldexpf(1.0f, -sh);
@@ -539,7 +603,21 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
 #pragma unroll
         for (uint32_t j = 0; j < NM; j++) xa[j] = xl[(t * NM + j) * 64u + xslot(lane, j)];
         uint4 a[NM];
-        if constexpr (M::MLX) {
+        if constexpr (M::BIAS) {
+            uint32_t mb;
+            float dd, dm;
+            M::decode(reinterpret_cast<const u32a*>(win + m * M::WB), t < nt, q, a, mb, dd, dm);
+            f32x4 tmp = zero;
+#pragma unroll
+            for (uint32_t j = 0; j < NM; j++)
+                tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, xa[j]), __builtin_bit_cast(h8, a[j]), tmp, 0, 0, 0);
+            // A: the sums of activation row lane % 16 for the lane's quarter's two sub-blocks
+            const uint4 xo = make_uint4(xs[(t * 16u + m) * 4u + q], 0u, 0u, 0u), wo = make_uint4(mb, 0u, 0u, 0u);
+            const f32x4 off = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, xo), __builtin_bit_cast(h8, wo), zero, 0, 0, 0);
+#pragma unroll
+            for (int c = 0; c < 4; c++) tmp[c] = fmaf(tmp[c], dd, -(off[c] * dm));
+            return tmp;
+        } else if constexpr (M::MLX) {
             uint32_t g0, g1;
             sbgroups(r, t, g0, g1);
             const uint32_t sh0 = 8u * ((g0 * es) & 3u), sh1 = 8u * ((g1 * es) & 3u);
@@ -781,7 +859,9 @@ int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16, uint32_t min_tiles) {
 
 bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool y_bf16,
                        uint32_t group) {
-    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K && enc != ENC_MLX_U4) || batch < 3 || batch > 16 || K % 256u) return false;
+    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K && enc != ENC_Q4_K && enc != ENC_MLX_U4) || batch < 3 || batch > 16 ||
+        K % 256u)
+        return false;
     if (enc == ENC_MLX_U4 && (group == 0 || group % 32u)) return false;
     uint32_t tiles = 0;
     uint64_t rows = 0;
@@ -798,12 +878,16 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     // 7-9 us on VALU at 5-8 rows, 13-15 against 14-18 us at 16 rows).
     // At 3-4 rows only the largest launches gain (8B lm_head at 4 rows: 114 us on MFMA against 181 us;
     // at 2 rows both take ~111 us).
-    const uint64_t bytes = rows * (enc == ENC_Q4_0 ? K / 32u * 18u : enc == ENC_Q6_K ? K / 256u * 210u : K / 2u);
+    const uint64_t bytes = rows * (enc == ENC_Q4_0   ? K / 32u * 18u
+                                   : enc == ENC_Q6_K ? K / 256u * 210u
+                                   : enc == ENC_Q4_K ? K / 256u * 144u
+                                                     : K / 2u);
     if (batch < 5 && tiles < kMfmaSplitTiles) return false;
     if (batch <= max_register_batch(enc) && bytes < (8ull << 20) && tiles < kMfmaSplitTiles) return false;
     const uint32_t min_tiles = mfma_min_tiles(enc, batch);
     const int mode = enc == ENC_Q4_0   ? mfma_mode<MfmaQ40>(K, tiles, y_bf16, min_tiles)
                    : enc == ENC_Q6_K   ? mfma_mode<MfmaQ6K>(K, tiles, y_bf16, min_tiles)
+                   : enc == ENC_Q4_K   ? mfma_mode<MfmaQ4K>(K, tiles, y_bf16, min_tiles)
                                        : mfma_mode<MfmaMlxU4>(K, tiles, y_bf16, min_tiles);
     return mode != 0;
 }
@@ -813,6 +897,7 @@ hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, u
     if (nprob < 1 || nprob > kMaxProblems) return hipErrorInvalidValue;
     if (enc == ENC_Q4_0) return launch_mfma<MfmaQ40>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     if (enc == ENC_Q6_K) return launch_mfma<MfmaQ6K>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
+    if (enc == ENC_Q4_K) return launch_mfma<MfmaQ4K>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     if (enc == ENC_MLX_U4) return launch_mfma<MfmaMlxU4>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     return hipErrorInvalidValue;
 }

@@ -198,6 +198,60 @@ def test_multi_weights_share_activations(ctx, batch):
         assert err <= TOL and err <= XF16, err
 
 
+# ---------------------------------------------------------------- MFMA GEMV (5..16 rows)
+# Large launches at 5..16 rows run on MFMA: B = sc·q exact in f16, d applied
+# per weight row in f32, the offsets Σ_j dmin·m_j·X_j through one more MFMA
+# whose activation sums X_j are rounded once to f16.  Per output the error is
+# at most 2^-11·Σ|w||x| (activation rounding) + 2^-11·Σ|dmin·m||x| (sums)
+# plus f32 accumulation.
+def offsets_of(data, n, k):
+    """|dmin·m| per weight: the dequantisation with every d set to zero."""
+    z = data.reshape(-1, 144).copy()
+    z[:, 0:2] = 0
+    return np.abs(oracle.dequant_gguf(Q4K, z.ravel(), n, k))
+
+
+MFMA_CASES = [  # (n, k, batch, y_bf16): split mode, whole tiles, K segments, a padded tile
+    (4096, 4096, 5, False), (4096, 4096, 16, True), (12288, 4096, 8, False), (4096, 12288, 16, False),
+    (20000, 1024, 12, False), (2056, 2048, 16, False), (2048, 4096, 7, True)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,k,batch,ybf16", MFMA_CASES)
+def test_gemv_mfma(ctx, n, k, batch, ybf16):
+    import torch
+    w, data = weight(n, k, seed=n + k + batch, off=4 if ybf16 else 0)
+    x = oracle.randn(batch * k, seed=batch * 3 + k).reshape(batch, k)
+    y = ctx.qlinear(w, dev(x), y_dtype=torch.bfloat16 if ybf16 else torch.float32).float().cpu().numpy()
+    wf = oracle.dequant_gguf(Q4K, data, n, k)
+    y64, absdot = oracle.linear_f64(x, wf)
+    absb = np.abs(x.astype(np.float64)) @ offsets_of(data, n, k).astype(np.float64).T
+    err = np.abs(y - y64) / absdot
+    bound = 2.0 ** -11 + 2.0 ** -11 * absb / absdot + 2e-5
+    if ybf16:
+        bound = bound + 2.0 ** -9 * np.abs(y64) / absdot
+    assert np.all(err <= bound), (err / bound).max()
+    assert oracle.normalized_error(y, y64, absdot) <= TOL
+
+
+@pytest.mark.gpu
+def test_gemv_mfma_large_offsets(ctx):
+    """Blocks whose offsets dominate (dmin·m far above d·sc·q): the offset
+    MFMA's rounding stays within its bound."""
+    n, k, batch = 4096, 2048, 16
+    data = oracle.synth_gguf(Q4K, n, k, 8).reshape(-1, 144)
+    data[:, 2:4] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)  # dmin = 0.5
+    data = data.ravel()
+    w = d.QWeight(d.ENC_Q4_K, n, k, dev(data))
+    x = oracle.randn(batch * k, seed=4).reshape(batch, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(Q4K, data, n, k))
+    absb = np.abs(x.astype(np.float64)) @ offsets_of(data, n, k).astype(np.float64).T
+    err = np.abs(y - y64) / absdot
+    assert np.all(err <= 2.0 ** -11 + 2.0 ** -11 * absb / absdot + 2e-5)
+    assert oracle.normalized_error(y, y64, absdot) <= TOL
+
+
 @pytest.mark.gpu
 def test_deterministic(ctx):
     w, _ = weight(4096, 4096, seed=1)
