@@ -206,13 +206,20 @@ dmx::GemvProblem problem_of(const dyninfer_qweight_t* w, void* y) {
 size_t esize(uint32_t dt) { return dt == DYNINFER_DTYPE_F32 ? 4 : 2; }
 
 // Whether `rows` activation rows run the prefill GEMM (else the GEMV kernels
-// over 16-row chunks).  The 16-row GEMV of Q4_0 and Q6_K runs on MFMA, and
-// two or three of its chunks take less time than staging plus a GEMM launch
-// below 48 rows; Q4_1, Q8_0 and MLX U4 take the GEMM from 17 rows (MLX
+// over 16-row chunks).  Q4_1, Q8_0 and MLX U4 take the GEMM from 17 rows (MLX
 // 4096x1024: 13.4 against 17.0 us at 17 rows, 19.8 against 380 us at 512).
+// The 16-row GEMV of Q4_0, Q6_K and Q4_K runs on MFMA, and two of its chunks
+// (17..32 rows) mostly take less time than staging plus a GEMM with so few
+// workgroups (Q4_0 4096x4096 at 24 rows: 21.5 against 23.8 us; Q6_K 1024x4096
+// 23.2 against 35.6 us), three never do (40 rows: Q4_0 4096x4096 32.2 against
+// 24.6 us, 12288x4096 52.4 against 28.2 us); with K above 8192 the MFMA GEMV
+// splits K over launches and the GEMM wins from 17 rows (Q4_0 4096x12288:
+// 60.9 against 73.2 us, Q4_K 66.9 against 81.8 us).
 bool has_prefill_gemm(uint32_t enc, uint32_t N, uint32_t K, uint32_t rows) {
-    const bool mfma_gemv = enc == DYNINFER_ENC_GGUF_Q4_0 || enc == DYNINFER_ENC_GGUF_Q6_K;
-    const uint32_t min_rows = mfma_gemv ? 48u : (uint32_t)dmx::kMaxGemvBatch + 1u;
+    const bool mfma_gemv =
+        enc == DYNINFER_ENC_GGUF_Q4_0 || enc == DYNINFER_ENC_GGUF_Q6_K || enc == DYNINFER_ENC_GGUF_Q4_K;
+    const uint32_t min_rows = mfma_gemv && K <= 8192u ? 2u * (uint32_t)dmx::kMaxGemvBatch + 1u
+                                                      : (uint32_t)dmx::kMaxGemvBatch + 1u;
     return rows >= min_rows && dmx::gemm_supported(enc, N, K, rows);
 }
 

@@ -100,4 +100,19 @@ __device__ __forceinline__ void q4k_scale_min(const uint8_t* s12, uint32_t j, ui
     }
 }
 
+// The same for the two sub-blocks 2i and 2i + 1 (i = 0..3) from the scale
+// bytes held as dwords s0 = bytes 0..3, s1 = 4..7, s2 = 8..11: they sit at
+// byte positions 2(i & 1) and 2(i & 1) + 1 of each.
+__device__ __forceinline__ void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t i,
+                                                   uint32_t (&sc)[2], uint32_t (&mn)[2]) {
+    const uint32_t sh = 16u * (i & 1u);
+    const uint32_t A = s0 >> sh, M = s1 >> sh, L = s2 >> sh;
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+        const uint32_t a = (A >> (8 * g)) & 0xFFu, m = (M >> (8 * g)) & 0xFFu, l = (L >> (8 * g)) & 0xFFu;
+        sc[g] = i < 2u ? (a & 63u) : ((l & 15u) | ((a >> 6) << 4));
+        mn[g] = i < 2u ? (m & 63u) : ((l >> 4) | ((m >> 6) << 4));
+    }
+}
+
 }  // namespace dmx

@@ -363,20 +363,10 @@ struct EncQ4K {
         return r;
     }
     // The 6-bit scales and mins of sub-blocks 2i and 2i + 1 (i = step 0..3)
-    // from the header dwords h[1..3]: they sit at scale-byte positions
-    // 2(i & 1) and 2(i & 1) + 1 of bytes 0..3 (scales j < 4, top bits of the
-    // scales j >= 4), 4..7 (mins j < 4, top bits of the mins j >= 4) and
-    // 8..11 (the low nibbles of j >= 4: scale low, min high).
+    // from the header dwords h[1..3] (device_common.hpp q4k_scale_min_pair).
     __device__ __forceinline__ static void scale_min(const uint32_t (&h)[4], uint32_t i, uint32_t (&sc)[NG],
                                                      uint32_t (&mn)[NG]) {
-        const uint32_t sh = 16u * (i & 1u);
-        const uint32_t A = h[1] >> sh, M = h[2] >> sh, L = h[3] >> sh;
-#pragma unroll
-        for (int g = 0; g < NG; g++) {
-            const uint32_t a = (A >> (8 * g)) & 0xFFu, m = (M >> (8 * g)) & 0xFFu, l = (L >> (8 * g)) & 0xFFu;
-            sc[g] = i < 2u ? (a & 63u) : ((l & 15u) | ((a >> 6) << 4));
-            mn[g] = i < 2u ? (m & 63u) : ((l >> 4) | ((m >> 6) << 4));
-        }
+        q4k_scale_min_pair(h[1], h[2], h[3], i, sc, mn);
     }
     __device__ __forceinline__ static Chunk unpack(const Raw& r, uint32_t u) {
         Chunk c;

@@ -1,5 +1,5 @@
-// Prefill GEMM on gfx950 MFMA for the GGUF encodings Q4_0, Q4_1, Q8_0 and
-// Q6_K and for MLX affine U4: Y[M, N] = X[M, K] · Wᵀ with f32 accumulation.
+// Prefill GEMM on gfx950 MFMA for the GGUF encodings Q4_0, Q4_1, Q8_0, Q6_K
+// and Q4_K and for MLX affine U4: Y[M, N] = X[M, K] · Wᵀ with f32 accumulation.
 //
 // Reference semantics: the same `emit_linear` contraction as decode
 // (gguf_codegen.rs:268-314, dequantisations :412-472 Q4_0, :382-410 Q8_0,
@@ -32,7 +32,8 @@
 //     the offset (exact) and a packed multiply by the block scale rounds once
 //     (Q4_0 RNE_f16((q-8)·d), Q8_0 RNE_f16(q·d)); Q4_1 a packed fma,
 //     RNE_f16(q·d + m); Q6_K RNE_f16((q-32)·RNE_f16(d·sc)) (its window and
-//     decode are described at WinQ6K); MLX U4 RNE_f16(q·s + b) (WinMlx).
+//     decode are described at WinQ6K); MLX U4 RNE_f16(q·s + b) (WinMlx);
+//     Q4_K RNE_f16(q·RNE_f16(d·sc) - RNE_f16(dmin·m)) (WinQ4K).
 //   * The weights are the MFMA's A operand and the activations its B, so each
 //     lane ends with 4 consecutive output columns of one row per block and
 //     stores them as one 16-byte (f32) or 8-byte (bf16) write.  K slices meet
@@ -41,7 +42,8 @@
 //   * Workgroups that read the same weight rows run on the same XCD
 //     (workgroup i goes to XCD i % 8).
 // Accuracy: |y - y_exact| <= 2^-10·Σ|w||x| (one f16 rounding of each weight and
-// of each activation; Q6_K's weights round twice: (2^-10 + 2^-11)·Σ|w||x|) +
+// of each activation; Q6_K's weights round twice: (2^-10 + 2^-11)·Σ|w||x|;
+// Q4_K's scale and offset round once each, adding 2^-11·Σ(|q·d·sc| + |dmin·m|)|x|) +
 // f32 accumulation error, inside the 2e-3 normalised tolerance.  Weights must
 // be finite in f16 (|w| <= 65504: |d| <= 8188 for Q4_0, |d·sc| <= 2047 for
 // Q6_K).
@@ -497,9 +499,95 @@ struct WinMlx {
     }
 };
 
+// GGUF Q4_K (GGML block_q4_K, 144-byte super-blocks of 256 weights; the
+// reference's schema gguf_block.rs:183-316): chunk g of a row is step
+// i = g % 4 of super-block g / 4, weights 64i + 0..63: lane half h decodes
+// nibble h of qs[32i + l], l = 0..31 (weight 64i + 32h + l, sub-block
+// 2i + h), so an MFMA k step takes l = 8t .. 8t+7 in the order of Q8_0.  The
+// window per row: the super-block's 16-byte header (d, dmin, the 12 scale
+// bytes) and the step's 32 code bytes, three 16-byte pieces (super-blocks
+// are 4-byte aligned: 144 = 36 dwords).  w = RNE_f16(q·RNE_f16(d·sc) -
+// RNE_f16(dmin·m)) by one packed fma (d·sc and dmin·m exact in f32).
+struct WinQ4K {
+    static constexpr uint32_t NP = 3, kCopies = NP;
+    static constexpr uint32_t kPitch = 16u * NP;
+    static constexpr uint32_t kBytes = 64u * kPitch;
+    static constexpr uint32_t kDw = 12;  // d|dmin, three scale dwords, 8 code dwords
+    static constexpr uint32_t kValuPerStep = 14;
+    struct Scale {
+        h2 ds, ndm, off;
+        uint32_t mask, magic;
+    };
+    uintptr_t rb[NP];  // row of each copy lane
+    uint32_t pp[NP];   // piece of each copy lane
+    uint32_t c0, lane;
+
+    __device__ void init(const GemmArgs& a, uint32_t n0, uint32_t lane_, uint32_t c0_) {
+        lane = lane_;
+        c0 = c0_;
+#pragma unroll
+        for (uint32_t q = 0; q < NP; q++) {
+            const uint32_t li = 64u * q + lane, r = li / NP;
+            const uint32_t n = n0 + r < a.N ? n0 + r : a.N - 1u;  // past N: re-read the last row (never stored)
+            rb[q] = (uintptr_t)a.w + (uintptr_t)n * a.rowbytes;
+            pp[q] = li % NP;
+        }
+    }
+    __device__ void issue(uint32_t c, uint8_t* win) const {
+        const uint32_t g = c0 + c, sb = g >> 2, i = g & 3u;
+#pragma unroll
+        for (uint32_t q = 0; q < NP; q++) {
+            const uint32_t o = pp[q] == 0u ? 0u : 16u + 32u * i + 16u * (pp[q] - 1u);
+            dma16(reinterpret_cast<const void*>(rb[q] + (uintptr_t)sb * 144u + o), win + 1024u * q);
+        }
+    }
+    __device__ void read(uint32_t, const uint8_t* win, uint32_t* raw) const {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint8_t* w = win + (32u * j + (lane & 31u)) * kPitch;
+            uint32_t* o = raw + j * kDw;
+#pragma unroll
+            for (uint32_t v = 0; v < NP; v++) {
+                const u32x4 x = *reinterpret_cast<const u32x4*>(w + 16u * v);
+                o[4 * v] = x.x;
+                o[4 * v + 1] = x.y;
+                o[4 * v + 2] = x.z;
+                o[4 * v + 3] = x.w;
+            }
+        }
+    }
+    __device__ Scale scale(uint32_t c, int, const uint32_t* r) const {
+        const uint32_t h = lane >> 5;
+        uint32_t sc[2], mn[2];
+        q4k_scale_min_pair(r[1], r[2], r[3], (c0 + c) & 3u, sc, mn);
+        const float d = f16_bits_to_f32(r[0]), dmin = f16_bits_to_f32(r[0] >> 16);
+        const _Float16 ds = (_Float16)(d * (float)(h ? sc[1] : sc[0]));      // exact f32 product, one rounding
+        const _Float16 dm = (_Float16)(-(dmin * (float)(h ? mn[1] : mn[0])));
+        const _Float16 o = h ? (_Float16)-64.0f : (_Float16)-1024.0f;
+        Scale s;
+        s.ds = h2{ds, ds};
+        s.ndm = h2{dm, dm};
+        s.off = h2{o, o};
+        s.mask = h ? 0x00F000F0u : 0x000F000Fu;
+        s.magic = h ? 0x54005400u : 0x64006400u;  // code bits under the exponent of 64 / 1024
+        return s;
+    }
+    __device__ h8 step(const uint32_t* r, const Scale& s, int t) const {
+        auto f = [&](uint32_t v) {
+            return as_u(__builtin_elementwise_fma(as_h2(and_or(v, s.mask, s.magic)) + s.off, s.ds, s.ndm));
+        };
+        const uint32_t c = r[4 + 2 * t], c2 = r[5 + 2 * t];
+        return as_h8(f(c), f(c >> 8), f(c2), f(c2 >> 8));
+    }
+};
+
 template <uint32_t ENC>
 struct WinOf {
     using type = WinBlocks<ENC>;
+};
+template <>
+struct WinOf<ENC_Q4_K> {
+    using type = WinQ4K;
 };
 template <>
 struct WinOf<ENC_MLX_U4> {
@@ -811,13 +899,15 @@ uint32_t gemm_layout(uint32_t enc) {
         case ENC_Q4_1: return Blk<ENC_Q4_1>::kLayout;
         case ENC_Q8_0: return Blk<ENC_Q8_0>::kLayout;
         case ENC_Q6_K: return XFRAG_BYTE;  // a lane's 32 codes in order, as Q8_0
+        case ENC_Q4_K: return XFRAG_BYTE;
         case ENC_MLX_U4: return XFRAG_WORD;
         default: return ~0u;
     }
 }
 
 bool gemm_supported(uint32_t enc, uint32_t N, uint32_t K, uint32_t M) {
-    return gemm_layout(enc) != ~0u && N > 0 && M > 0 && K >= 64u && K % (enc == ENC_Q6_K ? 256u : 64u) == 0;
+    return gemm_layout(enc) != ~0u && N > 0 && M > 0 && K >= 64u &&
+           K % (enc == ENC_Q6_K || enc == ENC_Q4_K ? 256u : 64u) == 0;
 }
 
 hipError_t gemm_launch(const GemmWeight& wt, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs, uint32_t M,
@@ -844,6 +934,7 @@ hipError_t gemm_launch(const GemmWeight& wt, uint32_t N, uint32_t K, const uint1
         case ENC_Q4_1: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q4_1>::kBytes; break;
         case ENC_Q8_0: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q8_0>::kBytes; break;
         case ENC_Q6_K: a.rowbytes = (uint64_t)(K / 256u) * 210u; break;
+        case ENC_Q4_K: a.rowbytes = (uint64_t)(K / 256u) * 144u; break;
         default: a.rowbytes = (uint64_t)K / 2u; break;  // MLX packed words (scales and biases besides)
     }
     // M-major tile order when the staged activations (2 bytes per element)
@@ -854,6 +945,7 @@ hipError_t gemm_launch(const GemmWeight& wt, uint32_t N, uint32_t K, const uint1
         case ENC_Q4_1: return launch_enc<ENC_Q4_1>(a, st);
         case ENC_Q8_0: return launch_enc<ENC_Q8_0>(a, st);
         case ENC_Q6_K: return launch_enc<ENC_Q6_K>(a, st);
+        case ENC_Q4_K: return launch_enc<ENC_Q4_K>(a, st);
         case ENC_MLX_U4: return launch_enc<ENC_MLX_U4>(a, st);
         default: return hipErrorInvalidValue;
     }

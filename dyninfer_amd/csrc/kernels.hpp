@@ -107,7 +107,7 @@ hipError_t gather_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, cons
 // 32.  Lane half h of k step 4c + t holds 8 k of k = 64c + 32h + (0..31):
 enum XFrag : uint32_t {
     XFRAG_NIB = 2,   // Q4_0, Q4_1: 4t, 4t+2, 4t+1, 4t+3, 16+4t, 18+4t, 17+4t, 19+4t
-    XFRAG_BYTE = 3,  // Q8_0, Q6_K: 8t + (0, 2, 1, 3, 4, 6, 5, 7)
+    XFRAG_BYTE = 3,  // Q8_0, Q6_K, Q4_K: 8t + (0, 2, 1, 3, 4, 6, 5, 7)
     XFRAG_WORD = 4,  // MLX U4:     8t + (0, 4, 1, 5, 2, 6, 3, 7)
 };
 hipError_t xprep_launch(const void* x, bool x_bf16, uint32_t M, uint32_t K, uint32_t layout, uint16_t* xh, float* rs,

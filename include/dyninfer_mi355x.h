@@ -116,12 +116,12 @@ const char* dyninfer_mi355x_last_error(void);
  * gguf_codegen.rs:157-159).  `rows` = activation rows (1..16 for decode; any for prefill).
  * x: [rows, K] row-major, 16-byte aligned, dtype x_dtype (f32 or bf16, every encoding);
  * y: [rows, N], dtype y_dtype (f32 or bf16).
- *   rows <= 16: the decode GEMV kernels (HBM-bound; 5..16 rows of large Q4_0, Q6_K and
- *     MLX weights on MFMA), activations rounded to f16 after a power-of-two scaling per
- *     scale group;
- *   rows >= 17: the prefill path.  Q4_1, Q8_0 and MLX U4 from 17 rows, Q4_0 and Q6_K
- *     from 48 rows (below that their 16-row MFMA GEMV chunks are faster), K a multiple
- *     of 64 (256 for Q6_K): x is staged once per call as f16 MFMA operand fragments,
+ *   rows <= 16: the decode GEMV kernels (HBM-bound; 5..16 rows of large Q4_0, Q6_K, Q4_K
+ *     and MLX weights on MFMA), activations rounded to f16 after a power-of-two scaling
+ *     per scale group;
+ *   rows >= 17: the prefill path.  Q4_1, Q8_0 and MLX U4 from 17 rows, Q4_0, Q6_K and
+ *     Q4_K from 33 rows, or from 17 when K > 8192 (below that two 16-row MFMA GEMV
+ *     chunks are mostly faster), K a multiple of 64 (256 for Q6_K and Q4_K): x is staged once per call as f16 MFMA operand fragments,
  *     each row scaled by a power of two (RNE) and the rows padded with zeros to a
  *     multiple of 32; then one MFMA GEMM per weight decodes the GGUF blocks or MLX words
  *     straight into MFMA operands.  The staging
@@ -135,8 +135,8 @@ const char* dyninfer_mi355x_last_error(void);
  *     then does on every replay (the no-allocation variant below avoids that).
  *     A stream that is destroyed while the context lives must have finished its work
  *     first (its handle may be reused by a new stream).  Every other case (K not a
- *     multiple of 64, Q4_0 and Q6_K below 48 rows) runs the GEMV kernels over 16-row
- *     chunks and needs no workspace.
+ *     multiple of 64, Q4_0, Q6_K and Q4_K at 17..32 rows with K <= 8192) runs the GEMV
+ *     kernels over 16-row chunks and needs no workspace.
  * Error bound: |y - y_exact| <= 2^-10 * sum_k |w||x| plus f32 accumulation, where a
  * prefill activation more than 2^29 below its row's largest magnitude may also be
  * flushed to f16 subnormals (absolute 2^-40 * max|x| each).

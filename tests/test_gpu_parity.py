@@ -360,7 +360,7 @@ def test_gemm(ctx, gtype, m, n, k, ybf16):
     assert np.all(err <= 2.0 ** -11 + 1e-5 + extra), err.max()
 
 
-# Q6_K: K a multiple of 256, the GEMM from 48 rows (shape -> TM, S)
+# Q6_K: K a multiple of 256, the GEMM from 33 rows (shape -> TM, S)
 GEMM_SHAPES_Q6K = [(50, 20000, 256),   # TM2 S1/2
                    (64, 1000, 512),
                    (100, 300, 512),    # TM4

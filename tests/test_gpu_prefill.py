@@ -4,8 +4,8 @@ decode, through the C ABI, against the CPU oracle:
   * prefill (rows >= 17) with f32 and bf16 activations for every encoding,
     through qlinear and qlinear_multi: the GGUF encodings run the
     staged-activation MFMA GEMM (x rounded once to f16 after a power-of-two
-    scaling per row; Q4_0 and Q6_K from 48 rows), MLX and the shorter Q4_0 and
-    Q6_K prefills the GEMV kernels over 16-row chunks (the chunks' x and y
+    scaling per row; Q4_0 and Q6_K from 33 rows, 17 when K > 8192), MLX and the
+    shorter Q4_0 and Q6_K prefills the GEMV kernels over 16-row chunks (the chunks' x and y
     pointer arithmetic is what the 17/32/200/512 row counts check);
   * bf16 activations on the decode GEMV for every encoding;
   * grouped launches (q/k/v, gate/up) for every encoding at the Qwen3-0.6B
@@ -84,6 +84,17 @@ def test_prefill_rows(ctx, kind, rows, xbf16):
     n, k = 384, 1024
     w, wf = make(kind, n, k, seed=rows + 3)
     xd, x = xs(rows, k, seed=rows, bf16=xbf16)
+    assert err_of(ctx.qlinear(w, xd), x, wf) <= tol(kind)
+
+
+@pytest.mark.parametrize("kind", ALL, ids=IDS.get)
+@pytest.mark.parametrize("rows", [17, 24])
+def test_prefill_long_k(ctx, kind, rows):
+    """K above 8192: the GEMM from 17 rows for every encoding (the MFMA GEMV
+    would split K over launches)."""
+    n, k = 320, 12288
+    w, wf = make(kind, n, k, seed=rows + 70)
+    xd, x = xs(rows, k, seed=rows + 1, bf16=False)
     assert err_of(ctx.qlinear(w, xd), x, wf) <= tol(kind)
 
 
@@ -244,7 +255,7 @@ def test_zero_point_rows(ctx, kind, rows):
     assert np.all(np.abs(y[:, :zr]) <= bound)
     # the prefill GEMM (GGUF encodings at 200 rows) and the MFMA GEMV (5..16 rows)
     # multiply exact zeros
-    exact = (kind in oracle.GGUF_TYPES and rows >= 48) or (kind == MLX and rows >= 17) or \
+    exact = (kind in oracle.GGUF_TYPES and rows >= 33) or (kind == MLX and rows >= 17) or \
         (rows >= 5 and rows <= 16 and kind in (oracle.Q4_0, oracle.Q6_K, MLX))
     if exact:
         assert not np.any(y[:, :zr]), np.abs(y[:, :zr]).max()

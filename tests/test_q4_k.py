@@ -252,6 +252,47 @@ def test_gemv_mfma_large_offsets(ctx):
     assert oracle.normalized_error(y, y64, absdot) <= TOL
 
 
+# ---------------------------------------------------------------- prefill GEMM (33+ rows; 17+ for K > 8192)
+# Staged f16 activations (one rounding each after a power-of-two row scaling)
+# times weights decoded to f16 as RNE_f16(q·RNE_f16(d·sc) - RNE_f16(dmin·m)):
+# per output at most 2^-10·Σ|w||x| + 2^-11·Σ(|q·d·sc| + |dmin·m|)|x| plus f32
+# accumulation, and |q·d·sc| <= |w| + |dmin·m|.
+GEMM_CASES = [  # (rows, n, k, x/y bf16, base offset); 33+ rows, or 17+ with K > 8192
+    (20, 512, 12288, False, 0), (33, 256, 1024, False, 0), (64, 1000, 2048, False, 4), (77, 3072, 1024, True, 0), (200, 1024, 3072, False, 0),
+    (512, 3072, 1024, True, 4), (512, 1024, 4096, False, 0)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,n,k,bf16,off", GEMM_CASES)
+def test_prefill_gemm(ctx, rows, n, k, bf16, off):
+    import torch
+    w, data = weight(n, k, seed=rows + n + k, off=off)
+    xt = torch.from_numpy(oracle.randn(rows * k, seed=rows + 9).reshape(rows, k))
+    if bf16:
+        xt = xt.to(torch.bfloat16)
+    y = ctx.qlinear(w, xt.cuda(), y_dtype=torch.bfloat16 if bf16 else torch.float32).float().cpu().numpy()
+    x = xt.float().numpy()
+    y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(Q4K, data, n, k))
+    absb = np.abs(x.astype(np.float64)) @ offsets_of(data, n, k).astype(np.float64).T
+    bound = 2.0 ** -10 + 2.0 ** -11 * (1.0 + 2.0 * absb / absdot) + 2e-5
+    if bf16:
+        bound = bound + 2.0 ** -9 * np.abs(y64) / absdot
+    err = np.abs(y - y64) / absdot
+    assert np.all(err <= bound), (err / bound).max()
+    assert oracle.normalized_error(y, y64, absdot) <= TOL
+
+
+@pytest.mark.gpu
+def test_prefill_gemm_multi(ctx):
+    rows, k = 96, 2048
+    ws = [weight(n, k, seed=n) for n in (2048, 512, 512)]
+    x = oracle.randn(rows * k, seed=3).reshape(rows, k)
+    ys = ctx.qlinear_multi([w for w, _ in ws], dev(x))
+    for (w, data), y in zip(ws, ys):
+        y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(Q4K, data, w.rows, k))
+        assert oracle.normalized_error(y.cpu().numpy(), y64, absdot) <= 2.0 ** -10 + 2.0 ** -10 + 2e-5
+
+
 @pytest.mark.gpu
 def test_deterministic(ctx):
     w, _ = weight(4096, 4096, seed=1)
