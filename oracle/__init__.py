@@ -20,12 +20,14 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
 
 Q4_0, Q4_1, Q8_0, Q6_K = 2, 3, 8, 14
-Q4_K = 12  # GGML's Q4_K: the reference declares its schema only (gguf_block.rs:183-316)
+# GGML's K-quants and IQ4_XS: the reference declares their schemas only (gguf_block.rs:183-316)
+Q4_K, Q5_K, IQ4_XS = 12, 13, 23
 GGUF_TYPES = (Q4_0, Q4_1, Q8_0, Q6_K)
 # (weights per block, bytes per block): gguf_codegen.rs:23-38
-BLOCK = {Q4_0: (32, 18), Q4_1: (32, 20), Q8_0: (32, 34), Q6_K: (256, 210), Q4_K: (256, 144)}
+BLOCK = {Q4_0: (32, 18), Q4_1: (32, 20), Q8_0: (32, 34), Q6_K: (256, 210), Q4_K: (256, 144), Q5_K: (256, 176),
+         IQ4_XS: (256, 136)}
 D_F32, D_F16, D_BF16 = 0, 1, 2
-NAMES = {Q4_0: "q4_0", Q4_1: "q4_1", Q8_0: "q8_0", Q6_K: "q6_k", Q4_K: "q4_k"}
+NAMES = {Q4_0: "q4_0", Q4_1: "q4_1", Q8_0: "q8_0", Q6_K: "q6_k", Q4_K: "q4_k", Q5_K: "q5_k", IQ4_XS: "iq4_xs"}
 
 _lib = None
 

@@ -2,7 +2,7 @@
  * CPU oracle for the quantized weight-matmul path — TEST INFRASTRUCTURE ONLY.
  *
  * This file restates, in plain C, the arithmetic the reference (goniz/dyninfer)
- * defines for GGUF Q4_0 / Q4_1 / Q8_0 / Q6_K (and Q4_K) blocks and MLX affine-U4 groups,
+ * defines for GGUF Q4_0 / Q4_1 / Q8_0 / Q6_K (and Q4_K / Q5_K / IQ4_XS) blocks and MLX affine-U4 groups,
  * plus the reference's deterministic fixture helpers (LCG fill, packers).
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
  * it, and only as the checker (or the timed CPU baseline).  The product path
@@ -21,7 +21,7 @@
 #include <omp.h>
 
 /* GGML type codes, crates/dyninfer-checkpoint-gguf/src/types.rs:10-43. */
-enum { T_Q4_0 = 2, T_Q4_1 = 3, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+enum { T_Q4_0 = 2, T_Q4_1 = 3, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
 /* Scale / activation dtypes used by this oracle. */
 enum { D_F32 = 0, D_F16 = 1, D_BF16 = 2 };
 
@@ -309,12 +309,71 @@ static void dq_q4_k(const uint8_t* blk, float* out) {
     }
 }
 
+/* Q5_K (GGUF type 13; schema only in the reference, gguf_block.rs:183-316
+ * "q5_k" 256 weights / 176 bytes [scale_min_f16 4, scales_and_mins_u6 12,
+ * high_bits 32, quants_u4 128], convention.rs:211,241).  GGML block_q5_K:
+ * d, dmin, scales[12] as Q4_K, qh[32] = bytes 16..48, qs[128] = 48..176.
+ * Weights 64i + l and 64i + 32 + l take the low and high nibbles of
+ * qs[32i + l] plus bit 2i and bit 2i + 1 of qh[l] as their fifth bit
+ * (GGML dequantize_row_q5_K): q = nibble + 16*bit, 0..31, and
+ *   w = (d * sc_j) * q - (dmin * m_j)
+ * d * sc (17 bits) times q (5 bits) is exact in f32: one rounding, at the
+ * subtraction. */
+static void dq_q5_k(const uint8_t* blk, float* out) {
+    const float d = load_f16(blk), dmin = load_f16(blk + 2);
+    const uint8_t* qh = blk + 16;
+    const uint8_t* qs = blk + 48;
+    for (int i = 0; i < 4; i++) {
+        int sc0, m0, sc1, m1;
+        q4_k_scale_min(blk + 4, 2 * i, &sc0, &m0);
+        q4_k_scale_min(blk + 4, 2 * i + 1, &sc1, &m1);
+        volatile float d0 = d * (float)sc0, o0 = dmin * (float)m0, d1 = d * (float)sc1, o1 = dmin * (float)m1;
+        for (int l = 0; l < 32; l++) {
+            const int q0 = (qs[32 * i + l] & 15) | (((qh[l] >> (2 * i)) & 1) << 4);
+            const int q1 = (qs[32 * i + l] >> 4) | (((qh[l] >> (2 * i + 1)) & 1) << 4);
+            volatile float a = d0 * (float)q0, b = d1 * (float)q1;
+            out[64 * i + l] = a - o0;
+            out[64 * i + 32 + l] = b - o1;
+        }
+    }
+}
+
+/* IQ4_XS (GGUF type 23; schema only in the reference, gguf_block.rs:183-316
+ * "iq4_xs" 256 weights / 136 bytes [scale_f16 2, scales_high_u16 2,
+ * scales_low_u8 4, nonlinear_quants_u4 128], convention.rs:221,267).  GGML
+ * block_iq4_xs: d = f16 bytes 0..2, scales_h = u16 bytes 2..4, scales_l[4] =
+ * bytes 4..8, qs[128] = bytes 8..136.  Sub-block ib (32 weights) has the
+ * 6-bit scale ls = nibble (ib & 1) of scales_l[ib / 2] | bits 2ib..2ib+1 of
+ * scales_h << 4; its weights 32ib + j and 32ib + 16 + j (j < 16) are the low
+ * and high nibbles of qs[16ib + j], looked up in GGML's kvalues_iq4nl
+ * codebook (a constant of the format) and scaled (dequantize_row_iq4_xs):
+ *   w = (d * (ls - 32)) * kvalues[q]
+ * d * (ls - 32) (17 bits) times an entry (7 bits) is exact in f32. */
+static const int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+static void dq_iq4_xs(const uint8_t* blk, float* out) {
+    const float d = load_f16(blk);
+    const unsigned sh = (unsigned)blk[2] | ((unsigned)blk[3] << 8);
+    const uint8_t* sl = blk + 4;
+    const uint8_t* qs = blk + 8;
+    for (int ib = 0; ib < 8; ib++) {
+        const int ls = ((sl[ib / 2] >> (4 * (ib % 2))) & 15) | (int)(((sh >> (2 * ib)) & 3) << 4);
+        volatile float dl = d * (float)(ls - 32);
+        for (int j = 0; j < 16; j++) {
+            out[32 * ib + j] = dl * (float)kIq4nl[qs[16 * ib + j] & 15];
+            out[32 * ib + 16 + j] = dl * (float)kIq4nl[qs[16 * ib + j] >> 4];
+        }
+    }
+}
+
 static int block_geom(int type, int* bw, int* bb) {
     switch (type) {
     case T_Q4_0: *bw = 32; *bb = 18; return 0;
     case T_Q4_1: *bw = 32; *bb = 20; return 0;
     case T_Q8_0: *bw = 32; *bb = 34; return 0;
     case T_Q4_K: *bw = 256; *bb = 144; return 0;
+    case T_Q5_K: *bw = 256; *bb = 176; return 0;
+    case T_IQ4_XS: *bw = 256; *bb = 136; return 0;
     case T_Q6_K: *bw = 256; *bb = 210; return 0;
     default: return -1;
     }
@@ -331,6 +390,8 @@ static void dq_block(int type, const uint8_t* blk, float* out) {
     case T_Q4_1: dq_q4_1(blk, out); break;
     case T_Q8_0: dq_q8_0(blk, out); break;
     case T_Q4_K: dq_q4_k(blk, out); break;
+    case T_Q5_K: dq_q5_k(blk, out); break;
+    case T_IQ4_XS: dq_iq4_xs(blk, out); break;
     case T_Q6_K: dq_q6_k(blk, out); break;
     }
 }
@@ -469,7 +530,9 @@ void oracle_randn_f32(float* out, uint64_t n, uint64_t seed, float scale) {
  *   Q4_1: as Q4_0 plus m = f16(N(0,1)*0.01)
  *   Q8_0: d as Q4_0, int8 codes uniform -127..127
  *   Q6_K: d as Q4_0, 16 int8 sub-scales uniform -32..31, 6-bit codes uniform 0..63
- *   Q4_K: d as Q4_0, dmin = f16(|N(0,1)|*0.005), the 12 scale bytes and the codes uniform */
+ *   Q4_K: d as Q4_0, dmin = f16(|N(0,1)|*0.005), the 12 scale bytes and the codes uniform
+ *   Q5_K: as Q4_K, the high bits uniform
+ *   IQ4_XS: d = f16(|N(0,1)|*0.0005), the scale bits and the codes uniform */
 int oracle_synth_gguf(int type, uint64_t rows, uint64_t cols, uint64_t seed, uint8_t* out) {
     int bw, bb;
     if (block_geom(type, &bw, &bb) || cols % (uint64_t)bw) return -1;
@@ -498,6 +561,17 @@ int oracle_synth_gguf(int type, uint64_t rows, uint64_t cols, uint64_t seed, uin
             store_f16(o + 2, fabsf(normal(&s)) * 0.005f);
             for (int i = 0; i < 12; i++) o[4 + i] = (uint8_t)(splitmix64(&s) & 0xFF);
             for (int i = 0; i < 128; i++) o[16 + i] = (uint8_t)(splitmix64(&s) & 0xFF);
+            break;
+        case T_Q5_K:
+            /* as Q4_K, with the high bits uniform */
+            store_f16(o, d);
+            store_f16(o + 2, fabsf(normal(&s)) * 0.005f);
+            for (int i = 0; i < 172; i++) o[4 + i] = (uint8_t)(splitmix64(&s) & 0xFF);
+            break;
+        case T_IQ4_XS:
+            /* d = f16(|N(0,1)|*0.0005) (codebook entries reach 127); scale bits and codes uniform */
+            store_f16(o, fabsf(normal(&s)) * 0.0005f);
+            for (int i = 0; i < 134; i++) o[2 + i] = (uint8_t)(splitmix64(&s) & 0xFF);
             break;
         case T_Q6_K: {
             /* draw each 6-bit code, then place its 4+2 bits per the layout */

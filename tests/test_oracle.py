@@ -13,7 +13,9 @@ independent source —
   * GGML's Q4_K scale/min packer (quantize_row_q4_K's 12-byte packing, the
     inverse of the decoder's unpacking) and the closed form
     f32(d*sc*q - dmin*m) with one rounding, on blocks built from chosen
-    scales, mins and codes;
+    scales, mins and codes; Q5_K likewise with the high-bit packer of
+    quantize_row_q5_K; IQ4_XS from the scale packer of quantize_row_iq4_xs and
+    the codebook's closed form f32(d*(ls-32)*kvalue);
   * a numpy vectorised MLX decoder (LSB-first nibbles) and numpy f64 matmul.
 A planted mistake (swapped nibble halves) is shown to fail the known answer.
 """
@@ -329,6 +331,114 @@ def test_q4_k_planted_scale_min_swap_fails():
     assert np.array_equal(got, (np.float64(np.float16(0.01)) * sc[j] * q - np.float64(np.float16(0.005)) * m[j]).astype(np.float32))
 
 
+def q5_k_block(d, dmin, sc, m, q) -> np.ndarray:
+    """A Q5_K block from its fields, packed as GGML's quantize_row_q5_K does:
+    code L of weight 64i + j (j < 32) and 64i + 32 + j go to the low and high
+    nibbles of qs[32i + j], their bit 4 to bits 2i and 2i + 1 of qh[j]."""
+    blk = np.zeros(176, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    blk[2:4] = np.frombuffer(np.float16(dmin).tobytes(), np.uint8)
+    blk[4:16] = pack_q4_k_scales(sc, m)
+    q = np.asarray(q, np.int64)
+    qh = np.zeros(32, np.int64)
+    ql = np.zeros(128, np.int64)
+    m1, m2 = 1, 2
+    for n in range(0, 256, 64):
+        for j in range(32):
+            l1, l2 = q[n + j], q[n + j + 32]
+            if l1 > 15:
+                l1 -= 16
+                qh[j] |= m1
+            if l2 > 15:
+                l2 -= 16
+                qh[j] |= m2
+            ql[n // 2 + j] = l1 | (l2 << 4)
+        m1 <<= 2
+        m2 <<= 2
+    blk[16:48] = qh
+    blk[48:176] = ql
+    return blk
+
+
+def test_q5_k_closed_form_from_chosen_fields():
+    rng = np.random.default_rng(15)
+    blocks, want = [], []
+    for b in range(20):
+        d = np.float16(rng.uniform(1e-4, 0.05))
+        dmin = np.float16(rng.uniform(0, 0.02)) if b % 6 else np.float16(0)
+        sc, m = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+        if b == 0:
+            sc[:], m[:] = 63, 63
+        q = rng.integers(0, 32, 256)
+        if b == 1:
+            q[:] = 31  # every high bit set
+        blocks.append(q5_k_block(d, dmin, sc, m, q))
+        j = np.arange(256) // 32
+        want.append((float(d) * sc[j].astype(np.float64) * q - float(dmin) * m[j].astype(np.float64)).astype(np.float32))
+    got = oracle.dequant_gguf(oracle.Q5_K, np.concatenate(blocks), 20, 256)
+    assert np.array_equal(got.view(np.uint32), np.stack(want).view(np.uint32))
+
+
+def test_q5_k_known_answer_block():
+    # q = index mod 32: weight 64i + l has bit 4 set for l >= 16 (and its high half for 32 + l >= 48)
+    sc, m = np.arange(1, 9), np.arange(8)
+    q = np.arange(256) % 32
+    blk = q5_k_block(1.0, 0.5, sc, m, q)
+    w = oracle.dequant_gguf(oracle.Q5_K, blk, 1, 256).ravel()
+    j = np.arange(256) // 32
+    assert np.array_equal(w, (1.0 * (j + 1) * q - 0.5 * j).astype(np.float32))
+    # qh[l] for l >= 16 has every bit set (both halves of every step), else none
+    assert list(blk[16:48]) == [0] * 16 + [255] * 16
+
+
+KVALUES_IQ4NL = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.int64)
+
+
+def iq4_xs_block(d, ls, q) -> np.ndarray:
+    """An IQ4_XS block from d, the eight 6-bit scales ls and 256 codebook
+    indices, packed as GGML's quantize_row_iq4_xs does: scales_l[ib/2] gets
+    the low nibble of ls at 4*(ib%2), scales_h its high two bits at 2*ib; the
+    sub-block's codes j and 16 + j share qs[16ib + j]."""
+    blk = np.zeros(136, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    sh, sl = 0, np.zeros(4, np.int64)
+    for ib in range(8):
+        sl[ib // 2] |= (int(ls[ib]) & 15) << (4 * (ib % 2))
+        sh |= (int(ls[ib]) >> 4) << (2 * ib)
+    blk[2:4] = [sh & 0xFF, sh >> 8]
+    blk[4:8] = sl
+    q = np.asarray(q, np.int64).reshape(8, 2, 16)
+    blk[8:136] = (q[:, 0, :] | (q[:, 1, :] << 4)).ravel()
+    return blk
+
+
+def test_iq4_xs_closed_form_from_chosen_fields():
+    rng = np.random.default_rng(23)
+    blocks, want = [], []
+    for b in range(20):
+        d = np.float16(rng.uniform(1e-5, 0.01))
+        ls = rng.integers(0, 64, 8)
+        if b == 0:
+            ls[:] = [0, 63, 32, 31, 1, 62, 33, 16]
+        q = rng.integers(0, 16, 256)
+        blocks.append(iq4_xs_block(d, ls, q))
+        ib = np.arange(256) // 32
+        want.append((float(d) * (ls[ib] - 32).astype(np.float64) * KVALUES_IQ4NL[q]).astype(np.float32))
+    got = oracle.dequant_gguf(oracle.IQ4_XS, np.concatenate(blocks), 20, 256)
+    assert np.array_equal(got.view(np.uint32), np.stack(want).view(np.uint32))
+
+
+def test_iq4_xs_known_answer_block():
+    # ls = 33 everywhere (scale d), index = weight mod 16: each 16-weight run spans the codebook
+    q = np.arange(256) % 16
+    blk = iq4_xs_block(0.25, np.full(8, 33), q)
+    assert list(blk[2:8]) == [0xAA, 0xAA, 0x11, 0x11, 0x11, 0x11]  # ls = 0b10_0001 per sub-block
+    w = oracle.dequant_gguf(oracle.IQ4_XS, blk, 1, 256).ravel()
+    assert np.array_equal(w, (0.25 * KVALUES_IQ4NL[q]).astype(np.float32))
+    # the codebook (typed here and in the oracle independently): strictly increasing, -127..113
+    assert np.all(np.diff(KVALUES_IQ4NL) > 0) and KVALUES_IQ4NL[0] == -127 and KVALUES_IQ4NL[-1] == 113
+
+
 def test_mlx_u4_numpy_decoder():
     rows, cols, g = 5, 256, 64
     for sdt in (oracle.D_BF16, oracle.D_F16, oracle.D_F32):
@@ -365,7 +475,7 @@ def test_linear_f32_sequential_within_f32_bound():
     assert np.all(np.abs(y - y64) <= 1000 * 2.0 ** -24 * a)
 
 
-@pytest.mark.parametrize("gtype", oracle.GGUF_TYPES + (oracle.Q4_K,), ids=oracle.NAMES.get)
+@pytest.mark.parametrize("gtype", oracle.GGUF_TYPES + (oracle.Q4_K, oracle.Q5_K, oracle.IQ4_XS), ids=oracle.NAMES.get)
 def test_cpu_baseline_contraction_within_tolerance(gtype):
     bw, _ = oracle.BLOCK[gtype]
     n, k = 40, 4 * bw * (2 if bw == 32 else 1)
