@@ -8,7 +8,8 @@
 //   Q6_K  (f32(q6 - 32) * f32(sc)) * f32(d)  gguf_codegen.rs:474-526
 //   MLX   f32(q) * s + b                     mlx_affine.rs:593-598
 //   Q4_K  (f32(d) * f32(sc)) * f32(q) - f32(dmin) * f32(m)   GGML dequantize_row_q4_K
-//         (the reference declares Q4_K's schema only, gguf_block.rs:183-316)
+//   Q5_K  the same with 5-bit q                               GGML dequantize_row_q5_K
+//         (the reference declares the K-quants' schemas only, gguf_block.rs:183-316)
 // Products that are exact (all but MLX with f32 scales) make fma contraction
 // harmless; the MLX f32-scale product is rounded explicitly before the add.
 #include "device_common.hpp"
@@ -51,16 +52,21 @@ __global__ __launch_bounds__(256) void gguf_dequant_kernel(const uint8_t* __rest
         const uint8_t* blk = w + t * 34;
         const float d = f16_bits_to_f32(load_u16le(blk));
         for (int l = 0; l < 32; l++) o[l] = (float)(int8_t)load_u8(blk + 2 + l) * d;
-    } else if constexpr (ENC == ENC_Q4_K) {  // slice t = sub-block t & 7 of super-block t/8
-        const uint8_t* blk = w + (t >> 3) * 144;
+    } else if constexpr (ENC == ENC_Q4_K || ENC == ENC_Q5_K) {  // slice t = sub-block t & 7 of super-block t/8
+        constexpr uint32_t BB = ENC == ENC_Q4_K ? 144u : 176u, QS = ENC == ENC_Q4_K ? 16u : 48u;
+        const uint8_t* blk = w + (t >> 3) * BB;
         const uint32_t j = (uint32_t)(t & 7u);
         const float d = f16_bits_to_f32(load_u16le(blk)), dmin = f16_bits_to_f32(load_u16le(blk + 2));
         uint32_t sc, m;
         q4k_scale_min(blk + 4, j, sc, m);
         const float ds = d * (float)sc, dm = dmin * (float)m;
-        const uint8_t* q = blk + 16 + 32 * (j >> 1);
+        const uint8_t* q = blk + QS + 32 * (j >> 1);
         const uint32_t sh = 4u * (j & 1u);  // odd sub-blocks are the high nibbles
-        for (int l = 0; l < 32; l++) o[l] = ds * (float)((load_u8(q + l) >> sh) & 15u) - dm;
+        for (int l = 0; l < 32; l++) {
+            uint32_t c = (load_u8(q + l) >> sh) & 15u;
+            if constexpr (ENC == ENC_Q5_K) c |= ((load_u8(blk + 16 + l) >> j) & 1u) << 4;  // bit j of qh[l]
+            o[l] = ds * (float)c - dm;
+        }
     } else {  // Q6_K: slice t = (super-block t/8, n, h, p) of 32 weights
         const uint64_t sb = t >> 3;
         const uint32_t r = (uint32_t)(t & 7u);
@@ -123,6 +129,7 @@ hipError_t dequant_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, con
     case ENC_Q8_0: hipLaunchKernelGGL(gguf_dequant_kernel<ENC_Q8_0>, grid, block, 0, stream, w, nslices, out); break;
     case ENC_Q6_K: hipLaunchKernelGGL(gguf_dequant_kernel<ENC_Q6_K>, grid, block, 0, stream, w, nslices, out); break;
     case ENC_Q4_K: hipLaunchKernelGGL(gguf_dequant_kernel<ENC_Q4_K>, grid, block, 0, stream, w, nslices, out); break;
+    case ENC_Q5_K: hipLaunchKernelGGL(gguf_dequant_kernel<ENC_Q5_K>, grid, block, 0, stream, w, nslices, out); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

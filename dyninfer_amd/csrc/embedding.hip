@@ -48,16 +48,23 @@ __device__ __forceinline__ float4 gguf_four(const uint8_t* __restrict__ row, uin
         const float d = f16_bits_to_f32(ld16(blk));
         const uint8_t* q = blk + 2 + (k & 31u);
         for (int i = 0; i < 4; i++) v[i] = (float)(int8_t)ld8(q + i) * d;
-    } else if constexpr (ENC == ENC_Q4_K) {  // idx = 64i + 32h + l: nibble h of qs[32i + l], sub-block 2i + h
-        const uint8_t* blk = row + (size_t)(k >> 8) * 144u;
+    } else if constexpr (ENC == ENC_Q4_K || ENC == ENC_Q5_K) {
+        // idx = 64i + 32h + l: nibble h of qs[32i + l] (Q5_K: | bit 2i + h of qh[l] << 4), sub-block 2i + h
+        constexpr uint32_t BB = ENC == ENC_Q4_K ? 144u : 176u, QS = ENC == ENC_Q4_K ? 16u : 48u;
+        const uint8_t* blk = row + (size_t)(k >> 8) * BB;
         const uint32_t idx = k & 255u, jsub = idx >> 5;
         const float d = f16_bits_to_f32(ld16(blk)), dmin = f16_bits_to_f32(ld16(blk + 2));
         uint32_t sc, m;
         q4k_scale_min(blk + 4, jsub, sc, m);
         const float ds = d * (float)sc, dm = dmin * (float)m;
-        const uint8_t* q = blk + 16 + 32 * (jsub >> 1) + (idx & 31u);
+        const uint32_t l0 = idx & 31u;
+        const uint8_t* q = blk + QS + 32 * (jsub >> 1) + l0;
         const uint32_t sh = 4u * (jsub & 1u);
-        for (int i = 0; i < 4; i++) v[i] = ds * (float)((ld8(q + i) >> sh) & 15u) - dm;
+        for (int i = 0; i < 4; i++) {
+            uint32_t c = (ld8(q + i) >> sh) & 15u;
+            if constexpr (ENC == ENC_Q5_K) c |= ((ld8(blk + 16 + l0 + i) >> jsub) & 1u) << 4;
+            v[i] = ds * (float)c - dm;
+        }
     } else {  // Q6_K: idx = n*128 + h*64 + p*32 + s*16 + l (gguf_codegen.rs:499-503)
         const uint8_t* blk = row + (size_t)(k >> 8) * 210u;
         const uint32_t idx = k & 255u;
@@ -158,6 +165,10 @@ hipError_t gather_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, cons
         break;
     case ENC_Q4_K:
         hipLaunchKernelGGL(gguf_gather_kernel<ENC_Q4_K>, grid, block, 0, stream, w, (uint64_t)(K / 256) * 144u, vocab,
+                           K, per_row, ids, out);
+        break;
+    case ENC_Q5_K:
+        hipLaunchKernelGGL(gguf_gather_kernel<ENC_Q5_K>, grid, block, 0, stream, w, (uint64_t)(K / 256) * 176u, vocab,
                            K, per_row, ids, out);
         break;
     default: return hipErrorInvalidValue;

@@ -24,6 +24,7 @@
 //   Q8_0  w = q·d                code q+128 (xor 0x80), off 128
 //   Q6_K  w = (q-32)·sc·d        6-bit code q,    off 32, per 16-weight group
 //   Q4_K  w = q·(d·sc) - dmin·m  code q,          off 0, - dmin·m·Σx, per 32-weight group
+//   Q5_K  as Q4_K with 5-bit codes (a fifth bit from qh)
 //   MLX   w = q·s + b            code q,          off 0, + b·Σx
 //
 // Layout contract with the activation staging (gemv_kernels.hpp): for code
@@ -394,6 +395,73 @@ struct EncQ4K {
     }
 };
 
+// ------------------------------------------------------------------ GGUF Q5_K
+// 176-byte super-block of 256 (GGML block_q5_K; the reference's schema
+// gguf_block.rs:183-316 "q5_k", convention.rs:211,241: scale_min_f16 4 B,
+// scales_and_mins_u6 12 B, high_bits 32 B, quants_u4 128 B): Q4_K's header,
+// qh = bytes 16..48, qs = 48..176.  Weight 64i + 32h + l (l < 32) has the 5-bit
+// code nibble h of qs[32i + l] | bit 2i + h of qh[l] << 4.  Chunks, scale groups
+// and activation layout as Q4_K; code dword t pairs its qs dword with qh
+// dword t (bytes 4t..4t+3, shifted down by 2i once per chunk), the fifth bit
+// moved under the nibble: bit 4 for the low nibbles, bit 8 (x16) for the high.
+struct EncQ5K {
+    static constexpr uint32_t ENC = ENC_Q5_K;
+    static constexpr int CW = 64, QK = 256, NT = 8, PPT = 4, NG = 2, BB = 176;
+    static constexpr bool AFFINE = true;
+    static constexpr int NRUN = 2, RUNLEN = 32, RUNSTRIDE = 32;
+    __device__ __forceinline__ static uint32_t xbase(uint32_t u) { return 64u * u; }
+    static constexpr float coef(bool) { return 1024.0f; }
+    static constexpr int xoff(int t, int h, int e) { return EncQ4K::xoff(t, h, e); }
+    static constexpr bool dv(int t, int h) { return EncQ4K::dv(t, h); }
+    static constexpr int grp(int t, int h) { return EncQ4K::grp(t, h); }
+    static constexpr int TSTRIDE = 4, NXR = 2;
+    static constexpr int xrun0(int r) { return EncQ4K::xrun0(r); }
+    struct Raw { uint32_t h[4]; uint32_t hb[NT]; uint32_t q[NT]; };
+    struct Chunk { uint32_t q[NT], hb[NT]; float ds[NG], dm[NG]; };
+    __device__ __forceinline__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u) {
+        const uint32_t* sb = reinterpret_cast<const uint32_t*>(w + (rowoff + (u >> 2) * (uint32_t)BB));
+        Raw r;
+        load_dwords<4>(sb, r.h);
+        load_dwords<NT>(sb + 4u, r.hb);
+        load_dwords<NT>(sb + 12u + 8u * (u & 3u), r.q);
+        return r;
+    }
+    __device__ __forceinline__ static Chunk unpack(const Raw& r, uint32_t u) {
+        Chunk c;
+        const uint32_t i = u & 3u;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            c.q[t] = r.q[t];
+            c.hb[t] = r.hb[t] >> (2u * i);  // bit 0 of each byte: low nibbles' fifth bit, bit 1: high
+        }
+        const float d = f16_bits_to_f32(r.h[0]), dmin = f16_bits_to_f32(r.h[0] >> 16);
+        uint32_t sc[NG], mn[NG];
+        q4k_scale_min_pair(r.h[1], r.h[2], r.h[3], i, sc, mn);
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            c.ds[g] = d * (float)sc[g];
+            c.dm[g] = -(dmin * (float)mn[g]);
+        }
+        return c;
+    }
+    __device__ __forceinline__ static void pairs(const Chunk& c, int t, uint32_t (&p)[PPT]) {
+        const uint32_t Q = c.q[t], H = c.hb[t], Q8 = Q >> 8, H8 = H >> 8;
+        p[0] = and_or(Q, 0x000F000Fu, and_or(H << 4, 0x00100010u, kMagic));   // (4t, 4t+2)
+        p[1] = and_or(Q, 0x00F000F0u, and_or(H << 7, 0x01000100u, kMagic));   // (32+4t, 34+4t) x16
+        p[2] = and_or(Q8, 0x000F000Fu, and_or(H8 << 4, 0x00100010u, kMagic)); // (4t+1, 4t+3)
+        p[3] = and_or(Q8, 0x00F000F0u, and_or(H8 << 7, 0x01000100u, kMagic)); // (33+4t, 35+4t) x16
+    }
+    __device__ __forceinline__ static float gscale(const Chunk& c, int g) { return c.ds[g]; }
+    __device__ __forceinline__ static float goffset(const Chunk& c, int g) { return c.dm[g]; }
+    __device__ __forceinline__ static void zero_if(Chunk& c, bool z) {
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            c.ds[g] = z ? 0.0f : c.ds[g];
+            c.dm[g] = z ? 0.0f : c.dm[g];
+        }
+    }
+};
+
 // ------------------------------------------------------------------ MLX affine U4
 // One chunk = 32 weights = 4 packed u32 words (weight i of a word = bits
 // 4i..4i+3, fixture.rs:307-311) sharing one scale and bias (group size is a
@@ -469,7 +537,7 @@ constexpr bool xruns_ok() {
     return 4 * E::NXR == 2 * E::PPT;
 }
 static_assert(xruns_ok<EncQ40>() && xruns_ok<EncQ41>() && xruns_ok<EncQ80>() && xruns_ok<EncQ6K>() &&
-                  xruns_ok<EncQ4K>() && xruns_ok<EncMlxU4>(),
+                  xruns_ok<EncQ4K>() && xruns_ok<EncQ5K>() && xruns_ok<EncMlxU4>(),
               "activation runs disagree with xoff()");
 
 }  // namespace dmx

@@ -1,5 +1,5 @@
-// Prefill GEMM on gfx950 MFMA for the GGUF encodings Q4_0, Q4_1, Q8_0, Q6_K
-// and Q4_K and for MLX affine U4: Y[M, N] = X[M, K] · Wᵀ with f32 accumulation.
+// Prefill GEMM on gfx950 MFMA for the GGUF encodings Q4_0, Q4_1, Q8_0, Q6_K,
+// Q4_K and Q5_K and for MLX affine U4: Y[M, N] = X[M, K] · Wᵀ with f32 accumulation.
 //
 // Reference semantics: the same `emit_linear` contraction as decode
 // (gguf_codegen.rs:268-314, dequantisations :412-472 Q4_0, :382-410 Q8_0,
@@ -508,15 +508,21 @@ struct WinMlx {
 // bytes) and the step's 32 code bytes, three 16-byte pieces (super-blocks
 // are 4-byte aligned: 144 = 36 dwords).  w = RNE_f16(q·RNE_f16(d·sc) -
 // RNE_f16(dmin·m)) by one packed fma (d·sc and dmin·m exact in f32).
-struct WinQ4K {
-    static constexpr uint32_t NP = 3, kCopies = NP;
+// Q5_K (block_q5_K, 176 bytes): the window adds qh (bytes 16..48, two more
+// pieces, kept before the codes); the fifth bit of weight 64i + 32h + l is bit
+// 2i + h of qh[l], moved under the nibble.
+template <bool Q5>
+struct WinQK {
+    static constexpr uint32_t NP = Q5 ? 5u : 3u, kCopies = NP;
     static constexpr uint32_t kPitch = 16u * NP;
     static constexpr uint32_t kBytes = 64u * kPitch;
-    static constexpr uint32_t kDw = 12;  // d|dmin, three scale dwords, 8 code dwords
-    static constexpr uint32_t kValuPerStep = 14;
+    static constexpr uint32_t QS = Q5 ? 12u : 4u;          // raw dword of the codes
+    static constexpr uint32_t SB = Q5 ? 176u : 144u;       // super-block bytes
+    static constexpr uint32_t kDw = QS + 8u;               // d|dmin, three scale dwords, [8 qh dwords,] 8 code dwords
+    static constexpr uint32_t kValuPerStep = Q5 ? 24 : 14;
     struct Scale {
         h2 ds, ndm, off;
-        uint32_t mask, magic;
+        uint32_t mask, magic, hsh, sl, mh;
     };
     uintptr_t rb[NP];  // row of each copy lane
     uint32_t pp[NP];   // piece of each copy lane
@@ -537,8 +543,10 @@ struct WinQ4K {
         const uint32_t g = c0 + c, sb = g >> 2, i = g & 3u;
 #pragma unroll
         for (uint32_t q = 0; q < NP; q++) {
-            const uint32_t o = pp[q] == 0u ? 0u : 16u + 32u * i + 16u * (pp[q] - 1u);
-            dma16(reinterpret_cast<const void*>(rb[q] + (uintptr_t)sb * 144u + o), win + 1024u * q);
+            const uint32_t p = pp[q];
+            // pieces: header, [qh, qh,] the step's two code pieces
+            const uint32_t o = p == 0u ? 0u : p + 2u < NP ? 16u * p : 16u * (QS / 4u) + 32u * i + 16u * (p + 2u - NP);
+            dma16(reinterpret_cast<const void*>(rb[q] + (uintptr_t)sb * SB + o), win + 1024u * q);
         }
     }
     __device__ void read(uint32_t, const uint8_t* win, uint32_t* raw) const {
@@ -570,16 +578,29 @@ struct WinQ4K {
         s.off = h2{o, o};
         s.mask = h ? 0x00F000F0u : 0x000F000Fu;
         s.magic = h ? 0x54005400u : 0x64006400u;  // code bits under the exponent of 64 / 1024
+        s.hsh = 2u * ((c0 + c) & 3u) + h;          // Q5_K: the qh bit of this half-step
+        s.sl = h ? 8u : 4u;                        // ... moved to bit 8 (x16) or 4
+        s.mh = h ? 0x01000100u : 0x00100010u;
         return s;
     }
     __device__ h8 step(const uint32_t* r, const Scale& s, int t) const {
-        auto f = [&](uint32_t v) {
-            return as_u(__builtin_elementwise_fma(as_h2(and_or(v, s.mask, s.magic)) + s.off, s.ds, s.ndm));
+        auto f = [&](uint32_t v, uint32_t e) {
+            uint32_t m = s.magic;
+            if constexpr (Q5) m = and_or(e << s.sl, s.mh, m);
+            return as_u(__builtin_elementwise_fma(as_h2(and_or(v, s.mask, m)) + s.off, s.ds, s.ndm));
         };
-        const uint32_t c = r[4 + 2 * t], c2 = r[5 + 2 * t];
-        return as_h8(f(c), f(c >> 8), f(c2), f(c2 >> 8));
+        const uint32_t c = r[QS + 2 * t], c2 = r[QS + 1 + 2 * t];
+        uint32_t e = 0, e2 = 0;
+        if constexpr (Q5) {
+            e = r[4 + 2 * t] >> s.hsh;
+            e2 = r[5 + 2 * t] >> s.hsh;
+        }
+        return as_h8(f(c, e), f(c >> 8, e >> 8), f(c2, e2), f(c2 >> 8, e2 >> 8));
     }
 };
+
+using WinQ4K = WinQK<false>;
+using WinQ5K = WinQK<true>;
 
 template <uint32_t ENC>
 struct WinOf {
@@ -588,6 +609,10 @@ struct WinOf {
 template <>
 struct WinOf<ENC_Q4_K> {
     using type = WinQ4K;
+};
+template <>
+struct WinOf<ENC_Q5_K> {
+    using type = WinQ5K;
 };
 template <>
 struct WinOf<ENC_MLX_U4> {
@@ -899,7 +924,8 @@ uint32_t gemm_layout(uint32_t enc) {
         case ENC_Q4_1: return Blk<ENC_Q4_1>::kLayout;
         case ENC_Q8_0: return Blk<ENC_Q8_0>::kLayout;
         case ENC_Q6_K: return XFRAG_BYTE;  // a lane's 32 codes in order, as Q8_0
-        case ENC_Q4_K: return XFRAG_BYTE;
+        case ENC_Q4_K:
+        case ENC_Q5_K: return XFRAG_BYTE;
         case ENC_MLX_U4: return XFRAG_WORD;
         default: return ~0u;
     }
@@ -907,7 +933,7 @@ uint32_t gemm_layout(uint32_t enc) {
 
 bool gemm_supported(uint32_t enc, uint32_t N, uint32_t K, uint32_t M) {
     return gemm_layout(enc) != ~0u && N > 0 && M > 0 && K >= 64u &&
-           K % (enc == ENC_Q6_K || enc == ENC_Q4_K ? 256u : 64u) == 0;
+           K % (enc == ENC_Q6_K || enc == ENC_Q4_K || enc == ENC_Q5_K ? 256u : 64u) == 0;
 }
 
 hipError_t gemm_launch(const GemmWeight& wt, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs, uint32_t M,
@@ -935,6 +961,7 @@ hipError_t gemm_launch(const GemmWeight& wt, uint32_t N, uint32_t K, const uint1
         case ENC_Q8_0: a.rowbytes = (uint64_t)(K / 32u) * Blk<ENC_Q8_0>::kBytes; break;
         case ENC_Q6_K: a.rowbytes = (uint64_t)(K / 256u) * 210u; break;
         case ENC_Q4_K: a.rowbytes = (uint64_t)(K / 256u) * 144u; break;
+        case ENC_Q5_K: a.rowbytes = (uint64_t)(K / 256u) * 176u; break;
         default: a.rowbytes = (uint64_t)K / 2u; break;  // MLX packed words (scales and biases besides)
     }
     // M-major tile order when the staged activations (2 bytes per element)
@@ -946,6 +973,7 @@ hipError_t gemm_launch(const GemmWeight& wt, uint32_t N, uint32_t K, const uint1
         case ENC_Q8_0: return launch_enc<ENC_Q8_0>(a, st);
         case ENC_Q6_K: return launch_enc<ENC_Q6_K>(a, st);
         case ENC_Q4_K: return launch_enc<ENC_Q4_K>(a, st);
+        case ENC_Q5_K: return launch_enc<ENC_Q5_K>(a, st);
         case ENC_MLX_U4: return launch_enc<ENC_MLX_U4>(a, st);
         default: return hipErrorInvalidValue;
     }

@@ -13,6 +13,7 @@ hipError_t gemv_launch_q4_1(const GemvParams& p, uint32_t B, uint32_t oneshot, b
 hipError_t gemv_launch_q8_0(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
 hipError_t gemv_launch_q6_k(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
 hipError_t gemv_launch_q4_k(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_q5_k(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
 hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
 
 hipError_t cached_occupancy(const void* kernel, size_t lds, int threads, int* per_cu, int* cus) {
@@ -76,7 +77,7 @@ namespace {
 
 struct EncInfo {
     uint32_t chunk_weights;  // weights one lane handles per step
-    bool wide;               // 64-weight chunks (Q6_K, Q4_K): fewer chunks per lane in latency mode
+    bool wide;               // 64-weight chunks (Q6_K, Q4_K, Q5_K): fewer chunks per lane in latency mode
 };
 
 bool enc_info(uint32_t enc, EncInfo& e) {
@@ -86,7 +87,8 @@ bool enc_info(uint32_t enc, EncInfo& e) {
     case ENC_Q8_0:
     case ENC_MLX_U4: e = {32, false}; return true;
     case ENC_Q6_K: e = {64, true}; return true;
-    case ENC_Q4_K: e = {64, true}; return true;
+    case ENC_Q4_K:
+    case ENC_Q5_K: e = {64, true}; return true;
     default: return false;
     }
 }
@@ -98,6 +100,7 @@ hipError_t launch(uint32_t enc, const GemvParams& p, uint32_t B, uint32_t onesho
     case ENC_Q8_0: return gemv_launch_q8_0(p, B, oneshot, xbf16, st);
     case ENC_Q6_K: return gemv_launch_q6_k(p, B, oneshot, xbf16, st);
     case ENC_Q4_K: return gemv_launch_q4_k(p, B, oneshot, xbf16, st);
+    case ENC_Q5_K: return gemv_launch_q5_k(p, B, oneshot, xbf16, st);
     case ENC_MLX_U4: return gemv_launch_mlx_u4(p, B, oneshot, xbf16, st);
     default: return hipErrorInvalidValue;
     }

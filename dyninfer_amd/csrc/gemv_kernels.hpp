@@ -699,7 +699,7 @@ __global__ __launch_bounds__(TH) void mlx_u4_gemv_oneshot_kernel(const GemvParam
 // keep the accumulators in registers (gemv_tiles adds the narrower tiles).
 template <class E, int B>
 constexpr int rows_per_group() {
-    if constexpr (E::ENC == ENC_Q6_K || E::ENC == ENC_Q4_K) return B <= 2 ? 2 : 1;  // 64-weight chunks
+    if constexpr (wide_chunks(E::ENC)) return B <= 2 ? 2 : 1;  // 64-weight chunks
     else return B <= 2 ? 4 : 2;
 }
 
@@ -871,14 +871,14 @@ hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot,
     }
     if (oneshot) {
         // chunks per lane (the host's limits): 1..4 for one activation row
-        // (Q6_K, Q4_K 1..2), 1..2 for 2 rows, 1 for 4
+        // (64-weight chunks 1..2), 1..2 for 2 rows, 1 for 4
 #define DMX_ONESHOT(b, c)                                                                             \
     if (B == b && oneshot == c)                                                                       \
         return launch_oneshot(gguf_gemv_oneshot_kernel<E, c, b, XBF16, 512>, gguf_gemv_oneshot_kernel<E, c, b, XBF16, 256>, \
                               p, lds, st);
         DMX_ONESHOT(1, 1)
         DMX_ONESHOT(1, 2)
-        if constexpr (E::ENC != ENC_Q6_K && E::ENC != ENC_Q4_K) {
+        if constexpr (!wide_chunks(E::ENC)) {
             DMX_ONESHOT(1, 3)
             DMX_ONESHOT(1, 4)
         }

@@ -1,5 +1,5 @@
-// Decode GEMV on MFMA for 3..16 activation rows, GGUF Q4_0, Q6_K and Q4_K and
-// MLX affine U4 (y[b, o] = Σ_k x[b, k]·w[o, k], f32 accumulation;
+// Decode GEMV on MFMA for 3..16 activation rows, GGUF Q4_0, Q6_K, Q4_K and
+// Q5_K and MLX affine U4 (y[b, o] = Σ_k x[b, k]·w[o, k], f32 accumulation;
 // gguf_codegen.rs:268-314 `emit_linear` with the dequantisations of :412-472
 // (Q4_0) and :474-526 (Q6_K), mlx_affine.rs:557-626 `emit_linear_u4`).
 //
@@ -207,11 +207,16 @@ struct MfmaQ6K {
 // 8q, 8q + 1 (exact), A the matching activation sums X/32 of each row
 // (staged with the activations, one f16 rounding), and that product is
 // subtracted times dmin.
-struct MfmaQ4K {
+// Q5_K (block_q5_K, 176 bytes, gguf_block.rs:183-316 "q5_k") decodes the
+// same way with 5-bit codes: the fifth bit, bit 2q + h of qh[l] (window
+// dwords 4..11), moved under the nibble (sc·q <= 1953, still exact).
+template <bool Q5>
+struct MfmaQK {
     static constexpr int KT = 256, NM = 8, PF = 4, TPI = 2;
-    static constexpr uint32_t UNIT = 256, UPT = 1, UB = 144;
+    static constexpr uint32_t UNIT = 256, UPT = 1, UB = Q5 ? 176u : 144u;
     static constexpr uint32_t TB = UB;
-    static constexpr uint32_t NP = 9, WB = 144;
+    static constexpr uint32_t NP = UB / 16u, WB = UB;  // 9 or 11 pieces: odd
+    static constexpr uint32_t QS = Q5 ? 12u : 4u;      // window dword of the codes
     static constexpr bool ROWSCALE = false, MLX = false, PAIR4 = false, BIAS = true;
     static constexpr uint32_t STAGE = 8;
     __device__ static uint32_t goff(uint32_t piece, uint32_t) { return 16u * piece; }
@@ -220,24 +225,34 @@ struct MfmaQ4K {
     // mb = the f16 pair (32·m_2q, 32·m_2q+1); d, dmin zero for a padding task
     __device__ static void decode(const u32a* win, bool ok, uint32_t q, uint4 (&a)[NM], uint32_t& mb, float& d,
                                   float& dmin) {
-        const uint32_t h[4] = {win[0], win[1], win[2], win[3]};
+        const uint32_t h0 = win[0];
         uint32_t sc[2], mn[2];
-        EncQ4K::scale_min(h, q, sc, mn);
-        d = ok ? f16_bits_to_f32(h[0]) : 0.0f;
-        dmin = ok ? f16_bits_to_f32(h[0] >> 16) : 0.0f;
+        q4k_scale_min_pair(win[1], win[2], win[3], q, sc, mn);
+        d = ok ? f16_bits_to_f32(h0) : 0.0f;
+        dmin = ok ? f16_bits_to_f32(h0 >> 16) : 0.0f;
         const _Float16 s0 = (_Float16)sc[0], s1 = (_Float16)sc[1];  // exact: < 64
         const h2 s2lo = {s0, s0}, s2hi = {s1, s1};
         mb = __builtin_bit_cast(uint32_t, h2{(_Float16)(32u * mn[0]), (_Float16)(32u * mn[1])});  // exact: <= 2016
 #pragma unroll
         for (int j = 0; j < NM; j++) {
-            const uint32_t D = win[4u + 8u * q + (uint32_t)j], D8 = D >> 8;
-            a[j] = make_uint4(wq(and_or(D, 0x000F000Fu, 0x64006400u), (_Float16)-1024.0f, s2lo),
-                              wq(and_or(D8, 0x000F000Fu, 0x64006400u), (_Float16)-1024.0f, s2lo),
-                              wq(and_or(D, 0x00F000F0u, 0x54005400u), (_Float16)-64.0f, s2hi),
-                              wq(and_or(D8, 0x00F000F0u, 0x54005400u), (_Float16)-64.0f, s2hi));
+            const uint32_t D = win[QS + 8u * q + (uint32_t)j], D8 = D >> 8;
+            uint32_t ml = 0x64006400u, mh = 0x54005400u, ml8 = ml, mh8 = mh;
+            if constexpr (Q5) {
+                const uint32_t H = win[4u + (uint32_t)j] >> (2u * q), H8 = H >> 8;
+                ml = and_or(H << 4, 0x00100010u, ml);
+                mh = and_or(H << 7, 0x01000100u, mh);
+                ml8 = and_or(H8 << 4, 0x00100010u, ml8);
+                mh8 = and_or(H8 << 7, 0x01000100u, mh8);
+            }
+            a[j] = make_uint4(wq(and_or(D, 0x000F000Fu, ml), (_Float16)-1024.0f, s2lo),
+                              wq(and_or(D8, 0x000F000Fu, ml8), (_Float16)-1024.0f, s2lo),
+                              wq(and_or(D, 0x00F000F0u, mh), (_Float16)-64.0f, s2hi),
+                              wq(and_or(D8, 0x00F000F0u, mh8), (_Float16)-64.0f, s2hi));
         }
     }
 };
+using MfmaQ4K = MfmaQK<false>;
+using MfmaQ5K = MfmaQK<true>;
 
 // MLX affine U4 (mlx_affine.rs:557-626, fixture.rs:307-311): a task is 256
 // weights of a row, 32 packed words (128 bytes, 16-byte aligned rows, so no
@@ -859,8 +874,8 @@ int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16, uint32_t min_tiles) {
 
 bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool y_bf16,
                        uint32_t group) {
-    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K && enc != ENC_Q4_K && enc != ENC_MLX_U4) || batch < 3 || batch > 16 ||
-        K % 256u)
+    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K && enc != ENC_Q4_K && enc != ENC_Q5_K && enc != ENC_MLX_U4) || batch < 3 ||
+        batch > 16 || K % 256u)
         return false;
     if (enc == ENC_MLX_U4 && (group == 0 || group % 32u)) return false;
     uint32_t tiles = 0;
@@ -881,6 +896,7 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     const uint64_t bytes = rows * (enc == ENC_Q4_0   ? K / 32u * 18u
                                    : enc == ENC_Q6_K ? K / 256u * 210u
                                    : enc == ENC_Q4_K ? K / 256u * 144u
+                                   : enc == ENC_Q5_K ? K / 256u * 176u
                                                      : K / 2u);
     if (batch < 5 && tiles < kMfmaSplitTiles) return false;
     if (batch <= max_register_batch(enc) && bytes < (8ull << 20) && tiles < kMfmaSplitTiles) return false;
@@ -888,6 +904,7 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     const int mode = enc == ENC_Q4_0   ? mfma_mode<MfmaQ40>(K, tiles, y_bf16, min_tiles)
                    : enc == ENC_Q6_K   ? mfma_mode<MfmaQ6K>(K, tiles, y_bf16, min_tiles)
                    : enc == ENC_Q4_K   ? mfma_mode<MfmaQ4K>(K, tiles, y_bf16, min_tiles)
+                   : enc == ENC_Q5_K   ? mfma_mode<MfmaQ5K>(K, tiles, y_bf16, min_tiles)
                                        : mfma_mode<MfmaMlxU4>(K, tiles, y_bf16, min_tiles);
     return mode != 0;
 }
@@ -898,6 +915,7 @@ hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, u
     if (enc == ENC_Q4_0) return launch_mfma<MfmaQ40>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     if (enc == ENC_Q6_K) return launch_mfma<MfmaQ6K>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     if (enc == ENC_Q4_K) return launch_mfma<MfmaQ4K>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
+    if (enc == ENC_Q5_K) return launch_mfma<MfmaQ5K>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     if (enc == ENC_MLX_U4) return launch_mfma<MfmaMlxU4>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     return hipErrorInvalidValue;
 }

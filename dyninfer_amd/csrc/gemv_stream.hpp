@@ -1,4 +1,4 @@
-// Batch-1 streaming GEMV for long weight streams (GGUF Q4_0/Q4_1/Q8_0/Q6_K/Q4_K).
+// Batch-1 streaming GEMV for long weight streams (GGUF Q4_0/Q4_1/Q8_0/Q6_K/Q4_K/Q5_K/IQ4_XS).
 //
 // Same arithmetic as the persistent pipeline in gemv_kernels.hpp (activations
 // staged in LDS as scaled f16 pairs, codes decoded by the exponent trick into
@@ -94,6 +94,22 @@ struct StreamLane<EncQ4K> {  // lane offset = its super-block's; step i = lane b
     }
 };
 
+template <>
+struct StreamLane<EncQ5K> {  // lane offset = its super-block's; step i = lane bits 1, 0
+    uint32_t off, oq;
+    __device__ __forceinline__ void init(uint32_t bsh, uint32_t lane_off, uint32_t q) {
+        off = bsh + lane_off;  // the base is 4-byte aligned (bsh = 0)
+        oq = off + 48u + 32u * q;
+    }
+    __device__ __forceinline__ EncQ5K::Raw load(const uint8_t* sb) const {
+        EncQ5K::Raw r;
+        load_dwords<4>(reinterpret_cast<const uint32_t*>(sb + off), r.h);
+        load_dwords<EncQ5K::NT>(reinterpret_cast<const uint32_t*>(sb + off + 16u), r.hb);
+        load_dwords<EncQ5K::NT>(reinterpret_cast<const uint32_t*>(sb + oq), r.q);
+        return r;
+    }
+};
+
 // f(integral_constant<int, i>) for i = 0..N-1, unrolled.
 template <class F, int... I>
 __device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I...>) {
@@ -182,7 +198,7 @@ __global__ __launch_bounds__(TH) void gguf_gemv_stream_kernel(const GemvParams p
     const uint32_t bsh = (uint32_t)((uintptr_t)w & 3u);
     const uint8_t* abase = w - bsh;  // 4-byte aligned
     StreamLane<E> sl;
-    if constexpr (E::ENC == ENC_Q6_K || E::ENC == ENC_Q4_K) sl.init(bsh, g * rowbytes + (j >> 2) * (uint32_t)E::BB, j & 3u);
+    if constexpr (wide_chunks(E::ENC)) sl.init(bsh, g * rowbytes + (j >> 2) * (uint32_t)E::BB, j & 3u);
     else sl.init(bsh, g * rowbytes + j * (uint32_t)E::BB);
     // first row of row step k (the last step ends at the weight's last row)
     auto row0 = [&](uint32_t k) {
@@ -249,7 +265,7 @@ __global__ __launch_bounds__(TH) void gguf_gemv_stream_kernel(const GemvParams p
 // CPL = 1; every weight needs at least G = 64/L rows.  Every scalar step
 // (a row, a chunk round) must be a multiple of 4 bytes so that a lane's
 // realignment is fixed: rows of an even number of blocks (Q4_0, Q8_0; Q6_K
-// an even number of super-blocks) and, for Q6_K and Q4_K, L >= 8.  Returns
+// an even number of super-blocks) and, for the super-block encodings, L >= 8.  Returns
 // hipErrorNotSupported when nothing fits (the caller then runs the
 // persistent pipeline).
 template <class E, bool XBF16>

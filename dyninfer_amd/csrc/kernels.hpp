@@ -9,7 +9,16 @@ namespace dmx {
 constexpr int kMaxProblems = 4;  // weights sharing one activation per GEMV launch
 constexpr int kMaxGemvBatch = 16;
 
-enum Enc : uint32_t { ENC_Q4_0 = 2, ENC_Q4_1 = 3, ENC_Q8_0 = 8, ENC_Q4_K = 12, ENC_Q6_K = 14, ENC_MLX_U4 = 0x1004 };
+enum Enc : uint32_t {
+    ENC_Q4_0 = 2,
+    ENC_Q4_1 = 3,
+    ENC_Q8_0 = 8,
+    ENC_Q4_K = 12,
+    ENC_Q5_K = 13,
+    ENC_Q6_K = 14,
+    ENC_IQ4_XS = 23,
+    ENC_MLX_U4 = 0x1004
+};
 enum DType : uint32_t { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
 
 // Kernel parameters of one GEMV launch (passed by value as the kernel
@@ -45,24 +54,23 @@ struct GemvParams {
 
 // Bytes of the GEMV activation tile in LDS per (activation row, chunk): the
 // chunk's f16 pairs plus 16 bytes of bank padding, then its constants
-// (gemv_kernels.hpp XTile).  Chunks: 32 weights, 64 for Q6_K and Q4_K.
-__host__ __device__ constexpr uint32_t xtile_chunk_weights(uint32_t enc) {
-    return enc == ENC_Q6_K || enc == ENC_Q4_K ? 64u : 32u;
+// (gemv_kernels.hpp XTile).  Chunks: 32 weights, 64 for Q6_K, Q4_K and Q5_K.
+__host__ __device__ constexpr bool wide_chunks(uint32_t enc) {
+    return enc == ENC_Q6_K || enc == ENC_Q4_K || enc == ENC_Q5_K;
 }
+__host__ __device__ constexpr uint32_t xtile_chunk_weights(uint32_t enc) { return wide_chunks(enc) ? 64u : 32u; }
 __host__ __device__ constexpr uint32_t xtile_chunk_bytes(uint32_t enc) {
     return enc == ENC_Q6_K ? 36u * 4u + 4u * 2u * 4u                      // 32 pair dwords + pad, 4 groups x (-C, s)
-         : enc == ENC_Q4_K ? 36u * 4u + 2u * 4u * 4u                      // 32 + pad, 2 groups x (-C, s, s.Σx, 0)
-         : (enc == ENC_Q8_0 || enc == ENC_Q4_0) ? 20u * 4u + 2u * 4u      // 16 + pad, (-C, s)
+         : (enc == ENC_Q4_K || enc == ENC_Q5_K) ? 36u * 4u + 2u * 4u * 4u  // 32 + pad, 2 groups x (-C, s, s.Σx, 0)
+         : (enc == ENC_Q8_0 || enc == ENC_Q4_0 || enc == ENC_IQ4_XS) ? 20u * 4u + 2u * 4u  // 16 + pad, (-C, s)
          : 20u * 4u + 4u * 4u;                                            // Q4_1, MLX: (-C, s, s.Σx, 0)
 }
 __host__ __device__ constexpr uint64_t xtile_bytes(uint32_t enc, uint32_t B, uint32_t K) {
     return (uint64_t)B * (K / xtile_chunk_weights(enc)) * xtile_chunk_bytes(enc);
 }
 // Widest activation batch one GEMV launch holds in registers (wider batches
-// run as several launches): 8 rows, 4 for the 64-weight chunks of Q6_K and Q4_K.
-__host__ __device__ constexpr uint32_t max_register_batch(uint32_t enc) {
-    return enc == ENC_Q6_K || enc == ENC_Q4_K ? 4u : 8u;
-}
+// run as several launches): 8 rows, 4 for the 64-weight chunks.
+__host__ __device__ constexpr uint32_t max_register_batch(uint32_t enc) { return wide_chunks(enc) ? 4u : 8u; }
 // LDS of one gfx950 workgroup.
 constexpr uint32_t kLdsBytes = 160u * 1024u;
 
@@ -79,7 +87,7 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
                        bool x_bf16, uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype,
                        hipStream_t stream);
 
-// Decode GEMV on MFMA for 3..16 activation rows (Q4_0, Q6_K, Q4_K, MLX U4; K a
+// Decode GEMV on MFMA for 3..16 activation rows (Q4_0, Q6_K, Q4_K, Q5_K, MLX U4; K a
 // multiple of 256): whether it serves a call, and the launch (several
 // launches when K needs more than one LDS segment; f32 outputs only then).
 bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool y_bf16,

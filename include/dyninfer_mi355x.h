@@ -56,6 +56,8 @@ enum {
     DYNINFER_ENC_GGUF_Q6_K = 14,
     DYNINFER_ENC_GGUF_Q4_K = 12, /* GGML's 144-byte super-block; a schema-only type in the reference
                                     (gguf_block.rs:183-316), decoded here as GGML dequantize_row_q4_K */
+    DYNINFER_ENC_GGUF_Q5_K = 13, /* GGML's 176-byte super-block (schema only in the reference),
+                                    decoded as GGML dequantize_row_q5_K */
     DYNINFER_ENC_MLX_AFFINE_U4 = 0x1004
 };
 
@@ -69,7 +71,7 @@ enum { DYNINFER_DTYPE_F32 = 0, DYNINFER_DTYPE_F16 = 1, DYNINFER_DTYPE_BF16 = 2 }
  * GGUF (PhysicalEncoding::BlockQuantized, crates/dyninfer-checkpoint-gguf/src/convention.rs:200-279):
  *   `data` = the tensor's interleaved blocks, N*(K/B)*bytes_per_block bytes; row o, block b
  *   starts at byte (o*K/B + b)*bytes_per_block (gguf_codegen.rs:350-367).  `data` must be
- *   2-byte aligned (4-byte for Q4_1 and Q4_K).  scales/biases/group_size/scale_dtype are ignored.
+ *   2-byte aligned (4-byte for Q4_1, Q4_K and Q5_K).  scales/biases/group_size/scale_dtype are ignored.
  * MLX affine U4 (PhysicalEncoding::GroupQuantized, crates/dyninfer-checkpoint-safetensors/src/mlx.rs:152-261):
  *   `data` = packed u32 [N, K/8] (lane i = bits 4i..4i+3), `scales`, `biases` = [N, K/group_size]
  *   of `scale_dtype` (f32/f16/bf16), each aligned to its element size.
@@ -235,7 +237,7 @@ int dyninfer_mi355x_gguf_find(const dyninfer_gguf_t* g, const char* name, dyninf
  * then waits for the copy (the source is pageable mapped memory).  */
 int dyninfer_mi355x_gguf_upload(const dyninfer_gguf_t* g, const char* name, void* dst, uint64_t dst_bytes,
                                 void* stream);
-/* Describes a rank-2 Q4_0/Q4_1/Q8_0/Q6_K/Q4_K tensor whose bytes are at device_data as a
+/* Describes a rank-2 Q4_0/Q4_1/Q8_0/Q6_K/Q4_K/Q5_K tensor whose bytes are at device_data as a
  * dyninfer_qweight_t (rows = dims[0], cols = dims[1]); other types are unsupported. */
 int dyninfer_mi355x_gguf_qweight(const dyninfer_gguf_t* g, const char* name, const void* device_data,
                                  dyninfer_qweight_t* out);

@@ -1,10 +1,11 @@
-"""GGUF Q4_K (GGML's block_q4_K) through the C ABI.
+"""GGUF Q4_K and Q5_K (GGML's block_q4_K, block_q5_K) through the C ABI.
 
-The reference declares Q4_K's schema only (gguf_block.rs:183-316: type 12,
-256 weights, 144 bytes, components scale_min_f16 / scales_and_mins_u6 /
-quants_u4; convention.rs:210,240), so its kernels here decode GGML's layout,
-which the oracle restates and pins (tests/test_oracle.py: the packer-side
-scale/min layout, a known-answer block, the one-rounding closed form).
+The reference declares their schemas only (gguf_block.rs:183-316: types 12
+and 13, 256 weights, 144 and 176 bytes, components scale_min_f16 /
+scales_and_mins_u6 / [high_bits /] quants_u4; convention.rs:210-211,240-241),
+so the kernels here decode GGML's layouts, which the oracle restates and pins
+(tests/test_oracle.py: the packer-side layouts, known-answer blocks, the
+one-rounding closed forms).
 
 Bars, as for the other encodings:
   * dequantisation and embedding rows: bit-exact (every f32 bit pattern)
@@ -24,7 +25,9 @@ import oracle
 
 TOL = 2e-3
 XF16 = 2.0 ** -11 + 2e-5
-Q4K = oracle.Q4_K
+KQ = [oracle.Q4_K, oracle.Q5_K]
+ENC = {oracle.Q4_K: d.ENC_Q4_K, oracle.Q5_K: d.ENC_Q5_K}
+kinds = pytest.mark.parametrize("kind", KQ, ids=oracle.NAMES.get)
 
 
 def dev(a):
@@ -32,13 +35,13 @@ def dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
 
 
-def weight(n, k, seed, off=0):
-    """A Q4_K weight of synthetic super-blocks, `off` bytes into a device buffer."""
+def weight(kind, n, k, seed, off=0):
+    """A weight of synthetic super-blocks, `off` bytes into a device buffer."""
     import torch
-    data = oracle.synth_gguf(Q4K, n, k, seed)
+    data = oracle.synth_gguf(kind, n, k, seed)
     buf = torch.zeros(data.size + 16, dtype=torch.uint8, device="cuda")
     buf[off:off + data.size] = dev(data)
-    w = d.QWeight(d.ENC_Q4_K, n, k, buf.data_ptr() + off, data_bytes=data.size)
+    w = d.QWeight(ENC[kind], n, k, buf.data_ptr() + off, data_bytes=data.size)
     w._keep = buf
     return w, data
 
@@ -56,16 +59,18 @@ def err_of(y, x, wf):
 
 
 # ---------------------------------------------------------------- host-side (no GPU)
-def test_q4_k_weight_rules():
-    w = lambda **kw: d.QWeight(d.ENC_Q4_K, kw.pop("n", 8), kw.pop("k", 512), kw.pop("data", 0x1000), **kw)
+@kinds
+def test_weight_rules(kind):
+    w = lambda **kw: d.QWeight(ENC[kind], kw.pop("n", 8), kw.pop("k", 512), kw.pop("data", 0x1000), **kw)
     assert d.supports(w(), 1) and d.supports(w(), 16) and d.supports(w(), 512, d.DTYPE_BF16, d.DTYPE_BF16)
     assert not d.supports(w(k=384), 1)          # K a multiple of 256
     assert "multiple of the block size 256" in d.library().dyninfer_mi355x_last_error().decode()
     assert not d.supports(w(data=0x1002), 1)    # 4-byte-aligned super-blocks
     assert "4-byte aligned" in d.library().dyninfer_mi355x_last_error().decode()
-    assert d.supports(w(data_bytes=8 * 2 * 144), 1)
-    assert not d.supports(w(data_bytes=8 * 2 * 144 - 4), 1)
-    assert d.block_geometry(d.ENC_Q4_K) == (256, 144)
+    bb = oracle.BLOCK[kind][1]
+    assert d.supports(w(data_bytes=8 * 2 * bb), 1)
+    assert not d.supports(w(data_bytes=8 * 2 * bb - 4), 1)
+    assert d.block_geometry(ENC[kind]) == (256, bb)
 
 
 def _s(x: str) -> bytes:
@@ -73,19 +78,20 @@ def _s(x: str) -> bytes:
     return struct.pack("<Q", len(b)) + b
 
 
-def test_gguf_q4_k_tensor_indexed_and_described():
-    """A GGUF file holding a type-12 tensor: its exact byte range, and a QWeight
-    of it (the reference indexes such tensors but has no kernel for them)."""
+@kinds
+def test_gguf_tensor_indexed_and_described(kind):
+    """A GGUF file holding a tensor of the type: its exact byte range, and a
+    QWeight of it (the reference indexes such tensors but has no kernel for them)."""
     n, k = 6, 512
-    raw = oracle.synth_gguf(Q4K, n, k, 4).tobytes()
+    raw = oracle.synth_gguf(kind, n, k, 4).tobytes()
     body = b"GGUF" + struct.pack("<IQQ", 3, 1, 1) + _s("general.architecture") + struct.pack("<I", 8) + _s("llama")
-    body += _s("blk.0.ffn_up.weight") + struct.pack("<I", 2) + struct.pack("<QQ", k, n) + struct.pack("<IQ", 12, 0)
+    body += _s("blk.0.ffn_up.weight") + struct.pack("<I", 2) + struct.pack("<QQ", k, n) + struct.pack("<IQ", kind, 0)
     body += b"\0" * ((32 - len(body) % 32) % 32)
     g = d.GgufFile.from_bytes(body + raw)
     t = g.tensors[0]
-    assert (t.type_code, t.nbytes, t.offset) == (12, len(raw), len(body))
+    assert (t.type_code, t.nbytes, t.offset) == (kind, len(raw), len(body))
     w = g.qweight("blk.0.ffn_up.weight", 0x1000)
-    assert (w.encoding, w.rows, w.cols, w.data_bytes) == (d.ENC_Q4_K, n, k, len(raw))
+    assert (w.encoding, w.rows, w.cols, w.data_bytes) == (ENC[kind], n, k, len(raw))
     with pytest.raises(d.DyninferError):
         g.qweight("blk.0.ffn_up.weight", 0x1002)
 
@@ -93,13 +99,15 @@ def test_gguf_q4_k_tensor_indexed_and_described():
 # ---------------------------------------------------------------- dequant / embedding
 @pytest.mark.gpu
 @pytest.mark.parametrize("n,k,off", [(1, 256, 0), (3, 512, 4), (64, 1024, 0), (33, 4096, 12)])
-def test_dequant_bit_exact(ctx, n, k, off):
-    w, data = weight(n, k, seed=n + k, off=off)
-    assert_bits_equal(ctx.dequant(w).cpu().numpy(), oracle.dequant_gguf(Q4K, data, n, k))
+@kinds
+def test_dequant_bit_exact(ctx, kind, n, k, off):
+    w, data = weight(kind, n, k, seed=n + k, off=off)
+    assert_bits_equal(ctx.dequant(w).cpu().numpy(), oracle.dequant_gguf(kind, data, n, k))
 
 
 @pytest.mark.gpu
-def test_dequant_special_fields(ctx):
+@kinds
+def test_dequant_special_fields(ctx, kind):
     """d, dmin over signed zeros, subnormals, max, inf and NaN; every scale and
     min byte pattern (0x00 / 0xFF / random) so the top-two-bit paths of
     sub-blocks 4..7 are all exercised."""
@@ -108,7 +116,7 @@ def test_dequant_special_fields(ctx):
     blocks = []
     for i, dbits in enumerate(specials):
         for j, mbits in enumerate((0x0000, 0x3C00, specials[(i + 3) % len(specials)])):
-            b = rng.integers(0, 256, 144, dtype=np.uint8)
+            b = rng.integers(0, 256, oracle.BLOCK[kind][1], dtype=np.uint8)
             b[0:2] = [dbits & 0xFF, dbits >> 8]
             b[2:4] = [mbits & 0xFF, mbits >> 8]
             if j == 0:
@@ -116,27 +124,29 @@ def test_dequant_special_fields(ctx):
             blocks.append(b)
     data = np.concatenate(blocks)
     rows = len(blocks)
-    w = d.QWeight(d.ENC_Q4_K, rows, 256, dev(data))
-    assert_bits_equal(ctx.dequant(w).cpu().numpy(), oracle.dequant_gguf(Q4K, data, rows, 256))
+    w = d.QWeight(ENC[kind], rows, 256, dev(data))
+    assert_bits_equal(ctx.dequant(w).cpu().numpy(), oracle.dequant_gguf(kind, data, rows, 256))
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("vocab,k,n", [(1, 256, 1), (37, 512, 5), (300, 1024, 64), (9, 4096, 17)])
-def test_embedding_bit_exact(ctx, vocab, k, n):
-    w, data = weight(vocab, k, seed=vocab * 3 + k)
+@kinds
+def test_embedding_bit_exact(ctx, kind, vocab, k, n):
+    w, data = weight(kind, vocab, k, seed=vocab * 3 + k)
     rng = np.random.default_rng(n)
     ids = rng.integers(0, vocab, n).astype(np.int64)
     ids[:min(n, 2)] = [0, vocab - 1][:min(n, 2)]
     out = ctx.embedding(w, dev(ids)).cpu().numpy()
-    assert np.array_equal(out.view(np.uint32), oracle.dequant_gguf(Q4K, data, vocab, k)[ids].view(np.uint32))
+    assert np.array_equal(out.view(np.uint32), oracle.dequant_gguf(kind, data, vocab, k)[ids].view(np.uint32))
 
 
 @pytest.mark.gpu
-def test_embedding_out_of_range_ids_are_nan_rows(ctx):
-    w, data = weight(12, 512, seed=2)
+@kinds
+def test_embedding_out_of_range_ids_are_nan_rows(ctx, kind):
+    w, data = weight(kind, 12, 512, seed=2)
     ids = np.array([3, -1, 12, 11], np.int64)
     out = ctx.embedding(w, dev(ids)).cpu().numpy()
-    ref = oracle.dequant_gguf(Q4K, data, 12, 512)
+    ref = oracle.dequant_gguf(kind, data, 12, 512)
     assert np.array_equal(out[0], ref[3]) and np.array_equal(out[3], ref[11])
     assert np.isnan(out[1]).all() and np.isnan(out[2]).all()
 
@@ -151,35 +161,38 @@ SHAPES = [(1, 256), (67, 512), (1024, 1024), (3072, 1024), (1024, 3072), (513, 4
 @pytest.mark.gpu
 @pytest.mark.parametrize("n,k", SHAPES)
 @pytest.mark.parametrize("batch", [1, 2, 3, 4, 8, 16])
-def test_gemv(ctx, n, k, batch):
-    w, data = weight(n, k, seed=100 + n + k + batch)
+@kinds
+def test_gemv(ctx, kind, n, k, batch):
+    w, data = weight(kind, n, k, seed=100 + n + k + batch)
     x = oracle.randn(batch * k, seed=n * 7 + batch).reshape(batch, k)
     y = ctx.qlinear(w, dev(x)).cpu().numpy()
-    err = err_of(y, x, oracle.dequant_gguf(Q4K, data, n, k))
+    err = err_of(y, x, oracle.dequant_gguf(kind, data, n, k))
     assert err <= TOL and err <= XF16, err
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows", [17, 40])
-def test_more_than_16_rows(ctx, rows):
+@kinds
+def test_more_than_16_rows(ctx, kind, rows):
     n, k = 768, 2048
-    w, data = weight(n, k, seed=rows)
+    w, data = weight(kind, n, k, seed=rows)
     x = oracle.randn(rows * k, seed=rows + 1).reshape(rows, k)
     y = ctx.qlinear(w, dev(x)).cpu().numpy()
-    err = err_of(y, x, oracle.dequant_gguf(Q4K, data, n, k))
+    err = err_of(y, x, oracle.dequant_gguf(kind, data, n, k))
     assert err <= TOL and err <= XF16, err
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("batch", [1, 4])
-def test_bf16_activations_and_outputs_offset_base(ctx, batch):
+@kinds
+def test_bf16_activations_and_outputs_offset_base(ctx, kind, batch):
     import torch
     n, k = 2048, 4096
-    w, data = weight(n, k, seed=77, off=4)
+    w, data = weight(kind, n, k, seed=77, off=4)
     x = torch.from_numpy(oracle.randn(batch * k, seed=5).reshape(batch, k)).to(torch.bfloat16)
     xr = x.float().numpy()
     y = ctx.qlinear(w, x.cuda(), y_dtype=torch.bfloat16).float().cpu().numpy()
-    y64, absdot = oracle.linear_f64(xr, oracle.dequant_gguf(Q4K, data, n, k))
+    y64, absdot = oracle.linear_f64(xr, oracle.dequant_gguf(kind, data, n, k))
     # bf16 outputs add one bf16 rounding of |y| (relative 2^-9)
     bound = XF16 + 2.0 ** -9 * np.max(np.abs(y64) / absdot)
     err = oracle.normalized_error(y, y64, absdot)
@@ -188,13 +201,14 @@ def test_bf16_activations_and_outputs_offset_base(ctx, batch):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("batch", [1, 2, 16])
-def test_multi_weights_share_activations(ctx, batch):
+@kinds
+def test_multi_weights_share_activations(ctx, kind, batch):
     k = 4096
-    ws = [weight(n, k, seed=n + batch) for n in (4096, 1024, 1024)]
+    ws = [weight(kind, n, k, seed=n + batch) for n in (4096, 1024, 1024)]
     x = oracle.randn(batch * k, seed=batch).reshape(batch, k)
     ys = ctx.qlinear_multi([w for w, _ in ws], dev(x))
     for (w, data), y in zip(ws, ys):
-        err = err_of(y.cpu().numpy(), x, oracle.dequant_gguf(Q4K, data, w.rows, k))
+        err = err_of(y.cpu().numpy(), x, oracle.dequant_gguf(kind, data, w.rows, k))
         assert err <= TOL and err <= XF16, err
 
 
@@ -204,11 +218,11 @@ def test_multi_weights_share_activations(ctx, batch):
 # whose activation sums X_j are rounded once to f16.  Per output the error is
 # at most 2^-11·Σ|w||x| (activation rounding) + 2^-11·Σ|dmin·m||x| (sums)
 # plus f32 accumulation.
-def offsets_of(data, n, k):
+def offsets_of(kind, data, n, k):
     """|dmin·m| per weight: the dequantisation with every d set to zero."""
-    z = data.reshape(-1, 144).copy()
+    z = data.reshape(-1, oracle.BLOCK[kind][1]).copy()
     z[:, 0:2] = 0
-    return np.abs(oracle.dequant_gguf(Q4K, z.ravel(), n, k))
+    return np.abs(oracle.dequant_gguf(kind, z.ravel(), n, k))
 
 
 MFMA_CASES = [  # (n, k, batch, y_bf16): split mode, whole tiles, K segments, a padded tile
@@ -218,14 +232,15 @@ MFMA_CASES = [  # (n, k, batch, y_bf16): split mode, whole tiles, K segments, a 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("n,k,batch,ybf16", MFMA_CASES)
-def test_gemv_mfma(ctx, n, k, batch, ybf16):
+@kinds
+def test_gemv_mfma(ctx, kind, n, k, batch, ybf16):
     import torch
-    w, data = weight(n, k, seed=n + k + batch, off=4 if ybf16 else 0)
+    w, data = weight(kind, n, k, seed=n + k + batch, off=4 if ybf16 else 0)
     x = oracle.randn(batch * k, seed=batch * 3 + k).reshape(batch, k)
     y = ctx.qlinear(w, dev(x), y_dtype=torch.bfloat16 if ybf16 else torch.float32).float().cpu().numpy()
-    wf = oracle.dequant_gguf(Q4K, data, n, k)
+    wf = oracle.dequant_gguf(kind, data, n, k)
     y64, absdot = oracle.linear_f64(x, wf)
-    absb = np.abs(x.astype(np.float64)) @ offsets_of(data, n, k).astype(np.float64).T
+    absb = np.abs(x.astype(np.float64)) @ offsets_of(kind, data, n, k).astype(np.float64).T
     err = np.abs(y - y64) / absdot
     bound = 2.0 ** -11 + 2.0 ** -11 * absb / absdot + 2e-5
     if ybf16:
@@ -235,18 +250,19 @@ def test_gemv_mfma(ctx, n, k, batch, ybf16):
 
 
 @pytest.mark.gpu
-def test_gemv_mfma_large_offsets(ctx):
+@kinds
+def test_gemv_mfma_large_offsets(ctx, kind):
     """Blocks whose offsets dominate (dmin·m far above d·sc·q): the offset
     MFMA's rounding stays within its bound."""
     n, k, batch = 4096, 2048, 16
-    data = oracle.synth_gguf(Q4K, n, k, 8).reshape(-1, 144)
+    data = oracle.synth_gguf(kind, n, k, 8).reshape(-1, oracle.BLOCK[kind][1])
     data[:, 2:4] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)  # dmin = 0.5
     data = data.ravel()
-    w = d.QWeight(d.ENC_Q4_K, n, k, dev(data))
+    w = d.QWeight(ENC[kind], n, k, dev(data))
     x = oracle.randn(batch * k, seed=4).reshape(batch, k)
     y = ctx.qlinear(w, dev(x)).cpu().numpy()
-    y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(Q4K, data, n, k))
-    absb = np.abs(x.astype(np.float64)) @ offsets_of(data, n, k).astype(np.float64).T
+    y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(kind, data, n, k))
+    absb = np.abs(x.astype(np.float64)) @ offsets_of(kind, data, n, k).astype(np.float64).T
     err = np.abs(y - y64) / absdot
     assert np.all(err <= 2.0 ** -11 + 2.0 ** -11 * absb / absdot + 2e-5)
     assert oracle.normalized_error(y, y64, absdot) <= TOL
@@ -264,16 +280,17 @@ GEMM_CASES = [  # (rows, n, k, x/y bf16, base offset); 33+ rows, or 17+ with K >
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows,n,k,bf16,off", GEMM_CASES)
-def test_prefill_gemm(ctx, rows, n, k, bf16, off):
+@kinds
+def test_prefill_gemm(ctx, kind, rows, n, k, bf16, off):
     import torch
-    w, data = weight(n, k, seed=rows + n + k, off=off)
+    w, data = weight(kind, n, k, seed=rows + n + k, off=off)
     xt = torch.from_numpy(oracle.randn(rows * k, seed=rows + 9).reshape(rows, k))
     if bf16:
         xt = xt.to(torch.bfloat16)
     y = ctx.qlinear(w, xt.cuda(), y_dtype=torch.bfloat16 if bf16 else torch.float32).float().cpu().numpy()
     x = xt.float().numpy()
-    y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(Q4K, data, n, k))
-    absb = np.abs(x.astype(np.float64)) @ offsets_of(data, n, k).astype(np.float64).T
+    y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(kind, data, n, k))
+    absb = np.abs(x.astype(np.float64)) @ offsets_of(kind, data, n, k).astype(np.float64).T
     bound = 2.0 ** -10 + 2.0 ** -11 * (1.0 + 2.0 * absb / absdot) + 2e-5
     if bf16:
         bound = bound + 2.0 ** -9 * np.abs(y64) / absdot
@@ -283,19 +300,21 @@ def test_prefill_gemm(ctx, rows, n, k, bf16, off):
 
 
 @pytest.mark.gpu
-def test_prefill_gemm_multi(ctx):
+@kinds
+def test_prefill_gemm_multi(ctx, kind):
     rows, k = 96, 2048
-    ws = [weight(n, k, seed=n) for n in (2048, 512, 512)]
+    ws = [weight(kind, n, k, seed=n) for n in (2048, 512, 512)]
     x = oracle.randn(rows * k, seed=3).reshape(rows, k)
     ys = ctx.qlinear_multi([w for w, _ in ws], dev(x))
     for (w, data), y in zip(ws, ys):
-        y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(Q4K, data, w.rows, k))
+        y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(kind, data, w.rows, k))
         assert oracle.normalized_error(y.cpu().numpy(), y64, absdot) <= 2.0 ** -10 + 2.0 ** -10 + 2e-5
 
 
 @pytest.mark.gpu
-def test_deterministic(ctx):
-    w, _ = weight(4096, 4096, seed=1)
+@kinds
+def test_deterministic(ctx, kind):
+    w, _ = weight(kind, 4096, 4096, seed=1)
     x = dev(oracle.randn(4096, seed=2).reshape(1, 4096))
     a = ctx.qlinear(w, x).cpu().numpy()
     for _ in range(3):
