@@ -27,7 +27,7 @@ from typing import Optional, Sequence
 
 __all__ = [
     "LIB_PATH", "DyninferError", "QWeight", "Context", "library", "candidates", "registry_select",
-    "registry_require", "precision_check", "supports", "ENC_Q4_0", "ENC_Q4_1", "ENC_Q8_0", "ENC_Q6_K", "ENC_Q4_K", "ENC_Q5_K", "ENC_MLX_U4",
+    "registry_require", "precision_check", "supports", "ENC_Q4_0", "ENC_Q4_1", "ENC_Q8_0", "ENC_Q6_K", "ENC_Q4_K", "ENC_Q5_K", "ENC_IQ4_XS", "ENC_MLX_U4",
     "DTYPE_F32", "DTYPE_F16", "DTYPE_BF16", "block_geometry", "weight_bytes", "ERR_INVALID_ARGUMENT",
     "ERR_UNSUPPORTED", "ERR_HIP", "ERR_DEVICE", "ERR_BUFFER_TOO_SMALL",
 ]
@@ -36,15 +36,15 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdyninfer
 
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_HIP, ERR_DEVICE, ERR_BUFFER_TOO_SMALL = 0, 1, 2, 3, 4, 5
 ENC_Q4_0, ENC_Q4_1, ENC_Q8_0, ENC_Q6_K, ENC_MLX_U4 = 2, 3, 8, 14, 0x1004
-# GGML's block_q4_K / block_q5_K: schema-only types in the reference (gguf_block.rs:183-316)
-ENC_Q4_K, ENC_Q5_K = 12, 13
+# GGML's block_q4_K / block_q5_K / block_iq4_xs: schema-only types in the reference (gguf_block.rs:183-316)
+ENC_Q4_K, ENC_Q5_K, ENC_IQ4_XS = 12, 13, 23
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 32 << 20  # DYNINFER_MI355X_NOALLOC_SCRATCH_BYTES
 ENCODING_IDS = {ENC_Q4_0: "gguf.q4_0", ENC_Q4_1: "gguf.q4_1", ENC_Q8_0: "gguf.q8_0", ENC_Q6_K: "gguf.q6_k",
-                ENC_Q4_K: "gguf.q4_k", ENC_Q5_K: "gguf.q5_k", ENC_MLX_U4: "mlx.affine.u4"}
+                ENC_Q4_K: "gguf.q4_k", ENC_Q5_K: "gguf.q5_k", ENC_IQ4_XS: "gguf.iq4_xs", ENC_MLX_U4: "mlx.affine.u4"}
 # (weights per block, bytes per block): gguf_codegen.rs:23-38; K-quants: gguf_block.rs:207-226
 _GGUF_BLOCK = {ENC_Q4_0: (32, 18), ENC_Q4_1: (32, 20), ENC_Q8_0: (32, 34), ENC_Q6_K: (256, 210),
-               ENC_Q4_K: (256, 144), ENC_Q5_K: (256, 176)}
+               ENC_Q4_K: (256, 144), ENC_Q5_K: (256, 176), ENC_IQ4_XS: (256, 136)}
 
 EXPORTED_SYMBOLS = (
     "dyninfer_mi355x_open", "dyninfer_mi355x_close", "dyninfer_mi355x_last_error", "dyninfer_mi355x_qlinear",
@@ -430,7 +430,7 @@ class GgufFile:
         return dst
 
     def qweight(self, name: str, device_data) -> QWeight:
-        """QWeight of a rank-2 Q4_0/Q4_1/Q8_0/Q6_K/Q4_K/Q5_K tensor whose bytes are at device_data."""
+        """QWeight of a rank-2 GGUF tensor (Q4_0/Q4_1/Q8_0/Q6_K/Q4_K/Q5_K/IQ4_XS) whose bytes are at device_data."""
         wc = _QWeightC()
         _check(self._lib.dyninfer_mi355x_gguf_qweight(self._h, name.encode(), _ptr(device_data), ctypes.byref(wc)))
         return QWeight(wc.encoding, wc.rows, wc.cols, device_data, data_bytes=wc.data_bytes)

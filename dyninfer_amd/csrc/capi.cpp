@@ -85,7 +85,8 @@ uint32_t block_weights(uint32_t enc) {
     case DYNINFER_ENC_GGUF_Q8_0: return 32;
     case DYNINFER_ENC_GGUF_Q6_K:
     case DYNINFER_ENC_GGUF_Q4_K:
-    case DYNINFER_ENC_GGUF_Q5_K: return 256;
+    case DYNINFER_ENC_GGUF_Q5_K:
+    case DYNINFER_ENC_GGUF_IQ4_XS: return 256;
     default: return 0;
     }
 }
@@ -98,6 +99,7 @@ uint64_t block_bytes(uint32_t enc) {
     case DYNINFER_ENC_GGUF_Q6_K: return 210;
     case DYNINFER_ENC_GGUF_Q4_K: return 144;
     case DYNINFER_ENC_GGUF_Q5_K: return 176;
+    case DYNINFER_ENC_GGUF_IQ4_XS: return 136;
     default: return 0;
     }
 }
@@ -110,6 +112,7 @@ const char* enc_name(uint32_t enc) {
     case DYNINFER_ENC_GGUF_Q6_K: return "gguf.q6_k";
     case DYNINFER_ENC_GGUF_Q4_K: return "gguf.q4_k";
     case DYNINFER_ENC_GGUF_Q5_K: return "gguf.q5_k";
+    case DYNINFER_ENC_GGUF_IQ4_XS: return "gguf.iq4_xs";
     case DYNINFER_ENC_MLX_AFFINE_U4: return "mlx.affine.u4";
     default: return "unknown";
     }
@@ -129,10 +132,11 @@ int check_weight(const dyninfer_qweight_t* w) {
             return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
                         std::string(enc_name(w->encoding)) + ": logical axis 1 (" + std::to_string(w->cols) +
                             ") is not a multiple of the block size " + std::to_string(bw));
-        const uintptr_t need = w->encoding == DYNINFER_ENC_GGUF_Q4_1 || w->encoding == DYNINFER_ENC_GGUF_Q4_K ||
-                                       w->encoding == DYNINFER_ENC_GGUF_Q5_K
-                                   ? 4
-                                   : 2;
+        // 2-byte aligned blocks for Q4_0, Q8_0 and Q6_K (18, 34 and 210 bytes), 4-byte for the rest
+        const uintptr_t need = w->encoding == DYNINFER_ENC_GGUF_Q4_0 || w->encoding == DYNINFER_ENC_GGUF_Q8_0 ||
+                                       w->encoding == DYNINFER_ENC_GGUF_Q6_K
+                                   ? 2
+                                   : 4;
         if (!aligned(w->data, need))
             return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string(enc_name(w->encoding)) +
                                                                   ": block data must be " + std::to_string(need) +
@@ -223,7 +227,8 @@ size_t esize(uint32_t dt) { return dt == DYNINFER_DTYPE_F32 ? 4 : 2; }
 // 60.9 against 73.2 us, Q4_K 66.9 against 81.8 us).
 bool has_prefill_gemm(uint32_t enc, uint32_t N, uint32_t K, uint32_t rows) {
     const bool mfma_gemv = enc == DYNINFER_ENC_GGUF_Q4_0 || enc == DYNINFER_ENC_GGUF_Q6_K ||
-                           enc == DYNINFER_ENC_GGUF_Q4_K || enc == DYNINFER_ENC_GGUF_Q5_K;
+                           enc == DYNINFER_ENC_GGUF_Q4_K || enc == DYNINFER_ENC_GGUF_Q5_K ||
+                           enc == DYNINFER_ENC_GGUF_IQ4_XS;
     const uint32_t min_rows = mfma_gemv && K <= 8192u ? 2u * (uint32_t)dmx::kMaxGemvBatch + 1u
                                                       : (uint32_t)dmx::kMaxGemvBatch + 1u;
     return rows >= min_rows && dmx::gemm_supported(enc, N, K, rows);
@@ -577,10 +582,11 @@ int dyninfer_mi355x_gguf_qweight(const dyninfer_gguf_t* g, const char* name, con
     if (!t) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string("no tensor named ") + name);
     if (t->shape.size() != 2) return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "tensor " + t->name + " is not rank 2");
     if (t->type_code != dmx::ENC_Q4_0 && t->type_code != dmx::ENC_Q4_1 && t->type_code != dmx::ENC_Q8_0 &&
-        t->type_code != dmx::ENC_Q6_K && t->type_code != dmx::ENC_Q4_K && t->type_code != dmx::ENC_Q5_K)
+        t->type_code != dmx::ENC_Q6_K && t->type_code != dmx::ENC_Q4_K && t->type_code != dmx::ENC_Q5_K &&
+        t->type_code != dmx::ENC_IQ4_XS)
         return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "tensor " + t->name + " has GGUF type " +
                                                          std::to_string(t->type_code) +
-                                                         ", not Q4_0/Q4_1/Q8_0/Q6_K/Q4_K/Q5_K");
+                                                         ", not Q4_0/Q4_1/Q8_0/Q6_K/Q4_K/Q5_K/IQ4_XS");
     std::memset(out, 0, sizeof *out);
     out->encoding = t->type_code;
     out->rows = t->shape[0];

@@ -9,7 +9,8 @@
 //   MLX   f32(q) * s + b                     mlx_affine.rs:593-598
 //   Q4_K  (f32(d) * f32(sc)) * f32(q) - f32(dmin) * f32(m)   GGML dequantize_row_q4_K
 //   Q5_K  the same with 5-bit q                               GGML dequantize_row_q5_K
-//         (the reference declares the K-quants' schemas only, gguf_block.rs:183-316)
+//   IQ4_XS (f32(d) * f32(ls - 32)) * f32(kvalues_iq4nl[q])    GGML dequantize_row_iq4_xs
+//         (the reference declares these schemas only, gguf_block.rs:183-316)
 // Products that are exact (all but MLX with f32 scales) make fma contraction
 // harmless; the MLX f32-scale product is rounded explicitly before the add.
 #include "device_common.hpp"
@@ -66,6 +67,19 @@ __global__ __launch_bounds__(256) void gguf_dequant_kernel(const uint8_t* __rest
             uint32_t c = (load_u8(q + l) >> sh) & 15u;
             if constexpr (ENC == ENC_Q5_K) c |= ((load_u8(blk + 16 + l) >> j) & 1u) << 4;  // bit j of qh[l]
             o[l] = ds * (float)c - dm;
+        }
+    } else if constexpr (ENC == ENC_IQ4_XS) {  // slice t = sub-block t & 7 of super-block t/8
+        const uint8_t* blk = w + (t >> 3) * 136;
+        const uint32_t ib = (uint32_t)(t & 7u);
+        const uint32_t ls = ((load_u8(blk + 4 + ib / 2) >> (4u * (ib & 1u))) & 15u) |
+                            (((load_u16le(blk + 2) >> (2u * ib)) & 3u) << 4);
+        const float dl = f16_bits_to_f32(load_u16le(blk)) * (float)((int32_t)ls - 32);
+        const uint8_t* q = blk + 8 + 16 * ib;
+        for (int l = 0; l < 16; l++) {
+            const uint32_t byte = load_u8(q + l);
+            // codebook entry = (v + 128) - 128, exact
+            o[l] = dl * (float)((int32_t)(iq4nl_lookup(byte & 15u) & 0xFFu) - 128);
+            o[16 + l] = dl * (float)((int32_t)(iq4nl_lookup(byte >> 4) & 0xFFu) - 128);
         }
     } else {  // Q6_K: slice t = (super-block t/8, n, h, p) of 32 weights
         const uint64_t sb = t >> 3;
@@ -130,6 +144,7 @@ hipError_t dequant_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, con
     case ENC_Q6_K: hipLaunchKernelGGL(gguf_dequant_kernel<ENC_Q6_K>, grid, block, 0, stream, w, nslices, out); break;
     case ENC_Q4_K: hipLaunchKernelGGL(gguf_dequant_kernel<ENC_Q4_K>, grid, block, 0, stream, w, nslices, out); break;
     case ENC_Q5_K: hipLaunchKernelGGL(gguf_dequant_kernel<ENC_Q5_K>, grid, block, 0, stream, w, nslices, out); break;
+    case ENC_IQ4_XS: hipLaunchKernelGGL(gguf_dequant_kernel<ENC_IQ4_XS>, grid, block, 0, stream, w, nslices, out); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -115,4 +115,27 @@ __device__ __forceinline__ void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uin
     }
 }
 
+// IQ4_XS / IQ4_NL: GGML's kvalues_iq4nl codebook (a constant of the format)
+//   {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113}
+// held as the bytes v + 128 (v ^ 0x80: unsigned, so an entry decodes like a
+// Q8_0 code), four entries per dword.
+constexpr uint32_t kIq4nlT0 = 0x3F2D1801u, kIq4nlT1 = 0x766A5D4Fu, kIq4nlT2 = 0xA6998D81u, kIq4nlT3 = 0xF1D9C5B5u;
+
+// The codebook bytes (v + 128) of four 4-bit indices held one per byte of
+// idx (each 0..15): entries 0..7 and 8..15 by one v_perm_b32 each, merged by
+// each index's bit 3 (a v_perm selector of 12 gives 0x00, of 13 0xFF).
+__device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t idx) {
+    const uint32_t lo = __builtin_amdgcn_perm(kIq4nlT1, kIq4nlT0, idx);
+    const uint32_t hi = __builtin_amdgcn_perm(kIq4nlT3, kIq4nlT2, idx & 0x07070707u);
+    const uint32_t msel = ((idx >> 3) & 0x01010101u) | 0x0C0C0C0Cu;
+    const uint32_t mask = __builtin_amdgcn_perm(0u, 0u, msel);
+    return (hi & mask) | (lo & ~mask);  // v_bfi_b32
+}
+
+// IQ4_XS sub-block ib's (0..7) 6-bit scale: nibble ib & 1 of scales_l[ib / 2]
+// (sl = scales_l as a dword) | bits 2ib..2ib+1 of scales_h (sh) << 4.
+__device__ __forceinline__ uint32_t iq4xs_scale(uint32_t sh, uint32_t sl, uint32_t ib) {
+    return ((sl >> (4u * ib)) & 15u) | (((sh >> (2u * ib)) & 3u) << 4);
+}
+
 }  // namespace dmx

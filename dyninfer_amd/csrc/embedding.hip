@@ -65,6 +65,14 @@ __device__ __forceinline__ float4 gguf_four(const uint8_t* __restrict__ row, uin
             if constexpr (ENC == ENC_Q5_K) c |= ((ld8(blk + 16 + l0 + i) >> jsub) & 1u) << 4;
             v[i] = ds * (float)c - dm;
         }
+    } else if constexpr (ENC == ENC_IQ4_XS) {  // idx = 32ib + 16h + l: nibble h of qs[16ib + l]
+        const uint8_t* blk = row + (size_t)(k >> 8) * 136u;
+        const uint32_t idx = k & 255u, ib = idx >> 5, hh = (idx >> 4) & 1u;
+        const uint32_t ls = ((ld8(blk + 4 + ib / 2) >> (4u * (ib & 1u))) & 15u) | (((ld16(blk + 2) >> (2u * ib)) & 3u) << 4);
+        const float dl = f16_bits_to_f32(ld16(blk)) * (float)((int32_t)ls - 32);
+        const uint8_t* q = blk + 8 + 16 * ib + (idx & 15u);
+        for (int i = 0; i < 4; i++)
+            v[i] = dl * (float)((int32_t)(iq4nl_lookup((ld8(q + i) >> (4u * hh)) & 15u) & 0xFFu) - 128);
     } else {  // Q6_K: idx = n*128 + h*64 + p*32 + s*16 + l (gguf_codegen.rs:499-503)
         const uint8_t* blk = row + (size_t)(k >> 8) * 210u;
         const uint32_t idx = k & 255u;
@@ -169,6 +177,10 @@ hipError_t gather_launch(uint32_t enc, const uint8_t* w, const uint8_t* sc, cons
         break;
     case ENC_Q5_K:
         hipLaunchKernelGGL(gguf_gather_kernel<ENC_Q5_K>, grid, block, 0, stream, w, (uint64_t)(K / 256) * 176u, vocab,
+                           K, per_row, ids, out);
+        break;
+    case ENC_IQ4_XS:
+        hipLaunchKernelGGL(gguf_gather_kernel<ENC_IQ4_XS>, grid, block, 0, stream, w, (uint64_t)(K / 256) * 136u, vocab,
                            K, per_row, ids, out);
         break;
     default: return hipErrorInvalidValue;

@@ -25,6 +25,7 @@
 //   Q6_K  w = (q-32)·sc·d        6-bit code q,    off 32, per 16-weight group
 //   Q4_K  w = q·(d·sc) - dmin·m  code q,          off 0, - dmin·m·Σx, per 32-weight group
 //   Q5_K  as Q4_K with 5-bit codes (a fifth bit from qh)
+//   IQ4_XS w = kv[q]·(ls-32)·d   codebook byte kv[q]+128, off 128, per 32-weight sub-block
 //   MLX   w = q·s + b            code q,          off 0, + b·Σx
 //
 // Layout contract with the activation staging (gemv_kernels.hpp): for code
@@ -462,6 +463,59 @@ struct EncQ5K {
     }
 };
 
+// ------------------------------------------------------------------ GGUF IQ4_XS
+// 136-byte super-block of 256 (GGML block_iq4_xs; the reference's schema
+// gguf_block.rs:183-316 "iq4_xs", convention.rs:221,267: scale_f16 2 B,
+// scales_high_u16 2 B, scales_low_u8 4 B, nonlinear_quants_u4 128 B): d,
+// scales_h, scales_l[4], qs = bytes 8..136.  Chunk u is sub-block ib = u & 7
+// of super-block u >> 3: 32 weights laid out as a Q4_0 block (low nibble of
+// qs[16ib + l] = weight l, high = 16 + l), each nibble an index into GGML's
+// kvalues_iq4nl codebook, w = kv·(ls - 32)·d with the sub-block's 6-bit
+// scale ls.  The codebook bytes kv + 128 (iq4nl_lookup) decode as Q8_0's
+// codes: pairs (4t, 4t+2), (16+4t, 18+4t), (4t+1, 4t+3), (17+4t, 19+4t),
+// all at mantissa bit 0.  Super-blocks are 4-byte aligned (136 = 34 dwords).
+struct EncIQ4XS {
+    static constexpr uint32_t ENC = ENC_IQ4_XS;
+    static constexpr int CW = 32, QK = 256, NT = 4, PPT = 4, NG = 1, BB = 136;
+    static constexpr bool AFFINE = false;
+    static constexpr int NRUN = 1, RUNLEN = 32, RUNSTRIDE = 0;
+    __device__ __forceinline__ static uint32_t xbase(uint32_t u) { return 32u * u; }
+    static constexpr float coef(bool) { return 1152.0f; }
+    static constexpr int xoff(int t, int h, int e) { return EncQ40::xoff(t, h, e); }
+    static constexpr bool dv(int, int) { return false; }
+    static constexpr int grp(int, int) { return 0; }
+    static constexpr int TSTRIDE = 4, NXR = 2;
+    static constexpr int xrun0(int r) { return EncQ40::xrun0(r); }
+    struct Raw { uint32_t h[2]; uint32_t q[NT]; };  // d | scales_h, scales_l; the sub-block's codes
+    struct Chunk { uint32_t q[NT]; float d; };
+    __device__ __forceinline__ static Raw load(const uint8_t* w, uint32_t rowoff, uint32_t u) {
+        const uint32_t* sb = reinterpret_cast<const uint32_t*>(w + (rowoff + (u >> 3) * (uint32_t)BB));
+        Raw r;
+        load_dwords<2>(sb, r.h);
+        load_dwords<NT>(sb + 2u + 4u * (u & 7u), r.q);
+        return r;
+    }
+    __device__ __forceinline__ static Chunk unpack(const Raw& r, uint32_t u) {
+        Chunk c;
+#pragma unroll
+        for (int t = 0; t < NT; t++) c.q[t] = r.q[t];
+        const int ls = (int)iq4xs_scale(r.h[0] >> 16, r.h[1], u & 7u);
+        c.d = f16_bits_to_f32(r.h[0]) * (float)(ls - 32);
+        return c;
+    }
+    __device__ __forceinline__ static void pairs(const Chunk& c, int t, uint32_t (&p)[PPT]) {
+        const uint32_t Q = c.q[t];
+        const uint32_t L = iq4nl_lookup(Q & 0x0F0F0F0Fu), H = iq4nl_lookup((Q >> 4) & 0x0F0F0F0Fu);
+        p[0] = and_or(L, 0x00FF00FFu, kMagic);       // (4t, 4t+2)
+        p[1] = and_or(H, 0x00FF00FFu, kMagic);       // (16+4t, 18+4t)
+        p[2] = and_or(L >> 8, 0x00FF00FFu, kMagic);  // (4t+1, 4t+3)
+        p[3] = and_or(H >> 8, 0x00FF00FFu, kMagic);  // (17+4t, 19+4t)
+    }
+    __device__ __forceinline__ static float gscale(const Chunk& c, int) { return c.d; }
+    __device__ __forceinline__ static float goffset(const Chunk&, int) { return 0.0f; }
+    __device__ __forceinline__ static void zero_if(Chunk& c, bool z) { c.d = z ? 0.0f : c.d; }
+};
+
 // ------------------------------------------------------------------ MLX affine U4
 // One chunk = 32 weights = 4 packed u32 words (weight i of a word = bits
 // 4i..4i+3, fixture.rs:307-311) sharing one scale and bias (group size is a
@@ -537,7 +591,7 @@ constexpr bool xruns_ok() {
     return 4 * E::NXR == 2 * E::PPT;
 }
 static_assert(xruns_ok<EncQ40>() && xruns_ok<EncQ41>() && xruns_ok<EncQ80>() && xruns_ok<EncQ6K>() &&
-                  xruns_ok<EncQ4K>() && xruns_ok<EncQ5K>() && xruns_ok<EncMlxU4>(),
+                  xruns_ok<EncQ4K>() && xruns_ok<EncQ5K>() && xruns_ok<EncIQ4XS>() && xruns_ok<EncMlxU4>(),
               "activation runs disagree with xoff()");
 
 }  // namespace dmx

@@ -1,5 +1,5 @@
 // Prefill GEMM on gfx950 MFMA for the GGUF encodings Q4_0, Q4_1, Q8_0, Q6_K,
-// Q4_K and Q5_K and for MLX affine U4: Y[M, N] = X[M, K] · Wᵀ with f32 accumulation.
+// Q4_K, Q5_K and IQ4_XS and for MLX affine U4: Y[M, N] = X[M, K] · Wᵀ with f32 accumulation.
 //
 // Reference semantics: the same `emit_linear` contraction as decode
 // (gguf_codegen.rs:268-314, dequantisations :412-472 Q4_0, :382-410 Q8_0,
@@ -602,9 +602,84 @@ struct WinQK {
 using WinQ4K = WinQK<false>;
 using WinQ5K = WinQK<true>;
 
+// GGUF IQ4_XS (GGML block_iq4_xs, 136-byte super-blocks of 256 weights; the
+// reference's schema gguf_block.rs:183-316): chunk g of a row covers
+// sub-blocks 2i and 2i + 1 (i = g % 4) of super-block g / 4; lane half h
+// decodes sub-block 2i + h, laid out as a Q4_0 block (XFRAG_NIB order), each
+// nibble looked up in the codebook (iq4nl_lookup) and decoded as Q8_0's codes:
+// w = RNE_f16(kv·RNE_f16(d·(ls - 32))).  The window per row: the 16 bytes
+// from the super-block's start (d, scales_h, scales_l) and the chunk's 32
+// code bytes, three 16-byte pieces within the super-block.
+struct WinIQ4XS {
+    static constexpr uint32_t NP = 3, kCopies = NP;
+    static constexpr uint32_t kPitch = 16u * NP;
+    static constexpr uint32_t kBytes = 64u * kPitch;
+    static constexpr uint32_t kDw = 12;  // d|scales_h, scales_l, two unused, 8 code dwords
+    static constexpr uint32_t kValuPerStep = 24;
+    struct Scale {
+        h2 ds;
+        uint32_t h;
+    };
+    uintptr_t rb[NP];
+    uint32_t pp[NP];
+    uint32_t c0, lane;
+
+    __device__ void init(const GemmArgs& a, uint32_t n0, uint32_t lane_, uint32_t c0_) {
+        lane = lane_;
+        c0 = c0_;
+#pragma unroll
+        for (uint32_t q = 0; q < NP; q++) {
+            const uint32_t li = 64u * q + lane, r = li / NP;
+            const uint32_t n = n0 + r < a.N ? n0 + r : a.N - 1u;  // past N: re-read the last row (never stored)
+            rb[q] = (uintptr_t)a.w + (uintptr_t)n * a.rowbytes;
+            pp[q] = li % NP;
+        }
+    }
+    __device__ void issue(uint32_t c, uint8_t* win) const {
+        const uint32_t g = c0 + c, sb = g >> 2, i = g & 3u;
+#pragma unroll
+        for (uint32_t q = 0; q < NP; q++) {
+            const uint32_t o = pp[q] == 0u ? 0u : 8u + 32u * i + 16u * (pp[q] - 1u);
+            dma16(reinterpret_cast<const void*>(rb[q] + (uintptr_t)sb * 136u + o), win + 1024u * q);
+        }
+    }
+    __device__ void read(uint32_t, const uint8_t* win, uint32_t* raw) const {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint8_t* w = win + (32u * j + (lane & 31u)) * kPitch;
+            uint32_t* o = raw + j * kDw;
+#pragma unroll
+            for (uint32_t v = 0; v < NP; v++) {
+                const u32x4 x = *reinterpret_cast<const u32x4*>(w + 16u * v);
+                o[4 * v] = x.x;
+                o[4 * v + 1] = x.y;
+                o[4 * v + 2] = x.z;
+                o[4 * v + 3] = x.w;
+            }
+        }
+    }
+    __device__ Scale scale(uint32_t c, int, const uint32_t* r) const {
+        const uint32_t h = lane >> 5, ib = 2u * ((c0 + c) & 3u) + h;
+        const float dl = f16_bits_to_f32(r[0]) * (float)((int)iq4xs_scale(r[0] >> 16, r[1], ib) - 32);  // exact
+        const _Float16 ds = (_Float16)dl;
+        return {h2{ds, ds}, h};
+    }
+    __device__ h8 step(const uint32_t* r, const Scale& s, int t) const {
+        const h2 o = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+        auto f = [&](uint32_t v) { return as_u((as_h2(and_or(v, 0x00FF00FFu, 0x64006400u)) + o) * s.ds); };
+        const uint32_t q = r[4u + 4u * s.h + (uint32_t)t];
+        const uint32_t L = iq4nl_lookup(q & 0x0F0F0F0Fu), H = iq4nl_lookup((q >> 4) & 0x0F0F0F0Fu);
+        return as_h8(f(L), f(L >> 8), f(H), f(H >> 8));
+    }
+};
+
 template <uint32_t ENC>
 struct WinOf {
     using type = WinBlocks<ENC>;
+};
+template <>
+struct WinOf<ENC_IQ4_XS> {
+    using type = WinIQ4XS;
 };
 template <>
 struct WinOf<ENC_Q4_K> {
@@ -926,6 +1001,7 @@ uint32_t gemm_layout(uint32_t enc) {
         case ENC_Q6_K: return XFRAG_BYTE;  // a lane's 32 codes in order, as Q8_0
         case ENC_Q4_K:
         case ENC_Q5_K: return XFRAG_BYTE;
+        case ENC_IQ4_XS: return XFRAG_NIB;  // a sub-block laid out as a Q4_0 block
         case ENC_MLX_U4: return XFRAG_WORD;
         default: return ~0u;
     }
@@ -933,7 +1009,7 @@ uint32_t gemm_layout(uint32_t enc) {
 
 bool gemm_supported(uint32_t enc, uint32_t N, uint32_t K, uint32_t M) {
     return gemm_layout(enc) != ~0u && N > 0 && M > 0 && K >= 64u &&
-           K % (enc == ENC_Q6_K || enc == ENC_Q4_K || enc == ENC_Q5_K ? 256u : 64u) == 0;
+           K % (enc == ENC_Q6_K || enc == ENC_Q4_K || enc == ENC_Q5_K || enc == ENC_IQ4_XS ? 256u : 64u) == 0;
 }
 
 hipError_t gemm_launch(const GemmWeight& wt, uint32_t N, uint32_t K, const uint16_t* xh, const float* rs, uint32_t M,
@@ -962,6 +1038,7 @@ hipError_t gemm_launch(const GemmWeight& wt, uint32_t N, uint32_t K, const uint1
         case ENC_Q6_K: a.rowbytes = (uint64_t)(K / 256u) * 210u; break;
         case ENC_Q4_K: a.rowbytes = (uint64_t)(K / 256u) * 144u; break;
         case ENC_Q5_K: a.rowbytes = (uint64_t)(K / 256u) * 176u; break;
+        case ENC_IQ4_XS: a.rowbytes = (uint64_t)(K / 256u) * 136u; break;
         default: a.rowbytes = (uint64_t)K / 2u; break;  // MLX packed words (scales and biases besides)
     }
     // M-major tile order when the staged activations (2 bytes per element)
@@ -974,6 +1051,7 @@ hipError_t gemm_launch(const GemmWeight& wt, uint32_t N, uint32_t K, const uint1
         case ENC_Q6_K: return launch_enc<ENC_Q6_K>(a, st);
         case ENC_Q4_K: return launch_enc<ENC_Q4_K>(a, st);
         case ENC_Q5_K: return launch_enc<ENC_Q5_K>(a, st);
+        case ENC_IQ4_XS: return launch_enc<ENC_IQ4_XS>(a, st);
         case ENC_MLX_U4: return launch_enc<ENC_MLX_U4>(a, st);
         default: return hipErrorInvalidValue;
     }

@@ -14,6 +14,7 @@ hipError_t gemv_launch_q8_0(const GemvParams& p, uint32_t B, uint32_t oneshot, b
 hipError_t gemv_launch_q6_k(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
 hipError_t gemv_launch_q4_k(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
 hipError_t gemv_launch_q5_k(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
+hipError_t gemv_launch_iq4_xs(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
 hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st);
 
 hipError_t cached_occupancy(const void* kernel, size_t lds, int threads, int* per_cu, int* cus) {
@@ -85,6 +86,7 @@ bool enc_info(uint32_t enc, EncInfo& e) {
     case ENC_Q4_0:
     case ENC_Q4_1:
     case ENC_Q8_0:
+    case ENC_IQ4_XS:
     case ENC_MLX_U4: e = {32, false}; return true;
     case ENC_Q6_K: e = {64, true}; return true;
     case ENC_Q4_K:
@@ -101,6 +103,7 @@ hipError_t launch(uint32_t enc, const GemvParams& p, uint32_t B, uint32_t onesho
     case ENC_Q6_K: return gemv_launch_q6_k(p, B, oneshot, xbf16, st);
     case ENC_Q4_K: return gemv_launch_q4_k(p, B, oneshot, xbf16, st);
     case ENC_Q5_K: return gemv_launch_q5_k(p, B, oneshot, xbf16, st);
+    case ENC_IQ4_XS: return gemv_launch_iq4_xs(p, B, oneshot, xbf16, st);
     case ENC_MLX_U4: return gemv_launch_mlx_u4(p, B, oneshot, xbf16, st);
     default: return hipErrorInvalidValue;
     }

@@ -1,5 +1,5 @@
-// Decode GEMV on MFMA for 3..16 activation rows, GGUF Q4_0, Q6_K, Q4_K and
-// Q5_K and MLX affine U4 (y[b, o] = Σ_k x[b, k]·w[o, k], f32 accumulation;
+// Decode GEMV on MFMA for 3..16 activation rows, GGUF Q4_0, Q6_K, Q4_K, Q5_K
+// and IQ4_XS and MLX affine U4 (y[b, o] = Σ_k x[b, k]·w[o, k], f32 accumulation;
 // gguf_codegen.rs:268-314 `emit_linear` with the dequantisations of :412-472
 // (Q4_0) and :474-526 (Q6_K), mlx_affine.rs:557-626 `emit_linear_u4`).
 //
@@ -253,6 +253,47 @@ struct MfmaQK {
 };
 using MfmaQ4K = MfmaQK<false>;
 using MfmaQ5K = MfmaQK<true>;
+
+// IQ4_XS (GGML block_iq4_xs, 136 bytes; gguf_block.rs:183-316 "iq4_xs"): a
+// task is one super-block; lane quarter q decodes sub-blocks 2q and 2q + 1,
+// laid out as Q4_0 blocks (MFMA j: code dword j & 3 of sub-block 2q + (j >> 2),
+// low nibbles run0, high nibbles run1), each index looked up in the codebook
+// (iq4nl_lookup) and decoded as Q8_0's codes: B = RNE_f16(kv·(ls - 32)), the
+// super-block's d multiplied per weight row in f32 (ROWSCALE).  The window:
+// pieces 0..7 hold bytes [0, 128), piece 8 bytes [120, 136) at LDS
+// [128, 144), so window dwords 32 and 33 sit at LDS dwords 34 and 35.
+struct MfmaIQ4XS {
+    static constexpr int KT = 256, NM = 8, PF = 4, TPI = 2;
+    static constexpr uint32_t UNIT = 256, UPT = 1, UB = 136;
+    static constexpr uint32_t TB = UB;
+    static constexpr uint32_t NP = 9, WB = 144;
+    static constexpr bool ROWSCALE = true, MLX = false, PAIR4 = false, BIAS = false;
+    static constexpr uint32_t STAGE = 8;
+    __device__ static uint32_t goff(uint32_t piece, uint32_t) { return piece < 8u ? 16u * piece : 120u; }
+    __device__ static uint32_t run0(uint32_t q, uint32_t j) { return 64u * q + 32u * (j >> 2) + 4u * (j & 3u); }
+    __device__ static uint32_t run1(uint32_t q, uint32_t j) { return run0(q, j) + 16u; }
+    __device__ static void decode(const u32a* win, uint32_t, bool ok, uint32_t q, uint4 (&a)[NM], float& d) {
+        const uint32_t h0 = win[0], h1 = win[1];
+        d = ok ? f16_bits_to_f32(h0) : 0.0f;  // padding task: zero weights
+        const h2 o = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t ib = 2u * q + (uint32_t)h;
+            const _Float16 sv = (_Float16)((int)iq4xs_scale(h0 >> 16, h1, ib) - 32);  // exact
+            const h2 s2 = {sv, sv};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t k = 2u + 4u * ib + (uint32_t)j;  // window dword of the code dword
+                const uint32_t Q = win[k < 32u ? k : k + 2u];
+                const uint32_t L = iq4nl_lookup(Q & 0x0F0F0F0Fu), H = iq4nl_lookup((Q >> 4) & 0x0F0F0F0Fu);
+                a[4 * h + j] = make_uint4(__builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, and_or(L, 0x00FF00FFu, 0x64006400u)) + o) * s2),
+                                          __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, and_or(L >> 8, 0x00FF00FFu, 0x64006400u)) + o) * s2),
+                                          __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, and_or(H, 0x00FF00FFu, 0x64006400u)) + o) * s2),
+                                          __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, and_or(H >> 8, 0x00FF00FFu, 0x64006400u)) + o) * s2));
+            }
+        }
+    }
+};
 
 // MLX affine U4 (mlx_affine.rs:557-626, fixture.rs:307-311): a task is 256
 // weights of a row, 32 packed words (128 bytes, 16-byte aligned rows, so no
@@ -874,8 +915,9 @@ int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16, uint32_t min_tiles) {
 
 bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool y_bf16,
                        uint32_t group) {
-    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K && enc != ENC_Q4_K && enc != ENC_Q5_K && enc != ENC_MLX_U4) || batch < 3 ||
-        batch > 16 || K % 256u)
+    if ((enc != ENC_Q4_0 && enc != ENC_Q6_K && enc != ENC_Q4_K && enc != ENC_Q5_K && enc != ENC_IQ4_XS &&
+         enc != ENC_MLX_U4) ||
+        batch < 3 || batch > 16 || K % 256u)
         return false;
     if (enc == ENC_MLX_U4 && (group == 0 || group % 32u)) return false;
     uint32_t tiles = 0;
@@ -897,6 +939,7 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
                                    : enc == ENC_Q6_K ? K / 256u * 210u
                                    : enc == ENC_Q4_K ? K / 256u * 144u
                                    : enc == ENC_Q5_K ? K / 256u * 176u
+                                   : enc == ENC_IQ4_XS ? K / 256u * 136u
                                                      : K / 2u);
     if (batch < 5 && tiles < kMfmaSplitTiles) return false;
     if (batch <= max_register_batch(enc) && bytes < (8ull << 20) && tiles < kMfmaSplitTiles) return false;
@@ -905,6 +948,7 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
                    : enc == ENC_Q6_K   ? mfma_mode<MfmaQ6K>(K, tiles, y_bf16, min_tiles)
                    : enc == ENC_Q4_K   ? mfma_mode<MfmaQ4K>(K, tiles, y_bf16, min_tiles)
                    : enc == ENC_Q5_K   ? mfma_mode<MfmaQ5K>(K, tiles, y_bf16, min_tiles)
+                   : enc == ENC_IQ4_XS ? mfma_mode<MfmaIQ4XS>(K, tiles, y_bf16, min_tiles)
                                        : mfma_mode<MfmaMlxU4>(K, tiles, y_bf16, min_tiles);
     return mode != 0;
 }
@@ -916,6 +960,8 @@ hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, u
     if (enc == ENC_Q6_K) return launch_mfma<MfmaQ6K>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     if (enc == ENC_Q4_K) return launch_mfma<MfmaQ4K>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     if (enc == ENC_Q5_K) return launch_mfma<MfmaQ5K>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
+    if (enc == ENC_IQ4_XS)
+        return launch_mfma<MfmaIQ4XS>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     if (enc == ENC_MLX_U4) return launch_mfma<MfmaMlxU4>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
     return hipErrorInvalidValue;
 }

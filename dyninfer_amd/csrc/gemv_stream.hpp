@@ -110,6 +110,21 @@ struct StreamLane<EncQ5K> {  // lane offset = its super-block's; step i = lane b
     }
 };
 
+template <>
+struct StreamLane<EncIQ4XS> {  // lane offset = its super-block's; sub-block ib = lane bits 2..0
+    uint32_t off, oq;
+    __device__ __forceinline__ void init(uint32_t bsh, uint32_t lane_off, uint32_t ib) {
+        off = bsh + lane_off;  // the base is 4-byte aligned (bsh = 0)
+        oq = off + 8u + 16u * ib;
+    }
+    __device__ __forceinline__ EncIQ4XS::Raw load(const uint8_t* sb) const {
+        EncIQ4XS::Raw r;
+        load_dwords<2>(reinterpret_cast<const uint32_t*>(sb + off), r.h);
+        load_dwords<EncIQ4XS::NT>(reinterpret_cast<const uint32_t*>(sb + oq), r.q);
+        return r;
+    }
+};
+
 // f(integral_constant<int, i>) for i = 0..N-1, unrolled.
 template <class F, int... I>
 __device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I...>) {
@@ -198,7 +213,10 @@ __global__ __launch_bounds__(TH) void gguf_gemv_stream_kernel(const GemvParams p
     const uint32_t bsh = (uint32_t)((uintptr_t)w & 3u);
     const uint8_t* abase = w - bsh;  // 4-byte aligned
     StreamLane<E> sl;
-    if constexpr (wide_chunks(E::ENC)) sl.init(bsh, g * rowbytes + (j >> 2) * (uint32_t)E::BB, j & 3u);
+    // lane j's chunk: block j / CPB, part j % CPB (CPB chunks per block; L is a
+    // multiple of CPB, so every chunk round keeps the part)
+    constexpr uint32_t CPB = (uint32_t)(E::QK / E::CW);
+    if constexpr (CPB > 1) sl.init(bsh, g * rowbytes + (j / CPB) * (uint32_t)E::BB, j % CPB);
     else sl.init(bsh, g * rowbytes + j * (uint32_t)E::BB);
     // first row of row step k (the last step ends at the weight's last row)
     auto row0 = [&](uint32_t k) {

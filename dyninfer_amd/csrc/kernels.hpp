@@ -87,7 +87,7 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
                        bool x_bf16, uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype,
                        hipStream_t stream);
 
-// Decode GEMV on MFMA for 3..16 activation rows (Q4_0, Q6_K, Q4_K, Q5_K, MLX U4; K a
+// Decode GEMV on MFMA for 3..16 activation rows (Q4_0, Q6_K, Q4_K, Q5_K, IQ4_XS, MLX U4; K a
 // multiple of 256): whether it serves a call, and the launch (several
 // launches when K needs more than one LDS segment; f32 outputs only then).
 bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool y_bf16,

@@ -76,12 +76,13 @@ Value candidate(const std::string& codec, const char* op_kind, const char* op_su
 const std::string& candidates_json() {
     static const std::string s = [] {
         Value all = Value::array();
-        // gguf.q4_k and gguf.q5_k are schema-only encodings in the reference
+        // gguf.q4_k, gguf.q5_k and gguf.iq4_xs are schema-only encodings in the reference
         // (gguf_block.rs:183-316): these entries give them their first kernels, decoding
-        // GGML's block_q4_K / block_q5_K.
+        // GGML's block_q4_K / block_q5_K / block_iq4_xs.
         struct G { const char* codec; long long block; bool gemm; };  // gemm: a prefill GEMM exists
         const G gguf[] = {{"gguf.q4_0", 32, true}, {"gguf.q4_1", 32, true}, {"gguf.q8_0", 32, true},
-                          {"gguf.q6_k", 256, true}, {"gguf.q4_k", 256, true}, {"gguf.q5_k", 256, true}};
+                          {"gguf.q6_k", 256, true}, {"gguf.q4_k", 256, true}, {"gguf.q5_k", 256, true},
+                          {"gguf.iq4_xs", 256, true}};
         for (const G& g : gguf) {
             const bool gemm = g.gemm;
             const std::string n = std::string("Consumes official GGML ") + g.codec +

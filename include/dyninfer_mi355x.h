@@ -58,6 +58,8 @@ enum {
                                     (gguf_block.rs:183-316), decoded here as GGML dequantize_row_q4_K */
     DYNINFER_ENC_GGUF_Q5_K = 13, /* GGML's 176-byte super-block (schema only in the reference),
                                     decoded as GGML dequantize_row_q5_K */
+    DYNINFER_ENC_GGUF_IQ4_XS = 23, /* GGML's 136-byte super-block with the kvalues_iq4nl codebook
+                                      (schema only in the reference), as dequantize_row_iq4_xs */
     DYNINFER_ENC_MLX_AFFINE_U4 = 0x1004
 };
 
@@ -71,7 +73,7 @@ enum { DYNINFER_DTYPE_F32 = 0, DYNINFER_DTYPE_F16 = 1, DYNINFER_DTYPE_BF16 = 2 }
  * GGUF (PhysicalEncoding::BlockQuantized, crates/dyninfer-checkpoint-gguf/src/convention.rs:200-279):
  *   `data` = the tensor's interleaved blocks, N*(K/B)*bytes_per_block bytes; row o, block b
  *   starts at byte (o*K/B + b)*bytes_per_block (gguf_codegen.rs:350-367).  `data` must be
- *   2-byte aligned (4-byte for Q4_1, Q4_K and Q5_K).  scales/biases/group_size/scale_dtype are ignored.
+ *   2-byte aligned (4-byte for Q4_1, Q4_K, Q5_K and IQ4_XS).  scales/biases/group_size/scale_dtype are ignored.
  * MLX affine U4 (PhysicalEncoding::GroupQuantized, crates/dyninfer-checkpoint-safetensors/src/mlx.rs:152-261):
  *   `data` = packed u32 [N, K/8] (lane i = bits 4i..4i+3), `scales`, `biases` = [N, K/group_size]
  *   of `scale_dtype` (f32/f16/bf16), each aligned to its element size.
@@ -118,12 +120,13 @@ const char* dyninfer_mi355x_last_error(void);
  * gguf_codegen.rs:157-159).  `rows` = activation rows (1..16 for decode; any for prefill).
  * x: [rows, K] row-major, 16-byte aligned, dtype x_dtype (f32 or bf16, every encoding);
  * y: [rows, N], dtype y_dtype (f32 or bf16).
- *   rows <= 16: the decode GEMV kernels (HBM-bound; 5..16 rows of large Q4_0, Q6_K, Q4_K
- *     and MLX weights on MFMA), activations rounded to f16 after a power-of-two scaling
- *     per scale group;
+ *   rows <= 16: the decode GEMV kernels (HBM-bound; 5..16 rows of large Q4_0, Q6_K, Q4_K,
+ *     Q5_K, IQ4_XS and MLX weights on MFMA), activations rounded to f16 after a
+ *     power-of-two scaling per scale group;
  *   rows >= 17: the prefill path.  Q4_1, Q8_0 and MLX U4 from 17 rows, Q4_0, Q6_K and
- *     Q4_K from 33 rows, or from 17 when K > 8192 (below that two 16-row MFMA GEMV
- *     chunks are mostly faster), K a multiple of 64 (256 for Q6_K and Q4_K): x is staged once per call as f16 MFMA operand fragments,
+ *     the K-quants / IQ4_XS from 33 rows, or from 17 when K > 8192 (below that two 16-row
+ *     MFMA GEMV chunks are mostly faster), K a multiple of 64 (256 for the super-block
+ *     encodings): x is staged once per call as f16 MFMA operand fragments,
  *     each row scaled by a power of two (RNE) and the rows padded with zeros to a
  *     multiple of 32; then one MFMA GEMM per weight decodes the GGUF blocks or MLX words
  *     straight into MFMA operands.  The staging
@@ -137,8 +140,8 @@ const char* dyninfer_mi355x_last_error(void);
  *     then does on every replay (the no-allocation variant below avoids that).
  *     A stream that is destroyed while the context lives must have finished its work
  *     first (its handle may be reused by a new stream).  Every other case (K not a
- *     multiple of 64, Q4_0, Q6_K and Q4_K at 17..32 rows with K <= 8192) runs the GEMV
- *     kernels over 16-row chunks and needs no workspace.
+ *     multiple of 64, Q4_0, Q6_K, Q4_K, Q5_K and IQ4_XS at 17..32 rows with K <= 8192)
+ *     runs the GEMV kernels over 16-row chunks and needs no workspace.
  * Error bound: |y - y_exact| <= 2^-10 * sum_k |w||x| plus f32 accumulation, where a
  * prefill activation more than 2^29 below its row's largest magnitude may also be
  * flushed to f16 subnormals (absolute 2^-40 * max|x| each).
@@ -237,7 +240,7 @@ int dyninfer_mi355x_gguf_find(const dyninfer_gguf_t* g, const char* name, dyninf
  * then waits for the copy (the source is pageable mapped memory).  */
 int dyninfer_mi355x_gguf_upload(const dyninfer_gguf_t* g, const char* name, void* dst, uint64_t dst_bytes,
                                 void* stream);
-/* Describes a rank-2 Q4_0/Q4_1/Q8_0/Q6_K/Q4_K/Q5_K tensor whose bytes are at device_data as a
+/* Describes a rank-2 Q4_0/Q4_1/Q8_0/Q6_K/Q4_K/Q5_K/IQ4_XS tensor whose bytes are at device_data as a
  * dyninfer_qweight_t (rows = dims[0], cols = dims[1]); other types are unsupported. */
 int dyninfer_mi355x_gguf_qweight(const dyninfer_gguf_t* g, const char* name, const void* device_data,
                                  dyninfer_qweight_t* out);

@@ -40,7 +40,7 @@ def test_nm_exports_are_c_linkage():
 
 def test_version_and_candidates_json():
     assert b"gfx950" in d.library().dyninfer_mi355x_version()
-    assert len(d.candidates()) == 35  # f32 and bf16-activation entries
+    assert len(d.candidates()) == 40  # f32 and bf16-activation entries
 
 
 def w(enc, rows=64, cols=256, data=0x1000, **kw):

@@ -154,7 +154,8 @@ def gguf_request(codec, n, k, op="linear", mode="decode"):
 
 
 @pytest.mark.parametrize("codec,block", [("gguf.q4_0", 32), ("gguf.q4_1", 32), ("gguf.q8_0", 32), ("gguf.q6_k", 256),
-                                         ("gguf.q4_k", 256), ("gguf.q5_k", 256), ("mlx.affine.u4", 32)])
+                                         ("gguf.q4_k", 256), ("gguf.q5_k", 256), ("gguf.iq4_xs", 256),
+                                         ("mlx.affine.u4", 32)])
 @pytest.mark.parametrize("op,suffix", [("linear", "matmul"), ("output_projection", "output")])
 @pytest.mark.parametrize("mode", ["decode", "prefill"])
 def test_mi355x_entry_wins_on_gfx950(codec, block, op, suffix, mode):
@@ -209,13 +210,14 @@ def test_axis_not_divisible_rejects():
 @pytest.mark.parametrize("codec,block,suffix", [("gguf.q4_0", 32, "gather"), ("gguf.q4_1", 32, "gather"),
                                                 ("gguf.q8_0", 32, "gather"), ("gguf.q6_k", 256, "gather"),
                                                 ("gguf.q4_k", 256, "gather"), ("gguf.q5_k", 256, "gather"),
+                                                ("gguf.iq4_xs", 256, "gather"),
                                                 ("mlx.affine.u4", 32, "embedding")])
 def test_embedding_selects_mi355x_gather_on_gfx950(codec, block, suffix):
     req = gguf_request(codec, 151936, 4 * block, op="embedding", mode="prefill")
     sel = d.registry_require(req, hip("gfx950"), full_registry())
     assert sel["descriptor"]["id"] == f"{codec}.{suffix}.mi355x_hip" and sel["score"] == 1400
     rep = d.registry_select(req, hip("gfx1151"), full_registry())
-    if codec in ("gguf.q4_k", "gguf.q5_k"):  # schema-only in the reference: no other kernel exists
+    if codec in ("gguf.q4_k", "gguf.q5_k", "gguf.iq4_xs"):  # schema-only in the reference: no other kernel
         assert "selected" not in rep
     else:
         assert rep["selected"]["descriptor"]["id"] in (f"{codec}.gather.iree_block_hip",
@@ -234,7 +236,7 @@ def test_candidates_match_the_serde_schema():
     keys = {"id", "operation", "encoding", "input_types", "output_types", "accumulator_types", "shape",
             "orientations", "target", "modes", "lowering", "deterministic_score", "readiness", "notes"}
     cands = d.candidates()
-    assert len(cands) == 35 and len({c["id"] for c in cands}) == 35
+    assert len(cands) == 40 and len({c["id"] for c in cands}) == 40
     for c in cands:
         assert set(c) == keys
         assert c["operation"] in ("embedding", "linear", "output_projection")
