@@ -56,6 +56,9 @@ def gguf_tensor(torch, d, enc: int, n: int, k: int, gen):
         if enc == d.ENC_Q4_1:
             m = (torch.randn(nblk, device=dev, generator=gen) * 0.01).half().view(torch.uint8).view(nblk, 2)
             blocks[:, 2:4] = m
+        elif enc in (d.ENC_Q4_K, d.ENC_Q5_K):  # dmin = |N(0,1)|*0.005; scale bytes, high bits, codes uniform
+            m = (torch.randn(nblk, device=dev, generator=gen).abs() * 0.005).half().view(torch.uint8).view(nblk, 2)
+            blocks[:, 2:4] = m
         elif enc == d.ENC_Q8_0:
             q = torch.randint(-127, 128, (nblk, 32), dtype=torch.int16, device=dev, generator=gen)
             blocks[:, 2:34] = q.to(torch.int8).view(torch.uint8)
@@ -114,6 +117,25 @@ def gguf_step_8b(torch, d, gen) -> StepSet:
               "h", ["gate", "up"])
         s.add("down.gguf.q6_k", [gguf_tensor(torch, d, d.ENC_Q6_K, h, f, gen)], "act", ["down"])
     s.add("lm_head.gguf.q6_k", [gguf_tensor(torch, d, d.ENC_Q6_K, c["vocab"], h, gen)], "h", ["logits"])
+    return s
+
+
+def gguf_step_8b_q4_k_m(torch, d, gen) -> StepSet:
+    """Qwen3-8B in llama.cpp's Q4_K_M mix: Q4_K weights, Q6_K for attn_v, every
+    other ffn_down and the lm_head (the 'more bits' tensors of that recipe)."""
+    c = QWEN8
+    s = StepSet("qwen3-8b gguf q4_k_m")
+    h, q, kv, f = c["hidden"], c["q"], c["kv"], c["ffn"]
+    K4, K6 = d.ENC_Q4_K, d.ENC_Q6_K
+    for layer in range(c["layers"]):
+        s.add("qk.gguf.q4_k", [gguf_tensor(torch, d, K4, q, h, gen), gguf_tensor(torch, d, K4, kv, h, gen)], "h", ["q", "k"])
+        s.add("v.gguf.q6_k", [gguf_tensor(torch, d, K6, kv, h, gen)], "h", ["v"])
+        s.add("o.gguf.q4_k", [gguf_tensor(torch, d, K4, h, q, gen)], "attn", ["o"])
+        s.add("gate_up.gguf.q4_k", [gguf_tensor(torch, d, K4, f, h, gen), gguf_tensor(torch, d, K4, f, h, gen)], "h",
+              ["gate", "up"])
+        down = K6 if layer % 2 == 0 else K4
+        s.add(f"down.{d.ENCODING_IDS[down]}", [gguf_tensor(torch, d, down, h, f, gen)], "act", ["down"])
+    s.add("lm_head.gguf.q6_k", [gguf_tensor(torch, d, K6, c["vocab"], h, gen)], "h", ["logits"])
     return s
 
 
@@ -457,6 +479,21 @@ def main() -> int:
                                "breakdown": breakdown_of(r.label_times(reps=5))}
             del r
         extra["config4_qwen3_8b_step"] = c4
+        log("Qwen3-8B Q4_K_M step ...")
+        sk = gguf_step_8b_q4_k_m(torch, d, gen)
+        ck = {"weight_bytes_per_step": sk.weight_bytes}
+        for b in (1, 4, 16):
+            r = StepRunner(torch, d, ctx, sk, b, torch.float32, torch.float32)
+            g = r.capture()
+            msk = r.time_graph(g, max(5, args.steps // 5), 2)
+            del g
+            ck[f"batch{b}"] = {"us_per_step": round(msk * 1e3, 1), "weight_GBps": round(sk.weight_bytes / msk / 1e6, 1),
+                               "hbm_frac": round(sk.weight_bytes / msk / 1e6 / HBM_PEAK_GBS, 4),
+                               "tokens_per_s": round(b / (msk * 1e-3), 1),
+                               "breakdown": breakdown_of(r.label_times(reps=5))}
+            del r
+        extra["qwen3_8b_q4_k_m_step"] = ck
+        del sk
         log("config 1 (Qwen3-0.6B mixed GGUF step) ...")
         s1 = gguf_step_06b(torch, d, gen)
         c1 = {"weight_bytes_per_step": s1.weight_bytes}
@@ -501,7 +538,8 @@ def main() -> int:
         extra["config3_other_encodings_gemm"] = {
             f"{name}_M512_N{n}_K{k}_xbf16": {kk: round(v, 4) for kk, v in
                                              bench_gemm(torch, d, ctx, 512, n, k, torch.bfloat16, enc=enc).items()}
-            for name, enc in (("q4_1", d.ENC_Q4_1), ("q8_0", d.ENC_Q8_0), ("q6_k", d.ENC_Q6_K))
+            for name, enc in (("q4_1", d.ENC_Q4_1), ("q8_0", d.ENC_Q8_0), ("q6_k", d.ENC_Q6_K), ("q4_k", d.ENC_Q4_K),
+                              ("q5_k", d.ENC_Q5_K), ("iq4_xs", d.ENC_IQ4_XS))
             for (n, k) in [(3072, 1024), (1024, 3072)]}
         g512 = c3["M512_N3072_K1024_xbf16"]
         extra["config3_roofline"] = {"bound": "mfma", "kernel": "xprep + gemm (Q4_0), M512 N3072 K1024, bf16 X",
