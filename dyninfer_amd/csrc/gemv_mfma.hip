@@ -339,10 +339,10 @@ struct MfmaMlxU4 {
     }
 };
 
-// LDS: activations [task][j][64 lanes] x 16 bytes, the inverse scales
-// [task][16 rows] f32, for BIAS encodings the activation sums [task][16
-// rows][4 quarters] as f16 pairs, then each wave's window of 16 rows x WB
-// bytes.  Tasks
+// LDS (real tasks only): activations [task][j][64 lanes] x 16 bytes, the
+// inverse scales [task][16 rows] f32, for BIAS encodings the activation sums
+// [task][16 rows][4 quarters] as f16 pairs, then each wave's window of 16 rows
+// x WB bytes.  Tasks
 // of a segment are padded to a multiple of PF (the padding tasks have zero
 // weights and activations).
 // Split mode (few tiles): the 8 waves of a workgroup share each tile, wave w
@@ -356,9 +356,11 @@ template <class M>
 __host__ __device__ constexpr uint32_t mfma_task_lds() {
     return M::NM * 64u * 16u + 64u + (M::BIAS ? 256u : 0u);
 }
+// LDS of a segment of nunit units: the real tasks only (padding tasks are
+// neither staged nor multiplied), then the windows.
 template <class M, bool SPLIT>
 __host__ __device__ constexpr uint32_t mfma_lds_bytes(uint32_t nunit) {
-    return mfma_tasks<M, SPLIT>(nunit) * mfma_task_lds<M>() + (kMfmaThreads / 64u) * 16u * M::WB;
+    return (nunit + M::UPT - 1u) / M::UPT * mfma_task_lds<M>() + (kMfmaThreads / 64u) * 16u * M::WB;
 }
 
 // Slot of A-operand lane l (row b = l % 16, quarter q = l / 16) in the 64
@@ -385,9 +387,9 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint4* xl = reinterpret_cast<uint4*>(lds);
-    float* inv = reinterpret_cast<float*>(lds + ng * NM * 64u * 16u);
-    uint32_t* xs = reinterpret_cast<uint32_t*>(lds + ng * (NM * 64u * 16u + 64u));  // BIAS: activation sums
-    uint8_t* wins = lds + ng * mfma_task_lds<M>();      // the waves' windows
+    float* inv = reinterpret_cast<float*>(lds + nt * NM * 64u * 16u);
+    uint32_t* xs = reinterpret_cast<uint32_t*>(lds + nt * (NM * 64u * 16u + 64u));  // BIAS: activation sums
+    uint8_t* wins = lds + nt * mfma_task_lds<M>();      // the waves' windows
     uint8_t* win = wins + wv * 16u * M::WB;             // this wave's window
 
     // ---- weight tiles.  Whole tiles per wave: wave wid takes tiles wid,
@@ -779,7 +781,8 @@ namespace {
 // below kMfmaSplitTiles 16-row tiles the eight waves of a workgroup share
 // each tile (split mode: 4096x12288 Q6_K 41 / 57 / 80 us, 4096x4096 Q4_0
 // 11.7 / 15.3 / 22.7 us, q/k/v 13.9 / 15.9 / 32.8 us) when a segment has at
-// least 8 tasks (one per wave); otherwise a wave takes whole tiles, which
+// least 4 tasks (Qwen3-0.6B MLX q/k/v, K = 1024, at 16 rows: 8.6 us split,
+// 11.5 us with one wave per tile running all four); otherwise a wave takes whole tiles, which
 // pays from kMfmaMinTiles tiles on (each workgroup stages all activations, a
 // few microseconds, before its first product: lm_head 124 us whole tiles,
 // 148 us split, 690 us VALU).
@@ -905,7 +908,7 @@ int mfma_mode(uint32_t K, uint32_t tiles, bool y_bf16, uint32_t min_tiles) {
     const uint32_t units = K / M::UNIT;
     if (tiles < kMfmaSplitTiles) {
         const uint32_t seg = mfma_segment<M, true>(units);
-        if (seg / M::UPT >= 8u && (!y_bf16 || seg == units)) return 2;
+        if (seg / M::UPT >= 4u && (!y_bf16 || seg == units)) return 2;
     }
     const uint32_t seg = mfma_segment<M, false>(units);
     return tiles >= min_tiles && seg > 0 && (!y_bf16 || seg == units) ? 1 : 0;
