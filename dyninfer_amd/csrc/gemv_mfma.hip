@@ -77,6 +77,7 @@ struct MfmaParams {
     void* y[kMaxProblems];
     const uint8_t* sc[kMaxProblems];  // MLX scales
     const uint8_t* bi[kMaxProblems];  // MLX biases
+    uint32_t split_ws_log2;           // split mode: log2 of the waves per tile (3, or 2: two tiles per workgroup)
 };
 
 // (c + off)·s for a packed pair (v_pk_add_f16, v_pk_mul_f16)
@@ -345,11 +346,12 @@ struct MfmaMlxU4 {
 // x WB bytes.  Tasks
 // of a segment are padded to a multiple of PF (the padding tasks have zero
 // weights and activations).
-// Split mode (few tiles): the 8 waves of a workgroup share each tile, wave w
-// taking tasks [w·T/8, (w+1)·T/8) with a ring of 2, so T is a multiple of 16.
+// Split mode (few tiles): the ws = 8 (or 4) waves of a group share each tile,
+// wave w of the group taking tasks [w·T/ws, (w+1)·T/ws) with a ring of 2, so
+// T is a multiple of 2·ws.
 template <class M, bool SPLIT>
-__host__ __device__ constexpr uint32_t mfma_tasks(uint32_t nunit) {
-    constexpr uint32_t pad = SPLIT ? 16u : (uint32_t)M::PF;
+__host__ __device__ constexpr uint32_t mfma_tasks(uint32_t nunit, uint32_t ws) {
+    const uint32_t pad = SPLIT ? 2u * ws : (uint32_t)M::PF;
     return ((nunit + M::UPT - 1u) / M::UPT + pad - 1u) / pad * pad;
 }
 template <class M>
@@ -383,7 +385,8 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     const uint32_t sidx = p.nseg > 1u ? blockIdx.x / p.grid : 0u, bid = blockIdx.x - sidx * p.grid;
     const uint32_t k0 = p.k0 + sidx * p.seg_units * M::UNIT;
     const uint32_t nunit = p.nunit - sidx * p.seg_units < p.seg_units ? p.nunit - sidx * p.seg_units : p.seg_units;
-    const uint32_t ng = mfma_tasks<M, SPLIT>(nunit), nt = nunit / M::UPT;  // tasks with padding, without
+    const uint32_t wsl = SPLIT ? p.split_ws_log2 : 0u, ws = 1u << wsl;  // waves per tile in split mode
+    const uint32_t ng = mfma_tasks<M, SPLIT>(nunit, ws), nt = nunit / M::UPT;  // tasks with padding, without
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint4* xl = reinterpret_cast<uint4*>(lds);
@@ -395,13 +398,19 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     // ---- weight tiles.  Whole tiles per wave: wave wid takes tiles wid,
     // wid + W, ..., waves numbered across workgroups first (wave i of
     // workgroup w is wid = i·grid + w), so a few tiles still spread over all
-    // CUs.  Split mode: workgroup w takes tiles w, w + grid, ... and its waves
-    // split each tile's tasks (wave v: tasks t0 = v·tpw .. t0 + tpw - 1).
-    const uint32_t wid = SPLIT ? bid : __builtin_amdgcn_readfirstlane(wv * p.grid + bid);
-    const uint32_t W = SPLIT ? p.grid : p.grid * NW;
-    const uint32_t tpw = SPLIT ? ng / NW : ng, t0 = SPLIT ? wv * tpw : 0u;
+    // CUs.  Split mode: the workgroup's waves form NW/ws groups of ws; group gi
+    // of workgroup w takes tiles w + gi·grid, ... (groups across workgroups
+    // first), and its waves split each tile's tasks (wave v of the group:
+    // tasks t0 = v·tpw .. t0 + tpw - 1).  Every wave of a workgroup runs the
+    // tile count of its group 0 (the most), so all pass the same barriers;
+    // a group past its own tiles recomputes its last one and stores nothing.
+    const uint32_t gi = SPLIT ? wv >> wsl : 0u, wg = SPLIT ? wv & (ws - 1u) : wv;
+    const uint32_t wid = SPLIT ? bid + gi * p.grid : __builtin_amdgcn_readfirstlane(wv * p.grid + bid);
+    const uint32_t W = SPLIT ? p.grid * (NW >> wsl) : p.grid * NW;
+    const uint32_t tpw = SPLIT ? ng >> wsl : ng, t0 = SPLIT ? wg * tpw : 0u;
     const uint32_t m = lane & 15u, q = lane >> 4;
     const uint32_t ntw = wid < p.total_tiles ? (p.total_tiles - wid + W - 1u) / W : 0u;  // tiles of this wave
+    const uint32_t nloop = SPLIT ? (bid < p.total_tiles ? (p.total_tiles - bid + W - 1u) / W : 0u) : ntw;
     const uint32_t rowbytes = (p.K / M::UNIT) * M::UB, seg0 = (k0 / M::UNIT) * M::UB;
 
     // the wave's i-th tile (past the end: its last, or any tile for a wave
@@ -732,22 +741,31 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
             }
         }
     };
-    for (uint32_t i = 0; i < ntw; i++) {
+    for (uint32_t i = 0; i < nloop; i++) {
         const Where wnxt = where(tile_at(i + 1u));
         const Rows rnxt = rows_of(wnxt);
-        const bool last = i + 1u == ntw;
+        const bool last = i + 1u == nloop;
         const uint32_t gend = last ? tpw - PF : tpw;  // rounds that reload
         for (uint32_t g0 = 0; g0 < gend; g0 += PF) round(g0, rnxt, std::true_type{});
         if (last) round(tpw - PF, rnxt, std::false_type{});
         if constexpr (SPLIT) {
             // the waves' partial tiles meet in their windows (a wave's last
-            // window reads precede these writes: in order); wave 0 adds and
-            // stores, then every window may be refilled
+            // window reads precede these writes: in order); wave 0 of each
+            // group adds its group's and stores, then every window may be refilled
             *reinterpret_cast<f32x4*>(win + 16u * lane) = acc;
             __syncthreads();
-            if (wv == 0u) {
+            auto add_group = [&](auto wsc) {  // the group's other windows, all reads issued together
+                constexpr uint32_t G = decltype(wsc)::value;
+                f32x4 part[G - 1];
 #pragma unroll
-                for (uint32_t v = 1; v < NW; v++) acc += *reinterpret_cast<const f32x4*>(wins + v * 16u * M::WB + 16u * lane);
+                for (uint32_t v = 1; v < G; v++)
+                    part[v - 1] = *reinterpret_cast<const f32x4*>(wins + (wv + v) * 16u * M::WB + 16u * lane);
+#pragma unroll
+                for (uint32_t v = 1; v < G; v++) acc += part[v - 1];
+            };
+            if (wg == 0u) {
+                if (wsl == 3u) add_group(std::integral_constant<uint32_t, 8>{});
+                else add_group(std::integral_constant<uint32_t, 4>{});
             }
         }
         // lane l holds weight row l % 16 of activation rows 4q..4q+3
@@ -755,7 +773,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const uint32_t b = 4u * q + (uint32_t)c;
-            if ((!SPLIT || wv == 0u) && b < p.batch && row < wcur.n) {
+            if ((!SPLIT || wg == 0u) && i < ntw && b < p.batch && row < wcur.n) {
                 const size_t idx = (size_t)b * wcur.n + row;
                 if constexpr (YBF16) gptr_mut<uint16_t>(wcur.y)[idx] = f32_to_bf16_bits(acc[c]);
                 else if (p.accumulate) {  // later K segments
@@ -847,6 +865,15 @@ hipError_t launch_mode(MfmaParams p, uint32_t units, bool y_bf16, hipStream_t st
     const uint64_t cap = (uint64_t)per_cu * cus;
     p.grid = (uint32_t)(p.total_tiles < cap ? p.total_tiles : cap);
     if (shared_tiles) p.grid = (p.total_tiles + nseg - 1u) / nseg;  // about nseg tiles per workgroup
+    // Split mode with more tiles than resident workgroups (one segment): two
+    // groups of 4 waves per workgroup, each on its own tile, so the tiles take
+    // one round instead of two (Qwen3-0.6B MLX gate/up, 384 tiles at ~161
+    // VGPRs: one 8-wave workgroup per CU).
+    p.split_ws_log2 = 3u;
+    if (SPLIT && nseg == 1u && p.total_tiles > cap && p.total_tiles <= 2u * cap) {
+        p.split_ws_log2 = 2u;
+        p.grid = (p.total_tiles + 1u) / 2u;
+    }
     p.k0 = 0;
     p.nunit = units;
     p.seg_units = seg;

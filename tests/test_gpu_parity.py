@@ -165,6 +165,10 @@ MFMA_CASES = [
     (oracle.Q6_K, 17000, 1024, 4, False, 0), (oracle.Q4_0, 20480, 1024, 3, True, 2),
     # more rows than one VALU register pass: whole tiles from 128 tiles
     (oracle.Q4_0, 2048, 1024, 12, False, 0), (oracle.Q6_K, 2570, 1024, 8, True, 2),
+    # split mode, more tiles than resident workgroups: two 4-wave tile groups per
+    # workgroup (an odd tile count leaves one group a recomputed, unstored tile)
+    (oracle.Q4_0, 6160, 1024, 16, False, 0), (oracle.Q6_K, 6160, 1024, 16, True, 2),
+    (oracle.Q4_0, 4104, 2048, 16, True, 0),
 ]
 
 
@@ -277,7 +281,8 @@ MLX_MFMA_CASES = [
     (1024, 3072, 64, oracle.D_F16, 12, True), (3072, 2048, 32, oracle.D_F32, 16, True),
     (2048, 4096, 128, oracle.D_BF16, 9, False), (4100, 2048, 64, oracle.D_BF16, 9, False),
     (20000, 1024, 64, oracle.D_BF16, 4, True),
-    (4096, 1024, 64, oracle.D_BF16, 16, True),  # 256 tiles, whole tiles (two VALU passes at 16 rows)
+    (4096, 1024, 64, oracle.D_BF16, 16, True),  # 256 tiles, split (two VALU passes at 16 rows)
+    (6160, 1024, 64, oracle.D_BF16, 16, True),  # 385 tiles: two 4-wave tile groups per workgroup
 ]
 
 
