@@ -51,6 +51,23 @@ def test_noalloc_matches_qlinear_multi_on_consecutive_calls(ctx):
             assert oracle.normalized_error(g, y64, absdot) <= F16X2
 
 
+@pytest.mark.parametrize("gtype", [oracle.Q4_K, oracle.Q5_K, oracle.IQ4_XS], ids=oracle.NAMES.get)
+def test_noalloc_super_block_encodings(ctx, gtype):
+    """The GGML super-block encodings through the no-allocation entry point:
+    a prefill (the GEMM, staging in the scratch array) then a decode call."""
+    enc = {oracle.Q4_K: d.ENC_Q4_K, oracle.Q5_K: d.ENC_Q5_K, oracle.IQ4_XS: d.ENC_IQ4_XS}[gtype]
+    k, shapes = 1024, [512, 256]
+    datas = [oracle.synth_gguf(gtype, n, k, 30 + i) for i, n in enumerate(shapes)]
+    ws = [d.QWeight(enc, n, k, dev(x)) for n, x in zip(shapes, datas)]
+    for rows in (200, 8):
+        x = oracle.randn(rows * k, seed=rows + 5).reshape(rows, k)
+        ref, got = _both(ctx, ws, dev(x))
+        for r, g in zip(ref, got):
+            assert np.array_equal(r.view(np.uint32), g.view(np.uint32)), rows
+        y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(gtype, datas[0], shapes[0], k))
+        assert oracle.normalized_error(got[0], y64, absdot) <= 2e-3
+
+
 def test_noalloc_decode_and_size_limit(ctx):
     k = 1024
     ws, _ = _weights(k, [384], seed=9)
