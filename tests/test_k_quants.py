@@ -319,3 +319,27 @@ def test_deterministic(ctx, kind):
     a = ctx.qlinear(w, x).cpu().numpy()
     for _ in range(3):
         assert np.array_equal(ctx.qlinear(w, x).cpu().numpy().view(np.uint32), a.view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("gtype", [oracle.Q4_K, oracle.Q5_K, oracle.IQ4_XS], ids=oracle.NAMES.get)
+def test_streaming_kernel_long_weight(ctx, gtype):
+    """One activation row over a 32768 x 4096 weight: enough row steps per wave
+    for the batch-1 streaming kernel (lanes per row 32 for the 64-weight
+    chunks, 64 for IQ4_XS).  Checked on 400 random rows, dequantised by the
+    oracle from their own bytes."""
+    n, k = 32768, 4096
+    enc = {oracle.Q4_K: d.ENC_Q4_K, oracle.Q5_K: d.ENC_Q5_K, oracle.IQ4_XS: d.ENC_IQ4_XS}[gtype]
+    bb = oracle.BLOCK[gtype][1]
+    data = oracle.synth_gguf(gtype, n, k, 17)
+    w = d.QWeight(enc, n, k, dev(data))
+    x = oracle.randn(k, seed=18).reshape(1, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    rows = np.sort(np.random.default_rng(19).choice(n, 400, replace=False))
+    rb = k // 256 * bb
+    sub = np.concatenate([data[r * rb:(r + 1) * rb] for r in rows])
+    wf = oracle.dequant_gguf(gtype, sub, len(rows), k)
+    y64, absdot = oracle.linear_f64(x, wf)
+    err = oracle.normalized_error(y[:, rows], y64, absdot)
+    assert err <= TOL and err <= 2.0 ** -11 + 2e-5, err
+
