@@ -148,6 +148,17 @@ def test_gemv(ctx, n, k, batch):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("n,k,batch", [(20000, 1024, 12), (17000, 2048, 16)])
+def test_gemv_mfma_whole_tiles(ctx, n, k, batch):
+    """At least 1024 tiles: the MFMA GEMV's whole-tile mode (a wave per tile)."""
+    w, data = weight(n, k, seed=n + batch)
+    x = oracle.randn(batch * k, seed=batch + 7).reshape(batch, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    err = err_of(y, x, oracle.dequant_gguf(IQ, data, n, k))
+    assert err <= TOL and err <= 2.0 ** -10 + 2e-5, err
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("batch", [1, 4, 16])
 def test_multi_and_bf16(ctx, batch):
     import torch
