@@ -343,3 +343,33 @@ def test_streaming_kernel_long_weight(ctx, gtype):
     err = oracle.normalized_error(y[:, rows], y64, absdot)
     assert err <= TOL and err <= 2.0 ** -11 + 2e-5, err
 
+
+@pytest.mark.gpu
+def test_gguf_file_mixed_super_blocks_upload_and_qlinear(ctx, tmp_path):
+    """A GGUF file in the spirit of a Q4_K_M checkpoint: Q4_K, Q5_K, IQ4_XS
+    and Q6_K tensors, indexed by path, each tensor's exact bytes uploaded and
+    multiplied through the QWeight the index describes."""
+    import torch
+    specs = {"blk.0.attn_q.weight": (oracle.Q4_K, 512, 1024), "blk.0.attn_v.weight": (oracle.Q6_K, 256, 1024),
+             "blk.0.ffn_down.weight": (oracle.Q5_K, 1024, 768), "blk.0.ffn_up.weight": (oracle.IQ4_XS, 768, 1024)}
+    raws = {name: oracle.synth_gguf(t, n, k, 40 + i) for i, (name, (t, n, k)) in enumerate(specs.items())}
+    body = b"GGUF" + struct.pack("<IQQ", 3, len(specs), 1) + _s("general.architecture") + struct.pack("<I", 8) + _s("qwen3")
+    data = b""
+    for name in sorted(specs):
+        t, n, k = specs[name]
+        data += b"\0" * ((32 - len(data) % 32) % 32)
+        body += _s(name) + struct.pack("<I", 2) + struct.pack("<QQ", k, n) + struct.pack("<IQ", t, len(data))
+        data += raws[name].tobytes()
+    body += b"\0" * ((32 - len(body) % 32) % 32)
+    path = tmp_path / "mixed.gguf"
+    path.write_bytes(body + data)
+    g = d.GgufFile(str(path))
+    for name, (t, n, k) in specs.items():
+        dev_bytes = g.upload(name)
+        assert torch.equal(dev_bytes.cpu(), torch.from_numpy(raws[name]))
+        w = g.qweight(name, dev_bytes)
+        x = oracle.randn(3 * k, seed=n).reshape(3, k)
+        y = ctx.qlinear(w, dev(x)).cpu().numpy()
+        err = err_of(y, x, oracle.dequant_gguf(t, raws[name], n, k))
+        assert err <= TOL and err <= 2.0 ** -11 + 2e-5, (name, err)
+
