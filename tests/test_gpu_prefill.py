@@ -261,6 +261,56 @@ def test_zero_point_rows(ctx, kind, rows):
         assert not np.any(y[:, :zr]), np.abs(y[:, :zr]).max()
 
 
+SUPER = {oracle.Q4_K: d.ENC_Q4_K, oracle.Q5_K: d.ENC_Q5_K, oracle.IQ4_XS: d.ENC_IQ4_XS}
+
+
+def _zero_rows_super_block(kind, n, k, seed):
+    """Weights whose first 64 rows dequantise to exactly 0 everywhere with
+    d != 0.  Q4_K / Q5_K: every code 0 and every sub-block min m = 0, keeping
+    the scales (GGML get_scale_min_k4: the mins are scale bytes 4..7 and the
+    high nibbles of bytes 8..11, block bytes 8..16).  IQ4_XS: every sub-block
+    scale ls = 32 (scales_h bits 0b10, scales_l nibbles 0), since its codebook
+    holds no zero."""
+    zr = 64
+    data = oracle.synth_gguf(kind, n, k, seed)
+    bw, bb = oracle.BLOCK[kind]
+    blk = data.reshape(n, k // bw, bb)
+    if kind == oracle.IQ4_XS:
+        blk[:zr, :, 2:4] = 0xAA
+        blk[:zr, :, 4:8] = 0
+        scale_max = 32.0  # |ls - 32|
+    else:
+        blk[:zr, :, 8:12] = 0
+        blk[:zr, :, 12:16] &= 0x0F
+        blk[:zr, :, 16:] = 0  # Q4_K qs; Q5_K qh then qs
+        scale_max = 63.0  # sc
+    wf = oracle.dequant_gguf(kind, data, n, k)
+    dbits = blk[:, :, 0].astype(np.uint16) | (blk[:, :, 1].astype(np.uint16) << 8)
+    dmax = (np.abs(dbits.view(np.float16).astype(np.float64)) * scale_max).max(axis=1)
+    assert not np.any(wf[:zr]) and np.all(dmax[:zr] > 0)
+    return d.QWeight(SUPER[kind], n, k, dev(data)), wf, zr, dmax
+
+
+@pytest.mark.parametrize("kind", list(SUPER), ids=oracle.NAMES.get)
+@pytest.mark.parametrize("rows", [1, 4, 16, 200])
+def test_zero_rows_super_block_encodings(ctx, kind, rows):
+    """Zero rows of the super-block encodings (see test_zero_point_rows): the
+    VALU GEMV leaves at most the same f32 residue, 2^-8 · sum_k |x_k| · max|d·sc|;
+    the prefill GEMM decodes exact zeros.  IQ4_XS's group scale d·(ls - 32) is
+    itself 0, so every path returns exactly 0."""
+    n, k = 6144, 1024
+    w, wf, zr, dmax = _zero_rows_super_block(kind, n, k, seed=rows + 23)
+    x = (oracle.randn(rows * k, seed=rows + 1) * 1000.0).reshape(rows, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    y64, absdot = oracle.linear_f64(x, wf)
+    assert oracle.normalized_error(y[:, zr:], y64[:, zr:], absdot[:, zr:]) <= 2e-3
+    bound = 2.0 ** -8 * np.abs(x).sum(axis=1, keepdims=True) * dmax[None, :zr]
+    print(f"zero-row residue / bound: {np.max(np.abs(y[:, :zr]) / bound):.3e}")
+    assert np.all(np.abs(y[:, :zr]) <= bound)
+    if kind == oracle.IQ4_XS or rows >= 33:
+        assert not np.any(y[:, :zr]), np.abs(y[:, :zr]).max()
+
+
 # ----------------------------------------------------------------- the prefill staging workspace
 def test_prefill_workspace_growth_across_calls_and_streams(ctx):
     """The context's staging workspace per stream: grown in stream order when a
