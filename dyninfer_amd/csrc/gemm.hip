@@ -150,7 +150,7 @@ template <>
 struct Blk<ENC_Q4_0> {
     // d (2 B) then 16 code bytes; byte j: k = j (low nibble), k = j + 16 (high).
     // Step t: code bytes 4t..4t+3 -> k = 4t+(0,2), 4t+(1,3), 16+4t+(0,2), 16+4t+(1,3).
-    static constexpr uint32_t kBytes = 18, kDw = 5, kLayout = XFRAG_NIB, kValuPerStep = 16;
+    static constexpr uint32_t kBytes = 18, kDw = 5, kLayout = XFRAG_NIB;
     struct Scale {
         h2 d;
         uint32_t sel;
@@ -173,7 +173,7 @@ template <>
 struct Blk<ENC_Q4_1> {
     // d, m (2 B each) then 16 code bytes (4-byte-aligned blocks): w = q·d + m;
     // k order as Q4_0.
-    static constexpr uint32_t kBytes = 20, kDw = 5, kLayout = XFRAG_NIB, kValuPerStep = 16;
+    static constexpr uint32_t kBytes = 20, kDw = 5, kLayout = XFRAG_NIB;
     struct Scale {
         h2 d, m;
     };
@@ -200,7 +200,7 @@ struct Blk<ENC_Q8_0> {
     // d (2 B) then 32 int8 codes; step t: codes 8t..8t+7 in the order
     // (0,2) (1,3) (4,6) (5,7): a code c as (c ^ 0x80) under the exponent of 1024
     // is 1152 + c.
-    static constexpr uint32_t kBytes = 34, kDw = 9, kLayout = XFRAG_BYTE, kValuPerStep = 20;
+    static constexpr uint32_t kBytes = 34, kDw = 9, kLayout = XFRAG_BYTE;
     struct Scale {
         h2 d;
         uint32_t sel;
@@ -236,7 +236,6 @@ struct WinBlocks {
     static constexpr uint32_t kCopies = NP;                                  // copy instructions per chunk
     static constexpr uint32_t kBytes = 64u * NP * 16u;
     static constexpr uint32_t kDw = B::kDw;
-    static constexpr uint32_t kValuPerStep = B::kValuPerStep;
     const uint8_t* src[NP];       // copy lane's piece for the slice's first chunk
     uint32_t off[2][kDw], sh[2];  // this lane's block dwords in the window, its block's start offset
 
@@ -302,7 +301,6 @@ struct WinQ6K {
     static constexpr uint32_t kPitch16 = 16u * kX16, kPitch4 = 4u * kX4;
     static constexpr uint32_t kBytes = 64u * (kPitch16 + kPitch4);
     static constexpr uint32_t kDw = 20;  // ql 9, qh 9, scale dword, d dword
-    static constexpr uint32_t kValuPerStep = 32;
     struct Scale {
         uint32_t sel, mN, magic, mH, sL;
         h2 off, ds0, ds1;
@@ -419,7 +417,6 @@ struct WinMlx {
     static constexpr uint32_t kAuxOff = 64u * 16u * kPieces;  // aux dwords after the 64 rows' pieces
     static constexpr uint32_t kBytes = kAuxOff + 256u * kAux;
     static constexpr uint32_t kDw = 6;  // 4 code words, scale dword, bias dword
-    static constexpr uint32_t kValuPerStep = 14;
     struct Scale {
         h2 s, b;
     };
@@ -519,7 +516,6 @@ struct WinQK {
     static constexpr uint32_t QS = Q5 ? 12u : 4u;          // raw dword of the codes
     static constexpr uint32_t SB = Q5 ? 176u : 144u;       // super-block bytes
     static constexpr uint32_t kDw = QS + 8u;               // d|dmin, three scale dwords, [8 qh dwords,] 8 code dwords
-    static constexpr uint32_t kValuPerStep = Q5 ? 24 : 14;
     struct Scale {
         h2 ds, ndm, off;
         uint32_t mask, magic, hsh, sl, mh;
@@ -615,7 +611,6 @@ struct WinIQ4XS {
     static constexpr uint32_t kPitch = 16u * NP;
     static constexpr uint32_t kBytes = 64u * kPitch;
     static constexpr uint32_t kDw = 12;  // d|scales_h, scales_l, two unused, 8 code dwords
-    static constexpr uint32_t kValuPerStep = 24;
     struct Scale {
         h2 ds;
         uint32_t h;
@@ -808,12 +803,14 @@ void gemm_kernel(const GemmArgs a) {
     // landed for every wave; every wave done reading chunk c), copy chunk c + R
     // into chunk c's slot, read chunk c + 1's weights, then the MFMAs of chunk
     // c in k-step order, each k step followed by the next chunk's activation
-    // reads of that step, with chunk c + 1's decode into wf[1 - p] spread
-    // between the MFMAs of k steps 1..3 (the MFMAs run in the matrix core while
-    // the decode issues).  Scheduling barriers keep the k steps in order.
+    // reads of that step, with chunk c + 1's decode into wf[1 - p] placed
+    // after the MFMAs of k steps 1..3 (the MFMAs run in the matrix core while
+    // the decode issues).  The compiler interleaves them: scheduling-group
+    // barriers that pinned one MFMA, then its share of the decode, ran 1-6%
+    // slower on every encoding.  The copies write slot c % R, the reads take
+    // slot (c + 1) % R, so their order within a step does not matter.
     // The last step reads a slot no chunk was copied into; its decode is
     // never multiplied.
-    constexpr int kValuPerMfma = (int)(3u * W::kValuPerStep + 2u * TM - 1u) / (2 * TM);  // ~3 decode pieces per k step
     auto step = [&](uint32_t c, int p) {
         // copies issued so far: chunks up to min(c + R, nc) - 1; chunk c + 1 must
         // have landed, the newer ones may stay in flight
@@ -823,7 +820,6 @@ void gemm_kernel(const GemmArgs a) {
         if (cn < nc) issue(cn, c % R);
         const uint32_t nxt = (c + 1u) % R;
         read_w(c + 1u);
-        __builtin_amdgcn_sched_barrier(0);
         typename W::Scale sc[2];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -842,15 +838,6 @@ void gemm_kernel(const GemmArgs a) {
                 }
             }
             read_a(nxt, t);
-            // one MFMA, then a share of the decode VALU, ...; the step's
-            // activation reads after its last MFMA
-#pragma unroll
-            for (int m = 0; m < 2 * TM; m++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (t > 0) __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x100, TM, 0);
-            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
