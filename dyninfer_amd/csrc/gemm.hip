@@ -126,15 +126,30 @@ __device__ __forceinline__ void ring_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// ring_barrier<k·PER>() for a wave-uniform k in [0, KMAX]: the copies of the
-// k newest chunks may stay in flight.
-template <uint32_t PER, uint32_t KMAX>
+// The wait of ring_barrier<n>() without the barrier: for a wave whose ring
+// slots no other wave reads or writes.
+template <uint32_t n>
+__device__ __forceinline__ void ring_wait() {
+    static_assert(n < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((n & 15u) | ((n >> 4) << 14) | (7u << 4));
+    asm volatile("" ::: "memory");
+}
+
+// ring_barrier<BASE + k·PER>() (ring_wait when !SYNC) for a wave-uniform k in
+// [0, KMAX]: the copies of the k newest chunks, and BASE newer register
+// loads, may stay in flight.
+template <uint32_t PER, uint32_t KMAX, uint32_t BASE = 0, bool SYNC = true>
 __device__ __forceinline__ void ring_barrier_k(uint32_t k) {
     if constexpr (KMAX == 0) {
-        ring_barrier<0>();
+        if constexpr (SYNC) ring_barrier<BASE>();
+        else ring_wait<BASE>();
     } else {
-        if (k >= KMAX) ring_barrier<KMAX * PER>();
-        else ring_barrier_k<PER, KMAX - 1>(k);
+        if (k >= KMAX) {
+            if constexpr (SYNC) ring_barrier<BASE + KMAX * PER>();
+            else ring_wait<BASE + KMAX * PER>();
+        } else {
+            ring_barrier_k<PER, KMAX - 1, BASE, SYNC>(k);
+        }
     }
 }
 
@@ -699,17 +714,30 @@ struct Geo {
     using W = typename WinOf<ENC>::type;
     static constexpr uint32_t WN = kWaves / S;                         // column subtiles per workgroup
     static constexpr uint32_t kWinBytes = W::kBytes;                    // a wave's 64-row window
-    static constexpr uint32_t kABytes = (uint32_t)S * 4u * TM * 1024u;  // activation fragments of a chunk
+    // S = 4: every wave multiplies a K slice of its own, so no two waves share
+    // an activation fragment.  The fragments then go from the staged
+    // activations straight into registers (kXReg), two chunks ahead, and the
+    // ring holds only the waves' own weight windows, so it needs no barrier.
+    // Not for Q6_K at TM = 2: its larger windows then wait on their copies
+    // (the compiler waits for all loads at each step's first MFMA), and the
+    // copies through LDS measured faster (M128 N3072 K1024 15.0 against 16.6
+    // µs; M512 at TM = 4 21.4 against 24.5).
+    static constexpr bool kXReg = S == 4 && !(ENC == ENC_Q6_K && TM == 2);
+    static constexpr uint32_t kABytes = kXReg ? 0u : (uint32_t)S * 4u * TM * 1024u;  // activation fragments of a chunk
     static constexpr uint32_t kSlot = kABytes + kWaves * kWinBytes;
     static constexpr uint32_t kRs = 32u * TM * 4u;                      // the tile's row factors
     static constexpr uint32_t kEpiPitch = 68u;                          // floats per output row in LDS
     static constexpr uint32_t kEpi = (uint32_t)kWaves * 32u * TM * kEpiPitch * 4u;  // every wave's whole tile
     static constexpr uint32_t kRoom = kLdsMax - kRs;
-    static constexpr uint32_t R = 4u * kSlot <= kRoom ? 4u : 3u * kSlot <= kRoom ? 3u : 2u;
+    static constexpr uint32_t R0 = 4u * kSlot <= kRoom ? 4u : 3u * kSlot <= kRoom ? 3u : 2u;
+    static constexpr uint32_t R = kXReg && R0 > 3u ? 3u : R0;  // (keeps the wait counts below 64)
     static constexpr uint32_t kRing = R * kSlot > kEpi ? R * kSlot : kEpi;  // the epilogue reuses the ring
     static constexpr uint32_t kLds = kRing + kRs;
-    static constexpr uint32_t kDmaA = 4u * TM / WN;  // activation copies per wave per chunk
+    static constexpr uint32_t kDmaA = kXReg ? 0u : 4u * TM / WN;  // activation copies per wave per chunk
     static constexpr uint32_t kDma = kDmaA + W::kCopies;  // all copies per wave per chunk
+    static constexpr uint32_t kXLoads = kXReg ? 4u * TM : 0u;  // activation register loads per wave per step
+    static_assert((R - 1u) * kXLoads + (R - 2u) * W::kCopies < 64 && 2u * kXLoads + (R - 1u) * W::kCopies < 64,
+                  "wait counts fit vmcnt");
     static constexpr bool kFits = 2u * kSlot <= kRoom;
     static_assert((4u * TM) % WN == 0, "activation fragments split evenly over the slice's waves");
 };
@@ -744,11 +772,13 @@ void gemm_kernel(const GemmArgs a) {
     const uint32_t nc = nchk / S, c0 = nc * ks;
 
     // Activation copies: this wave copies fragments f = ns, ns + WN, ... of its
-    // slice's 4·TM per chunk (f = 4·i + t: row block i, k step t).
-    const uint16_t* xsrc[G::kDmaA];
-    uint32_t xdst[G::kDmaA];
+    // slice's 4·TM per chunk (f = 4·i + t: row block i, k step t); with kXReg
+    // (WN = 1) it loads all of them into registers instead.
+    constexpr uint32_t NX = G::kXReg ? 4u * TM : G::kDmaA;
+    const uint16_t* xsrc[NX];
+    uint32_t xdst[NX];
 #pragma unroll
-    for (uint32_t q = 0; q < G::kDmaA; q++) {
+    for (uint32_t q = 0; q < NX; q++) {
         const uint32_t f = ns + q * G::WN, i = f / 4u, t = f % 4u;
         const uint32_t mb = mb0 + i < mbs ? mb0 + i : mbs - 1u;  // past M: re-read the last block (never stored)
         xsrc[q] = a.xh + (((size_t)mb * ksteps + 4u * c0 + t) * 64u + lane) * 8u;
@@ -779,16 +809,28 @@ void gemm_kernel(const GemmArgs a) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
     // Registers: the activation fragments of the chunk being multiplied (each
-    // refilled from the next chunk's slot once its MFMAs have issued), and the
-    // raw and decoded weights of the current and the next chunk.
-    h8 xa[TM][4];
+    // refilled from the next chunk's slot once its MFMAs have issued; with
+    // kXReg, two sets: chunk c's in xa[c % 2], refilled from global memory with
+    // chunk c + 2's), and the raw and decoded weights of the current and the
+    // next chunk.
+    constexpr int NXA = G::kXReg ? 2 : 1;
+    h8 xa[NXA][TM][4];
     uint32_t raw[W::kDw * 2];
     h8 wf[2][2][4];
     auto read_w = [&](uint32_t c) { win.read(c, slot_w(c % R, wave), raw); };  // chunk c's weights
     auto read_a = [&](uint32_t slot, int t) {
         const uint8_t* sa = slot_a(slot) + ks * 4u * TM * 1024u + lane * 16u;
 #pragma unroll
-        for (int i = 0; i < TM; i++) xa[i][t] = *reinterpret_cast<const h8*>(sa + (4u * i + t) * 1024u);
+        for (int i = 0; i < TM; i++) xa[0][i][t] = *reinterpret_cast<const h8*>(sa + (4u * i + t) * 1024u);
+    };
+    // kXReg: k step t of chunk c (past the slice: its last chunk again, never
+    // multiplied) into register set p; every step loads 4·TM fragments, so
+    // the ring's wait counts are fixed
+    auto load_a = [&](uint32_t c, int p, int t) {
+        const uint32_t cc = c < nc ? c : nc - 1u;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+            xa[p][i][t] = *gptr<h8>(xsrc[4 * i + t] + (size_t)cc * 4u * 512u);
     };
     auto decode_all = [&](uint32_t c, int p) {
 #pragma unroll
@@ -810,14 +852,22 @@ void gemm_kernel(const GemmArgs a) {
     // slower on every encoding.  The copies write slot c % R, the reads take
     // slot (c + 1) % R, so their order within a step does not matter.
     // The last step reads a slot no chunk was copied into; its decode is
-    // never multiplied.
+    // never multiplied.  With kXReg the step loads chunk c + 2's activation
+    // fragments into register set p after each k step, and waits for its own
+    // copies only: chunk c + 1's weights, with the activation loads of the
+    // last R - 1 steps still in flight.
     auto step = [&](uint32_t c, int p) {
         // copies issued so far: chunks up to min(c + R, nc) - 1; chunk c + 1 must
         // have landed, the newer ones may stay in flight
+        // (kXReg: every step issues the same copies and loads, past the end
+        // chunk nc - 1's window again, so the counts are fixed and the
+        // compiler's own waits for the activation registers stay partial)
         const uint32_t last = c + R - 1u < nc - 1u ? c + R - 1u : nc - 1u;
-        ring_barrier_k<G::kDma, R - 2u>(last > c + 1u ? last - c - 1u : 0u);
+        ring_barrier_k<G::kDma, R - 2u, (R - 1u) * G::kXLoads, !G::kXReg>(
+            G::kXReg ? R - 2u : last > c + 1u ? last - c - 1u : 0u);
         const uint32_t cn = c + R;
-        if (cn < nc) issue(cn, c % R);
+        if constexpr (G::kXReg) issue(cn < nc ? cn : nc - 1u, c % R);
+        else if (cn < nc) issue(cn, c % R);
         const uint32_t nxt = (c + 1u) % R;
         read_w(c + 1u);
         typename W::Scale sc[2];
@@ -826,7 +876,8 @@ void gemm_kernel(const GemmArgs a) {
 #pragma unroll
             for (int m = 0; m < 2 * TM; m++) {
                 const int i = m >> 1, j = m & 1;
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[p][j][t], xa[i][t], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[p][j][t], xa[G::kXReg ? p : 0][i][t], acc[i][j],
+                                                                   0, 0, 0);
             }
             if (t > 0) {
                 // decode pieces (weight block kj, k step kt) k = 3(t-1) .. (steps 1, 2, 3 take 3, 3, 2)
@@ -837,17 +888,28 @@ void gemm_kernel(const GemmArgs a) {
                     wf[1 - p][kj][kt] = win.step(raw + kj * W::kDw, sc[kj], kt);
                 }
             }
-            read_a(nxt, t);
+            if constexpr (G::kXReg) load_a(c + 2u, p, t);
+            else read_a(nxt, t);
         }
     };
 
 #pragma unroll
     for (uint32_t c = 0; c < R; c++)
-        if (c < nc) issue(c, c);
-    ring_barrier_k<G::kDma, R - 1u>((nc < R ? nc : R) - 1u);  // chunk 0 landed for every wave
-    read_w(0);
+        if (G::kXReg || c < nc) issue(c < nc ? c : nc - 1u, c);
+    if constexpr (G::kXReg) {
 #pragma unroll
-    for (int t = 0; t < 4; t++) read_a(0, t);
+        for (int t = 0; t < 4; t++) load_a(0u, 0, t);
+#pragma unroll
+        for (int t = 0; t < 4; t++) load_a(1u, 1, t);
+    }
+    // chunk 0 landed (for every wave; with kXReg for this one, chunks 0 and 1's
+    // activation loads still in flight)
+    ring_barrier_k<G::kDma, R - 1u, 2u * G::kXLoads, !G::kXReg>(G::kXReg ? R - 1u : (nc < R ? nc : R) - 1u);
+    read_w(0);
+    if constexpr (!G::kXReg) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) read_a(0, t);
+    }
     decode_all(0, 0);
     uint32_t c = 0;
     for (; c + 2u <= nc; c += 2u) {
