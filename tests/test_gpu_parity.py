@@ -398,6 +398,29 @@ def test_gemm_q6_k(ctx, m, n, k, ybf16):
     assert np.all(err <= 2.0 ** -10 + 1e-5 + extra), err.max()
 
 
+@pytest.mark.parametrize("gtype", [oracle.Q4_0, oracle.Q8_0, oracle.Q6_K, oracle.IQ4_XS], ids=oracle.NAMES.get)
+@pytest.mark.parametrize("k", [512, 768, 1280])
+def test_gemm_four_slices_short_and_odd(ctx, gtype, k):
+    """M512 N3072 takes four K slices per workgroup (TM4 S4), so every wave loads
+    its own slice's activation fragments into registers two chunks ahead.
+    These K give 2, 3 and 5 chunks per slice: the shortest slice, and odd
+    counts that end on the unpaired step and re-copy the last chunk's window
+    past the end."""
+    m, n = 512, 3072
+    data = oracle.synth_gguf(gtype, n, k, seed=k + 5)
+    enc = {**ENC, oracle.IQ4_XS: d.ENC_IQ4_XS}[gtype]
+    w = d.QWeight(enc, n, k, dev(data))
+    xb = oracle.f32_to_bf16_bits(oracle.randn(m * k, seed=k)).reshape(m, k)
+    x = oracle.bf16_bits_to_f32(xb)
+    y = ctx.qlinear(w, dev(xb).view(torch.bfloat16)).cpu().numpy()
+    y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(gtype, data, n, k))
+    err = np.abs(y.astype(np.float64) - y64) / np.where(absdot > 0, absdot, 1)
+    # one f16 rounding of each weight (Q6_K twice; IQ4_XS kv·RNE_f16(d·(ls-32)) then the
+    # product: three halves of 2^-10), exact bf16 activations, f32 accumulation
+    bound = {oracle.Q6_K: 2.0 ** -10 + 1e-5, oracle.IQ4_XS: 3 * 2.0 ** -11 + 2e-5}.get(gtype, 2.0 ** -11 + 1e-5)
+    assert np.all(err <= bound), err.max()
+
+
 @pytest.mark.parametrize("gtype", [oracle.Q4_0, oracle.Q8_0, oracle.Q6_K], ids=oracle.NAMES.get)
 @pytest.mark.parametrize("m,n,k", [(200, 384, 1024), (512, 3072, 1024), (96, 1040, 2048), (512, 1024, 3072), (130, 2000, 768),
                                    (2048, 3072, 768), (20, 20000, 256), (33, 512, 2048)])
