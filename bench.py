@@ -329,7 +329,8 @@ def bench_embedding(torch, d, ctx, enc, vocab, k, n, iters=50):
 
 def cpu_baseline(threads_all: int = 16, runs: int = 5):
     """The oracle's CPU contraction (dequantisation adjacent to an f32 dot, the
-    reference's CPU semantics) timed on this host: a
+    reference's CPU semantics) timed on this host, as the baseline rules ask
+    (1-thread and all-thread rates, median of several runs): a
     bounded sample of config 4 with the step's byte mix — one Qwen3-8B layer's
     matmuls (q/k/v/o/gate/up Q4_0, down Q6_K) plus 1/36 of the Q6_K lm_head rows
     — at 1 thread and at all threads of this box's CPU share, median of
