@@ -224,13 +224,17 @@ size_t esize(uint32_t dt) { return dt == DYNINFER_DTYPE_F32 ? 4 : 2; }
 // 23.2 against 35.6 us), three never do (40 rows: Q4_0 4096x4096 32.2 against
 // 24.6 us, 12288x4096 52.4 against 28.2 us); with K above 8192 the MFMA GEMV
 // splits K over launches and the GEMM wins from 17 rows (Q4_0 4096x12288:
-// 60.9 against 73.2 us, Q4_K 66.9 against 81.8 us).
-bool has_prefill_gemm(uint32_t enc, uint32_t N, uint32_t K, uint32_t rows) {
+// 60.9 against 73.2 us, Q4_K 66.9 against 81.8 us).  Except Q6_K with f32
+// outputs: at K above 8192 its GEMM has few row tiles, each decoding long
+// Q6_K slices, and the 16-row MFMA GEMV chunks win up to 32 rows (4096x12288:
+// 46 against 102 us at 17 rows, 71 against 103 at 32; 107 against 106 at 48).
+// With bf16 outputs the MFMA GEMV does not split K, so the GEMM stays.
+bool has_prefill_gemm(uint32_t enc, uint32_t N, uint32_t K, uint32_t rows, bool y_bf16) {
     const bool mfma_gemv = enc == DYNINFER_ENC_GGUF_Q4_0 || enc == DYNINFER_ENC_GGUF_Q6_K ||
                            enc == DYNINFER_ENC_GGUF_Q4_K || enc == DYNINFER_ENC_GGUF_Q5_K ||
                            enc == DYNINFER_ENC_GGUF_IQ4_XS;
-    const uint32_t min_rows = mfma_gemv && K <= 8192u ? 2u * (uint32_t)dmx::kMaxGemvBatch + 1u
-                                                      : (uint32_t)dmx::kMaxGemvBatch + 1u;
+    const bool two_chunks = mfma_gemv && (K <= 8192u || (enc == DYNINFER_ENC_GGUF_Q6_K && !y_bf16));
+    const uint32_t min_rows = two_chunks ? 2u * (uint32_t)dmx::kMaxGemvBatch + 1u : (uint32_t)dmx::kMaxGemvBatch + 1u;
     return rows >= min_rows && dmx::gemm_supported(enc, N, K, rows);
 }
 
@@ -394,7 +398,8 @@ static int qlinear_multi_impl(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight
     if (!aligned(x, 16)) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "activations must be 16-byte aligned");
     bool gemm = true;
     for (uint32_t i = 0; i < count && gemm; i++)
-        gemm = has_prefill_gemm(ws[i].encoding, (uint32_t)ws[i].rows, (uint32_t)ws[i].cols, rows);
+        gemm = has_prefill_gemm(ws[i].encoding, (uint32_t)ws[i].rows, (uint32_t)ws[i].cols, rows,
+                                y_dtype == DYNINFER_DTYPE_BF16);
     if (gemm && (uint64_t)rows * ws[0].cols >= (1ull << 31))
         return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "prefill: rows * K must stay below 2^31 (32-bit activation offsets)");
     const uint64_t need = gemm ? dmx::prefill_workspace_bytes(rows, (uint32_t)ws[0].cols) : 0;

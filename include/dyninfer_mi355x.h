@@ -124,8 +124,9 @@ const char* dyninfer_mi355x_last_error(void);
  *     Q5_K, IQ4_XS and MLX weights on MFMA), activations rounded to f16 after a
  *     power-of-two scaling per scale group;
  *   rows >= 17: the prefill path.  Q4_1, Q8_0 and MLX U4 from 17 rows, Q4_0, Q6_K and
- *     the K-quants / IQ4_XS from 33 rows, or from 17 when K > 8192 (below that two 16-row
- *     MFMA GEMV chunks are mostly faster), K a multiple of 64 (256 for the super-block
+ *     the K-quants / IQ4_XS from 33 rows, or from 17 when K > 8192 except Q6_K with f32
+ *     outputs (below that two 16-row MFMA GEMV chunks are mostly faster), K a multiple
+ *     of 64 (256 for the super-block
  *     encodings): x is staged once per call as f16 MFMA operand fragments,
  *     each row scaled by a power of two (RNE) and the rows padded with zeros to a
  *     multiple of 32; then one MFMA GEMM per weight decodes the GGUF blocks or MLX words

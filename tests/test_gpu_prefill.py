@@ -4,7 +4,8 @@ decode, through the C ABI, against the CPU oracle:
   * prefill (rows >= 17) with f32 and bf16 activations for every encoding,
     through qlinear and qlinear_multi: the GGUF encodings run the
     staged-activation MFMA GEMM (x rounded once to f16 after a power-of-two
-    scaling per row; Q4_0 and Q6_K from 33 rows, 17 when K > 8192), MLX and the
+    scaling per row; Q4_0 and Q6_K from 33 rows, 17 when K > 8192 except Q6_K
+    with f32 outputs), MLX and the
     shorter Q4_0 and Q6_K prefills the GEMV kernels over 16-row chunks (the chunks' x and y
     pointer arithmetic is what the 17/32/200/512 row counts check);
   * bf16 activations on the decode GEMV for every encoding;
@@ -88,14 +89,17 @@ def test_prefill_rows(ctx, kind, rows, xbf16):
 
 
 @pytest.mark.parametrize("kind", ALL, ids=IDS.get)
-@pytest.mark.parametrize("rows", [17, 24])
-def test_prefill_long_k(ctx, kind, rows):
+@pytest.mark.parametrize("rows", [17, 24, 33])
+@pytest.mark.parametrize("ybf16", [False, True])
+def test_prefill_long_k(ctx, kind, rows, ybf16):
     """K above 8192: the GEMM from 17 rows for every encoding (the MFMA GEMV
-    would split K over launches)."""
+    would split K over launches), except Q6_K with f32 outputs, which keeps
+    16-row MFMA GEMV chunks (their K split over launches) up to 32 rows."""
     n, k = 320, 12288
     w, wf = make(kind, n, k, seed=rows + 70)
     xd, x = xs(rows, k, seed=rows + 1, bf16=False)
-    assert err_of(ctx.qlinear(w, xd), x, wf) <= tol(kind)
+    y = ctx.qlinear(w, xd, y_dtype=torch.bfloat16 if ybf16 else torch.float32)
+    assert err_of(y, x, wf, ybf16=ybf16) <= tol(kind)
 
 
 @pytest.mark.parametrize("kind", ALL, ids=IDS.get)
