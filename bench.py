@@ -89,68 +89,60 @@ class StepSet:
         self.weight_bytes += sum(w.nbytes for w in ws)
 
 
-def gguf_step_06b(torch, d, gen) -> StepSet:
-    c = QWEN06
-    s = StepSet("qwen3-0.6b mixed gguf")
+# The launches of each decode step, in step order, per layer then the lm_head:
+# (label, encoding, [(N, K) of each weight sharing the launch's activation],
+# activation key, [output keys]).  Encodings: GGUF type names or "mlx_u4"
+# (group 64, bf16 scales and biases).  tests/test_gpu_bench_launches.py checks
+# every distinct launch of these layouts against the oracle.
+def step_layout(name: str):
+    c = QWEN8 if name in ("config4", "q4_k_m") else QWEN06
+    h, q, kv, f = c["hidden"], c["q"], c["kv"], c["ffn"]
+    out = []
     for layer in range(c["layers"]):
-        enc = d.ENC_Q4_0 if layer % 2 == 0 else d.ENC_Q4_1
-        h, q, kv, f = c["hidden"], c["q"], c["kv"], c["ffn"]
-        s.add(f"qkv.{d.ENCODING_IDS[enc]}", [gguf_tensor(torch, d, enc, q, h, gen), gguf_tensor(torch, d, enc, kv, h, gen),
-                                             gguf_tensor(torch, d, enc, kv, h, gen)], "h", ["q", "k", "v"])
-        s.add(f"o.{d.ENCODING_IDS[enc]}", [gguf_tensor(torch, d, enc, h, q, gen)], "attn", ["o"])
-        s.add(f"gate_up.{d.ENCODING_IDS[enc]}", [gguf_tensor(torch, d, enc, f, h, gen), gguf_tensor(torch, d, enc, f, h, gen)],
-              "h", ["gate", "up"])
-        s.add("down.gguf.q8_0", [gguf_tensor(torch, d, d.ENC_Q8_0, h, f, gen)], "act", ["down"])
-    s.add("lm_head.gguf.q6_k", [gguf_tensor(torch, d, d.ENC_Q6_K, c["vocab"], c["hidden"], gen)], "h", ["logits"])
-    return s
+        if name == "config4":
+            e = ["q4_0"] * 4 + ["q6_k"]
+        elif name == "config1":
+            e = ["q4_0" if layer % 2 == 0 else "q4_1"] * 4 + ["q8_0"]
+        elif name == "config2":
+            e = ["mlx_u4"] * 5
+        elif name == "q4_k_m":  # llama.cpp's Q4_K_M: Q6_K for attn_v, every other ffn_down and the lm_head
+            out.append(("qk.gguf.q4_k", "q4_k", [(q, h), (kv, h)], "h", ["q", "k"]))
+            out.append(("v.gguf.q6_k", "q6_k", [(kv, h)], "h", ["v"]))
+            out.append(("o.gguf.q4_k", "q4_k", [(h, q)], "attn", ["o"]))
+            out.append(("gate_up.gguf.q4_k", "q4_k", [(f, h), (f, h)], "h", ["gate", "up"]))
+            dn = "q6_k" if layer % 2 == 0 else "q4_k"
+            out.append((f"down.gguf.{dn}", dn, [(h, f)], "act", ["down"]))
+            continue
+        else:
+            raise ValueError(name)
+        tag = lambda enc: "mlx.u4" if enc == "mlx_u4" else f"gguf.{enc}"
+        out.append((f"qkv.{tag(e[0])}", e[0], [(q, h), (kv, h), (kv, h)], "h", ["q", "k", "v"]))
+        out.append((f"o.{tag(e[1])}", e[1], [(h, q)], "attn", ["o"]))
+        out.append((f"gate_up.{tag(e[2])}", e[2], [(f, h), (f, h)], "h", ["gate", "up"]))
+        out.append((f"down.{tag(e[4])}", e[4], [(h, f)], "act", ["down"]))
+    head = "mlx_u4" if name == "config2" else "q6_k"
+    out.append((f"lm_head.{'mlx.u4' if head == 'mlx_u4' else 'gguf.q6_k'}", head, [(c["vocab"], h)], "h", ["logits"]))
+    return out
 
 
-def gguf_step_8b(torch, d, gen) -> StepSet:
-    c = QWEN8
-    s = StepSet("qwen3-8b gguf")
-    h, q, kv, f = c["hidden"], c["q"], c["kv"], c["ffn"]
-    for _ in range(c["layers"]):
-        s.add("qkv.gguf.q4_0", [gguf_tensor(torch, d, d.ENC_Q4_0, q, h, gen), gguf_tensor(torch, d, d.ENC_Q4_0, kv, h, gen),
-                                gguf_tensor(torch, d, d.ENC_Q4_0, kv, h, gen)], "h", ["q", "k", "v"])
-        s.add("o.gguf.q4_0", [gguf_tensor(torch, d, d.ENC_Q4_0, h, q, gen)], "attn", ["o"])
-        s.add("gate_up.gguf.q4_0", [gguf_tensor(torch, d, d.ENC_Q4_0, f, h, gen), gguf_tensor(torch, d, d.ENC_Q4_0, f, h, gen)],
-              "h", ["gate", "up"])
-        s.add("down.gguf.q6_k", [gguf_tensor(torch, d, d.ENC_Q6_K, h, f, gen)], "act", ["down"])
-    s.add("lm_head.gguf.q6_k", [gguf_tensor(torch, d, d.ENC_Q6_K, c["vocab"], h, gen)], "h", ["logits"])
-    return s
+# activation rows of each layout's timed batches, and its activation / output dtypes
+STEP_BATCHES = {"config4": (1, 4, 16), "config1": (1, 4), "config2": (1, 8, 16), "q4_k_m": (1, 4, 16)}
+STEP_DTYPES = {"config4": ("f32", "f32"), "config1": ("f32", "f32"), "config2": ("bf16", "bf16"),
+               "q4_k_m": ("f32", "f32")}
+STEP_NAMES = {"config4": "qwen3-8b gguf", "config1": "qwen3-0.6b mixed gguf",
+              "config2": "qwen3-0.6b mlx affine u4 g64", "q4_k_m": "qwen3-8b gguf q4_k_m"}
 
 
-def gguf_step_8b_q4_k_m(torch, d, gen) -> StepSet:
-    """Qwen3-8B in llama.cpp's Q4_K_M mix: Q4_K weights, Q6_K for attn_v, every
-    other ffn_down and the lm_head (the 'more bits' tensors of that recipe)."""
-    c = QWEN8
-    s = StepSet("qwen3-8b gguf q4_k_m")
-    h, q, kv, f = c["hidden"], c["q"], c["kv"], c["ffn"]
-    K4, K6 = d.ENC_Q4_K, d.ENC_Q6_K
-    for layer in range(c["layers"]):
-        s.add("qk.gguf.q4_k", [gguf_tensor(torch, d, K4, q, h, gen), gguf_tensor(torch, d, K4, kv, h, gen)], "h", ["q", "k"])
-        s.add("v.gguf.q6_k", [gguf_tensor(torch, d, K6, kv, h, gen)], "h", ["v"])
-        s.add("o.gguf.q4_k", [gguf_tensor(torch, d, K4, h, q, gen)], "attn", ["o"])
-        s.add("gate_up.gguf.q4_k", [gguf_tensor(torch, d, K4, f, h, gen), gguf_tensor(torch, d, K4, f, h, gen)], "h",
-              ["gate", "up"])
-        down = K6 if layer % 2 == 0 else K4
-        s.add(f"down.{d.ENCODING_IDS[down]}", [gguf_tensor(torch, d, down, h, f, gen)], "act", ["down"])
-    s.add("lm_head.gguf.q6_k", [gguf_tensor(torch, d, K6, c["vocab"], h, gen)], "h", ["logits"])
-    return s
-
-
-def mlx_step_06b(torch, d, gen) -> StepSet:
-    c = QWEN06
-    s = StepSet("qwen3-0.6b mlx affine u4 g64")
-    h, q, kv, f = c["hidden"], c["q"], c["kv"], c["ffn"]
-    for _ in range(c["layers"]):
-        s.add("qkv.mlx.u4", [mlx_tensor(torch, d, q, h, 64, gen), mlx_tensor(torch, d, kv, h, 64, gen),
-                             mlx_tensor(torch, d, kv, h, 64, gen)], "h", ["q", "k", "v"])
-        s.add("o.mlx.u4", [mlx_tensor(torch, d, h, q, 64, gen)], "attn", ["o"])
-        s.add("gate_up.mlx.u4", [mlx_tensor(torch, d, f, h, 64, gen), mlx_tensor(torch, d, f, h, 64, gen)], "h",
-              ["gate", "up"])
-        s.add("down.mlx.u4", [mlx_tensor(torch, d, h, f, 64, gen)], "act", ["down"])
-    s.add("lm_head.mlx.u4", [mlx_tensor(torch, d, c["vocab"], h, 64, gen)], "h", ["logits"])
+def build_step(torch, d, name: str, gen) -> StepSet:
+    """Seeded synthetic weights for every launch of step_layout(name), on the device."""
+    s = StepSet(STEP_NAMES[name])
+    for label, enc, shapes, xin, outs in step_layout(name):
+        if enc == "mlx_u4":
+            ws = [mlx_tensor(torch, d, n, k, 64, gen) for n, k in shapes]
+        else:
+            e = getattr(d, "ENC_" + enc.upper())
+            ws = [gguf_tensor(torch, d, e, n, k, gen) for n, k in shapes]
+        s.add(label, ws, xin, outs)
     return s
 
 
@@ -273,29 +265,83 @@ def bench_rotating_gemv(torch, d, ctx, enc, n, k, batch, pool_bytes=1.2e9, iters
             "hbm_frac": w0.nbytes / ms / 1e6 / HBM_PEAK_GBS}
 
 
-def bench_gemm(torch, d, ctx, m, n, k, xdtype, iters=50, enc=None):
-    """Config 3: prefill GEMM (f16 MFMA, f32 accumulate, bf16 Y; Q4_0 unless
-    `enc`), x f32 or bf16.  One call = the activation staging kernel (x to f16
-    operand fragments with a per-row power-of-two scale) plus the GEMM, both
-    inside the timed region (HIP events on the launch stream); the GEMM
-    kernel's own duration is in the rocprofv3 summary under profiles/."""
+def bench_gemm(torch, d, ctx, m, n, k, xdtype, calls=20, reps=10, enc=None):
+    """Config 3: one prefill call (f16 MFMA, f32 accumulate, bf16 Y; Q4_0 unless
+    `enc`), x f32 or bf16: the activation staging kernel (x to f16 operand
+    fragments with a per-row power-of-two scale) plus the GEMM, into a
+    workspace allocated once up front and sized by the library's query.
+    `calls` back-to-back calls (one weight, one activation) are captured in a
+    HIP graph and replayed between HIP events on the launch stream, so the
+    time per call is GPU time plus the graph's dispatch gaps, without host
+    launch overhead.  `eager_us` is the same call issued from Python."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(3)
     w = gguf_tensor(torch, d, d.ENC_Q4_0 if enc is None else enc, n, k, gen)
     x = torch.randn(m, k, device="cuda", generator=gen).to(xdtype)
     y = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    wsb = d.prefill_workspace_bytes([w], m, d.DTYPE_BF16 if xdtype == torch.bfloat16 else d.DTYPE_F32, d.DTYPE_BF16)
+    work = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
     st = torch.cuda.Stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(st):
         for _ in range(3):
-            ctx.qlinear(w, x, y, stream=st)
+            ctx.qlinear(w, x, y, stream=st, workspace=work)
         torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(st)
-        for _ in range(iters):
-            ctx.qlinear(w, x, y, stream=st)
+        for _ in range(reps * 5):
+            ctx.qlinear(w, x, y, stream=st, workspace=work)
         b.record(st)
         torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / iters
+        eager_ms = a.elapsed_time(b) / (reps * 5)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            for _ in range(calls):
+                ctx.qlinear(w, x, y, stream=st, workspace=work)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        a.record(st)
+        for _ in range(reps):
+            g.replay()
+        b.record(st)
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / (reps * calls)
+    del g
+    tflops = 2.0 * m * n * k / ms / 1e9
+    return {"us": ms * 1e3, "TFLOPs": tflops, "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS, "eager_us": eager_ms * 1e3,
+            "workspace_bytes": wsb}
+
+
+def bench_dense_gemm(torch, m, n, k, calls=20, reps=10):
+    """The dense counterpart of config 3 on the same box: Y = X·Wᵀ with bf16 X
+    [M, K] and a dense bf16 W (torch.matmul, i.e. hipBLASLt), bf16 Y, timed as
+    bench_gemm (a graph of `calls` products, replayed between HIP events).
+    The right operand is materialised as a contiguous [K, N] tensor."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    x = torch.randn(m, k, device="cuda", generator=gen).bfloat16()
+    wt = torch.randn(n, k, device="cuda", generator=gen).bfloat16().t().contiguous()
+    y = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    st = torch.cuda.Stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(st):
+        for _ in range(3):
+            torch.matmul(x, wt, out=y)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            for _ in range(calls):
+                torch.matmul(x, wt, out=y)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        a.record(st)
+        for _ in range(reps):
+            g.replay()
+        b.record(st)
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / (reps * calls)
+    del g
     tflops = 2.0 * m * n * k / ms / 1e9
     return {"us": ms * 1e3, "TFLOPs": tflops, "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS}
 
@@ -327,7 +373,7 @@ def bench_embedding(torch, d, ctx, enc, vocab, k, n, iters=50):
             "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
-def cpu_baseline(threads_all: int = 16, runs: int = 5):
+def cpu_baseline(threads_all: int | None = None, runs: int = 5):
     """The oracle's CPU contraction (dequantisation adjacent to an f32 dot, the
     reference's CPU semantics) timed on this host, as the baseline rules ask
     (1-thread and all-thread rates, median of several runs): a
@@ -337,6 +383,8 @@ def cpu_baseline(threads_all: int = 16, runs: int = 5):
     `runs` runs after a warm-up.  tokens/s = GB/s / the step's 4.88 GB."""
     import numpy as np
     import oracle
+    if threads_all is None:  # the CPUs this process may run on (its share of the box), not the host's count
+        threads_all = len(os.sched_getaffinity(0))
     c = QWEN8
     h, q, kv, f = c["hidden"], c["q"], c["kv"], c["ffn"]
     mats = [(oracle.Q4_0, q, h), (oracle.Q4_0, kv, h), (oracle.Q4_0, kv, h), (oracle.Q4_0, h, q),
@@ -365,7 +413,7 @@ def cpu_baseline(threads_all: int = 16, runs: int = 5):
             "nproc": os.cpu_count(), "one_thread": out[1], "all_threads": allc,
             "sample": f"config-4 byte mix: one Qwen3-8B layer's 7 matmuls + 1/36 of the Q6_K lm_head rows "
                       f"({nbytes} weight bytes) at batch 1, median of {runs} runs each at 1 and {threads_all} "
-                      f"OpenMP threads (this box's CPU share; nproc reports {os.cpu_count()}), "
+                      f"OpenMP threads (the CPUs in this process's affinity mask; the host has {os.cpu_count()}), "
                       f"oracle/oracle.c qlinear_gguf_f32 (C++ restatement of dyninfer CPU semantics)"}
 
 
@@ -373,6 +421,16 @@ def cpu_baseline(threads_all: int = 16, runs: int = 5):
 def breakdown_of(stats):
     return {k: {"launches_per_step": n, "us_per_launch": round(us, 3), "GBps": round(nb / (us * 1e-6) / 1e9, 1)}
             for k, (n, us, nb) in sorted(stats.items())}
+
+
+def us_per_label(stats):
+    """{label: µs per launch} (the compact form of breakdown_of)."""
+    return {k: round(us, 2) for k, (n, us, nb) in sorted(stats.items())}
+
+
+def step_entry(nbytes, b, ms):
+    return {"us_per_step": round(ms * 1e3, 1), "hbm_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(b / (ms * 1e-3), 1)}
 
 
 def main() -> int:
@@ -410,18 +468,20 @@ def main() -> int:
             wg = gguf_tensor(torch, d, enc, 3072, 1024, gen)
             xg = torch.randn(m, 1024, device="cuda", generator=gen).bfloat16()
             yg = torch.empty(m, 3072, device="cuda", dtype=torch.bfloat16)
+            work = torch.empty(d.prefill_workspace_bytes([wg], m, d.DTYPE_BF16, d.DTYPE_BF16), dtype=torch.uint8,
+                               device="cuda")
             torch.cuda.synchronize()
             for _ in range(30):
-                ctx.qlinear(wg, xg, yg)
+                ctx.qlinear(wg, xg, yg, workspace=work)
             torch.cuda.synchronize()
         print("gemm probe: Q4_0 M512, Q4_0 M2048, Q4_1, Q8_0, Q6_K M512 (N3072 K1024), 30 calls each", flush=True)
         return 0
 
     if args.pmc_probe and args.probe_config == 1:
-        s4 = gguf_step_06b(torch, d, gen)
+        s4 = build_step(torch, d, "config1", gen)
     else:
         log("building config 4 weights (Qwen3-8B GGUF, 4.88 GB) ...")
-        s4 = gguf_step_8b(torch, d, gen)
+        s4 = build_step(torch, d, "config4", gen)
     r4 = StepRunner(torch, d, ctx, s4, args.batch, torch.float32, torch.float32)
     if args.pmc_probe:
         src = torch.ones(16 << 20, dtype=torch.float32, device="cuda")
@@ -445,7 +505,8 @@ def main() -> int:
     g4 = r4.capture()
     ms = r4.time_graph(g4, args.steps, args.warmup)
     del g4
-    value = s4.weight_bytes / ms / 1e6
+    step_bytes, step_launches = s4.weight_bytes, len(s4.launches)
+    value = step_bytes / ms / 1e6
     log(f"config 4 batch {args.batch}: {ms * 1e3:.1f} us/step, {value:.1f} GB/s")
 
     # dominant kernel of the step: the launch label with the largest total time
@@ -464,94 +525,79 @@ def main() -> int:
         if dom_label in tj.get("bytes_per_launch", {}):
             roofline["traffic"] = tj["bytes_per_launch"][dom_label]
             roofline["traffic_source"] = tj.get("source")
-    extra = {"config4_batch1_breakdown": breakdown_of(stats)}
+    # `extra` (stdout) holds the compact figures; `detail` (one JSON line on
+    # stderr) the per-label breakdowns in full
+    c4 = {"weight_bytes_per_step": s4.weight_bytes, f"batch{args.batch}": step_entry(s4.weight_bytes, args.batch, ms),
+          f"batch{args.batch}_us_per_launch": us_per_label(stats)}
+    extra = {"config4": c4}
+    detail = {"config4": {f"batch{args.batch}": breakdown_of(stats)}}
     del r4
 
     if not args.no_extra:
-        c4 = {"weight_bytes_per_step": s4.weight_bytes}
         for b in (4, 16):
             r = StepRunner(torch, d, ctx, s4, b, torch.float32, torch.float32)
             g = r.capture()
             ms8 = r.time_graph(g, max(5, args.steps // 5), 2)
             del g
-            c4[f"batch{b}"] = {"us_per_step": round(ms8 * 1e3, 1), "weight_GBps": round(s4.weight_bytes / ms8 / 1e6, 1),
-                               "hbm_frac": round(s4.weight_bytes / ms8 / 1e6 / HBM_PEAK_GBS, 4),
-                               "tokens_per_s": round(b / (ms8 * 1e-3), 1),
-                               "breakdown": breakdown_of(r.label_times(reps=5))}
+            st8 = r.label_times(reps=5)
+            c4[f"batch{b}"] = step_entry(s4.weight_bytes, b, ms8)
+            c4[f"batch{b}_us_per_launch"] = us_per_label(st8)
+            detail["config4"][f"batch{b}"] = breakdown_of(st8)
             del r
-        extra["config4_qwen3_8b_step"] = c4
-        log("Qwen3-8B Q4_K_M step ...")
-        sk = gguf_step_8b_q4_k_m(torch, d, gen)
-        ck = {"weight_bytes_per_step": sk.weight_bytes}
-        for b in (1, 4, 16):
-            r = StepRunner(torch, d, ctx, sk, b, torch.float32, torch.float32)
-            g = r.capture()
-            msk = r.time_graph(g, max(5, args.steps // 5), 2)
-            del g
-            ck[f"batch{b}"] = {"us_per_step": round(msk * 1e3, 1), "weight_GBps": round(sk.weight_bytes / msk / 1e6, 1),
-                               "hbm_frac": round(sk.weight_bytes / msk / 1e6 / HBM_PEAK_GBS, 4),
-                               "tokens_per_s": round(b / (msk * 1e-3), 1),
-                               "breakdown": breakdown_of(r.label_times(reps=5))}
-            del r
-        extra["qwen3_8b_q4_k_m_step"] = ck
-        del sk
-        log("config 1 (Qwen3-0.6B mixed GGUF step) ...")
-        s1 = gguf_step_06b(torch, d, gen)
-        c1 = {"weight_bytes_per_step": s1.weight_bytes}
-        for b in (1, 4):
-            r = StepRunner(torch, d, ctx, s1, b, torch.float32, torch.float32)
-            g = r.capture()
-            ms1 = r.time_graph(g, max(10, args.steps), 5)
-            del g
-            c1[f"batch{b}"] = {"us_per_step": round(ms1 * 1e3, 1), "weight_GBps": round(s1.weight_bytes / ms1 / 1e6, 1),
-                               "hbm_frac": round(s1.weight_bytes / ms1 / 1e6 / HBM_PEAK_GBS, 4),
-                               "tokens_per_s": round(b / (ms1 * 1e-3), 1),
-                               "breakdown": breakdown_of(r.label_times(reps=10))}
-            del r
-        extra["config1_qwen3_06b_mixed_step"] = c1
-        del s1
+        del s4
+        steps_extra = (("q4_k_m", "qwen3_8b_q4_k_m", torch.float32), ("config1", "config1", torch.float32),
+                       ("config2", "config2", torch.bfloat16))
+        for name, key, dt in steps_extra:
+            log(f"{STEP_NAMES[name]} step ...")
+            sx = build_step(torch, d, name, gen)
+            cx = {"weight_bytes_per_step": sx.weight_bytes}
+            detail[key] = {}
+            for b in STEP_BATCHES[name]:
+                r = StepRunner(torch, d, ctx, sx, b, dt, dt)
+                g = r.capture()
+                msx = r.time_graph(g, max(10, args.steps // 2), 3)
+                del g
+                cx[f"batch{b}"] = step_entry(sx.weight_bytes, b, msx)
+                stx = r.label_times(reps=5)
+                detail[key][f"batch{b}"] = breakdown_of(stx)
+                if name == "config2" or b == 1:
+                    cx[f"batch{b}_us_per_launch"] = us_per_label(stx)
+                del r
+            extra[key] = cx
+            del sx
         log("config 0 (rotating pool) ...")
-        extra["config0_q4_0_3072x1024_b1"] = {k: round(v, 4) for k, v in
-                                              bench_rotating_gemv(torch, d, ctx, d.ENC_Q4_0, 3072, 1024, 1).items()}
-        log("config 2 (MLX U4 step) ...")
-        s2 = mlx_step_06b(torch, d, gen)
-        c2 = {"weight_bytes_per_step": s2.weight_bytes}
-        for b in (1, 8, 16):
-            r2 = StepRunner(torch, d, ctx, s2, b, torch.bfloat16, torch.bfloat16)
-            g = r2.capture()
-            ms2 = r2.time_graph(g, max(5, args.steps // 2), 3)
-            del g
-            c2[f"batch{b}"] = {"us_per_step": round(ms2 * 1e3, 1), "weight_GBps": round(s2.weight_bytes / ms2 / 1e6, 1),
-                               "hbm_frac": round(s2.weight_bytes / ms2 / 1e6 / HBM_PEAK_GBS, 4),
-                               "tokens_per_s": round(b / (ms2 * 1e-3), 1)}
-            del r2
-        extra["config2_mlx_u4_step"] = c2
-        del s2
-        log("config 3 (Q4_0 GEMM) ...")
-        c3 = {}
+        extra["config0"] = {k: round(v, 4) for k, v in
+                            bench_rotating_gemv(torch, d, ctx, d.ENC_Q4_0, 3072, 1024, 1).items()}
+        log("config 3 (Q4_0 GEMM) and the dense bf16 GEMM ...")
+        c3, c3f = {}, {}
         for m in (128, 512, 2048):
             for (n, k) in [(3072, 1024), (1024, 3072), (2048, 1024)]:
-                for xn, xdt in (("xbf16", torch.bfloat16), ("xf32", torch.float32)):
-                    c3[f"M{m}_N{n}_K{k}_{xn}"] = {kk: round(v, 4) for kk, v in
-                                                  bench_gemm(torch, d, ctx, m, n, k, xdt).items()}
-        extra["config3_q4_0_gemm"] = c3
+                r = bench_gemm(torch, d, ctx, m, n, k, torch.bfloat16)
+                dn_ = bench_dense_gemm(torch, m, n, k)
+                rf = bench_gemm(torch, d, ctx, m, n, k, torch.float32)
+                c3[f"M{m}_N{n}_K{k}"] = {"us": round(r["us"], 2), "TFLOPs": round(r["TFLOPs"], 1),
+                                         "mfma_frac": round(r["mfma_frac"], 4), "eager_us": round(r["eager_us"], 2),
+                                         "xf32_us": round(rf["us"], 2), "workspace_bytes": r["workspace_bytes"],
+                                         "dense_bf16_us": round(dn_["us"], 2),
+                                         "dense_bf16_frac": round(dn_["mfma_frac"], 4)}
+        extra["config3_q4_0"] = c3
         log("prefill GEMM, other encodings ...")
-        extra["config3_other_encodings_gemm"] = {
-            f"{name}_M512_N{n}_K{k}_xbf16": {kk: round(v, 4) for kk, v in
-                                             bench_gemm(torch, d, ctx, 512, n, k, torch.bfloat16, enc=enc).items()}
+        extra["config3_other_encodings_us"] = {
+            f"{name}_M512_N{n}_K{k}": round(bench_gemm(torch, d, ctx, 512, n, k, torch.bfloat16, enc=enc)["us"], 2)
             for name, enc in (("q4_1", d.ENC_Q4_1), ("q8_0", d.ENC_Q8_0), ("q6_k", d.ENC_Q6_K), ("q4_k", d.ENC_Q4_K),
                               ("q5_k", d.ENC_Q5_K), ("iq4_xs", d.ENC_IQ4_XS))
             for (n, k) in [(3072, 1024), (1024, 3072)]}
-        g512 = c3["M512_N3072_K1024_xbf16"]
-        extra["config3_roofline"] = {"bound": "mfma", "kernel": "xprep + gemm (Q4_0), M512 N3072 K1024, bf16 X",
-                                     "achieved": round(g512["TFLOPs"], 1), "peak": MFMA_F16_PEAK_TFLOPS,
-                                     "unit": "TFLOP/s", "frac": round(g512["mfma_frac"], 4),
-                                     "flops_per_launch": 2 * 512 * 3072 * 1024, "avg_call_us": round(g512["us"], 3),
-                                     "timing": "HIP events around 50 back-to-back calls (staging + GEMM); "
-                                               "includes the dispatch gaps"}
+        g512 = c3["M512_N3072_K1024"]
+        extra["config3_roofline"] = {"bound": "mfma", "kernel": "xprep + gemm (Q4_0), M512 N3072 K1024, bf16 X and Y",
+                                     "achieved": g512["TFLOPs"], "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                     "frac": g512["mfma_frac"], "flops_per_launch": 2 * 512 * 3072 * 1024,
+                                     "avg_call_us": g512["us"],
+                                     "dense_bf16_same_shape_frac": g512["dense_bf16_frac"],
+                                     "timing": "HIP events around graph replays of 20 calls (staging + GEMM, "
+                                               "caller workspace); includes the dispatch gaps"}
         log("embedding gather (tied Qwen3 embeddings) ...")
-        extra["embedding_gather"] = {
-            f"{name}_n{n}": bench_embedding(torch, d, ctx, enc, 151936, k, n)
+        extra["embedding_gather_GBps"] = {
+            f"{name}_n{n}": bench_embedding(torch, d, ctx, enc, 151936, k, n)["GBps"]
             for name, enc, k in (("q6_k_151936x1024", d.ENC_Q6_K, 1024), ("q4_0_151936x4096", d.ENC_Q4_0, 4096))
             for n in (1, 512, 4096)}
 
@@ -573,15 +619,16 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32 in/out, f16-rounded activations, f32 accumulate",
         "data": "synthetic (seeded GGUF blocks in the BASELINE distributions, resident in HBM)",
-        "config": {"workload": "BASELINE config 4: Qwen3-8B GGUF decode-step GEMV set (36 layers of Q4_0 "
-                               "q/k/v/o/gate/up and Q6_K down, Q6_K lm_head), graph-replayed",
-                   "batch": args.batch, "weight_bytes_per_step": s4.weight_bytes,
-                   "launches_per_step": len(s4.launches), "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "config": {"workload": "BASELINE config 4: Qwen3-8B GGUF decode-step GEMV set (Q4_0 q/k/v/o/gate/up, "
+                               "Q6_K down and lm_head), graph-replayed",
+                   "batch": args.batch, "weight_bytes_per_step": step_bytes,
+                   "launches_per_step": step_launches, "hbm_frac": round(value / HBM_PEAK_GBS, 4),
                    "tokens_per_s": round(args.batch / (ms * 1e-3), 1)},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "extra": extra,
     }
+    log("bench detail: " + json.dumps(detail))
     print(json.dumps(out), flush=True)
     return 0
 

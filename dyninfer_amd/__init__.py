@@ -28,7 +28,8 @@ from typing import Optional, Sequence
 __all__ = [
     "LIB_PATH", "DyninferError", "QWeight", "Context", "library", "candidates", "registry_select",
     "registry_require", "precision_check", "supports", "ENC_Q4_0", "ENC_Q4_1", "ENC_Q8_0", "ENC_Q6_K", "ENC_Q4_K", "ENC_Q5_K", "ENC_IQ4_XS", "ENC_MLX_U4",
-    "DTYPE_F32", "DTYPE_F16", "DTYPE_BF16", "block_geometry", "weight_bytes", "ERR_INVALID_ARGUMENT",
+    "DTYPE_F32", "DTYPE_F16", "DTYPE_BF16", "block_geometry", "weight_bytes", "prefill_workspace_bytes",
+    "ERR_INVALID_ARGUMENT",
     "ERR_UNSUPPORTED", "ERR_HIP", "ERR_DEVICE", "ERR_BUFFER_TOO_SMALL",
 ]
 
@@ -57,7 +58,7 @@ EXPORTED_SYMBOLS = (
     "dyninfer_mi355x_safetensors_open", "dyninfer_mi355x_safetensors_open_memory", "dyninfer_mi355x_safetensors_close",
     "dyninfer_mi355x_safetensors_tensor_count", "dyninfer_mi355x_safetensors_metadata_json",
     "dyninfer_mi355x_safetensors_tensor", "dyninfer_mi355x_safetensors_find", "dyninfer_mi355x_safetensors_upload",
-    "dyninfer_mi355x_safetensors_mlx_qweight",
+    "dyninfer_mi355x_safetensors_mlx_qweight", "dyninfer_mi355x_prefill_workspace_bytes",
 )
 
 
@@ -107,8 +108,9 @@ def library() -> ctypes.CDLL:
         "dyninfer_mi355x_open": (I, [I, ctypes.POINTER(P)]),
         "dyninfer_mi355x_close": (I, [P]),
         "dyninfer_mi355x_last_error": (ctypes.c_char_p, []),
-        "dyninfer_mi355x_qlinear": (I, [P, W, P, U32, U32, P, U32, P]),
-        "dyninfer_mi355x_qlinear_multi": (I, [P, W, U32, P, U32, U32, ctypes.POINTER(P), U32, P]),
+        "dyninfer_mi355x_qlinear": (I, [P, W, P, U32, U32, P, U32, P, ctypes.c_uint64, P]),
+        "dyninfer_mi355x_qlinear_multi": (I, [P, W, U32, P, U32, U32, ctypes.POINTER(P), U32, P, ctypes.c_uint64, P]),
+        "dyninfer_mi355x_prefill_workspace_bytes": (I, [W, U32, U32, U32, U32, ctypes.POINTER(ctypes.c_uint64)]),
         "dyninfer_mi355x_qlinear_multi_noalloc": (I, [P, W, U32, P, U32, U32, ctypes.POINTER(P), U32, P]),
         "dyninfer_mi355x_dequant": (I, [P, W, P, P]),
         "dyninfer_mi355x_embedding": (I, [P, W, P, U32, P, P]),
@@ -239,6 +241,16 @@ def supports(w: QWeight, rows: int, x_dtype: int = DTYPE_F32, y_dtype: int = DTY
     return bool(library().dyninfer_mi355x_supports(ctypes.byref(wc), rows, x_dtype, y_dtype))
 
 
+def prefill_workspace_bytes(ws: Sequence[QWeight], rows: int, x_dtype: int = DTYPE_F32,
+                            y_dtype: int = DTYPE_F32) -> int:
+    """Device workspace bytes a qlinear / qlinear_multi call over ``ws`` with these rows
+    and dtypes needs (0 when it runs no prefill GEMM); dyninfer_mi355x_prefill_workspace_bytes."""
+    arr = (_QWeightC * len(ws))(*[w.c() for w in ws])
+    n = ctypes.c_uint64(0)
+    _check(library().dyninfer_mi355x_prefill_workspace_bytes(arr, len(ws), rows, x_dtype, y_dtype, ctypes.byref(n)))
+    return n.value
+
+
 class Context:
     """An open library context on one gfx950 device (dyninfer_mi355x_open/close)."""
 
@@ -250,9 +262,10 @@ class Context:
         self._h = h
 
     def close(self) -> None:
+        """dyninfer_mi355x_close; raises DyninferError on a non-zero status."""
         if getattr(self, "_h", None):
-            self._lib.dyninfer_mi355x_close(self._h)
-            self._h = None
+            h, self._h = self._h, None
+            _check(self._lib.dyninfer_mi355x_close(h))
 
     def __enter__(self):
         return self
@@ -273,30 +286,54 @@ class Context:
             return torch.cuda.current_stream().cuda_stream
         return stream if isinstance(stream, int) else stream.cuda_stream
 
-    def qlinear(self, w: QWeight, x, y=None, y_dtype=None, stream=None):
-        """y = x · Wᵀ (f32 accumulation).  x: [rows, K] f32 or bf16 device tensor."""
+    def _workspace(self, ws, x, rows: int, ydt: int, stream, workspace):
+        """(pointer, bytes, keep-alive) of the call's device workspace: the caller's
+        ``workspace`` tensor, or a new torch allocation of the size the library asks
+        for (torch's caching allocator, tied to the launch stream), or none."""
+        import torch
+        need = prefill_workspace_bytes(ws, rows, _dtype_code(x), ydt)
+        if need == 0:
+            return None, 0, None
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+            if stream is not None:
+                st = stream if isinstance(stream, torch.cuda.Stream) else torch.cuda.ExternalStream(int(stream))
+                workspace.record_stream(st)  # not reused before the call's work on `stream` completes
+        return workspace.data_ptr(), workspace.numel() * workspace.element_size(), workspace
+
+    def qlinear(self, w: QWeight, x, y=None, y_dtype=None, stream=None, workspace=None):
+        """y = x · Wᵀ (f32 accumulation).  x: [rows, K] f32 or bf16 device tensor.
+        workspace: a device tensor of at least prefill_workspace_bytes([w], rows, …)
+        bytes for a prefill call (one is allocated through torch when omitted)."""
         import torch
         rows = x.shape[0] if x.dim() == 2 else 1
         if y is None:
             y = torch.empty((rows, w.rows), dtype=y_dtype or torch.float32, device=x.device)
+        wp, wn, _keep = self._workspace([w], x, rows, _dtype_code(y), stream, workspace)
         wc = w.c()
         _check(self._lib.dyninfer_mi355x_qlinear(self._h, ctypes.byref(wc), x.data_ptr(), _dtype_code(x), rows,
-                                                 y.data_ptr(), _dtype_code(y), self._stream(stream)))
+                                                 y.data_ptr(), _dtype_code(y), wp, wn, self._stream(stream)))
         return y
 
-    def qlinear_multi(self, ws: Sequence[QWeight], x, ys=None, y_dtype=None, stream=None, noalloc=False):
+    def qlinear_multi(self, ws: Sequence[QWeight], x, ys=None, y_dtype=None, stream=None, noalloc=False,
+                      workspace=None):
         """One launch for several weights sharing activation x (same encoding and K).
         noalloc: dyninfer_mi355x_qlinear_multi_noalloc (prefill staging in the
-        device's static scratch; the caller passes the outputs)."""
+        device's static scratch; the caller passes the outputs); otherwise the
+        prefill workspace is ``workspace`` or a torch allocation as in qlinear."""
         import torch
         rows = x.shape[0] if x.dim() == 2 else 1
         if ys is None:
             ys = [torch.empty((rows, w.rows), dtype=y_dtype or torch.float32, device=x.device) for w in ws]
         arr = (_QWeightC * len(ws))(*[w.c() for w in ws])
         yp = (ctypes.c_void_p * len(ws))(*[y.data_ptr() for y in ys])
-        fn = self._lib.dyninfer_mi355x_qlinear_multi_noalloc if noalloc else self._lib.dyninfer_mi355x_qlinear_multi
-        _check(fn(self._h, arr, len(ws), x.data_ptr(), _dtype_code(x), rows, yp, _dtype_code(ys[0]),
-                  self._stream(stream)))
+        if noalloc:
+            _check(self._lib.dyninfer_mi355x_qlinear_multi_noalloc(self._h, arr, len(ws), x.data_ptr(), _dtype_code(x),
+                                                                   rows, yp, _dtype_code(ys[0]), self._stream(stream)))
+            return ys
+        wp, wn, _keep = self._workspace(ws, x, rows, _dtype_code(ys[0]), stream, workspace)
+        _check(self._lib.dyninfer_mi355x_qlinear_multi(self._h, arr, len(ws), x.data_ptr(), _dtype_code(x), rows, yp,
+                                                       _dtype_code(ys[0]), wp, wn, self._stream(stream)))
         return ys
 
     def dequant(self, w: QWeight, out=None, stream=None):

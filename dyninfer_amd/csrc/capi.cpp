@@ -17,7 +17,6 @@
 #include <cerrno>
 #include <cstdio>
 #include <cstring>
-#include <mutex>
 #include <string>
 #include <vector>
 
@@ -33,20 +32,13 @@
 constexpr size_t kScratchBytes = DYNINFER_MI355X_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
-// A context's prefill staging workspace for one stream: grown in stream order
-// (the old buffer released with hipFreeAsync behind the work that used it),
-// kept for the next call on that stream, released at close.
-struct StreamWorkspace {
-    hipStream_t st;
-    uint8_t* p;
-    uint64_t bytes;
-};
-
+// A context: the device it was opened on and that device's copy of `scratch`.
+// Immutable after dyninfer_mi355x_open, so calls from any number of threads
+// share it without locks; each call's temporary lives in the caller's
+// workspace (or, for the no-allocation entry point, in `scratch`).
 struct dyninfer_mi355x_ctx {
     int device;
-    uint8_t* scratch;  // this device's copy of `scratch`
-    std::mutex mu;     // held from workspace lookup until the call's launches are enqueued
-    std::vector<StreamWorkspace> work;
+    uint8_t* scratch;
 };
 
 namespace {
@@ -238,53 +230,6 @@ bool has_prefill_gemm(uint32_t enc, uint32_t N, uint32_t K, uint32_t rows, bool 
     return rows >= min_rows && dmx::gemm_supported(enc, N, K, rows);
 }
 
-// Device memory of one prefill call.  Normally the context's workspace for the
-// stream (grown when too small).  Under stream capture the call never uses a
-// context workspace, which a later regrowth could free while the graph still
-// names it: it takes a transient stream-ordered allocation, released after its
-// launches, that the captured graph allocates and frees on each replay.
-struct Workspace {
-    uint8_t* p = nullptr;
-    hipStream_t st = nullptr;
-    bool owned = false;
-    ~Workspace() {
-        if (owned) (void)hipFreeAsync(p, st);
-    }
-};
-
-hipError_t acquire_workspace(dyninfer_mi355x_ctx_t* ctx, hipStream_t st, uint64_t need, Workspace& wk) {
-    wk.st = st;
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    hipError_t e = hipStreamIsCapturing(st, &cap);
-    if (e != hipSuccess) return e;
-    if (cap != hipStreamCaptureStatusNone) {
-        e = hipMallocAsync(reinterpret_cast<void**>(&wk.p), (size_t)need, st);
-        wk.owned = e == hipSuccess;
-        return e;
-    }
-    StreamWorkspace* sw = nullptr;
-    for (StreamWorkspace& w : ctx->work)
-        if (w.st == st) sw = &w;
-    if (sw && sw->bytes >= need) {
-        wk.p = sw->p;
-        return hipSuccess;
-    }
-    uint64_t bytes = 1u << 20;  // powers of two from 1 MiB: few regrowths as prefill lengths vary
-    while (bytes < need) bytes *= 2;
-    uint8_t* p = nullptr;
-    e = hipMallocAsync(reinterpret_cast<void**>(&p), (size_t)bytes, st);
-    if (e != hipSuccess) return e;
-    if (sw) {
-        (void)hipFreeAsync(sw->p, st);  // after the work already queued on st that uses it
-        sw->p = p;
-        sw->bytes = bytes;
-    } else {
-        ctx->work.push_back({st, p, bytes});
-    }
-    wk.p = p;
-    return hipSuccess;
-}
-
 // The prefill path: x staged once (xprep), then one GEMM per weight.
 hipError_t prefill(const dyninfer_qweight_t* ws, uint32_t count, const void* x, uint32_t x_dtype, uint32_t rows,
                    void* const* ys, uint32_t y_dtype, uint8_t* work, hipStream_t st) {
@@ -355,18 +300,7 @@ int dyninfer_mi355x_open(int device, dyninfer_mi355x_ctx_t** out_ctx) {
 }
 
 int dyninfer_mi355x_close(dyninfer_mi355x_ctx_t* ctx) {
-    if (!ctx) return DYNINFER_MI355X_OK;
-    hipError_t first = hipSuccess;
-    {
-        DeviceGuard g(ctx->device);
-        // hipFree waits for the device, so work still using a workspace completes first
-        for (StreamWorkspace& w : ctx->work) {
-            const hipError_t e = hipFree(w.p);
-            if (first == hipSuccess) first = e;
-        }
-    }
-    delete ctx;
-    if (first != hipSuccess) return hip_fail(first, "hipFree (prefill staging workspace)");
+    delete ctx;  // the context holds no device memory (the scratch array belongs to the code object)
     return DYNINFER_MI355X_OK;
 }
 
@@ -375,19 +309,14 @@ int dyninfer_mi355x_supports(const dyninfer_qweight_t* w, uint32_t rows, uint32_
     return 1;
 }
 
-// qlinear_multi; noalloc takes the prefill workspace from the device's static
-// scratch array instead of a stream-ordered allocation.
-static int qlinear_multi_impl(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws, uint32_t count, const void* x,
-                              uint32_t x_dtype, uint32_t rows, void* const* ys, uint32_t y_dtype, void* stream,
-                              bool noalloc) {
-    if (int rc = check_ctx(ctx)) return rc;
+// Validation and routing of a qlinear_multi call, shared by the call and the
+// workspace query: whether it runs the prefill GEMM, and the workspace it needs.
+static int plan_multi(const dyninfer_qweight_t* ws, uint32_t count, uint32_t x_dtype, uint32_t rows,
+                      uint32_t y_dtype, bool& gemm, uint64_t& need) {
     if (!ws || count == 0 || count > (uint32_t)dmx::kMaxProblems)
         return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "count must be 1..4 with a weight array");
-    if (!x || !ys) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "x / y pointers are NULL");
     for (uint32_t i = 0; i < count; i++) {
         if (int rc = check_weight(&ws[i])) return rc;
-        if (!ys[i]) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "output pointer is NULL");
-        if (!aligned(ys[i], esize(y_dtype))) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "output is misaligned");
         if (ws[i].encoding != ws[0].encoding || ws[i].cols != ws[0].cols ||
             (ws[0].encoding == DYNINFER_ENC_MLX_AFFINE_U4 &&
              (ws[i].group_size != ws[0].group_size || ws[i].scale_dtype != ws[0].scale_dtype)))
@@ -395,59 +324,90 @@ static int qlinear_multi_impl(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight
                         "grouped weights must share encoding, K, group size and scale dtype");
     }
     if (int rc = check_io(x_dtype, y_dtype, rows)) return rc;
-    if (!aligned(x, 16)) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "activations must be 16-byte aligned");
-    bool gemm = true;
+    gemm = true;
     for (uint32_t i = 0; i < count && gemm; i++)
         gemm = has_prefill_gemm(ws[i].encoding, (uint32_t)ws[i].rows, (uint32_t)ws[i].cols, rows,
                                 y_dtype == DYNINFER_DTYPE_BF16);
     if (gemm && (uint64_t)rows * ws[0].cols >= (1ull << 31))
         return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "prefill: rows * K must stay below 2^31 (32-bit activation offsets)");
-    const uint64_t need = gemm ? dmx::prefill_workspace_bytes(rows, (uint32_t)ws[0].cols) : 0;
-    if (noalloc && need > kScratchBytes)
-        return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
-                    "qlinear_multi_noalloc: the prefill staging of " + std::to_string(rows) + " rows x K " +
-                        std::to_string(ws[0].cols) + " needs " + std::to_string(need) +
-                        " bytes, more than the static scratch of " + std::to_string(kScratchBytes) +
-                        " bytes; split the rows or call dyninfer_mi355x_qlinear_multi");
+    need = gemm ? dmx::prefill_workspace_bytes(rows, (uint32_t)ws[0].cols) : 0;
+    return 0;
+}
+
+// qlinear_multi with the caller's workspace, or (noalloc) with the device's
+// static scratch array.
+static int qlinear_multi_impl(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws, uint32_t count, const void* x,
+                              uint32_t x_dtype, uint32_t rows, void* const* ys, uint32_t y_dtype, void* workspace,
+                              uint64_t workspace_bytes, void* stream, bool noalloc) {
+    if (int rc = check_ctx(ctx)) return rc;
+    bool gemm = false;
+    uint64_t need = 0;
+    if (int rc = plan_multi(ws, count, x_dtype, rows, y_dtype, gemm, need)) return rc;
+    if (!x || !ys) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "x / y pointers are NULL");
+    for (uint32_t i = 0; i < count; i++) {
+        if (!ys[i]) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "output pointer is NULL");
+        if (!aligned(ys[i], esize(y_dtype))) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "output is misaligned");
+    }
+    if (!aligned(x, 16)) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "activations must be 16-byte aligned");
+    uint8_t* work = nullptr;
+    if (noalloc) {
+        if (need > kScratchBytes)
+            return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
+                        "qlinear_multi_noalloc: the prefill staging of " + std::to_string(rows) + " rows x K " +
+                            std::to_string(ws[0].cols) + " needs " + std::to_string(need) +
+                            " bytes, more than the static scratch of " + std::to_string(kScratchBytes) +
+                            " bytes; split the rows or call dyninfer_mi355x_qlinear_multi");
+        work = ctx->scratch;
+    } else if (need) {
+        if (!workspace || workspace_bytes < need)
+            return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT,
+                        "prefill of " + std::to_string(rows) + " rows x K " + std::to_string(ws[0].cols) +
+                            " needs a device workspace of " + std::to_string(need) + " bytes (got " +
+                            (workspace ? std::to_string(workspace_bytes) + " bytes" : std::string("NULL")) +
+                            "); size it with dyninfer_mi355x_prefill_workspace_bytes");
+        if (!aligned(workspace, 256))
+            return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "the prefill workspace must be 256-byte aligned");
+        work = static_cast<uint8_t*>(workspace);
+    }
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipError_t e;
-    if (gemm) {
-        Workspace wk;
-        wk.st = st;
-        if (noalloc) {
-            wk.p = ctx->scratch;
-            e = prefill(ws, count, x, x_dtype, rows, ys, y_dtype, wk.p, st);
-        } else {
-            std::lock_guard<std::mutex> lock(ctx->mu);
-            e = acquire_workspace(ctx, st, need, wk);
-            if (e != hipSuccess) return hip_fail(e, "hipMallocAsync (prefill staging workspace)");
-            e = prefill(ws, count, x, x_dtype, rows, ys, y_dtype, wk.p, st);
-        }
-    } else {
-        e = gemv_rows(ws, count, x, x_dtype, rows, ys, y_dtype, st);
-    }
+    const hipError_t e = gemm ? prefill(ws, count, x, x_dtype, rows, ys, y_dtype, work, st)
+                              : gemv_rows(ws, count, x, x_dtype, rows, ys, y_dtype, st);
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return DYNINFER_MI355X_OK;
+}
+
+int dyninfer_mi355x_prefill_workspace_bytes(const dyninfer_qweight_t* ws, uint32_t count, uint32_t rows,
+                                            uint32_t x_dtype, uint32_t y_dtype, uint64_t* out_bytes) {
+    if (!out_bytes) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "out_bytes is NULL");
+    *out_bytes = 0;
+    bool gemm = false;
+    uint64_t need = 0;
+    if (int rc = plan_multi(ws, count, x_dtype, rows, y_dtype, gemm, need)) return rc;
+    *out_bytes = need;
     return DYNINFER_MI355X_OK;
 }
 
 int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws, uint32_t count,
                                   const void* x, uint32_t x_dtype, uint32_t rows, void* const* ys, uint32_t y_dtype,
-                                  void* stream) {
-    return qlinear_multi_impl(ctx, ws, count, x, x_dtype, rows, ys, y_dtype, stream, false);
+                                  void* workspace, uint64_t workspace_bytes, void* stream) {
+    return qlinear_multi_impl(ctx, ws, count, x, x_dtype, rows, ys, y_dtype, workspace, workspace_bytes, stream,
+                              false);
 }
 
 int dyninfer_mi355x_qlinear_multi_noalloc(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws, uint32_t count,
                                           const void* x, uint32_t x_dtype, uint32_t rows, void* const* ys,
                                           uint32_t y_dtype, void* stream) {
-    return qlinear_multi_impl(ctx, ws, count, x, x_dtype, rows, ys, y_dtype, stream, true);
+    return qlinear_multi_impl(ctx, ws, count, x, x_dtype, rows, ys, y_dtype, nullptr, 0, stream, true);
 }
 
 int dyninfer_mi355x_qlinear(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* w, const void* x, uint32_t x_dtype,
-                            uint32_t rows, void* y, uint32_t y_dtype, void* stream) {
+                            uint32_t rows, void* y, uint32_t y_dtype, void* workspace, uint64_t workspace_bytes,
+                            void* stream) {
     void* ys[1] = {y};
-    return dyninfer_mi355x_qlinear_multi(ctx, w, 1, x, x_dtype, rows, ys, y_dtype, stream);
+    return dyninfer_mi355x_qlinear_multi(ctx, w, 1, x, x_dtype, rows, ys, y_dtype, workspace, workspace_bytes,
+                                         stream);
 }
 
 int dyninfer_mi355x_dequant(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* w, float* out, void* stream) {

@@ -17,14 +17,21 @@
  *     thread (thread-local, unlike the wrapper's process-global g_last_error,
  *     wrapper.c:238);
  *   - opaque context handle with open/close pair (wrapper.h:39-60);
- *   - weights, activations and outputs are caller-owned device memory; the library
- *     never repacks or copies weights and derives no parameters from them
- *     (README.md:5-9, crates/dyninfer-compiler/src/lib.rs:630); its one device
- *     allocation is the prefill staging workspace of a prefill GEMM call (see
- *     dyninfer_mi355x_qlinear), owned by the context;
- *   - work is enqueued asynchronously on the caller's HIP stream (`stream` is a
- *     hipStream_t passed as void*; NULL = the null stream); concurrent calls on
- *     distinct streams are allowed; there is no CPU fallback (README.md:83-84).
+ *   - weights, activations, outputs and the prefill workspace are caller-owned
+ *     device memory; the library never repacks or copies weights and derives no
+ *     parameters from them (README.md:5-9, crates/dyninfer-compiler/src/lib.rs:630),
+ *     and it allocates no device memory: a call's temporary (the prefill staging of
+ *     dyninfer_mi355x_qlinear) lives in a workspace the caller sizes with
+ *     dyninfer_mi355x_prefill_workspace_bytes and passes in, the counterpart of the
+ *     reference's device-local, non-persistent GPU temporaries
+ *     (docs/quantization/mlx-affine-u4.md:26-27) bound like its parameters as
+ *     caller-described ranges (third_party/iree_runtime_c_api/wrapper.h:18-29);
+ *   - the context is immutable after dyninfer_mi355x_open (no locks, no caches):
+ *     any number of threads may call with one context at once; work is enqueued
+ *     asynchronously on the caller's HIP stream (`stream` is a hipStream_t passed as
+ *     void*; NULL = the null stream); calls in flight at the same time (distinct
+ *     streams or threads) need distinct workspaces; there is no CPU fallback
+ *     (README.md:83-84).
  */
 #ifndef DYNINFER_MI355X_H
 #define DYNINFER_MI355X_H
@@ -129,27 +136,34 @@ const char* dyninfer_mi355x_last_error(void);
  *     of 64 (256 for the super-block
  *     encodings): x is staged once per call as f16 MFMA operand fragments,
  *     each row scaled by a power of two (RNE) and the rows padded with zeros to a
- *     multiple of 32; then one MFMA GEMM per weight decodes the GGUF blocks or MLX words
- *     straight into MFMA operands.  The staging
- *     needs a device workspace of round_up(round_up(rows, 32)*K*2, 256) +
- *     4*round_up(rows, 256) bytes.  The context keeps one
- *     per stream handle, allocated on first use and grown in stream order
- *     (hipMallocAsync; the old one hipFreeAsync'd behind the work that used it), and
- *     releases them at dyninfer_mi355x_close.  Under stream capture the call uses no
- *     context workspace (a later regrowth could free it while the graph names it): it
- *     allocates and frees a transient one in stream order, which the captured graph
- *     then does on every replay (the no-allocation variant below avoids that).
- *     A stream that is destroyed while the context lives must have finished its work
- *     first (its handle may be reused by a new stream).  Every other case (K not a
- *     multiple of 64, Q4_0, Q6_K, Q4_K, Q5_K and IQ4_XS at 17..32 rows with K <= 8192)
- *     runs the GEMV kernels over 16-row chunks and needs no workspace.
- * Error bound: |y - y_exact| <= 2^-10 * sum_k |w||x| plus f32 accumulation, where a
- * prefill activation more than 2^29 below its row's largest magnitude may also be
- * flushed to f16 subnormals (absolute 2^-40 * max|x| each).
+ *     multiple of 32, into the caller's workspace; then one MFMA GEMM per weight
+ *     decodes the GGUF blocks or MLX words straight into MFMA operands.  Every other
+ *     case (K not a multiple of 64, Q4_0, Q6_K, Q4_K, Q5_K and IQ4_XS at 17..32 rows
+ *     with K <= 8192) runs the GEMV kernels over 16-row chunks.
+ * workspace: device memory of at least dyninfer_mi355x_prefill_workspace_bytes() for
+ *   the same arguments, 256-byte aligned, or NULL when that size is 0 (every call of
+ *   1..16 rows, and the 16-row-chunk prefill).  A call whose workspace is missing,
+ *   misaligned or too small fails with DYNINFER_MI355X_ERR_INVALID_ARGUMENT before
+ *   anything is enqueued.  The call's kernels write and read it in stream order; the
+ *   caller may reuse it for the next call on the same stream, and must not touch it
+ *   (or hand it to a call on another stream) until this call's work has completed.
+ *   Nothing the workspace holds carries over between calls.
+ * Error bound (per output, plus f32 accumulation error), with |w||x| summed over k:
+ *   GGUF Q4_0, Q4_1, Q8_0, IQ4_XS and MLX U4: 2^-10 * sum |w||x| (IQ4_XS prefill:
+ *   3 * 2^-11 * sum |w||x|);
+ *   Q6_K: (2^-10 + 2^-11) * sum |w||x|;
+ *   Q4_K and Q5_K, whose prefill and 5..16-row weights are RNE_f16(q*RNE_f16(d*sc) -
+ *   RNE_f16(dmin*m)): (2^-10 + 2^-11) * sum |w||x| + 2^-10 * sum |dmin*m||x|, the
+ *   offset term counting each weight's dmin*m, which may nearly cancel q*d*sc;
+ *   MLX U4 with f32 scales and biases (each rounded to f16 before q*s + b) adds
+ *   2^-11 * sum (q*|s| + |b|)|x|;
+ *   and a prefill activation more than 2^29 below its row's largest magnitude may also
+ *   be flushed to f16 subnormals (absolute 2^-40 * max|x| each).
  */
 int dyninfer_mi355x_qlinear(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* w,
                             const void* x, uint32_t x_dtype, uint32_t rows,
-                            void* y, uint32_t y_dtype, void* stream);
+                            void* y, uint32_t y_dtype, void* workspace, uint64_t workspace_bytes,
+                            void* stream);
 
 /*
  * Several weights that share one activation (q/k/v, gate/up) in a single launch:
@@ -161,16 +175,29 @@ int dyninfer_mi355x_qlinear(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t
  */
 int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws,
                                   uint32_t count, const void* x, uint32_t x_dtype, uint32_t rows,
-                                  void* const* ys, uint32_t y_dtype, void* stream);
+                                  void* const* ys, uint32_t y_dtype, void* workspace,
+                                  uint64_t workspace_bytes, void* stream);
+
+/*
+ * Device workspace bytes that dyninfer_mi355x_qlinear (count = 1) or _qlinear_multi
+ * needs for these weights, rows and dtypes, in *out_bytes: 0 for every call that runs
+ * no prefill GEMM, else round_up(round_up(rows, 32)*K*2, 256) + 4*round_up(rows, 256)
+ * (the f16 operand fragments of x, then one f32 row factor per row).  Validates the
+ * arguments as the call does (same status codes, pointers checked for alignment only);
+ * host-only, enqueues nothing.  The reference's temporary-memory qualification
+ * (docs/quantization/mlx-affine-u4.md:52-54) reads this figure.
+ */
+int dyninfer_mi355x_prefill_workspace_bytes(const dyninfer_qweight_t* ws, uint32_t count, uint32_t rows,
+                                            uint32_t x_dtype, uint32_t y_dtype, uint64_t* out_bytes);
 
 /*
  * No counterpart in the reference.  For callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops or harnesses that forbid hipMalloc):
  * dyninfer_mi355x_qlinear_multi with the prefill staging workspace (a call that runs the
- * prefill GEMM: round_up(round_up(rows, 32)*K*2, 256) + 4*round_up(rows, 256) bytes)
- * taken from a static device array of DYNINFER_MI355X_NOALLOC_SCRATCH_BYTES per device
- * (allocated when the library's code object loads on a device, held until the process
- * ends) instead of a stream-ordered allocation.  A larger staging is rejected with
+ * prefill GEMM: dyninfer_mi355x_prefill_workspace_bytes) taken from a static device
+ * array of DYNINFER_MI355X_NOALLOC_SCRATCH_BYTES per device (allocated when the
+ * library's code object loads on a device, held until the process ends) instead of a
+ * caller-supplied workspace, for callers that can neither allocate nor hold one.  A larger staging is rejected with
  * DYNINFER_MI355X_ERR_UNSUPPORTED (2048 rows fit K <= 8128, 512 rows K <= 32704).
  * Calls no hipMalloc/hipFree or allocating routine.  Every call on one device shares
  * that device's array and leaves it holding the last staging: calls that overlap on

@@ -21,3 +21,28 @@ def ctx():
     c = d.Context(0)
     yield c
     c.close()
+
+
+def _graph_node_types(g):
+    """Node types (hipGraphNodeType: 0 kernel, 10 memory allocation, 11 memory
+    free, ...) of a captured torch.cuda.CUDAGraph(keep_graph=True), read
+    through the process's one HIP runtime (the one torch loaded)."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    graph = ctypes.c_void_p(g.raw_cuda_graph())
+    n = ctypes.c_size_t(0)
+    assert hip.hipGraphGetNodes(graph, None, ctypes.byref(n)) == 0
+    nodes = (ctypes.c_void_p * n.value)()
+    assert hip.hipGraphGetNodes(graph, nodes, ctypes.byref(n)) == 0
+    types = []
+    for i in range(n.value):
+        t = ctypes.c_int(-1)
+        assert hip.hipGraphNodeGetType(ctypes.c_void_p(nodes[i]), ctypes.byref(t)) == 0
+        types.append(t.value)
+    return types
+
+
+@pytest.fixture
+def graph_node_types():
+    return _graph_node_types

@@ -100,7 +100,7 @@ def test_gguf_data_component_byte_total(enc, rows, cols, nbytes):
     lib = d.library()
     wc = w(enc, rows, cols, data_bytes=nbytes - 2).c()
     rc = lib.dyninfer_mi355x_qlinear(ctypes.c_void_p(1), ctypes.byref(wc), 0x1000, d.DTYPE_F32, 1, 0x2000,
-                                     d.DTYPE_F32, None)
+                                     d.DTYPE_F32, None, 0, None)
     assert rc == d.ERR_UNSUPPORTED  # rejected host-side before any launch
 
 
@@ -120,7 +120,8 @@ def test_mlx_component_byte_lengths():
 def test_calls_without_context_fail_cleanly():
     lib = d.library()
     wc = w(d.ENC_Q4_0).c()
-    rc = lib.dyninfer_mi355x_qlinear(None, ctypes.byref(wc), 0x1000, d.DTYPE_F32, 1, 0x2000, d.DTYPE_F32, None)
+    rc = lib.dyninfer_mi355x_qlinear(None, ctypes.byref(wc), 0x1000, d.DTYPE_F32, 1, 0x2000, d.DTYPE_F32, None, 0,
+                                     None)
     assert rc == d.ERR_INVALID_ARGUMENT
     assert "context" in lib.dyninfer_mi355x_last_error().decode()
     rc = lib.dyninfer_mi355x_dequant(None, ctypes.byref(wc), 0x1000, None)
@@ -149,6 +150,70 @@ def test_last_error_is_thread_local():
     t.join()
     assert seen == [""]
     assert lib.dyninfer_mi355x_last_error().decode() == main_msg
+
+
+def _ws_bytes(m, k):
+    """The documented workspace size: round_up(round_up(m, 32)·k·2, 256) + 4·round_up(m, 256)."""
+    return (((m + 31) // 32 * 32 * k * 2 + 255) // 256) * 256 + 4 * ((m + 255) // 256 * 256)
+
+
+@pytest.mark.parametrize("enc,k", [(d.ENC_Q4_0, 1024), (d.ENC_Q4_1, 1024), (d.ENC_Q8_0, 3072), (d.ENC_Q6_K, 4096),
+                                   (d.ENC_Q4_K, 4096), (d.ENC_IQ4_XS, 1024)])
+def test_prefill_workspace_bytes_follows_the_routing(enc, k):
+    """0 for decode rows and for the 16-row-chunk prefill, the documented staging size
+    whenever the call runs the prefill GEMM (host-only query, no device needed)."""
+    ws = [w(enc, 3072, k), w(enc, 1024, k)]
+    for rows in (1, 4, 16):
+        assert d.prefill_workspace_bytes(ws, rows) == 0
+    chunked = enc in (d.ENC_Q4_0, d.ENC_Q6_K, d.ENC_Q4_K, d.ENC_Q5_K, d.ENC_IQ4_XS) and k <= 8192
+    for rows in (17, 32):
+        assert d.prefill_workspace_bytes(ws, rows, d.DTYPE_BF16, d.DTYPE_BF16) == (0 if chunked else _ws_bytes(rows, k))
+    for rows in (33, 128, 512, 2048, 3000):
+        assert d.prefill_workspace_bytes(ws, rows, d.DTYPE_BF16, d.DTYPE_BF16) == _ws_bytes(rows, k)
+        assert d.prefill_workspace_bytes(ws[:1], rows) == _ws_bytes(rows, k)
+
+
+def test_prefill_workspace_bytes_validates_like_the_call():
+    lib = d.library()
+    arr = (d._QWeightC * 2)(w(d.ENC_Q4_0, 64, 1024).c(), w(d.ENC_Q4_0, 64, 512).c())
+    n = ctypes.c_uint64(7)
+    assert lib.dyninfer_mi355x_prefill_workspace_bytes(arr, 2, 64, d.DTYPE_F32, d.DTYPE_F32,
+                                                       ctypes.byref(n)) == d.ERR_INVALID_ARGUMENT
+    assert "grouped weights must share" in lib.dyninfer_mi355x_last_error().decode() and n.value == 0
+    assert lib.dyninfer_mi355x_prefill_workspace_bytes(arr, 1, 64, d.DTYPE_F16, d.DTYPE_F32,
+                                                       ctypes.byref(n)) == d.ERR_UNSUPPORTED
+    assert lib.dyninfer_mi355x_prefill_workspace_bytes(arr, 1, 0, d.DTYPE_F32, d.DTYPE_F32,
+                                                       ctypes.byref(n)) == d.ERR_INVALID_ARGUMENT
+    assert lib.dyninfer_mi355x_prefill_workspace_bytes(arr, 5, 64, d.DTYPE_F32, d.DTYPE_F32,
+                                                       ctypes.byref(n)) == d.ERR_INVALID_ARGUMENT
+    assert lib.dyninfer_mi355x_prefill_workspace_bytes(arr, 1, 64, d.DTYPE_F32, d.DTYPE_F32,
+                                                       None) == d.ERR_INVALID_ARGUMENT
+    assert lib.dyninfer_mi355x_prefill_workspace_bytes(arr, 1, 64, d.DTYPE_F32, d.DTYPE_F32,
+                                                       ctypes.byref(n)) == d.OK
+    assert n.value == _ws_bytes(64, 1024)
+
+
+def test_prefill_rejects_a_missing_or_short_workspace_before_launching():
+    """A prefill call checks its workspace host-side (pointer, size, 256-byte alignment)
+    and enqueues nothing when it is wrong; the context pointer is only checked for NULL
+    here, so no device is touched."""
+    lib = d.library()
+    wc = w(d.ENC_Q4_0, 64, 1024).c()
+    need = _ws_bytes(64, 1024)
+    fake = ctypes.c_void_p(1)
+    for ptr, nbytes in ((None, 0), (None, need), (0x10000, need - 1), (0x10000 + 128, need)):
+        rc = lib.dyninfer_mi355x_qlinear(fake, ctypes.byref(wc), 0x1000, d.DTYPE_F32, 64, 0x2000, d.DTYPE_F32, ptr,
+                                         nbytes, None)
+        assert rc == d.ERR_INVALID_ARGUMENT, (ptr, nbytes)
+        msg = lib.dyninfer_mi355x_last_error().decode()
+        assert "workspace" in msg, msg
+    assert f"needs a device workspace of {need} bytes" in (
+        lib.dyninfer_mi355x_qlinear(fake, ctypes.byref(wc), 0x1000, d.DTYPE_F32, 64, 0x2000, d.DTYPE_F32, None, 0,
+                                    None) and lib.dyninfer_mi355x_last_error().decode())
+
+
+def test_close_of_null_context_is_ok():
+    assert d.library().dyninfer_mi355x_close(None) == d.OK
 
 
 def test_registry_output_buffer_too_small():

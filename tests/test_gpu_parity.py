@@ -323,12 +323,13 @@ def test_gemv_mlx_f32_io(ctx):
 # Shapes select every wave tile (TM = 1, 2, 4 row blocks of 32) and K split
 # (S = 1, 2, 4 slices per workgroup) the launcher picks, with ragged rows and
 # columns: (m, n, k) -> (TM, S).
-GEMM_SHAPES = [(17, 130, 96),      # TM1 S1, K of three blocks
+GEMM_SHAPES = [(17, 130, 64),      # K of one 64-k chunk: Q4_1/Q8_0 GEMM (Q4_0 16-row GEMV chunks)
+               (40, 256, 64),      # one chunk, every type on the GEMM
+               (64, 1000, 64),     # one chunk, ragged N
                (17, 256, 1024),    # TM1 S4
                (20, 20000, 256),   # TM1 S2
                (33, 512, 2048),    # TM2 S4
                (50, 20000, 256),   # TM2 S2
-               (64, 1000, 96),     # TM2 S1
                (100, 300, 128),    # TM4 S2, two-block slices
                (200, 384, 1024),   # TM4 S4, ragged last row tile
                (512, 3072, 1024),  # TM4 S4 (Qwen3-0.6B gate/up)
@@ -440,6 +441,7 @@ def test_gemm_offset_weights(ctx, gtype, m, n, k):
 # a dword (K / group odd with 16-bit scales) and component bases 2 bytes into a
 # dword.
 GEMM_MLX_CASES = [
+    (17, 130, 64, 32, oracle.D_BF16), (40, 256, 64, 64, oracle.D_F16),  # K of one 64-k chunk
     (17, 256, 1024, 64, oracle.D_BF16), (33, 512, 2048, 32, oracle.D_F16), (50, 20000, 256, 128, oracle.D_BF16),
     (100, 300, 1088, 64, oracle.D_BF16), (200, 384, 1024, 32, oracle.D_F32), (512, 3072, 1024, 64, oracle.D_BF16),
     (512, 1024, 3072, 64, oracle.D_F16), (2048, 3072, 1024, 128, oracle.D_BF16), (2000, 3000, 1024, 64, oracle.D_F32),

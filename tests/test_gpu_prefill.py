@@ -315,49 +315,102 @@ def test_zero_rows_super_block_encodings(ctx, kind, rows):
         assert not np.any(y[:, :zr]), np.abs(y[:, :zr]).max()
 
 
-# ----------------------------------------------------------------- the prefill staging workspace
-def test_prefill_workspace_growth_across_calls_and_streams(ctx):
-    """The context's staging workspace per stream: grown in stream order when a
-    longer prefill arrives (the old one released behind the work using it),
-    reused by shorter ones; two streams keep distinct workspaces."""
+# ----------------------------------------------------------------- the caller's prefill workspace
+HIP_NODE_KERNEL, HIP_NODE_MEM_ALLOC, HIP_NODE_MEM_FREE = 0, 10, 11
+
+
+def test_prefill_two_threads_two_streams_one_context(ctx):
+    """One context, two host threads, each issuing prefill calls of several sizes
+    (and a decode call) on a stream of its own with a workspace of its own,
+    reused call after call: the context is immutable, so the calls need no
+    lock, and every output matches the oracle."""
+    import threading
     n, k = 512, 1024
     w, wf = make(oracle.Q4_0, n, k, seed=31)
-    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
-    cases = []
-    for i, (rows, st) in enumerate([(17, sa), (2048, sa), (64, sa), (1500, sb), (33, sb), (3000, sa)]):
-        xd, x = xs(rows, k, seed=100 + i, bf16=i % 2 == 1)
-        with torch.cuda.stream(st):
-            y = ctx.qlinear(w, xd, stream=st)
-        cases.append((y, x))
+    plans = {0: [(17, False), (2048, True), (64, False), (4, True)], 1: [(1500, True), (33, False), (3000, True)]}
+    inputs = {t: [xs(rows, k, seed=100 + 10 * t + i, bf16=bf) for i, (rows, bf) in enumerate(p)]
+              for t, p in plans.items()}
+    need = {t: max(d.prefill_workspace_bytes([w], rows, d.DTYPE_F32, d.DTYPE_F32) for rows, _ in p)
+            for t, p in plans.items()}
+    assert need[0] == d.prefill_workspace_bytes([w], 2048) and need[1] == d.prefill_workspace_bytes([w], 3000)
+    work = {t: torch.empty(need[t], dtype=torch.uint8, device="cuda") for t in plans}
+    streams = {t: torch.cuda.Stream() for t in plans}
+    outs, errors = {t: [] for t in plans}, []
+    start = threading.Barrier(len(plans))
     torch.cuda.synchronize()
-    for y, x in cases:
-        assert err_of(y, x, wf) <= F16X2
+
+    def run(t):
+        try:
+            st = streams[t]
+            with torch.cuda.stream(st):
+                start.wait()
+                for xd, _ in inputs[t]:
+                    y = torch.empty((xd.shape[0], n), dtype=torch.float32, device="cuda")
+                    ctx.qlinear(w, xd, y, stream=st, workspace=work[t])
+                    outs[t].append(y)
+            st.synchronize()
+        except Exception as e:  # surfaced by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(t,)) for t in plans]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for t in plans:
+        for y, (_, x) in zip(outs[t], inputs[t]):
+            assert err_of(y, x, wf) <= F16X2, (t, y.shape)
 
 
-def test_prefill_graph_capture_replays(ctx):
-    """A prefill captured in a HIP graph (its staging a transient stream-ordered
-    allocation owned by the graph) and replayed three times, with eager prefill
-    calls of other sizes between the replays: every replay equals the eager result."""
+def test_prefill_graph_capture_replays_without_allocations(ctx, graph_node_types):
+    """A prefill captured in a HIP graph with a caller workspace allocated
+    beforehand: the graph holds kernel nodes only (no allocation or free
+    node), and three replays, with eager prefill calls of other sizes between
+    them, each equal the eager result bit for bit."""
     n, k, rows = 768, 1024, 200
     w, wf = make(oracle.Q4_0, n, k, seed=41)
     xd, x = xs(rows, k, seed=42, bf16=False)
     eager = ctx.qlinear(w, xd).cpu().numpy()
     assert err_of(torch.from_numpy(eager), x, wf) <= F16X2
     y = torch.empty((rows, n), device="cuda")
+    work = torch.empty(d.prefill_workspace_bytes([w], rows), dtype=torch.uint8, device="cuda")
     st = torch.cuda.Stream()
     with torch.cuda.stream(st):
-        ctx.qlinear(w, xd, y, stream=st)
+        ctx.qlinear(w, xd, y, stream=st, workspace=work)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
+        g = torch.cuda.CUDAGraph(keep_graph=True)
         with torch.cuda.graph(g, stream=st):
-            ctx.qlinear(w, xd, y, stream=st)
+            ctx.qlinear(w, xd, y, stream=st, workspace=work)
     torch.cuda.synchronize()
+    types = graph_node_types(g)
+    assert types and all(t == HIP_NODE_KERNEL for t in types), types
+    g.instantiate()
     for i in range(3):
         y.fill_(float("nan"))
         other, _ = xs(300 + 100 * i, k, seed=50 + i, bf16=True)
-        ctx.qlinear(w, other)  # eager work between the replays
+        ctx.qlinear(w, other)  # eager work between the replays (its own workspace)
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(y.cpu().numpy().view(np.uint32), eager.view(np.uint32)), i
     del g
+
+
+def test_context_close_after_prefills_on_two_streams():
+    """A second context runs prefills on two streams, then closes with status OK
+    (Context.close raises on any other status)."""
+    n, k = 256, 1024
+    w, wf = make(oracle.Q8_0, n, k, seed=61)
+    c2 = d.Context(0)
+    cases = []
+    for i, st in enumerate((torch.cuda.Stream(), torch.cuda.Stream())):
+        xd, x = xs(100 + 50 * i, k, seed=62 + i, bf16=i == 1)
+        with torch.cuda.stream(st):
+            cases.append((c2.qlinear(w, xd, stream=st), x))
+    torch.cuda.synchronize()
+    c2.close()
+    assert c2._h is None
+    for y, x in cases:
+        assert err_of(y, x, wf) <= F16X2

@@ -3,8 +3,9 @@ through the C ABI: the same kernels with the prefill staging taken from the
 device's static scratch array instead of a stream-ordered allocation, so the
 outputs must be bit-identical, and both within the f16 bound of the oracle.
 Two prefill calls in a row (the second smaller, over the first call's
-leftover staging), a decode call, and a staging beyond the scratch size
-(rejected host-side, after which calls still work)."""
+leftover staging), a decode call, a staging beyond the scratch size
+(rejected host-side, after which calls still work), and a prefill captured in
+a HIP graph (kernel nodes only) whose replays equal the eager call."""
 import numpy as np
 import pytest
 import torch
@@ -90,3 +91,44 @@ def test_noalloc_decode_and_size_limit(ctx):
     assert np.array_equal(ref[0].view(np.uint32), got[0].view(np.uint32))
     ref, got = _both(ctx, ws, x)
     assert np.array_equal(ref[0].view(np.uint32), got[0].view(np.uint32))
+
+
+def test_noalloc_prefill_graph_capture_replays(ctx, graph_node_types):
+    """The callers this entry point is for capture it: a 200 x 768 x 1024 Q4_0
+    prefill captured in a HIP graph holds kernel nodes only (no allocation or
+    free node), and three replays, each after eager no-allocation calls of
+    other sizes that overwrite the shared scratch array, equal the eager call
+    bit for bit."""
+    k, rows = 1024, 200
+    ws, datas = _weights(k, [768], seed=21)
+    x = oracle.randn(rows * k, seed=22).reshape(rows, k)
+    xd = dev(x)
+    eager = [torch.empty((rows, 768), dtype=torch.float32, device="cuda")]
+    ctx.qlinear_multi(ws, xd, eager, noalloc=True)
+    torch.cuda.synchronize()
+    eager = eager[0].cpu().numpy()
+    y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(oracle.Q4_0, datas[0], 768, k))
+    assert oracle.normalized_error(eager, y64, absdot) <= F16X2
+    y = [torch.empty((rows, 768), dtype=torch.float32, device="cuda")]
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        ctx.qlinear_multi(ws, xd, y, stream=st, noalloc=True)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph(keep_graph=True)
+        with torch.cuda.graph(g, stream=st):
+            ctx.qlinear_multi(ws, xd, y, stream=st, noalloc=True)
+    torch.cuda.synchronize()
+    types = graph_node_types(g)
+    assert types and all(t == 0 for t in types), types
+    g.instantiate()
+    for i in range(3):
+        other_rows = 300 + 150 * i
+        xo = dev(oracle.randn(other_rows * k, seed=23 + i).reshape(other_rows, k))
+        yo = [torch.empty((other_rows, 768), dtype=torch.float32, device="cuda")]
+        ctx.qlinear_multi(ws, xo, yo, noalloc=True)  # overwrites the scratch staging
+        y[0].fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(y[0].cpu().numpy().view(np.uint32), eager.view(np.uint32)), i
+    del g
