@@ -20,6 +20,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = [
     "gemv_q6_k.hip", "gemv_q4_k.hip", "gemv_q5_k.hip", "gemv_iq4_xs.hip", "gemv_q4_0.hip", "gemv_q4_1.hip", "gemv_q8_0.hip", "gemv_mlx_u4.hip",
+    "gemm_q6_k.hip", "gemm_q5_k.hip", "gemm_iq4_xs.hip", "gemm_q4_k.hip", "gemm_q8_0.hip", "gemm_mlx_u4.hip",
+    "gemm_q4_0.hip", "gemm_q4_1.hip",
     "gemv.hip", "gemv_mfma.hip", "gemm.hip", "xprep.hip", "dequant.hip", "embedding.hip",
     "capi.cpp", "registry.cpp", "gguf.cpp", "safetensors.cpp",
 ]

@@ -39,13 +39,17 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
     return __uint_as_float(bits << 16);
 }
 
-// f32 -> bf16 round-to-nearest-even (NaN quieted).
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+// f32 -> bf16 round-to-nearest-even (NaN quieted) by gfx950's v_cvt_pk_bf16_f32,
+// two values per instruction: bit-identical on this part to the integer form
+// (u + 0x7FFF + ((u >> 16) & 1)) >> 16 with NaN -> (u >> 16) | 0x40, over every
+// class of input (ties, subnormals, infinities, NaN payloads).  The integer form
+// with its NaN test compiled to a divergent branch per value.
+typedef float dmx_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 dmx_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(dmx_f32x2{lo, hi}, dmx_bf16x2));
 }
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) { return (uint16_t)f32x2_to_bf16x2_bits(f, 0.0f); }
 
 // Byte lane i of a dword as float (v_cvt_f32_ubyte{0..3}).
 template <int I>

@@ -1,0 +1,4 @@
+// Prefill GEMM kernels of one encoding (compiled on their own, in parallel with the others).
+#include "gemm_impl.hpp"
+
+template hipError_t dmx::gemm::launch_plan<dmx::ENC_Q4_1>(const GemmArgs&, const GemmPlan&, hipStream_t);

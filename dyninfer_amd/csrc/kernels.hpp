@@ -131,6 +131,14 @@ inline uint64_t prefill_workspace_bytes(uint32_t M, uint32_t K) {
     return prefill_xh_bytes(M, K) + (((uint64_t)M + 255u) & ~(uint64_t)255u) * 4u;
 }
 
+// Prefill GEMM launch plan (gemm.hip): workgroups of four waves, each owning a
+// (32·tm) x (32·nb·4/s) tile of Y, the waves split over s K slices.
+struct GemmPlan {
+    uint32_t tm, nb, s;
+    uint32_t mt, nt;  // workgroup tiles along M and N
+};
+GemmPlan gemm_plan(uint32_t enc, uint32_t N, uint32_t K, uint32_t M);
+
 // Prefill GEMM on MFMA (gemm.hip): Y[M, N] = diag(rs) · (Xh[M, K] · Wᵀ), Xh/rs
 // from xprep_launch(gemm_layout(enc)); Y f32 or bf16.  gemm_layout returns ~0u
 // for encodings without a GEMM.  The weight: GGUF blocks at w, or MLX U4

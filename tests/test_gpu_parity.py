@@ -320,22 +320,27 @@ def test_gemv_mlx_f32_io(ctx):
 
 
 # ----------------------------------------------------------------- GEMM (MFMA prefill)
-# Shapes select every wave tile (TM = 1, 2, 4 row blocks of 32) and K split
-# (S = 1, 2, 4 slices per workgroup) the launcher picks, with ragged rows and
-# columns: (m, n, k) -> (TM, S).
-GEMM_SHAPES = [(17, 130, 64),      # K of one 64-k chunk: Q4_1/Q8_0 GEMM (Q4_0 16-row GEMV chunks)
-               (40, 256, 64),      # one chunk, every type on the GEMM
+# Shapes that select every launch plan the GEMM's planner picks for Q4_0, Q4_1
+# and Q8_0: TM = 2 or 4 activation row blocks and NB = 2 or 3 weight row
+# blocks (of 32) per wave, S = 1, 2 or 4 K slices per 4-wave workgroup; plus
+# ragged rows and columns, one-chunk K, and chunk counts no split divides.
+# (m, n, k) -> (TM, NB, S) for Q4_0:
+GEMM_SHAPES = [(17, 130, 64),      # one 64-k chunk: Q4_1/Q8_0 GEMM (Q4_0 takes 16-row GEMV chunks)
+               (40, 256, 64),      # one chunk, every type on the GEMM (2, 2, 1)
                (64, 1000, 64),     # one chunk, ragged N
-               (17, 256, 1024),    # TM1 S4
-               (20, 20000, 256),   # TM1 S2
-               (33, 512, 2048),    # TM2 S4
-               (50, 20000, 256),   # TM2 S2
-               (100, 300, 128),    # TM4 S2, two-block slices
-               (200, 384, 1024),   # TM4 S4, ragged last row tile
-               (512, 3072, 1024),  # TM4 S4 (Qwen3-0.6B gate/up)
-               (512, 1024, 3072),  # TM4 S4 (down)
-               (512, 6144, 1024),  # TM4 S2
-               (2048, 3072, 1024),  # TM4 S1
+               (17, 256, 1024),    # (2, 2, 4)
+               (20, 20000, 256),   # (2, 3, 2)
+               (33, 512, 2048),    # (2, 2, 4)
+               (50, 20000, 256),   # (2, 3, 2)
+               (100, 300, 128),    # (2, 2, 2), two-chunk slices
+               (200, 384, 1024),   # ragged last row tile
+               (512, 3072, 1024),  # (2, 3, 4) (Qwen3-0.6B gate/up)
+               (512, 1024, 3072),  # (2, 2, 4) (down)
+               (512, 6144, 1024),
+               (768, 2048, 1024),  # (4, 2, 4)
+               (768, 3072, 1024),  # (2, 3, 2)
+               (1536, 2048, 1024),  # (4, 2, 2)
+               (2048, 3072, 1024),  # (4, 2, 1)
                (2000, 3000, 1024),  # ragged rows and columns
                (2048, 64, 8128),   # 127 chunks of 64 k: no K split divides them
                (300, 200, 4032),   # 63 chunks
@@ -366,15 +371,17 @@ def test_gemm(ctx, gtype, m, n, k, ybf16):
     assert np.all(err <= 2.0 ** -11 + 1e-5 + extra), err.max()
 
 
-# Q6_K: K a multiple of 256, the GEMM from 33 rows (shape -> TM, S)
-GEMM_SHAPES_Q6K = [(50, 20000, 256),   # TM2 S1/2
+# Q6_K: K a multiple of 256, the GEMM from 33 rows (shape -> TM, NB, S)
+GEMM_SHAPES_Q6K = [(50, 20000, 256),
                    (64, 1000, 512),
-                   (100, 300, 512),    # TM4
+                   (100, 300, 512),
                    (200, 384, 1024),
-                   (512, 3072, 1024),
-                   (512, 1024, 3072),  # TM2 S4
+                   (512, 3072, 1024),  # (2, 3, 4)
+                   (512, 1024, 3072),  # (2, 2, 4)
                    (512, 6144, 1024),
-                   (2048, 3072, 1024),  # TM4 S1
+                   (768, 2048, 1024),  # (2, 2, 2)
+                   (768, 3072, 1024),  # (4, 2, 2)
+                   (2048, 3072, 1024),  # (4, 2, 1)
                    (2000, 3000, 1024),  # ragged
                    (300, 200, 4096)]
 
@@ -445,7 +452,7 @@ GEMM_MLX_CASES = [
     (17, 256, 1024, 64, oracle.D_BF16), (33, 512, 2048, 32, oracle.D_F16), (50, 20000, 256, 128, oracle.D_BF16),
     (100, 300, 1088, 64, oracle.D_BF16), (200, 384, 1024, 32, oracle.D_F32), (512, 3072, 1024, 64, oracle.D_BF16),
     (512, 1024, 3072, 64, oracle.D_F16), (2048, 3072, 1024, 128, oracle.D_BF16), (2000, 3000, 1024, 64, oracle.D_F32),
-    (300, 200, 4032, 64, oracle.D_BF16),
+    (300, 200, 4032, 64, oracle.D_BF16), (768, 2048, 1024, 64, oracle.D_BF16), (1536, 2048, 1024, 32, oracle.D_F16),
 ]
 
 
