@@ -114,164 +114,243 @@ __device__ __forceinline__ float absmax3(float a, float b, float c) {
     return r;
 }
 
-// One staging thread's share: code dword t = idx % NT of (activation row,
-// chunk) item = idx / NT; its NXR runs of 4 activations.
+// Staging threads per scale group (activation row b, chunk u, group g): SP
+// adjacent threads (SP = 1, 2 or 4, dividing NT) share a group, thread q
+// taking code dwords t = q·NT/SP .. (q+1)·NT/SP - 1.  Pair h = g + NG·k of
+// code dword t belongs to group g (grp(t, h) = h mod NG); a thread loads, for
+// each of its code dwords, the group's runs of 4 activations (NXR runs for
+// one-group chunks, run g otherwise, at xrun0(r) + TSTRIDE·t), takes the
+// group's largest magnitude and sums over its SP lanes (DPP, no LDS), and
+// stores its pairs.  With SP = 1 a group needs no cross-lane step at all;
+// wider SP spreads the group over more lanes, which keeps each load
+// instruction's addresses denser (fewer cache lines per instruction) when
+// the workgroup has threads to spare.  Checked at compile time by
+// group_runs_ok: the positions of group g are those of group 0 shifted by
+// RUNSTRIDE·g = xrun0(g).
 template <class E>
-struct XStage {
-    float v[E::NXR][4];
-    uint32_t item;
-    bool live;  // item < B·nch: the thread stores
+constexpr bool group_runs_ok() {
+    for (int t = 0; t < E::NT; t++)
+        for (int h = 0; h < E::PPT; h++)
+            for (int e = 0; e < 2; e++) {
+                const int g = h % E::NG;
+                if (E::grp(t, h) != g) return false;
+                if (E::xoff(t, h, e) - E::RUNSTRIDE * g != E::xoff(t, h - g, e)) return false;
+                if (E::NG > 1 && xrun_of<E>(h - g, e) != 0) return false;  // group 0 reads run 0 only
+                if (E::dv(t, h) != E::dv(0, h)) return false;               // the x16 flag is per pair slot
+            }
+    if (E::NG > 1) {
+        if (E::NXR != E::NG) return false;
+        for (int r = 0; r < E::NXR; r++)
+            if (E::xrun0(r) != E::RUNSTRIDE * r) return false;
+    }
+    return E::PPT % E::NG == 0;
+}
+
+// op over the SP adjacent lanes of a group (SP = 1, 2, 4), the result in every lane
+template <int SP, class OP>
+__device__ __forceinline__ uint32_t sp_reduce(uint32_t v, OP op) {
+    if constexpr (SP >= 2) v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+    if constexpr (SP >= 4) v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    return v;
+}
+
+template <class E, int SP>
+struct GStage {
+    static constexpr int TT = E::NT / SP;                   // code dwords per thread
+    static constexpr int RPG = E::NG == 1 ? E::NXR : 1;     // runs of 4 per code dword in one group
+    float v[TT][RPG][4];
+    uint32_t item;  // b·nch + u
+    uint32_t g;     // scale group within the chunk
+    uint32_t q;     // part of the group (code dwords q·TT ..)
+    bool live;      // the group exists: the thread stores
 };
 
-// Issues the loads of staging thread idx (no use of the loaded values, so
-// loads issued after it are not waited for).
-template <class E, int B, bool XBF16>
-__device__ __forceinline__ void xstage_load(const GemvParams& p, uint32_t nch, uint32_t idx, XStage<E>& s) {
-    const uint32_t items = (uint32_t)B * nch;
-    const uint32_t it = idx / (uint32_t)E::NT, t = idx % (uint32_t)E::NT;
-    s.live = it < items;
-    s.item = s.live ? it : items - 1u;  // spare threads redo the last chunk, unstored
+// Issues the loads of staging thread idx (the values are not used here, so
+// loads issued after this are not waited for).
+template <class E, int SP, int B, bool XBF16>
+__device__ __forceinline__ void gstage_load(const GemvParams& p, uint32_t nch, uint32_t idx, GStage<E, SP>& s) {
+    using S = GStage<E, SP>;
+    const uint32_t groups = (uint32_t)B * nch * (uint32_t)E::NG;
+    s.q = SP == 1 ? 0u : idx % (uint32_t)SP;
+    const uint32_t gi0 = SP == 1 ? idx : idx / (uint32_t)SP;
+    s.live = gi0 < groups;
+    const uint32_t gi = s.live ? gi0 : groups - 1u;  // spare lanes redo the last group, unstored
+    s.g = E::NG == 1 ? 0u : gi % (uint32_t)E::NG;
+    s.item = E::NG == 1 ? gi : gi / (uint32_t)E::NG;
     const uint32_t b = B == 1 ? 0u : s.item / nch, u = s.item - b * nch;
     // Rows past the batch restage row 0: in bounds, and their sums are never
     // stored.  Activation offsets are 32-bit (the activations are < 4 GiB).
-    const uint32_t base = (b < p.batch ? b : 0u) * p.ldx + E::xbase(u) + (uint32_t)E::TSTRIDE * t;
+    const uint32_t base = (b < p.batch ? b : 0u) * p.ldx + E::xbase(u) + (uint32_t)E::RUNSTRIDE * s.g +
+                          (uint32_t)E::TSTRIDE * (uint32_t)S::TT * s.q;
 #pragma unroll
-    for (int r = 0; r < E::NXR; r++) load_x4<XBF16>(p.x, base + (uint32_t)E::xrun0(r), s.v[r]);
+    for (int tt = 0; tt < S::TT; tt++)
+#pragma unroll
+        for (int r = 0; r < S::RPG; r++)
+            load_x4<XBF16>(p.x, base + (uint32_t)(E::xrun0(r) + E::TSTRIDE * tt), s.v[tt][r]);
 }
 
-// The rest of staging thread (t, s.item): picks each scale group's power of
-// two s = 2^(e-14) from the group's largest magnitude over the chunk (frexp
-// exponent e, so |x|/s < 2^14), writes the dword's PPT f16 pairs in decode
-// order (one RNE rounding of x/s, or of x/(16s) for pairs meeting x16 codes)
-// and, from lane t = 0, the group constants -C = -Σ coef·v and s·Σx over the
-// stored values v (their f32 sums reduced across the chunk's NT lanes).
-template <class E, int B>
-__device__ __forceinline__ void xstage_store(uint8_t* lds, uint32_t nch, uint32_t t, const XStage<E>& s) {
+// The rest of staging thread s: the group's power of two s = 2^(e-14) from
+// its largest magnitude (frexp exponent e, so |x|/s < 2^14), its pairs in
+// decode order (one RNE rounding of x/s, or of x/(16s) for pairs meeting x16
+// codes) and, from part q = 0, the constants -C = -Σ coef·v and s·Σx over the
+// stored values v (f32 sums over the SP parts).
+template <class E, int SP, int B>
+__device__ __forceinline__ void gstage_store(uint8_t* lds, uint32_t nch, const GStage<E, SP>& s) {
     using XT = XTile<E>;
+    using S = GStage<E, SP>;
     typedef float f32x2 __attribute__((ext_vector_type(2)));
-    uint32_t* xp = reinterpret_cast<uint32_t*>(lds);
-    float* xc = reinterpret_cast<float*>(lds + (size_t)B * nch * XT::XPW * 4u);
-    auto val = [&](int h, int e) -> float {
-        const int r = xrun_of<E>(h, e);
-        return s.v[r][E::xoff(0, h, e) - E::xrun0(r)];
-    };
-    // each group's largest magnitude: its 2·PPT/NG activations folded three at
-    // a time (the running maximum is non-negative, so its abs is a no-op)
-    constexpr int NV = 2 * E::PPT / E::NG;
-    static_assert(NV >= 3, "a group holds at least 3 activations per dword");
-    uint32_t mx[E::NG];
+    constexpr int KP = E::PPT / E::NG, NV = S::TT * S::RPG * 4;
+    const float* vv = &s.v[0][0][0];
+    // largest magnitude: independent triples, then their maximum
+    float m3[(NV + 2) / 3];
 #pragma unroll
-    for (int g = 0; g < E::NG; g++) {
-        float a[NV];
-        int n = 0;
+    for (int i = 0; i < NV; i += 3) m3[i / 3] = absmax3(vv[i], vv[i + 1 < NV ? i + 1 : i], vv[i + 2 < NV ? i + 2 : i]);
+    constexpr int N3 = (NV + 2) / 3;
+    float m = m3[0];
 #pragma unroll
-        for (int h = 0; h < E::PPT; h++)
-            if (E::grp(0, h) == g) {
-                a[n++] = val(h, 0);
-                a[n++] = val(h, 1);
-            }
-        float m = absmax3(a[0], a[1], a[2]);
+    for (int i = 1; i < N3; i += 2) m = absmax3(m, m3[i], m3[i + 1 < N3 ? i + 1 : i]);
+    uint32_t mx = sp_reduce<SP>(__float_as_uint(m), [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+    int ex = 0;
+    (void)frexpf(__uint_as_float(mx), &ex);  // non-negative floats order as integers
+    ex = ex < -110 ? -110 : ex;                // keeps s = 2^(e-14) a normal f32
+    uint32_t pr[S::TT][KP];
+    float C[2] = {0.0f, 0.0f}, Sx[2] = {0.0f, 0.0f};  // two chains each
 #pragma unroll
-        for (int i = 3; i < NV; i += 2) m = absmax3(m, a[i], a[i + 1 < NV ? i + 1 : i]);
-        mx[g] = __float_as_uint(m);  // non-negative floats order as integers
-    }
-    int ex[E::NG];
+    for (int tt = 0; tt < S::TT; tt++)
 #pragma unroll
-    for (int g = 0; g < E::NG; g++) {
-        mx[g] = lanes_reduce<E::NT>(mx[g], [](uint32_t a, uint32_t b) { return a > b ? a : b; });
-        int e = 0;
-        (void)frexpf(__uint_as_float(mx[g]), &e);
-        ex[g] = e < -110 ? -110 : e;  // keeps s = 2^(e-14) a normal f32
-    }
-    uint32_t pr[E::PPT];
-    float C[E::NG], S[E::NG];
-#pragma unroll
-    for (int g = 0; g < E::NG; g++) C[g] = S[g] = 0.0f;
-#pragma unroll
-    for (int h = 0; h < E::PPT; h++) {
-        const int g = E::grp(0, h);
-        const bool dv = E::dv(0, h);
-        const int sh = (dv ? 10 : 14) - ex[g];
-        const f32x2 f = {ldexpf(val(h, 0), sh), ldexpf(val(h, 1), sh)};
-        pr[h] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));  // v_cvt_pk_f16_f32 (RNE)
-        const uint32_t cf = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)E::coef(dv)) * 0x00010001u;
-        C[g] = dot2(pr[h], cf, C[g]);
-        if constexpr (XT::NCF == 4) S[g] = dot2(pr[h], dv ? 0x4C004C00u : 0x3C003C00u, S[g]);  // (16, 16) or (1, 1)
-    }
-    auto fadd = [](uint32_t a, uint32_t b) { return __float_as_uint(__uint_as_float(a) + __uint_as_float(b)); };
-#pragma unroll
-    for (int g = 0; g < E::NG; g++) {
-        C[g] = __uint_as_float(lanes_reduce<E::NT>(__float_as_uint(C[g]), fadd));
-        if constexpr (XT::NCF == 4) S[g] = __uint_as_float(lanes_reduce<E::NT>(__float_as_uint(S[g]), fadd));
-    }
-    if (s.live) {
-        uint32_t* dst = xp + (size_t)s.item * XT::XPW + t * (uint32_t)E::PPT;
-        if constexpr (E::PPT % 4 == 0) {
-#pragma unroll
-            for (int h = 0; h < E::PPT; h += 4)
-                *reinterpret_cast<uint4*>(dst + h) = make_uint4(pr[h], pr[h + 1], pr[h + 2], pr[h + 3]);
-        } else {
-            static_assert(E::PPT == 2, "pairs per code dword: 2, 4 or 8");
-            *reinterpret_cast<uint2*>(dst) = make_uint2(pr[0], pr[1]);
+        for (int k = 0; k < KP; k++) {
+            const int h0 = E::NG * k;  // pair h0 + g of code dword q·TT + tt
+            const bool dv = E::NG == 1 ? E::dv(0, h0) : E::dv(0, h0 + (int)s.g);
+            const int sh = (dv ? 10 : 14) - ex;
+            auto val = [&](int e) {
+                const int r = xrun_of<E>(h0, e);
+                return s.v[tt][r][E::xoff(0, h0, e) - E::xrun0(r)];
+            };
+            const f32x2 f = {ldexpf(val(0), sh), ldexpf(val(1), sh)};
+            pr[tt][k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));  // v_cvt_pk_f16_f32 (RNE)
+            const uint32_t c1 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)E::coef(false)) * 0x00010001u;
+            const uint32_t c16 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)E::coef(true)) * 0x00010001u;
+            const int ch = (tt * KP + k) & 1;
+            C[ch] = dot2(pr[tt][k], dv ? c16 : c1, C[ch]);
+            if constexpr (XT::NCF == 4) Sx[ch] = dot2(pr[tt][k], dv ? 0x4C004C00u : 0x3C003C00u, Sx[ch]);  // (16, 16) or (1, 1)
         }
-        if (t == 0) {
+    auto fadd = [](uint32_t a, uint32_t b) { return __float_as_uint(__uint_as_float(a) + __uint_as_float(b)); };
+    const float Ct = __uint_as_float(sp_reduce<SP>(__float_as_uint(C[0] + C[1]), fadd));
+    float St = 0.0f;
+    if constexpr (XT::NCF == 4) St = __uint_as_float(sp_reduce<SP>(__float_as_uint(Sx[0] + Sx[1]), fadd));
+    if (s.live) {
+        uint32_t* xp = reinterpret_cast<uint32_t*>(lds) + (size_t)s.item * XT::XPW + s.q * (uint32_t)(S::TT * E::PPT);
+        float* xc = reinterpret_cast<float*>(lds + (size_t)B * nch * XT::XPW * 4u);
+        if constexpr (E::NG == 1 && (S::TT * E::PPT) % 4 == 0) {
+            // the thread's pairs are TT·PPT consecutive dwords
 #pragma unroll
-            for (int g = 0; g < E::NG; g++) {
-                const float sc = ldexpf(1.0f, ex[g] - 14);
-                float* c = xc + ((size_t)s.item * E::NG + g) * XT::NCF;
-                if constexpr (XT::NCF == 4) {
-                    *reinterpret_cast<float4*>(c) = make_float4(-C[g], sc, sc * S[g], 0.0f);
-                } else {
-                    *reinterpret_cast<float2*>(c) = make_float2(-C[g], sc);
-                }
+            for (int i = 0; i < S::TT * E::PPT; i += 4)
+                *reinterpret_cast<uint4*>(xp + i) =
+                    make_uint4(pr[i / KP][i % KP], pr[(i + 1) / KP][(i + 1) % KP], pr[(i + 2) / KP][(i + 2) % KP],
+                               pr[(i + 3) / KP][(i + 3) % KP]);
+        } else if constexpr (E::NG == 1 && (S::TT * E::PPT) % 2 == 0) {
+#pragma unroll
+            for (int i = 0; i < S::TT * E::PPT; i += 2)
+                *reinterpret_cast<uint2*>(xp + i) = make_uint2(pr[i / KP][i % KP], pr[(i + 1) / KP][(i + 1) % KP]);
+        } else {
+#pragma unroll
+            for (int tt = 0; tt < S::TT; tt++)
+#pragma unroll
+                for (int k = 0; k < KP; k++) xp[tt * E::PPT + E::NG * k + (int)s.g] = pr[tt][k];
+        }
+        if (s.q == 0) {
+            const float sc = ldexpf(1.0f, ex - 14);
+            float* c = xc + ((size_t)s.item * E::NG + s.g) * XT::NCF;
+            if constexpr (XT::NCF == 4) {
+                *reinterpret_cast<float4*>(c) = make_float4(-Ct, sc, sc * St, 0.0f);
+            } else {
+                *reinterpret_cast<float2*>(c) = make_float2(-Ct, sc);
             }
         }
     }
 }
 
-// Stages activation rows [0, batch) into the tile (rows up to B restage row 0),
-// one thread per code dword: B·nch·NT staging threads, P per workgroup thread
-// per round.  The first round's activation loads are issued, then mid() (the
-// caller's first weight loads), then the first round is computed: loads
-// return in issue order, so the activations arrive ahead of the weights and
-// the staging arithmetic runs while the weights are in flight.  Later rounds
-// (large batches) load after the weights.  Ends with a barrier.
-template <class E, int B, bool XBF16, int P, int TH, class MID>
-__device__ __forceinline__ void stage_x_rounds(uint8_t* lds, const GemvParams& p, MID&& mid) {
+// Stages activation rows [0, batch) into the tile (rows up to B restage row
+// 0): B·nch·NG·SP staging threads in rounds of TH (the workgroup size).  The
+// first round's activation loads are issued, then mid() (the caller's first
+// weight loads), then the first round is computed: loads return in issue
+// order, so the activations arrive ahead of the weights and the staging
+// arithmetic runs while the weights are in flight.  Waves with no group in a
+// round skip it (a wave-uniform branch).  Later rounds (long rows, large
+// batches) load after the weights.  Ends with a barrier.
+template <class E, int SP, int B, bool XBF16, int TH, class MID>
+__device__ __forceinline__ void stage_x_sp(uint8_t* lds, const GemvParams& p, MID&& mid) {
     const uint32_t nch = p.K / (uint32_t)E::CW;
-    const uint32_t total = (uint32_t)B * nch * (uint32_t)E::NT;
-    const uint32_t t = threadIdx.x % (uint32_t)E::NT;  // the workgroup size is a multiple of NT
-    XStage<E> s[P];
-#pragma unroll
-    for (int ps = 0; ps < P; ps++) xstage_load<E, B, XBF16>(p, nch, threadIdx.x + (uint32_t)ps * TH, s[ps]);
+    const uint32_t total = (uint32_t)B * nch * (uint32_t)E::NG * (uint32_t)SP;
+    const uint32_t wave0 = threadIdx.x & ~63u;  // first thread of this wave
+    GStage<E, SP> s;
+    const bool first = wave0 < total;
+    if (first) gstage_load<E, SP, B, XBF16>(p, nch, threadIdx.x, s);
     __builtin_amdgcn_sched_barrier(0);
     mid();
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int ps = 0; ps < P; ps++) xstage_store<E, B>(lds, nch, t, s[ps]);
-    for (uint32_t base = (uint32_t)P * TH; base < total; base += (uint32_t)P * TH) {
-#pragma unroll
-        for (int ps = 0; ps < P; ps++)
-            xstage_load<E, B, XBF16>(p, nch, base + threadIdx.x + (uint32_t)ps * TH, s[ps]);
-#pragma unroll
-        for (int ps = 0; ps < P; ps++) xstage_store<E, B>(lds, nch, t, s[ps]);
+    if (first) gstage_store<E, SP, B>(lds, nch, s);
+    for (uint32_t base = TH; base < total; base += TH) {
+        if (base + wave0 < total) {
+            gstage_load<E, SP, B, XBF16>(p, nch, base + threadIdx.x, s);
+            gstage_store<E, SP, B>(lds, nch, s);
+        }
     }
     __syncthreads();
 }
 
-// Rounds of P passes, P the power of two covering the staging threads, at
-// most 16 activations (registers) per thread in flight: every variant is
-// compiled into the kernel, so the widest one sets its register count.  TH is
-// the workgroup size.
-template <class E, int B, bool XBF16, int TH = kGemvThreads, class MID>
+// Activation staging mode of a GEMV kernel, a template parameter chosen per
+// launch (xmode()): the source dtype and the staging threads per scale
+// group.  One staging variant per kernel keeps each kernel's code small: these
+// launches are short, and each starts by fetching its code (a kernel holding
+// both variants, picked at run time, ran the Qwen3-0.6B GGUF step 410 us
+// against 393 us).
+enum XMode : int {
+    XM_F32 = 0,        // f32 rows, one thread per group
+    XM_BF16 = 1,       // bf16 rows, one thread per group
+    XM_F32_SPLIT = 2,  // f32 rows, two threads per 32-activation group
+};
+
+// Two threads per group for f32 rows with 32-activation groups when the
+// staged rows hold 64..128 groups: a thread then issues four 16-byte loads
+// instead of eight, and more of the workgroup's waves share the staging.
+// Below 64 groups a single wave stages either way, and the cross-lane step
+// of a split costs more than the loads it saves.  Measured per step (one
+// MI355X, graph replay): the Qwen3-8B GGUF step 1.30 -> 1.27-1.29 ms with the
+// split at K = 4096 (128 groups); the Qwen3-0.6B projections (K = 1024, 32
+// groups) 393 us unsplit against 405 us split; bf16 rows gain nothing.
+template <class E>
+inline int xmode(bool x_bf16, uint32_t B, uint32_t K) {
+    if (x_bf16) return XM_BF16;
+    const uint32_t groups = B * (K / (uint32_t)E::CW) * (uint32_t)E::NG;
+    return E::RUNLEN == 32 && groups >= 64u && groups <= 128u ? XM_F32_SPLIT : XM_F32;
+}
+
+template <class E, int B, int XM, int TH = kGemvThreads, class MID>
 __device__ __forceinline__ void stage_x_auto(uint8_t* lds, const GemvParams& p, MID&& mid) {
-    constexpr int PMAX = 4 / E::NXR > 0 ? 4 / E::NXR : 1;
-    const uint32_t passes = ((uint32_t)B * (p.K / (uint32_t)E::CW) * (uint32_t)E::NT + TH - 1u) / TH;
-    if (PMAX == 1 || passes <= 1u) stage_x_rounds<E, B, XBF16, 1, TH>(lds, p, mid);
-    else if constexpr (PMAX >= 2) {
-        if (PMAX == 2 || passes <= 2u) stage_x_rounds<E, B, XBF16, 2, TH>(lds, p, mid);
-        else stage_x_rounds<E, B, XBF16, (PMAX >= 4 ? 4 : 2), TH>(lds, p, mid);
+    static_assert(group_runs_ok<E>(), "scale groups disagree with xoff()");
+    constexpr int SP = XM == XM_F32_SPLIT ? 2 : 1;
+    static_assert(E::NT % SP == 0 && (SP == 1 || E::RUNLEN == 32), "a group's code dwords split evenly");
+    stage_x_sp<E, SP, B, XM == XM_BF16, TH>(lds, p, mid);
+}
+
+// Staging for the streaming kernel (long launches whose waves all wait at
+// the staging barrier): the widest split (4, 2 or 1 threads per group,
+// dividing NT) whose threads fit one round of the workgroup, so that each
+// thread's share, and the barrier's wait, is shortest.  Measured on the
+// Qwen3-8B Q4_K_M gate/up (Q4_K 2 x 12288 x 4096): 13.4-13.5 us per launch at
+// four threads per group against 13.9 us at two and 14.4-14.8 us at one.
+template <class E, bool XBF16, int TH, class MID>
+__device__ __forceinline__ void stage_x_fit(uint8_t* lds, const GemvParams& p, MID&& mid) {
+    static_assert(group_runs_ok<E>(), "scale groups disagree with xoff()");
+    const uint32_t groups = (p.K / (uint32_t)E::CW) * (uint32_t)E::NG;
+    if constexpr (E::NT % 4 == 0 && TH <= 512) {
+        if (4u * groups <= (uint32_t)TH) return stage_x_sp<E, 4, 1, XBF16, TH>(lds, p, mid);
     }
+    if constexpr (E::NT % 2 == 0) {
+        if (2u * groups <= (uint32_t)TH) return stage_x_sp<E, 2, 1, XBF16, TH>(lds, p, mid);
+    }
+    stage_x_sp<E, 1, 1, XBF16, TH>(lds, p, mid);
 }
 
 // ---------------------------------------------------------------- chunk dot product
@@ -636,20 +715,20 @@ __device__ __forceinline__ void gemv_oneshot(const GemvParams& p, const uint8_t*
 // ---------------------------------------------------------------- GGUF
 // Weight offsets are 32-bit (the C ABI limits one weight to 4 GiB), so loads
 // use a uniform 64-bit base plus a per-lane 32-bit offset.
-template <class E, int B, int R, bool XBF16, int TH = kGemvThreads>
+template <class E, int B, int R, int XM, int TH = kGemvThreads>
 __global__ __launch_bounds__(TH) void gguf_gemv_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
     const uint32_t rowbytes = (p.K / (uint32_t)E::QK) * (uint32_t)E::BB;
     auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) { return E::load(rb.w, row * rowbytes, u); };
-    gemv_pipeline<E, R, B, TH>(p, xlds, load, [&](auto&& mid) { stage_x_auto<E, B, XBF16, TH>(xlds, p, mid); });
+    gemv_pipeline<E, R, B, TH>(p, xlds, load, [&](auto&& mid) { stage_x_auto<E, B, XM, TH>(xlds, p, mid); });
 }
 
-template <class E, int CPL, int B, bool XBF16, int TH>
+template <class E, int CPL, int B, int XM, int TH>
 __global__ __launch_bounds__(TH) void gguf_gemv_oneshot_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
     const uint32_t rowbytes = (p.K / (uint32_t)E::QK) * (uint32_t)E::BB;
     auto load = [&](const RowBlock& rb, uint32_t row, uint32_t u) { return E::load(rb.w, row * rowbytes, u); };
-    gemv_oneshot<E, CPL, B, TH>(p, xlds, load, [&](auto&& mid) { stage_x_auto<E, B, XBF16, TH>(xlds, p, mid); });
+    gemv_oneshot<E, CPL, B, TH>(p, xlds, load, [&](auto&& mid) { stage_x_auto<E, B, XM, TH>(xlds, p, mid); });
 }
 
 // ---------------------------------------------------------------- MLX affine U4
@@ -680,18 +759,18 @@ struct MlxLoad {
     }
 };
 
-template <int B, int R, bool XBF16>
+template <int B, int R, int XM>
 __global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
     gemv_pipeline<EncMlxU4, R, B, kGemvThreads>(p, xlds, MlxLoad(p),
-                                                [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XBF16>(xlds, p, mid); });
+                                                [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XM>(xlds, p, mid); });
 }
 
-template <int CPL, int B, bool XBF16, int TH>
+template <int CPL, int B, int XM, int TH>
 __global__ __launch_bounds__(TH) void mlx_u4_gemv_oneshot_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
     gemv_oneshot<EncMlxU4, CPL, B, TH>(p, xlds, MlxLoad(p),
-                                        [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XBF16, TH>(xlds, p, mid); });
+                                        [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XM, TH>(xlds, p, mid); });
 }
 
 // Widest rows per lane group instantiated for a register batch B: more rows
@@ -858,15 +937,16 @@ hipError_t launch_oneshot(KERNEL k512, KERNEL k256, GemvParams p, size_t lds, hi
 // oneshot = chunks per lane selects the latency-mode kernel, 0 the
 // persistent pipeline.  The row-block layout is set here, per tile.
 // Activations are f32 (the reference's precision contract for quantized
-// linears, crates/dyninfer-compiler/src/lib.rs:289-306) or bf16 (XBF16).
-template <class E, bool XBF16>
+// linears, crates/dyninfer-compiler/src/lib.rs:289-306) or bf16, staged as XM says (XMode).
+template <class E, int XM>
 hipError_t launch_gguf_gemv_stream(GemvParams p, size_t lds, hipStream_t st);  // gemv_stream.hpp
 
-template <class E, bool XBF16>
+template <class E, int XM>
 hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot, hipStream_t st) {
     const size_t lds = (size_t)xtile_bytes(E::ENC, B, p.K);
     if (B == 1 && !oneshot) {  // long stream of one activation row: the streaming kernel where it fits
-        const hipError_t e = launch_gguf_gemv_stream<E, XBF16>(p, lds, st);
+        // (the streaming kernel picks its staging split itself: two modes, not three)
+        const hipError_t e = launch_gguf_gemv_stream<E, XM == XM_BF16 ? XM_BF16 : XM_F32>(p, lds, st);
         if (e != hipErrorNotSupported) return e;
     }
     if (oneshot) {
@@ -874,7 +954,7 @@ hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot,
         // (64-weight chunks 1..2), 1..2 for 2 rows, 1 for 4
 #define DMX_ONESHOT(b, c)                                                                             \
     if (B == b && oneshot == c)                                                                       \
-        return launch_oneshot(gguf_gemv_oneshot_kernel<E, c, b, XBF16, 512>, gguf_gemv_oneshot_kernel<E, c, b, XBF16, 256>, \
+        return launch_oneshot(gguf_gemv_oneshot_kernel<E, c, b, XM, 512>, gguf_gemv_oneshot_kernel<E, c, b, XM, 256>, \
                               p, lds, st);
         DMX_ONESHOT(1, 1)
         DMX_ONESHOT(1, 2)
@@ -905,12 +985,12 @@ hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot,
 #define DMX_CASE(b)                                                                                            \
     case b:                                                                                                    \
         if constexpr (b <= max_register_batch(E::ENC))                                                         \
-            n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, b, decltype(r)::value, XBF16>; }); \
+            n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, b, decltype(r)::value, XM>; }); \
         break;
     switch (B) {
     case 1:
-        n = big ? gemv_tiles<E, 1>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, 1, decltype(r)::value, XBF16, 1024>; }, 1024u)
-                : gemv_tiles<E, 1>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, 1, decltype(r)::value, XBF16>; });
+        n = big ? gemv_tiles<E, 1>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, 1, decltype(r)::value, XM, 1024>; }, 1024u)
+                : gemv_tiles<E, 1>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, 1, decltype(r)::value, XM>; });
         break;
         DMX_CASE(2)
         DMX_CASE(4)

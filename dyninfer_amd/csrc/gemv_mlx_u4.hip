@@ -3,14 +3,14 @@
 
 namespace dmx {
 namespace {
-template <bool XBF16>
+template <int XM>
 hipError_t launch_mlx(const GemvParams& p, uint32_t B, uint32_t oneshot, hipStream_t st) {
     using E = EncMlxU4;
     const size_t lds = (size_t)xtile_bytes(E::ENC, B, p.K);
     if (oneshot) {
 #define DMX_ONESHOT(b, c)                                                                                  \
     if (B == b && oneshot == c)                                                                            \
-        return launch_oneshot(mlx_u4_gemv_oneshot_kernel<c, b, XBF16, 512>, mlx_u4_gemv_oneshot_kernel<c, b, XBF16, 256>, \
+        return launch_oneshot(mlx_u4_gemv_oneshot_kernel<c, b, XM, 512>, mlx_u4_gemv_oneshot_kernel<c, b, XM, 256>, \
                               p, lds, st);
         DMX_ONESHOT(1, 1)
         DMX_ONESHOT(1, 2)
@@ -26,7 +26,7 @@ hipError_t launch_mlx(const GemvParams& p, uint32_t B, uint32_t oneshot, hipStre
     int n = 0;
 #define DMX_CASE(b)                                                                                        \
     case b:                                                                                                \
-        n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return mlx_u4_gemv_kernel<b, decltype(r)::value, XBF16>; }); \
+        n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return mlx_u4_gemv_kernel<b, decltype(r)::value, XM>; }); \
         break;
     switch (B) {
         DMX_CASE(1)
@@ -43,6 +43,10 @@ hipError_t launch_mlx(const GemvParams& p, uint32_t B, uint32_t oneshot, hipStre
 }  // namespace
 
 hipError_t gemv_launch_mlx_u4(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st) {
-    return xbf16 ? launch_mlx<true>(p, B, oneshot, st) : launch_mlx<false>(p, B, oneshot, st);
+    switch (xmode<EncMlxU4>(xbf16, B, p.K)) {
+    case XM_BF16: return launch_mlx<XM_BF16>(p, B, oneshot, st);
+    case XM_F32_SPLIT: return launch_mlx<XM_F32_SPLIT>(p, B, oneshot, st);
+    default: return launch_mlx<XM_F32>(p, B, oneshot, st);
+    }
 }
 }  // namespace dmx

@@ -182,7 +182,7 @@ constexpr int stream_depth() {
 constexpr uint32_t kStreamWaves = 16;
 constexpr int stream_gcd(int a, int b) { return b ? stream_gcd(b, a % b) : a; }
 
-template <class E, int CPL, bool XBF16, int TH>
+template <class E, int CPL, int XM, int TH>
 __global__ __launch_bounds__(TH) void gguf_gemv_stream_kernel(const GemvParams p) {
     constexpr int D = stream_depth<E>();
     constexpr int U = D / stream_gcd(D, CPL) * CPL;  // tasks per unrolled round: lcm(D, CPL)
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(TH) void gguf_gemv_stream_kernel(const GemvParams p
     float* res = reinterpret_cast<float*>(xlds + xtb) + (threadIdx.x >> 6) * p.res_steps * G;
 
     typename E::Raw buf[D];
-    stage_x_auto<E, 1, XBF16, TH>(xlds, p, [&] {
+    stage_x_fit<E, XM == XM_BF16, TH>(xlds, p, [&] {
 #pragma unroll
         for (int d = 0; d < D; d++) buf[d] = sl.load(sbase((uint32_t)d));
     });
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(TH) void gguf_gemv_stream_kernel(const GemvParams p
 // an even number of super-blocks) and, for the super-block encodings, L >= 8.  Returns
 // hipErrorNotSupported when nothing fits (the caller then runs the
 // persistent pipeline).
-template <class E, bool XBF16>
+template <class E, int XM>
 hipError_t launch_gguf_gemv_stream(GemvParams p, size_t lds, hipStream_t st) {
     const uint32_t nch = p.K / (uint32_t)E::CW;
     if (((p.K / (uint32_t)E::QK) * (uint32_t)E::BB) % 4u) return hipErrorNotSupported;
@@ -315,7 +315,7 @@ hipError_t launch_gguf_gemv_stream(GemvParams p, size_t lds, hipStream_t st) {
     const uint32_t threads = big ? 1024u : 512u;
     GemvKernel k = nullptr;
 #define DMX_STREAM(c)                                                                                        \
-    if (cpl == c) k = big ? gguf_gemv_stream_kernel<E, c, XBF16, 1024> : gguf_gemv_stream_kernel<E, c, XBF16, 512>;
+    if (cpl == c) k = big ? gguf_gemv_stream_kernel<E, c, XM, 1024> : gguf_gemv_stream_kernel<E, c, XM, 512>;
     DMX_STREAM(1)
     DMX_STREAM(2)
     DMX_STREAM(3)
@@ -363,7 +363,13 @@ hipError_t launch_gguf_gemv_stream(GemvParams p, size_t lds, hipStream_t st) {
 
 template <class E>
 hipError_t launch_gguf_gemv(const GemvParams& p, uint32_t B, uint32_t oneshot, bool xbf16, hipStream_t st) {
-    return xbf16 ? launch_gguf_gemv_x<E, true>(p, B, oneshot, st) : launch_gguf_gemv_x<E, false>(p, B, oneshot, st);
+    switch (xmode<E>(xbf16, B, p.K)) {
+    case XM_BF16: return launch_gguf_gemv_x<E, XM_BF16>(p, B, oneshot, st);
+    case XM_F32_SPLIT:
+        if constexpr (E::RUNLEN == 32) return launch_gguf_gemv_x<E, XM_F32_SPLIT>(p, B, oneshot, st);
+        return hipErrorInvalidValue;
+    default: return launch_gguf_gemv_x<E, XM_F32>(p, B, oneshot, st);
+    }
 }
 
 }  // namespace dmx

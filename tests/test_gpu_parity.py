@@ -310,11 +310,14 @@ def test_gemv_mfma_mlx(ctx, n, k, g, sdtype, batch, xbf16):
     assert np.all(err <= 2.0 ** -10 + 1e-4 + extra), err.max()
 
 
-def test_gemv_mlx_f32_io(ctx):
-    n, k, g = 257, 2048, 64
+# f32 activations: one row of 2048 and 4096 (64 and 128 groups of 32: two
+# staging threads per group), four rows of 2048 (256 groups: one thread)
+@pytest.mark.parametrize("batch,k", [(1, 2048), (1, 4096), (4, 2048)])
+def test_gemv_mlx_f32_io(ctx, batch, k):
+    n, g = 257, 64
     packed, sc, bi = oracle.synth_mlx_u4(n, k, g, oracle.D_BF16, seed=4)
     w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), g, oracle.D_BF16)
-    x = oracle.randn(4 * k, seed=9).reshape(4, k)
+    x = oracle.randn(batch * k, seed=9).reshape(batch, k)
     y = ctx.qlinear(w, dev(x)).cpu().numpy()
     assert gemv_err(y, x, oracle.dequant_mlx_u4(packed, sc, bi, oracle.D_BF16, n, k, g)) <= XF16
 
