@@ -299,6 +299,173 @@ __device__ __forceinline__ void stage_x_sp(uint8_t* lds, const GemvParams& p, MI
     __syncthreads();
 }
 
+// ---- Staging of several f32 activation rows: one thread per code dword.
+// Its loads are the densest (consecutive lanes on consecutive 16-byte runs),
+// which matters once the rows hold many groups: thread-per-group staging of 4
+// rows of 4096 (512 groups, eight 16-byte loads per lane 128 bytes apart, a
+// cache line per lane per load) took ~4 us before the first product, and the
+// Qwen3-8B GGUF step at 4 rows ran 2.50 ms against 2.31 ms with this staging.
+// One staging thread's share: code dword t = idx % NT of (activation row,
+// chunk) item = idx / NT; its NXR runs of 4 activations.
+template <class E>
+struct XStage {
+    float v[E::NXR][4];
+    uint32_t item;
+    bool live;  // item < B·nch: the thread stores
+};
+
+// Issues the loads of staging thread idx (no use of the loaded values, so
+// loads issued after it are not waited for).
+template <class E, int B, bool XBF16>
+__device__ __forceinline__ void xstage_load(const GemvParams& p, uint32_t nch, uint32_t idx, XStage<E>& s) {
+    const uint32_t items = (uint32_t)B * nch;
+    const uint32_t it = idx / (uint32_t)E::NT, t = idx % (uint32_t)E::NT;
+    s.live = it < items;
+    s.item = s.live ? it : items - 1u;  // spare threads redo the last chunk, unstored
+    const uint32_t b = B == 1 ? 0u : s.item / nch, u = s.item - b * nch;
+    // Rows past the batch restage row 0: in bounds, and their sums are never
+    // stored.  Activation offsets are 32-bit (the activations are < 4 GiB).
+    const uint32_t base = (b < p.batch ? b : 0u) * p.ldx + E::xbase(u) + (uint32_t)E::TSTRIDE * t;
+#pragma unroll
+    for (int r = 0; r < E::NXR; r++) load_x4<XBF16>(p.x, base + (uint32_t)E::xrun0(r), s.v[r]);
+}
+
+// The rest of staging thread (t, s.item): picks each scale group's power of
+// two s = 2^(e-14) from the group's largest magnitude over the chunk (frexp
+// exponent e, so |x|/s < 2^14), writes the dword's PPT f16 pairs in decode
+// order (one RNE rounding of x/s, or of x/(16s) for pairs meeting x16 codes)
+// and, from lane t = 0, the group constants -C = -Σ coef·v and s·Σx over the
+// stored values v (their f32 sums reduced across the chunk's NT lanes).
+template <class E, int B>
+__device__ __forceinline__ void xstage_store(uint8_t* lds, uint32_t nch, uint32_t t, const XStage<E>& s) {
+    using XT = XTile<E>;
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    uint32_t* xp = reinterpret_cast<uint32_t*>(lds);
+    float* xc = reinterpret_cast<float*>(lds + (size_t)B * nch * XT::XPW * 4u);
+    auto val = [&](int h, int e) -> float {
+        const int r = xrun_of<E>(h, e);
+        return s.v[r][E::xoff(0, h, e) - E::xrun0(r)];
+    };
+    // each group's largest magnitude: its 2·PPT/NG activations folded three at
+    // a time (the running maximum is non-negative, so its abs is a no-op)
+    constexpr int NV = 2 * E::PPT / E::NG;
+    static_assert(NV >= 3, "a group holds at least 3 activations per dword");
+    uint32_t mx[E::NG];
+#pragma unroll
+    for (int g = 0; g < E::NG; g++) {
+        float a[NV];
+        int n = 0;
+#pragma unroll
+        for (int h = 0; h < E::PPT; h++)
+            if (E::grp(0, h) == g) {
+                a[n++] = val(h, 0);
+                a[n++] = val(h, 1);
+            }
+        float m = absmax3(a[0], a[1], a[2]);
+#pragma unroll
+        for (int i = 3; i < NV; i += 2) m = absmax3(m, a[i], a[i + 1 < NV ? i + 1 : i]);
+        mx[g] = __float_as_uint(m);  // non-negative floats order as integers
+    }
+    int ex[E::NG];
+#pragma unroll
+    for (int g = 0; g < E::NG; g++) {
+        mx[g] = lanes_reduce<E::NT>(mx[g], [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+        int e = 0;
+        (void)frexpf(__uint_as_float(mx[g]), &e);
+        ex[g] = e < -110 ? -110 : e;  // keeps s = 2^(e-14) a normal f32
+    }
+    uint32_t pr[E::PPT];
+    float C[E::NG], S[E::NG];
+#pragma unroll
+    for (int g = 0; g < E::NG; g++) C[g] = S[g] = 0.0f;
+#pragma unroll
+    for (int h = 0; h < E::PPT; h++) {
+        const int g = E::grp(0, h);
+        const bool dv = E::dv(0, h);
+        const int sh = (dv ? 10 : 14) - ex[g];
+        const f32x2 f = {ldexpf(val(h, 0), sh), ldexpf(val(h, 1), sh)};
+        pr[h] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));  // v_cvt_pk_f16_f32 (RNE)
+        const uint32_t cf = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)E::coef(dv)) * 0x00010001u;
+        C[g] = dot2(pr[h], cf, C[g]);
+        if constexpr (XT::NCF == 4) S[g] = dot2(pr[h], dv ? 0x4C004C00u : 0x3C003C00u, S[g]);  // (16, 16) or (1, 1)
+    }
+    auto fadd = [](uint32_t a, uint32_t b) { return __float_as_uint(__uint_as_float(a) + __uint_as_float(b)); };
+#pragma unroll
+    for (int g = 0; g < E::NG; g++) {
+        C[g] = __uint_as_float(lanes_reduce<E::NT>(__float_as_uint(C[g]), fadd));
+        if constexpr (XT::NCF == 4) S[g] = __uint_as_float(lanes_reduce<E::NT>(__float_as_uint(S[g]), fadd));
+    }
+    if (s.live) {
+        uint32_t* dst = xp + (size_t)s.item * XT::XPW + t * (uint32_t)E::PPT;
+        if constexpr (E::PPT % 4 == 0) {
+#pragma unroll
+            for (int h = 0; h < E::PPT; h += 4)
+                *reinterpret_cast<uint4*>(dst + h) = make_uint4(pr[h], pr[h + 1], pr[h + 2], pr[h + 3]);
+        } else {
+            static_assert(E::PPT == 2, "pairs per code dword: 2, 4 or 8");
+            *reinterpret_cast<uint2*>(dst) = make_uint2(pr[0], pr[1]);
+        }
+        if (t == 0) {
+#pragma unroll
+            for (int g = 0; g < E::NG; g++) {
+                const float sc = ldexpf(1.0f, ex[g] - 14);
+                float* c = xc + ((size_t)s.item * E::NG + g) * XT::NCF;
+                if constexpr (XT::NCF == 4) {
+                    *reinterpret_cast<float4*>(c) = make_float4(-C[g], sc, sc * S[g], 0.0f);
+                } else {
+                    *reinterpret_cast<float2*>(c) = make_float2(-C[g], sc);
+                }
+            }
+        }
+    }
+}
+
+// Stages activation rows [0, batch) into the tile (rows up to B restage row 0),
+// one thread per code dword: B·nch·NT staging threads, P per workgroup thread
+// per round.  The first round's activation loads are issued, then mid() (the
+// caller's first weight loads), then the first round is computed: loads
+// return in issue order, so the activations arrive ahead of the weights and
+// the staging arithmetic runs while the weights are in flight.  Later rounds
+// (large batches) load after the weights.  Ends with a barrier.
+template <class E, int B, bool XBF16, int P, int TH, class MID>
+__device__ __forceinline__ void stage_x_rounds(uint8_t* lds, const GemvParams& p, MID&& mid) {
+    const uint32_t nch = p.K / (uint32_t)E::CW;
+    const uint32_t total = (uint32_t)B * nch * (uint32_t)E::NT;
+    const uint32_t t = threadIdx.x % (uint32_t)E::NT;  // the workgroup size is a multiple of NT
+    XStage<E> s[P];
+#pragma unroll
+    for (int ps = 0; ps < P; ps++) xstage_load<E, B, XBF16>(p, nch, threadIdx.x + (uint32_t)ps * TH, s[ps]);
+    __builtin_amdgcn_sched_barrier(0);
+    mid();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ps = 0; ps < P; ps++) xstage_store<E, B>(lds, nch, t, s[ps]);
+    for (uint32_t base = (uint32_t)P * TH; base < total; base += (uint32_t)P * TH) {
+#pragma unroll
+        for (int ps = 0; ps < P; ps++)
+            xstage_load<E, B, XBF16>(p, nch, base + threadIdx.x + (uint32_t)ps * TH, s[ps]);
+#pragma unroll
+        for (int ps = 0; ps < P; ps++) xstage_store<E, B>(lds, nch, t, s[ps]);
+    }
+    __syncthreads();
+}
+
+// Rounds of P passes, P the power of two covering the staging threads, at
+// most 16 activations (registers) per thread in flight: every variant is
+// compiled into the kernel, so the widest one sets its register count.  TH is
+// the workgroup size.
+template <class E, int B, bool XBF16, int TH, class MID>
+__device__ __forceinline__ void stage_x_dwords(uint8_t* lds, const GemvParams& p, MID&& mid) {
+    constexpr int PMAX = 4 / E::NXR > 0 ? 4 / E::NXR : 1;
+    const uint32_t passes = ((uint32_t)B * (p.K / (uint32_t)E::CW) * (uint32_t)E::NT + TH - 1u) / TH;
+    if (PMAX == 1 || passes <= 1u) stage_x_rounds<E, B, XBF16, 1, TH>(lds, p, mid);
+    else if constexpr (PMAX >= 2) {
+        if (PMAX == 2 || passes <= 2u) stage_x_rounds<E, B, XBF16, 2, TH>(lds, p, mid);
+        else stage_x_rounds<E, B, XBF16, (PMAX >= 4 ? 4 : 2), TH>(lds, p, mid);
+    }
+}
+
+
 // Activation staging mode of a GEMV kernel, a template parameter chosen per
 // launch (xmode()): the source dtype and the staging threads per scale
 // group.  One staging variant per kernel keeps each kernel's code small: these
@@ -319,19 +486,29 @@ enum XMode : int {
 // MI355X, graph replay): the Qwen3-8B GGUF step 1.30 -> 1.27-1.29 ms with the
 // split at K = 4096 (128 groups); the Qwen3-0.6B projections (K = 1024, 32
 // groups) 393 us unsplit against 405 us split; bf16 rows gain nothing.
+// Several f32 activation rows (B > 1) stage one thread per code dword
+// (stage_x_dwords); bf16 rows, half the bytes per group, stage one thread per
+// group at every batch (the Qwen3-0.6B MLX step at 4 rows: 617 us against
+// 633 us).
 template <class E>
 inline int xmode(bool x_bf16, uint32_t B, uint32_t K) {
     if (x_bf16) return XM_BF16;
     const uint32_t groups = B * (K / (uint32_t)E::CW) * (uint32_t)E::NG;
-    return E::RUNLEN == 32 && groups >= 64u && groups <= 128u ? XM_F32_SPLIT : XM_F32;
+    return B == 1 && E::RUNLEN == 32 && groups >= 64u && groups <= 128u ? XM_F32_SPLIT : XM_F32;
 }
+// The mode of a B-row kernel: the split names no other kernel than f32 at B > 1.
+constexpr int xmode_rows(int xm, int B) { return B > 1 && xm == XM_F32_SPLIT ? XM_F32 : xm; }
 
 template <class E, int B, int XM, int TH = kGemvThreads, class MID>
 __device__ __forceinline__ void stage_x_auto(uint8_t* lds, const GemvParams& p, MID&& mid) {
-    static_assert(group_runs_ok<E>(), "scale groups disagree with xoff()");
-    constexpr int SP = XM == XM_F32_SPLIT ? 2 : 1;
-    static_assert(E::NT % SP == 0 && (SP == 1 || E::RUNLEN == 32), "a group's code dwords split evenly");
-    stage_x_sp<E, SP, B, XM == XM_BF16, TH>(lds, p, mid);
+    if constexpr (B > 1 && XM != XM_BF16) {
+        stage_x_dwords<E, B, false, TH>(lds, p, mid);
+    } else {
+        static_assert(group_runs_ok<E>(), "scale groups disagree with xoff()");
+        constexpr int SP = XM == XM_F32_SPLIT && B == 1 ? 2 : 1;
+        static_assert(E::NT % SP == 0 && (SP == 1 || E::RUNLEN == 32), "a group's code dwords split evenly");
+        stage_x_sp<E, SP, B, XM == XM_BF16, TH>(lds, p, mid);
+    }
 }
 
 // Staging for the streaming kernel (long launches whose waves all wait at
@@ -954,7 +1131,8 @@ hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot,
         // (64-weight chunks 1..2), 1..2 for 2 rows, 1 for 4
 #define DMX_ONESHOT(b, c)                                                                             \
     if (B == b && oneshot == c)                                                                       \
-        return launch_oneshot(gguf_gemv_oneshot_kernel<E, c, b, XM, 512>, gguf_gemv_oneshot_kernel<E, c, b, XM, 256>, \
+        return launch_oneshot(gguf_gemv_oneshot_kernel<E, c, b, xmode_rows(XM, b), 512>,                         \
+                              gguf_gemv_oneshot_kernel<E, c, b, xmode_rows(XM, b), 256>, \
                               p, lds, st);
         DMX_ONESHOT(1, 1)
         DMX_ONESHOT(1, 2)
@@ -985,7 +1163,7 @@ hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot,
 #define DMX_CASE(b)                                                                                            \
     case b:                                                                                                    \
         if constexpr (b <= max_register_batch(E::ENC))                                                         \
-            n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, b, decltype(r)::value, XM>; }); \
+            n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, b, decltype(r)::value, xmode_rows(XM, b)>; }); \
         break;
     switch (B) {
     case 1:

@@ -10,7 +10,8 @@ hipError_t launch_mlx(const GemvParams& p, uint32_t B, uint32_t oneshot, hipStre
     if (oneshot) {
 #define DMX_ONESHOT(b, c)                                                                                  \
     if (B == b && oneshot == c)                                                                            \
-        return launch_oneshot(mlx_u4_gemv_oneshot_kernel<c, b, XM, 512>, mlx_u4_gemv_oneshot_kernel<c, b, XM, 256>, \
+        return launch_oneshot(mlx_u4_gemv_oneshot_kernel<c, b, xmode_rows(XM, b), 512>,                      \
+                              mlx_u4_gemv_oneshot_kernel<c, b, xmode_rows(XM, b), 256>, \
                               p, lds, st);
         DMX_ONESHOT(1, 1)
         DMX_ONESHOT(1, 2)
@@ -26,7 +27,7 @@ hipError_t launch_mlx(const GemvParams& p, uint32_t B, uint32_t oneshot, hipStre
     int n = 0;
 #define DMX_CASE(b)                                                                                        \
     case b:                                                                                                \
-        n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return mlx_u4_gemv_kernel<b, decltype(r)::value, XM>; }); \
+        n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return mlx_u4_gemv_kernel<b, decltype(r)::value, xmode_rows(XM, b)>; }); \
         break;
     switch (B) {
         DMX_CASE(1)
