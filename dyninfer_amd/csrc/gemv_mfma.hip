@@ -971,10 +971,8 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
                                    : enc == ENC_Q5_K ? K / 256u * 176u
                                    : enc == ENC_IQ4_XS ? K / 256u * 136u
                                                      : K / 2u);
-#ifndef DMX_MFMA_FORCE
     if (batch < 5 && tiles < kMfmaSplitTiles) return false;
     if (batch <= max_register_batch(enc) && bytes < (8ull << 20) && tiles < kMfmaSplitTiles) return false;
-#endif
     const uint32_t min_tiles = mfma_min_tiles(enc, batch);
     const int mode = enc == ENC_Q4_0   ? mfma_mode<MfmaQ40>(K, tiles, y_bf16, min_tiles)
                    : enc == ENC_Q6_K   ? mfma_mode<MfmaQ6K>(K, tiles, y_bf16, min_tiles)
