@@ -374,7 +374,9 @@ __device__ __forceinline__ uint32_t xslot(uint32_t l, uint32_t j) { return l ^ (
 
 }  // namespace
 
-template <class M, bool YBF16, bool SPLIT>
+// ROWS16: the launch's batch is 9..16 (all 16 rows of the A side staged, the
+// staging indices compile-time), else 3..8 (4 or 8 rows staged).
+template <class M, bool YBF16, bool SPLIT, bool ROWS16>
 __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr uint32_t NM = M::NM, UPR = 4u * NM;  // staging units per (task, row): (q, j)
@@ -514,8 +516,20 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     // 32 units of (g, b) lie on consecutive lanes, their maximum reduced by
     // DPP within rows of 16 lanes and v_permlane16_swap across two.  Chunks
     // of passes: all of a chunk's loads leave before the first is converted.
-    // only the segment's real tasks: padding tasks are never multiplied
-    const uint32_t nunits = nt * 16u * UPR, npass = (nunits + kMfmaThreads - 1u) / kMfmaThreads;
+    // only the segment's real tasks (padding tasks are never multiplied) and
+    // the batch's rows rounded up to RB = 4, 8 or 16: rows RB..15 of the
+    // MFMA's A side are never staged, and whatever bits their LDS slots hold
+    // reach only output rows that are never stored (each output row reads its
+    // own activation row).  Per step, the Qwen3-8B GGUF batch 4: 2.29 ->
+    // 2.19 ms, batch 8: 3.07 -> 2.73 ms.  Zero-filling those rows first (all
+    // slots, then a barrier on the LDS writes) cost more than it saved: 2.23
+    // and 2.94 ms.
+    const uint32_t rbl = ROWS16 ? 4u : p.batch <= 4u ? 2u : 3u;  // log2 RB
+    const uint32_t nunits = nt * (UPR << rbl), npass = (nunits + kMfmaThreads - 1u) / kMfmaThreads;
+    // unit u = pass·512 + tid: task g = pass·(16/RB) + tid / (32·RB), row
+    // b = (tid / 32) % RB (a constant of the thread), e = tid % 32
+    static_assert(kMfmaThreads == 16u * 32u, "a pass is 16 (task, row) pairs of 32 units");
+    const uint32_t tg = tid >> (5u + rbl), tb = (tid >> 5u) & ((1u << rbl) - 1u), gstep = 16u >> rbl;
     // A unit's raw activations, loaded unconditionally (a unit past the tasks
     // or the batch reads row 0, in bounds, and stages zeros): a load under a
     // per-lane branch would make its wave wait for it where the branch joins,
@@ -527,7 +541,8 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     auto xload = [&](auto xb, uint32_t pass, XRaw& r) {
         constexpr bool XB = decltype(xb)::value;
         const uint32_t u = pass * kMfmaThreads + tid;
-        const uint32_t g = u / (16u * UPR), b = (u / UPR) % 16u, e = u % UPR, qq = e / NM, j = e % NM;
+        const uint32_t g = ROWS16 ? u / (16u * UPR) : pass * gstep + tg, b = ROWS16 ? (u / UPR) % 16u : tb;
+        const uint32_t e = u % UPR, qq = e / NM, j = e % NM;
         r.ok = u < nunits && b < p.batch && g < nt;
         const size_t xk0 = r.ok ? (size_t)b * p.K + k0 + M::KT * g : 0u;
         if constexpr (XB) {  // two runs of 4 bf16: 8 bytes each
@@ -567,7 +582,8 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     };
     auto xstore = [&](uint32_t pass, const float (&v)[8]) {
         const uint32_t u = pass * kMfmaThreads + tid;
-        const uint32_t g = u / (16u * UPR), b = (u / UPR) % 16u, e = u % UPR, qq = e / NM, j = e % NM;
+        const uint32_t g = ROWS16 ? u / (16u * UPR) : pass * gstep + tg, b = ROWS16 ? (u / UPR) % 16u : tb;
+        const uint32_t e = u % UPR, qq = e / NM, j = e % NM;
         float mv = absmax3(v[0], v[1], v[2]);
         mv = absmax3(mv, v[3], v[4]);
         mv = absmax3(mv, v[5], v[6]);
@@ -835,7 +851,12 @@ template <class M, bool SPLIT>
 hipError_t launch_mode(MfmaParams p, uint32_t units, bool y_bf16, hipStream_t st) {
     uint32_t seg = mfma_segment<M, SPLIT>(units);
     if (seg == 0 || (y_bf16 && seg < units)) return hipErrorInvalidValue;
-    auto kernel = y_bf16 ? gemv_mfma_kernel<M, true, SPLIT> : gemv_mfma_kernel<M, false, SPLIT>;
+    // (a kernel whose row count is a run-time value stages 4 and 8 rows in a
+    // quarter and half of the passes, but runs 16 rows ~1% slower than one
+    // whose staging indices are constants: two instantiations)
+    const bool r16 = p.batch > 8u;
+    auto kernel = y_bf16 ? (r16 ? gemv_mfma_kernel<M, true, SPLIT, true> : gemv_mfma_kernel<M, true, SPLIT, false>)
+                         : (r16 ? gemv_mfma_kernel<M, false, SPLIT, true> : gemv_mfma_kernel<M, false, SPLIT, false>);
     int cus = 0, per_cu = 0;
     hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), mfma_lds_bytes<M, SPLIT>(seg), kMfmaThreads,
                                     &per_cu, &cus);
