@@ -628,7 +628,10 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
         }
     };
     static_assert(UPR == 32, "a (task, row) spans two rows of 16 lanes");
-    constexpr uint32_t kStageChunk = M::STAGE;
+    // 16 rows: chunks of 4 passes (per step, Qwen3-8B GGUF at 16 rows 3.23 ms
+    // with chunks of 8, 3.13 with 4, 3.22 with 2 and 6, 3.41 with 16; the
+    // MLX step 1126 -> 1095 us); 4 and 8 rows keep M::STAGE (4 cost 3% at 8)
+    constexpr uint32_t kStageChunk = ROWS16 ? 4u : M::STAGE;
     // The first chunk's activation loads leave first, then the first PF
     // tasks' weight loads: loads complete in issue order, so the staging
     // converts while the weights are in flight (weights first made every wave
