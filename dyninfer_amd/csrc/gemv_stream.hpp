@@ -265,9 +265,12 @@ __global__ __launch_bounds__(TH) void gguf_gemv_stream_kernel(const GemvParams p
         }
     };
     // whole rounds of U tasks, branch-free (U is a multiple of CPL, so a
-    // round starts a row step), then the last partial round task by task
+    // round starts a row step), then the last round, whole or partial, task
+    // by task: it reloads only tasks that exist, so a wave's end does not wait
+    // for D loads of its last row step again (per step, Qwen3-8B GGUF 1.295 ->
+    // 1.284 ms, Q4_K_M 1.407 -> 1.390 ms)
     uint32_t t0 = 0;
-    for (; t0 + (uint32_t)U <= T; t0 += (uint32_t)U) unroll<U>([&](auto uc) { task(t0, uc, true); });
+    for (; t0 + (uint32_t)U < T; t0 += (uint32_t)U) unroll<U>([&](auto uc) { task(t0, uc, true); });
     if (t0 < T)
         unroll<U>([&](auto uc) {
             const uint32_t t = t0 + (uint32_t)decltype(uc)::value;
