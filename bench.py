@@ -163,15 +163,21 @@ class StepRunner:
             dt = xdtype if key in ("h", "attn", "act") else ydtype
             self.bufs[key] = (torch.randn(batch, n, device="cuda", generator=gen)).to(dt)
         self.stream = torch.cuda.Stream()
+        # one workspace for every launch of the step (they run in stream order):
+        # the MFMA GEMV stages its activations in it once per call
+        code = {torch.float32: d.DTYPE_F32, torch.bfloat16: d.DTYPE_BF16}
+        need = max(d.prefill_workspace_bytes(ws, batch, code[self.bufs[xin].dtype], code[self.bufs[outs[0]].dtype])
+                   for _, ws, xin, outs in steps.launches)
+        self.work = torch.empty(need, dtype=torch.uint8, device="cuda") if need else None
 
     def launch(self, i: int, stream) -> None:
         _, ws, xin, outs = self.set.launches[i]
         x = self.bufs[xin]
         ys = [self.bufs[o] for o in outs]
         if len(ws) == 1:
-            self.ctx.qlinear(ws[0], x, ys[0], stream=stream)
+            self.ctx.qlinear(ws[0], x, ys[0], stream=stream, workspace=self.work)
         else:
-            self.ctx.qlinear_multi(ws, x, ys, stream=stream)
+            self.ctx.qlinear_multi(ws, x, ys, stream=stream, workspace=self.work)
 
     def step(self, stream) -> None:
         for i in range(len(self.set.launches)):

@@ -243,8 +243,10 @@ def supports(w: QWeight, rows: int, x_dtype: int = DTYPE_F32, y_dtype: int = DTY
 
 def prefill_workspace_bytes(ws: Sequence[QWeight], rows: int, x_dtype: int = DTYPE_F32,
                             y_dtype: int = DTYPE_F32) -> int:
-    """Device workspace bytes a qlinear / qlinear_multi call over ``ws`` with these rows
-    and dtypes needs (0 when it runs no prefill GEMM); dyninfer_mi355x_prefill_workspace_bytes."""
+    """Device workspace bytes of a qlinear / qlinear_multi call over ``ws`` with these rows
+    and dtypes (dyninfer_mi355x_prefill_workspace_bytes): required by a call that runs the
+    prefill GEMM, optional for a decode call on the MFMA GEMV (which then stages its
+    activations once per call), 0 for every other call."""
     arr = (_QWeightC * len(ws))(*[w.c() for w in ws])
     n = ctypes.c_uint64(0)
     _check(library().dyninfer_mi355x_prefill_workspace_bytes(arr, len(ws), rows, x_dtype, y_dtype, ctypes.byref(n)))
@@ -289,8 +291,11 @@ class Context:
     def _workspace(self, ws, x, rows: int, ydt: int, stream, workspace):
         """(pointer, bytes, keep-alive) of the call's device workspace: the caller's
         ``workspace`` tensor, or a new torch allocation of the size the library asks
-        for (torch's caching allocator, tied to the launch stream), or none."""
+        for (torch's caching allocator, tied to the launch stream), or none (also when
+        ``workspace`` is False: a decode call then runs without its optional one)."""
         import torch
+        if workspace is False:
+            return None, 0, None
         need = prefill_workspace_bytes(ws, rows, _dtype_code(x), ydt)
         if need == 0:
             return None, 0, None
@@ -304,7 +309,8 @@ class Context:
     def qlinear(self, w: QWeight, x, y=None, y_dtype=None, stream=None, workspace=None):
         """y = x · Wᵀ (f32 accumulation).  x: [rows, K] f32 or bf16 device tensor.
         workspace: a device tensor of at least prefill_workspace_bytes([w], rows, …)
-        bytes for a prefill call (one is allocated through torch when omitted)."""
+        bytes (one is allocated through torch when omitted and that size is not 0), or
+        False for none (decode calls only)."""
         import torch
         rows = x.shape[0] if x.dim() == 2 else 1
         if y is None:

@@ -246,9 +246,10 @@ hipError_t prefill(const dyninfer_qweight_t* ws, uint32_t count, const void* x, 
     return e;
 }
 
-// Runs rows > 16 through the GEMV kernels 16 activation rows at a time.
+// Runs rows > 16 through the GEMV kernels 16 activation rows at a time (the
+// chunks one after another on the stream, each free to use the workspace).
 hipError_t gemv_rows(const dyninfer_qweight_t* ws, uint32_t count, const void* x, uint32_t x_dtype, uint32_t rows,
-                     void* const* ys, uint32_t y_dtype, hipStream_t st) {
+                     void* const* ys, uint32_t y_dtype, uint8_t* work, uint64_t work_bytes, hipStream_t st) {
     const uint32_t K = (uint32_t)ws[0].cols;
     for (uint32_t r0 = 0; r0 < rows; r0 += dmx::kMaxGemvBatch) {
         const uint32_t nb = rows - r0 < (uint32_t)dmx::kMaxGemvBatch ? rows - r0 : (uint32_t)dmx::kMaxGemvBatch;
@@ -257,10 +258,26 @@ hipError_t gemv_rows(const dyninfer_qweight_t* ws, uint32_t count, const void* x
             probs[i] = problem_of(&ws[i], static_cast<uint8_t*>(ys[i]) + (size_t)r0 * ws[i].rows * esize(y_dtype));
         const void* xr = static_cast<const uint8_t*>(x) + (size_t)r0 * K * esize(x_dtype);
         hipError_t e = dmx::gemv_launch(ws[0].encoding, probs, (int)count, K, xr, x_dtype == DYNINFER_DTYPE_BF16, nb,
-                                        y_dtype == DYNINFER_DTYPE_BF16, ws[0].group_size, ws[0].scale_dtype, st);
+                                        y_dtype == DYNINFER_DTYPE_BF16, ws[0].group_size, ws[0].scale_dtype, work,
+                                        work_bytes, st);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+// The optional workspace of the GEMV chunks of a call (the largest any chunk
+// of 16 rows, or the last, smaller one, would use).
+uint64_t gemv_rows_workspace(const dyninfer_qweight_t* ws, uint32_t count, uint32_t rows, uint32_t y_dtype) {
+    dmx::GemvProblem probs[dmx::kMaxProblems];
+    for (uint32_t i = 0; i < count; i++) probs[i] = problem_of(&ws[i], nullptr);
+    auto need = [&](uint32_t nb) {
+        return dmx::gemv_workspace_bytes(ws[0].encoding, probs, (int)count, nb, (uint32_t)ws[0].cols,
+                                         y_dtype == DYNINFER_DTYPE_BF16, ws[0].group_size);
+    };
+    const uint64_t last = need(rows % (uint32_t)dmx::kMaxGemvBatch ? rows % (uint32_t)dmx::kMaxGemvBatch
+                                                                    : (uint32_t)dmx::kMaxGemvBatch);
+    const uint64_t full = rows > (uint32_t)dmx::kMaxGemvBatch ? need((uint32_t)dmx::kMaxGemvBatch) : 0;
+    return last > full ? last : full;
 }
 
 }  // namespace
@@ -310,7 +327,9 @@ int dyninfer_mi355x_supports(const dyninfer_qweight_t* w, uint32_t rows, uint32_
 }
 
 // Validation and routing of a qlinear_multi call, shared by the call and the
-// workspace query: whether it runs the prefill GEMM, and the workspace it needs.
+// workspace query: whether it runs the prefill GEMM, and its workspace, which
+// the prefill GEMM needs and the GEMV kernels may use (the MFMA GEMV stages
+// the activations once per call in it instead of once per workgroup).
 static int plan_multi(const dyninfer_qweight_t* ws, uint32_t count, uint32_t x_dtype, uint32_t rows,
                       uint32_t y_dtype, bool& gemm, uint64_t& need) {
     if (!ws || count == 0 || count > (uint32_t)dmx::kMaxProblems)
@@ -330,7 +349,7 @@ static int plan_multi(const dyninfer_qweight_t* ws, uint32_t count, uint32_t x_d
                                 y_dtype == DYNINFER_DTYPE_BF16);
     if (gemm && (uint64_t)rows * ws[0].cols >= (1ull << 31))
         return fail(DYNINFER_MI355X_ERR_UNSUPPORTED, "prefill: rows * K must stay below 2^31 (32-bit activation offsets)");
-    need = gemm ? dmx::prefill_workspace_bytes(rows, (uint32_t)ws[0].cols) : 0;
+    need = gemm ? dmx::prefill_workspace_bytes(rows, (uint32_t)ws[0].cols) : gemv_rows_workspace(ws, count, rows, y_dtype);
     return 0;
 }
 
@@ -350,30 +369,36 @@ static int qlinear_multi_impl(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight
     }
     if (!aligned(x, 16)) return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "activations must be 16-byte aligned");
     uint8_t* work = nullptr;
+    uint64_t work_bytes = 0;
     if (noalloc) {
-        if (need > kScratchBytes)
+        if (gemm && need > kScratchBytes)
             return fail(DYNINFER_MI355X_ERR_UNSUPPORTED,
                         "qlinear_multi_noalloc: the prefill staging of " + std::to_string(rows) + " rows x K " +
                             std::to_string(ws[0].cols) + " needs " + std::to_string(need) +
                             " bytes, more than the static scratch of " + std::to_string(kScratchBytes) +
                             " bytes; split the rows or call dyninfer_mi355x_qlinear_multi");
         work = ctx->scratch;
-    } else if (need) {
+        work_bytes = kScratchBytes;
+    } else if (need && (gemm || workspace)) {  // required for prefill; optional (NULL accepted) for the GEMV
+        const char* what = gemm ? "prefill" : "decode";
         if (!workspace || workspace_bytes < need)
             return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT,
-                        "prefill of " + std::to_string(rows) + " rows x K " + std::to_string(ws[0].cols) +
-                            " needs a device workspace of " + std::to_string(need) + " bytes (got " +
+                        std::string(what) + " of " + std::to_string(rows) + " rows x K " + std::to_string(ws[0].cols) +
+                            (gemm ? " needs a device workspace of " : " takes a device workspace (or NULL) of ") +
+                            std::to_string(need) + " bytes (got " +
                             (workspace ? std::to_string(workspace_bytes) + " bytes" : std::string("NULL")) +
                             "); size it with dyninfer_mi355x_prefill_workspace_bytes");
         if (!aligned(workspace, 256))
-            return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, "the prefill workspace must be 256-byte aligned");
+            return fail(DYNINFER_MI355X_ERR_INVALID_ARGUMENT, std::string("the ") + what +
+                                                                  " workspace must be 256-byte aligned");
         work = static_cast<uint8_t*>(workspace);
+        work_bytes = workspace_bytes;
     }
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const hipError_t e = gemm ? prefill(ws, count, x, x_dtype, rows, ys, y_dtype, work, st)
-                              : gemv_rows(ws, count, x, x_dtype, rows, ys, y_dtype, st);
+                              : gemv_rows(ws, count, x, x_dtype, rows, ys, y_dtype, work, work_bytes, st);
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     return DYNINFER_MI355X_OK;
 }

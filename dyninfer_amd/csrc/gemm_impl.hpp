@@ -89,48 +89,6 @@ __device__ __forceinline__ h8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t
     return __builtin_bit_cast(h8, u32x4{a, b, c, d});
 }
 
-// 16 bytes per lane from global memory into LDS at dst + 16·lane (dst
-// wave-uniform): global_load_lds_dwordx4, counted by vmcnt.
-__device__ __forceinline__ void dma16(const void* src, void* dst) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                     (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
-}
-
-// 4 bytes per lane into LDS at dst + 4·lane: global_load_lds_dword.
-__device__ __forceinline__ void dma4(const void* src, void* dst) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                     (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
-}
-
-// s_waitcnt vmcnt(n), other counters unconstrained.
-template <uint32_t n>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(n < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((n & 15u) | ((n >> 4) << 14) | (7u << 4) | (15u << 8));
-}
-
-// The ring's step barrier: this wave's copies older than its last n have
-// landed in LDS and its LDS reads are done (s_waitcnt vmcnt(n) lgkmcnt(0)),
-// then s_barrier.  __syncthreads() would also wait for the copies still in
-// flight (its fence waits for vmcnt(0)); the empty asm statements keep the
-// compiler from moving memory accesses across the barrier.
-template <uint32_t n>
-__device__ __forceinline__ void ring_barrier() {
-    static_assert(n < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((n & 15u) | ((n >> 4) << 14) | (7u << 4));
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-// The wait of ring_barrier<n>() without the barrier: for a wave whose ring
-// slots no other wave reads or writes.
-template <uint32_t n>
-__device__ __forceinline__ void ring_wait() {
-    static_assert(n < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((n & 15u) | ((n >> 4) << 14) | (7u << 4));
-    asm volatile("" ::: "memory");
-}
 
 // ring_barrier<BASE + k·PER>() (ring_wait when !SYNC) for a wave-uniform k in
 // [0, KMAX]: the copies of the k newest chunks, and BASE newer register

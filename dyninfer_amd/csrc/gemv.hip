@@ -111,14 +111,22 @@ hipError_t launch(uint32_t enc, const GemvParams& p, uint32_t B, uint32_t onesho
 
 }  // namespace
 
+uint64_t gemv_workspace_bytes(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K,
+                              bool y_bf16, uint32_t group) {
+    if (nprob < 1 || nprob > kMaxProblems) return 0;
+    return gemv_mfma_workspace_bytes(enc, probs, nprob, batch, K, y_bf16, group);
+}
+
 hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x, bool x_bf16,
-                       uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype, hipStream_t stream) {
+                       uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype, void* work, uint64_t work_bytes,
+                       hipStream_t stream) {
     EncInfo info;
     if (!enc_info(enc, info) || nprob < 1 || nprob > kMaxProblems || batch < 1 || batch > (uint32_t)kMaxGemvBatch)
         return hipErrorInvalidValue;
     // 5..16 activation rows: every weight decoded once for all rows, on MFMA
     if (gemv_mfma_applies(enc, probs, nprob, batch, K, y_bf16, group))
-        return gemv_mfma_launch(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, stream);
+        return gemv_mfma_launch(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, work, work_bytes,
+                                stream);
     // Register batch: the next power of two, halved while its activation tile
     // does not fit one workgroup's LDS; larger batches run as several passes.
     uint32_t lim = 0;
@@ -138,7 +146,7 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
                 sub[i].y = static_cast<uint8_t*>(probs[i].y) + (size_t)r0 * probs[i].n * yes;
             }
             const void* xr = static_cast<const uint8_t*>(x) + (size_t)r0 * K * xes;
-            hipError_t e = gemv_launch(enc, sub, nprob, K, xr, x_bf16, nb, y_bf16, group, sdtype, stream);
+            hipError_t e = gemv_launch(enc, sub, nprob, K, xr, x_bf16, nb, y_bf16, group, sdtype, nullptr, 0, stream);
             if (e != hipSuccess) return e;
         }
         return hipSuccess;

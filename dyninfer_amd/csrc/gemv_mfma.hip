@@ -29,7 +29,9 @@
 //     b, scaled by a power of two per (row, task) whose largest magnitude
 //     lands in [2^13, 2^14) (no overflow, no flush of the task's large values),
 //     rounded once to f16; a task's MFMAs accumulate into a zeroed tile that
-//     is then added to the f32 total times the inverse scale;
+//     is then added to the f32 total times the inverse scale.  With a
+//     workspace, a prep kernel stages them so once per call, in the LDS
+//     layout, and each workgroup copies its segment by LDS DMA;
 //   * weights stream coalesced: a task's bytes of the tile's 16 rows (one
 //     4-byte-aligned window per row) are loaded as 16-byte pieces with
 //     consecutive lanes on consecutive pieces of a row, so a load
@@ -78,6 +80,7 @@ struct MfmaParams {
     const uint8_t* sc[kMaxProblems];  // MLX scales
     const uint8_t* bi[kMaxProblems];  // MLX biases
     uint32_t split_ws_log2;           // split mode: log2 of the waves per tile (3, or 2: two tiles per workgroup)
+    const uint8_t* pre;               // XS_PRE: the activations staged by gemv_mfma_prep_kernel
 };
 
 // (c + off)·s for a packed pair (v_pk_add_f16, v_pk_mul_f16)
@@ -372,12 +375,85 @@ __host__ __device__ constexpr uint32_t mfma_lds_bytes(uint32_t nunit) {
 // threads of one (task, row) spread their writes over the LDS bank groups.
 __device__ __forceinline__ uint32_t xslot(uint32_t l, uint32_t j) { return l ^ ((j + 4u * ((l >> 4) & 1u)) & 7u); }
 
+// The staged form of one unit, the 8 activations v of activation row b for MFMA
+// j of lane quarter q of a task: its f16 pairs in the B-operand order, the
+// (task, row)'s inverse scale and, for the offset encodings, the quarter's
+// scaled sums.  The 32 units of a (task, row) sit on 32 aligned consecutive
+// lanes, which all call this together: the maximum (DPP within rows of 16
+// lanes, v_permlane16_swap across two) and the quarter sums (8 lanes) are
+// cross-lane.
+struct Staged {
+    uint4 val;
+    float inv;
+    uint32_t xs;
+};
+template <class M>
+__device__ __forceinline__ Staged stage_unit(const float (&v)[8]) {
+    float mv = absmax3(v[0], v[1], v[2]);
+    mv = absmax3(mv, v[3], v[4]);
+    mv = absmax3(mv, v[5], v[6]);
+    mv = absmax3(mv, v[7], v[7]);
+    uint32_t mx = __float_as_uint(mv);  // non-negative floats order as integers
+    mx = lanes_reduce<8>(mx, [](uint32_t a, uint32_t c) { return a > c ? a : c; });
+    mx = max(mx, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0x140, 0xF, 0xF, false));  // row_mirror: 16 lanes
+    {  // and the neighbouring row of 16
+        const auto r = __builtin_amdgcn_permlane16_swap(mx, mx, false, false);
+        mx = max(r[0], r[1]);
+    }
+    int ex = 0;
+    (void)frexpf(__uint_as_float(mx), &ex);
+    ex = ex < -110 ? -110 : ex;  // keeps the scale a normal f32
+    const int sh = 14 - ex;      // largest magnitude / 2^(ex-14) < 2^14
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    auto pk = [&](float a, float c) {
+        const f32x2 f = {ldexpf(a, sh), ldexpf(c, sh)};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));  // RNE
+    };
+    Staged st;
+    // pair order: (r, r+2) (r+1, r+3) of each run, or (r, r+4) ... (r+3, r+7)
+    // of one run of 8 (MLX words)
+    st.val = M::PAIR4 ? make_uint4(pk(v[0], v[4]), pk(v[1], v[5]), pk(v[2], v[6]), pk(v[3], v[7]))
+                      : make_uint4(pk(v[0], v[2]), pk(v[1], v[3]), pk(v[4], v[6]), pk(v[5], v[7]));
+    st.inv = ldexpf(1.0f, -sh);
+    st.xs = 0u;
+    if constexpr (M::BIAS) {
+        // the unit's two runs summed as stored (f16 values, exact in f32
+        // but for the last bits of 32-term sums), over the NM units of
+        // its quarter (8 consecutive lanes), stored / 32 as f16 (below
+        // 2^14) for the offset MFMA
+        const uint32_t one2 = 0x3C003C00u;
+        float s0 = dot2(st.val.x, one2, dot2(st.val.y, one2, 0.0f)), s1 = dot2(st.val.z, one2, dot2(st.val.w, one2, 0.0f));
+        auto fadd = [](uint32_t a, uint32_t c) { return __float_as_uint(__uint_as_float(a) + __uint_as_float(c)); };
+        s0 = __uint_as_float(lanes_reduce<8>(__float_as_uint(s0), fadd));
+        s1 = __uint_as_float(lanes_reduce<8>(__float_as_uint(s1), fadd));
+        const f32x2 f = {s0 * 0.03125f, s1 * 0.03125f};
+        st.xs = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));
+    }
+    return st;
+}
+
+// The staged activations of a whole call in device memory (the caller's
+// workspace), laid out as one workgroup's LDS holds a segment: the fragments
+// of every task of K, then the inverse scales of every (task, row), then (for
+// the offset encodings) the quarter sums; a segment's tasks are a contiguous
+// range of each part.
+template <class M>
+__host__ __device__ constexpr uint64_t mfma_prestage_bytes(uint32_t K) {
+    return (uint64_t)(K / M::KT) * mfma_task_lds<M>();
+}
+
 }  // namespace
 
-// ROWS16: the launch's batch is 9..16 (all 16 rows of the A side staged, the
-// staging indices compile-time), else 3..8 (4 or 8 rows staged).
-template <class M, bool YBF16, bool SPLIT, bool ROWS16>
+// How a workgroup fills its LDS with the segment's activations: it stages them
+// itself, the batch being 3..8 (4 or 8 rows of the A side staged) or 9..16
+// (all 16 rows, the staging indices compile-time), or it copies them from the
+// call's workspace, where gemv_mfma_prep_kernel staged them once for all
+// workgroups.
+enum MfmaStaging { XS_ROWS8 = 0, XS_ROWS16 = 1, XS_PRE = 2 };
+
+template <class M, bool YBF16, bool SPLIT, int XS>
 __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParams p) {
+    constexpr bool ROWS16 = XS == XS_ROWS16;
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr uint32_t NM = M::NM, UPR = 4u * NM;  // staging units per (task, row): (q, j)
     constexpr uint32_t NSLOT = 16u * M::NP, NLD = (NSLOT + 63u) / 64u;  // window pieces, loads per lane
@@ -584,47 +660,11 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
         const uint32_t u = pass * kMfmaThreads + tid;
         const uint32_t g = ROWS16 ? u / (16u * UPR) : pass * gstep + tg, b = ROWS16 ? (u / UPR) % 16u : tb;
         const uint32_t e = u % UPR, qq = e / NM, j = e % NM;
-        float mv = absmax3(v[0], v[1], v[2]);
-        mv = absmax3(mv, v[3], v[4]);
-        mv = absmax3(mv, v[5], v[6]);
-        mv = absmax3(mv, v[7], v[7]);
-        uint32_t mx = __float_as_uint(mv);  // non-negative floats order as integers
-        mx = lanes_reduce<8>(mx, [](uint32_t a, uint32_t c) { return a > c ? a : c; });
-        mx = max(mx, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0x140, 0xF, 0xF, false));  // row_mirror: 16 lanes
-        {  // and the neighbouring row of 16
-            const auto r = __builtin_amdgcn_permlane16_swap(mx, mx, false, false);
-            mx = max(r[0], r[1]);
-        }
-        int ex = 0;
-        (void)frexpf(__uint_as_float(mx), &ex);
-        ex = ex < -110 ? -110 : ex;  // keeps the scale a normal f32
-        const int sh = 14 - ex;      // largest magnitude / 2^(ex-14) < 2^14
-        typedef float f32x2 __attribute__((ext_vector_type(2)));
-        auto pk = [&](float a, float c) {
-            const f32x2 f = {ldexpf(a, sh), ldexpf(c, sh)};
-            return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));  // RNE
-        };
-        // pair order: (r, r+2) (r+1, r+3) of each run, or (r, r+4) ... (r+3, r+7)
-        // of one run of 8 (MLX words)
-        const uint4 val = M::PAIR4 ? make_uint4(pk(v[0], v[4]), pk(v[1], v[5]), pk(v[2], v[6]), pk(v[3], v[7]))
-                                   : make_uint4(pk(v[0], v[2]), pk(v[1], v[3]), pk(v[4], v[6]), pk(v[5], v[7]));
-        if constexpr (M::BIAS) {
-            // the unit's two runs summed as stored (f16 values, exact in f32
-            // but for the last bits of 32-term sums), over the NM units of
-            // its quarter (8 consecutive lanes), stored / 32 as f16 (below
-            // 2^14) for the offset MFMA
-            const uint32_t one2 = 0x3C003C00u;
-            float s0 = dot2(val.x, one2, dot2(val.y, one2, 0.0f)), s1 = dot2(val.z, one2, dot2(val.w, one2, 0.0f));
-            auto fadd = [](uint32_t a, uint32_t c) { return __float_as_uint(__uint_as_float(a) + __uint_as_float(c)); };
-            s0 = __uint_as_float(lanes_reduce<8>(__float_as_uint(s0), fadd));
-            s1 = __uint_as_float(lanes_reduce<8>(__float_as_uint(s1), fadd));
-            typedef float f32x2 __attribute__((ext_vector_type(2)));
-            const f32x2 f = {s0 * 0.03125f, s1 * 0.03125f};
-            if (u < nunits && j == 0) xs[(g * 16u + b) * 4u + qq] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));
-        }
+        const Staged st = stage_unit<M>(v);
         if (u < nunits) {
-            xl[(g * NM + j) * 64u + xslot(b + 16u * qq, j)] = val;
-            if (e == 0) inv[g * 16u + b] = ldexpf(1.0f, -sh);
+            xl[(g * NM + j) * 64u + xslot(b + 16u * qq, j)] = st.val;
+            if (e == 0) inv[g * 16u + b] = st.inv;
+            if (M::BIAS && j == 0) xs[(g * 16u + b) * 4u + qq] = st.xs;
         }
     };
     static_assert(UPR == 32, "a (task, row) spans two rows of 16 lanes");
@@ -671,9 +711,29 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
             }
         }
     };
-    if (p.x_bf16) stage(std::true_type{});
-    else stage(std::false_type{});
-    __syncthreads();
+    if constexpr (XS == XS_PRE) {
+        // The segment's staged tasks are one contiguous range of the workspace,
+        // laid out as LDS holds them: copied by LDS DMA, 1 KiB per wave
+        // instruction (the last one partial), then the first PF tasks' weight
+        // loads; the wait before the barrier covers the copies only (loads
+        // complete in issue order), so the weights stay in flight.  (Copying
+        // only the staged rows' slots of each fragment chunk, half of them at
+        // 5..8 rows, measured slower: a per-lane test per instruction.)
+        constexpr uint32_t TL = mfma_task_lds<M>();
+        const uint8_t* src = p.pre + (size_t)sidx * (p.seg_units / M::UPT) * TL;
+        const uint32_t bytes = nt * TL, nch = (bytes + 1023u) / 1024u;
+        for (uint32_t c = wv; c < nch; c += NW)
+            if (c * 1024u + 16u * lane < bytes) dma16(src + c * 1024u + 16u * lane, lds + c * 1024u);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < PF; s++) load(rcur, t0 + (uint32_t)s, ring[s], rx[s]);
+        __builtin_amdgcn_sched_barrier(0);
+        ring_barrier<(uint32_t)PF * (NLD + (M::MLX ? 4u : 0u))>();  // (__syncthreads would wait for all loads)
+    } else {
+        if (p.x_bf16) stage(std::true_type{});
+        else stage(std::false_type{});
+        __syncthreads();
+    }
 
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 acc = zero;
@@ -850,16 +910,96 @@ __global__ __launch_bounds__(256) void mfma_zero_outputs_kernel(const MfmaParams
     if (i < p.nprob && e < (uint64_t)p.batch * pick(i, p.n)) gptr_mut<float>(pick(i, p.y))[e] = 0.0f;
 }
 
+// Stages a call's activations once, into the workspace, for a launch whose
+// workgroups copy them (XS_PRE): unit u = (task g of all of K, row b < RB, e =
+// q·NM + j) as the in-kernel staging forms it, with the 32 units of a (task,
+// row) on 32 consecutive lanes, stored where segment g / seg_tasks of the
+// launch finds it in its contiguous range (laid out as its LDS).  Rows past
+// the batch stage zeros; rows RB..15 are not staged (their slots reach only
+// output rows that are never stored).  Also clears the f32 outputs of a
+// launch whose segments add into them.
+constexpr uint32_t kMfmaPrepThreads = 256;
+template <class M>
+__global__ __launch_bounds__(kMfmaPrepThreads) void gemv_mfma_prep_kernel(const MfmaParams p, uint32_t rbl) {
+    constexpr uint32_t NM = M::NM, UPR = 4u * NM, TL = mfma_task_lds<M>();
+    static_assert(UPR == 32, "a (task, row) spans 32 lanes");
+    const uint32_t tid = threadIdx.x, gid = blockIdx.x * kMfmaPrepThreads + tid;
+    const uint32_t tall = p.nunit / M::UPT, seg_tasks = p.seg_units / M::UPT;
+    const uint32_t total = tall * (UPR << rbl);
+    const uint32_t u = gid < total ? gid : 0u;
+    const uint32_t g = u >> (5u + rbl), b = (u >> 5u) & ((1u << rbl) - 1u), e = u % UPR, qq = e / NM, j = e % NM;
+    const bool ok = gid < total && b < p.batch;
+    const size_t xk0 = ok ? (size_t)b * p.K + M::KT * g : 0u;
+    float v[8];
+    if (p.x_bf16) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const uint16_t* xr = static_cast<const uint16_t*>(p.x) + xk0;
+        const u32x2 lo2 = *gptr<u32x2>(xr + M::run0(qq, j)), hi2 = *gptr<u32x2>(xr + M::run1(qq, j));
+        const uint32_t w[4] = {lo2[0], lo2[1], hi2[0], hi2[1]};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+        }
+    } else {
+        const float* xr = static_cast<const float*>(p.x) + xk0;
+        const f32x4 lo4 = *gptr<f32x4>(xr + M::run0(qq, j)), hi4 = *gptr<f32x4>(xr + M::run1(qq, j));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[i] = lo4[i];
+            v[4 + i] = hi4[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = ok ? v[i] : 0.0f;
+    const Staged st = stage_unit<M>(v);  // every lane: the cross-lane steps need whole groups of 32
+    if (gid < total) {
+        const uint32_t sg = g / seg_tasks, t = g - sg * seg_tasks;
+        const uint32_t nts = tall - sg * seg_tasks < seg_tasks ? tall - sg * seg_tasks : seg_tasks;
+        uint8_t* base = const_cast<uint8_t*>(p.pre) + (size_t)sg * seg_tasks * TL;
+        *gptr_mut<u32x4>(base + ((t * NM + j) * 64u + xslot(b + 16u * qq, j)) * 16u) = u32x4{st.val.x, st.val.y, st.val.z, st.val.w};
+        if (e == 0) *gptr_mut<float>(base + nts * NM * 1024u + (t * 16u + b) * 4u) = st.inv;
+        if (M::BIAS && j == 0) *gptr_mut<uint32_t>(base + nts * (NM * 1024u + 64u) + ((t * 16u + b) * 4u + qq) * 4u) = st.xs;
+    }
+    if (p.accumulate) {  // every segment adds into y
+        const uint32_t stride = gridDim.x * kMfmaPrepThreads;
+        for (uint32_t i = 0; i < p.nprob; i++) {
+            const uint32_t elems = p.batch * pick(i, p.n);
+            for (uint32_t ei = gid; ei < elems; ei += stride) gptr_mut<float>(pick(i, p.y))[ei] = 0.0f;
+        }
+    }
+}
+
+// Whether a launch stages its activations once per call (when the caller
+// gives a workspace) rather than in every workgroup: from K =
+// kMfmaPrestageMinK on, at 9..16 rows, or when K takes several LDS segments
+// (each staged by its own workgroups, and y cleared by one more launch, which
+// the prep kernel replaces).  Per launch, Qwen3-8B Q4_0/Q6_K at 16 rows: q/k/v
+// 13.5 -> 11.6 us, o_proj 11.5 -> 9.3, gate/up 23.4 -> 22.6, down_proj (K =
+// 12288, three segments) 35.0 -> 26.5, lm_head 123 either way; at 8 rows the
+// prep launch costs more than it saves on one segment (q/k/v 11.3 -> 11.5,
+// gate/up 21.6 -> 22.6, lm_head 116 -> 120 us) and down_proj still gains,
+// 30.3 -> 26.5 us.
+constexpr uint32_t kMfmaPrestageMinK = 2048;
+template <class M>
+bool mfma_prestages(uint32_t K, uint32_t batch, int mode) {
+    if (K < kMfmaPrestageMinK || mode == 0) return false;
+    const uint32_t units = K / M::UNIT;
+    const uint32_t seg = mode == 2 ? mfma_segment<M, true>(units) : mfma_segment<M, false>(units);
+    return batch > 8u || seg < units;
+}
+
 template <class M, bool SPLIT>
-hipError_t launch_mode(MfmaParams p, uint32_t units, bool y_bf16, hipStream_t st) {
+hipError_t launch_mode(MfmaParams p, uint32_t units, bool y_bf16, uint8_t* pre, hipStream_t st) {
     uint32_t seg = mfma_segment<M, SPLIT>(units);
     if (seg == 0 || (y_bf16 && seg < units)) return hipErrorInvalidValue;
     // (a kernel whose row count is a run-time value stages 4 and 8 rows in a
     // quarter and half of the passes, but runs 16 rows ~1% slower than one
     // whose staging indices are constants: two instantiations)
     const bool r16 = p.batch > 8u;
-    auto kernel = y_bf16 ? (r16 ? gemv_mfma_kernel<M, true, SPLIT, true> : gemv_mfma_kernel<M, true, SPLIT, false>)
-                         : (r16 ? gemv_mfma_kernel<M, false, SPLIT, true> : gemv_mfma_kernel<M, false, SPLIT, false>);
+    auto kernel = pre ? (y_bf16 ? gemv_mfma_kernel<M, true, SPLIT, XS_PRE> : gemv_mfma_kernel<M, false, SPLIT, XS_PRE>)
+                : y_bf16 ? (r16 ? gemv_mfma_kernel<M, true, SPLIT, XS_ROWS16> : gemv_mfma_kernel<M, true, SPLIT, XS_ROWS8>)
+                         : (r16 ? gemv_mfma_kernel<M, false, SPLIT, XS_ROWS16> : gemv_mfma_kernel<M, false, SPLIT, XS_ROWS8>);
     int cus = 0, per_cu = 0;
     hipError_t e = cached_occupancy(reinterpret_cast<const void*>(kernel), mfma_lds_bytes<M, SPLIT>(seg), kMfmaThreads,
                                     &per_cu, &cus);
@@ -903,7 +1043,15 @@ hipError_t launch_mode(MfmaParams p, uint32_t units, bool y_bf16, hipStream_t st
     p.seg_units = seg;
     p.nseg = nseg;
     p.accumulate = nseg > 1u ? 1u : 0u;
-    if (nseg > 1u) {  // every segment adds into y (f32): clear it first
+    if (pre) {  // stage once (and clear y when the segments add into it)
+        p.pre = pre;
+        const uint32_t rbl = p.batch <= 4u ? 2u : p.batch <= 8u ? 3u : 4u;
+        const uint64_t total = (uint64_t)(units / M::UPT) * (32u << rbl);
+        hipLaunchKernelGGL(gemv_mfma_prep_kernel<M>, dim3((unsigned)((total + kMfmaPrepThreads - 1u) / kMfmaPrepThreads)),
+                           dim3(kMfmaPrepThreads), 0, st, p, rbl);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    } else if (nseg > 1u) {  // every segment adds into y (f32): clear it first
         uint32_t nmax = 0;
         for (uint32_t i = 0; i < p.nprob; i++) nmax = p.n[i] > nmax ? p.n[i] : nmax;
         const uint64_t elems = (uint64_t)p.batch * nmax;
@@ -925,7 +1073,8 @@ uint32_t mfma_min_tiles(uint32_t enc, uint32_t batch) {
 
 template <class M>
 hipError_t launch_mfma(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x, bool x_bf16,
-                       uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype, hipStream_t st) {
+                       uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype, void* work, uint64_t work_bytes,
+                       hipStream_t st) {
     const uint32_t min_tiles = mfma_min_tiles(enc, batch);
     MfmaParams p = {};
     uint32_t tiles = 0;
@@ -948,8 +1097,11 @@ hipError_t launch_mfma(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     p.group = group;
     p.sdtype = sdtype;
     const uint32_t units = K / M::UNIT;
-    return mfma_mode<M>(K, tiles, y_bf16, min_tiles) == 2 ? launch_mode<M, true>(p, units, y_bf16, st)
-                                                  : launch_mode<M, false>(p, units, y_bf16, st);
+    const int mode = mfma_mode<M>(K, tiles, y_bf16, min_tiles);
+    uint8_t* pre = work && work_bytes >= mfma_prestage_bytes<M>(K) && mfma_prestages<M>(K, batch, mode)
+                       ? static_cast<uint8_t*>(work)
+                       : nullptr;
+    return mode == 2 ? launch_mode<M, true>(p, units, y_bf16, pre, st) : launch_mode<M, false>(p, units, y_bf16, pre, st);
 }
 
 // 2: split mode, 1: whole tiles per wave, 0: not on MFMA (with bf16 outputs
@@ -1007,16 +1159,39 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     return mode != 0;
 }
 
+uint64_t gemv_mfma_workspace_bytes(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K,
+                                   bool y_bf16, uint32_t group) {
+    if (!gemv_mfma_applies(enc, probs, nprob, batch, K, y_bf16, group)) return 0;
+    uint32_t tiles = 0;
+    for (int i = 0; i < nprob; i++) tiles += (probs[i].n + 15u) / 16u;
+    const uint32_t min_tiles = mfma_min_tiles(enc, batch);
+    auto size = [&](auto pol) -> uint64_t {
+        using M = decltype(pol);
+        if (!mfma_prestages<M>(K, batch, mfma_mode<M>(K, tiles, y_bf16, min_tiles))) return 0;
+        return (mfma_prestage_bytes<M>(K) + 255u) & ~(uint64_t)255u;
+    };
+    return enc == ENC_Q4_0   ? size(MfmaQ40{})
+         : enc == ENC_Q6_K   ? size(MfmaQ6K{})
+         : enc == ENC_Q4_K   ? size(MfmaQ4K{})
+         : enc == ENC_Q5_K   ? size(MfmaQ5K{})
+         : enc == ENC_IQ4_XS ? size(MfmaIQ4XS{})
+                             : size(MfmaMlxU4{});
+}
+
 hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x, bool x_bf16,
-                            uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype, hipStream_t st) {
+                            uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype, void* work,
+                            uint64_t work_bytes, hipStream_t st) {
     if (nprob < 1 || nprob > kMaxProblems) return hipErrorInvalidValue;
-    if (enc == ENC_Q4_0) return launch_mfma<MfmaQ40>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
-    if (enc == ENC_Q6_K) return launch_mfma<MfmaQ6K>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
-    if (enc == ENC_Q4_K) return launch_mfma<MfmaQ4K>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
-    if (enc == ENC_Q5_K) return launch_mfma<MfmaQ5K>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
-    if (enc == ENC_IQ4_XS)
-        return launch_mfma<MfmaIQ4XS>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
-    if (enc == ENC_MLX_U4) return launch_mfma<MfmaMlxU4>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, st);
+    auto go = [&](auto pol) {
+        return launch_mfma<decltype(pol)>(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, work,
+                                          work_bytes, st);
+    };
+    if (enc == ENC_Q4_0) return go(MfmaQ40{});
+    if (enc == ENC_Q6_K) return go(MfmaQ6K{});
+    if (enc == ENC_Q4_K) return go(MfmaQ4K{});
+    if (enc == ENC_Q5_K) return go(MfmaQ5K{});
+    if (enc == ENC_IQ4_XS) return go(MfmaIQ4XS{});
+    if (enc == ENC_MLX_U4) return go(MfmaMlxU4{});
     return hipErrorInvalidValue;
 }
 

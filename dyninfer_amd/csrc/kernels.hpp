@@ -82,10 +82,16 @@ struct GemvProblem {
     uint32_t n;
 };
 
-// Decode GEMV: y_i[r, :] = x[r, :] · W_iᵀ for r < batch (<= 16).
+// Decode GEMV: y_i[r, :] = x[r, :] · W_iᵀ for r < batch (<= 16).  work: an
+// optional device workspace (256-byte aligned, or NULL) of work_bytes, used by
+// the MFMA GEMV when it holds gemv_workspace_bytes.
 hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x,
-                       bool x_bf16, uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype,
-                       hipStream_t stream);
+                       bool x_bf16, uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype, void* work,
+                       uint64_t work_bytes, hipStream_t stream);
+// The workspace with which a decode GEMV call stages its activations once per
+// call instead of once per workgroup (0: none helps).
+uint64_t gemv_workspace_bytes(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K,
+                              bool y_bf16, uint32_t group);
 
 // Decode GEMV on MFMA for 3..16 activation rows (Q4_0, Q6_K, Q4_K, Q5_K, IQ4_XS, MLX U4; K a
 // multiple of 256): whether it serves a call, and the launch (several
@@ -93,7 +99,13 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
 bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool y_bf16,
                        uint32_t group);
 hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x, bool x_bf16,
-                            uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype, hipStream_t stream);
+                            uint32_t batch, bool y_bf16, uint32_t group, uint32_t sdtype, void* work,
+                            uint64_t work_bytes, hipStream_t stream);
+// The workspace with which an MFMA GEMV call stages its activations once (the
+// f16 fragments, inverse scales and offset sums of every 256-k task), or 0
+// when it stages them in every workgroup.
+uint64_t gemv_mfma_workspace_bytes(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K,
+                                   bool y_bf16, uint32_t group);
 
 // Whether one activation row of K elements fits the GEMV's LDS tile.
 bool gemv_k_supported(uint32_t enc, uint32_t K);

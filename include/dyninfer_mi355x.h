@@ -21,7 +21,8 @@
  *     device memory; the library never repacks or copies weights and derives no
  *     parameters from them (README.md:5-9, crates/dyninfer-compiler/src/lib.rs:630),
  *     and it allocates no device memory: a call's temporary (the prefill staging of
- *     dyninfer_mi355x_qlinear) lives in a workspace the caller sizes with
+ *     dyninfer_mi355x_qlinear, and the optional activation staging of its 3..16-row
+ *     MFMA GEMV) lives in a workspace the caller sizes with
  *     dyninfer_mi355x_prefill_workspace_bytes and passes in, the counterpart of the
  *     reference's device-local, non-persistent GPU temporaries
  *     (docs/quantization/mlx-affine-u4.md:26-27) bound like its parameters as
@@ -141,10 +142,15 @@ const char* dyninfer_mi355x_last_error(void);
  *     case (K not a multiple of 64, Q4_0, Q6_K, Q4_K, Q5_K and IQ4_XS at 17..32 rows
  *     with K <= 8192) runs the GEMV kernels over 16-row chunks.
  * workspace: device memory of at least dyninfer_mi355x_prefill_workspace_bytes() for
- *   the same arguments, 256-byte aligned, or NULL when that size is 0 (every call of
- *   1..16 rows, and the 16-row-chunk prefill).  A call whose workspace is missing,
- *   misaligned or too small fails with DYNINFER_MI355X_ERR_INVALID_ARGUMENT before
- *   anything is enqueued.  The call's kernels write and read it in stream order; the
+ *   the same arguments, 256-byte aligned, or NULL when that size is 0.  A call that
+ *   runs the GEMV kernels (1..16 rows, and the 16-row chunks) may also pass NULL: the
+ *   size is then that of an optional staging (the MFMA GEMV with K >= 2048, at 9..16
+ *   rows or with K too long for one LDS segment: the activations are staged once per
+ *   call by a small kernel and copied into each workgroup's LDS, instead of being
+ *   staged by every workgroup; same results).  A call
+ *   whose workspace is given but misaligned or too small, or missing when the prefill
+ *   GEMM needs it, fails with DYNINFER_MI355X_ERR_INVALID_ARGUMENT before anything is
+ *   enqueued.  The call's kernels write and read it in stream order; the
  *   caller may reuse it for the next call on the same stream, and must not touch it
  *   (or hand it to a call on another stream) until this call's work has completed.
  *   Nothing the workspace holds carries over between calls.
@@ -179,10 +185,15 @@ int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qwe
                                   uint64_t workspace_bytes, void* stream);
 
 /*
- * Device workspace bytes that dyninfer_mi355x_qlinear (count = 1) or _qlinear_multi
- * needs for these weights, rows and dtypes, in *out_bytes: 0 for every call that runs
- * no prefill GEMM, else round_up(round_up(rows, 32)*K*2, 256) + 4*round_up(rows, 256)
- * (the f16 operand fragments of x, then one f32 row factor per row).  Validates the
+ * Device workspace bytes of dyninfer_mi355x_qlinear (count = 1) or _qlinear_multi for
+ * these weights, rows and dtypes, in *out_bytes.  A call that runs the prefill GEMM
+ * needs round_up(round_up(rows, 32)*K*2, 256) + 4*round_up(rows, 256) (the f16
+ * operand fragments of x, then one f32 row factor per row).  A GEMV call (16-row
+ * chunks beyond 16 rows) that runs on the MFMA GEMV with K >= 2048, at 9..16 rows or
+ * with K too long for one LDS segment (K > 4096 at most shapes), takes an optional
+ * round_up((K/256) * T, 256), T = 8256 (T = 8512 for Q4_K and Q5_K): per 256 k, the
+ * f16 MFMA fragments of 16 activation rows, their 16 f32 inverse scales (and the
+ * f16 sums of the offset encodings); every other call 0.  Validates the
  * arguments as the call does (same status codes, pointers checked for alignment only);
  * host-only, enqueues nothing.  The reference's temporary-memory qualification
  * (docs/quantization/mlx-affine-u4.md:52-54) reads this figure.
@@ -202,8 +213,10 @@ int dyninfer_mi355x_prefill_workspace_bytes(const dyninfer_qweight_t* ws, uint32
  * Calls no hipMalloc/hipFree or allocating routine.  Every call on one device shares
  * that device's array and leaves it holding the last staging: calls that overlap on
  * one device (concurrent streams, or threads without ordering) race and may return
- * wrong results; calls ordered on one stream are safe.  Decode calls (rows <= 16) use
- * no scratch and are identical to dyninfer_mi355x_qlinear_multi.
+ * wrong results; calls ordered on one stream are safe.  Decode calls stage their
+ * activations in the array too where the MFMA GEMV takes the optional staging
+ * (K/256 * 8.5 KiB, when that fits), with results identical to
+ * dyninfer_mi355x_qlinear_multi's.
  */
 #define DYNINFER_MI355X_NOALLOC_SCRATCH_BYTES (32u << 20)
 int dyninfer_mi355x_qlinear_multi_noalloc(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qweight_t* ws,

@@ -157,17 +157,30 @@ def _ws_bytes(m, k):
     return (((m + 31) // 32 * 32 * k * 2 + 255) // 256) * 256 + 4 * ((m + 255) // 256 * 256)
 
 
+def _decode_ws_bytes(enc, k):
+    """The documented optional workspace of a decode call on the MFMA GEMV (K >= 2048):
+    K/256 tasks of 8 KiB of f16 fragments and 64 bytes of scales, plus 256 bytes of
+    offset sums for Q4_K and Q5_K, rounded up to 256."""
+    per = 8192 + 64 + (256 if enc in (d.ENC_Q4_K, d.ENC_Q5_K) else 0)
+    return (k // 256 * per + 255) // 256 * 256
+
+
 @pytest.mark.parametrize("enc,k", [(d.ENC_Q4_0, 1024), (d.ENC_Q4_1, 1024), (d.ENC_Q8_0, 3072), (d.ENC_Q6_K, 4096),
                                    (d.ENC_Q4_K, 4096), (d.ENC_IQ4_XS, 1024)])
 def test_prefill_workspace_bytes_follows_the_routing(enc, k):
-    """0 for decode rows and for the 16-row-chunk prefill, the documented staging size
-    whenever the call runs the prefill GEMM (host-only query, no device needed)."""
+    """The documented staging size whenever the call runs the prefill GEMM; for GEMV
+    calls 0, or the optional staging of 16-row chunks on the MFMA GEMV (these 256
+    tiles of 16 weight rows take it at 16 rows, not at 1 or 4; K >= 2048 only)
+    (host-only query, no device needed)."""
     ws = [w(enc, 3072, k), w(enc, 1024, k)]
-    for rows in (1, 4, 16):
+    mfma16 = _decode_ws_bytes(enc, k) if enc in (d.ENC_Q6_K, d.ENC_Q4_K) else 0
+    for rows in (1, 4):
         assert d.prefill_workspace_bytes(ws, rows) == 0
+    assert d.prefill_workspace_bytes(ws, 16) == mfma16
     chunked = enc in (d.ENC_Q4_0, d.ENC_Q6_K, d.ENC_Q4_K, d.ENC_Q5_K, d.ENC_IQ4_XS) and k <= 8192
     for rows in (17, 32):
-        assert d.prefill_workspace_bytes(ws, rows, d.DTYPE_BF16, d.DTYPE_BF16) == (0 if chunked else _ws_bytes(rows, k))
+        assert d.prefill_workspace_bytes(ws, rows, d.DTYPE_BF16, d.DTYPE_BF16) == (mfma16 if chunked
+                                                                                     else _ws_bytes(rows, k))
     for rows in (33, 128, 512, 2048, 3000):
         assert d.prefill_workspace_bytes(ws, rows, d.DTYPE_BF16, d.DTYPE_BF16) == _ws_bytes(rows, k)
         assert d.prefill_workspace_bytes(ws[:1], rows) == _ws_bytes(rows, k)

@@ -22,7 +22,8 @@ pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
 XF16 = 2.0 ** -11 + 2e-5
-ENC = {oracle.Q4_0: d.ENC_Q4_0, oracle.Q4_1: d.ENC_Q4_1, oracle.Q8_0: d.ENC_Q8_0, oracle.Q6_K: d.ENC_Q6_K}
+ENC = {oracle.Q4_0: d.ENC_Q4_0, oracle.Q4_1: d.ENC_Q4_1, oracle.Q8_0: d.ENC_Q8_0, oracle.Q6_K: d.ENC_Q6_K,
+       oracle.Q4_K: d.ENC_Q4_K, oracle.Q5_K: d.ENC_Q5_K, oracle.IQ4_XS: d.ENC_IQ4_XS}
 
 
 def dev(a):
@@ -192,31 +193,104 @@ def test_gemv_mfma(ctx, gtype, n, k, batch, ybf16, off):
     assert np.all(err <= 2.0 ** -10 + 2e-5 + extra), err.max()
 
 
+# The optional workspace of the MFMA GEMV (K >= 2048, at 9..16 rows or when K
+# takes several LDS segments): a prep kernel stages the activations once per
+# call and every workgroup copies them into LDS, instead of staging them itself.
+# The staged values and the order of the products are the same, so the outputs
+# are identical (K segments add atomically, in either order: within 1e-6 of
+# Σ|w||x|).  The workspace starts as 0xFF bytes (NaN in f16 and f32), so
+# activation rows the prep kernel leaves unstaged (past the batch rounded up
+# to 4, 8 or 16) must not reach a stored output.  3 rows take the MFMA GEMV
+# on >= 1024 tiles only: 1025 tiles, the oracle on the first 2048 rows.
+PRESTAGE_CASES = [c for c in MFMA_CASES if c[2] >= 2048 and (c[3] > 8 or c[2] > 4096)] + [
+    (oracle.Q4_0, 16400, 8192, 3, False, 0), (oracle.Q4_K, 6144, 4096, 16, False, 0),
+    (oracle.Q5_K, 4096, 12288, 9, False, 0), (oracle.IQ4_XS, 6144, 2048, 12, True, 0)]
+
+
+@pytest.mark.parametrize("gtype,n,k,batch,ybf16,off", PRESTAGE_CASES,
+                         ids=[f"{oracle.NAMES[c[0]]}-{c[1]}x{c[2]}-b{c[3]}{'-bf16' if c[4] else ''}{'-off2' if c[5] else ''}"
+                              for c in PRESTAGE_CASES])
+def test_gemv_mfma_workspace_is_optional(ctx, gtype, n, k, batch, ybf16, off):
+    w, data = gguf(gtype, n, k, seed=n + k + batch + 1, off=off)
+    x = oracle.randn(batch * k, seed=batch + 1).reshape(batch, k)
+    ydt = torch.bfloat16 if ybf16 else torch.float32
+    need = d.prefill_workspace_bytes([w], batch, d.DTYPE_F32, d.DTYPE_BF16 if ybf16 else d.DTYPE_F32)
+    per = 8192 + 64 + (256 if gtype in (oracle.Q4_K, oracle.Q5_K) else 0)
+    assert need == (k // 256 * per + 255) // 256 * 256
+    assert d.prefill_workspace_bytes([w], 1) == 0
+    work = torch.full((need,), 0xFF, dtype=torch.uint8, device="cuda")
+    y_pre = ctx.qlinear(w, dev(x), y_dtype=ydt, workspace=work)
+    y_own = ctx.qlinear(w, dev(x), y_dtype=ydt, workspace=False)
+
+    def host(y):
+        if ybf16:
+            return oracle.bf16_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(batch, n)
+        return y.cpu().numpy()
+
+    a, b = host(y_pre), host(y_own)
+    nc = min(n, 2048)
+    wf = oracle.dequant_gguf(gtype, data[:len(data) // n * nc], nc, k)
+    y64, absdot = oracle.linear_f64(x, wf)
+    den = np.where(absdot > 0, absdot, 1)
+    if k <= 4096:  # one K segment: no atomics
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    else:
+        assert np.max(np.abs(a[:, :nc].astype(np.float64) - b[:, :nc]) / den) <= 1e-6
+    extra = np.abs(y64) * 2.0 ** -8 / den if ybf16 else 0.0
+    bound = 2.0 ** -10 + 2e-5 if gtype in (oracle.Q4_0, oracle.Q6_K, oracle.IQ4_XS) else 2e-3
+    err = np.abs(a[:, :nc].astype(np.float64) - y64) / den
+    assert np.all(err <= bound + extra), err.max()
+
+
+@pytest.mark.parametrize("n,k,g,sdtype,batch", [(1024, 3072, 64, oracle.D_F16, 12), (2048, 4096, 128, oracle.D_BF16, 9),
+                                               (3072, 2048, 32, oracle.D_F32, 16)])
+def test_gemv_mfma_mlx_workspace_is_optional(ctx, n, k, g, sdtype, batch):
+    """MLX affine U4 on the MFMA GEMV with its optional workspace and without: identical."""
+    packed, sc, bi = oracle.synth_mlx_u4(n, k, g, sdtype, seed=n + k + g)
+    w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), g, sdtype)
+    xb = oracle.f32_to_bf16_bits(oracle.randn(batch * k, seed=batch + 11)).reshape(batch, k)
+    xd = dev(xb).view(torch.bfloat16)
+    need = d.prefill_workspace_bytes([w], batch, d.DTYPE_BF16, d.DTYPE_F32)
+    assert need == (k // 256 * (8192 + 64) + 255) // 256 * 256
+    work = torch.full((need,), 0xFF, dtype=torch.uint8, device="cuda")
+    a = ctx.qlinear(w, xd, workspace=work).cpu().numpy()
+    b = ctx.qlinear(w, xd, workspace=False).cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    y64, absdot = oracle.linear_f64(oracle.bf16_bits_to_f32(xb), oracle.dequant_mlx_u4(packed, sc, bi, sdtype, n, k, g))
+    assert oracle.normalized_error(a, y64, absdot) <= 2.0 ** -10 + 1e-4
+
+
 @pytest.mark.parametrize("gtype,n,k", [(oracle.Q6_K, 4096, 12288), (oracle.Q4_0, 2048, 16384)],
                          ids=["q6_k-4096x12288", "q4_0-2048x16384"])
-def test_gemv_mfma_segments_graph_replays(ctx, gtype, n, k):
-    """Long K at 16 rows: a fill kernel zeroes y, then every K segment adds into
-    it atomically.  Captured in a HIP graph and replayed three times with eager
-    launches between: every replay must clear and re-accumulate (agreeing with
-    the eager result up to the order of the atomic adds) and stay in the f16 bound."""
+@pytest.mark.parametrize("staged", [True, False], ids=["workspace", "no-workspace"])
+def test_gemv_mfma_segments_graph_replays(ctx, gtype, n, k, staged):
+    """Long K at 16 rows: a kernel zeroes y (the prep kernel that stages the
+    activations into the workspace, or a fill kernel), then every K segment adds
+    into it atomically.  Captured in a HIP graph and replayed three times with
+    eager launches between (over the same workspace): every replay must clear
+    and re-accumulate (agreeing with the eager result up to the order of the
+    atomic adds) and stay in the f16 bound."""
     w, data = gguf(gtype, n, k, seed=n + k)
     x = dev(oracle.randn(16 * k, seed=5).reshape(16, k))
-    eager = ctx.qlinear(w, x).cpu().numpy()
+    need = d.prefill_workspace_bytes([w], 16)
+    assert need > 0
+    work = torch.empty(need, dtype=torch.uint8, device="cuda") if staged else False
+    eager = ctx.qlinear(w, x, workspace=work).cpu().numpy()
     y64, absdot = oracle.linear_f64(x.cpu().numpy(), oracle.dequant_gguf(gtype, data, n, k))
     assert oracle.normalized_error(eager, y64, absdot) <= 2.0 ** -10 + 2e-5
     y = torch.full((16, n), 7.0, device="cuda")
     st = torch.cuda.Stream()
     with torch.cuda.stream(st):
-        ctx.qlinear(w, x, y, stream=st)
+        ctx.qlinear(w, x, y, stream=st, workspace=work)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=st):
-            ctx.qlinear(w, x, y, stream=st)
+            ctx.qlinear(w, x, y, stream=st, workspace=work)
     torch.cuda.synchronize()
     den = np.where(absdot > 0, absdot, 1)
     for _ in range(3):
         y.fill_(7.0)
-        ctx.qlinear(w, x * 0.5)  # eager work between the replays
+        ctx.qlinear(w, x * 0.5, workspace=work)  # eager work between the replays
         g.replay()
         torch.cuda.synchronize()
         got = y.cpu().numpy()

@@ -3,7 +3,8 @@ through the C ABI: the same kernels with the prefill staging taken from the
 device's static scratch array instead of a stream-ordered allocation, so the
 outputs must be bit-identical, and both within the f16 bound of the oracle.
 Two prefill calls in a row (the second smaller, over the first call's
-leftover staging), a decode call, a staging beyond the scratch size
+leftover staging), decode calls (two in a row staging their activations in
+the scratch array, the second smaller), a staging beyond the scratch size
 (rejected host-side, after which calls still work), and a prefill captured in
 a HIP graph (kernel nodes only) whose replays equal the eager call."""
 import numpy as np
@@ -67,6 +68,22 @@ def test_noalloc_super_block_encodings(ctx, gtype):
             assert np.array_equal(r.view(np.uint32), g.view(np.uint32)), rows
         y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(gtype, datas[0], shapes[0], k))
         assert oracle.normalized_error(got[0], y64, absdot) <= 2e-3
+
+
+def test_noalloc_decode_staged_in_scratch(ctx):
+    """16 then 9 activation rows on the MFMA GEMV (K >= 2048: the activations
+    staged once per call, here in the scratch array): equal to the call with a
+    workspace and to the one without, bit for bit, and within the f16 bound."""
+    for k, rows, shapes, seed in ((4096, 16, [4096, 1024, 1024], 40), (2048, 9, [6144], 50)):
+        ws, datas = _weights(k, shapes, seed=seed)
+        x = oracle.randn(rows * k, seed=seed + 1).reshape(rows, k)
+        ref, got = _both(ctx, ws, dev(x))
+        own = [y.cpu().numpy() for y in ctx.qlinear_multi(ws, dev(x), workspace=False)]
+        for r, g, o, data, n in zip(ref, got, own, datas, shapes):
+            assert np.array_equal(r.view(np.uint32), g.view(np.uint32)), (k, rows, n)
+            assert np.array_equal(o.view(np.uint32), g.view(np.uint32)), (k, rows, n)
+            y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(oracle.Q4_0, data, n, k))
+            assert oracle.normalized_error(g, y64, absdot) <= F16X2
 
 
 def test_noalloc_decode_and_size_limit(ctx):
