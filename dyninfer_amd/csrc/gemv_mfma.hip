@@ -467,6 +467,20 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     const uint32_t ng = mfma_tasks<M, SPLIT>(nunit, ws), nt = nunit / M::UPT;  // tasks with padding, without
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if constexpr (XS == XS_PRE) {
+        // The segment's staged tasks are one contiguous range of the workspace,
+        // laid out as LDS holds them: copied by LDS DMA, 1 KiB per wave
+        // instruction (the last one partial), issued before the tile set-up
+        // (whose kernel-argument loads then overlap the copies).  Copying only
+        // the staged rows' slots of each fragment chunk, half of them at 5..8
+        // rows, measured slower: a per-lane test per instruction.
+        constexpr uint32_t TL = mfma_task_lds<M>();
+        const uint8_t* src = p.pre + (size_t)sidx * (p.seg_units / M::UPT) * TL;
+        const uint32_t bytes = nt * TL, nch = (bytes + 1023u) / 1024u;
+        for (uint32_t c = wv; c < nch; c += NW)
+            if (c * 1024u + 16u * lane < bytes) dma16(src + c * 1024u + 16u * lane, lds + c * 1024u);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     uint4* xl = reinterpret_cast<uint4*>(lds);
     float* inv = reinterpret_cast<float*>(lds + nt * NM * 64u * 16u);
     uint32_t* xs = reinterpret_cast<uint32_t*>(lds + nt * (NM * 64u * 16u + 64u));  // BIAS: activation sums
@@ -712,19 +726,9 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
         }
     };
     if constexpr (XS == XS_PRE) {
-        // The segment's staged tasks are one contiguous range of the workspace,
-        // laid out as LDS holds them: copied by LDS DMA, 1 KiB per wave
-        // instruction (the last one partial), then the first PF tasks' weight
-        // loads; the wait before the barrier covers the copies only (loads
-        // complete in issue order), so the weights stay in flight.  (Copying
-        // only the staged rows' slots of each fragment chunk, half of them at
-        // 5..8 rows, measured slower: a per-lane test per instruction.)
-        constexpr uint32_t TL = mfma_task_lds<M>();
-        const uint8_t* src = p.pre + (size_t)sidx * (p.seg_units / M::UPT) * TL;
-        const uint32_t bytes = nt * TL, nch = (bytes + 1023u) / 1024u;
-        for (uint32_t c = wv; c < nch; c += NW)
-            if (c * 1024u + 16u * lane < bytes) dma16(src + c * 1024u + 16u * lane, lds + c * 1024u);
-        __builtin_amdgcn_sched_barrier(0);
+        // the copies (issued at the top) and then the first PF tasks' weight
+        // loads are in flight; the wait before the barrier covers the copies
+        // only (loads complete in issue order), so the weights stay in flight
 #pragma unroll
         for (int s = 0; s < PF; s++) load(rcur, t0 + (uint32_t)s, ring[s], rx[s]);
         __builtin_amdgcn_sched_barrier(0);
@@ -1028,7 +1032,16 @@ hipError_t launch_mode(MfmaParams p, uint32_t units, bool y_bf16, uint8_t* pre, 
     // the workgroups first
     const uint64_t cap = (uint64_t)per_cu * cus;
     p.grid = (uint32_t)(p.total_tiles < cap ? p.total_tiles : cap);
-    if (shared_tiles) p.grid = (p.total_tiles + nseg - 1u) / nseg;  // about nseg tiles per workgroup
+    if (shared_tiles) {
+        // about nseg tiles per workgroup, all nseg segments' workgroups resident
+        // at once: a workgroup more than the CUs hold runs after the others
+        // (8B down_proj at 16 rows, 256 tiles in three segments: 86 workgroups
+        // a segment left two for a second round, 25.5 us; 85, one of them
+        // taking a fourth tile, ~19 us)
+        p.grid = (p.total_tiles + nseg - 1u) / nseg;
+        const uint32_t fit = (uint32_t)(cap / nseg);
+        p.grid = p.grid < fit ? p.grid : (fit ? fit : 1u);
+    }
     // Split mode with more tiles than resident workgroups (one segment): two
     // groups of 4 waves per workgroup, each on its own tile, so the tiles take
     // one round instead of two (Qwen3-0.6B MLX gate/up, 384 tiles at ~161
