@@ -29,11 +29,13 @@
 //              (nibbles j and j+4 of a word decode together).  Rows M .. roundup(M, 32) - 1
 // are written as zeros, so the GEMM reads whole fragments.
 //
-// Mapping: one wave per row (4 rows per 256-thread workgroup); lane l takes
-// the 8-element output slots l, l+64, ... (slot 8c + 2t + h: chunk c, step t,
-// half h).  Rows with K <= 12288 keep their values in registers between the
-// max pass and the conversion pass; longer rows reload them (cache hits), four
-// slots in flight per lane.
+// Mapping: one wave per row; lane l takes the 8-element output slots l, l+64,
+// ... (slot 8c + 2t + h: chunk c, step t, half h).  K <= 4096 and M >= 1024:
+// eight rows per 512-thread workgroup, whose slots meet in LDS and leave as
+// whole 128-byte lines of the fragments.  Otherwise four rows per 256-thread
+// workgroup, each lane storing its own 16-byte slots; rows with K <= 12288
+// keep their values in registers between the max pass and the conversion
+// pass, longer rows reload them (cache hits), four slots in flight per lane.
 // NaN and inf: the row's scale is taken as 2^15 and the non-finite values
 // propagate to the row's outputs.
 #include "device_common.hpp"
@@ -106,13 +108,15 @@ __device__ __forceinline__ size_t frag_offset(uint32_t m, uint32_t slot, uint32_
 // read by the next kernel, not by this one, and streaming it out during the
 // kernel rather than leaving dirty L2 lines for the end-of-kernel write-back
 // measured 7.3 -> 6.1 us at M = 2048, K = 1024.
+typedef uint32_t xu4 __attribute__((ext_vector_type(4)));
+template <uint32_t LAYOUT>
+__device__ __forceinline__ xu4 pack8(const float (&v)[8], int sh) {
+    return LAYOUT == XFRAG_WORD ? xu4{pk(v[0], v[4], sh), pk(v[1], v[5], sh), pk(v[2], v[6], sh), pk(v[3], v[7], sh)}
+                                : xu4{pk(v[0], v[2], sh), pk(v[1], v[3], sh), pk(v[4], v[6], sh), pk(v[5], v[7], sh)};
+}
 template <uint32_t LAYOUT>
 __device__ __forceinline__ void store8(uint16_t* xh, size_t off, const float (&v)[8], int sh) {
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4 q = LAYOUT == XFRAG_WORD
-                        ? u32x4{pk(v[0], v[4], sh), pk(v[1], v[5], sh), pk(v[2], v[6], sh), pk(v[3], v[7], sh)}
-                        : u32x4{pk(v[0], v[2], sh), pk(v[1], v[3], sh), pk(v[4], v[6], sh), pk(v[5], v[7], sh)};
-    __builtin_nontemporal_store(q, gptr_mut<u32x4>(xh + off));
+    __builtin_nontemporal_store(pack8<LAYOUT>(v, sh), gptr_mut<xu4>(xh + off));
 }
 
 // Maximum over the wave (unsigned), every lane receiving it.
@@ -191,11 +195,74 @@ __global__ __launch_bounds__(kXprepWaves * 64) void xprep_kernel(const void* __r
     if (lane == 0) gptr_mut<float>(rs)[m] = ldexpf(1.0f, e - 15);
 }
 
+// Rows of K <= kXprepLinesMaxK: eight rows per 512-thread workgroup (one wave
+// each), the rows' 16-byte slots gathered in LDS so that the eight rows' slots
+// of one (k step, half), consecutive in the fragment, leave as one 128-byte
+// line: a store instruction writes 8 whole lines instead of 64 pieces of 64
+// lines.
+constexpr uint32_t kXprepLinesRows = 8, kXprepLinesMaxK = 4096, kXprepLinesMinRows = 1024;
+template <bool XBF16, uint32_t LAYOUT, int NR>
+__global__ __launch_bounds__(kXprepLinesRows * 64) void xprep_lines_kernel(const void* __restrict__ x, uint32_t M,
+                                                                          uint32_t K, uint16_t* __restrict__ xh,
+                                                                          float* __restrict__ rs) {
+    static_assert(NR > 0 && NR * 512 <= (int)kXprepLinesMaxK, "the row's slots are held in registers");
+    extern __shared__ xu4 tile[];  // [slot][row of the eight]: K · 16 bytes
+    const uint32_t lane = threadIdx.x & 63u, r = threadIdx.x >> 6;
+    const uint32_t m0 = blockIdx.x * kXprepLinesRows, m = m0 + r;  // Mp is a multiple of 8: m < Mp
+    const uint32_t slots = K / 8u, ksteps = K / 16u;
+    const bool real = m < M;  // rows M .. Mp - 1 are zeros
+    const size_t row = real ? (size_t)m * K : 0u;
+    uint32_t mx = 0;
+    float v[NR][8];
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+        const uint32_t g = lane + 64u * (uint32_t)i;
+        if (g < slots) {
+            load8<XBF16, LAYOUT>(x, row, g, v[i]);
+#pragma unroll
+            for (int q = 0; q < 8; q++) v[i][q] = real ? v[i][q] : 0.0f;
+            mx = absbits_max8(v[i], mx);
+        }
+    }
+    mx = wave_umax(mx);
+    int e = mx >= 0x7F800000u ? 0 : (int)(mx >> 23) - 126;
+    e = e < -110 ? -110 : e;
+    const int sh = 15 - e;
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+        const uint32_t g = lane + 64u * (uint32_t)i;
+        if (g < slots) tile[g * kXprepLinesRows + r] = pack8<LAYOUT>(v[i], sh);
+    }
+    if (lane == 0) gptr_mut<float>(rs)[m] = real ? ldexpf(1.0f, e - 15) : 0.0f;
+    __syncthreads();
+    // piece p = (slot g, row r') of the eight rows: line g at frag_offset(m0, g)
+    for (uint32_t p = threadIdx.x; p < slots * kXprepLinesRows; p += kXprepLinesRows * 64u) {
+        const uint32_t g = p / kXprepLinesRows, rr = p % kXprepLinesRows;
+        __builtin_nontemporal_store(tile[p], gptr_mut<xu4>(xh + frag_offset(m0 + rr, g, ksteps)));
+    }
+}
+
 template <bool XBF16, uint32_t LAYOUT>
 hipError_t launch_xprep(const void* x, uint32_t M, uint32_t K, uint16_t* xh, float* rs, hipStream_t st) {
     const uint32_t Mp = (M + 31u) & ~31u;
     const dim3 grid((Mp + kXprepWaves - 1) / kXprepWaves), block(kXprepWaves * 64);
     const uint32_t slots = K / 8u;
+    // (on fewer rows the 8-row workgroups are too few: M = 512, K = 1024 took
+    // 14.5 us per prefill call against 14.1 with 4-row workgroups; at M =
+    // 2048 the whole lines gave 28.0 -> 26.8 us at K = 1024, 38.7 -> 30.5 us
+    // at K = 3072)
+    if (K <= kXprepLinesMaxK && Mp >= kXprepLinesMinRows) {
+        const dim3 lgrid(Mp / kXprepLinesRows), lblock(kXprepLinesRows * 64);
+        const size_t lds = (size_t)K * 16u;  // 64 KiB at most
+        if (slots <= 64u)
+            hipLaunchKernelGGL((xprep_lines_kernel<XBF16, LAYOUT, 1>), lgrid, lblock, lds, st, x, M, K, xh, rs);
+        else if (slots <= 128u)
+            hipLaunchKernelGGL((xprep_lines_kernel<XBF16, LAYOUT, 2>), lgrid, lblock, lds, st, x, M, K, xh, rs);
+        else if (slots <= 256u)
+            hipLaunchKernelGGL((xprep_lines_kernel<XBF16, LAYOUT, 4>), lgrid, lblock, lds, st, x, M, K, xh, rs);
+        else hipLaunchKernelGGL((xprep_lines_kernel<XBF16, LAYOUT, 8>), lgrid, lblock, lds, st, x, M, K, xh, rs);
+        return hipGetLastError();
+    }
     if (slots <= 64u) hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 1>), grid, block, 0, st, x, M, Mp, K, xh, rs);
     else if (slots <= 128u) hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 2>), grid, block, 0, st, x, M, Mp, K, xh, rs);
     else if (slots <= 256u) hipLaunchKernelGGL((xprep_kernel<XBF16, LAYOUT, 4>), grid, block, 0, st, x, M, Mp, K, xh, rs);
