@@ -11,6 +11,8 @@ Bars (written here as the tests use them):
     accumulation: the GEMV tests also hold it to XF16 = 2^-11 + 2e-5, which a
     dropped or mis-scaled block (an error of order 1/blocks per row) exceeds.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -240,6 +242,38 @@ def test_gemv_mfma_workspace_is_optional(ctx, gtype, n, k, batch, ybf16, off):
     bound = 2.0 ** -10 + 2e-5 if gtype in (oracle.Q4_0, oracle.Q6_K, oracle.IQ4_XS) else 2e-3
     err = np.abs(a[:, :nc].astype(np.float64) - y64) / den
     assert np.all(err <= bound + extra), err.max()
+
+
+def test_gemv_mfma_workspace_checks(ctx):
+    """A decode call's optional workspace: NULL runs without it; one that is given
+    must be 256-byte aligned and at least the reported size, else
+    ERR_INVALID_ARGUMENT before anything is enqueued (the outputs keep their
+    sentinel)."""
+    n, k, batch = 6144, 4096, 16
+    w, data = gguf(oracle.Q4_0, n, k, seed=77)
+    x = dev(oracle.randn(batch * k, seed=78).reshape(batch, k))
+    need = d.prefill_workspace_bytes([w], batch)
+    assert need == (k // 256 * 8256 + 255) // 256 * 256
+    buf = torch.empty(need + 512, dtype=torch.uint8, device="cuda")
+    y = torch.full((batch, n), 7.0, device="cuda")
+    lib = d.library()
+    wc = w.c()
+    for ptr, nbytes in ((buf.data_ptr(), need - 256), (buf.data_ptr() + 16, need)):
+        rc = lib.dyninfer_mi355x_qlinear(ctx._h, ctypes.byref(wc), x.data_ptr(), d.DTYPE_F32, batch, y.data_ptr(),
+                                         d.DTYPE_F32, ptr, nbytes, torch.cuda.current_stream().cuda_stream)
+        assert rc == d.ERR_INVALID_ARGUMENT, rc
+        assert "decode" in lib.dyninfer_mi355x_last_error().decode()
+    torch.cuda.synchronize()
+    assert bool((y == 7.0).all())
+    rc = lib.dyninfer_mi355x_qlinear(ctx._h, ctypes.byref(wc), x.data_ptr(), d.DTYPE_F32, batch, y.data_ptr(),
+                                     d.DTYPE_F32, None, 0, torch.cuda.current_stream().cuda_stream)
+    assert rc == d.OK
+    y_null = y.cpu().numpy().copy()
+    rc = lib.dyninfer_mi355x_qlinear(ctx._h, ctypes.byref(wc), x.data_ptr(), d.DTYPE_F32, batch, y.data_ptr(),
+                                     d.DTYPE_F32, buf.data_ptr(), need, torch.cuda.current_stream().cuda_stream)
+    assert rc == d.OK
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), y_null.view(np.uint32))
+    assert gemv_err(y_null, x.cpu().numpy(), oracle.dequant_gguf(oracle.Q4_0, data, n, k)) <= 2.0 ** -10 + 2e-5
 
 
 @pytest.mark.parametrize("n,k,g,sdtype,batch", [(1024, 3072, 64, oracle.D_F16, 12), (2048, 4096, 128, oracle.D_BF16, 9),
