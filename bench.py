@@ -454,8 +454,9 @@ def main() -> int:
                     help="for rocprofv3 --pmc: one 64 MiB device copy (the counters' calibration), then one "
                          "eager decode step (--probe-config) and one M512 config-3 GEMM; prints the launch labels "
                          "in dispatch order")
-    ap.add_argument("--probe-config", type=int, default=4, choices=(1, 4),
-                    help="the decode step --pmc-probe runs: config 4 (Qwen3-8B) or config 1 (Qwen3-0.6B mixed GGUF)")
+    ap.add_argument("--probe-config", type=int, default=4, choices=(1, 2, 4),
+                    help="the decode step --pmc-probe runs (at --batch rows): config 4 (Qwen3-8B), config 1 "
+                         "(Qwen3-0.6B mixed GGUF) or config 2 (Qwen3-0.6B MLX, bf16 in/out)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -483,12 +484,12 @@ def main() -> int:
         print("gemm probe: Q4_0 M512, Q4_0 M2048, Q4_1, Q8_0, Q6_K M512 (N3072 K1024), 30 calls each", flush=True)
         return 0
 
-    if args.pmc_probe and args.probe_config == 1:
-        s4 = build_step(torch, d, "config1", gen)
-    else:
+    name = {1: "config1", 2: "config2", 4: "config4"}[args.probe_config] if args.pmc_probe else "config4"
+    if name == "config4":
         log("building config 4 weights (Qwen3-8B GGUF, 4.88 GB) ...")
-        s4 = build_step(torch, d, "config4", gen)
-    r4 = StepRunner(torch, d, ctx, s4, args.batch, torch.float32, torch.float32)
+    s4 = build_step(torch, d, name, gen)
+    dts = {"f32": torch.float32, "bf16": torch.bfloat16}
+    r4 = StepRunner(torch, d, ctx, s4, args.batch, dts[STEP_DTYPES[name][0]], dts[STEP_DTYPES[name][1]])
     if args.pmc_probe:
         src = torch.ones(16 << 20, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
