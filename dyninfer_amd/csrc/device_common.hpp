@@ -30,6 +30,13 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* gptr_mut(void* p
     return (__attribute__((address_space(1))) T*)(p);
 }
 
+// floor(n / g) as one v_mul_hi_u32 with magic = ceil(2^32 / g) (group_magic):
+// magic = (2^32 + e) / g with 0 <= e < g, so n·magic / 2^32 = n/g + n·e/(g·2^32),
+// and for n·e < 2^32 (every n and g below 2^16: the GEMV's K bound) the excess
+// stays below 1/g and the floor is exact.  The MLX kernels find a k's scale
+// group this way instead of by a 32-bit division (~8 VALU instructions each).
+__device__ __forceinline__ uint32_t div_magic(uint32_t n, uint32_t magic) { return __umulhi(n, magic); }
+
 // 16 bytes per lane from global memory into LDS at dst + 16·lane (dst
 // wave-uniform): global_load_lds_dwordx4, counted by vmcnt.
 __device__ __forceinline__ void dma16(const void* src, void* dst) {

@@ -127,6 +127,7 @@ hipError_t gemm_launch(const GemmWeight& wt, uint32_t N, uint32_t K, const uint1
     a.sc = wt.sc;
     a.bi = wt.bi;
     a.group = wt.group;
+    a.gmagic = group_magic(wt.group);
     a.sdtype = wt.sdtype;
     switch (enc) {
         case ENC_Q4_0: a.rowbytes = (uint64_t)(K / 32u) * 18u; break;

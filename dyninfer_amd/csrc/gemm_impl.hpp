@@ -74,6 +74,7 @@ struct GemmArgs {
     const uint8_t* sc;  // MLX U4: scales and biases [N, K/group] of dtype sdtype
     const uint8_t* bi;
     uint32_t group, sdtype;
+    uint32_t gmagic;  // group_magic(group)
 };
 
 // (a & m) | b as one v_and_or_b32 (mask in a scalar register: a VOP3 op takes
@@ -411,12 +412,12 @@ struct WinMlx {
     const uint8_t* src[kPieces];             // copy lane's piece of the slice's first chunk
     uintptr_t srow[kAuxQ], brow[kAuxQ];      // copy lane's row of scales and biases
     uint32_t ssh[NB], bsh[NB];               // this lane's rows' scale and bias row starts mod 4 (per N-block j)
-    uint32_t c0, es, group, sdtype, lane;
+    uint32_t c0, es, gmagic, sdtype, lane;
 
     __device__ void init(const GemmArgs& a, uint32_t n0, uint32_t lane_, uint32_t c0_) {
         lane = lane_;
         c0 = c0_;
-        group = a.group;
+        gmagic = a.gmagic;
         sdtype = a.sdtype;
         es = a.sdtype == DT_F32 ? 4u : 2u;
         const uint32_t rbytes = a.K / 2u, sbytes = a.K / a.group * es;
@@ -440,7 +441,7 @@ struct WinMlx {
         }
     }
     // byte offset in a scale row of the group of the chunk's 32-k half hh
-    __device__ uint32_t goff(uint32_t c, uint32_t hh) const { return (64u * (c0 + c) + 32u * hh) / group * es; }
+    __device__ uint32_t goff(uint32_t c, uint32_t hh) const { return div_magic(64u * (c0 + c) + 32u * hh, gmagic) * es; }
     __device__ void issue(uint32_t c, uint8_t* win) const {
 #pragma unroll
         for (uint32_t q = 0; q < kPieces; q++) dma16(src[q] + (size_t)c * 32u, win + 1024u * q);

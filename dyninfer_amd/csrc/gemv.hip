@@ -197,6 +197,7 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     p.lanes_log2 = lanes_log2;
     p.y_bf16 = y_bf16 ? 1u : 0u;
     p.group = group;
+    p.gmagic = group_magic(group);
     p.sdtype = sdtype;
     return launch(enc, p, B, oneshot, x_bf16, stream);  // lays out the row blocks per tile
 }

@@ -915,15 +915,15 @@ __global__ __launch_bounds__(TH) void gguf_gemv_oneshot_kernel(const GemvParams 
 // scale and bias (f32, or f16/bf16 bits).
 struct MlxLoad {
     const GemvParams& p;
-    uint32_t ngroups, chunks_per_group;
+    uint32_t ngroups;
     bool f32s;
     __device__ __forceinline__ explicit MlxLoad(const GemvParams& q)
-        : p(q), ngroups(q.K / q.group), chunks_per_group(q.group / 32u), f32s(q.sdtype == DT_F32) {}
+        : p(q), ngroups(q.K / q.group), f32s(q.sdtype == DT_F32) {}
     __device__ __forceinline__ EncMlxU4::Raw operator()(const RowBlock& rb, uint32_t row, uint32_t u) const {
         EncMlxU4::Raw r;
         const uint8_t* wb = rb.w;
         load_dwords<4>(reinterpret_cast<const uint32_t*>(wb + (row * (p.K / 2u) + u * 16u)), r.w);
-        const uint32_t gi = row * ngroups + u / chunks_per_group;
+        const uint32_t gi = row * ngroups + div_magic(32u * u, p.gmagic);  // chunk u: k = 32u .. 32u + 31
         const uint8_t* scb = rb.sc;
         const uint8_t* bib = rb.bi;
         if (f32s) {

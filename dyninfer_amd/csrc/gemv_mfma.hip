@@ -74,6 +74,7 @@ struct MfmaParams {
     uint32_t accumulate;  // add to y (later segments; f32 outputs only)
     uint32_t x_bf16;      // activations bf16 (else f32)
     uint32_t group;       // MLX group size
+    uint32_t gmagic;      // group_magic(group)
     uint32_t sdtype;      // MLX scale/bias dtype
     const void* x;
     void* y[kMaxProblems];
@@ -584,8 +585,8 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     // the scale/bias groups of task t for this lane: k 64q..64q+31 and 64q+32..64q+63
     auto sbgroups = [&](const Rows& r, uint32_t t, uint32_t& g0, uint32_t& g1) {
         const uint32_t kl = k0 + (t < nt ? t : nt - 1u) * M::KT + 64u * q;
-        g0 = r.rowm * gpr + kl / p.group;
-        g1 = r.rowm * gpr + (kl + 32u) / p.group;
+        g0 = r.rowm * gpr + div_magic(kl, p.gmagic);
+        g1 = r.rowm * gpr + div_magic(kl + 32u, p.gmagic);
     };
     auto load = [&](const Rows& r, uint32_t t, u32x4 (&v)[NLD], uint32_t (&aux)[4]) {
 #pragma unroll
@@ -1108,6 +1109,7 @@ hipError_t launch_mfma(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     p.x = x;
     p.x_bf16 = x_bf16 ? 1u : 0u;
     p.group = group;
+    p.gmagic = group_magic(group);
     p.sdtype = sdtype;
     const uint32_t units = K / M::UNIT;
     const int mode = mfma_mode<M>(K, tiles, y_bf16, min_tiles);

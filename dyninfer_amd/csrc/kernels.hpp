@@ -24,6 +24,9 @@ enum DType : uint32_t { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
 // Kernel parameters of one GEMV launch (passed by value as the kernel
 // argument).  The fields that address the first weight loads lead, in the
 // first 96 bytes, so that they arrive in one round of scalar loads.
+// ceil(2^32 / g) for div_magic (g >= 2); 0 for g = 0.
+inline uint32_t group_magic(uint32_t g) { return g < 2u ? 0u : (uint32_t)(((1ull << 32) + g - 1u) / g); }
+
 struct GemvParams {
     const uint8_t* w[kMaxProblems];   // GGUF blocks, or MLX packed words
     uint32_t n[kMaxProblems];
@@ -42,6 +45,7 @@ struct GemvParams {
     const uint8_t* bi[kMaxProblems];  // MLX biases
     uint32_t y_bf16;      // store bf16 instead of f32
     uint32_t group;       // MLX group size
+    uint32_t gmagic;      // group_magic(group)
     uint32_t sdtype;      // MLX scale/bias dtype
     // Persistent pipeline: waves [wave_end[i-1], wave_end[i]) serve problem i
     // (wave_end[nprob-1] = all waves launched), each a contiguous run of the

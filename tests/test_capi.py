@@ -7,6 +7,7 @@ import os
 import re
 import threading
 
+import numpy as np
 import pytest
 
 import dyninfer_amd as d
@@ -237,3 +238,13 @@ def test_registry_output_buffer_too_small():
     rc = lib.dyninfer_mi355x_registry_select(None, req, b'{"driver":"hip","architecture":"gfx950","features":[]}',
                                              ctypes.cast(buf, ctypes.c_void_p), 8, ctypes.byref(n))
     assert rc == d.ERR_BUFFER_TOO_SMALL and n.value > 8
+
+
+def test_group_magic_division_is_exact():
+    """The MLX kernels find a k's scale group as floor(k·magic / 2^32) with magic =
+    ceil(2^32 / g) (one v_mul_hi_u32, group_magic in kernels.hpp): exact for every
+    group size g (a multiple of 32) and every k below 2^16, the GEMV's bound on K."""
+    n = np.arange(1 << 16, dtype=np.uint64)
+    for g in range(32, 1 << 16, 32):
+        magic = np.uint64(((1 << 32) + g - 1) // g)
+        assert np.array_equal((n * magic) >> np.uint64(32), n // np.uint64(g)), g
