@@ -318,10 +318,16 @@ struct MfmaMlxU4 {
     __device__ static uint32_t run0(uint32_t q, uint32_t j) { return 64u * q + 8u * j; }
     __device__ static uint32_t run1(uint32_t q, uint32_t j) { return run0(q, j) + 4u; }
     // a scale or bias bit pattern (f32, or f16/bf16 in the low half) to f16
+    // (all three formed and one selected: the dtype is uniform, and a branch per
+    // value put 36 uniform branches in each round of four tasks)
     __device__ static _Float16 sb_f16(uint32_t bits, uint32_t sdtype) {
-        if (sdtype == DT_F32) return (_Float16)__uint_as_float(bits);
-        if (sdtype == DT_F16) return __builtin_bit_cast(_Float16, (uint16_t)bits);
-        return (_Float16)__uint_as_float(bits << 16);  // bf16
+        const _Float16 f32v = (_Float16)__uint_as_float(bits);
+        const _Float16 f16v = __builtin_bit_cast(_Float16, (uint16_t)bits);
+        const _Float16 bf16v = (_Float16)__uint_as_float(bits << 16);
+        const uint16_t r = sdtype == DT_F32 ? __builtin_bit_cast(uint16_t, f32v)
+                         : sdtype == DT_F16 ? __builtin_bit_cast(uint16_t, f16v)
+                                            : __builtin_bit_cast(uint16_t, bf16v);
+        return __builtin_bit_cast(_Float16, r);
     }
     // aux = (s, b) of the group of words 0..3 and of words 4..7
     __device__ static void decode(const u32a* win, uint32_t q, const uint32_t (&aux)[4], uint32_t sdtype,
