@@ -277,9 +277,11 @@ def test_gemv_mfma_workspace_checks(ctx):
 
 
 @pytest.mark.parametrize("n,k,g,sdtype,batch", [(1024, 3072, 64, oracle.D_F16, 12), (2048, 4096, 128, oracle.D_BF16, 9),
-                                               (3072, 2048, 32, oracle.D_F32, 16)])
+                                               (3072, 2048, 32, oracle.D_F32, 16), (1024, 8192, 64, oracle.D_BF16, 16)])
 def test_gemv_mfma_mlx_workspace_is_optional(ctx, n, k, g, sdtype, batch):
-    """MLX affine U4 on the MFMA GEMV with its optional workspace and without: identical."""
+    """MLX affine U4 on the MFMA GEMV with its optional workspace and without: identical
+    (K = 8192 takes two LDS segments adding into f32 outputs: equal up to the order of
+    the atomic adds)."""
     packed, sc, bi = oracle.synth_mlx_u4(n, k, g, sdtype, seed=n + k + g)
     w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), g, sdtype)
     xb = oracle.f32_to_bf16_bits(oracle.randn(batch * k, seed=batch + 11)).reshape(batch, k)
@@ -289,8 +291,11 @@ def test_gemv_mfma_mlx_workspace_is_optional(ctx, n, k, g, sdtype, batch):
     work = torch.full((need,), 0xFF, dtype=torch.uint8, device="cuda")
     a = ctx.qlinear(w, xd, workspace=work).cpu().numpy()
     b = ctx.qlinear(w, xd, workspace=False).cpu().numpy()
-    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     y64, absdot = oracle.linear_f64(oracle.bf16_bits_to_f32(xb), oracle.dequant_mlx_u4(packed, sc, bi, sdtype, n, k, g))
+    if k <= 4096:
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    else:
+        assert np.max(np.abs(a.astype(np.float64) - b) / np.where(absdot > 0, absdot, 1)) <= 1e-6
     assert oracle.normalized_error(a, y64, absdot) <= 2.0 ** -10 + 1e-4
 
 
