@@ -188,6 +188,7 @@ __global__ __launch_bounds__(TH) void gguf_gemv_stream_kernel(const GemvParams p
     constexpr int U = D / stream_gcd(D, CPL) * CPL;  // tasks per unrolled round: lcm(D, CPL)
     using XT = XTile<E>;
     extern __shared__ __align__(16) uint8_t xlds[];
+    gemv_args_up_front(p);
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (uint32_t)(TH / 64) + (threadIdx.x >> 6));
     const uint32_t lg = p.lanes_log2, L = 1u << lg, G = 64u >> lg;
