@@ -451,6 +451,21 @@ __host__ __device__ constexpr uint64_t mfma_prestage_bytes(uint32_t K) {
 
 }  // namespace
 
+// The kernel arguments the set-up reads, made operands of empty asm statements
+// at the kernel's top so the compiler loads them together rather than each
+// behind a wait for the one before (as the VALU GEMV's gemv_args_up_front).
+template <bool MLX>
+__device__ __forceinline__ void mfma_args_up_front(const MfmaParams& p) {
+    asm volatile("" ::"s"(p.w[0]), "s"(p.w[1]), "s"(p.w[2]), "s"(p.w[3]), "s"(p.y[0]), "s"(p.y[1]), "s"(p.y[2]),
+                 "s"(p.y[3]), "s"(p.x), "s"(p.pre));
+    asm volatile("" ::"s"(p.n[0]), "s"(p.n[1]), "s"(p.n[2]), "s"(p.n[3]), "s"(p.tile_begin[0]), "s"(p.tile_begin[1]),
+                 "s"(p.tile_begin[2]), "s"(p.tile_begin[3]), "s"(p.total_tiles), "s"(p.grid), "s"(p.K), "s"(p.k0),
+                 "s"(p.nunit), "s"(p.seg_units), "s"(p.nseg), "s"(p.nprob), "s"(p.batch), "s"(p.split_ws_log2));
+    if constexpr (MLX)
+        asm volatile("" ::"s"(p.sc[0]), "s"(p.sc[1]), "s"(p.sc[2]), "s"(p.sc[3]), "s"(p.bi[0]), "s"(p.bi[1]),
+                     "s"(p.bi[2]), "s"(p.bi[3]), "s"(p.group), "s"(p.gmagic), "s"(p.sdtype));
+}
+
 // How a workgroup fills its LDS with the segment's activations: it stages them
 // itself, the batch being 3..8 (4 or 8 rows of the A side staged) or 9..16
 // (all 16 rows, the staging indices compile-time), or it copies them from the
@@ -462,6 +477,7 @@ template <class M, bool YBF16, bool SPLIT, int XS>
 __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParams p) {
     constexpr bool ROWS16 = XS == XS_ROWS16;
     extern __shared__ __align__(16) uint8_t lds[];
+    mfma_args_up_front<M::MLX>(p);
     constexpr uint32_t NM = M::NM, UPR = 4u * NM;  // staging units per (task, row): (q, j)
     constexpr uint32_t NSLOT = 16u * M::NP, NLD = (NSLOT + 63u) / 64u;  // window pieces, loads per lane
     constexpr int PF = SPLIT ? 2 : M::PF;  // tasks of raw loads in flight per wave
