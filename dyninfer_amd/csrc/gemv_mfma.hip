@@ -466,16 +466,20 @@ __device__ __forceinline__ void mfma_args_up_front(const MfmaParams& p) {
                      "s"(p.bi[2]), "s"(p.bi[3]), "s"(p.group), "s"(p.gmagic), "s"(p.sdtype));
 }
 
-// How a workgroup fills its LDS with the segment's activations: it stages them
+// How a workgroup gets the segment's activations: it stages them in LDS
 // itself, the batch being 3..8 (4 or 8 rows of the A side staged) or 9..16
-// (all 16 rows, the staging indices compile-time), or it copies them from the
-// call's workspace, where gemv_mfma_prep_kernel staged them once for all
-// workgroups.
-enum MfmaStaging { XS_ROWS8 = 0, XS_ROWS16 = 1, XS_PRE = 2 };
+// (all 16 rows, the staging indices compile-time), or it copies them into LDS
+// from the call's workspace, where gemv_mfma_prep_kernel staged them once for
+// all workgroups (XS_PRE), or (split mode, eight waves per tile, two tasks per
+// wave: XS_REG) each wave loads its own two tasks' operands from the workspace
+// into registers, which serve every tile it takes, and LDS holds only the
+// weight windows.
+enum MfmaStaging { XS_ROWS8 = 0, XS_ROWS16 = 1, XS_PRE = 2, XS_REG = 3 };
 
 template <class M, bool YBF16, bool SPLIT, int XS>
 __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParams p) {
-    constexpr bool ROWS16 = XS == XS_ROWS16;
+    constexpr bool ROWS16 = XS == XS_ROWS16, REG = XS == XS_REG;
+    static_assert(!REG || SPLIT, "register operands serve the split mode's fixed tasks per wave");
     extern __shared__ __align__(16) uint8_t lds[];
     mfma_args_up_front<M::MLX>(p);
     constexpr uint32_t NM = M::NM, UPR = 4u * NM;  // staging units per (task, row): (q, j)
@@ -507,7 +511,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     uint4* xl = reinterpret_cast<uint4*>(lds);
     float* inv = reinterpret_cast<float*>(lds + nt * NM * 64u * 16u);
     uint32_t* xs = reinterpret_cast<uint32_t*>(lds + nt * (NM * 64u * 16u + 64u));  // BIAS: activation sums
-    uint8_t* wins = lds + nt * mfma_task_lds<M>();      // the waves' windows
+    uint8_t* wins = lds + (REG ? 0u : nt * mfma_task_lds<M>());  // the waves' windows
     uint8_t* win = wins + wv * 16u * M::WB;             // this wave's window
 
     // ---- weight tiles.  Whole tiles per wave: wave wid takes tiles wid,
@@ -748,7 +752,27 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
             }
         }
     };
-    if constexpr (XS == XS_PRE) {
+    // XS_REG: the wave's tasks t0, t0 + 1 (every tile's), their fragments in
+    // the A layout, inverse scales of rows 4q..4q+3 and (offset encodings)
+    // the quarter sums, as the workspace holds them (padding tasks read the
+    // last real task: in bounds, never multiplied)
+    u32x4 xreg[REG ? PF : 1][NM];
+    f32x4 ireg[REG ? PF : 1];
+    uint32_t sreg[REG ? PF : 1];
+    if constexpr (REG) {
+        constexpr uint32_t TL = mfma_task_lds<M>();
+        const uint8_t* seg = p.pre + (size_t)sidx * (p.seg_units / M::UPT) * TL;
+#pragma unroll
+        for (int s = 0; s < PF; s++) {
+            const uint32_t t = t0 + (uint32_t)s, tc = t < nt ? t : nt - 1u;
+#pragma unroll
+            for (uint32_t j = 0; j < NM; j++) xreg[s][j] = *gptr<u32x4>(seg + ((tc * NM + j) * 64u + xslot(lane, j)) * 16u);
+            ireg[s] = *gptr<f32x4>(seg + nt * NM * 1024u + (tc * 16u + 4u * q) * 4u);
+            if constexpr (M::BIAS) sreg[s] = *gptr<uint32_t>(seg + nt * (NM * 1024u + 64u) + ((tc * 16u + m) * 4u + q) * 4u);
+        }
+#pragma unroll
+        for (int s = 0; s < PF; s++) load(rcur, t0 + (uint32_t)s, ring[s], rx[s]);
+    } else if constexpr (XS == XS_PRE) {
         // the copies (issued at the top) and then the first PF tasks' weight
         // loads are in flight; the wait before the barrier covers the copies
         // only (loads complete in issue order), so the weights stay in flight
@@ -769,12 +793,19 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     // task's writes wait for these reads), the lane's quarter decoded from
     // its row, and the task's MFMAs into a zeroed tile; rs = the row scale
     // (Q6_K's d).
-    auto product = [&](const u32x4 (&v)[NLD], const uint32_t (&aux)[4], const Rows& r, uint32_t t, float& rs) {
+    auto product = [&](const u32x4 (&v)[NLD], const uint32_t (&aux)[4], const Rows& r, uint32_t t, float& rs,
+                       const u32x4 (&xr)[NM], uint32_t xsr) {
 #pragma unroll
         for (uint32_t i = 0; i < NLD; i++) *reinterpret_cast<u32x4*>(win + lo[i]) = v[i];
-        uint4 xa[NM];
+        u32x4 xa[NM];
 #pragma unroll
-        for (uint32_t j = 0; j < NM; j++) xa[j] = xl[(t * NM + j) * 64u + xslot(lane, j)];
+        for (uint32_t j = 0; j < NM; j++) {
+            if constexpr (REG) xa[j] = xr[j];
+            else {
+                const uint4 l = xl[(t * NM + j) * 64u + xslot(lane, j)];
+                xa[j] = u32x4{l.x, l.y, l.z, l.w};
+            }
+        }
         uint4 a[NM];
         if constexpr (M::BIAS) {
             uint32_t mb;
@@ -785,7 +816,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
             for (uint32_t j = 0; j < NM; j++)
                 tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, xa[j]), __builtin_bit_cast(h8, a[j]), tmp, 0, 0, 0);
             // A: the sums of activation row lane % 16 for the lane's quarter's two sub-blocks
-            const uint4 xo = make_uint4(xs[(t * 16u + m) * 4u + q], 0u, 0u, 0u), wo = make_uint4(mb, 0u, 0u, 0u);
+            const uint4 xo = make_uint4(REG ? xsr : xs[(t * 16u + m) * 4u + q], 0u, 0u, 0u), wo = make_uint4(mb, 0u, 0u, 0u);
             const f32x4 off = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, xo), __builtin_bit_cast(h8, wo), zero, 0, 0, 0);
 #pragma unroll
             for (int c = 0; c < 4; c++) tmp[c] = fmaf(tmp[c], dd, -(off[c] * dm));
@@ -829,7 +860,9 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
             float rs[M::TPI] = {};
 #pragma unroll
             for (int k = 0; k < M::TPI; k++)
-                if (g + (uint32_t)k < nt) prd[k] = product(ring[s + k], rx[s + k], rcur, g + (uint32_t)k, rs[k]);
+                if (g + (uint32_t)k < nt)  // (XS_REG: tpw == PF, so ring slot s + k holds the wave's task s + k)
+                    prd[k] = product(ring[s + k], rx[s + k], rcur, g + (uint32_t)k, rs[k], xreg[REG ? s + k : 0],
+                                     sreg[REG ? s + k : 0]);
             if constexpr (decltype(refill)::value) {
                 const bool wrap = g0 + (uint32_t)s + PF >= tpw;  // the refills belong to the next tile
                 const uint32_t gn = wrap ? g + PF - tpw : g + PF;
@@ -840,7 +873,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
             for (int k = 0; k < M::TPI; k++) {
                 if (g + (uint32_t)k >= nt) continue;
                 // inverse activation scales of rows 4q..4q+3
-                f32x4 sc = *reinterpret_cast<const f32x4*>(inv + (g + (uint32_t)k) * 16u + 4u * q);
+                f32x4 sc = REG ? ireg[REG ? s + k : 0] : *reinterpret_cast<const f32x4*>(inv + (g + (uint32_t)k) * 16u + 4u * q);
                 if constexpr (M::ROWSCALE) sc *= rs[k];
 #pragma unroll
                 for (int c = 0; c < 4; c++) acc[c] = fmaf(prd[k][c], sc[c], acc[c]);
@@ -1079,6 +1112,22 @@ hipError_t launch_mode(MfmaParams p, uint32_t units, bool y_bf16, uint8_t* pre, 
     p.seg_units = seg;
     p.nseg = nseg;
     p.accumulate = nseg > 1u ? 1u : 0u;
+    // split mode with eight waves per tile and two tasks per wave: each wave's
+    // operands in registers (XS_REG), no copy into LDS
+    size_t lds_launch = lds;
+    if constexpr (SPLIT) {
+        if (pre && p.split_ws_log2 == 3u && mfma_tasks<M, true>(seg, 8u) == 16u) {
+            auto kreg = y_bf16 ? gemv_mfma_kernel<M, true, true, XS_REG> : gemv_mfma_kernel<M, false, true, XS_REG>;
+            const size_t lreg = (kMfmaThreads / 64u) * 16u * M::WB;  // the windows only
+            int rcus = 0, rper = 0;
+            e = cached_occupancy(reinterpret_cast<const void*>(kreg), lreg, kMfmaThreads, &rper, &rcus);
+            if (e != hipSuccess) return e;
+            if ((uint64_t)rper * rcus >= (uint64_t)p.grid * nseg) {  // all workgroups resident, as planned
+                kernel = kreg;
+                lds_launch = lreg;
+            }
+        }
+    }
     if (pre) {  // stage once (and clear y when the segments add into it)
         p.pre = pre;
         const uint32_t rbl = p.batch <= 4u ? 2u : p.batch <= 8u ? 3u : 4u;
@@ -1096,7 +1145,7 @@ hipError_t launch_mode(MfmaParams p, uint32_t units, bool y_bf16, uint8_t* pre, 
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kernel, dim3(p.grid * nseg), dim3(kMfmaThreads), lds, st, p);
+    hipLaunchKernelGGL(kernel, dim3(p.grid * nseg), dim3(kMfmaThreads), lds_launch, st, p);
     return hipGetLastError();
 }
 

@@ -206,7 +206,10 @@ def test_gemv_mfma(ctx, gtype, n, k, batch, ybf16, off):
 # on >= 1024 tiles only: 1025 tiles, the oracle on the first 2048 rows.
 PRESTAGE_CASES = [c for c in MFMA_CASES if c[2] >= 2048 and (c[3] > 8 or c[2] > 4096)] + [
     (oracle.Q4_0, 16400, 8192, 3, False, 0), (oracle.Q4_K, 6144, 4096, 16, False, 0),
-    (oracle.Q5_K, 4096, 12288, 9, False, 0), (oracle.IQ4_XS, 6144, 2048, 12, True, 0)]
+    (oracle.Q5_K, 4096, 12288, 9, False, 0), (oracle.IQ4_XS, 6144, 2048, 12, True, 0),
+    # split mode, 16 tasks per segment: each wave's staged operands in registers
+    (oracle.Q4_0, 4096, 4096, 16, False, 0), (oracle.Q4_K, 4096, 12288, 16, False, 0),
+    (oracle.IQ4_XS, 2048, 4096, 12, True, 0)]
 
 
 @pytest.mark.parametrize("gtype,n,k,batch,ybf16,off", PRESTAGE_CASES,
@@ -277,7 +280,8 @@ def test_gemv_mfma_workspace_checks(ctx):
 
 
 @pytest.mark.parametrize("n,k,g,sdtype,batch", [(1024, 3072, 64, oracle.D_F16, 12), (2048, 4096, 128, oracle.D_BF16, 9),
-                                               (3072, 2048, 32, oracle.D_F32, 16), (1024, 8192, 64, oracle.D_BF16, 16)])
+                                               (3072, 2048, 32, oracle.D_F32, 16), (1024, 8192, 64, oracle.D_BF16, 16),
+                                               (2048, 4096, 64, oracle.D_F16, 16)])
 def test_gemv_mfma_mlx_workspace_is_optional(ctx, n, k, g, sdtype, batch):
     """MLX affine U4 on the MFMA GEMV with its optional workspace and without: identical
     (K = 8192 takes two LDS segments adding into f32 outputs: equal up to the order of
