@@ -573,8 +573,10 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
         lo[i] = pr[i] * M::WB + 16u * pc[i];
     }
     // a tile's 4-byte-aligned weight base and the byte offsets (from it) of
-    // the segment's start in this lane's decode row and load rows (rows past
-    // the problem re-read its last one: in bounds, never stored)
+    // the segment's start in this lane's decode row (om) and load rows (oi;
+    // for tasks a multiple of 4 bytes long, oi is already the offset of the
+    // lane's piece in the segment's first task); rows past the problem
+    // re-read its last one: in bounds, never stored
     struct Rows {
         const uint8_t* abase;
         const uint8_t* sc;
@@ -595,7 +597,11 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
         }
         r.om = off(m);
 #pragma unroll
-        for (uint32_t i = 0; i < NLD; i++) r.oi[i] = off(pr[i]);
+        for (uint32_t i = 0; i < NLD; i++) {
+            const uint32_t o = off(pr[i]);
+            // tasks a multiple of 4 bytes long: the piece's offset within its task is the same in every task
+            r.oi[i] = M::TB % 4u == 0u ? (o & ~3u) + M::goff(pc[i], o & 3u) : o;
+        }
         return r;
     };
     // task t's window start from a row's segment offset (padding tasks
@@ -617,8 +623,14 @@ __global__ __launch_bounds__(kMfmaThreads) void gemv_mfma_kernel(const MfmaParam
     auto load = [&](const Rows& r, uint32_t t, u32x4 (&v)[NLD], uint32_t (&aux)[4]) {
 #pragma unroll
         for (uint32_t i = 0; i < NLD; i++) {
-            const uint32_t o = task_off(r.oi[i], t);
-            v[i] = *gptr<u32x4>(r.abase + (o & ~3u) + M::goff(pc[i], o & 3u));
+            // one 32-bit offset from a wave-uniform base (every piece starts
+            // inside the tensor, below 4 GiB): no per-lane 64-bit address add
+            if constexpr (M::TB % 4u == 0u) {
+                v[i] = *gptr<u32x4>(r.abase + (t < nt ? t : nt - 1u) * M::TB + r.oi[i]);
+            } else {
+                const uint32_t o = task_off(r.oi[i], t);
+                v[i] = *gptr<u32x4>(r.abase + ((o & ~3u) + M::goff(pc[i], o & 3u)));
+            }
         }
         if constexpr (M::MLX) {
             uint32_t g0, g1;
