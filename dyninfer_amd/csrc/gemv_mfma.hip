@@ -1245,7 +1245,12 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
                                    : enc == ENC_Q5_K ? K / 256u * 176u
                                    : enc == ENC_IQ4_XS ? K / 256u * 136u
                                                      : K / 2u);
-    if (batch < 5 && tiles < kMfmaSplitTiles) return false;
+    // At 3-4 rows the VALU GEMV's per-row dot products are cheap enough that
+    // only the largest launches gain, and Q4_0 (the cheapest MFMA decode) from
+    // kMfmaMinTiles tiles: per launch at 4 rows, the 8B q/k/v (384 tiles)
+    // 10.58 -> 9.82 us; o_proj (256 tiles) 7.5 -> 7.9, the Q6_K down_proj 17.9
+    // -> 20.2 and the Q4_K q/k 10.0 -> 10.5 stay on VALU.
+    if (batch < 5 && tiles < kMfmaSplitTiles && !(enc == ENC_Q4_0 && tiles >= kMfmaMinTiles)) return false;
     if (batch <= max_register_batch(enc) && bytes < (8ull << 20) && tiles < kMfmaSplitTiles) return false;
     const uint32_t min_tiles = mfma_min_tiles(enc, batch);
     const int mode = enc == ENC_Q4_0   ? mfma_mode<MfmaQ40>(K, tiles, y_bf16, min_tiles)

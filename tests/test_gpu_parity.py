@@ -164,8 +164,9 @@ MFMA_CASES = [
     (oracle.Q4_0, 20480, 1024, 9, False, 0), (oracle.Q6_K, 17000, 1024, 16, True, 2),
     (oracle.Q6_K, 1040, 4096, 16, False, 0), (oracle.Q6_K, 4096, 12288, 16, False, 0),
     (oracle.Q4_0, 4096, 4096, 8, True, 0),
-    # 3-4 rows: only launches of >= 1024 tiles
+    # 3-4 rows: launches of >= 1024 tiles, and Q4_0 from 384 tiles (split mode)
     (oracle.Q6_K, 17000, 1024, 4, False, 0), (oracle.Q4_0, 20480, 1024, 3, True, 2),
+    (oracle.Q4_0, 6144, 4096, 4, False, 0), (oracle.Q4_0, 6150, 4096, 3, True, 2),
     # more rows than one VALU register pass: whole tiles from 128 tiles
     (oracle.Q4_0, 2048, 1024, 12, False, 0), (oracle.Q6_K, 2570, 1024, 8, True, 2),
     # split mode, more tiles than resident workgroups: two 4-wave tile groups per
