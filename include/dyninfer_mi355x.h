@@ -129,7 +129,7 @@ const char* dyninfer_mi355x_last_error(void);
  * x: [rows, K] row-major, 16-byte aligned, dtype x_dtype (f32 or bf16, every encoding);
  * y: [rows, N], dtype y_dtype (f32 or bf16).
  *   rows <= 16: the decode GEMV kernels (HBM-bound; 5..16 rows of large Q4_0, Q6_K, Q4_K,
- *     Q5_K, IQ4_XS and MLX weights on MFMA), activations rounded to f16 after a
+ *     Q5_K, IQ4_XS and MLX weights on MFMA, and at 3..4 rows the largest of them), activations rounded to f16 after a
  *     power-of-two scaling per scale group;
  *   rows >= 17: the prefill path.  Q4_1, Q8_0 and MLX U4 from 17 rows, Q4_0, Q6_K and
  *     the K-quants / IQ4_XS from 33 rows, or from 17 when K > 8192 except Q6_K with f32
@@ -158,7 +158,7 @@ const char* dyninfer_mi355x_last_error(void);
  *   GGUF Q4_0, Q4_1, Q8_0, IQ4_XS and MLX U4: 2^-10 * sum |w||x| (IQ4_XS prefill:
  *   3 * 2^-11 * sum |w||x|);
  *   Q6_K: (2^-10 + 2^-11) * sum |w||x|;
- *   Q4_K and Q5_K, whose prefill and 5..16-row weights are RNE_f16(q*RNE_f16(d*sc) -
+ *   Q4_K and Q5_K, whose prefill and MFMA-GEMV weights are RNE_f16(q*RNE_f16(d*sc) -
  *   RNE_f16(dmin*m)): (2^-10 + 2^-11) * sum |w||x| + 2^-10 * sum |dmin*m||x|, the
  *   offset term counting each weight's dmin*m, which may nearly cancel q*d*sc;
  *   MLX U4 with f32 scales and biases (each rounded to f16 before q*s + b) adds
