@@ -180,6 +180,21 @@ constexpr int stream_depth() {
     return E::ENC == ENC_Q6_K ? 3 : 2;
 }
 constexpr uint32_t kStreamWaves = 16;
+// The streaming instantiations that keep their ring and chunk state in
+// registers: with 64-weight chunks the unrolled rounds of Q4_K, Q5_K and Q6_K
+// spill at 1024 threads (128 registers per lane) for Q4_K at 3+ chunks per
+// lane, Q5_K at 2+ and Q6_K at 2, 4, 6 and 8, and at 512 threads for Q4_K and
+// Q5_K at 4+.  Those shapes run the persistent pipeline instead, which is
+// faster than the spilling kernels by far (single row, per launch: Q4_K 16384
+// x 12288 91.6 -> 24.7 us, x 16384 258 -> 31.8 us, Q5_K 16384 x 12288 130 ->
+// 31.0 us, Q6_K 16384 x 16384 58.1 -> 46.4 us).
+template <class E, int CPL, int TH>
+constexpr bool stream_fits() {
+    if constexpr (E::ENC == ENC_Q4_K) return TH == 1024 ? CPL <= 2 : CPL <= 3;
+    if constexpr (E::ENC == ENC_Q5_K) return TH == 1024 ? CPL <= 1 : CPL <= 3;
+    if constexpr (E::ENC == ENC_Q6_K) return TH == 1024 ? CPL == 1 || CPL == 3 : true;
+    return true;
+}
 constexpr int stream_gcd(int a, int b) { return b ? stream_gcd(b, a % b) : a; }
 
 template <class E, int CPL, int XM, int TH>
@@ -288,8 +303,8 @@ __global__ __launch_bounds__(TH) void gguf_gemv_stream_kernel(const GemvParams p
 // (a row, a chunk round) must be a multiple of 4 bytes so that a lane's
 // realignment is fixed: rows of an even number of blocks (Q4_0, Q8_0; Q6_K
 // an even number of super-blocks) and, for the super-block encodings, L >= 8.  Returns
-// hipErrorNotSupported when nothing fits (the caller then runs the
-// persistent pipeline).
+// hipErrorNotSupported when nothing fits or the instantiation would spill
+// (stream_fits): the caller then runs the persistent pipeline.
 template <class E, int XM>
 hipError_t launch_gguf_gemv_stream(GemvParams p, size_t lds, hipStream_t st) {
     const uint32_t nch = p.K / (uint32_t)E::CW;
@@ -319,7 +334,10 @@ hipError_t launch_gguf_gemv_stream(GemvParams p, size_t lds, hipStream_t st) {
     const uint32_t threads = big ? 1024u : 512u;
     GemvKernel k = nullptr;
 #define DMX_STREAM(c)                                                                                        \
-    if (cpl == c) k = big ? gguf_gemv_stream_kernel<E, c, XM, 1024> : gguf_gemv_stream_kernel<E, c, XM, 512>;
+    if constexpr (stream_fits<E, c, 1024>())                                                                 \
+        if (cpl == c && big) k = gguf_gemv_stream_kernel<E, c, XM, 1024>;                                    \
+    if constexpr (stream_fits<E, c, 512>())                                                                  \
+        if (cpl == c && !big) k = gguf_gemv_stream_kernel<E, c, XM, 512>;
     DMX_STREAM(1)
     DMX_STREAM(2)
     DMX_STREAM(3)
@@ -327,6 +345,7 @@ hipError_t launch_gguf_gemv_stream(GemvParams p, size_t lds, hipStream_t st) {
     DMX_STREAM(6)
     DMX_STREAM(8)
 #undef DMX_STREAM
+    if (!k) return hipErrorNotSupported;
     int cus = 0, per_cu = 0;
     hipError_t e = cached_occupancy(reinterpret_cast<const void*>(k), lds, (int)threads, &per_cu, &cus);
     if (e != hipSuccess) return e;

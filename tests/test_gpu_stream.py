@@ -66,6 +66,7 @@ Q6K = [(151936, 1024),   # L 8, CPL 2 (the Qwen3-0.6B lm_head)
        (30001, 4096),    # L 32, CPL 2
        (12500, 12288),   # L 64, CPL 3 (1024-thread workgroups)
        (12300, 8192),    # L 64, CPL 2
+       (12300, 16384),   # L 64, CPL 4 at 1024 threads: would spill, persistent pipeline
        (100003, 512),    # L 8, CPL 1
        (5000, 1280)]     # 5 super-blocks per row (1050 bytes): not a multiple of 4, persistent pipeline
 

@@ -323,12 +323,14 @@ def test_deterministic(ctx, kind):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("gtype", [oracle.Q4_K, oracle.Q5_K, oracle.IQ4_XS], ids=oracle.NAMES.get)
-def test_streaming_kernel_long_weight(ctx, gtype):
-    """One activation row over a 32768 x 4096 weight: enough row steps per wave
-    for the batch-1 streaming kernel (lanes per row 32 for the 64-weight
-    chunks, 64 for IQ4_XS).  Checked on 400 random rows, dequantised by the
-    oracle from their own bytes."""
-    n, k = 32768, 4096
+@pytest.mark.parametrize("n,k", [(32768, 4096), (12400, 12288), (12300, 16384)])
+def test_streaming_kernel_long_weight(ctx, gtype, n, k):
+    """One activation row over a weight with enough row steps per wave for the
+    batch-1 streaming kernel: 32768 x 4096 streams (lanes per row 32 for the
+    64-weight chunks, 64 for IQ4_XS); at K = 12288 and 16384 (3 and 4 chunks
+    per lane in 1024-thread workgroups) Q4_K and Q5_K would spill there and run
+    the persistent pipeline instead.  Checked on 400 random rows, dequantised
+    by the oracle from their own bytes."""
     enc = {oracle.Q4_K: d.ENC_Q4_K, oracle.Q5_K: d.ENC_Q5_K, oracle.IQ4_XS: d.ENC_IQ4_XS}[gtype]
     bb = oracle.BLOCK[gtype][1]
     data = oracle.synth_gguf(gtype, n, k, 17)
