@@ -959,10 +959,16 @@ hipError_t launch_s(const GemmArgs& a, uint32_t s, hipStream_t st) {
     return hipErrorInvalidConfiguration;
 }
 
+// Configurations whose registers spill (IQ4_XS at TM 2, NB 3: 40 dwords per
+// lane) are neither planned nor built.
+template <uint32_t ENC, int TM, int NB>
+constexpr bool kNoSpill = !(ENC == ENC_IQ4_XS && TM == 2 && NB == 3);
+
 template <uint32_t ENC>
 hipError_t launch_plan(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
     if (p.tm == 2 && p.nb == 2) return launch_s<ENC, 2, 2>(a, p.s, st);
-    if (p.tm == 2 && p.nb == 3) return launch_s<ENC, 2, 3>(a, p.s, st);
+    if constexpr (kNoSpill<ENC, 2, 3>)
+        if (p.tm == 2 && p.nb == 3) return launch_s<ENC, 2, 3>(a, p.s, st);
     if (p.tm == 4 && p.nb == 2) return launch_s<ENC, 4, 2>(a, p.s, st);
     if (p.tm == 4 && p.nb == 3) return launch_s<ENC, 4, 3>(a, p.s, st);
     return hipErrorInvalidConfiguration;
@@ -971,6 +977,7 @@ hipError_t launch_plan(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
 // Whether configuration (TM, NB, S) of encoding ENC fits one workgroup's LDS.
 template <uint32_t ENC>
 bool fits(int tm, int nb, int s) {
+    if (tm == 2 && nb == 3 && !kNoSpill<ENC, 2, 3>) return false;
     auto f = [&](auto geo2, auto geo3) { return nb == 2 ? geo2 : geo3; };
     if (tm == 2)
         return s == 4 ? f(Geo<ENC, 2, 2, 4>::kFits, Geo<ENC, 2, 3, 4>::kFits)
