@@ -127,6 +127,13 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     if (gemv_mfma_applies(enc, probs, nprob, batch, K, y_bf16, group))
         return gemv_mfma_launch(enc, probs, nprob, K, x, x_bf16, batch, y_bf16, group, sdtype, work, work_bytes,
                                 stream);
+    // bf16 outputs and K in several segments: on MFMA when the workspace holds f32 accumulators
+    if (y_bf16 && work) {
+        const uint64_t need = gemv_mfma_bf16_acc_bytes(enc, probs, nprob, batch, K, group);
+        if (need && work_bytes >= need)
+            return gemv_mfma_launch_bf16_acc(enc, probs, nprob, K, x, x_bf16, batch, group, sdtype, work, work_bytes,
+                                             stream);
+    }
     // Register batch: the next power of two, halved while its activation tile
     // does not fit one workgroup's LDS; larger batches run as several passes.
     uint32_t lim = 0;

@@ -982,6 +982,20 @@ __global__ __launch_bounds__(256) void mfma_zero_outputs_kernel(const MfmaParams
     if (i < p.nprob && e < (uint64_t)p.batch * pick(i, p.n)) gptr_mut<float>(pick(i, p.y))[e] = 0.0f;
 }
 
+// bf16 outputs of a launch whose K segments added into f32 accumulators (the
+// caller's workspace): problem blockIdx.y, element e of its [batch, n] rows,
+// rounded to nearest even as every GEMV epilogue rounds.
+struct MfmaBf16Out {
+    const float* src[kMaxProblems];
+    uint16_t* dst[kMaxProblems];
+    uint32_t count[kMaxProblems];
+};
+__global__ __launch_bounds__(256) void mfma_bf16_outputs_kernel(const MfmaBf16Out c) {
+    const uint32_t i = blockIdx.y;
+    const uint32_t e = blockIdx.x * 256u + threadIdx.x;
+    if (e < pick(i, c.count)) gptr_mut<uint16_t>(pick(i, c.dst))[e] = f32_to_bf16_bits(gptr<float>(pick(i, c.src))[e]);
+}
+
 // Stages a call's activations once, into the workspace, for a launch whose
 // workgroups copy them (XS_PRE): unit u = (task g of all of K, row b < RB, e =
 // q·NM + j) as the in-kernel staging forms it, with the 32 units of a (task,
@@ -1264,7 +1278,8 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
 
 uint64_t gemv_mfma_workspace_bytes(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K,
                                    bool y_bf16, uint32_t group) {
-    if (!gemv_mfma_applies(enc, probs, nprob, batch, K, y_bf16, group)) return 0;
+    if (!gemv_mfma_applies(enc, probs, nprob, batch, K, y_bf16, group))
+        return y_bf16 ? gemv_mfma_bf16_acc_bytes(enc, probs, nprob, batch, K, group) : 0;
     uint32_t tiles = 0;
     for (int i = 0; i < nprob; i++) tiles += (probs[i].n + 15u) / 16u;
     const uint32_t min_tiles = mfma_min_tiles(enc, batch);
@@ -1296,6 +1311,60 @@ hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, u
     if (enc == ENC_IQ4_XS) return go(MfmaIQ4XS{});
     if (enc == ENC_MLX_U4) return go(MfmaMlxU4{});
     return hipErrorInvalidValue;
+}
+
+// bf16 outputs: K segments cannot add into them, so a launch with K too long
+// for one LDS segment leaves the MFMA GEMV (onto the VALU GEMV's two register
+// passes at 9..16 rows: 4096 x 12288 at 16 rows 63-74 us against 17-23 us with
+// f32 outputs).  Given a workspace, the segments add into f32 accumulators in
+// it (after the staged activations) and one more launch rounds them to bf16.
+namespace {
+uint64_t bf16_acc_bytes(const GemvProblem* probs, int nprob, uint32_t batch) {
+    uint64_t s = 0;
+    for (int i = 0; i < nprob; i++) s += ((uint64_t)batch * probs[i].n * 4u + 255u) & ~(uint64_t)255u;
+    return s;
+}
+}  // namespace
+
+uint64_t gemv_mfma_bf16_acc_bytes(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K,
+                                  uint32_t group) {
+    if (gemv_mfma_applies(enc, probs, nprob, batch, K, true, group) ||
+        !gemv_mfma_applies(enc, probs, nprob, batch, K, false, group))
+        return 0;
+    const uint64_t pre = gemv_mfma_workspace_bytes(enc, probs, nprob, batch, K, false, group);
+    return pre ? pre + bf16_acc_bytes(probs, nprob, batch) : 0;  // (a segmented launch always prestages)
+}
+
+hipError_t gemv_mfma_launch_bf16_acc(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x,
+                                     bool x_bf16, uint32_t batch, uint32_t group, uint32_t sdtype, void* work,
+                                     uint64_t work_bytes, hipStream_t st) {
+    if (nprob < 1 || nprob > kMaxProblems) return hipErrorInvalidValue;
+    const uint64_t need = gemv_mfma_bf16_acc_bytes(enc, probs, nprob, batch, K, group);
+    if (!need || !work || work_bytes < need || ((uintptr_t)work & 255u)) return hipErrorInvalidValue;
+    const uint64_t pre = gemv_mfma_workspace_bytes(enc, probs, nprob, batch, K, false, group);
+    GemvProblem acc[kMaxProblems];
+    MfmaBf16Out c{};
+    uint8_t* a = static_cast<uint8_t*>(work) + pre;
+    uint32_t most = 0;
+    for (int i = 0; i < kMaxProblems; i++) {
+        const int k = i < nprob ? i : nprob - 1;
+        acc[i] = probs[k];
+        c.count[i] = i < nprob ? batch * probs[i].n : 0u;
+        if (i < nprob) {
+            acc[i].y = a;
+            c.src[i] = reinterpret_cast<const float*>(a);
+            c.dst[i] = static_cast<uint16_t*>(probs[i].y);
+            a += ((uint64_t)c.count[i] * 4u + 255u) & ~(uint64_t)255u;
+            most = c.count[i] > most ? c.count[i] : most;
+        } else {
+            c.src[i] = c.src[0];
+            c.dst[i] = c.dst[0];
+        }
+    }
+    hipError_t e = gemv_mfma_launch(enc, acc, nprob, K, x, x_bf16, batch, false, group, sdtype, work, pre, st);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(mfma_bf16_outputs_kernel, dim3((most + 255u) / 256u, (unsigned)nprob), dim3(256), 0, st, c);
+    return hipGetLastError();
 }
 
 }  // namespace dmx

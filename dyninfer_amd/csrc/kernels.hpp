@@ -98,8 +98,9 @@ uint64_t gemv_workspace_bytes(uint32_t enc, const GemvProblem* probs, int nprob,
                               bool y_bf16, uint32_t group);
 
 // Decode GEMV on MFMA for 3..16 activation rows (Q4_0, Q6_K, Q4_K, Q5_K, IQ4_XS, MLX U4; K a
-// multiple of 256): whether it serves a call, and the launch (several
-// launches when K needs more than one LDS segment; f32 outputs only then).
+// multiple of 256): whether it serves a call, and the launch (K in several LDS
+// segments adds into f32 outputs; bf16 outputs then take
+// gemv_mfma_launch_bf16_acc below, given a workspace).
 bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K, bool y_bf16,
                        uint32_t group);
 hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x, bool x_bf16,
@@ -107,9 +108,19 @@ hipError_t gemv_mfma_launch(uint32_t enc, const GemvProblem* probs, int nprob, u
                             uint64_t work_bytes, hipStream_t stream);
 // The workspace with which an MFMA GEMV call stages its activations once (the
 // f16 fragments, inverse scales and offset sums of every 256-k task), or 0
-// when it stages them in every workgroup.
+// when it stages them in every workgroup; for bf16 outputs with K in several
+// segments, gemv_mfma_bf16_acc_bytes.
 uint64_t gemv_mfma_workspace_bytes(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K,
                                    bool y_bf16, uint32_t group);
+// bf16 outputs with K too long for one LDS segment: the workspace the MFMA
+// GEMV needs to add its segments in f32 (the staged activations, then f32
+// accumulators of every problem's [batch, n] outputs), or 0 when the launch is
+// not such a case; and that launch (the workspace at least that large).
+uint64_t gemv_mfma_bf16_acc_bytes(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t batch, uint32_t K,
+                                  uint32_t group);
+hipError_t gemv_mfma_launch_bf16_acc(uint32_t enc, const GemvProblem* probs, int nprob, uint32_t K, const void* x,
+                                     bool x_bf16, uint32_t batch, uint32_t group, uint32_t sdtype, void* work,
+                                     uint64_t work_bytes, hipStream_t st);
 
 // Whether one activation row of K elements fits the GEMV's LDS tile.
 bool gemv_k_supported(uint32_t enc, uint32_t K);

@@ -147,7 +147,9 @@ const char* dyninfer_mi355x_last_error(void);
  *   size is then that of an optional staging (the MFMA GEMV with K >= 2048, at 9..16
  *   rows or with K too long for one LDS segment: the activations are staged once per
  *   call by a small kernel and copied into each workgroup's LDS, instead of being
- *   staged by every workgroup; same results).  A call
+ *   staged by every workgroup; same results; with bf16 outputs and K too long for one
+ *   LDS segment the workspace also holds f32 accumulators, and without it those
+ *   calls run the VALU GEMV, ~3x slower at 9..16 rows).  A call
  *   whose workspace is given but misaligned or too small, or missing when the prefill
  *   GEMM needs it, fails with DYNINFER_MI355X_ERR_INVALID_ARGUMENT before anything is
  *   enqueued.  The call's kernels write and read it in stream order; the
@@ -193,7 +195,10 @@ int dyninfer_mi355x_qlinear_multi(dyninfer_mi355x_ctx_t* ctx, const dyninfer_qwe
  * with K too long for one LDS segment (K > 4096 at most shapes), takes an optional
  * round_up((K/256) * T, 256), T = 8256 (T = 8512 for Q4_K and Q5_K): per 256 k, the
  * f16 MFMA fragments of 16 activation rows, their 16 f32 inverse scales (and the
- * f16 sums of the offset encodings); every other call 0.  Validates the
+ * f16 sums of the offset encodings); with bf16 outputs and K too long for one LDS
+ * segment, plus round_up(rows*N*4, 256) per weight for the f32 accumulators its K
+ * segments add into (without a workspace such a call runs the VALU GEMV); every
+ * other call 0.  Validates the
  * arguments as the call does (same status codes, pointers checked for alignment only);
  * host-only, enqueues nothing.  The reference's temporary-memory qualification
  * (docs/quantization/mlx-affine-u4.md:52-54) reads this figure.

@@ -248,6 +248,43 @@ def test_gemv_mfma_workspace_is_optional(ctx, gtype, n, k, batch, ybf16, off):
     assert np.all(err <= bound + extra), err.max()
 
 
+# bf16 outputs with K in several LDS segments: the MFMA GEMV adds the segments
+# into f32 accumulators in the workspace (after the staged activations) and a
+# last launch rounds them to bf16; without a workspace the VALU GEMV runs.
+BF16_LONG_K = [(oracle.Q4_0, 4096, 12288, 16), (oracle.Q6_K, 2048, 8192, 9), (oracle.Q4_K, 1040, 12288, 12),
+               (oracle.IQ4_XS, 3000, 8192, 16)]
+
+
+@pytest.mark.parametrize("gtype,n,k,batch", BF16_LONG_K,
+                         ids=[f"{oracle.NAMES[c[0]]}-{c[1]}x{c[2]}-b{c[3]}" for c in BF16_LONG_K])
+def test_gemv_mfma_bf16_outputs_long_k(ctx, gtype, n, k, batch):
+    w, data = gguf(gtype, n, k, seed=n + k + batch + 5)
+    x = oracle.randn(batch * k, seed=batch + 5).reshape(batch, k)
+    per = 8192 + 64 + (256 if gtype in (oracle.Q4_K, oracle.Q5_K) else 0)
+    pre = (k // 256 * per + 255) // 256 * 256
+    need = d.prefill_workspace_bytes([w], batch, d.DTYPE_F32, d.DTYPE_BF16)
+    assert need == pre + (batch * n * 4 + 255) // 256 * 256
+    assert d.prefill_workspace_bytes([w], batch, d.DTYPE_F32, d.DTYPE_F32) == pre
+    work = torch.full((need,), 0xFF, dtype=torch.uint8, device="cuda")
+
+    def host(y):
+        return oracle.bf16_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(batch, n)
+
+    a = host(ctx.qlinear(w, dev(x), y_dtype=torch.bfloat16, workspace=work))
+    b = host(ctx.qlinear(w, dev(x), y_dtype=torch.bfloat16, workspace=False))
+    f = ctx.qlinear(w, dev(x), y_dtype=torch.float32, workspace=work).cpu().numpy()
+    nc = min(n, 1024)
+    wf = oracle.dequant_gguf(gtype, data[:len(data) // n * nc], nc, k)
+    y64, absdot = oracle.linear_f64(x, wf)
+    den = np.where(absdot > 0, absdot, 1)
+    bound = 2.0 ** -10 + 2e-5 if gtype in (oracle.Q4_0, oracle.Q6_K, oracle.IQ4_XS) else 2e-3
+    for y in (a, b):  # MFMA through the f32 accumulators, and the VALU GEMV
+        err = np.abs(y[:, :nc].astype(np.float64) - y64) / den - np.abs(y64) * 2.0 ** -8 / den
+        assert np.all(err <= bound), err.max()
+    # the MFMA launch's f32 sums rounded once (the segments' atomic order aside)
+    assert np.all(np.abs(a[:, :nc].astype(np.float64) - f[:, :nc]) <= np.abs(f[:, :nc]) * 2.0 ** -8 + 1e-6 * den)
+
+
 def test_gemv_mfma_workspace_checks(ctx):
     """A decode call's optional workspace: NULL runs without it; one that is given
     must be 256-byte aligned and at least the reported size, else
@@ -302,6 +339,28 @@ def test_gemv_mfma_mlx_workspace_is_optional(ctx, n, k, g, sdtype, batch):
     else:
         assert np.max(np.abs(a.astype(np.float64) - b) / np.where(absdot > 0, absdot, 1)) <= 1e-6
     assert oracle.normalized_error(a, y64, absdot) <= 2.0 ** -10 + 1e-4
+
+
+def test_gemv_mfma_mlx_bf16_outputs_long_k(ctx):
+    """MLX U4 with bf16 in/out and K = 12288 (three LDS segments) at 16 rows: on
+    the MFMA GEMV through f32 accumulators in the workspace, and on the VALU GEMV
+    without one; both against the oracle."""
+    n, k, g, sdtype, batch = 2048, 12288, 64, oracle.D_BF16, 16
+    packed, sc, bi = oracle.synth_mlx_u4(n, k, g, sdtype, seed=31)
+    w = d.QWeight(d.ENC_MLX_U4, n, k, dev(packed), dev(sc), dev(bi), g, sdtype)
+    xb = oracle.f32_to_bf16_bits(oracle.randn(batch * k, seed=32)).reshape(batch, k)
+    xd = dev(xb).view(torch.bfloat16)
+    pre = (k // 256 * (8192 + 64) + 255) // 256 * 256
+    need = d.prefill_workspace_bytes([w], batch, d.DTYPE_BF16, d.DTYPE_BF16)
+    assert need == pre + batch * n * 4
+    work = torch.full((need,), 0xFF, dtype=torch.uint8, device="cuda")
+    y64, absdot = oracle.linear_f64(oracle.bf16_bits_to_f32(xb), oracle.dequant_mlx_u4(packed, sc, bi, sdtype, n, k, g))
+    den = np.where(absdot > 0, absdot, 1)
+    for ws in (work, False):
+        y = ctx.qlinear(w, xd, y_dtype=torch.bfloat16, workspace=ws)
+        y = oracle.bf16_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(batch, n)
+        err = np.abs(y.astype(np.float64) - y64) / den - np.abs(y64) * 2.0 ** -8 / den
+        assert np.all(err <= 2.0 ** -10 + 2e-5), err.max()
 
 
 @pytest.mark.parametrize("gtype,n,k", [(oracle.Q6_K, 4096, 12288), (oracle.Q4_0, 2048, 16384)],
