@@ -4,7 +4,8 @@ device's static scratch array instead of a stream-ordered allocation, so the
 outputs must be bit-identical, and both within the f16 bound of the oracle.
 Two prefill calls in a row (the second smaller, over the first call's
 leftover staging), decode calls (two in a row staging their activations in
-the scratch array, the second smaller), a staging beyond the scratch size
+the scratch array, the second smaller; bf16 outputs with long K, whose f32
+accumulators the array also holds), a staging beyond the scratch size
 (rejected host-side, after which calls still work), and a prefill captured in
 a HIP graph (kernel nodes only) whose replays equal the eager call."""
 import numpy as np
@@ -84,6 +85,25 @@ def test_noalloc_decode_staged_in_scratch(ctx):
             assert np.array_equal(o.view(np.uint32), g.view(np.uint32)), (k, rows, n)
             y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(oracle.Q4_0, data, n, k))
             assert oracle.normalized_error(g, y64, absdot) <= F16X2
+
+
+def test_noalloc_decode_bf16_outputs_long_k(ctx):
+    """bf16 outputs with K = 12288 at 16 rows (three LDS segments): the segments
+    add into f32 accumulators in the scratch array after the staged activations,
+    then one launch rounds them to bf16.  Every output is written (the outputs
+    start as NaN) and lies within the f16 bound plus the bf16 rounding."""
+    k, shapes, rows = 12288, [2048, 1024], 16
+    ws, datas = _weights(k, shapes, seed=60)
+    x = oracle.randn(rows * k, seed=61).reshape(rows, k)
+    outs = [torch.full((rows, n), float("nan"), dtype=torch.bfloat16, device="cuda") for n in shapes]
+    ctx.qlinear_multi(ws, dev(x), outs, noalloc=True)
+    torch.cuda.synchronize()
+    for o, data, n in zip(outs, datas, shapes):
+        g = o.float().cpu().numpy().astype(np.float64)
+        assert not np.isnan(g).any()
+        y64, absdot = oracle.linear_f64(x, oracle.dequant_gguf(oracle.Q4_0, data, n, k))
+        den = np.where(absdot > 0, absdot, 1)
+        assert np.all(np.abs(g - y64) / den - np.abs(y64) * 2.0 ** -8 / den <= F16X2)
 
 
 def test_noalloc_decode_and_size_limit(ctx):
