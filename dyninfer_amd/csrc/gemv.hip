@@ -174,16 +174,21 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     // weight chunks: 2; at 3 the 8B down_proj ran slower than the pipeline,
     // Q4_K 4096 x 12288 12.6 against 9.1 us), 2 for 2 rows, 1 for 4 (64-weight
     // chunks: at most 2048 row blocks; 12288 x 4096 Q4_K 28.6 us against 17.7
-    // us in the pipeline, 1024 x 4096 6.3 against 6.7 us).  More chunks or
-    // rows cost more in registers, and waves per SIMD, than the latency
-    // saves (timed on the config-1/4 steps).  Otherwise the persistent
-    // pipeline, whose rows per lane group the encoding's launcher picks from
-    // the occupancy of each instantiated tile.
+    // us in the pipeline, 1024 x 4096 6.3 against 6.7 us).  64-weight chunks
+    // at 2 rows: at most 4096 row blocks at 1 chunk per lane and 2048 at 2
+    // (per launch, Q4_K/Q5_K/Q6_K 13824 x 5120: 30.4/32.1/32.0 us in latency
+    // mode against 18.9/22.1/21.7 in the pipeline, 12288 x 4096 13.7 against
+    // 11.5 us (Q4_K), 4096 x 5120 10.8 against 9.5; 1024 x 5120 6.6 against
+    // 6.8, 4096 x 4096 6.8 either way).  More chunks or rows cost more in
+    // registers, and waves per SIMD, than the latency saves (timed on the
+    // config-1/4 steps).  Otherwise the persistent pipeline, whose rows per
+    // lane group the encoding's launcher picks from the occupancy of each
+    // instantiated tile.
     uint64_t rbs1 = 0;
     for (int i = 0; i < nprob; i++) rbs1 += (probs[i].n + (64u >> lanes_log2) - 1) / (64u >> lanes_log2);
     const uint32_t cpl = (nch + L - 1) >> lanes_log2;
     const uint32_t max_cpl = B == 1 ? (info.wide ? 2u : 4u) : B == 2 ? 2u : B == 4 ? 1u : 0u;
-    const uint64_t max_rbs = B == 4 && info.wide ? 2048u : 16384u;
+    const uint64_t max_rbs = !info.wide || B == 1 ? 16384u : B == 4 ? 2048u : cpl == 1 ? 4096u : 2048u;
     const uint32_t oneshot = cpl >= 1 && cpl <= max_cpl && rbs1 <= max_rbs ? cpl : 0u;
 
     GemvParams p = {};

@@ -171,6 +171,21 @@ def test_gemv(ctx, kind, n, k, batch):
 
 
 @pytest.mark.gpu
+@kinds
+@pytest.mark.parametrize("n,k", [(6144, 5120), (8192, 4096)])
+def test_two_rows_many_row_blocks(ctx, kind, n, k):
+    """Two activation rows over more row blocks than the 2-row latency mode takes
+    for 64-weight chunks (2048 at 2 chunks per lane, 4096 at 1): the persistent
+    pipeline.  Checked on the first 1024 rows."""
+    w, data = weight(kind, n, k, seed=200 + n + k)
+    x = oracle.randn(2 * k, seed=201).reshape(2, k)
+    y = ctx.qlinear(w, dev(x)).cpu().numpy()
+    nc = 1024
+    err = err_of(y[:, :nc], x, oracle.dequant_gguf(kind, data[:len(data) // n * nc], nc, k))
+    assert err <= TOL and err <= XF16, err
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("rows", [17, 40])
 @kinds
 def test_more_than_16_rows(ctx, kind, rows):
