@@ -1260,11 +1260,15 @@ bool gemv_mfma_applies(uint32_t enc, const GemvProblem* probs, int nprob, uint32
                                    : enc == ENC_IQ4_XS ? K / 256u * 136u
                                                      : K / 2u);
     // At 3-4 rows the VALU GEMV's per-row dot products are cheap enough that
-    // only the largest launches gain, and Q4_0 (the cheapest MFMA decode) from
-    // kMfmaMinTiles tiles: per launch at 4 rows, the 8B q/k/v (384 tiles)
-    // 10.58 -> 9.82 us; o_proj (256 tiles) 7.5 -> 7.9, the Q6_K down_proj 17.9
-    // -> 20.2 and the Q4_K q/k 10.0 -> 10.5 stay on VALU.
-    if (batch < 5 && tiles < kMfmaSplitTiles && !(enc == ENC_Q4_0 && tiles >= kMfmaMinTiles)) return false;
+    // only the largest launches gain, and Q4_0 (the cheapest MFMA decode) with
+    // K = 4096 on 384-512 tiles: per launch at 4 rows, the 8B q/k/v (384 tiles)
+    // 10.58 -> 9.82 us, 8192 x 4096 11.6 -> 11.3; o_proj (256 tiles) 7.5 -> 7.9,
+    // the Q6_K down_proj 17.9 -> 20.2 and the Q4_K q/k 10.0 -> 10.5 stay on
+    // VALU, and so do other Q4_0 shapes (10240 x 4096 12.9 -> 14.5, 14336 x
+    // 4096 17.0 -> 17.5, 6144 x 5120 14.3 -> 17.6, 13824 x 5120 23.0 -> 29.1,
+    // 6144 x 8192 15.8 -> 19.6 on MFMA).
+    const bool q4_0_few = enc == ENC_Q4_0 && K == 4096u && tiles >= kMfmaMinTiles && tiles <= 512u;
+    if (batch < 5 && tiles < kMfmaSplitTiles && !q4_0_few) return false;
     if (batch <= max_register_batch(enc) && bytes < (8ull << 20) && tiles < kMfmaSplitTiles) return false;
     const uint32_t min_tiles = mfma_min_tiles(enc, batch);
     const int mode = enc == ENC_Q4_0   ? mfma_mode<MfmaQ40>(K, tiles, y_bf16, min_tiles)
