@@ -955,11 +955,11 @@ struct MlxLoad {
     }
 };
 
-template <int B, int R, int XM>
-__global__ __launch_bounds__(kGemvThreads) void mlx_u4_gemv_kernel(const GemvParams p) {
+template <int B, int R, int XM, int TH = kGemvThreads>
+__global__ __launch_bounds__(TH) void mlx_u4_gemv_kernel(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t xlds[];
-    gemv_pipeline<EncMlxU4, R, B, kGemvThreads>(p, xlds, MlxLoad(p),
-                                                [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XM>(xlds, p, mid); });
+    gemv_pipeline<EncMlxU4, R, B, TH>(p, xlds, MlxLoad(p),
+                                      [&](auto&& mid) { stage_x_auto<EncMlxU4, B, XM, TH>(xlds, p, mid); });
 }
 
 template <int CPL, int B, int XM, int TH>
@@ -1010,6 +1010,7 @@ inline void split_waves(GemvParams& p, uint32_t rows_per_rb, uint32_t threads) {
 }
 
 typedef void (*GemvKernel)(GemvParams);
+constexpr int kGemvMaxTiles = 6;
 
 // One persistent-pipeline instantiation: rows per lane group and its kernel.
 struct GemvTile {
@@ -1036,13 +1037,19 @@ struct GemvTile {
 // 2-row tiles (both split evenly, 16 and 8 waves per CU); the 8B gate/up (two
 // 12288-row problems) on 4-row tiles left half the waves 2 row blocks and
 // half 1 (49% of HBM peak), 1- and 2-row tiles split them evenly (54%).
+// Between tiles of equal rows per wave, the one whose busiest CU holds fewer
+// rows (a grid below the CU count in 512-thread workgroups leaves CUs idle
+// that 256-thread workgroups fill), ties to the first listed.  The even-split
+// rule takes the first-listed workgroup size only: at one workgroup per CU
+// (the 8B Q6_K down_proj at 4 rows, 96 KiB of activations) 256 threads split
+// evenly with half the waves, 23.3 us per launch against 17.9.
 inline hipError_t launch_persistent_best(const GemvTile* t, int n, const GemvParams& p0, size_t lds,
                                          uint32_t cpl, hipStream_t st) {
     const uint32_t groups = 64u >> p0.lanes_log2;  // lane groups per wave
     uint64_t total_rows = 0;
     for (uint32_t k = 0; k < p0.nprob; k++) total_rows += p0.n[k];
     int pick = -1, even = -1;
-    uint64_t best = ~(uint64_t)0;
+    uint64_t best = ~(uint64_t)0, best_load = ~(uint64_t)0;
     GemvParams q = p0, chosen = p0, chosen_even = p0;
     for (int i = 0; i < n; i++) {
         q = p0;
@@ -1066,12 +1073,14 @@ inline hipError_t launch_persistent_best(const GemvTile* t, int n, const GemvPar
         }
         const uint64_t rows = rbs * rows_per_rb;
         const uint64_t load = rows * waves * (((uint64_t)q.grid + (uint64_t)cus - 1) / (uint64_t)cus);
-        if (even < 0 && rbs * cpl >= 8 && load * 100 <= total_rows * 105 / (uint64_t)cus) {
+        if (even < 0 && t[i].threads == t[0].threads && rbs * cpl >= 8 &&
+            load * 100 <= total_rows * 105 / (uint64_t)cus) {
             even = i;
             chosen_even = q;
         }
-        if (rows < best) {
+        if (rows < best || (rows == best && load < best_load)) {
             best = rows;
+            best_load = load;
             pick = i;
             chosen = q;
         }
@@ -1088,9 +1097,10 @@ inline hipError_t launch_persistent_best(const GemvTile* t, int n, const GemvPar
 // The persistent tiles instantiated for register batch B: the default rows per
 // group W, half of it, and for one activation row every power of two down
 // to one row.  gemv_tile<R>() names the kernel of R rows, of `threads`
-// threads per workgroup.
+// threads per workgroup.  2-8 activation rows list them twice, in 512- and
+// 256-thread workgroups (kGemvMaxTiles entries at most).
 template <class E, int B, class MK>
-int gemv_tiles(GemvTile (&t)[3], MK&& gemv_tile, uint32_t threads = kGemvThreads) {
+int gemv_tiles(GemvTile* t, MK&& gemv_tile, uint32_t threads = kGemvThreads) {
     constexpr int W = rows_per_group<E, B>();
     int n = 0;
     t[n++] = {(uint32_t)W, gemv_tile(std::integral_constant<int, W>()), threads};
@@ -1167,7 +1177,7 @@ hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot,
 #undef DMX_ONESHOT
         return hipErrorInvalidValue;
     }
-    GemvTile t[3];
+    GemvTile t[kGemvMaxTiles];
     int n = 0;
     // One activation row and K > 8192: 1024-thread workgroups, one per CU,
     // stage the activations half as often per CU, in one round of loads.
@@ -1181,8 +1191,10 @@ hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot,
     const bool big = B == 1 && p.K > 8192u;
 #define DMX_CASE(b)                                                                                            \
     case b:                                                                                                    \
-        if constexpr (b <= max_register_batch(E::ENC))                                                         \
+        if constexpr (b <= max_register_batch(E::ENC)) {                                                       \
             n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, b, decltype(r)::value, xmode_rows(XM, b)>; }); \
+            n += gemv_tiles<E, b>(t + n, [](auto r) -> GemvKernel { return gguf_gemv_kernel<E, b, decltype(r)::value, xmode_rows(XM, b), 256>; }, 256u); \
+        }                                                                                                      \
         break;
     switch (B) {
     case 1:

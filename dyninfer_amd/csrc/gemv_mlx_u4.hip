@@ -23,11 +23,13 @@ hipError_t launch_mlx(const GemvParams& p, uint32_t B, uint32_t oneshot, hipStre
 #undef DMX_ONESHOT
         return hipErrorInvalidValue;
     }
-    GemvTile t[3];
+    GemvTile t[kGemvMaxTiles];
     int n = 0;
 #define DMX_CASE(b)                                                                                        \
     case b:                                                                                                \
         n = gemv_tiles<E, b>(t, [](auto r) -> GemvKernel { return mlx_u4_gemv_kernel<b, decltype(r)::value, xmode_rows(XM, b)>; }); \
+        if constexpr (b > 1)                                                                               \
+            n += gemv_tiles<E, b>(t + n, [](auto r) -> GemvKernel { return mlx_u4_gemv_kernel<b, decltype(r)::value, xmode_rows(XM, b), 256>; }, 256u); \
         break;
     switch (B) {
         DMX_CASE(1)
