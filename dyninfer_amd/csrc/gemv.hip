@@ -172,7 +172,10 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     // a lane's chunks loaded at once) when the matrices give at most 16384
     // such row blocks and a lane few chunks: 4 for one activation row (64-
     // weight chunks: 2; at 3 the 8B down_proj ran slower than the pipeline,
-    // Q4_K 4096 x 12288 12.6 against 9.1 us), 2 for 2 rows, 1 for 4 (64-weight
+    // Q4_K 4096 x 12288 12.6 against 9.1 us), 2 for 2 and 8 rows (at 8 rows
+    // the Qwen3-0.6B MLX step 853 -> 744 us per launch set, q/k/v 6.9 -> 5.5
+    // us, down 8.1 -> 7.7; 2 chunks take ~300 registers there, so that kernel
+    // runs in 256-thread workgroups only), 1 for 4 (64-weight
     // chunks: at most 2048 row blocks; 12288 x 4096 Q4_K 28.6 us against 17.7
     // us in the pipeline, 1024 x 4096 6.3 against 6.7 us).  64-weight chunks
     // at 2 rows: at most 4096 row blocks at 1 chunk per lane and 2048 at 2
@@ -187,7 +190,7 @@ hipError_t gemv_launch(uint32_t enc, const GemvProblem* probs, int nprob, uint32
     uint64_t rbs1 = 0;
     for (int i = 0; i < nprob; i++) rbs1 += (probs[i].n + (64u >> lanes_log2) - 1) / (64u >> lanes_log2);
     const uint32_t cpl = (nch + L - 1) >> lanes_log2;
-    const uint32_t max_cpl = B == 1 ? (info.wide ? 2u : 4u) : B == 2 ? 2u : B == 4 ? 1u : 0u;
+    const uint32_t max_cpl = B == 1 ? (info.wide ? 2u : 4u) : B == 2 ? 2u : B == 4 ? 1u : B == 8 ? 2u : 0u;
     const uint64_t max_rbs = !info.wide || B == 1 ? 16384u : B == 4 ? 2048u : cpl == 1 ? 4096u : 2048u;
     const uint32_t oneshot = cpl >= 1 && cpl <= max_cpl && rbs1 <= max_rbs ? cpl : 0u;
 

@@ -1117,11 +1117,12 @@ int gemv_tiles(GemvTile* t, MK&& gemv_tile, uint32_t threads = kGemvThreads) {
 // them in 512-thread groups; measured on the Qwen3-0.6B projections (1,024
 // and 3,072 waves) 256 threads took 5-15% less time per launch, and on
 // launches that split evenly either way (2,048, 4,096, 6,144 waves) it cost
-// up to 12%.
+// up to 12%.  A null k512 (a kernel built for 256 threads only) always
+// launches k256.
 template <class KERNEL>
 hipError_t launch_oneshot(KERNEL k512, KERNEL k256, GemvParams p, size_t lds, hipStream_t st) {
     int cus = 0, per_cu = 0;
-    hipError_t e = cached_occupancy(reinterpret_cast<const void*>(k512), lds, 512, &per_cu, &cus);
+    hipError_t e = k512 ? cached_occupancy(reinterpret_cast<const void*>(k512), lds, 512, &per_cu, &cus) : hipSuccess;
     if (e != hipSuccess) return e;
     e = cached_occupancy(reinterpret_cast<const void*>(k256), lds, 256, &per_cu, &cus);
     if (e != hipSuccess) return e;
@@ -1131,7 +1132,7 @@ hipError_t launch_oneshot(KERNEL k512, KERNEL k256, GemvParams p, size_t lds, hi
         const uint64_t wgs = ((uint64_t)p.total_rb + waves - 1) / waves;
         return (wgs + (uint64_t)cus - 1) / (uint64_t)cus * waves;
     };
-    const bool small = busiest(4) < busiest(8);
+    const bool small = !k512 || busiest(4) < busiest(8);
     const uint32_t waves = small ? 4u : 8u;
     p.grid = (p.total_rb + waves - 1) / waves;
     hipLaunchKernelGGL(small ? k256 : k512, dim3(p.grid), dim3(waves * 64u), lds, st, p);
@@ -1174,6 +1175,13 @@ hipError_t launch_gguf_gemv_x(const GemvParams& p, uint32_t B, uint32_t oneshot,
             DMX_ONESHOT(2, 2)
         }
         if constexpr (max_register_batch(E::ENC) >= 4) DMX_ONESHOT(4, 1)
+        if constexpr (max_register_batch(E::ENC) >= 8) {
+            DMX_ONESHOT(8, 1)
+            // 8 rows of 2 chunks per lane take ~300 registers: 256-thread workgroups only
+            if (B == 8 && oneshot == 2)
+                return launch_oneshot<GemvKernel>(nullptr, gguf_gemv_oneshot_kernel<E, 2, 8, xmode_rows(XM, 8), 256>,
+                                                  p, lds, st);
+        }
 #undef DMX_ONESHOT
         return hipErrorInvalidValue;
     }

@@ -20,6 +20,11 @@ hipError_t launch_mlx(const GemvParams& p, uint32_t B, uint32_t oneshot, hipStre
         DMX_ONESHOT(2, 1)
         DMX_ONESHOT(2, 2)
         DMX_ONESHOT(4, 1)
+        DMX_ONESHOT(8, 1)
+        // 8 rows of 2 chunks per lane take ~300 registers: 256-thread workgroups only
+        if (B == 8 && oneshot == 2)
+            return launch_oneshot<GemvKernel>(nullptr, mlx_u4_gemv_oneshot_kernel<2, 8, xmode_rows(XM, 8), 256>, p,
+                                              lds, st);
 #undef DMX_ONESHOT
         return hipErrorInvalidValue;
     }

@@ -132,6 +132,32 @@ def test_gemv_gguf_odd_batches(ctx, gtype, batch):
     assert err <= XF16, err
 
 
+LATENCY8_CASES = [(g, n, k) for g in (oracle.Q4_0, oracle.Q4_1, oracle.Q8_0, oracle.IQ4_XS)
+                  for n, k in ((1000, 2048), (700, 3072), (1024, 4096))]
+LATENCY8_CASES += [(g, 6150, 1056) for g in (oracle.Q4_0, oracle.Q8_0)]
+
+
+@pytest.mark.parametrize("gtype,n,k", LATENCY8_CASES, ids=[f"{oracle.NAMES[g]}-{n}x{k}" for g, n, k in LATENCY8_CASES])
+@pytest.mark.parametrize("batch,xbf16", [(6, False), (8, False), (8, True)])
+def test_gemv_latency_mode_eight_rows(ctx, gtype, n, k, batch, xbf16):
+    """5-8 activation rows on small launches: one wave per row block with all
+    of a lane's chunks loaded at once, 1 chunk per lane (K = 2048) or 2 (K =
+    3072, where the lanes past the last chunk add zero, 4096, and 1056 in 32
+    lanes; that kernel is built for 256-thread workgroups and must never be
+    launched with 512, including at 6150 rows, where 256 and 512 threads put
+    the same number of waves on the busiest CU)."""
+    w, data = gguf(gtype, n, k, seed=500 + n + batch)
+    x = oracle.randn(batch * k, seed=n + batch).reshape(batch, k)
+    if xbf16:
+        xb = oracle.f32_to_bf16_bits(x.reshape(-1)).reshape(batch, k)
+        xd, x = dev(xb).view(torch.bfloat16), oracle.bf16_bits_to_f32(xb).reshape(batch, k)
+    else:
+        xd = dev(x)
+    y = ctx.qlinear(w, xd).cpu().numpy()
+    err = gemv_err(y, x, oracle.dequant_gguf(gtype, data, n, k))
+    assert err <= XF16, err
+
+
 @pytest.mark.parametrize("batch", [1, 4])
 def test_gemv_multi_qkv(ctx, batch):
     # q/k/v of Qwen3-0.6B share one activation: one launch, three outputs
