@@ -138,14 +138,16 @@ LATENCY8_CASES += [(g, 6150, 1056) for g in (oracle.Q4_0, oracle.Q8_0)]
 
 
 @pytest.mark.parametrize("gtype,n,k", LATENCY8_CASES, ids=[f"{oracle.NAMES[g]}-{n}x{k}" for g, n, k in LATENCY8_CASES])
-@pytest.mark.parametrize("batch,xbf16", [(6, False), (8, False), (8, True)])
+@pytest.mark.parametrize("batch,xbf16", [(3, True), (4, False), (6, False), (8, False), (8, True)])
 def test_gemv_latency_mode_eight_rows(ctx, gtype, n, k, batch, xbf16):
-    """5-8 activation rows on small launches: one wave per row block with all
-    of a lane's chunks loaded at once, 1 chunk per lane (K = 2048) or 2 (K =
-    3072, where the lanes past the last chunk add zero, 4096, and 1056 in 32
-    lanes; that kernel is built for 256-thread workgroups and must never be
-    launched with 512, including at 6150 rows, where 256 and 512 threads put
-    the same number of waves on the busiest CU)."""
+    """3-8 activation rows on small launches.  At 5-8 rows latency mode (one
+    wave per row block with all of a lane's chunks loaded at once) at 1 chunk
+    per lane (K = 2048) or 2 (K = 3072, where the lanes past the last chunk add
+    zero, 4096, and 1056 in 32 lanes); at 3-4 rows latency mode at 1 chunk,
+    the persistent pipeline at 2.  The 8-row kernel of 2 chunks is built for
+    256-thread workgroups and must never be launched with 512, including at
+    6150 rows, where 256 and 512 threads put the same number of waves on the
+    busiest CU."""
     w, data = gguf(gtype, n, k, seed=500 + n + batch)
     x = oracle.randn(batch * k, seed=n + batch).reshape(batch, k)
     if xbf16:
