@@ -1065,7 +1065,9 @@ __global__ __launch_bounds__(kMfmaPrepThreads) void gemv_mfma_prep_kernel(const 
 // 12288, three segments) 35.0 -> 26.5, lm_head 123 either way; at 8 rows the
 // prep launch costs more than it saves on one segment (q/k/v 11.3 -> 11.5,
 // gate/up 21.6 -> 22.6, lm_head 116 -> 120 us) and down_proj still gains,
-// 30.3 -> 26.5 us.
+// 30.3 -> 26.5 us.  From K = 1024 it lost at 12-16 rows on every shape timed
+// (bf16 in/out, per launch: MLX 4096 x 1024 8.9 -> 10.2 us, 12288 x 1024
+// 13.6 -> 15.1; Q4_0 4096 x 1024 7.4 -> 8.5, 12288 x 1024 11.2 -> 12.0).
 constexpr uint32_t kMfmaPrestageMinK = 2048;
 template <class M>
 bool mfma_prestages(uint32_t K, uint32_t batch, int mode) {
